@@ -1,0 +1,245 @@
+"""Benchmark of the MI355X quantized sparse-MoE layer (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--batch 32]
+
+One step = one forward of the MoE layer (router, permute, int4 gate_up + SwiGLU, int4 down,
+gated shared expert, combine) over one batch of synthetic tokens, with weights and inputs
+resident in HBM. Workload: Qwen3.5-397B-A17B-shaped layer, hidden 4096,
+512 experts, top-10 softmax, expert intermediate 1024, shared expert 1024, int4 g64, decode batch
+32 tokens. To time HBM rather than the 256 MB Infinity Cache, the timed loop rotates over
+`--layers` copies of the layer (distinct memory) and a pool of distinct input batches (so the
+routed experts change every step).
+
+Printed (one JSON line): whole-layer tokens/s (`value`), per-step time, the dominant kernel's
+roofline (routed gate_up+SwiGLU: algorithmic bytes per launch / its average duration, HIP events
+on the launch stream), a sweep over the other decode batches and the 4096-token prefill, and the
+CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host cores, bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0       # MI355X dense bf16 MFMA
+METRIC = "MoE-layer tokens/sec + achieved HBM GB/s (decode) / MFMA util (prefill), int4g64"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=8, help="layer copies rotated for cold HBM")
+    ap.add_argument("--pool", type=int, default=16, help="distinct input batches rotated")
+    ap.add_argument("--sweep", default="1,8,128,4096", help="extra batch sizes ('' = none)")
+    ap.add_argument("--kernel-reps", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
+    ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
+              f"--gpus {args.gpus} is not supported. Multi-GPU sharding is a design note "
+              "(expert- or tensor-parallel over xGMI), not a measured path.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from quanta_amd import _lib as L
+    from quanta_amd import ops, synth
+    from quanta_amd.moe import TiledExperts, prepare, qwen35_route, tile_experts_packed
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    L.load()
+    dev = torch.device("cuda", 0)
+    spec = synth.spec(args.config)
+    cfg = spec.cfg
+    H, E, k, I = cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size
+    Is = cfg.shared_expert_intermediate_size
+
+    t0 = time.time()
+    base = synth.make_layer(args.config, device=dev)
+    log(f"generated {args.config} layer in {time.time() - t0:.1f}s")
+    # resident (tiled) layer copies at distinct addresses; the native stacks are dropped
+    layers = []
+    gu0 = TiledExperts(**tile_experts_packed(base["experts_gate_up"]))
+    dn0 = TiledExperts(**tile_experts_packed(base["experts_down"]))
+    native_cpu = None
+    if not args.no_cpu_baseline:
+        native_cpu = {kk: ({q: (v.cpu() if isinstance(v, torch.Tensor) else v) for q, v in vv.items()}
+                           if isinstance(vv, dict) else vv.cpu()) for kk, vv in base.items()}
+    del base["experts_gate_up"], base["experts_down"]
+    for li in range(args.layers):
+        def cp(te):
+            return TiledExperts({q: (v.clone() if isinstance(v, torch.Tensor) else v) for q, v in te.items()})
+        p = {kk: v.clone() for kk, v in base.items()}
+        p["experts_gate_up"] = gu0 if li == 0 else cp(gu0)
+        p["experts_down"] = dn0 if li == 0 else cp(dn0)
+        layers.append(p)
+    torch.cuda.synchronize()
+    log(f"{args.layers} resident layer copies ready ({time.time() - t0:.1f}s)")
+
+    def run_batch(N, steps, warmup, pool, regime=L.REGIME_AUTO):
+        xs = [synth.make_inputs(args.config, N, device=dev, seed=100 + i) for i in range(pool)]
+        preps = [prepare(p, cfg, regime=regime) for p in layers]
+        ws = torch.empty(ops.forward_workspace(preps[0].cfg, N), dtype=torch.uint8, device=dev)
+        out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+
+        def step(i):
+            pr = preps[i % len(preps)]
+            ops.forward(pr.cfg, pr.weights, xs[i % pool], out=out, ws=ws)
+
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            step(i)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        # distinct experts per batch (U) for the algorithmic byte count
+        us = []
+        for x in xs:
+            idx, _ = qwen35_route(x, layers[0]["gate"], cfg)
+            us.append(int(torch.unique(idx).numel()))
+        return ms, us, xs, preps
+
+    # ------------------------------------------------------------------ headline workload
+    N = args.batch
+    if args.only == "kernel":
+        steps_layer = 1
+    else:
+        steps_layer = args.steps
+    ms, us, xs, preps = run_batch(N, steps_layer, args.warmup, args.pool)
+    U = sum(us) / len(us)
+    layer_bytes = synth.algorithmic_bytes(cfg, U, N)
+    log(f"N={N}: {ms * 1e3:.1f} us/step, U={U:.1f}, layer {layer_bytes / ms / 1e6:.0f} GB/s")
+
+    # ------------------------------------------------------------------ dominant kernel
+    # routed gate_up + SwiGLU, launched alone on the real permuted inputs, rotating layers
+    kern = None
+    if args.only != "layer":
+        regime = L.REGIME_SMALL if N <= 256 else L.REGIME_LARGE
+        m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
+        inputs = []
+        for x in xs[:4]:
+            idx, _ = qwen35_route(x, layers[0]["gate"], cfg)
+            counts, offsets, tile_off, sorted_slot, inv = ops.permute(idx, E, m_tile)
+            inputs.append((x, offsets, tile_off, sorted_slot, int((counts > 0).sum())))
+        h = torch.empty(N * k, I, dtype=torch.bfloat16, device=dev)
+
+        def launch(i):
+            pr = preps[i % len(preps)]
+            x, offsets, tile_off, sorted_slot, _ = inputs[i % len(inputs)]
+            ops.grouped_qmm(x, K=H, n_rows=2 * I, weight_format=L.FMT_INT4_G64,
+                            codes=pr.gu["codes"], sb=pr.gu["sb"], epilogue=L.EPI_SWIGLU,
+                            out_rows=N * k, regime=regime, slot_of=sorted_slot, slot_div=k,
+                            n_slots=N * k, offsets=offsets, tile_off=tile_off, n_experts=E, out=h)
+
+        for i in range(8):
+            launch(i)
+        torch.cuda.synchronize()
+        reps = args.kernel_reps
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            launch(i)
+        e1.record()
+        torch.cuda.synchronize()
+        kms = e0.elapsed_time(e1) / reps
+        u_k = sum(t[4] for t in inputs) / len(inputs)
+        per_expert = 2 * I * H * 9 // 16                   # int4 codes + bf16 scale/bias per 64
+        kbytes = u_k * per_expert + N * H * 2 + N * k * I * 2
+        kern = dict(name=f"qmm_small_kernel<int4,swiglu,ksplit>" if regime == L.REGIME_SMALL
+                    else "qmm_large_kernel<int4,swiglu>", us=kms * 1e3, bytes=kbytes, U=u_k)
+        log(f"gate_up kernel: {kms * 1e3:.1f} us, {kbytes / kms / 1e6:.0f} GB/s")
+
+    # ------------------------------------------------------------------ sweep
+    sweep = []
+    if args.only == "" and args.sweep:
+        for n2 in [int(v) for v in args.sweep.split(",") if v]:
+            st = max(10, args.steps // 4) if n2 <= 256 else max(5, args.steps // 20)
+            m2, u2, _, _ = run_batch(n2, st, 3, min(args.pool, 8))
+            U2 = sum(u2) / len(u2)
+            b2 = synth.algorithmic_bytes(cfg, U2, n2)
+            f2 = synth.algorithmic_flops(cfg, n2)
+            rec = dict(N=n2, ms_per_step=round(m2, 5), tokens_per_s=round(n2 / (m2 / 1e3), 1),
+                       distinct_experts=round(U2, 1), hbm_gbps=round(b2 / m2 / 1e6, 1),
+                       hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4),
+                       tflops=round(f2 / m2 / 1e9, 2),
+                       mfma_frac=round(f2 / m2 / 1e9 / BF16_PEAK_TFLOPS, 4))
+            sweep.append(rec)
+            log(f"sweep {rec}")
+
+    # ------------------------------------------------------------------ CPU baseline
+    cpu = None
+    if native_cpu is not None and args.only == "":
+        from oracle import torch_cpu
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        xs_cpu = [x.cpu() for x in xs[:args.cpu_reps]]
+        torch_cpu.moe_forward(xs_cpu[0][:2], native_cpu, cfg)      # warm-up
+        t1 = time.perf_counter()
+        for x in xs_cpu:
+            torch_cpu.moe_forward(x, native_cpu, cfg)
+        dt = time.perf_counter() - t1
+        cpu = dict(value=round(N * len(xs_cpu) / dt, 2), unit="tokens/s", cores=cores, kind="port",
+                   sample=f"{len(xs_cpu)} batches of {N} tokens of the {args.config} workload "
+                          f"(torch-CPU fp32 port, oracle/torch_cpu.py), {dt:.1f}s")
+        log(f"cpu baseline: {cpu}")
+
+    roofline = None
+    if kern is not None:
+        achieved = kern["bytes"] / (kern["us"] * 1e-6) / 1e9
+        roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                        frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
+                        kernel=kern["name"], kernel_us=round(kern["us"], 2),
+                        bytes_per_launch=int(kern["bytes"]), distinct_experts=round(kern["U"], 1))
+    line = {
+        "metric": METRIC,
+        "value": round(N / (ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps_layer,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}-decode-N{N}" if N <= 256 else f"{args.config}-prefill-N{N}",
+                   "hidden": H, "experts": E, "top_k": k, "inter": I, "shared_inter": Is,
+                   "batch_tokens": N, "weights": "int4-g64 affine, bf16 scale/bias",
+                   "layer_copies": args.layers, "input_pool": args.pool},
+        "layer_hbm_gbps": round(layer_bytes / ms / 1e6, 1),
+        "layer_hbm_frac": round(layer_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

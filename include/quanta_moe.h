@@ -1,0 +1,188 @@
+/*
+ * quanta_moe.h -- C ABI of the MI355X (gfx950) quantized sparse-MoE block.
+ *
+ * The reference (pmrjge/quanta) has no native boundary: its block is the Python function
+ * qwen35_moe (src/quanta/qwen35/moe.py:154-202) over MLX primitives (mx.gather_qmm,
+ * mx.argpartition, mx.argsort, mx.softmax, mx.dequantize). Each entry point below replaces
+ * one of those steps; the citation names the reference line it stands in for. The Python
+ * mirror of the reference surface (quanta_amd.moe.qwen35_moe / Qwen35MoEModule) binds these
+ * symbols with ctypes.
+ *
+ * Conventions (all entry points):
+ *  - Every pointer is a DEVICE pointer owned by the caller; the library never allocates.
+ *    Scratch memory comes from the caller through `ws` (size from qmoe_forward_workspace).
+ *  - `stream` is a hipStream_t (NULL = the default stream). Calls enqueue work and return
+ *    without synchronising the host.
+ *  - Return value: QMOE_OK (0), QMOE_EINVAL (-1, bad argument, nothing enqueued) or
+ *    QMOE_EHIP (-2, HIP launch error). qmoe_last_error() holds a thread-local message.
+ *  - bf16 tensors are passed as uint16_t bit patterns, packed int4 codes as uint32 words.
+ *  - No global mutable state besides the thread-local error string: calls on different
+ *    streams are independent; calls sharing workspace must be ordered by the caller.
+ */
+#ifndef QUANTA_MOE_H_
+#define QUANTA_MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMOE_ABI_VERSION 1
+
+#define QMOE_OK 0
+#define QMOE_EINVAL (-1)
+#define QMOE_EHIP (-2)
+
+/* scoring functions (cfg.scoring_func, src/quanta/qwen35/config.py:129) */
+#define QMOE_SCORE_SOFTMAX 0
+#define QMOE_SCORE_SIGMOID 1
+
+/* expert weight formats, both in this library's MFMA-tiled layout (see qmoe_tile_*) */
+#define QMOE_FMT_INT4_G64 0
+#define QMOE_FMT_BF16 1
+
+/* router weight storage */
+#define QMOE_ROUTER_BF16_TILED 0 /* bf16 [router_rows, H] tiled; row E = shared-expert gate */
+#define QMOE_ROUTER_F32 1        /* fp32 row-major [E, H]; shared gate fp32 [H] separately */
+
+/* grouped-qmm regimes */
+#define QMOE_REGIME_AUTO 0
+#define QMOE_REGIME_SMALL 1 /* 16-token m-tiles, weights streamed to registers (decode) */
+#define QMOE_REGIME_LARGE 2 /* 128x128 tiles, LDS-dequantised bf16 MFMA (prefill) */
+
+/* grouped-qmm epilogues */
+#define QMOE_EPI_SWIGLU 0 /* out[:, j] = bf16(silu(bf16(gate_j)) * bf16(up_j)), rows = [gate; up] */
+#define QMOE_EPI_BF16 1
+#define QMOE_EPI_F32 2
+
+/* Block configuration. Mirrors Qwen35Config's MoE fields (src/quanta/qwen35/config.py:125-130)
+ * plus the DeepSeek/GLM router fields (n_group, topk_group, routed_scaling_factor,
+ * src/quanta/glm/config.py:65,69). */
+typedef struct {
+  int32_t hidden;        /* H, multiple of 128 */
+  int32_t n_experts;     /* E <= 1024 */
+  int32_t top_k;         /* k (num_experts_per_tok or topk_override), 1 <= k <= min(E, 64) */
+  int32_t inter;         /* I, multiple of 128 */
+  int32_t shared_inter;  /* Is, 0 = no shared expert, else multiple of 128 */
+  int32_t scoring;       /* QMOE_SCORE_* */
+  int32_t norm_topk;     /* renormalise the k weights: w /= sum(w) + 1e-20 */
+  int32_t n_group;       /* expert groups (1 = plain top-k) */
+  int32_t topk_group;    /* groups kept when n_group > 1 */
+  float routed_scale;    /* routed_scaling_factor applied after renormalisation */
+  int32_t expert_format; /* QMOE_FMT_* */
+  int32_t router_format; /* QMOE_ROUTER_* */
+  int32_t router_rows;   /* rows of the tiled bf16 router (>= E + shared_gated, % 128 == 0) */
+  int32_t shared_gated;  /* 1: shared output scaled by sigmoid(x . shared_expert_gate) */
+  int32_t regime;        /* QMOE_REGIME_* for the routed experts (AUTO: small for N <= 256) */
+} qmoe_config_t;
+
+/* Prepared (resident) weights of one block; every array is device memory. */
+typedef struct {
+  const void* router_w;           /* see router_format */
+  const float* router_bias;       /* [E] e_score_correction_bias (selection only) or NULL */
+  const float* shared_gate_w;     /* [H] fp32, only with QMOE_ROUTER_F32 */
+  const uint32_t* gu_codes;       /* routed gate|up [E, 2I, H]: tiled int4 codes or tiled bf16 */
+  const uint16_t* gu_sb;          /* tiled scale/bias (int4 only) */
+  const uint32_t* dn_codes;       /* routed down [E, H, I] */
+  const uint16_t* dn_sb;
+  const uint16_t* sh_gu;          /* shared gate|up [2*Is, H] tiled bf16 */
+  const uint16_t* sh_dn;          /* shared down [H, Is] tiled bf16 */
+} qmoe_weights_t;
+
+int qmoe_abi_version(void);
+const char* qmoe_last_error(void);
+
+/* Whole block: y[N,H] = bf16(sum_s w[t,s] * expert_{idx[t,s]}(x[t]) + shared(x[t])).
+ * Replaces qwen35_moe (src/quanta/qwen35/moe.py:154-202) for one token chunk: router
+ * (:178), packed routed SwiGLU via two gather_qmm (:85-124, :189), fp32 combine (:191),
+ * gated shared expert (:145-151, :201) and the bf16 cast (:202). N <= 65535. */
+size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N);
+int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x, int64_t N,
+                 uint16_t* y, void* ws, size_t ws_bytes, void* stream);
+
+/* Top-k selection from router logits [N, ld_logits] (fp32): softmax or sigmoid scores,
+ * optional correction bias [E] for selection, group-limited selection when n_group > 1,
+ * renormalisation (+1e-20) and routed_scale. Outputs idx[N,k] (int32, canonical order:
+ * choice value descending, id ascending) and w[N,k] (fp32). With has_shared_gate, column E
+ * holds the shared-gate logit and shared_gate_out[N] = sigmoid(logit).
+ * Replaces qwen35_route (src/quanta/qwen35/moe.py:36-56) and MoEGate.__call__
+ * (src/quanta/modeling/moe.py:33-44; src/quanta/glm/moe.py:44-55). */
+int qmoe_router_topk(const float* logits, int64_t ld_logits, const float* bias, int64_t N, int E,
+                     int k, int scoring, int n_group, int topk_group, int norm_topk,
+                     float routed_scale, int has_shared_gate, int32_t* idx, float* w,
+                     float* shared_gate_out, void* stream);
+
+/* Router logits for an fp32 router weight [E,H] (row-major): logits[t, e] = x[t] . wr[e] in
+ * fp32; column E = x[t] . shared_gate when shared_gate != NULL. Replaces the fp32 matmul
+ * xf.astype(f32) @ gate_w.astype(f32).T (src/quanta/qwen35/moe.py:47). bf16 routers go through
+ * qmoe_grouped_qmm with QMOE_EPI_F32 (products of bf16 are exact in fp32). */
+int qmoe_router_logits_f32(const uint16_t* x, const float* wr, const float* shared_gate,
+                           int64_t N, int H, int E, float* logits, int64_t ld_logits,
+                           void* stream);
+
+/* Stable permute of the N*k (token, slot) pairs by expert id. Outputs counts[E],
+ * offsets[E+1], tile_off[E+1] (prefix of ceil(count/m_tile)), sorted_slot[N*k]
+ * (sorted position -> slot t*k+s) and inv[N*k] (slot -> sorted position, -1 for ids outside
+ * [0,E)). Requires distinct experts within each token (true of any top-k router).
+ * Replaces order = argsort(exp), inv = argsort(order) (src/quanta/modeling/moe.py:81-85;
+ * src/quanta/dsv4/moe.py:107-112). */
+int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_t* counts,
+                 int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
+                 void* stream);
+
+/* Grouped matmul over expert segments: out[p, :] = act[row(p)] . W_e^T for sorted positions
+ * p of expert e (offsets/tile_off from qmoe_permute; m_tile 16 for QMOE_REGIME_SMALL, 128 for
+ * QMOE_REGIME_LARGE), with row(p) = slot_of[p] / slot_div (slot_of NULL: row(p) = p). With
+ * offsets == NULL the call is one dense segment of dense_rows rows. W is tiled int4-g64
+ * (codes + sb) or tiled bf16 (codes), [n_experts][n_rows][K]. Epilogue QMOE_EPI_SWIGLU treats
+ * rows [0, n_rows/2) as gate and [n_rows/2, n_rows) as up.
+ * Replaces mx.gather_qmm(..., transpose=True, group_size=64, bits=4)
+ * (src/quanta/qwen35/moe.py:117-123, src/quanta/dsv4/moe.py:119-124) with the SwiGLU of
+ * src/quanta/qwen35/moe.py:59-63 fused, and mx.gather_mm (src/quanta/qwen35/moe.py:79-81). */
+int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_of, int slot_div,
+                     int64_t n_slots, const int32_t* offsets, const int32_t* tile_off,
+                     int n_experts, int64_t dense_rows, int K, int n_rows, int weight_format,
+                     const void* codes, const uint16_t* sb, int epilogue, void* out, int ld_out,
+                     int regime, void* stream);
+
+/* y[t] = bf16(sum_s w[t,s] * d[inv[t*k+s]] + shared_gate[t] * shared_out[t]) (fp32 sums in
+ * slot order; shared_out/shared_gate may be NULL). Replaces the combine
+ * mx.sum(slots.astype(f32) * w[..., None], axis=1) and the final add/cast
+ * (src/quanta/qwen35/moe.py:191,201-202; sorted unpermute src/quanta/modeling/moe.py:94-97). */
+int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* w, int64_t N, int k, int H,
+                 const uint16_t* shared_out, const float* shared_gate, uint16_t* y, void* stream);
+
+/* Bit-exact dequant of a native affine int4-g64 stack: out[rows, in] bf16 =
+ * bf16(fma(scale, code, bias)). Replaces mx.dequantize (src/quanta/bake/quant.py:32-36;
+ * src/quanta/qwen35/artifact.py:105-115). */
+int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias, int64_t rows,
+                 int64_t in_features, int bits, int group_size, uint16_t* out, void* stream);
+
+/* One-time layout transform of a native int4-g64 stack [n_mats][rows][in] (packed u32
+ * [.., in/8], scale/bias bf16 [.., in/64]) into the MFMA-tiled layout (codes: same byte count;
+ * sb: [n_mats][rows/16][in/128][16][2][2] bf16). rows % 16 == 0, in % 128 == 0. Stands in for
+ * holding the packed triplet verbatim (Qwen35MoEModule.set_experts_packed,
+ * src/quanta/qwen35/model.py:49-55; Qwen35Artifact.moe_packed,
+ * src/quanta/qwen35/artifact.py:205-229). */
+int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                   int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                   uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
+
+/* Inverse check of qmoe_tile_int4: tiled stack -> bf16 [n_mats][rows][in], bit-identical to
+ * qmoe_dequant of the native stack. Test/inspection entry point. */
+int qmoe_dequant_tiled(const uint32_t* tiled_codes, const uint16_t* tiled_sb, int64_t n_mats,
+                       int64_t rows, int64_t in_features, uint16_t* out, void* stream);
+
+/* Row-major bf16 [n_mats][rows][in] -> MFMA-tiled [n_mats][rows/16][in/32][64][8].
+ * rows % 16 == 0, in % 32 == 0. Used for the shared expert, the bf16 router and bf16
+ * routed experts (set_experts, src/quanta/qwen35/model.py:46-47). */
+int qmoe_tile_bf16(const uint16_t* w, int64_t n_mats, int64_t rows, int64_t in_features,
+                   uint16_t* tiled, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUANTA_MOE_H_ */

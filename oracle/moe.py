@@ -1,0 +1,241 @@
+"""Oracle: float64 restatement of the quantized sparse-MoE block.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Arrays holding bf16 data are float64 arrays whose values are exactly representable in bf16.
+Every function cites the reference lines it restates. The bf16 materialisation points of the
+reference's dtype flow are kept (`round_bf16` where MLX produces a bf16 array):
+  gu = bf16(x . deq(W_gu)^T)       (gather_qmm output follows the bf16 scale dtype)
+  h  = bf16(silu(g) * u)           (bf16 elementwise ops; here one rounding)
+  d  = bf16(h . deq(W_d)^T)
+  routed = sum_s f32(d) * w        (float32 combine; here float64)
+  shared = bf16 SwiGLU chain, times sigmoid(x_f32 . g_f32)
+  y = bf16(routed + shared)
+The GPU path keeps float32 accumulators at the same points, so results agree to bf16
+rounding, which the BASELINE tolerances (max-abs 2e-2, rel-L2 5e-3) bound.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.quant import dequant_exact, round_bf16
+
+
+def _silu(v: np.ndarray) -> np.ndarray:
+    """silu(x) = x * sigmoid(x) (`src/quanta/qwen35/moe.py:32-33`)."""
+    return v / (1.0 + np.exp(-v))
+
+
+def _sigmoid(v: np.ndarray) -> np.ndarray:
+    return 1.0 / (1.0 + np.exp(-v))
+
+
+# ----------------------------------------------------------------------------- routing
+
+
+def topk_canonical(choice: np.ndarray, k: int) -> np.ndarray:
+    """Top-k indices per row in this build's canonical order: value descending, id ascending
+    on ties. `mx.argpartition(-s, k-1)[:, :k]` (`src/quanta/qwen35/moe.py:52`) returns the same
+    SET in an unspecified order (parity unpinned at the MLX boundary for the order); the
+    reference's own routing gate compares sets (`parity/glm_moe_test.py:98-102`)."""
+    n, e = choice.shape
+    ids = np.broadcast_to(np.arange(e), choice.shape)
+    order = np.lexsort((ids, -choice), axis=-1)
+    return order[:, :k]
+
+
+def group_limit(choice: np.ndarray, n_group: int, topk_group: int) -> np.ndarray:
+    """Group-limited selection mask (DeepSeek-V3 `noaux_tc`).
+
+    Follows transformers 5.15.0 `models/deepseek_v3/modeling_deepseek_v3.py:149-164` (the
+    reference asserts n_group == 1, `src/quanta/modeling/moe.py:34`): group score = sum of the
+    two largest choice values in each of the n_group contiguous expert groups; keep the
+    topk_group best groups (canonical order on ties); every expert outside them gets -inf.
+    """
+    n, e = choice.shape
+    g = choice.reshape(n, n_group, e // n_group)
+    top2 = np.sort(g, axis=-1)[..., -2:].sum(axis=-1)
+    gidx = topk_canonical(top2, topk_group)
+    keep = np.zeros((n, n_group), dtype=bool)
+    np.put_along_axis(keep, gidx, True, axis=-1)
+    mask = np.repeat(keep, e // n_group, axis=-1)
+    return np.where(mask, choice, -np.inf)
+
+
+def route(x: np.ndarray, wr: np.ndarray, *, k: int, scoring: str = "softmax",
+          norm_topk: bool = True, bias: np.ndarray | None = None, n_group: int = 1,
+          topk_group: int = 1, scale: float = 1.0):
+    """Router -> (idx [N,k] int32, w [N,k] float64, logits, scores).
+
+    softmax (`src/quanta/qwen35/moe.py:47-55`): logits = x . Wr^T in float (here float64),
+    scores = softmax(logits); top-k of scores; w = scores[idx]; if norm_topk,
+    w /= sum(w) + 1e-20.
+    sigmoid + correction bias (`src/quanta/modeling/moe.py:36-43`, `src/quanta/glm/moe.py:48-55`):
+    scores = sigmoid(logits); select by scores + bias (optionally group-limited); weights are
+    the bias-free scores, renormalised, then times `scale` (routed_scaling_factor).
+    """
+    logits = x.astype(np.float64) @ wr.astype(np.float64).T
+    if scoring == "softmax":
+        m = logits.max(axis=-1, keepdims=True)
+        p = np.exp(logits - m)
+        scores = p / p.sum(axis=-1, keepdims=True)
+    elif scoring == "sigmoid":
+        scores = _sigmoid(logits)
+    else:
+        raise ValueError(scoring)
+    choice = scores + bias[None, :].astype(np.float64) if bias is not None else scores.copy()
+    if n_group > 1:
+        choice = group_limit(choice, n_group, topk_group)
+    idx = topk_canonical(choice, k)
+    w = np.take_along_axis(scores, idx, axis=-1)
+    if norm_topk:
+        w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
+    w = w * scale
+    return idx.astype(np.int32), w, logits, scores, choice
+
+
+def route_margin(choice: np.ndarray, k: int) -> np.ndarray:
+    """Per-row gap between the k-th and (k+1)-th largest choice values (inf when k == E).
+    Rows whose gap is below the float32 evaluation error of the logits can legitimately
+    select a different k-th expert on the GPU; tests report and exclude them."""
+    s = -np.sort(-choice, axis=-1)
+    if k >= choice.shape[1]:
+        return np.full(choice.shape[0], np.inf)
+    return s[:, k - 1] - s[:, k]
+
+
+# ----------------------------------------------------------------------------- permute
+
+
+def permute(idx: np.ndarray, n_experts: int):
+    """Stable sort of the flattened (token, slot) list by expert id.
+
+    Restates `order = argsort(exp)` / `inv = argsort(order)` (`src/quanta/modeling/moe.py:81-85`,
+    `src/quanta/dsv4/moe.py:68,107-110`; MLX argsort is stable per `dsv4/moe.py:68`).
+    Returns counts[E], offsets[E+1], order[mc] (sorted position -> slot), inv[mc]
+    (slot -> sorted position).
+    """
+    exp = np.asarray(idx).reshape(-1).astype(np.int64)
+    order = np.argsort(exp, kind="stable")
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    counts = np.bincount(exp, minlength=n_experts)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    return (counts.astype(np.int32), offsets.astype(np.int32), order.astype(np.int32),
+            inv.astype(np.int32))
+
+
+# ----------------------------------------------------------------------------- expert math
+
+
+def gather_qmm(xrows: np.ndarray, experts: np.ndarray, packed: np.ndarray, scale: np.ndarray,
+               bias: np.ndarray, in_features: int, *, round_out: bool = True) -> np.ndarray:
+    """y[m] = x[m] . (s*q + b)[experts[m]]^T per row, float64, rounded to bf16.
+
+    Restates `mx.gather_qmm(x, packed, scale, bias, rhs_indices=exp, transpose=True)`
+    (`src/quanta/qwen35/moe.py:117-123`): the weight stack is [E, out, in] affine int4 with
+    bf16 scale/bias per 64 along `in`; output dtype follows the bf16 scale dtype.
+    """
+    experts = np.asarray(experts).reshape(-1)
+    out = np.zeros((xrows.shape[0], packed.shape[1]), dtype=np.float64)
+    for e in np.unique(experts):
+        sel = experts == e
+        w = dequant_exact(packed[e], scale[e], bias[e], in_features)
+        out[sel] = xrows[sel].astype(np.float64) @ w.T
+    return round_bf16(out) if round_out else out
+
+
+def gather_mm(xrows: np.ndarray, experts: np.ndarray, stack: np.ndarray) -> np.ndarray:
+    """bf16 sibling (`mx.gather_mm`, `src/quanta/qwen35/moe.py:66-82`): y[m] = x[m] . W[e]^T."""
+    experts = np.asarray(experts).reshape(-1)
+    out = np.zeros((xrows.shape[0], stack.shape[1]), dtype=np.float64)
+    for e in np.unique(experts):
+        sel = experts == e
+        out[sel] = xrows[sel].astype(np.float64) @ stack[e].astype(np.float64).T
+    return round_bf16(out)
+
+
+def swiglu(gu: np.ndarray, inter: int) -> np.ndarray:
+    """SwiGLU on the fused gate|up activation (`src/quanta/qwen35/moe.py:59-63`):
+    gate = first `inter` columns, up = the rest; h = bf16(silu(g) * u)."""
+    g = gu[:, :inter]
+    u = gu[:, inter:]
+    return round_bf16(_silu(g) * u)
+
+
+def combine(d: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """routed[t] = sum_s d[t*k+s] * w[t,s] (`src/quanta/qwen35/moe.py:191`), float64."""
+    n, k = w.shape
+    return (d.reshape(n, k, -1) * w[:, :, None]).sum(axis=1)
+
+
+def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
+                  gate: np.ndarray | None):
+    """Shared SwiGLU expert (`src/quanta/qwen35/moe.py:145-151`): bf16 chain
+    out = bf16(bf16(silu(bf16(x Wg^T)) * bf16(x Wu^T)) Wd^T), then times
+    sg = sigmoid(x_f32 . g_f32) when a gate is given (Qwen); DeepSeek/GLM shared experts are
+    ungated (`src/quanta/glm/moe.py:83-84`). Returns (scaled float64 out, out bf16, sg)."""
+    x = x.astype(np.float64)
+    g = round_bf16(x @ wg.astype(np.float64).T)
+    u = round_bf16(x @ wu.astype(np.float64).T)
+    h = round_bf16(_silu(g) * u)
+    out = round_bf16(h @ wd.astype(np.float64).T)
+    if gate is None:
+        return out, out, None
+    sg = _sigmoid(x @ gate.astype(np.float64).reshape(-1))
+    return out * sg[:, None], out, sg
+
+
+# ----------------------------------------------------------------------------- the block
+
+
+def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "softmax",
+                norm_topk: bool = True, n_group: int = 1, topk_group: int = 1,
+                scale: float = 1.0):
+    """Whole block y = bf16(routed + shared) for x [N, H] (`src/quanta/qwen35/moe.py:154-202`).
+
+    `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
+      gate [E,H]; gu_packed [E,2I,H/8], gu_scale/gu_bias [E,2I,H/64] (bf16 bits);
+      dn_packed [E,H,I/8], dn_scale/dn_bias [E,H,I/64]; optional e_score_correction_bias [E];
+      optional shared_gate_proj [Is,H], shared_up_proj [Is,H], shared_down_proj [H,Is],
+      shared_expert_gate [1,H].
+    Returns (y bf16-valued float64 [N,H], dict of intermediates).
+    """
+    n, hdim = x.shape
+    idx, w, logits, scores, choice = route(
+        x, p["gate"], k=k, scoring=scoring, norm_topk=norm_topk,
+        bias=p.get("e_score_correction_bias"), n_group=n_group, topk_group=topk_group,
+        scale=scale)
+    exp = idx.reshape(-1)
+    tok = np.repeat(np.arange(n), k)
+    gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim)
+    h = swiglu(gu, inter)
+    d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter)
+    routed = combine(d, w)
+    y = routed.copy()
+    sh = None
+    if p.get("shared_gate_proj") is not None:
+        sh, sh_out, sg = shared_expert(x, p["shared_gate_proj"], p["shared_up_proj"],
+                                       p["shared_down_proj"], p.get("shared_expert_gate"))
+        y = y + sh
+    inter_d = dict(idx=idx, w=w, logits=logits, scores=scores, choice=choice, gu=gu, h=h, d=d,
+                   routed=routed, shared=sh)
+    return round_bf16(y), inter_d
+
+
+def moe_dense_reference(x: np.ndarray, idx: np.ndarray, w: np.ndarray, gu_dense: np.ndarray,
+                        dn_dense: np.ndarray, inter: int) -> np.ndarray:
+    """Run-every-expert oracle (`src/quanta/qwen35/moe.py:127-142`): every expert on every
+    token, combined with the routing weight scattered onto the chosen experts (0 elsewhere).
+    `gu_dense` [E,2I,H] / `dn_dense` [E,H,I] are dequantized float64 stacks. Unrounded float64
+    throughout; this is the cross-check for the sparse gather path, not a bf16 flow."""
+    n = x.shape[0]
+    e = gu_dense.shape[0]
+    gu = np.einsum("nh,eoh->neo", x.astype(np.float64), gu_dense)
+    hh = _silu(gu[..., :inter]) * gu[..., inter:]
+    d = np.einsum("nei,ehi->neh", hh, dn_dense)
+    gates = np.zeros((n, e))
+    rows = np.repeat(np.arange(n), idx.shape[1])
+    gates[rows, idx.reshape(-1)] = w.reshape(-1)
+    return (d * gates[:, :, None]).sum(axis=1)

@@ -1,0 +1,125 @@
+"""ctypes binding of the C ABI in include/quanta_moe.h (the in-tree `_qmoe.so`).
+
+The library is loaded on first use. There is no CPU fallback: if the shared object is missing or
+cannot be loaded, every entry point raises, naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("_qmoe.so")
+HEADER = Path(__file__).resolve().parent.parent / "include" / "quanta_moe.h"
+
+QMOE_OK, QMOE_EINVAL, QMOE_EHIP = 0, -1, -2
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+FMT_INT4_G64, FMT_BF16 = 0, 1
+ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
+REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
+EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
+SMALL_M_TILE, LARGE_M_TILE = 16, 128
+
+
+class QmoeConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int32),
+        ("n_experts", ctypes.c_int32),
+        ("top_k", ctypes.c_int32),
+        ("inter", ctypes.c_int32),
+        ("shared_inter", ctypes.c_int32),
+        ("scoring", ctypes.c_int32),
+        ("norm_topk", ctypes.c_int32),
+        ("n_group", ctypes.c_int32),
+        ("topk_group", ctypes.c_int32),
+        ("routed_scale", ctypes.c_float),
+        ("expert_format", ctypes.c_int32),
+        ("router_format", ctypes.c_int32),
+        ("router_rows", ctypes.c_int32),
+        ("shared_gated", ctypes.c_int32),
+        ("regime", ctypes.c_int32),
+    ]
+
+
+class QmoeWeights(ctypes.Structure):
+    _fields_ = [
+        ("router_w", ctypes.c_void_p),
+        ("router_bias", ctypes.c_void_p),
+        ("shared_gate_w", ctypes.c_void_p),
+        ("gu_codes", ctypes.c_void_p),
+        ("gu_sb", ctypes.c_void_p),
+        ("dn_codes", ctypes.c_void_p),
+        ("dn_sb", ctypes.c_void_p),
+        ("sh_gu", ctypes.c_void_p),
+        ("sh_dn", ctypes.c_void_p),
+    ]
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/quanta_moe.h
+SIGNATURES = {
+    "qmoe_abi_version": (_I, []),
+    "qmoe_last_error": (ctypes.c_char_p, []),
+    "qmoe_forward_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),
+    "qmoe_forward": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _I64, _P, _P,
+                          ctypes.c_size_t, _P]),
+    "qmoe_router_topk": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P]),
+    "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
+    "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _I, _P,
+                              _I, _I, _P]),
+    "qmoe_combine": (_I, [_P, _P, _P, _I64, _I, _I, _P, _P, _P, _P]),
+    "qmoe_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
+    "qmoe_tile_int4": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "qmoe_dequant_tiled": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "qmoe_tile_bf16": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/quanta_moe.h."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+def load() -> ctypes.CDLL:
+    """Load `_qmoe.so` (once) and attach the ctypes signatures. Raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"quanta_amd HIP extension not built ({LIB_PATH} missing); run "
+                "`python -m quanta_amd.build` (or __graft_entry__.build()) first")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.qmoe_abi_version() != 1:
+            raise RuntimeError("quanta_amd: ABI version mismatch; rebuild the extension")
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Translate a C-ABI status into a Python exception (ValueError for bad arguments)."""
+    if rc == QMOE_OK:
+        return
+    msg = load().qmoe_last_error().decode(errors="replace")
+    if rc == QMOE_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: HIP error: {msg}")

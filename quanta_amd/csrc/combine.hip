@@ -1,0 +1,316 @@
+// Unpermute + weighted combine + gated shared expert + bf16 cast, and the C-ABI entry points
+// for the grouped qmm and the whole-block forward.
+//
+// Reference: routed[t] = sum_s f32(d[t, s]) * w[t, s] (src/quanta/qwen35/moe.py:191; the sorted
+// variant restores slot order with d[inv] first, src/quanta/modeling/moe.py:94-97);
+// y = bf16(routed + f32(shared_out) * sigmoid(x . g)) (src/quanta/qwen35/moe.py:145-151,201-202).
+// The combine gathers each slot's row through inv (no atomics), summing in slot order, so the
+// output is deterministic.
+#include <string>
+
+#include "qmoe_internal.h"
+#include "../../include/quanta_moe.h"
+
+namespace qmoe {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(const std::string& msg) {
+  set_error(msg);
+  return QMOE_EINVAL;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error(std::string(what) + ": " + hipGetErrorString(err));
+    return QMOE_EHIP;
+  }
+  return QMOE_OK;
+}
+
+__global__ void __launch_bounds__(256) combine_kernel(
+    const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
+    int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ shared_out,
+    const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
+  const int t = blockIdx.y;
+  const int h8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (h8 >= H) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < k; ++s) {
+    const int64_t m = static_cast<int64_t>(t) * k + s;
+    const int pos = inv[m];
+    if (pos < 0 || pos >= n_pos) continue;
+    const float ws = w[m];
+    const uint4 v = *reinterpret_cast<const uint4*>(d + static_cast<int64_t>(pos) * H + h8);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] += bf16lo_to_f32(vv[j]) * ws;
+      acc[2 * j + 1] += bf16hi_to_f32(vv[j]) * ws;
+    }
+  }
+  if (shared_out) {
+    const float g = shared_gate ? shared_gate[t] : 1.0f;
+    const uint4 v = *reinterpret_cast<const uint4*>(shared_out + static_cast<int64_t>(t) * H + h8);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] += bf16lo_to_f32(vv[j]) * g;
+      acc[2 * j + 1] += bf16hi_to_f32(vv[j]) * g;
+    }
+  }
+  uint4 o;
+  o.x = pack_bf16x2(acc[0], acc[1]);
+  o.y = pack_bf16x2(acc[2], acc[3]);
+  o.z = pack_bf16x2(acc[4], acc[5]);
+  o.w = pack_bf16x2(acc[6], acc[7]);
+  *reinterpret_cast<uint4*>(y + static_cast<int64_t>(t) * H + h8) = o;
+}
+
+int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
+                   const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
+                   hipStream_t stream) {
+  dim3 grid((H / 8 + 255) / 256, N);
+  combine_kernel<<<grid, 256, 0, stream>>>(d, inv, w, N, k, H, static_cast<int64_t>(N) * k,
+                                           shared_out, shared_gate, y);
+  return check_launch("combine");
+}
+
+int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int topk_group);
+
+// ------------------------------------------------------------------ forward workspace layout
+struct WsLayout {
+  size_t logits, idx, w, sg, counts, offsets, tile_off, sorted, inv, h, d, sh_h, sh_out, total;
+};
+
+static inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
+  WsLayout L{};
+  const int64_t mc = N * c.top_k;
+  const int64_t ld = (c.router_format == QMOE_ROUTER_F32) ? c.n_experts + 1 : c.router_rows;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  L.logits = take(static_cast<size_t>(N) * ld * 4);
+  L.idx = take(static_cast<size_t>(mc) * 4);
+  L.w = take(static_cast<size_t>(mc) * 4);
+  L.sg = take(static_cast<size_t>(N) * 4);
+  L.counts = take(static_cast<size_t>(c.n_experts) * 4);
+  L.offsets = take(static_cast<size_t>(c.n_experts + 1) * 4);
+  L.tile_off = take(static_cast<size_t>(c.n_experts + 1) * 4);
+  L.sorted = take(static_cast<size_t>(mc) * 4);
+  L.inv = take(static_cast<size_t>(mc) * 4);
+  L.h = take(static_cast<size_t>(mc) * c.inter * 2);
+  L.d = take(static_cast<size_t>(mc) * c.hidden * 2);
+  L.sh_h = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.shared_inter : 0) * 2);
+  L.sh_out = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.hidden : 0) * 2);
+  L.total = o;
+  return L;
+}
+
+static int validate_config(const qmoe_config_t& c) {
+  const int rc = validate_routing(1, c.hidden, c.n_experts, c.top_k, c.scoring, c.n_group,
+                                  c.topk_group);
+  if (rc) return rc;
+  if (c.hidden % 128) return fail("config: hidden % 128 == 0 required");
+  if (c.inter <= 0 || c.inter % 128) return fail("config: inter % 128 == 0 required");
+  if (c.shared_inter < 0 || c.shared_inter % 128) return fail("config: shared_inter % 128 == 0 required");
+  if (c.expert_format != QMOE_FMT_INT4_G64 && c.expert_format != QMOE_FMT_BF16)
+    return fail("config: expert_format must be int4-g64 (0) or bf16 (1)");
+  if (c.router_format == QMOE_ROUTER_BF16_TILED) {
+    if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 128)
+      return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 128");
+  } else if (c.router_format != QMOE_ROUTER_F32) {
+    return fail("config: unknown router_format");
+  }
+  if (c.regime < QMOE_REGIME_AUTO || c.regime > QMOE_REGIME_LARGE) return fail("config: bad regime");
+  return 0;
+}
+
+}  // namespace qmoe
+
+using namespace qmoe;
+
+extern "C" const char* qmoe_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int qmoe_abi_version(void) { return QMOE_ABI_VERSION; }
+
+extern "C" int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* w, int64_t N, int k,
+                            int H, const uint16_t* shared_out, const float* shared_gate,
+                            uint16_t* y, void* stream) {
+  if (N <= 0 || N > 65535 || k <= 0 || H <= 0 || H % 8) return fail("qmoe_combine: need 0 < N <= 65535, H % 8 == 0");
+  if (!d || !inv || !w || !y) return fail("qmoe_combine: null pointer");
+  return launch_combine(d, inv, w, static_cast<int>(N), k, H, shared_out, shared_gate, y,
+                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_of,
+                                int slot_div, int64_t n_slots, const int32_t* offsets,
+                                const int32_t* tile_off, int n_experts, int64_t dense_rows,
+                                int K, int n_rows, int weight_format, const void* codes,
+                                const uint16_t* sb, int epilogue, void* out, int ld_out,
+                                int regime, void* stream) {
+  if (!act || !codes || !out) return fail("qmoe_grouped_qmm: null pointer");
+  if (weight_format == QMOE_FMT_INT4_G64 && !sb) return fail("qmoe_grouped_qmm: int4 needs sb");
+  if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16)
+    return fail("qmoe_grouped_qmm: bad weight_format");
+  if (epilogue < QMOE_EPI_SWIGLU || epilogue > QMOE_EPI_F32) return fail("qmoe_grouped_qmm: bad epilogue");
+  if (regime != QMOE_REGIME_SMALL && regime != QMOE_REGIME_LARGE)
+    return fail("qmoe_grouped_qmm: regime must be small (1) or large (2)");
+  if (slot_of && slot_div <= 0) return fail("qmoe_grouped_qmm: slot_div must be positive");
+  const int out_cols = (epilogue == QMOE_EPI_SWIGLU) ? n_rows / 2 : n_rows;
+  if (ld_out < out_cols) return fail("qmoe_grouped_qmm: ld_out too small");
+  QmmArgs a{};
+  a.act = act;
+  a.act_rows = act_rows;
+  a.slot_of = slot_of;
+  a.slot_div = slot_div > 0 ? slot_div : 1;
+  a.n_slots = n_slots;
+  a.offsets = offsets;
+  a.tile_off = tile_off;
+  a.dense_rows = dense_rows;
+  a.n_experts = offsets ? n_experts : 1;
+  a.K = K;
+  a.n_rows = n_rows;
+  a.codes = codes;
+  a.sb = sb;
+  a.out = out;
+  a.ld_out = ld_out;
+  const int m_tile = (regime == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
+  int64_t bound;
+  if (offsets) {
+    if (!tile_off || n_experts <= 0) return fail("qmoe_grouped_qmm: segmented mode needs tile_off");
+    bound = mtile_upper_bound(n_slots, n_experts, m_tile);
+  } else {
+    if (dense_rows <= 0) return fail("qmoe_grouped_qmm: dense_rows must be positive");
+    bound = (dense_rows + m_tile - 1) / m_tile;
+  }
+  return launch_qmm(a, weight_format, epilogue, regime, bound, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
+  if (!cfg || N <= 0) return 0;
+  return ws_layout(*cfg, N).total;
+}
+
+static int pick_regime(const qmoe_config_t& c, int64_t N) {
+  if (c.regime != QMOE_REGIME_AUTO) return c.regime;
+  return (N <= 256) ? QMOE_REGIME_SMALL : QMOE_REGIME_LARGE;
+}
+
+extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
+                            int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream_) {
+  if (!cfg || !wts || !x || !y || !ws) return fail("qmoe_forward: null pointer");
+  const qmoe_config_t& c = *cfg;
+  int rc = validate_config(c);
+  if (rc) return rc;
+  if (N <= 0 || N > 65535) return fail("qmoe_forward: 0 < N <= 65535 tokens per call");
+  const WsLayout L = ws_layout(c, N);
+  if (ws_bytes < L.total) return fail("qmoe_forward: workspace too small");
+  if (!wts->router_w || !wts->gu_codes || !wts->dn_codes) return fail("qmoe_forward: missing weights");
+  if (c.expert_format == QMOE_FMT_INT4_G64 && (!wts->gu_sb || !wts->dn_sb))
+    return fail("qmoe_forward: int4 experts need scale/bias");
+  if (c.shared_inter > 0 && (!wts->sh_gu || !wts->sh_dn)) return fail("qmoe_forward: missing shared expert");
+  if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
+    return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
+
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  char* base = static_cast<char*>(ws);
+  float* logits = reinterpret_cast<float*>(base + L.logits);
+  int32_t* idx = reinterpret_cast<int32_t*>(base + L.idx);
+  float* wv = reinterpret_cast<float*>(base + L.w);
+  float* sg = reinterpret_cast<float*>(base + L.sg);
+  int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
+  int32_t* offsets = reinterpret_cast<int32_t*>(base + L.offsets);
+  int32_t* tile_off = reinterpret_cast<int32_t*>(base + L.tile_off);
+  int32_t* sorted = reinterpret_cast<int32_t*>(base + L.sorted);
+  int32_t* inv = reinterpret_cast<int32_t*>(base + L.inv);
+  uint16_t* h = reinterpret_cast<uint16_t*>(base + L.h);
+  uint16_t* d = reinterpret_cast<uint16_t*>(base + L.d);
+  uint16_t* sh_h = reinterpret_cast<uint16_t*>(base + L.sh_h);
+  uint16_t* sh_out = reinterpret_cast<uint16_t*>(base + L.sh_out);
+
+  const int n = static_cast<int>(N);
+  const int64_t mc = N * c.top_k;
+  const int regime = pick_regime(c, N);
+  const int m_tile = (regime == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
+  const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4 : FMT_BF16;
+  const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
+
+  // 1. router logits (+ the shared-expert gate logit in column E)
+  int ld = 0;
+  if (c.router_format == QMOE_ROUTER_F32) {
+    ld = c.n_experts + 1;
+    rc = launch_router_f32(x, static_cast<const float*>(wts->router_w),
+                           has_sg ? wts->shared_gate_w : nullptr, n, c.hidden, c.n_experts, logits,
+                           ld, stream);
+  } else {
+    ld = c.router_rows;
+    QmmArgs a{};
+    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
+    a.K = c.hidden; a.n_rows = c.router_rows; a.codes = wts->router_w; a.out = logits; a.ld_out = ld;
+    const int rreg = (N <= 256) ? QMOE_REGIME_SMALL : QMOE_REGIME_LARGE;
+    const int rt = (rreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
+    rc = launch_qmm(a, FMT_BF16, EPI_F32, rreg, (N + rt - 1) / rt, stream);
+  }
+  if (rc) return rc;
+  // 2. top-k
+  rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
+                   c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream);
+  if (rc) return rc;
+  // 3. stable permute by expert
+  rc = launch_permute(idx, n, c.top_k, c.n_experts, m_tile, counts, offsets, tile_off, sorted, inv,
+                      stream);
+  if (rc) return rc;
+  const int64_t bound = mtile_upper_bound(mc, c.n_experts, m_tile);
+  // 4. routed gate_up + SwiGLU -> h (sorted order)
+  {
+    QmmArgs a{};
+    a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
+    a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+    a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
+    a.out = h; a.ld_out = c.inter;
+    rc = launch_qmm(a, wfmt, EPI_SWIGLU, regime, bound, stream);
+    if (rc) return rc;
+  }
+  // 5. shared expert gate_up + SwiGLU
+  const int sreg = (N <= 256) ? QMOE_REGIME_SMALL : QMOE_REGIME_LARGE;
+  const int st = (sreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
+  if (c.shared_inter > 0) {
+    QmmArgs a{};
+    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
+    a.K = c.hidden; a.n_rows = 2 * c.shared_inter; a.codes = wts->sh_gu; a.out = sh_h;
+    a.ld_out = c.shared_inter;
+    rc = launch_qmm(a, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, stream);
+    if (rc) return rc;
+  }
+  // 6. routed down -> d (sorted order)
+  {
+    QmmArgs a{};
+    a.act = h; a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
+    a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+    a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
+    a.out = d; a.ld_out = c.hidden;
+    rc = launch_qmm(a, wfmt, EPI_BF16, regime, bound, stream);
+    if (rc) return rc;
+  }
+  // 7. shared expert down
+  if (c.shared_inter > 0) {
+    QmmArgs a{};
+    a.act = sh_h; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
+    a.K = c.shared_inter; a.n_rows = c.hidden; a.codes = wts->sh_dn; a.out = sh_out;
+    a.ld_out = c.hidden;
+    rc = launch_qmm(a, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, stream);
+    if (rc) return rc;
+  }
+  // 8. unpermute + weighted combine + gated shared + bf16
+  return launch_combine(d, inv, wv, n, c.top_k, c.hidden, c.shared_inter > 0 ? sh_out : nullptr,
+                        has_sg ? sg : nullptr, y, stream);
+}

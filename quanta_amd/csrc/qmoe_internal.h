@@ -1,0 +1,143 @@
+// Internal helpers shared by the quantized-MoE HIP sources (gfx950 / CDNA4 only).
+//
+// Layout vocabulary used throughout:
+//   * "native" int4 stack  : packed u32 [mats][rows][K/8], scale/bias bf16 [mats][rows][K/64]
+//                            (the reference's affine_packed triplet, LSB-first nibbles).
+//   * "tiled" int4 stack   : codes u32 [mats][rows/16][K/128][64 lanes][4 words] and
+//                            sb bf16 [mats][rows/16][K/128][16 rows][2 groups][scale,bias].
+//                            One 16-row x 128-K superblock is 1 KiB of codes, read by one
+//                            wavefront as a single contiguous dwordx4 load per lane.
+//                            Lane l (row l%16, lane group g=l/16) holds words {2g,2g+1} of
+//                            group 2p followed by words {2g,2g+1} of group 2p+1.
+//   * "tiled" bf16 matrix  : [mats][rows/16][K/32][64 lanes][8 bf16]; lane l holds
+//                            W[16R + l%16][32c + 8(l/16) .. +8).
+// Both tiled layouts put each lane's MFMA B-fragment (weight row = l%16, 8 consecutive K of
+// one 64-wide scale group) in 16 contiguous bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+namespace qmoe {
+
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+// Native 16-byte vector (HIP's uint4 is a struct whose copies lower to memcpy, which can
+// pin arrays of it in scratch); used for all raw 16-byte global/LDS traffic in the kernels.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ error reporting
+void set_error(const std::string& msg);
+int fail(const std::string& msg);           // set_error + return QMOE_EINVAL
+int check_launch(const char* what);         // hipGetLastError -> QMOE_EHIP on failure
+
+// ------------------------------------------------------------------ bf16 helpers
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t pair) {
+  return __uint_as_float(pair & 0xFFFF0000u);
+}
+// Round-to-nearest-even float -> bf16 (NaN -> quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Nibble unpack used by the int4 MFMA path: word w holds codes c0..c7 (nibble i = code i).
+// Output register r (r = 0..3) holds the bf16 pair (128 + c_r, 128 + c_{r+4}); 128 + c is exact
+// in bf16 (7 mantissa bits cover 128..255 in steps of 1). The activation fragment is permuted
+// to the same pair order by pair_permute().
+__device__ __forceinline__ bf16x8_t unpack_q128(uint32_t w) {
+  const uint32_t m = 0x000F000Fu, o = 0x43004300u;
+  uint32_t r0 = (w & m) | o;
+  uint32_t r1 = ((w >> 4) & m) | o;
+  uint32_t r2 = ((w >> 8) & m) | o;
+  uint32_t r3 = ((w >> 12) & m) | o;
+  bf16x8_t v;
+  uint32_t* p = reinterpret_cast<uint32_t*>(&v);
+  p[0] = r0; p[1] = r1; p[2] = r2; p[3] = r3;
+  return v;
+}
+
+// Activation fragment for unpack_q128: input is 8 consecutive bf16 x0..x7 as 4 u32 pairs
+// P0=(x0,x1) P1=(x2,x3) P2=(x4,x5) P3=(x6,x7); output pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7).
+__device__ __forceinline__ bf16x8_t pair_permute(uint4 q) {
+  bf16x8_t v;
+  uint32_t* p = reinterpret_cast<uint32_t*>(&v);
+  // v_perm_b32(src0, src1, sel): byte k of result = byte sel_k of {src0:src1} (src1 = bytes 0-3).
+  p[0] = __builtin_amdgcn_perm(q.z, q.x, 0x05040100u);
+  p[1] = __builtin_amdgcn_perm(q.z, q.x, 0x07060302u);
+  p[2] = __builtin_amdgcn_perm(q.w, q.y, 0x05040100u);
+  p[3] = __builtin_amdgcn_perm(q.w, q.y, 0x07060302u);
+  return v;
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 q) {
+  bf16x8_t v;
+  __builtin_memcpy(&v, &q, 16);
+  return v;
+}
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 q) { return __builtin_bit_cast(bf16x8_t, q); }
+
+__device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+
+// Upper bound on the number of m-tiles a permuted (token, slot) list can produce.
+inline int64_t mtile_upper_bound(int64_t mc, int64_t n_experts, int64_t m_tile) {
+  int64_t active = mc < n_experts ? mc : n_experts;
+  return (mc + m_tile - 1) / m_tile + active;
+}
+
+// Launchers shared between entry points (defined in the .hip files).
+int launch_router_f32(const uint16_t* x, const float* wr, const float* shared_gate, int N, int H,
+                      int E, float* logits, int ld_logits, hipStream_t stream);
+int launch_topk(const float* logits, int ld_logits, const float* bias, int N, int E, int k,
+                int scoring, int n_group, int topk_group, int norm_topk, float scale,
+                int has_shared_gate, int32_t* idx, float* w, float* shared_gate_out,
+                hipStream_t stream);
+int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,
+                   int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
+                   hipStream_t stream);
+
+struct QmmArgs {
+  const uint16_t* act;        // activation rows (bf16), row stride K
+  int64_t act_rows;           // number of activation rows (bounds check)
+  const int32_t* slot_of;     // sorted position -> slot id (nullable: identity)
+  int slot_div;               // activation row = slot / slot_div
+  int64_t n_slots;            // total sorted positions (bounds check on slot ids)
+  const int32_t* offsets;     // [E+1] segment offsets (nullable: dense, one segment of M rows)
+  const int32_t* tile_off;    // [E+1] m-tile prefix per segment (nullable in dense mode)
+  int64_t dense_rows;         // M for dense mode
+  int n_experts;              // E (1 in dense mode)
+  int K;                      // reduction length
+  int n_rows;                 // weight rows per expert (2I for SwiGLU)
+  const void* codes;          // tiled int4 codes or tiled bf16 weights
+  const uint16_t* sb;         // tiled scale/bias (int4 only)
+  void* out;                  // output rows by sorted position
+  int ld_out;                 // output row stride (elements)
+};
+
+enum { FMT_INT4 = 0, FMT_BF16 = 1 };
+enum { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
+
+int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,
+               hipStream_t stream);
+int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
+                   const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
+                   hipStream_t stream);
+
+constexpr int kSmallMTile = 16;
+constexpr int kLargeMTile = 128;
+
+}  // namespace qmoe

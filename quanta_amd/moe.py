@@ -1,0 +1,481 @@
+"""The quantized sparse-MoE block on MI355X: the reference's Python surface over the HIP C ABI.
+
+Mirrors `qwen35_moe` / `qwen35_route` (src/quanta/qwen35/moe.py:36-56,154-202) and
+`Qwen35MoEModule` (src/quanta/qwen35/model.py:28-70): same parameter-dict keys, same
+`sparse` / `token_chunk` / `topk_override` arguments, same fail-loud errors (ValueError for a bad
+`topk_override`, ValueError for the dense oracle on packed experts), packed-dict auto-detection,
+fp32 combine, sigmoid-gated shared expert and bf16 output. It adds the DeepSeek/GLM router fields
+(`scoring_func="sigmoid"`, `e_score_correction_bias`, `n_group`/`topk_group`,
+`routed_scaling_factor`; src/quanta/modeling/moe.py:33-44, src/quanta/glm/moe.py:44-55).
+
+All compute runs in the HIP kernels of `_qmoe.so`; there is no CPU path. Weights are converted
+once into the MFMA-tiled layouts the kernels stream (cached per source tensor for the functional
+API; held directly by the module).
+"""
+
+from __future__ import annotations
+
+import collections
+import ctypes
+import math
+import weakref
+from dataclasses import dataclass
+
+import torch
+
+from quanta_amd import _lib as L
+from quanta_amd import ops
+
+
+# ----------------------------------------------------------------------------------- config
+
+
+@dataclass(frozen=True)
+class MoEConfig:
+    """MoE fields of `Qwen35Config` (src/quanta/qwen35/config.py:125-130) plus the DeepSeek/GLM
+    router fields. Any object exposing these attribute names works where a config is taken."""
+
+    hidden_size: int
+    num_experts: int
+    num_experts_per_tok: int
+    moe_intermediate_size: int
+    shared_expert_intermediate_size: int = 0
+    scoring_func: str = "softmax"
+    norm_topk_prob: bool = True
+    n_group: int = 1
+    topk_group: int = 1
+    routed_scaling_factor: float = 1.0
+
+    @property
+    def moe_gate_up_out(self) -> int:
+        """Stacked gate_up output width = 2 * moe_intermediate_size (config.py:223-225)."""
+        return 2 * self.moe_intermediate_size
+
+    @property
+    def has_shared_expert(self) -> bool:
+        return self.shared_expert_intermediate_size > 0
+
+
+def _cfg(cfg, name, default=None):
+    v = getattr(cfg, name, default)
+    return default if v is None else v
+
+
+# ----------------------------------------------------------------------------------- tiled experts
+
+
+class TiledExperts(dict):
+    """A routed expert stack resident in the MFMA-tiled layout.
+
+    Keys: "format" ("int4_g64" | "bf16"), "codes" (tiled int4 words / tiled bf16), "sb" (tiled
+    scale+bias, int4 only), "shape" (E, rows, K), "group_size", "bits". Produced from the
+    reference's packed triplet {packed, scale, bias, group_size, bits}
+    (src/quanta/qwen35/artifact.py:199-203) or from a bf16 [E, rows, K] stack.
+    """
+
+    @property
+    def is_packed(self) -> bool:
+        return self["format"] == "int4_g64"
+
+
+def tile_experts_packed(d: dict) -> TiledExperts:
+    """Reference packed triplet -> TiledExperts. Fails loud unless bits == 4 and group_size == 64
+    (the kernels' format; the manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
+    if isinstance(d, TiledExperts):
+        return d
+    bits, gs = int(d["bits"]), int(d["group_size"])
+    if bits != 4 or gs != 64:
+        raise ValueError(f"packed experts must be affine int4 with group_size 64 (got bits={bits}, "
+                         f"group_size={gs})")
+    packed, scale, bias = d["packed"], d["scale"], d["bias"]
+    if scale.dtype != torch.bfloat16 or bias.dtype != torch.bfloat16:
+        raise TypeError("packed experts need bf16 scale and bias")
+    if packed.dim() != 3:
+        raise ValueError("packed experts must be a stacked [E, out, in*bits/32] tensor")
+    E, rows, W = packed.shape
+    codes, sb = ops.tile_int4(packed.contiguous(), scale.contiguous(), bias.contiguous(),
+                              group_size=gs)
+    return TiledExperts(format="int4_g64", codes=codes, sb=sb, shape=(E, rows, W * 8),
+                        group_size=gs, bits=bits)
+
+
+def tile_experts_bf16(stack: torch.Tensor) -> TiledExperts:
+    """bf16 expert stack [E, rows, K] -> TiledExperts (format "bf16")."""
+    if isinstance(stack, TiledExperts):
+        return stack
+    if stack.dtype != torch.bfloat16:
+        raise TypeError(f"bf16 expert stacks only (got {stack.dtype})")
+    if stack.dim() != 3:
+        raise ValueError("expert stack must be [E, out, in]")
+    return TiledExperts(format="bf16", codes=ops.tile_bf16(stack.contiguous()), sb=None,
+                        shape=tuple(stack.shape), group_size=0, bits=16)
+
+
+def _is_packed(v) -> bool:
+    """Auto-detection of packed experts, as the reference does with isinstance(dict)
+    (src/quanta/qwen35/moe.py:181)."""
+    if isinstance(v, TiledExperts):
+        return v.is_packed
+    return isinstance(v, dict)
+
+
+# ----------------------------------------------------------------------------------- cache
+
+_CACHE: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+_CACHE_MAX = 64
+
+
+def _tkey(t):
+    if t is None:
+        return None
+    if isinstance(t, dict):
+        return tuple((k, _tkey(v)) for k, v in sorted(t.items()) if isinstance(v, torch.Tensor))
+    return (t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device)
+
+
+def _cached(kind: str, tensors: tuple, build):
+    """Memoise a weight preparation on the identity and version of its source tensors. Entries
+    hold weak references, so a freed source never matches a new tensor at the same address."""
+    key = (kind,) + tuple(_tkey(t) for t in tensors)
+    hit = _CACHE.get(key)
+    if hit is not None:
+        refs, value = hit
+        if all(r() is t for r, t in zip(refs, _flat(tensors))):
+            _CACHE.move_to_end(key)
+            return value
+    value = build()
+    for dead in [kk for kk, (refs, _) in _CACHE.items() if any(r() is None for r in refs)]:
+        del _CACHE[dead]
+    _CACHE[key] = (tuple(weakref.ref(t) for t in _flat(tensors)), value)
+    while len(_CACHE) > _CACHE_MAX:
+        _CACHE.popitem(last=False)
+    return value
+
+
+def _flat(tensors):
+    out = []
+    for t in tensors:
+        if isinstance(t, dict):
+            out.extend(v for k, v in sorted(t.items()) if isinstance(v, torch.Tensor))
+        elif t is not None:
+            out.append(t)
+    return out
+
+
+def clear_cache() -> None:
+    _CACHE.clear()
+
+
+# ----------------------------------------------------------------------------------- prepare
+
+
+@dataclass
+class Prepared:
+    """Everything one qmoe_forward call needs, with the tensors kept alive."""
+
+    cfg: L.QmoeConfig
+    weights: L.QmoeWeights
+    keep: tuple
+    router_tiled: torch.Tensor | None
+    router_f32: torch.Tensor | None
+    shared_gate_f32: torch.Tensor | None
+    gu: TiledExperts
+    dn: TiledExperts
+    sh_gu: torch.Tensor | None
+    sh_dn: torch.Tensor | None
+    bias: torch.Tensor | None
+
+
+def _prepare_router(gate: torch.Tensor, sgate: torch.Tensor | None, E: int, H: int):
+    """Router weight [E, H] (+ optional shared-expert gate [1, H]) -> resident form.
+
+    bf16 router (the artifact dtype, src/quanta/qwen35/bake.py:147-148): one tiled bf16 matrix
+    whose row E is the shared gate, padded to a multiple of 128 rows; its logits come from the
+    bf16 MFMA path (bf16 x bf16 products are exact in fp32). fp32 router (or fp32 gate): kept
+    fp32 row-major for the fp32 VALU logits kernel, preserving xf.f32 @ gate.f32.T exactly."""
+    if gate.shape != (E, H):
+        raise ValueError(f"gate must be [{E}, {H}] (got {tuple(gate.shape)})")
+    gated = sgate is not None
+    if gate.dtype == torch.bfloat16 and (not gated or sgate.dtype == torch.bfloat16):
+        rows = int(math.ceil((E + (1 if gated else 0)) / 128.0)) * 128
+        full = torch.zeros(rows, H, dtype=torch.bfloat16, device=gate.device)
+        full[:E] = gate
+        if gated:
+            full[E] = sgate.reshape(H)
+        return ("bf16", ops.tile_bf16(full), rows, None)
+    wr = gate.to(torch.float32).contiguous()
+    sg = sgate.to(torch.float32).reshape(H).contiguous() if gated else None
+    return ("f32", wr, E + 1, sg)
+
+
+def _prepare_shared(p: dict, H: int, Is: int):
+    wg, wu, wd = p["shared_gate_proj"], p["shared_up_proj"], p["shared_down_proj"]
+    for t, nm in ((wg, "shared_gate_proj"), (wu, "shared_up_proj"), (wd, "shared_down_proj")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{nm} must be bf16 (the shared expert runs in bf16)")
+    if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is):
+        raise ValueError("shared expert shapes must be gate/up [Is, H] and down [H, Is]")
+    gu = torch.cat([wg, wu], dim=0).contiguous()
+    return ops.tile_bf16(gu), ops.tile_bf16(wd.contiguous())
+
+
+def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUTO) -> Prepared:
+    """Resolve the parameter dict `p` (reference keys, src/quanta/qwen35/moe.py:159-161) into the
+    resident kernel form. Conversions are cached on the source tensors."""
+    H = int(_cfg(cfg, "hidden_size"))
+    E = int(_cfg(cfg, "num_experts"))
+    I = int(_cfg(cfg, "moe_intermediate_size"))
+    Is = int(_cfg(cfg, "shared_expert_intermediate_size", 0))
+    k = int(topk if topk is not None else _cfg(cfg, "num_experts_per_tok"))
+    scoring = str(_cfg(cfg, "scoring_func", "softmax"))
+    if scoring not in ("softmax", "sigmoid"):
+        raise ValueError(f"scoring_func {scoring!r} not supported (softmax | sigmoid)")
+
+    gu_src, dn_src = p["experts_gate_up"], p["experts_down"]
+    packed = _is_packed(gu_src)
+    if packed != _is_packed(dn_src):
+        raise ValueError("experts_gate_up and experts_down must both be packed or both bf16")
+    if packed:
+        gu = _cached("gu", (gu_src,), lambda: tile_experts_packed(gu_src))
+        dn = _cached("dn", (dn_src,), lambda: tile_experts_packed(dn_src))
+    else:
+        gu = _cached("gu16", (gu_src,), lambda: tile_experts_bf16(gu_src))
+        dn = _cached("dn16", (dn_src,), lambda: tile_experts_bf16(dn_src))
+    if tuple(gu["shape"]) != (E, 2 * I, H) or tuple(dn["shape"]) != (E, H, I):
+        raise ValueError(f"expert stacks must be gate_up [{E},{2 * I},{H}] and down [{E},{H},{I}] "
+                         f"(got {gu['shape']} and {dn['shape']})")
+
+    has_shared = Is > 0 and p.get("shared_gate_proj") is not None
+    sgate = p.get("shared_expert_gate") if has_shared else None
+    gate = p["gate"]
+    rkind, rw, rrows, sg32 = _cached("router", (gate, sgate), lambda: _prepare_router(gate, sgate, E, H))
+    sh_gu = sh_dn = None
+    if has_shared:
+        sh_gu, sh_dn = _cached("shared", (p["shared_gate_proj"], p["shared_up_proj"],
+                                          p["shared_down_proj"]),
+                               lambda: _prepare_shared(p, H, Is))
+    bias = p.get("e_score_correction_bias")
+    if bias is not None:
+        bias = bias.to(torch.float32).reshape(E).contiguous()
+
+    c = L.QmoeConfig()
+    c.hidden, c.n_experts, c.top_k, c.inter = H, E, k, I
+    c.shared_inter = Is if has_shared else 0
+    c.scoring = L.SCORE_SOFTMAX if scoring == "softmax" else L.SCORE_SIGMOID
+    c.norm_topk = int(bool(_cfg(cfg, "norm_topk_prob", True)))
+    c.n_group = int(_cfg(cfg, "n_group", 1))
+    c.topk_group = int(_cfg(cfg, "topk_group", 1))
+    c.routed_scale = float(_cfg(cfg, "routed_scaling_factor", 1.0))
+    c.expert_format = L.FMT_INT4_G64 if packed else L.FMT_BF16
+    c.router_format = L.ROUTER_BF16_TILED if rkind == "bf16" else L.ROUTER_F32
+    c.router_rows = rrows
+    c.shared_gated = int(sgate is not None)
+    c.regime = regime
+
+    w = L.QmoeWeights()
+    w.router_w = rw.data_ptr()
+    w.router_bias = bias.data_ptr() if bias is not None else None
+    w.shared_gate_w = sg32.data_ptr() if sg32 is not None else None
+    w.gu_codes = gu["codes"].data_ptr()
+    w.gu_sb = gu["sb"].data_ptr() if gu["sb"] is not None else None
+    w.dn_codes = dn["codes"].data_ptr()
+    w.dn_sb = dn["sb"].data_ptr() if dn["sb"] is not None else None
+    w.sh_gu = sh_gu.data_ptr() if sh_gu is not None else None
+    w.sh_dn = sh_dn.data_ptr() if sh_dn is not None else None
+    keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn)
+    return Prepared(c, w, keep, rw if rkind == "bf16" else None, rw if rkind == "f32" else None,
+                    sg32, gu, dn, sh_gu, sh_dn, bias)
+
+
+# ----------------------------------------------------------------------------------- routing
+
+
+def _router_logits(xf: torch.Tensor, pr: Prepared) -> torch.Tensor:
+    c = pr.cfg
+    if c.router_format == L.ROUTER_F32:
+        return ops.router_logits_f32(xf, pr.router_f32, pr.shared_gate_f32)
+    n = xf.shape[0]
+    regime = L.REGIME_SMALL if n <= 256 else L.REGIME_LARGE
+    return ops.grouped_qmm(xf, K=c.hidden, n_rows=c.router_rows, weight_format=L.FMT_BF16,
+                           codes=pr.router_tiled, sb=None, epilogue=L.EPI_F32, out_rows=n,
+                           regime=regime, dense_rows=n)
+
+
+def _topk(logits: torch.Tensor, pr: Prepared, k: int):
+    c = pr.cfg
+    return ops.router_topk(logits, c.n_experts, k, scoring=c.scoring, bias=pr.bias,
+                           n_group=c.n_group, topk_group=c.topk_group, norm_topk=bool(c.norm_topk),
+                           routed_scale=c.routed_scale, has_shared_gate=bool(c.shared_gated))
+
+
+def qwen35_route(xf: torch.Tensor, gate_w: torch.Tensor, cfg, *, topk_override: int | None = None,
+                 e_score_correction_bias: torch.Tensor | None = None):
+    """Top-k routing -> (idx [N,k] int32, w [N,k] fp32), on the GPU.
+
+    Mirrors `qwen35_route` (src/quanta/qwen35/moe.py:36-56): fp32 logits, softmax (or sigmoid)
+    scores, top-k, gathered scores renormalised with +1e-20 when norm_topk_prob. Returned in the
+    canonical order (score descending, id ascending); the reference's argpartition gives the
+    same set unordered. With the DeepSeek/GLM fields it is MoEGate.__call__
+    (src/quanta/modeling/moe.py:33-44): selection by sigmoid + bias, optional groups, scaling.
+    """
+    if xf.dtype != torch.bfloat16:
+        raise TypeError("qwen35_route: x must be bf16")
+    E, H = int(_cfg(cfg, "num_experts")), int(_cfg(cfg, "hidden_size"))
+    k = topk_override if topk_override is not None else int(_cfg(cfg, "num_experts_per_tok"))
+    kind, rw, rows, _ = _cached("router", (gate_w, None), lambda: _prepare_router(gate_w, None, E, H))
+    xf = xf.contiguous()
+    n = xf.shape[0]
+    if kind == "f32":
+        logits = ops.router_logits_f32(xf, rw, None)
+    else:
+        logits = ops.grouped_qmm(xf, K=H, n_rows=rows, weight_format=L.FMT_BF16, codes=rw, sb=None,
+                                 epilogue=L.EPI_F32, out_rows=n,
+                                 regime=L.REGIME_SMALL if n <= 256 else L.REGIME_LARGE,
+                                 dense_rows=n)
+    scoring = L.SCORE_SOFTMAX if _cfg(cfg, "scoring_func", "softmax") == "softmax" else L.SCORE_SIGMOID
+    bias = None if e_score_correction_bias is None else e_score_correction_bias.float().reshape(E).contiguous()
+    idx, w, _ = ops.router_topk(logits, E, k, scoring=scoring, bias=bias,
+                                n_group=int(_cfg(cfg, "n_group", 1)),
+                                topk_group=int(_cfg(cfg, "topk_group", 1)),
+                                norm_topk=bool(_cfg(cfg, "norm_topk_prob", True)),
+                                routed_scale=float(_cfg(cfg, "routed_scaling_factor", 1.0)))
+    return idx, w
+
+
+# ----------------------------------------------------------------------------------- the block
+
+
+def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
+    """Run-every-expert path (`sparse=False`, bf16 stacks only; src/quanta/qwen35/moe.py:127-142):
+    every expert runs on every token and the combine uses the routing weight scattered onto the
+    chosen experts (0 elsewhere). Built from the op-level entry points."""
+    c = pr.cfg
+    n, E = xf.shape[0], c.n_experts
+    logits = _router_logits(xf, pr)
+    idx, w, sg = _topk(logits, pr, k)
+    idx_all = torch.arange(E, dtype=torch.int32, device=xf.device).repeat(n, 1).contiguous()
+    w_all = torch.zeros(n, E, dtype=torch.float32, device=xf.device)
+    w_all.scatter_(1, idx.long(), w)
+    regime = L.REGIME_SMALL if n * E <= 256 * 16 else L.REGIME_LARGE
+    m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
+    counts, offsets, tile_off, sorted_slot, inv = ops.permute(idx_all, E, m_tile)
+    fmt = c.expert_format
+    h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.inter, weight_format=fmt,
+                        codes=pr.gu["codes"], sb=pr.gu["sb"], epilogue=L.EPI_SWIGLU,
+                        out_rows=n * E, regime=regime, slot_of=sorted_slot, slot_div=E,
+                        n_slots=n * E, offsets=offsets, tile_off=tile_off, n_experts=E)
+    d = ops.grouped_qmm(h, K=c.inter, n_rows=c.hidden, weight_format=fmt, codes=pr.dn["codes"],
+                        sb=pr.dn["sb"], epilogue=L.EPI_BF16, out_rows=n * E, regime=regime,
+                        n_slots=n * E, offsets=offsets, tile_off=tile_off, n_experts=E)
+    sh_out = None
+    if c.shared_inter > 0:
+        sreg = L.REGIME_SMALL if n <= 256 else L.REGIME_LARGE
+        sh_h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.shared_inter, weight_format=L.FMT_BF16,
+                               codes=pr.sh_gu, sb=None, epilogue=L.EPI_SWIGLU, out_rows=n,
+                               regime=sreg, dense_rows=n)
+        sh_out = ops.grouped_qmm(sh_h, K=c.shared_inter, n_rows=c.hidden, weight_format=L.FMT_BF16,
+                                 codes=pr.sh_dn, sb=None, epilogue=L.EPI_BF16, out_rows=n,
+                                 regime=sreg, dense_rows=n)
+    return ops.combine(d, inv, w_all, sh_out, sg)
+
+
+def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chunk: int = 8192,
+               topk_override: int | None = None, regime: int = L.REGIME_AUTO) -> torch.Tensor:
+    """Full MoE block: routed top-k experts + gated shared expert. `x` [B,S,H] bf16 -> [B,S,H].
+
+    Mirrors `qwen35_moe` (src/quanta/qwen35/moe.py:154-202). `p` keys: gate [E,H];
+    experts_gate_up / experts_down as packed triplet dicts {packed, scale, bias, group_size, bits}
+    (int4 g64; or TiledExperts) or bf16 stacks [E,2I,H] / [E,H,I]; shared_gate_proj,
+    shared_up_proj [Is,H]; shared_down_proj [H,Is]; shared_expert_gate [1,H] (omit it for an
+    ungated DeepSeek/GLM shared expert); optional e_score_correction_bias [E].
+    `sparse=False` is the run-every-expert oracle and, as in the reference, refuses packed experts.
+    Tokens beyond `token_chunk` are processed chunk by chunk (output-equivalent).
+    """
+    if x.dim() != 3:
+        raise ValueError("x must be [B, S, hidden]")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bf16 (got {x.dtype}); the block computes on bf16 activations")
+    b, s, hidden = x.shape
+    n = b * s
+    k_max = int(_cfg(cfg, "num_experts_per_tok"))
+    topk = topk_override if topk_override is not None else k_max
+    if topk < 1 or topk > k_max:
+        raise ValueError(f"topk_override {topk_override} must be in [1, {k_max}]")
+    packed = _is_packed(p["experts_gate_up"])
+    if not sparse and packed:
+        raise ValueError("qwen35_moe(sparse=False) is the bf16 dense oracle; packed int4 experts "
+                         "require sparse=True (gather_qmm). Refusing to dequant silently.")
+    pr = prepare(p, cfg, topk=topk, regime=regime)
+    xf = x.reshape(n, hidden).contiguous()
+    if n == 0:
+        return x.clone()
+    if not sparse:
+        return _routed_dense(xf, pr, topk).reshape(b, s, hidden)
+    chunk = token_chunk if token_chunk and token_chunk > 0 else n
+    chunk = min(chunk, 65535)
+    y = torch.empty_like(xf)
+    ws = torch.empty(max(ops.forward_workspace(pr.cfg, min(n, chunk)), 1), dtype=torch.uint8,
+                     device=x.device)
+    for c0 in range(0, n, chunk):
+        c1 = min(c0 + chunk, n)
+        ops.forward(pr.cfg, pr.weights, xf[c0:c1], out=y[c0:c1], ws=ws)
+    return y.reshape(b, s, hidden)
+
+
+class Qwen35MoEModule(torch.nn.Module):
+    """Module wrapper over :func:`qwen35_moe` holding the router, expert and shared params
+    (src/quanta/qwen35/model.py:28-70).
+
+    Differences, both from holding tensors eagerly on a GPU: the routed expert stacks start as
+    None (the reference's `mx.zeros` stacks are lazy and never materialised before the loader
+    sets them), and `set_experts` / `set_experts_packed` convert the stacks once into the
+    resident MFMA-tiled layout (`TiledExperts`, still a dict for packed experts) instead of
+    holding the caller's arrays, so a layer is resident once, not twice.
+    """
+
+    def __init__(self, cfg, *, device: torch.device | str | None = None,
+                 dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.cfg = cfg
+        dev = torch.device(device) if device is not None else torch.device("cuda")
+        h, e = int(_cfg(cfg, "hidden_size")), int(_cfg(cfg, "num_experts"))
+        si = int(_cfg(cfg, "shared_expert_intermediate_size", 0))
+        self.gate = torch.zeros(e, h, dtype=dtype, device=dev)
+        self.experts_gate_up = None
+        self.experts_down = None
+        self.shared_gate_proj = torch.zeros(si, h, dtype=dtype, device=dev)
+        self.shared_up_proj = torch.zeros(si, h, dtype=dtype, device=dev)
+        self.shared_down_proj = torch.zeros(h, si, dtype=dtype, device=dev)
+        self.shared_expert_gate = torch.zeros(1, h, dtype=dtype, device=dev)
+        self.e_score_correction_bias = None
+        self.token_chunk = 8192
+
+    def set_experts(self, gate_up: torch.Tensor, down: torch.Tensor) -> None:
+        """bf16 expert stacks [E,2I,H] / [E,H,I] (src/quanta/qwen35/model.py:46-47)."""
+        self.experts_gate_up, self.experts_down = tile_experts_bf16(gate_up), tile_experts_bf16(down)
+
+    def set_experts_packed(self, gate_up: dict, down: dict) -> None:
+        """Packed int4 triplets {packed, scale, bias, group_size, bits}
+        (src/quanta/qwen35/model.py:49-55); converted once to the tiled resident layout."""
+        self.experts_gate_up, self.experts_down = tile_experts_packed(gate_up), tile_experts_packed(down)
+
+    def _params(self) -> dict:
+        if self.experts_gate_up is None or self.experts_down is None:
+            raise ValueError("experts not set: call set_experts or set_experts_packed first")
+        p = {
+            "gate": self.gate,
+            "experts_gate_up": self.experts_gate_up,
+            "experts_down": self.experts_down,
+            "shared_gate_proj": self.shared_gate_proj,
+            "shared_up_proj": self.shared_up_proj,
+            "shared_down_proj": self.shared_down_proj,
+            "shared_expert_gate": self.shared_expert_gate,
+        }
+        if self.e_score_correction_bias is not None:
+            p["e_score_correction_bias"] = self.e_score_correction_bias
+        return p
+
+    def forward(self, x: torch.Tensor, *, sparse: bool = True,
+                topk_override: int | None = None) -> torch.Tensor:
+        return qwen35_moe(x, self._params(), self.cfg, sparse=sparse, token_chunk=self.token_chunk,
+                          topk_override=topk_override)

@@ -1,0 +1,161 @@
+"""Seeded synthetic MoE layers and inputs for the BASELINE configurations (any torch device).
+
+Config ids follow BASELINE.json `configs`:
+  c0  H512  / E16  / top-2 softmax / I256, no shared expert, fp32 router      (N = 8)
+  c1  H2048 / E256 / top-8 softmax / I512, shared I512 with sigmoid gate      (N = 1, 8, 32, 64)
+  c2  H4096 / E512 / top-10 softmax / I1024, shared I1024 with sigmoid gate   (N = 1, 8, 32, 128)
+  c3  H7168 / E256 / sigmoid + correction bias, 8 groups keep 4, top-8, x2.5, ungated shared
+      I2048, expert I2048                                                      (N = 1, 16, 64)
+  c4  the c2 shape at a 4096-token prefill with Zipf(1.1) expert popularity  (N = 4096)
+Weights: router N(0, 0.02) (fp32 for c0, bf16 otherwise, as the artifact stores it); experts
+bf16 N(0, 0.02) quantized RTN affine int4 g64 (quanta_amd.quant.quantize_affine); shared expert
+bf16 N(0, 0.02); c3 correction bias N(0, 0.01) fp32. Inputs x ~ N(0, 1) in bf16.
+
+c4 popularity: a seeded permutation assigns every expert a popularity rank r_e, and router
+column 0 carries the logit bias beta_e = -1.1 * tau * log(r_e) while x[:, 0] is held at 1.0, so
+logit_e = beta_e + (noise of std sqrt(H-1)*0.02). tau = 0.8 was calibrated offline so that the
+realised top-10 histogram over 4096 tokens has a log-log slope of about -1.1 across ranks 2..64
+(hottest experts take thousands of tokens, the median a handful, some none).
+
+Generation is chunked over experts so even c2 (3.4 GiB of packed experts) stays within a few GiB
+of temporaries. All randomness comes from one torch.Generator seeded per (config, layer).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from quanta_amd.moe import MoEConfig
+from quanta_amd.quant import quantize_affine
+
+ZIPF_TAU = 0.8
+ZIPF_S = 1.1
+
+
+@dataclass(frozen=True)
+class SynthSpec:
+    cfg: MoEConfig
+    batches: tuple
+    router_fp32: bool
+    shared_gated: bool
+    bias_std: float
+    zipf: bool
+
+
+SPECS = {
+    "c0": SynthSpec(MoEConfig(512, 16, 2, 256, 0), (8,), True, False, 0.0, False),
+    "c1": SynthSpec(MoEConfig(2048, 256, 8, 512, 512), (1, 8, 32, 64), False, True, 0.0, False),
+    "c2": SynthSpec(MoEConfig(4096, 512, 10, 1024, 1024), (1, 8, 32, 128), False, True, 0.0, False),
+    "c3": SynthSpec(MoEConfig(7168, 256, 8, 2048, 2048, scoring_func="sigmoid", norm_topk_prob=True,
+                              n_group=8, topk_group=4, routed_scaling_factor=2.5),
+                    (1, 16, 64), False, False, 0.01, False),
+    "c4": SynthSpec(MoEConfig(4096, 512, 10, 1024, 1024), (4096,), False, True, 0.0, True),
+}
+
+
+def spec(name: str) -> SynthSpec:
+    return SPECS[name]
+
+
+def scaled_spec(name: str, **dims) -> SynthSpec:
+    """A spec with some MoEConfig fields replaced (same routing style), for reduced-size tests."""
+    s = SPECS[name]
+    c = s.cfg
+    fields = {f: getattr(c, f) for f in c.__dataclass_fields__}
+    fields.update(dims)
+    return SynthSpec(MoEConfig(**fields), s.batches, s.router_fp32, s.shared_gated, s.bias_std,
+                     s.zipf)
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def _normal(shape, std, g, device, dtype=torch.float32):
+    return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std).to(dtype)
+
+
+def _quantized_stack(E, rows, K, g, device, chunk_elems=1 << 28):
+    """Stack of E experts [rows, K] ~ N(0, 0.02) bf16, RTN int4 g64 -> packed triplet dict."""
+    packed = torch.empty(E, rows, K // 8, dtype=torch.int32, device=device)
+    scale = torch.empty(E, rows, K // 64, dtype=torch.bfloat16, device=device)
+    bias = torch.empty_like(scale)
+    per = max(1, chunk_elems // (rows * K))
+    for e0 in range(0, E, per):
+        e1 = min(E, e0 + per)
+        w = _normal((e1 - e0, rows, K), 0.02, g, device, torch.bfloat16)
+        q, s, b = quantize_affine(w, 4, 64, scale_dtype=torch.bfloat16)
+        packed[e0:e1], scale[e0:e1], bias[e0:e1] = q, s, b
+        del w, q, s, b
+    return {"packed": packed, "scale": scale, "bias": bias, "group_size": 64, "bits": 4}
+
+
+def zipf_logit_bias(E: int, g: torch.Generator, device) -> torch.Tensor:
+    perm = torch.randperm(E, generator=g, device=device)
+    rank = torch.empty(E, dtype=torch.float32, device=device)
+    rank[perm] = torch.arange(1, E + 1, dtype=torch.float32, device=device)
+    return -ZIPF_S * ZIPF_TAU * torch.log(rank)
+
+
+def make_layer(name: str | SynthSpec, *, device="cuda", seed: int | None = None,
+               layer: int = 0) -> dict:
+    """Parameter dict with the reference keys (src/quanta/qwen35/moe.py:159-161); routed experts as
+    packed triplets in the reference's native layout."""
+    s = SPECS[name] if isinstance(name, str) else name
+    c = s.cfg
+    cid = int(name[1]) if isinstance(name, str) else 9
+    g = _gen(device, (1000 + cid if seed is None else seed) * 1009 + layer)
+    H, E, I, Is = c.hidden_size, c.num_experts, c.moe_intermediate_size, c.shared_expert_intermediate_size
+    p: dict = {}
+    gate = _normal((E, H), 0.02, g, device)
+    if s.zipf:
+        gate[:, 0] = zipf_logit_bias(E, g, device)
+    p["gate"] = gate if s.router_fp32 else gate.to(torch.bfloat16)
+    p["experts_gate_up"] = _quantized_stack(E, 2 * I, H, g, device)
+    p["experts_down"] = _quantized_stack(E, H, I, g, device)
+    if Is > 0:
+        p["shared_gate_proj"] = _normal((Is, H), 0.02, g, device, torch.bfloat16)
+        p["shared_up_proj"] = _normal((Is, H), 0.02, g, device, torch.bfloat16)
+        p["shared_down_proj"] = _normal((H, Is), 0.02, g, device, torch.bfloat16)
+        if s.shared_gated:
+            p["shared_expert_gate"] = _normal((1, H), 0.02, g, device, torch.bfloat16)
+    if s.bias_std > 0:
+        p["e_score_correction_bias"] = _normal((E,), s.bias_std, g, device)
+    return p
+
+
+def make_inputs(name: str | SynthSpec, N: int, *, device="cuda", seed: int = 0) -> torch.Tensor:
+    """x [N, H] bf16 ~ N(0, 1); for the Zipf config channel 0 is held at 1.0."""
+    s = SPECS[name] if isinstance(name, str) else name
+    g = _gen(device, 7919 + seed)
+    x = torch.randn(N, s.cfg.hidden_size, generator=g, device=device, dtype=torch.float32)
+    if s.zipf:
+        x[:, 0] = 1.0
+    return x.to(torch.bfloat16)
+
+
+def algorithmic_bytes(cfg, distinct_experts: int, N: int, router_bytes_per_elem: int = 2) -> int:
+    """Bytes a layer call must move at minimum: U*B_e + S + R + A with B_e = 3*I*H*0.5625 (int4
+    codes + bf16 scale and bias per 64), S = 3*Is*H*2, R = E*H*elem, A = 4*N*H (bf16 in and out)."""
+    H, E, I = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size
+    Is = cfg.shared_expert_intermediate_size
+    be = 3 * I * H * 9 // 16
+    return distinct_experts * be + 3 * Is * H * 2 + E * H * router_bytes_per_elem + 4 * N * H
+
+
+def algorithmic_flops(cfg, N: int, k: int | None = None) -> int:
+    """2*N*(k*3*I*H + 3*Is*H + E*H)."""
+    H, E, I = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size
+    Is = cfg.shared_expert_intermediate_size
+    k = cfg.num_experts_per_tok if k is None else k
+    return 2 * N * (k * 3 * I * H + 3 * Is * H + E * H)
+
+
+def expected_distinct(E: int, k: int, N: int) -> float:
+    """E[U] under uniform routing: E * (1 - (1 - k/E)^N)."""
+    return E * (1.0 - math.pow(1.0 - k / E, N))

@@ -1,0 +1,75 @@
+"""Shared helpers for the GPU parity tests: numpy <-> torch conversion of bf16/word data and the
+tolerance metrics the BASELINE parity gates use."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import quant as oq
+
+# BASELINE parity gates for the bf16 layer output
+MAX_ABS = 2e-2
+REL_L2 = 5e-3
+
+
+def bf16_dev(bits: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def words_dev(words: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(words).view(np.int32)).to(dev)
+
+
+def bits_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().astype(np.uint16)
+
+
+def f64(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def words_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().cpu().numpy().view(np.uint32)
+
+
+def metrics(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
+    d = got.astype(np.float64) - want.astype(np.float64)
+    max_abs = float(np.max(np.abs(d))) if d.size else 0.0
+    rel = float(np.linalg.norm(d) / max(np.linalg.norm(want), 1e-30))
+    return max_abs, rel
+
+
+def assert_close(got, want, what="", max_abs=MAX_ABS, rel_l2=REL_L2):
+    ma, rl = metrics(got, want)
+    print(f"[parity] {what}: max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert ma <= max_abs and rl <= rel_l2, f"{what}: max_abs={ma:.3e} rel_l2={rl:.3e}"
+
+
+def oracle_params_from_torch(p: dict) -> dict:
+    """Reference-keyed torch parameter dict (any device) -> the oracle's numpy parameters."""
+    out = {"gate": f64(p["gate"])}
+    for pre, key in (("gu", "experts_gate_up"), ("dn", "experts_down")):
+        out[f"{pre}_packed"] = words_np(p[key]["packed"])
+        out[f"{pre}_scale"] = bits_np(p[key]["scale"])
+        out[f"{pre}_bias"] = bits_np(p[key]["bias"])
+    for k in ("shared_gate_proj", "shared_up_proj", "shared_down_proj", "shared_expert_gate"):
+        if p.get(k) is not None:
+            out[k] = f64(p[k])
+    if p.get("e_score_correction_bias") is not None:
+        out["e_score_correction_bias"] = f64(p["e_score_correction_bias"])
+    return out
+
+
+def near_tie_rows(margin: np.ndarray, logits_scale: np.ndarray, tol: float = 1e-5) -> np.ndarray:
+    """Rows whose top-k boundary gap is within float32 evaluation error of the router logits."""
+    return margin <= tol * np.maximum(logits_scale, 1.0)
+
+
+def route_sets_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    return all(set(x) == set(y) for x, y in zip(a.tolist(), b.tolist()))
+
+
+__all__ = ["bf16_dev", "words_dev", "bits_np", "f64", "words_np", "metrics", "assert_close",
+           "oracle_params_from_torch", "near_tie_rows", "route_sets_equal", "oq"]

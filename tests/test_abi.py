@@ -1,0 +1,94 @@
+"""CPU tier: the C-ABI library loads, exports every symbol include/quanta_moe.h declares, and
+rejects bad arguments before touching the GPU (each call below fails validation, so no HIP work
+is enqueued and nothing is dereferenced)."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from quanta_amd import _lib as L
+
+
+def test_library_loads_and_abi_version():
+    lib = L.load()
+    assert lib.qmoe_abi_version() == 1
+
+
+def test_every_header_symbol_is_exported_and_bound():
+    lib = L.load()
+    declared = L.header_symbols()
+    assert declared, "no symbols parsed from the header"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/quanta_moe.h but not exported"
+    assert sorted(L.SIGNATURES) == declared, "ctypes signature table out of sync with the header"
+
+
+def test_struct_layouts_match_header_field_order():
+    text = L.HEADER.read_text()
+    for struct, name in ((L.QmoeConfig, "qmoe_config_t"), (L.QmoeWeights, "qmoe_weights_t")):
+        body = text.split("typedef struct {", 1)[1] if name == "qmoe_config_t" else \
+            text.split("typedef struct {", 2)[2]
+        body = body.split("}", 1)[0]
+        for fname, _ in struct._fields_:
+            assert f" {fname};" in body, f"{name}.{fname} missing from header"
+
+
+def _last_error() -> str:
+    return L.load().qmoe_last_error().decode()
+
+
+@pytest.mark.parametrize("call, fragment", [
+    (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 3, 64, None, None), "bits=4"),
+    (lambda lib: lib.qmoe_dequant(None, None, None, 4, 100, 4, 64, None, None), "in_features"),
+    (lambda lib: lib.qmoe_tile_int4(None, None, None, 1, 15, 128, 64, None, None, None), "rows % 16"),
+    (lambda lib: lib.qmoe_tile_bf16(None, 1, 16, 33, None, None), "in_features % 32"),
+    (lambda lib: lib.qmoe_permute(None, 0, 2, 16, 16, None, None, None, None, None, None), "N,k"),
+    (lambda lib: lib.qmoe_permute(None, 4, 2, 2000, 16, None, None, None, None, None, None), "E <= 1024"),
+    (lambda lib: lib.qmoe_router_topk(None, 16, None, 4, 16, 17, 0, 1, 1, 1, 1.0, 0, None, None, None,
+                                      None), "k <= min"),
+    (lambda lib: lib.qmoe_router_topk(None, 16, None, 4, 16, 2, 0, 3, 1, 1, 1.0, 0, None, None, None,
+                                      None), "n_group"),
+    (lambda lib: lib.qmoe_router_topk(None, 16, None, 4, 16, 8, 1, 8, 2, 1, 1.0, 0, None, None, None,
+                                      None), "kept groups"),
+    (lambda lib: lib.qmoe_combine(None, None, None, 4, 2, 100, None, None, None, None), "H % 8"),
+    (lambda lib: lib.qmoe_grouped_qmm(None, 1, None, 1, 1, None, None, 1, 1, 128, 16, 0, None, None,
+                                      0, None, 16, 1, None), "null pointer"),
+])
+def test_invalid_arguments_rejected(call, fragment):
+    rc = call(L.load())
+    assert rc == L.QMOE_EINVAL
+    assert fragment in _last_error()
+
+
+def test_forward_rejects_bad_config():
+    lib = L.load()
+    cfg = L.QmoeConfig(hidden=100, n_experts=16, top_k=2, inter=128, shared_inter=0, scoring=0,
+                       norm_topk=1, n_group=1, topk_group=1, routed_scale=1.0, expert_format=0,
+                       router_format=1, router_rows=0, shared_gated=0, regime=0)
+    w = L.QmoeWeights()
+    dummy = ctypes.c_void_p(16)
+    rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
+    assert rc == L.QMOE_EINVAL and "hidden % 128" in _last_error()
+    assert lib.qmoe_forward_workspace(ctypes.byref(cfg), 0) == 0
+
+
+def test_workspace_grows_with_tokens():
+    lib = L.load()
+    cfg = L.QmoeConfig(hidden=4096, n_experts=512, top_k=10, inter=1024, shared_inter=1024,
+                       scoring=0, norm_topk=1, n_group=1, topk_group=1, routed_scale=1.0,
+                       expert_format=0, router_format=0, router_rows=640, shared_gated=1, regime=0)
+    a = lib.qmoe_forward_workspace(ctypes.byref(cfg), 1)
+    b = lib.qmoe_forward_workspace(ctypes.byref(cfg), 128)
+    assert 0 < a < b
+    # h (mc*I bf16) + d (mc*H bf16) dominate
+    assert b >= 128 * 10 * (1024 + 4096) * 2
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    from quanta_amd import ops
+
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.tile_bf16(torch.zeros(16, 32, dtype=torch.bfloat16))

@@ -1,0 +1,235 @@
+"""GPU tier: the whole block through the reference surface (qwen35_moe / Qwen35MoEModule) and the
+C ABI's qmoe_forward, against the golden fixtures and, at the BASELINE configurations' full sizes,
+against the oracle on sampled tokens plus size-independent properties.
+
+Bars (BASELINE parity gates): top-k expert ids bit-exact outside float32 near-ties; layer output
+bf16 within max-abs 2e-2 and relative L2 5e-3.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from oracle import quant as oq
+from quanta_amd import _lib as L
+from quanta_amd import ops, synth
+from quanta_amd.moe import MoEConfig, Qwen35MoEModule, qwen35_moe, qwen35_route
+from tests._util import (assert_close, bf16_dev, bits_np, f64, oracle_params_from_torch,
+                         words_dev, words_np)
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ----------------------------------------------------------------------------------- fixtures
+
+
+def _fixture(name, dev):
+    a = dict(np.load(GOLDEN / f"{name}.npz"))
+    H, E, k, I, Is, ng, tg, norm, sig = a["dims"].tolist()
+    cfg = MoEConfig(H, E, k, I, Is, scoring_func="sigmoid" if sig else "softmax",
+                    norm_topk_prob=bool(norm), n_group=ng, topk_group=tg,
+                    routed_scaling_factor=float(a["routed_scale"][0]))
+    p = {"gate": torch.from_numpy(a["gate_f32"]).to(dev) if "gate_f32" in a else bf16_dev(a["gate"], dev)}
+    for pre, key in (("gu", "experts_gate_up"), ("dn", "experts_down")):
+        p[key] = {"packed": words_dev(a[f"{pre}_packed"], dev), "scale": bf16_dev(a[f"{pre}_scale"], dev),
+                  "bias": bf16_dev(a[f"{pre}_bias"], dev), "group_size": 64, "bits": 4}
+    for kk in ("shared_gate_proj", "shared_up_proj", "shared_down_proj", "shared_expert_gate"):
+        if kk in a:
+            p[kk] = bf16_dev(a[kk], dev)
+    if "e_score_correction_bias" in a:
+        p["e_score_correction_bias"] = torch.from_numpy(a["e_score_correction_bias"]).to(dev)
+    x = bf16_dev(a["x"], dev)
+    return a, cfg, p, x
+
+
+@pytest.mark.parametrize("name", ["c0", "c1mini", "c3mini"])
+def test_block_golden(gpu, name):
+    a, cfg, p, x = _fixture(name, gpu)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    assert_close(f64(y), oq.bf16_bits_to_f32(a["y"]), f"golden {name}")
+    idx, w = qwen35_route(x, p["gate"], cfg,
+                          e_score_correction_bias=p.get("e_score_correction_bias"))
+    ok = a["margin"] > 1e-6
+    assert np.array_equal(idx.cpu().numpy()[ok], a["idx"][ok])
+    assert np.allclose(w.cpu().numpy()[ok], a["w"][ok], rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("name", ["c0", "c1mini"])
+@pytest.mark.parametrize("regime", [L.REGIME_SMALL, L.REGIME_LARGE])
+def test_block_golden_both_regimes(gpu, name, regime):
+    a, cfg, p, x = _fixture(name, gpu)
+    y = qwen35_moe(x[None], p, cfg, regime=regime)[0]
+    assert_close(f64(y), oq.bf16_bits_to_f32(a["y"]), f"golden {name} regime={regime}")
+
+
+def test_module_equals_function(gpu):
+    a, cfg, p, x = _fixture("c1mini", gpu)
+    mod = Qwen35MoEModule(cfg, device=gpu)
+    mod.gate = p["gate"]
+    for kk in ("shared_gate_proj", "shared_up_proj", "shared_down_proj", "shared_expert_gate"):
+        setattr(mod, kk, p[kk])
+    mod.set_experts_packed(p["experts_gate_up"], p["experts_down"])
+    y_mod = mod(x[None])
+    y_fn = qwen35_moe(x[None], p, cfg)
+    assert torch.equal(y_mod, y_fn)
+    assert isinstance(mod.experts_gate_up, dict)   # packed auto-detection still sees a dict
+
+
+def test_topk_override_and_errors(gpu):
+    a, cfg, p, x = _fixture("c1mini", gpu)
+    op = oracle_params_from_torch(p)
+    xf = f64(x)
+    for k in (1, 2):
+        y = qwen35_moe(x[None], p, cfg, topk_override=k)[0]
+        want, _ = om.moe_forward(xf, op, k=k, inter=cfg.moe_intermediate_size)
+        assert_close(f64(y), want, f"topk_override={k}")
+    for bad in (0, cfg.num_experts_per_tok + 1):
+        with pytest.raises(ValueError, match="topk_override"):
+            qwen35_moe(x[None], p, cfg, topk_override=bad)
+    with pytest.raises(ValueError, match="sparse=False"):
+        qwen35_moe(x[None], p, cfg, sparse=False)
+    with pytest.raises(TypeError):
+        qwen35_moe(x[None].float(), p, cfg)
+    bad = dict(p["experts_gate_up"], group_size=32)
+    with pytest.raises(ValueError, match="group_size 64"):
+        qwen35_moe(x[None], dict(p, experts_gate_up=bad), cfg)
+
+
+def test_token_chunking_and_batch_invariance(gpu):
+    a, cfg, p, x = _fixture("c1mini", gpu)
+    full = qwen35_moe(x[None], p, cfg, token_chunk=8192)
+    chunked = qwen35_moe(x[None], p, cfg, token_chunk=3)
+    assert torch.equal(full, chunked)   # per-token work is independent of the batch
+    for t in (0, 5, 15):
+        single = qwen35_moe(x[t:t + 1][None], p, cfg)
+        assert torch.equal(single[0, 0], full[0, t])
+
+
+def test_dense_oracle_path_matches_sparse(gpu):
+    """bf16 expert stacks: sparse gather path == run-every-expert path (sparse=False), and both
+    match the packed path on the same (dequantized) codes, as the reference's
+    _moe_packed_parity gate checks (parity/qwen35_forward_test.py:216-271)."""
+    a, cfg, p, x = _fixture("c1mini", gpu)
+    gu, dn = p["experts_gate_up"], p["experts_down"]
+    p16 = dict(p, experts_gate_up=ops.dequant(gu["packed"], gu["scale"], gu["bias"]),
+               experts_down=ops.dequant(dn["packed"], dn["scale"], dn["bias"]))
+    y_sparse = f64(qwen35_moe(x[None], p16, cfg))
+    y_dense = f64(qwen35_moe(x[None], p16, cfg, sparse=False))
+    y_packed = f64(qwen35_moe(x[None], p, cfg))
+    assert_close(y_dense, y_sparse, "dense vs sparse (bf16 stacks)")
+    assert_close(y_packed, y_sparse, "packed vs bf16-dequant stacks")
+
+
+def test_forward_capi_rejects_bad_workspace(gpu):
+    a, cfg, p, x = _fixture("c0", gpu)
+    from quanta_amd.moe import prepare
+
+    pr = prepare(p, cfg)
+    small = torch.empty(16, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError, match="workspace too small"):
+        L.check(L.load().qmoe_forward(__import__("ctypes").byref(pr.cfg),
+                                      __import__("ctypes").byref(pr.weights), x.data_ptr(),
+                                      x.shape[0], x.data_ptr(), small.data_ptr(), 16, None),
+                "qmoe_forward")
+
+
+# ----------------------------------------------------------------------------------- full size
+
+_LAYERS: dict = {}
+
+
+def _layer(name, dev):
+    if name not in _LAYERS:
+        _LAYERS.clear()
+        torch.cuda.empty_cache()
+        _LAYERS[name] = synth.make_layer(name, device=dev)
+    return _LAYERS[name]
+
+
+def _oracle_tokens(p, cfg, x64, toks, idx, w):
+    """Oracle output for the sampled tokens only, fetching just the routed experts."""
+    H, I = cfg.hidden_size, cfg.moe_intermediate_size
+    gu, dn = p["experts_gate_up"], p["experts_down"]
+    cache = {}
+
+    def expert(e):
+        if e not in cache:
+            cache[e] = (oq.dequant_exact(words_np(gu["packed"][e]), bits_np(gu["scale"][e]),
+                                         bits_np(gu["bias"][e]), H),
+                        oq.dequant_exact(words_np(dn["packed"][e]), bits_np(dn["scale"][e]),
+                                         bits_np(dn["bias"][e]), I))
+        return cache[e]
+
+    out = np.zeros((len(toks), H))
+    sh = None
+    if p.get("shared_gate_proj") is not None:
+        sh, _, _ = om.shared_expert(x64[toks], f64(p["shared_gate_proj"]), f64(p["shared_up_proj"]),
+                                    f64(p["shared_down_proj"]),
+                                    f64(p["shared_expert_gate"]) if p.get("shared_expert_gate") is not None else None)
+    for i, t in enumerate(toks):
+        for s in range(idx.shape[1]):
+            wg, wd = expert(int(idx[t, s]))
+            gu_v = oq.round_bf16(x64[t] @ wg.T)
+            h = oq.round_bf16(gu_v[:I] / (1 + np.exp(-gu_v[:I])) * gu_v[I:])
+            d = oq.round_bf16(h @ wd.T)
+            out[i] += w[t, s] * d
+    if sh is not None:
+        out += sh
+    return oq.round_bf16(out)
+
+
+@pytest.mark.parametrize("name,N", [("c1", 1), ("c1", 64), ("c2", 1), ("c2", 8), ("c2", 32),
+                                    ("c2", 128), ("c3", 1), ("c3", 16), ("c3", 64)])
+def test_block_full_size(gpu, name, N):
+    spec = synth.spec(name)
+    cfg = spec.cfg
+    p = _layer(name, gpu)
+    x = synth.make_inputs(name, N, device=gpu, seed=N)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    assert torch.isfinite(y.float()).all()
+    x64 = f64(x)
+    bias = f64(p["e_score_correction_bias"]) if p.get("e_score_correction_bias") is not None else None
+    idx_o, w_o, logits_o, _, choice_o = om.route(
+        x64, f64(p["gate"]), k=cfg.num_experts_per_tok, scoring=cfg.scoring_func,
+        norm_topk=cfg.norm_topk_prob, bias=bias, n_group=cfg.n_group, topk_group=cfg.topk_group,
+        scale=cfg.routed_scaling_factor)
+    idx, w = qwen35_route(x, p["gate"], cfg, e_score_correction_bias=p.get("e_score_correction_bias"))
+    idx, w = idx.cpu().numpy(), w.cpu().numpy().astype(np.float64)
+    sel = logits_o if cfg.scoring_func == "softmax" and bias is None else choice_o
+    tie = om.route_margin(sel, cfg.num_experts_per_tok) <= 1e-5 * np.max(np.abs(x64) @ np.abs(f64(p["gate"])).T, axis=1)
+    print(f"[parity] {name} N={N}: {int(tie.sum())} near-tie rows of {N}")
+    assert np.array_equal(idx[~tie], idx_o[~tie])
+    toks = list(range(N)) if N <= 2 else sorted({0, N // 2, N - 1})
+    toks = [t for t in toks if not tie[t]]
+    want = _oracle_tokens(p, cfg, x64, toks, idx_o, w_o)
+    assert_close(f64(y)[toks], want, f"{name} N={N} tokens {toks}")
+
+
+def test_prefill_zipf_c4(gpu):
+    cfg = synth.spec("c4").cfg
+    p = _layer("c4", gpu)
+    N = 4096
+    x = synth.make_inputs("c4", N, device=gpu, seed=1)
+    y_large = qwen35_moe(x[None], p, cfg)[0]                       # auto: large-M regime
+    y_small = qwen35_moe(x[None], p, cfg, regime=L.REGIME_SMALL)[0]
+    assert torch.isfinite(y_large.float()).all()
+    assert_close(f64(y_large), f64(y_small), "c4 large vs small regime")
+    idx, w = qwen35_route(x, p["gate"], cfg)
+    counts = torch.bincount(idx.reshape(-1).long(), minlength=cfg.num_experts).cpu().numpy()
+    print(f"[parity] c4 routing: max {counts.max()} median {int(np.median(counts))} "
+          f"empty {(counts == 0).sum()}")
+    assert counts.sum() == N * cfg.num_experts_per_tok and counts.max() > 500 and (counts == 0).any()
+    x64 = f64(x)
+    idx_o, w_o, logits_o, _, _ = om.route(x64, f64(p["gate"]), k=cfg.num_experts_per_tok)
+    toks = [0, 1234, 4095]
+    tie = om.route_margin(logits_o, cfg.num_experts_per_tok) <= 1e-4
+    toks = [t for t in toks if not tie[t]]
+    assert np.array_equal(idx.cpu().numpy()[toks], idx_o[toks])
+    want = _oracle_tokens(p, cfg, x64, toks, idx_o, w_o)
+    assert_close(f64(y_large)[toks], want, "c4 sampled tokens")

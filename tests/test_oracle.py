@@ -1,0 +1,386 @@
+"""CPU tier: pin the oracle (oracle/) against independent checks, and the product's host-side
+format code (quanta_amd.quant) against the oracle.
+
+No reference golden vectors exist for this path (the reference's MoE gates regenerate their data
+from mx.random and need a live MLX, which is absent), so every oracle function is pinned here by
+something that does not share its code: exact rational arithmetic, brute force on tiny inputs,
+bit-level known answers, torch/scipy library routines, invariants, special cases that reduce to a
+dense product, and transformers' own (third-party) DeepSeek-V3 and Qwen3.5-MoE modules.
+"""
+
+from __future__ import annotations
+
+import itertools
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from oracle import quant as oq
+
+# ----------------------------------------------------------------------------------- bf16
+
+
+def _rne_bf16_fraction(v: Fraction) -> Fraction:
+    """Round an exact rational to the nearest bf16 value (ties to even), normal range only."""
+    if v == 0:
+        return Fraction(0)
+    sign = -1 if v < 0 else 1
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** (e - 7)
+    q, r = divmod(a, ulp)
+    if r * 2 > ulp or (r * 2 == ulp and q % 2 == 1):
+        q += 1
+    return sign * q * ulp
+
+
+def _rne_f32_fraction(v: Fraction) -> Fraction:
+    if v == 0:
+        return Fraction(0)
+    sign = -1 if v < 0 else 1
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** (e - 23)
+    q, r = divmod(a, ulp)
+    if r * 2 > ulp or (r * 2 == ulp and q % 2 == 1):
+        q += 1
+    return sign * q * ulp
+
+
+def test_bf16_known_answers():
+    vals = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.0, 0.0, np.inf, np.nan], np.float32)
+    bits = oq.f32_to_bf16_bits(vals)
+    assert bits[0] == 0x3F80
+    assert bits[1] == 0x3F80          # halfway, ties to even (down)
+    assert bits[2] == 0x3F82          # halfway, ties to even (up)
+    assert bits[3] == 0xC000
+    assert bits[4] == 0x0000
+    assert bits[5] == 0x7F80
+    assert bits[6] == 0x7FC0
+
+
+def test_bf16_matches_torch_rne():
+    rng = np.random.default_rng(1)
+    v = (rng.standard_normal(100_000) * 10.0 ** rng.integers(-6, 6, 100_000)).astype(np.float32)
+    ours = oq.f32_to_bf16_bits(v)
+    ref = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().astype(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+# ----------------------------------------------------------------------------------- pack / unpack
+
+
+def test_pack_int4_known_answer():
+    codes = np.array([[0, 1, 2, 3, 4, 5, 6, 7, 15, 15, 15, 15, 15, 15, 15, 15]], np.uint32)
+    w = oq.pack_affine(codes, 4)
+    assert w.tolist() == [[0x76543210, 0xFFFFFFFF]]
+
+
+def _brute_pack(codes, bits):
+    out = []
+    for row in codes:
+        stream = []
+        for c in row:
+            stream += [(int(c) >> b) & 1 for b in range(bits)]
+        out.append([sum(stream[32 * w + j] << j for j in range(32)) for w in range(len(stream) // 32)])
+    return np.array(out, dtype=np.uint64).astype(np.uint32)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+def test_pack_unpack_brute_force_and_roundtrip(bits):
+    rng = np.random.default_rng(bits)
+    n_in = 64 if bits in (2, 4, 8) else 96
+    codes = rng.integers(0, 1 << bits, size=(5, n_in)).astype(np.uint32)
+    packed = oq.pack_affine(codes, bits)
+    assert np.array_equal(packed, _brute_pack(codes, bits))
+    assert np.array_equal(oq.unpack_affine(packed, n_in, bits), codes)
+
+
+def test_unpack_int4_fast_equals_general():
+    rng = np.random.default_rng(3)
+    words = rng.integers(0, 2 ** 32, size=(7, 3, 16), dtype=np.uint64).astype(np.uint32)
+    assert np.array_equal(oq.unpack_int4_fast(words, 128), oq.unpack_affine(words, 128, 4))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+def test_product_pack_matches_oracle(bits):
+    from quanta_amd import quant as q
+
+    rng = np.random.default_rng(10 + bits)
+    n_in = 128 if bits in (2, 4, 8) else 96
+    codes = rng.integers(0, 1 << bits, size=(3, 4, n_in)).astype(np.uint32)
+    ours = q.pack_affine(torch.from_numpy(codes.astype(np.int64)), bits).numpy().view(np.uint32)
+    assert np.array_equal(ours, oq.pack_affine(codes, bits))
+    back = q.unpack_affine(torch.from_numpy(ours.view(np.int32)), n_in, bits).numpy()
+    assert np.array_equal(back.astype(np.uint32), codes)
+
+
+# ----------------------------------------------------------------------------------- quantize / dequant
+
+
+def test_quantizer_error_bound_and_product_equality():
+    from quanta_amd import quant as q
+
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((6, 256)) * 0.02).astype(np.float32)
+    packed, s_bits, b_bits, codes = oq.quantize_rtn(w, 4, 64)
+    assert codes.max() <= 15
+    deq = oq.dequant_exact(packed, s_bits, b_bits, 256)
+    wb = oq.bf16_bits_to_f32(oq.f32_to_bf16_bits(w)).astype(np.float64)
+    s = np.repeat(oq.bf16_bits_to_f32(s_bits).astype(np.float64), 64, axis=-1)
+    # RTN: within half a step (plus the bf16 rounding of scale/bias, which can push the
+    # top code's reconstruction one bf16 step of the bias away)
+    assert np.all(np.abs(deq - wb) <= 0.5 * s * (1 + 2 ** -6) + np.abs(wb) * 2 ** -7 + 1e-12)
+    qp, qs, qb = q.quantize_affine(torch.from_numpy(w), 4, 64, scale_dtype=torch.bfloat16)
+    assert np.array_equal(qp.numpy().view(np.uint32), packed)
+    assert np.array_equal(qs.view(torch.int16).numpy().astype(np.uint16), s_bits)
+    assert np.array_equal(qb.view(torch.int16).numpy().astype(np.uint16), b_bits)
+
+
+def test_dequant_exact_rational():
+    """bf16(fp32(s)*q + fp32(b)) checked with exact rationals (independent of numpy rounding)."""
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((3, 128)) * 0.05).astype(np.float32)
+    packed, s_bits, b_bits, codes = oq.quantize_rtn(w, 4, 64)
+    got = oq.dequant_bf16_bits(packed, s_bits, b_bits, 128)
+    sf = oq.bf16_bits_to_f32(s_bits)
+    bf = oq.bf16_bits_to_f32(b_bits)
+    for r, c in itertools.product(range(3), range(128)):
+        g = c // 64
+        exact = Fraction(float(sf[r, g])) * int(codes[r, c]) + Fraction(float(bf[r, g]))
+        want = _rne_bf16_fraction(_rne_f32_fraction(exact))
+        assert Fraction(float(oq.bf16_bits_to_f32(got[r, c]))) == want, (r, c)
+
+
+def test_dequant_special_codes():
+    s_bits = oq.f32_to_bf16_bits(np.full((1, 1), 0.0625, np.float32))
+    b_bits = oq.f32_to_bf16_bits(np.full((1, 1), -0.5, np.float32))
+    codes = np.array([[0] * 32 + [15] * 32], np.uint32)
+    words = oq.pack_affine(codes, 4)
+    vals = oq.bf16_bits_to_f32(oq.dequant_bf16_bits(words, s_bits, b_bits, 64))
+    assert np.all(vals[0, :32] == -0.5) and np.all(vals[0, 32:] == 15 * 0.0625 - 0.5)
+
+
+# ----------------------------------------------------------------------------------- routing
+
+
+def _brute_route(x, wr, k, scoring, bias=None, n_group=1, topk_group=1, norm=True, scale=1.0):
+    out_idx, out_w = [], []
+    for t in range(x.shape[0]):
+        logit = [float(np.dot(x[t].astype(np.float64), wr[e].astype(np.float64)))
+                 for e in range(wr.shape[0])]
+        if scoring == "softmax":
+            m = max(logit)
+            ex = [np.exp(v - m) for v in logit]
+            sc = [v / sum(ex) for v in ex]
+        else:
+            sc = [1 / (1 + np.exp(-v)) for v in logit]
+        ch = [sc[e] + (bias[e] if bias is not None else 0.0) for e in range(len(sc))]
+        allowed = set(range(len(sc)))
+        if n_group > 1:
+            gs = len(sc) // n_group
+            gscore = [sum(sorted(ch[g * gs:(g + 1) * gs])[-2:]) for g in range(n_group)]
+            keep = sorted(range(n_group), key=lambda g: (-gscore[g], g))[:topk_group]
+            allowed = {e for e in range(len(sc)) if e // gs in keep}
+        sel = sorted(allowed, key=lambda e: (-ch[e], e))[:k]
+        w = [sc[e] for e in sel]
+        if norm:
+            tot = sum(w) + 1e-20
+            w = [v / tot for v in w]
+        out_idx.append(sel)
+        out_w.append([v * scale for v in w])
+    return np.array(out_idx), np.array(out_w)
+
+
+@pytest.mark.parametrize("case", [
+    dict(scoring="softmax"),
+    dict(scoring="sigmoid"),
+    dict(scoring="sigmoid", bias=True, n_group=4, topk_group=2, scale=2.5),
+    dict(scoring="sigmoid", bias=True, norm=False),
+])
+def test_route_brute_force(case):
+    rng = np.random.default_rng(6)
+    E, H, N, k = 16, 24, 9, 3
+    x = rng.standard_normal((N, H))
+    wr = rng.standard_normal((E, H)) * 0.3
+    bias = rng.standard_normal(E) * 0.1 if case.get("bias") else None
+    kw = dict(scoring=case["scoring"], bias=bias, n_group=case.get("n_group", 1),
+              topk_group=case.get("topk_group", 1), norm=case.get("norm", True),
+              scale=case.get("scale", 1.0))
+    bi, bw = _brute_route(x, wr, k, **kw)
+    idx, w, *_ = om.route(x, wr, k=k, scoring=kw["scoring"], norm_topk=kw["norm"], bias=bias,
+                          n_group=kw["n_group"], topk_group=kw["topk_group"], scale=kw["scale"])
+    assert np.array_equal(idx, bi)
+    assert np.allclose(w, bw, rtol=1e-12, atol=0)
+
+
+def test_route_softmax_matches_torch_topk():
+    from scipy.special import softmax
+
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((64, 128))
+    wr = rng.standard_normal((64, 128)) * 0.02
+    idx, w, logits, scores, _ = om.route(x, wr, k=8, scoring="softmax")
+    assert np.allclose(scores, softmax(x @ wr.T, axis=-1), rtol=1e-12)
+    tv, ti = torch.topk(torch.from_numpy(scores), 8, dim=-1)
+    assert all(set(a) == set(b) for a, b in zip(idx.tolist(), ti.numpy().tolist()))
+    assert np.allclose(w, (tv / tv.sum(-1, keepdim=True)).numpy(), rtol=1e-12)
+
+
+def test_group_route_matches_transformers_deepseek_v3():
+    tf = pytest.importorskip("transformers")
+    from transformers.models.deepseek_v3.configuration_deepseek_v3 import DeepseekV3Config
+    from transformers.models.deepseek_v3.modeling_deepseek_v3 import DeepseekV3TopkRouter
+
+    E, H, N, k = 32, 48, 40, 4
+    cfg = DeepseekV3Config(hidden_size=H, n_routed_experts=E, num_experts_per_tok=k, n_group=8,
+                           topk_group=3, norm_topk_prob=True, routed_scaling_factor=2.5)
+    router = DeepseekV3TopkRouter(cfg).double()
+    rng = np.random.default_rng(8)
+    wr = rng.standard_normal((E, H)) * 0.2
+    bias = rng.standard_normal(E) * 0.05
+    with torch.no_grad():
+        router.weight.copy_(torch.from_numpy(wr))
+        router.e_score_correction_bias.copy_(torch.from_numpy(bias))
+    x = rng.standard_normal((N, H))
+    with torch.no_grad():
+        out = router(torch.from_numpy(x))
+    tw, ti = out[1].numpy(), out[2].numpy()
+    idx, w, *_ = om.route(x, wr, k=k, scoring="sigmoid", bias=bias, n_group=8, topk_group=3,
+                          scale=2.5)
+    for t in range(N):
+        assert set(idx[t]) == set(ti[t])
+        d_ours = dict(zip(idx[t], w[t]))
+        for e, v in zip(ti[t], tw[t]):   # transformers' router evaluates in float32
+            assert abs(d_ours[e] - v) < 1e-6 * max(1.0, abs(v))
+
+
+# ----------------------------------------------------------------------------------- permute
+
+
+def test_permute_brute_force_and_invariants():
+    rng = np.random.default_rng(9)
+    N, k, E = 37, 5, 13
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(N)]).astype(np.int32)
+    counts, offsets, order, inv = om.permute(idx, E)
+    exp = idx.reshape(-1)
+    brute = sorted(range(N * k), key=lambda m: (exp[m], m))
+    assert order.tolist() == brute
+    assert offsets[-1] == N * k and np.array_equal(np.diff(offsets), counts)
+    assert np.array_equal(inv[order], np.arange(N * k))
+    assert np.array_equal(counts, np.bincount(exp, minlength=E))
+
+
+# ----------------------------------------------------------------------------------- expert math
+
+
+def _tiny_layer(rng, E=6, H=128, I=64, Is=64, gated=True):
+    gu_w = (rng.standard_normal((E, 2 * I, H)) * 0.05).astype(np.float32)
+    dn_w = (rng.standard_normal((E, H, I)) * 0.05).astype(np.float32)
+    gq = oq.quantize_rtn(gu_w, 4, 64)
+    dq = oq.quantize_rtn(dn_w, 4, 64)
+    bf = lambda a: oq.bf16_bits_to_f32(oq.f32_to_bf16_bits(a)).astype(np.float64)
+    p = dict(gate=bf(rng.standard_normal((E, H)) * 0.1),
+             gu_packed=gq[0], gu_scale=gq[1], gu_bias=gq[2],
+             dn_packed=dq[0], dn_scale=dq[1], dn_bias=dq[2])
+    if Is:
+        p.update(shared_gate_proj=bf(rng.standard_normal((Is, H)) * 0.05),
+                 shared_up_proj=bf(rng.standard_normal((Is, H)) * 0.05),
+                 shared_down_proj=bf(rng.standard_normal((H, Is)) * 0.05))
+        if gated:
+            p["shared_expert_gate"] = bf(rng.standard_normal((1, H)) * 0.1)
+    return p
+
+
+def test_gather_qmm_matches_explicit_loop():
+    rng = np.random.default_rng(11)
+    p = _tiny_layer(rng, E=3, H=128, I=64)
+    x = oq.round_bf16(rng.standard_normal((5, 128)))
+    ex = np.array([2, 0, 1, 2, 0])
+    got = om.gather_qmm(x, ex, p["gu_packed"], p["gu_scale"], p["gu_bias"], 128, round_out=False)
+    codes = oq.unpack_affine(p["gu_packed"], 128, 4)
+    s = oq.bf16_bits_to_f32(p["gu_scale"])
+    b = oq.bf16_bits_to_f32(p["gu_bias"])
+    for m in range(5):
+        for o in range(0, 128, 17):
+            acc = 0.0
+            for kk in range(128):
+                acc += float(x[m, kk]) * (float(s[ex[m], o, kk // 64]) * int(codes[ex[m], o, kk])
+                                          + float(b[ex[m], o, kk // 64]))
+            assert abs(got[m, o] - acc) < 1e-9
+
+
+def test_sparse_equals_dense_when_k_equals_E():
+    """k = E: the sparse gather path equals the run-every-expert oracle (special case that reduces
+    to dense per-expert products, src/quanta/qwen35/moe.py:127-142)."""
+    rng = np.random.default_rng(12)
+    E, H, I = 4, 128, 64
+    p = _tiny_layer(rng, E=E, H=H, I=I, Is=0)
+    x = oq.round_bf16(rng.standard_normal((6, H)))
+    idx, w, *_ = om.route(x, p["gate"], k=E)
+    gu_d = oq.dequant_exact(p["gu_packed"], p["gu_scale"], p["gu_bias"], H)
+    dn_d = oq.dequant_exact(p["dn_packed"], p["dn_scale"], p["dn_bias"], I)
+    dense = om.moe_dense_reference(x, idx, w, gu_d, dn_d, I)
+    exp = idx.reshape(-1)
+    tok = np.repeat(np.arange(6), E)
+    gu = om.gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], H, round_out=False)
+    hh = gu[:, :I] / (1 + np.exp(-gu[:, :I])) * gu[:, I:]
+    d = om.gather_qmm(hh, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], I, round_out=False)
+    assert np.allclose(om.combine(d, w), dense, rtol=1e-10, atol=1e-12)
+
+
+def test_block_matches_transformers_qwen35_moe():
+    """The oracle's routing + expert + gated-shared structure equals transformers' independent
+    Qwen3.5-MoE sparse block (float64, dequantized weights). The oracle's bf16 materialisation
+    points are disabled by comparing its unrounded dense reference path plus shared expert."""
+    pytest.importorskip("transformers")
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from transformers.models.qwen3_5_moe.modeling_qwen3_5_moe import Qwen3_5MoeSparseMoeBlock
+
+    rng = np.random.default_rng(13)
+    E, H, I, Is, k, N = 8, 128, 64, 64, 3, 7
+    p = _tiny_layer(rng, E=E, H=H, I=I, Is=Is)
+    cfg = Qwen3_5MoeTextConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k,
+                               moe_intermediate_size=I, shared_expert_intermediate_size=Is)
+    blk = Qwen3_5MoeSparseMoeBlock(cfg).double()
+    gu_d = oq.dequant_exact(p["gu_packed"], p["gu_scale"], p["gu_bias"], H)
+    dn_d = oq.dequant_exact(p["dn_packed"], p["dn_scale"], p["dn_bias"], I)
+    with torch.no_grad():
+        blk.gate.weight.copy_(torch.from_numpy(p["gate"]))
+        blk.experts.gate_up_proj.copy_(torch.from_numpy(gu_d))
+        blk.experts.down_proj.copy_(torch.from_numpy(dn_d))
+        blk.shared_expert.gate_proj.weight.copy_(torch.from_numpy(p["shared_gate_proj"]))
+        blk.shared_expert.up_proj.weight.copy_(torch.from_numpy(p["shared_up_proj"]))
+        blk.shared_expert.down_proj.weight.copy_(torch.from_numpy(p["shared_down_proj"]))
+        blk.shared_expert_gate.weight.copy_(torch.from_numpy(p["shared_expert_gate"]))
+    x = oq.round_bf16(rng.standard_normal((N, H)))
+    with torch.no_grad():
+        y_hf = blk(torch.from_numpy(x)[None])[0].numpy()
+    idx, w, *_ = om.route(x, p["gate"], k=k)
+    routed = om.moe_dense_reference(x, idx, w, gu_d, dn_d, I)
+    g = x @ p["shared_gate_proj"].T
+    u = x @ p["shared_up_proj"].T
+    sh = ((g / (1 + np.exp(-g))) * u) @ p["shared_down_proj"].T
+    sg = 1 / (1 + np.exp(-(x @ p["shared_expert_gate"].reshape(-1))))
+    y = routed + sh * sg[:, None]
+    # transformers' router evaluates its softmax in float32; everything else is float64
+    assert np.allclose(y, y_hf, rtol=1e-6, atol=1e-7)
+    with torch.no_grad():
+        _, _, hf_idx = blk.gate(torch.from_numpy(x))
+    assert all(set(a) == set(b) for a, b in zip(idx.tolist(), hf_idx.numpy().tolist()))
+    # and the bf16-materialising oracle stays within bf16 distance of the exact block
+    y_bf, _ = om.moe_forward(x, p, k=k, inter=I)
+    assert np.max(np.abs(y_bf - y)) < 2e-2 * max(1.0, np.max(np.abs(y)))
+
+
+def test_route_margin_flags_ties():
+    choice = np.array([[3.0, 1.0, 1.0, 0.5], [4.0, 3.0, 2.0, 1.0]])
+    m = om.route_margin(choice, 2)
+    assert m[0] == 0.0 and m[1] == 1.0
