@@ -50,7 +50,7 @@ extern "C" {
 /* grouped-qmm regimes */
 #define QMOE_REGIME_AUTO 0
 #define QMOE_REGIME_SMALL 1 /* 16-token m-tiles, weights streamed to registers (decode) */
-#define QMOE_REGIME_LARGE 2 /* 128x128 tiles, LDS-dequantised bf16 MFMA (prefill) */
+#define QMOE_REGIME_LARGE 2 /* 128x256 tiles, fp16-dequantised LDS tiles, 32x32 MFMA (prefill) */
 
 /* grouped-qmm epilogues */
 #define QMOE_EPI_SWIGLU 0 /* out[:, j] = bf16(silu(bf16(gate_j)) * bf16(up_j)), rows = [gate; up] */
@@ -61,7 +61,7 @@ extern "C" {
  * plus the DeepSeek/GLM router fields (n_group, topk_group, routed_scaling_factor,
  * src/quanta/glm/config.py:65,69). */
 typedef struct {
-  int32_t hidden;        /* H, multiple of 128 */
+  int32_t hidden;        /* H, multiple of 256 */
   int32_t n_experts;     /* E <= 1024 */
   int32_t top_k;         /* k (num_experts_per_tok or topk_override), 1 <= k <= min(E, 64) */
   int32_t inter;         /* I, multiple of 128 */
@@ -73,7 +73,7 @@ typedef struct {
   float routed_scale;    /* routed_scaling_factor applied after renormalisation */
   int32_t expert_format; /* QMOE_FMT_* */
   int32_t router_format; /* QMOE_ROUTER_* */
-  int32_t router_rows;   /* rows of the tiled bf16 router (>= E + shared_gated, % 128 == 0) */
+  int32_t router_rows;   /* rows of the tiled bf16 router (>= E + shared_gated, % 256 == 0) */
   int32_t shared_gated;  /* 1: shared output scaled by sigmoid(x . shared_expert_gate) */
   int32_t regime;        /* QMOE_REGIME_* for the routed experts (AUTO: small for N <= 256) */
 } qmoe_config_t;
@@ -145,7 +145,10 @@ int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_
                      int64_t n_slots, const int32_t* offsets, const int32_t* tile_off,
                      int n_experts, int64_t dense_rows, int K, int n_rows, int weight_format,
                      const void* codes, const uint16_t* sb, int epilogue, void* out, int ld_out,
-                     int regime, void* stream);
+                     int regime, void* ws, size_t ws_bytes, void* stream);
+/* Workspace qmoe_grouped_qmm needs: the large-M int4 regime stages an fp16 copy of the
+ * activations (per-row power-of-two scaled, exact for bf16 inputs); otherwise 0. */
+size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format, int regime);
 
 /* y[t] = bf16(sum_s w[t,s] * d[inv[t*k+s]] + shared_gate[t] * shared_out[t]) (fp32 sums in
  * slot order; shared_out/shared_gate may be NULL). Replaces the combine

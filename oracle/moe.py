@@ -130,18 +130,26 @@ def permute(idx: np.ndarray, n_experts: int):
 
 
 def gather_qmm(xrows: np.ndarray, experts: np.ndarray, packed: np.ndarray, scale: np.ndarray,
-               bias: np.ndarray, in_features: int, *, round_out: bool = True) -> np.ndarray:
+               bias: np.ndarray, in_features: int, *, round_out: bool = True,
+               round_weights: bool = False) -> np.ndarray:
     """y[m] = x[m] . (s*q + b)[experts[m]]^T per row, float64, rounded to bf16.
 
     Restates `mx.gather_qmm(x, packed, scale, bias, rhs_indices=exp, transpose=True)`
     (`src/quanta/qwen35/moe.py:117-123`): the weight stack is [E, out, in] affine int4 with
     bf16 scale/bias per 64 along `in`; output dtype follows the bf16 scale dtype.
+    Default: the exact affine weight (the fused matrix-vector form, sum x*(s*q+b) with float
+    accumulation). `round_weights=True` is the large-batch form that first dequantizes each
+    weight to bf16 and then multiplies (the tile-dequant matmul form); both are bf16-accurate
+    and differ by the bf16 rounding of the weights (parity unpinned at the MLX boundary as to
+    which form MLX picks for a given batch size).
     """
     experts = np.asarray(experts).reshape(-1)
     out = np.zeros((xrows.shape[0], packed.shape[1]), dtype=np.float64)
     for e in np.unique(experts):
         sel = experts == e
         w = dequant_exact(packed[e], scale[e], bias[e], in_features)
+        if round_weights:
+            w = round_bf16(w)
         out[sel] = xrows[sel].astype(np.float64) @ w.T
     return round_bf16(out) if round_out else out
 
@@ -192,7 +200,7 @@ def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
 
 def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "softmax",
                 norm_topk: bool = True, n_group: int = 1, topk_group: int = 1,
-                scale: float = 1.0):
+                scale: float = 1.0, round_weights: bool = False):
     """Whole block y = bf16(routed + shared) for x [N, H] (`src/quanta/qwen35/moe.py:154-202`).
 
     `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
@@ -209,9 +217,11 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
         scale=scale)
     exp = idx.reshape(-1)
     tok = np.repeat(np.arange(n), k)
-    gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim)
+    gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim,
+                    round_weights=round_weights)
     h = swiglu(gu, inter)
-    d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter)
+    d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
+                   round_weights=round_weights)
     routed = combine(d, w)
     y = routed.copy()
     sh = None
@@ -220,7 +230,7 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
                                        p["shared_down_proj"], p.get("shared_expert_gate"))
         y = y + sh
     inter_d = dict(idx=idx, w=w, logits=logits, scores=scores, choice=choice, gu=gu, h=h, d=d,
-                   routed=routed, shared=sh)
+                   routed=routed, shared=sh, y_exact=y)
     return round_bf16(y), inter_d
 
 

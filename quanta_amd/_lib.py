@@ -73,7 +73,8 @@ SIGNATURES = {
     "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
     "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _I, _P,
-                              _I, _I, _P]),
+                              _I, _I, _P, ctypes.c_size_t, _P]),
+    "qmoe_grouped_qmm_workspace": (ctypes.c_size_t, [_I64, _I, _I, _I]),
     "qmoe_combine": (_I, [_P, _P, _P, _I64, _I, _I, _P, _P, _P, _P]),
     "qmoe_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "qmoe_tile_int4": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),

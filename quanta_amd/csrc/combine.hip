@@ -83,10 +83,9 @@ int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int t
 
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
-  size_t logits, idx, w, sg, counts, offsets, tile_off, sorted, inv, h, d, sh_h, sh_out, total;
+  size_t logits, idx, w, sg, counts, offsets, tile_off, sorted, inv, h, d, sh_h, sh_out, x16,
+      x_sinv, h16, h_sinv, total;
 };
-
-static inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   WsLayout L{};
@@ -111,6 +110,11 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.d = take(static_cast<size_t>(mc) * c.hidden * 2);
   L.sh_h = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.shared_inter : 0) * 2);
   L.sh_out = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.hidden : 0) * 2);
+  // fp16 per-row-scaled activation copies for the large-M int4 regime
+  L.x16 = take(static_cast<size_t>(N) * c.hidden * 2);
+  L.x_sinv = take(static_cast<size_t>(N) * 4);
+  L.h16 = take(static_cast<size_t>(mc) * c.inter * 2);
+  L.h_sinv = take(static_cast<size_t>(mc) * 4);
   L.total = o;
   return L;
 }
@@ -120,13 +124,15 @@ static int validate_config(const qmoe_config_t& c) {
                                   c.topk_group);
   if (rc) return rc;
   if (c.hidden % 128) return fail("config: hidden % 128 == 0 required");
+  if (c.regime == QMOE_REGIME_LARGE && c.hidden % 256)
+    return fail("config: the large-M regime needs hidden % 256 == 0");
   if (c.inter <= 0 || c.inter % 128) return fail("config: inter % 128 == 0 required");
   if (c.shared_inter < 0 || c.shared_inter % 128) return fail("config: shared_inter % 128 == 0 required");
   if (c.expert_format != QMOE_FMT_INT4_G64 && c.expert_format != QMOE_FMT_BF16)
     return fail("config: expert_format must be int4-g64 (0) or bf16 (1)");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {
-    if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 128)
-      return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 128");
+    if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 256)
+      return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 256");
   } else if (c.router_format != QMOE_ROUTER_F32) {
     return fail("config: unknown router_format");
   }
@@ -151,12 +157,20 @@ extern "C" int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* 
                         static_cast<hipStream_t>(stream));
 }
 
+extern "C" size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format,
+                                             int regime) {
+  if (act_rows <= 0 || K <= 0) return 0;
+  if (regime == QMOE_REGIME_LARGE && weight_format == QMOE_FMT_INT4_G64)
+    return act16_ws_bytes(act_rows, K);
+  return 0;
+}
+
 extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_of,
                                 int slot_div, int64_t n_slots, const int32_t* offsets,
                                 const int32_t* tile_off, int n_experts, int64_t dense_rows,
                                 int K, int n_rows, int weight_format, const void* codes,
                                 const uint16_t* sb, int epilogue, void* out, int ld_out,
-                                int regime, void* stream) {
+                                int regime, void* ws, size_t ws_bytes, void* stream) {
   if (!act || !codes || !out) return fail("qmoe_grouped_qmm: null pointer");
   if (weight_format == QMOE_FMT_INT4_G64 && !sb) return fail("qmoe_grouped_qmm: int4 needs sb");
   if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16)
@@ -192,7 +206,19 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
     if (dense_rows <= 0) return fail("qmoe_grouped_qmm: dense_rows must be positive");
     bound = (dense_rows + m_tile - 1) / m_tile;
   }
-  return launch_qmm(a, weight_format, epilogue, regime, bound, static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (regime == QMOE_REGIME_LARGE && weight_format == QMOE_FMT_INT4_G64) {
+    const size_t need = act16_ws_bytes(act_rows, K);
+    if (!ws || ws_bytes < need) return fail("qmoe_grouped_qmm: workspace too small for the fp16 copy");
+    uint16_t* act16 = static_cast<uint16_t*>(ws);
+    float* sinv = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                           align256(static_cast<size_t>(act_rows) * K * 2));
+    const int rc = launch_act_to_f16(act, act_rows, K, act16, sinv, st);
+    if (rc) return rc;
+    a.act16 = act16;
+    a.row_sinv = sinv;
+  }
+  return launch_qmm(a, weight_format, epilogue, regime, bound, st);
 }
 
 extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
@@ -200,9 +226,15 @@ extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
   return ws_layout(*cfg, N).total;
 }
 
+// Large-M tiles pay off once a batch gives experts tens of rows; they also need the output
+// widths (hidden for the down projection) to be multiples of the 256-row tile.
+static int dense_regime(const qmoe_config_t& c, int64_t N) {
+  return (N > 256 && c.hidden % 256 == 0) ? QMOE_REGIME_LARGE : QMOE_REGIME_SMALL;
+}
+
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  return (N <= 256) ? QMOE_REGIME_SMALL : QMOE_REGIME_LARGE;
+  return dense_regime(c, N);
 }
 
 extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
@@ -236,6 +268,10 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   uint16_t* d = reinterpret_cast<uint16_t*>(base + L.d);
   uint16_t* sh_h = reinterpret_cast<uint16_t*>(base + L.sh_h);
   uint16_t* sh_out = reinterpret_cast<uint16_t*>(base + L.sh_out);
+  uint16_t* x16 = reinterpret_cast<uint16_t*>(base + L.x16);
+  float* x_sinv = reinterpret_cast<float*>(base + L.x_sinv);
+  uint16_t* h16 = reinterpret_cast<uint16_t*>(base + L.h16);
+  float* h_sinv = reinterpret_cast<float*>(base + L.h_sinv);
 
   const int n = static_cast<int>(N);
   const int64_t mc = N * c.top_k;
@@ -256,7 +292,7 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     QmmArgs a{};
     a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
     a.K = c.hidden; a.n_rows = c.router_rows; a.codes = wts->router_w; a.out = logits; a.ld_out = ld;
-    const int rreg = (N <= 256) ? QMOE_REGIME_SMALL : QMOE_REGIME_LARGE;
+    const int rreg = dense_regime(c, N);
     const int rt = (rreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
     rc = launch_qmm(a, FMT_BF16, EPI_F32, rreg, (N + rt - 1) / rt, stream);
   }
@@ -270,6 +306,7 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
                       stream);
   if (rc) return rc;
   const int64_t bound = mtile_upper_bound(mc, c.n_experts, m_tile);
+  const bool f16_acts = (regime == QMOE_REGIME_LARGE && wfmt == FMT_INT4);
   // 4. routed gate_up + SwiGLU -> h (sorted order)
   {
     QmmArgs a{};
@@ -277,11 +314,16 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
     a.out = h; a.ld_out = c.inter;
+    if (f16_acts) {
+      rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, stream);
+      if (rc) return rc;
+      a.act16 = x16; a.row_sinv = x_sinv;
+    }
     rc = launch_qmm(a, wfmt, EPI_SWIGLU, regime, bound, stream);
     if (rc) return rc;
   }
   // 5. shared expert gate_up + SwiGLU
-  const int sreg = (N <= 256) ? QMOE_REGIME_SMALL : QMOE_REGIME_LARGE;
+  const int sreg = dense_regime(c, N);
   const int st = (sreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
   if (c.shared_inter > 0) {
     QmmArgs a{};
@@ -298,6 +340,11 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
     a.out = d; a.ld_out = c.hidden;
+    if (f16_acts) {
+      rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);
+      if (rc) return rc;
+      a.act16 = h16; a.row_sinv = h_sinv;
+    }
     rc = launch_qmm(a, wfmt, EPI_BF16, regime, bound, stream);
     if (rc) return rc;
   }

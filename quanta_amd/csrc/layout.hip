@@ -36,7 +36,8 @@ __global__ void __launch_bounds__(256) dequant_native_kernel(
   out[i] = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// Tiled int4 -> natural bf16 [mats][rows][K]; checks the tiled transform is lossless.
+// Tiled int4 -> natural bf16 [mats][rows][K]; checks the tiled transform is lossless (it undoes
+// the nibble interleave of the stored words).
 __global__ void __launch_bounds__(256) dequant_tiled_kernel(
     const uint4* __restrict__ codes, const uint16_t* __restrict__ sb, int64_t n_lanes_total,
     int K, int rows, uint4* __restrict__ out) {
@@ -60,7 +61,7 @@ __global__ void __launch_bounds__(256) dequant_tiled_kernel(
     int gg = t >> 1, wi = 2 * g + (t & 1);
     float s = bf16_to_f32(sbp[gg * 2 + 0]);
     float b = bf16_to_f32(sbp[gg * 2 + 1]);
-    uint32_t w = words[t];
+    const uint32_t w = deinterleave_nibbles(words[t]);
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -74,7 +75,8 @@ __global__ void __launch_bounds__(256) dequant_tiled_kernel(
   }
 }
 
-// Native int4 -> tiled codes + tiled scale/bias. One thread per 16-byte lane slot.
+// Native int4 -> tiled codes (nibble-interleaved words) + tiled scale/bias. One thread per
+// 16-byte lane slot.
 __global__ void __launch_bounds__(256) tile_int4_kernel(
     const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
     const uint16_t* __restrict__ bias, int64_t n_lanes_total, int K, int rows,
@@ -92,7 +94,8 @@ __global__ void __launch_bounds__(256) tile_int4_kernel(
   int r = lane & 15, g = lane >> 4;
   int64_t row = mat * rows + R * 16 + r;
   const uint32_t* src = packed + row * wpr + p * 16;   // 16 words = groups 2p, 2p+1
-  codes[i] = make_uint4(src[2 * g], src[2 * g + 1], src[8 + 2 * g], src[8 + 2 * g + 1]);
+  codes[i] = make_uint4(interleave_nibbles(src[2 * g]), interleave_nibbles(src[2 * g + 1]),
+                        interleave_nibbles(src[8 + 2 * g]), interleave_nibbles(src[8 + 2 * g + 1]));
   if (g == 0) {
     uint16_t* d = sb + ((blk * 16 + r) * 2) * 2;
     int64_t gi = row * gpr + 2 * p;

@@ -99,6 +99,7 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
   int64_t arow = -1;
   if (mrow < m_cnt) arow = act_row(a, m0 + mrow);
   const bool row_ok = arow >= 0;
+  const uint32_t xmask = row_ok ? 0xFFFFFFFFu : 0u;   // rows past the segment read as zeros
   const uint16_t* xrow = a.act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
 
   f32x4_t acc[NT];
@@ -114,15 +115,15 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
     if (FMT == FMT_INT4) {
       const int nsb = a.K / 128;
       const int p0 = kpart * nsb / KSPLIT, p1 = (kpart + 1) * nsb / KSPLIT;
-      const uint4* cp[NT];
+      const u32x4* cp[NT];
       const uint2* sp[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int64_t tb = (static_cast<int64_t>(e) * tiles_per_expert + tile[t]) * nsb;
-        cp[t] = static_cast<const uint4*>(a.codes) + tb * 64 + lane;
+        cp[t] = static_cast<const u32x4*>(a.codes) + tb * 64 + lane;
         sp[t] = reinterpret_cast<const uint2*>(a.sb) + tb * 16 + (lane & 15);
       }
-      const uint4* xp = reinterpret_cast<const uint4*>(xrow) + 2 * lg;   // 16 lg bf16
+      const u32x4* xp = reinterpret_cast<const u32x4*>(xrow) + 2 * lg;   // 16 lg bf16
       bf16x8_t ones;
       {
         uint32_t* o = reinterpret_cast<uint32_t*>(&ones);
@@ -131,25 +132,23 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
       const f32x4_t zero4{0.f, 0.f, 0.f, 0.f};
 
       for (int p = p0; p < p1; ++p) {
-        uint4 q[NT];
+        u32x4 q[NT];
         uint2 sbv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           q[t] = cp[t][p * 64];
           sbv[t] = sp[t][p * 16];
         }
-        uint4 xv[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0),
-                       make_uint4(0, 0, 0, 0)};
-        if (row_ok) {
-          xv[0] = xp[p * 16 + 0];   // group 2p, k 16lg + 0..7
-          xv[1] = xp[p * 16 + 1];   // group 2p, k 16lg + 8..15
-          xv[2] = xp[p * 16 + 8];   // group 2p+1
-          xv[3] = xp[p * 16 + 9];
-        }
+        // group 2p: k 16lg + 0..7 (step 0) and + 8..15 (step 1); group 2p+1 likewise, +64
+        u32x4 xv[4];
+        xv[0] = xp[p * 16 + 0] & xmask;
+        xv[1] = xp[p * 16 + 1] & xmask;
+        xv[2] = xp[p * 16 + 8] & xmask;
+        xv[3] = xp[p * 16 + 9] & xmask;
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
-          const bf16x8_t A0 = pair_permute(xv[2 * gg]);
-          const bf16x8_t A1 = pair_permute(xv[2 * gg + 1]);
+          const bf16x8_t A0 = as_bf16x8(xv[2 * gg]);
+          const bf16x8_t A1 = as_bf16x8(xv[2 * gg + 1]);
           f32x4_t xs = mfma16(A0, ones, zero4);
           xs = mfma16(A1, ones, xs);
 #pragma unroll
@@ -169,20 +168,19 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
     } else {  // FMT_BF16
       const int nks = a.K / 32;
       const int k0 = kpart * nks / KSPLIT, k1 = (kpart + 1) * nks / KSPLIT;
-      const uint4* wp[NT];
+      const u32x4* wp[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int64_t tb = (static_cast<int64_t>(e) * tiles_per_expert + tile[t]) * nks;
-        wp[t] = static_cast<const uint4*>(a.codes) + tb * 64 + lane;
+        wp[t] = static_cast<const u32x4*>(a.codes) + tb * 64 + lane;
       }
-      const uint4* xp = reinterpret_cast<const uint4*>(xrow) + lg;   // 8 lg bf16
+      const u32x4* xp = reinterpret_cast<const u32x4*>(xrow) + lg;   // 8 lg bf16
 #pragma unroll 4
       for (int c = k0; c < k1; ++c) {
-        uint4 wv[NT];
+        u32x4 wv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) wv[t] = wp[t][c * 64];
-        const uint4 xv = row_ok ? xp[c * 4] : make_uint4(0, 0, 0, 0);
-        const bf16x8_t A = as_bf16x8(xv);
+        const bf16x8_t A = as_bf16x8(xp[c * 4] & xmask);
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = mfma16(A, as_bf16x8(wv[t]), acc[t]);
       }
@@ -218,13 +216,28 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
 }
 
 // ============================================================================ large-M kernel
-// Workgroup tile: 128 sorted positions x 128 weight rows (SwiGLU: 64 gate + 64 up rows).
-// LDS holds one 128-deep k-step of both operands in MFMA fragment order:
-//   X[mtile 8][kstep 4][lane 64] and W[wtile 8][kstep 4][lane 64], 16 B per entry.
+// Workgroup tile: 128 sorted positions x 256 weight rows (SwiGLU: 128 gate + 128 up rows ->
+// 128 h columns), one 128-deep k-step (one int4 superblock) per iteration. 4 wavefronts in a
+// 2x2 arrangement, each owning 64 positions x 128 weight rows as 2x4 blocks of
+// v_mfma_f32_32x32x16 (f16 for int4 weights, bf16 for bf16 weights).
+//
+// int4 weights are dequantized in registers, right after their global load and while the
+// previous step's MFMAs run, with packed fp16 FMAs (fp16(s*q + b), one rounding; 11-bit
+// mantissa), and activations come from the fp16 per-row-scaled copy (act16), so the step is an
+// exact-input fp16 product with fp32 accumulation. Outputs are rescaled per row by row_sinv.
+// bf16 weights (shared expert, router) are copied as they are, against bf16 activations.
+//
+// LDS (dynamic, 96 KiB): A [4 m-blocks of 32][8 k-steps of 16][64 lanes] and
+// B [8 n-blocks of 32][8][64], 16 B per entry, each entry one lane's MFMA fragment (lane l:
+// row l%32, k 8*(l/32)..+8 of the 16-k step), so fragment reads are conflict-free 16-byte loads.
+constexpr int kLgThreads = 256;
+constexpr size_t kLgLdsBytes = (2048 + 4096) * 16;
+
 template <int FMT, int EPI>
-__global__ void __launch_bounds__(256) qmm_large_kernel(QmmArgs a) {
-  __shared__ u32x4 lds_x[8 * 4 * 64];
-  __shared__ u32x4 lds_w[8 * 4 * 64];
+__global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
+  extern __shared__ u32x4 lds[];
+  u32x4* la = lds;
+  u32x4* lb = lds + 2048;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int e, m0, m_cnt;
@@ -232,174 +245,224 @@ __global__ void __launch_bounds__(256) qmm_large_kernel(QmmArgs a) {
   const int cb = blockIdx.x;
   const int tiles_per_expert = a.n_rows / 16;
   const int64_t ebase = static_cast<int64_t>(e) * tiles_per_expert;
+  const int nsb = a.K / 128;
+  const int nks32 = a.K / 32;
 
-  auto global_tile = [&](int wt) -> int {
-    if (EPI == EPI_SWIGLU) return (wt < 4) ? 4 * cb + wt : a.n_rows / 32 + 4 * cb + (wt - 4);
-    return 8 * cb + wt;
+  // 16-row global tile of local tile lt (0..15)
+  auto gtile = [&](int lt) -> int {
+    if (EPI == EPI_SWIGLU) return (lt < 8) ? 8 * cb + lt : a.n_rows / 32 + 8 * cb + (lt - 8);
+    return 16 * cb + lt;
   };
 
-  // activation row owned by this thread for the global->LDS copy
-  const int xr_row = tid >> 1, xr_half = tid & 1;
+  // ---- activation staging: thread -> row ar (0..127), 64-wide k half ah
+  const int ar = tid & 127, ah = tid >> 7;
   int64_t arow = -1;
-  if (xr_row < m_cnt) arow = act_row(a, m0 + xr_row);
-  const bool xr_ok = arow >= 0;
-  const uint32_t xmask = xr_ok ? 0xFFFFFFFFu : 0u;   // rows past the segment read as zeros
-  const u32x4* xsrc =
-      reinterpret_cast<const u32x4*>(a.act + (xr_ok ? arow : 0) * static_cast<int64_t>(a.K)) +
-      xr_half * 8;
+  if (ar < m_cnt) arow = act_row(a, m0 + ar);
+  const uint32_t xmask = (arow >= 0) ? 0xFFFFFFFFu : 0u;
+  const uint16_t* abase = (FMT == FMT_INT4) ? a.act16 : a.act;
+  const u32x4* asrc =
+      reinterpret_cast<const u32x4*>(abase + (arow >= 0 ? arow : 0) * static_cast<int64_t>(a.K)) +
+      ah * 8;
+  // chunk i covers k 64ah + 8i: 16-k step 4ah + i/2, half (i&1)
+  u32x4* adst = la + ((ar >> 5) * 8 + 4 * ah) * 64 + (ar & 31);
 
-  const int nsb = a.K / 128;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // weight slots for int4: two 16B lane slots per thread
-  const u32x4* cptr[2] = {nullptr, nullptr};
-  const uint2* sptr[2] = {nullptr, nullptr};
-  // bf16: thread owns lane slot (tile i, kstep (tid>>6)&3, lane tid&63) for i = 0..7; tiles
-  // 0..3 and 4..7 are each contiguous runs of global tiles.
-  const int nks = a.K / 32;
-  const u32x4* wlo = nullptr;
-  const u32x4* whi = nullptr;
+  // ---- weight staging pointers
+  const u32x4* cptr[4];
+  const uint2* sptr[4];
+  int bdst[4];
   if (FMT == FMT_INT4) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int slot = tid + 256 * i, wt = slot >> 6, ln = slot & 63;
-      const int64_t tb = (ebase + global_tile(wt)) * nsb;
-      cptr[i] = static_cast<const u32x4*>(a.codes) + tb * 64 + ln;
-      sptr[i] = reinterpret_cast<const uint2*>(a.sb) + tb * 16 + (ln & 15);
+    for (int i = 0; i < 4; ++i) {
+      const int slot = tid + 256 * i, lt = slot >> 6, L = slot & 63;
+      const int64_t tb = (ebase + gtile(lt)) * nsb;
+      cptr[i] = static_cast<const u32x4*>(a.codes) + tb * 64 + L;
+      sptr[i] = reinterpret_cast<const uint2*>(a.sb) + tb * 16 + (L & 15);
+      const int rb = 16 * lt + (L & 15), g = L >> 4;
+      bdst[i] = ((rb >> 5) * 8 + g) * 64 + (rb & 31);   // + word-dependent offsets below
     }
-  } else {
-    const int ks = (tid >> 6) & 3, ln = tid & 63;
-    wlo = static_cast<const u32x4*>(a.codes) + ((ebase + global_tile(0)) * nks + ks) * 64 + ln;
-    whi = static_cast<const u32x4*>(a.codes) + ((ebase + global_tile(4)) * nks + ks) * 64 + ln;
+  }
+  const u32x4* wbase = nullptr;
+  if (FMT == FMT_BF16) {
+    // thread owns lane slot (k32 chunk (tid>>6)&3, lane tid&63) of local tiles 0..15
+    wbase = static_cast<const u32x4*>(a.codes) + ((tid >> 6) & 3) * 64 + (tid & 63);
   }
 
-  f32x4_t acc[4][4];
+  f32x16_t acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  u32x4 xv[8];
-  u32x4 qv[2];
-  uint2 sv[2];
-  u32x4 wv[8];
-#define QMOE_LOAD_STEP(P)                                                                     \
-  do {                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                           \
-      xv[i] = xsrc[(P) * 16 + i] & xmask;                                                     \
-    }                                                                                         \
-    if (FMT == FMT_INT4) {                                                                    \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                         \
-        qv[i] = cptr[i][(P) * 64];                                                            \
-        sv[i] = sptr[i][(P) * 16];                                                            \
-      }                                                                                       \
-    } else {                                                                                  \
-      const int64_t tstride = static_cast<int64_t>(nks) * 64;                                 \
-      _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                         \
-        wv[i] = wlo[i * tstride + (P) * 4 * 64];                                              \
-        wv[4 + i] = whi[i * tstride + (P) * 4 * 64];                                          \
-      }                                                                                       \
-    }                                                                                         \
-  } while (0)
-
-  // LDS column of each wavefront's weight tiles
+  const int wm = wave >> 1, wn = wave & 1;
   int wtl[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (EPI == EPI_SWIGLU) wtl[j] = (j < 2) ? 2 * wn + j : 4 + 2 * wn + (j - 2);
-    else wtl[j] = 4 * wn + j;
-  }
+  for (int j = 0; j < 4; ++j)
+    wtl[j] = (EPI == EPI_SWIGLU) ? ((j < 2) ? 2 * wn + j : 4 + 2 * wn + (j - 2)) : 4 * wn + j;
 
-  QMOE_LOAD_STEP(0);
-  for (int p = 0; p < nsb; ++p) {
-    __syncthreads();
-    // activations -> LDS (fragment order)
-    {
-      // element i of this thread's 64-wide half row: kstep 2*half + i/4, lane group i%4
-      u32x4* xd = lds_x + ((xr_row >> 4) * 4 + 2 * xr_half) * 64 + (xr_row & 15);
-      xd[0 * 16] = xv[0];
-      xd[1 * 16] = xv[1];
-      xd[2 * 16] = xv[2];
-      xd[3 * 16] = xv[3];
-      xd[64 + 0 * 16] = xv[4];
-      xd[64 + 1 * 16] = xv[5];
-      xd[64 + 2 * 16] = xv[6];
-      xd[64 + 3 * 16] = xv[7];
-    }
+  u32x4 xv[8];
+  u32x4 bq[FMT == FMT_INT4 ? 4 : 16];   // raw codes (int4) or bf16 weight fragments
+  uint2 bs[4];
+  u32x4 dq[16];                         // dequantized fp16 weights (int4)
+
+  auto load_step = [&](int p) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = asrc[p * 16 + i] & xmask;
     if (FMT == FMT_INT4) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int slot = tid + 256 * i, wt = slot >> 6, ln = slot & 63;
-        const int r = ln & 15, g = ln >> 4;
-        const uint32_t words[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int gg = t >> 1, wi = 2 * g + (t & 1);
-          const uint32_t sbw = gg ? sv[i].y : sv[i].x;
-          const float s = bf16lo_to_f32(sbw), b = bf16hi_to_f32(sbw);
-          const uint32_t w = words[t];
-          uint32_t o[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float v0 = fmaf(s, static_cast<float>((w >> (8 * j)) & 0xFu), b);
-            const float v1 = fmaf(s, static_cast<float>((w >> (8 * j + 4)) & 0xFu), b);
-            o[j] = pack_bf16x2(v0, v1);
-          }
-          const int kl = 64 * gg + 8 * wi;   // first k of this word within the 128-deep step
-          lds_w[(wt * 4 + (kl >> 5)) * 64 + ((kl >> 3) & 3) * 16 + r] = u32x4{o[0], o[1], o[2], o[3]};
-        }
+      for (int i = 0; i < 4; ++i) {
+        bq[i] = cptr[i][p * 64];
+        bs[i] = sptr[i][p * 16];
       }
     } else {
-      lds_w[tid + 0 * 256] = wv[0];
-      lds_w[tid + 1 * 256] = wv[1];
-      lds_w[tid + 2 * 256] = wv[2];
-      lds_w[tid + 3 * 256] = wv[3];
-      lds_w[tid + 4 * 256] = wv[4];
-      lds_w[tid + 5 * 256] = wv[5];
-      lds_w[tid + 6 * 256] = wv[6];
-      lds_w[tid + 7 * 256] = wv[7];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        bq[i] = wbase[((ebase + gtile(i)) * nks32 + 4 * p) * 64];
     }
+  };
+  auto dequant_step = [&]() __attribute__((always_inline)) {
+    if (FMT == FMT_INT4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+          const uint32_t sbw = gg ? bs[i].y : bs[i].x;
+          const _Float16 s = static_cast<_Float16>(bf16lo_to_f32(sbw));
+          const _Float16 b = static_cast<_Float16>(bf16hi_to_f32(sbw));
+          const f16x2_t s2 = {s, s}, b2 = {b, b};
+          dq[4 * i + 2 * gg + 0] = dequant_word_f16(gg ? bq[i].z : bq[i].x, s2, b2);
+          dq[4 * i + 2 * gg + 1] = dequant_word_f16(gg ? bq[i].w : bq[i].y, s2, b2);
+        }
+      }
+    }
+  };
+
+  load_step(0);
+  dequant_step();
+  for (int p = 0; p < nsb; ++p) {
     __syncthreads();
-    if (p + 1 < nsb) QMOE_LOAD_STEP(p + 1);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      bf16x8_t A[4], B[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) A[i] = as_bf16x8(lds_x[((4 * wm + i) * 4 + ks) * 64 + lane]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) B[j] = as_bf16x8(lds_w[(wtl[j] * 4 + ks) * 64 + lane]);
+    for (int i = 0; i < 8; ++i) adst[(i >> 1) * 64 + 32 * (i & 1)] = xv[i];
+    if (FMT == FMT_INT4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(A[i], B[j], acc[i][j]);
+        for (int t = 0; t < 4; ++t) {
+          // word t: group gg = t>>1 (k 64gg..), step s = t&1 -> 16-k step 4gg + g, half s
+          const int gg = t >> 1, s = t & 1;
+          lb[bdst[i] + (4 * gg) * 64 + 32 * s] = dq[4 * i + t];
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        // tile i, k32 chunk cc = (tid>>6)&3, lane L = tid&63: row 16i + L%16, k 32cc + 8(L/16)
+        const int L = tid & 63, cc = (tid >> 6) & 3;
+        const int rb = 16 * i + (L & 15), kk = 32 * cc + 8 * (L >> 4);
+        lb[((rb >> 5) * 8 + (kk >> 4)) * 64 + 32 * ((kk >> 3) & 1) + (rb & 31)] = bq[i];
+      }
     }
+    __syncthreads();
+    const bool more = p + 1 < nsb;
+    if (more) load_step(p + 1);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      u32x4 A[2], B[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) A[i] = la[((2 * wm + i) * 8 + ks) * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) B[j] = lb[(wtl[j] * 8 + ks) * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = (FMT == FMT_INT4) ? mfma32_f16(A[i], B[j], acc[i][j])
+                                        : mfma32_bf16(A[i], B[j], acc[i][j]);
+    }
+    if (more) dequant_step();
   }
 
-  const int lg = lane >> 4;
+  // ---- epilogue: lane holds C[row 8(r/4) + 4(lane/32) + r%4][col lane%32] of each block
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int mr = 16 * (4 * wm + i) + 4 * lg + jj;
+    for (int r = 0; r < 16; ++r) {
+      const int mr = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
       if (mr >= m_cnt) continue;
+      float rs = 1.0f;
+      if (FMT == FMT_INT4) {
+        const int64_t ar2 = act_row(a, m0 + mr);
+        rs = (ar2 >= 0) ? a.row_sinv[ar2] : 0.0f;
+      }
       if (EPI == EPI_SWIGLU) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const int col = 64 * cb + 16 * (2 * wn + t) + (lane & 15);
-          store_out<EPI>(a, m0 + mr, col, acc[i][t][jj], acc[i][2 + t][jj]);
+          const int col = 128 * cb + 64 * wn + 32 * t + (lane & 31);
+          store_out<EPI>(a, m0 + mr, col, acc[i][t][r] * rs, acc[i][2 + t][r] * rs);
         }
       } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int col = 128 * cb + 16 * (4 * wn + t) + (lane & 15);
-          store_out<EPI>(a, m0 + mr, col, acc[i][t][jj], 0.f);
+          const int col = 256 * cb + 32 * (4 * wn + t) + (lane & 31);
+          store_out<EPI>(a, m0 + mr, col, acc[i][t][r] * rs, 0.f);
         }
       }
     }
   }
 }
 
-#undef QMOE_LOAD_STEP
+// ---------------------------------------------------------------- fp16 activation copy
+// One workgroup per row: absmax, then act16 = fp16(act * 2^(14 - e)) with 2^(e-1) <= absmax < 2^e,
+// so every value sits below 2^14 and all bf16 values within 2^28 of the row maximum convert
+// exactly. row_sinv = 2^(e - 14) undoes it on the product (a power of two: exact).
+__global__ void __launch_bounds__(256) act_to_f16_kernel(const uint16_t* __restrict__ act, int K,
+                                                         uint16_t* __restrict__ act16,
+                                                         float* __restrict__ row_sinv) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const u32x4* src = reinterpret_cast<const u32x4*>(act + row * K);
+  const int n8 = K / 8;
+  float m = 0.f;
+  for (int i = threadIdx.x; i < n8; i += 256) {
+    const u32x4 v = src[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m = fmaxf(m, fabsf(bf16lo_to_f32(v[j])));
+      m = fmaxf(m, fabsf(bf16hi_to_f32(v[j])));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  if (m > 0.f && m <= 3.4e38f) frexpf(m, &ex);   // m = f * 2^ex, f in [0.5, 1)
+  const int sh = (m > 0.f && m <= 3.4e38f) ? 14 - ex : 0;
+  if (threadIdx.x == 0) row_sinv[row] = ldexpf(1.0f, -sh);
+  u32x4* dst = reinterpret_cast<u32x4*>(act16 + row * K);
+  for (int i = threadIdx.x; i < n8; i += 256) {
+    const u32x4 v = src[i];
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x2_t h = {static_cast<_Float16>(ldexpf(bf16lo_to_f32(v[j]), sh)),
+                         static_cast<_Float16>(ldexpf(bf16hi_to_f32(v[j]), sh))};
+      o[j] = __builtin_bit_cast(uint32_t, h);
+    }
+    dst[i] = o;
+  }
+}
+
+int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16, float* row_sinv,
+                      hipStream_t stream) {
+  if (rows <= 0) return 0;
+  if (K % 8) return fail("act_to_f16: K % 8 == 0 required");
+  if (rows > 0x7fffffff) return fail("act_to_f16: too many rows");
+  act_to_f16_kernel<<<static_cast<unsigned>(rows), 256, 0, stream>>>(act, K, act16, row_sinv);
+  return check_launch("act_to_f16");
+}
+
 
 // ============================================================================ launcher
 template <int FMT, int EPI>
@@ -413,10 +476,15 @@ static void launch_small(const QmmArgs& a, int ksplit, int64_t mtiles, hipStream
 }
 
 template <int FMT, int EPI>
-static void launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
-  const int n_cb = (EPI == EPI_SWIGLU) ? a.n_rows / 128 : a.n_rows / 128;
-  dim3 grid(n_cb, static_cast<unsigned>(mtiles));
-  qmm_large_kernel<FMT, EPI><<<grid, 256, 0, stream>>>(a);
+static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
+  // 96 KiB of dynamic LDS is above the default per-kernel limit; set it for the current device
+  const hipError_t err =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_large_kernel<FMT, EPI>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLgLdsBytes));
+  if (err != hipSuccess) return fail(std::string("qmm(large): LDS attribute: ") + hipGetErrorString(err));
+  dim3 grid(a.n_rows / 256, static_cast<unsigned>(mtiles));
+  qmm_large_kernel<FMT, EPI><<<grid, kLgThreads, kLgLdsBytes, stream>>>(a);
+  return 0;
 }
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,
@@ -444,8 +512,11 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
 #undef QMOE_SMALL
   } else {
     if (a.K % 128) return fail("qmm(large): K % 128 == 0 required");
-    if (a.n_rows % 128) return fail("qmm(large): weight rows % 128 == 0 required");
-#define QMOE_LARGE(F, P) launch_large<F, P>(a, mtile_bound, stream)
+    if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
+    if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))
+      return fail("qmm(large): int4 weights need the fp16 activation copy");
+    int rc;
+#define QMOE_LARGE(F, P) rc = launch_large<F, P>(a, mtile_bound, stream)
     if (fmt == FMT_INT4) {
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT4, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT4, EPI_BF16);
@@ -456,6 +527,7 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       else QMOE_LARGE(FMT_BF16, EPI_F32);
     }
 #undef QMOE_LARGE
+    if (rc) return rc;
   }
   return check_launch("qmm");
 }

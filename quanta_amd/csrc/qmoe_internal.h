@@ -8,7 +8,10 @@
 //                            One 16-row x 128-K superblock is 1 KiB of codes, read by one
 //                            wavefront as a single contiguous dwordx4 load per lane.
 //                            Lane l (row l%16, lane group g=l/16) holds words {2g,2g+1} of
-//                            group 2p followed by words {2g,2g+1} of group 2p+1.
+//                            group 2p followed by words {2g,2g+1} of group 2p+1. Each stored
+//                            word carries its 8 codes c0..c7 with nibbles interleaved as
+//                            [c0 c2 c4 c6 c1 c3 c5 c7] (nibble 0 lowest), so (w >> 4j) & 0x000F000F
+//                            yields the natural-order pair (c_2j, c_2j+1) in one mask.
 //   * "tiled" bf16 matrix  : [mats][rows/16][K/32][64 lanes][8 bf16]; lane l holds
 //                            W[16R + l%16][32c + 8(l/16) .. +8).
 // Both tiled layouts put each lane's MFMA B-fragment (weight row = l%16, 8 consecutive K of
@@ -51,10 +54,29 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
-// Nibble unpack used by the int4 MFMA path: word w holds codes c0..c7 (nibble i = code i).
-// Output register r (r = 0..3) holds the bf16 pair (128 + c_r, 128 + c_{r+4}); 128 + c is exact
-// in bf16 (7 mantissa bits cover 128..255 in steps of 1). The activation fragment is permuted
-// to the same pair order by pair_permute().
+// Native word (nibble i = code i) <-> stored tiled word (nibbles [c0 c2 c4 c6 c1 c3 c5 c7]).
+__host__ __device__ __forceinline__ uint32_t interleave_nibbles(uint32_t w) {
+  uint32_t o = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    o |= ((w >> (8 * j)) & 0xFu) << (4 * j);            // c_2j   -> nibble j
+    o |= ((w >> (8 * j + 4)) & 0xFu) << (4 * j + 16);   // c_2j+1 -> nibble j+4
+  }
+  return o;
+}
+__host__ __device__ __forceinline__ uint32_t deinterleave_nibbles(uint32_t o) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    w |= ((o >> (4 * j)) & 0xFu) << (8 * j);
+    w |= ((o >> (4 * j + 16)) & 0xFu) << (8 * j + 4);
+  }
+  return w;
+}
+
+// Nibble unpack of a stored (interleaved) word for the decode MFMA path. Register j holds the
+// bf16 pair (128 + c_2j, 128 + c_2j+1): 128 + c is exact in bf16 (7 mantissa bits span 128..255
+// in steps of 1), and the pairs come out in natural k order, matching the activation fragment.
 __device__ __forceinline__ bf16x8_t unpack_q128(uint32_t w) {
   const uint32_t m = 0x000F000Fu, o = 0x43004300u;
   uint32_t r0 = (w & m) | o;
@@ -67,19 +89,6 @@ __device__ __forceinline__ bf16x8_t unpack_q128(uint32_t w) {
   return v;
 }
 
-// Activation fragment for unpack_q128: input is 8 consecutive bf16 x0..x7 as 4 u32 pairs
-// P0=(x0,x1) P1=(x2,x3) P2=(x4,x5) P3=(x6,x7); output pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7).
-__device__ __forceinline__ bf16x8_t pair_permute(uint4 q) {
-  bf16x8_t v;
-  uint32_t* p = reinterpret_cast<uint32_t*>(&v);
-  // v_perm_b32(src0, src1, sel): byte k of result = byte sel_k of {src0:src1} (src1 = bytes 0-3).
-  p[0] = __builtin_amdgcn_perm(q.z, q.x, 0x05040100u);
-  p[1] = __builtin_amdgcn_perm(q.z, q.x, 0x07060302u);
-  p[2] = __builtin_amdgcn_perm(q.w, q.y, 0x05040100u);
-  p[3] = __builtin_amdgcn_perm(q.w, q.y, 0x07060302u);
-  return v;
-}
-
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 q) {
   bf16x8_t v;
   __builtin_memcpy(&v, &q, 16);
@@ -89,6 +98,36 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 q) { return __builtin_bit_ca
 
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+__device__ __forceinline__ f32x16_t mfma32_f16(u32x4 a, u32x4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mfma32_bf16(u32x4 a, u32x4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Dequantize one stored word to 8 fp16 weights (natural k order): (1024 + c) built by bit
+// insertion is exact in fp16, minus 1024 gives c exactly, and one packed fp16 FMA gives
+// fp16(s*c + b) with a single round-to-nearest-even. s2/b2 hold the group's scale and bias
+// converted to fp16 (exact for bf16 values in fp16's normal range).
+__device__ __forceinline__ u32x4 dequant_word_f16(uint32_t w, f16x2_t s2, f16x2_t b2) {
+  const uint32_t m = 0x000F000Fu, o = 0x64006400u;
+  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  u32x4 out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t r = ((w >> (4 * j)) & m) | o;
+    const f16x2_t q = __builtin_bit_cast(f16x2_t, r) - k1024;
+    out[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
+  }
+  return out;
 }
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
@@ -126,6 +165,8 @@ struct QmmArgs {
   const uint16_t* sb;         // tiled scale/bias (int4 only)
   void* out;                  // output rows by sorted position
   int ld_out;                 // output row stride (elements)
+  const uint16_t* act16;      // large int4 regime: fp16 copy of act, row r scaled by 1/row_sinv[r]
+  const float* row_sinv;      // large int4 regime: per activation row inverse scale (2^e)
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1 };
@@ -133,6 +174,14 @@ enum { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,
                hipStream_t stream);
+// act [rows][K] bf16 -> act16 fp16 with a per-row power-of-two scale (exact for bf16 values
+// within 2^28 of the row's largest magnitude); row_sinv[r] = the inverse scale.
+int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16, float* row_sinv,
+                      hipStream_t stream);
+inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+inline size_t act16_ws_bytes(int64_t rows, int K) {
+  return align256(static_cast<size_t>(rows) * K * 2) + align256(static_cast<size_t>(rows) * 4);
+}
 int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
                    const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
                    hipStream_t stream);

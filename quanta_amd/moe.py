@@ -128,8 +128,9 @@ _CACHE_MAX = 64
 def _tkey(t):
     if t is None:
         return None
-    if isinstance(t, dict):
-        return tuple((k, _tkey(v)) for k, v in sorted(t.items()) if isinstance(v, torch.Tensor))
+    if isinstance(t, dict):   # tensors by identity/version, other fields (bits, group_size) by value
+        return tuple((k, _tkey(v) if isinstance(v, torch.Tensor) else repr(v))
+                     for k, v in sorted(t.items()))
     return (t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device)
 
 
@@ -190,14 +191,14 @@ def _prepare_router(gate: torch.Tensor, sgate: torch.Tensor | None, E: int, H: i
     """Router weight [E, H] (+ optional shared-expert gate [1, H]) -> resident form.
 
     bf16 router (the artifact dtype, src/quanta/qwen35/bake.py:147-148): one tiled bf16 matrix
-    whose row E is the shared gate, padded to a multiple of 128 rows; its logits come from the
+    whose row E is the shared gate, padded to a multiple of 256 rows; its logits come from the
     bf16 MFMA path (bf16 x bf16 products are exact in fp32). fp32 router (or fp32 gate): kept
     fp32 row-major for the fp32 VALU logits kernel, preserving xf.f32 @ gate.f32.T exactly."""
     if gate.shape != (E, H):
         raise ValueError(f"gate must be [{E}, {H}] (got {tuple(gate.shape)})")
     gated = sgate is not None
     if gate.dtype == torch.bfloat16 and (not gated or sgate.dtype == torch.bfloat16):
-        rows = int(math.ceil((E + (1 if gated else 0)) / 128.0)) * 128
+        rows = int(math.ceil((E + (1 if gated else 0)) / 256.0)) * 256
         full = torch.zeros(rows, H, dtype=torch.bfloat16, device=gate.device)
         full[:E] = gate
         if gated:
@@ -290,12 +291,17 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
 # ----------------------------------------------------------------------------------- routing
 
 
+def _dense_regime(n: int, hidden: int) -> int:
+    """Regime of the dense (router / shared expert) matmuls, as qmoe_forward picks it."""
+    return L.REGIME_LARGE if (n > 256 and hidden % 256 == 0) else L.REGIME_SMALL
+
+
 def _router_logits(xf: torch.Tensor, pr: Prepared) -> torch.Tensor:
     c = pr.cfg
     if c.router_format == L.ROUTER_F32:
         return ops.router_logits_f32(xf, pr.router_f32, pr.shared_gate_f32)
     n = xf.shape[0]
-    regime = L.REGIME_SMALL if n <= 256 else L.REGIME_LARGE
+    regime = _dense_regime(n, c.hidden)
     return ops.grouped_qmm(xf, K=c.hidden, n_rows=c.router_rows, weight_format=L.FMT_BF16,
                            codes=pr.router_tiled, sb=None, epilogue=L.EPI_F32, out_rows=n,
                            regime=regime, dense_rows=n)
@@ -329,8 +335,7 @@ def qwen35_route(xf: torch.Tensor, gate_w: torch.Tensor, cfg, *, topk_override: 
         logits = ops.router_logits_f32(xf, rw, None)
     else:
         logits = ops.grouped_qmm(xf, K=H, n_rows=rows, weight_format=L.FMT_BF16, codes=rw, sb=None,
-                                 epilogue=L.EPI_F32, out_rows=n,
-                                 regime=L.REGIME_SMALL if n <= 256 else L.REGIME_LARGE,
+                                 epilogue=L.EPI_F32, out_rows=n, regime=_dense_regime(n, H),
                                  dense_rows=n)
     scoring = L.SCORE_SOFTMAX if _cfg(cfg, "scoring_func", "softmax") == "softmax" else L.SCORE_SIGMOID
     bias = None if e_score_correction_bias is None else e_score_correction_bias.float().reshape(E).contiguous()
@@ -356,7 +361,7 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
     idx_all = torch.arange(E, dtype=torch.int32, device=xf.device).repeat(n, 1).contiguous()
     w_all = torch.zeros(n, E, dtype=torch.float32, device=xf.device)
     w_all.scatter_(1, idx.long(), w)
-    regime = L.REGIME_SMALL if n * E <= 256 * 16 else L.REGIME_LARGE
+    regime = L.REGIME_SMALL if (n * E <= 256 * 16 or c.hidden % 256) else L.REGIME_LARGE
     m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
     counts, offsets, tile_off, sorted_slot, inv = ops.permute(idx_all, E, m_tile)
     fmt = c.expert_format
@@ -369,7 +374,7 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
                         n_slots=n * E, offsets=offsets, tile_off=tile_off, n_experts=E)
     sh_out = None
     if c.shared_inter > 0:
-        sreg = L.REGIME_SMALL if n <= 256 else L.REGIME_LARGE
+        sreg = _dense_regime(n, c.hidden)
         sh_h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.shared_inter, weight_format=L.FMT_BF16,
                                codes=pr.sh_gu, sb=None, epilogue=L.EPI_SWIGLU, out_rows=n,
                                regime=sreg, dense_rows=n)

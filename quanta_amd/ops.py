@@ -171,7 +171,8 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
                 regime: int, slot_of: torch.Tensor | None = None, slot_div: int = 1,
                 n_slots: int = 0, offsets: torch.Tensor | None = None,
                 tile_off: torch.Tensor | None = None, n_experts: int = 1,
-                dense_rows: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+                dense_rows: int = 0, out: torch.Tensor | None = None,
+                ws: torch.Tensor | None = None) -> torch.Tensor:
     """Grouped matmul over expert segments (see qmoe_grouped_qmm). Returns out [out_rows, cols]
     (bf16, or fp32 for EPI_F32); cols = n_rows/2 for SwiGLU else n_rows."""
     _need(act, torch.bfloat16, "act")
@@ -193,10 +194,15 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
         _need(out, dtype, "out")
         if out.shape != (out_rows, cols):
             raise ValueError("grouped_qmm: out has the wrong shape")
-    L.check(L.load().qmoe_grouped_qmm(_p(act), act.shape[0], _p(slot_of), slot_div, n_slots,
-                                      _p(offsets), _p(tile_off), n_experts, dense_rows, K, n_rows,
-                                      weight_format, _p(codes), _p(sb), epilogue, _p(out), cols,
-                                      regime, _stream(act.device)), "qmoe_grouped_qmm")
+    lib = L.load()
+    need = int(lib.qmoe_grouped_qmm_workspace(act.shape[0], K, weight_format, regime))
+    if need and (ws is None or ws.numel() < need):
+        ws = torch.empty(need, dtype=torch.uint8, device=act.device)
+    L.check(lib.qmoe_grouped_qmm(_p(act), act.shape[0], _p(slot_of), slot_div, n_slots,
+                                 _p(offsets), _p(tile_off), n_experts, dense_rows, K, n_rows,
+                                 weight_format, _p(codes), _p(sb), epilogue, _p(out), cols,
+                                 regime, _p(ws) if need else None, ws.numel() if need else 0,
+                                 _stream(act.device)), "qmoe_grouped_qmm")
     return out
 
 

@@ -34,15 +34,26 @@ def words_np(t: torch.Tensor) -> np.ndarray:
 
 
 def metrics(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
-    d = got.astype(np.float64) - want.astype(np.float64)
-    max_abs = float(np.max(np.abs(d))) if d.size else 0.0
+    """(max-abs error scaled by max(1, max|want|), relative L2 error).
+
+    The max-abs gate is absolute for outputs up to magnitude 1 and relative to the output's
+    largest magnitude beyond that, as the reference's own bf16 gates measure it
+    (`_relmax` = max|a-b| / max|b|, parity/bf16_scale_g64_test.py:24-25): one bf16 ulp of an
+    output of magnitude 8 is already 0.031, so a purely absolute 2e-2 bound would reject
+    correctly rounded results."""
+    want = want.astype(np.float64)
+    d = got.astype(np.float64) - want
+    scale = max(1.0, float(np.max(np.abs(want)))) if want.size else 1.0
+    max_abs = float(np.max(np.abs(d))) / scale if d.size else 0.0
     rel = float(np.linalg.norm(d) / max(np.linalg.norm(want), 1e-30))
     return max_abs, rel
 
 
 def assert_close(got, want, what="", max_abs=MAX_ABS, rel_l2=REL_L2):
+    """`want` should be the oracle's unrounded (float64) result: the GPU's bf16 output then
+    carries exactly one rounding, not two."""
     ma, rl = metrics(got, want)
-    print(f"[parity] {what}: max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    print(f"[parity] {what}: max_abs(scaled)={ma:.3e} rel_l2={rl:.3e}", flush=True)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     assert ma <= max_abs and rl <= rel_l2, f"{what}: max_abs={ma:.3e} rel_l2={rl:.3e}"
 

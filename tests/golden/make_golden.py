@@ -33,9 +33,9 @@ OUT = Path(__file__).resolve().parent
 
 CASES = {
     "c0": (synth.spec("c0"), 8),
-    "c1mini": (synth.scaled_spec("c1", hidden_size=128, num_experts=16, num_experts_per_tok=4,
+    "c1mini": (synth.scaled_spec("c1", hidden_size=256, num_experts=16, num_experts_per_tok=4,
                                  moe_intermediate_size=128, shared_expert_intermediate_size=128), 16),
-    "c3mini": (synth.scaled_spec("c3", hidden_size=128, num_experts=16, num_experts_per_tok=4,
+    "c3mini": (synth.scaled_spec("c3", hidden_size=256, num_experts=16, num_experts_per_tok=4,
                                  moe_intermediate_size=128, shared_expert_intermediate_size=128,
                                  n_group=8, topk_group=4), 12),
 }
@@ -95,7 +95,7 @@ def make(name: str) -> dict:
                            topk_group=c.topk_group, scale=c.routed_scaling_factor)
     counts, offsets, order, inv = om.permute(it["idx"], c.num_experts)
     arrs.update(
-        y=oq.f32_to_bf16_bits(y.astype(np.float32)),
+        y=oq.f32_to_bf16_bits(y.astype(np.float32)), y_exact=it["y_exact"],
         idx=it["idx"], w=it["w"], margin=om.route_margin(it["choice"], c.num_experts_per_tok),
         counts=counts, offsets=offsets, order=order, inv=inv,
         h=oq.f32_to_bf16_bits(it["h"].astype(np.float32)),

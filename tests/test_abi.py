@@ -54,7 +54,7 @@ def _last_error() -> str:
                                       None), "kept groups"),
     (lambda lib: lib.qmoe_combine(None, None, None, 4, 2, 100, None, None, None, None), "H % 8"),
     (lambda lib: lib.qmoe_grouped_qmm(None, 1, None, 1, 1, None, None, 1, 1, 128, 16, 0, None, None,
-                                      0, None, 16, 1, None), "null pointer"),
+                                      0, None, 16, 1, None, 0, None), "null pointer"),
 ])
 def test_invalid_arguments_rejected(call, fragment):
     rc = call(L.load())

@@ -127,7 +127,7 @@ def test_router_bf16_mfma_logits(gpu):
     for N, E, H in ((1, 512, 4096), (40, 256, 2048), (300, 512, 4096)):
         x = oq.round_bf16(rng.standard_normal((N, H)))
         wr = oq.round_bf16(rng.standard_normal((E, H)) * 0.02)
-        rows = ((E + 1 + 127) // 128) * 128
+        rows = ((E + 1 + 255) // 256) * 256
         full = np.zeros((rows, H))
         full[:E] = wr
         tiled = ops.tile_bf16(bf16_dev(oq.f32_to_bf16_bits(full.astype(np.float32)), gpu))
@@ -197,12 +197,11 @@ def _qmm_problem(rng, N, k, E, H, rows, fmt):
 @pytest.mark.parametrize("regime", [L.REGIME_SMALL, L.REGIME_LARGE])
 @pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
 @pytest.mark.parametrize("N,k,E,H,rows", [(7, 3, 6, 256, 256), (40, 2, 5, 512, 384),
-                                          (1, 4, 8, 4096, 256), (200, 4, 4, 1024, 128)])
+                                          (1, 4, 8, 4096, 256), (200, 4, 4, 1024, 128),
+                                          (300, 3, 5, 768, 512), (129, 2, 3, 256, 768)])
 def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows):
-    if epi == L.EPI_SWIGLU and rows % (256 if regime == L.REGIME_LARGE else 32):
-        pytest.skip("SwiGLU tiles need n_rows % 256 in the large regime")
-    if regime == L.REGIME_LARGE and rows % 128:
-        pytest.skip("large regime needs n_rows % 128")
+    if regime == L.REGIME_LARGE and rows % 256:
+        pytest.skip("the large regime tiles 256 weight rows")
     rng = np.random.default_rng(N * 13 + E + H + rows + fmt)
     idx, x, w, dense = _qmm_problem(rng, N, k, E, H, rows, fmt)
     m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
@@ -223,7 +222,9 @@ def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows):
     want = oq.round_bf16(full)
     if epi == L.EPI_SWIGLU:
         want = om.swiglu(want, rows // 2)
-    assert_close(f64(out), want, f"qmm fmt={fmt} regime={regime} epi={epi} N={N} E={E} H={H}")
+    # intermediate activations reach |h| ~ 10, so the absolute bound scales with the magnitude
+    assert_close(f64(out), want, f"qmm fmt={fmt} regime={regime} epi={epi} N={N} E={E} H={H}",
+                 rel_l2=4e-3)
 
 
 def test_combine_vs_oracle(gpu):
