@@ -143,17 +143,18 @@ def main():
         inputs = []
         for x in xs[:4]:
             idx, _ = qwen35_route(x, layers[0]["gate"], cfg)
-            counts, offsets, tile_off, sorted_slot, inv = ops.permute(idx, E, m_tile)
-            inputs.append((x, offsets, tile_off, sorted_slot, int((counts > 0).sum())))
+            counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(idx, E, m_tile)
+            inputs.append((x, offsets, tile_off, sorted_slot, tile_map, int((counts > 0).sum())))
         h = torch.empty(N * k, I, dtype=torch.bfloat16, device=dev)
 
         def launch(i):
             pr = preps[i % len(preps)]
-            x, offsets, tile_off, sorted_slot, _ = inputs[i % len(inputs)]
+            x, offsets, tile_off, sorted_slot, tile_map, _ = inputs[i % len(inputs)]
             ops.grouped_qmm(x, K=H, n_rows=2 * I, weight_format=L.FMT_INT4_G64,
                             codes=pr.gu["codes"], sb=pr.gu["sb"], epilogue=L.EPI_SWIGLU,
                             out_rows=N * k, regime=regime, slot_of=sorted_slot, slot_div=k,
-                            n_slots=N * k, offsets=offsets, tile_off=tile_off, n_experts=E, out=h)
+                            n_slots=N * k, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
+                            n_experts=E, out=h)
 
         for i in range(8):
             launch(i)
@@ -166,7 +167,7 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         kms = e0.elapsed_time(e1) / reps
-        u_k = sum(t[4] for t in inputs) / len(inputs)
+        u_k = sum(t[5] for t in inputs) / len(inputs)
         per_expert = 2 * I * H * 9 // 16                   # int4 codes + bf16 scale/bias per 64
         kbytes = u_k * per_expert + N * H * 2 + N * k * I * 2
         kern = dict(name=f"qmm_small_kernel<int4,swiglu,ksplit>" if regime == L.REGIME_SMALL
@@ -189,6 +190,26 @@ def main():
                        mfma_frac=round(f2 / m2 / 1e9 / BF16_PEAK_TFLOPS, 4))
             sweep.append(rec)
             log(f"sweep {rec}")
+
+    # ------------------------------------------------------------------ measured copy peak
+    # device-to-device copy of 2 GiB (read + write bytes), the practical HBM ceiling next to
+    # the 8 TB/s vendor figure
+    copy_gbps = None
+    if args.only == "":
+        src = torch.empty(1 << 30, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        copy_gbps = round(2 * src.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e6), 1)
+        del src, dst
+        log(f"copy bandwidth {copy_gbps} GB/s")
 
     # ------------------------------------------------------------------ CPU baseline
     cpu = None
@@ -233,6 +254,7 @@ def main():
                    "batch_tokens": N, "weights": "int4-g64 affine, bf16 scale/bias",
                    "layer_copies": args.layers, "input_pool": args.pool},
         "layer_hbm_gbps": round(layer_bytes / ms / 1e6, 1),
+        "measured_copy_gbps": copy_gbps,
         "layer_hbm_frac": round(layer_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -126,11 +126,14 @@ int qmoe_router_logits_f32(const uint16_t* x, const float* wr, const float* shar
  * offsets[E+1], tile_off[E+1] (prefix of ceil(count/m_tile)), sorted_slot[N*k]
  * (sorted position -> slot t*k+s) and inv[N*k] (slot -> sorted position, -1 for ids outside
  * [0,E)). Requires distinct experts within each token (true of any top-k router).
+ * Optional tile_map (int32 x4 per m-tile, max_tiles >= ceil(N*k/m_tile) + min(E, N*k)) receives
+ * {expert, first sorted position, rows, 0} per m-tile and {-1,0,0,0} past the last one; passing
+ * it to qmoe_grouped_qmm saves each workgroup a search of tile_off.
  * Replaces order = argsort(exp), inv = argsort(order) (src/quanta/modeling/moe.py:81-85;
  * src/quanta/dsv4/moe.py:107-112). */
 int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_t* counts,
                  int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
-                 void* stream);
+                 int32_t* tile_map, int64_t max_tiles, void* stream);
 
 /* Grouped matmul over expert segments: out[p, :] = act[row(p)] . W_e^T for sorted positions
  * p of expert e (offsets/tile_off from qmoe_permute; m_tile 16 for QMOE_REGIME_SMALL, 128 for
@@ -143,7 +146,8 @@ int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_
  * src/quanta/qwen35/moe.py:59-63 fused, and mx.gather_mm (src/quanta/qwen35/moe.py:79-81). */
 int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_of, int slot_div,
                      int64_t n_slots, const int32_t* offsets, const int32_t* tile_off,
-                     int n_experts, int64_t dense_rows, int K, int n_rows, int weight_format,
+                     const int32_t* tile_map, int n_experts, int64_t dense_rows, int K,
+                     int n_rows, int weight_format,
                      const void* codes, const uint16_t* sb, int epilogue, void* out, int ld_out,
                      int regime, void* ws, size_t ws_bytes, void* stream);
 /* Workspace qmoe_grouped_qmm needs: the large-M int4 regime stages an fp16 copy of the

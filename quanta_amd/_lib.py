@@ -23,6 +23,11 @@ EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
 
 
+def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
+    """Most m-tiles a permuted list of mc slots over n_experts can produce."""
+    return (mc + m_tile - 1) // m_tile + min(mc, n_experts)
+
+
 class QmoeConfig(ctypes.Structure):
     _fields_ = [
         ("hidden", ctypes.c_int32),
@@ -71,9 +76,9 @@ SIGNATURES = {
                           ctypes.c_size_t, _P]),
     "qmoe_router_topk": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P]),
     "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
-    "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
-    "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _I, _P,
-                              _I, _I, _P, ctypes.c_size_t, _P]),
+    "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),
+    "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _I,
+                              _P, _I, _I, _P, ctypes.c_size_t, _P]),
     "qmoe_grouped_qmm_workspace": (ctypes.c_size_t, [_I64, _I, _I, _I]),
     "qmoe_combine": (_I, [_P, _P, _P, _I64, _I, _I, _P, _P, _P, _P]),
     "qmoe_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),

@@ -31,51 +31,64 @@ int check_launch(const char* what) {
   return QMOE_OK;
 }
 
-__global__ void __launch_bounds__(256) combine_kernel(
+// One 64-thread workgroup per (token, 512 features): the k slot rows are gathered through inv
+// with their loads issued together (8 at a time), then summed in slot order.
+__global__ void __launch_bounds__(64) combine_kernel(
     const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
     int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ shared_out,
     const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
   const int t = blockIdx.y;
-  const int h8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const int h8 = (blockIdx.x * 64 + threadIdx.x) * 8;
   if (h8 >= H) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < k; ++s) {
-    const int64_t m = static_cast<int64_t>(t) * k + s;
-    const int pos = inv[m];
-    if (pos < 0 || pos >= n_pos) continue;
-    const float ws = w[m];
-    const uint4 v = *reinterpret_cast<const uint4*>(d + static_cast<int64_t>(pos) * H + h8);
-    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+  const int64_t m0 = static_cast<int64_t>(t) * k;
+  for (int s0 = 0; s0 < k; s0 += 8) {
+    u32x4 v[8];
+    float ws[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[2 * j] += bf16lo_to_f32(vv[j]) * ws;
-      acc[2 * j + 1] += bf16hi_to_f32(vv[j]) * ws;
+    for (int j = 0; j < 8; ++j) {
+      ws[j] = 0.f;
+      v[j] = u32x4{0u, 0u, 0u, 0u};
+      if (s0 + j < k) {
+        const int pos = inv[m0 + s0 + j];
+        if (pos >= 0 && pos < n_pos) {
+          ws[j] = w[m0 + s0 + j];
+          v[j] = *reinterpret_cast<const u32x4*>(d + static_cast<int64_t>(pos) * H + h8);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] += bf16lo_to_f32(v[j][q]) * ws[j];
+        acc[2 * q + 1] += bf16hi_to_f32(v[j][q]) * ws[j];
+      }
     }
   }
   if (shared_out) {
     const float g = shared_gate ? shared_gate[t] : 1.0f;
-    const uint4 v = *reinterpret_cast<const uint4*>(shared_out + static_cast<int64_t>(t) * H + h8);
-    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    const u32x4 v = *reinterpret_cast<const u32x4*>(shared_out + static_cast<int64_t>(t) * H + h8);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[2 * j] += bf16lo_to_f32(vv[j]) * g;
-      acc[2 * j + 1] += bf16hi_to_f32(vv[j]) * g;
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] += bf16lo_to_f32(v[q]) * g;
+      acc[2 * q + 1] += bf16hi_to_f32(v[q]) * g;
     }
   }
-  uint4 o;
-  o.x = pack_bf16x2(acc[0], acc[1]);
-  o.y = pack_bf16x2(acc[2], acc[3]);
-  o.z = pack_bf16x2(acc[4], acc[5]);
-  o.w = pack_bf16x2(acc[6], acc[7]);
-  *reinterpret_cast<uint4*>(y + static_cast<int64_t>(t) * H + h8) = o;
+  u32x4 o;
+  o[0] = pack_bf16x2(acc[0], acc[1]);
+  o[1] = pack_bf16x2(acc[2], acc[3]);
+  o[2] = pack_bf16x2(acc[4], acc[5]);
+  o[3] = pack_bf16x2(acc[6], acc[7]);
+  *reinterpret_cast<u32x4*>(y + static_cast<int64_t>(t) * H + h8) = o;
 }
 
 int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
                    const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
                    hipStream_t stream) {
-  dim3 grid((H / 8 + 255) / 256, N);
-  combine_kernel<<<grid, 256, 0, stream>>>(d, inv, w, N, k, H, static_cast<int64_t>(N) * k,
-                                           shared_out, shared_gate, y);
+  dim3 grid((H + 511) / 512, N);
+  combine_kernel<<<grid, 64, 0, stream>>>(d, inv, w, N, k, H, static_cast<int64_t>(N) * k,
+                                          shared_out, shared_gate, y);
   return check_launch("combine");
 }
 
@@ -83,8 +96,9 @@ int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int t
 
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
-  size_t logits, idx, w, sg, counts, offsets, tile_off, sorted, inv, h, d, sh_h, sh_out, x16,
-      x_sinv, h16, h_sinv, total;
+  size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, sorted, inv, h, d, sh_h,
+      sh_out, x16, x_sinv, h16, h_sinv, total;
+  int64_t max_tiles;
 };
 
 static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
@@ -104,6 +118,9 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.counts = take(static_cast<size_t>(c.n_experts) * 4);
   L.offsets = take(static_cast<size_t>(c.n_experts + 1) * 4);
   L.tile_off = take(static_cast<size_t>(c.n_experts + 1) * 4);
+  // tile descriptors for whichever m-tile the regime uses (16 needs the most entries)
+  L.max_tiles = mtile_upper_bound(mc, c.n_experts, kSmallMTile);
+  L.tile_map = take(static_cast<size_t>(L.max_tiles) * 16);
   L.sorted = take(static_cast<size_t>(mc) * 4);
   L.inv = take(static_cast<size_t>(mc) * 4);
   L.h = take(static_cast<size_t>(mc) * c.inter * 2);
@@ -167,10 +184,10 @@ extern "C" size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight
 
 extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_of,
                                 int slot_div, int64_t n_slots, const int32_t* offsets,
-                                const int32_t* tile_off, int n_experts, int64_t dense_rows,
-                                int K, int n_rows, int weight_format, const void* codes,
-                                const uint16_t* sb, int epilogue, void* out, int ld_out,
-                                int regime, void* ws, size_t ws_bytes, void* stream) {
+                                const int32_t* tile_off, const int32_t* tile_map, int n_experts,
+                                int64_t dense_rows, int K, int n_rows, int weight_format,
+                                const void* codes, const uint16_t* sb, int epilogue, void* out,
+                                int ld_out, int regime, void* ws, size_t ws_bytes, void* stream) {
   if (!act || !codes || !out) return fail("qmoe_grouped_qmm: null pointer");
   if (weight_format == QMOE_FMT_INT4_G64 && !sb) return fail("qmoe_grouped_qmm: int4 needs sb");
   if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16)
@@ -189,6 +206,7 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
   a.n_slots = n_slots;
   a.offsets = offsets;
   a.tile_off = tile_off;
+  a.tile_map = offsets ? reinterpret_cast<const int4*>(tile_map) : nullptr;
   a.dense_rows = dense_rows;
   a.n_experts = offsets ? n_experts : 1;
   a.K = K;
@@ -262,6 +280,7 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
   int32_t* offsets = reinterpret_cast<int32_t*>(base + L.offsets);
   int32_t* tile_off = reinterpret_cast<int32_t*>(base + L.tile_off);
+  int32_t* tile_map = reinterpret_cast<int32_t*>(base + L.tile_map);
   int32_t* sorted = reinterpret_cast<int32_t*>(base + L.sorted);
   int32_t* inv = reinterpret_cast<int32_t*>(base + L.inv);
   uint16_t* h = reinterpret_cast<uint16_t*>(base + L.h);
@@ -302,16 +321,17 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
                    c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream);
   if (rc) return rc;
   // 3. stable permute by expert
-  rc = launch_permute(idx, n, c.top_k, c.n_experts, m_tile, counts, offsets, tile_off, sorted, inv,
-                      stream);
-  if (rc) return rc;
   const int64_t bound = mtile_upper_bound(mc, c.n_experts, m_tile);
+  rc = launch_permute(idx, n, c.top_k, c.n_experts, m_tile, counts, offsets, tile_off, sorted, inv,
+                      tile_map, bound, stream);
+  if (rc) return rc;
   const bool f16_acts = (regime == QMOE_REGIME_LARGE && wfmt == FMT_INT4);
   // 4. routed gate_up + SwiGLU -> h (sorted order)
   {
     QmmArgs a{};
     a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+    a.tile_map = reinterpret_cast<const int4*>(tile_map);
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
     a.out = h; a.ld_out = c.inter;
     if (f16_acts) {
@@ -338,6 +358,7 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     QmmArgs a{};
     a.act = h; a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+    a.tile_map = reinterpret_cast<const int4*>(tile_map);
     a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
     a.out = d; a.ld_out = c.hidden;
     if (f16_acts) {

@@ -48,7 +48,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* 
 __global__ void __launch_bounds__(kPermThreads) permute_kernel(
     const int32_t* __restrict__ idx, int N, int k, int E, int m_tile, int experts_per_wg,
     int words_per_expert, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ tile_off, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ inv) {
+    int32_t* __restrict__ tile_off, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ inv,
+    int4* __restrict__ tile_map, int max_tiles) {
   __shared__ int hist[1024];
   __shared__ int offs[1025];
   __shared__ int scan_tmp[40];
@@ -96,6 +97,16 @@ __global__ void __launch_bounds__(kPermThreads) permute_kernel(
       offsets[E] = total;
       tile_off[E] = scan_tmp[38];
     }
+    // Per-tile descriptors {expert, first sorted position, rows, 0} for the grouped-qmm grid,
+    // and a -1 sentinel in every unused entry up to max_tiles, so a workgroup resolves its tile
+    // with one 16-byte load.
+    if (tile_map) {
+      if (tid < E)
+        for (int i = 0; i < tiles; ++i)
+          tile_map[tex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
+      for (int t = scan_tmp[38] + tid; t < max_tiles; t += kPermThreads)
+        tile_map[t] = make_int4(-1, 0, 0, 0);
+    }
   }
 
   // Per-expert exclusive popcount prefix over the token bitmap words.
@@ -134,14 +145,18 @@ __global__ void __launch_bounds__(kPermThreads) permute_kernel(
 
 int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,
                    int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
-                   hipStream_t stream) {
+                   int32_t* tile_map, int64_t max_tiles, hipStream_t stream) {
   const int words = (N + 31) / 32;
   int per_wg = (kPermLdsWords / 2) / words;
   if (per_wg < 1) return fail("permute: N too large for the LDS token bitmap");
   if (per_wg > E) per_wg = E;
   const int n_wg = (E + per_wg - 1) / per_wg;
+  if (tile_map && max_tiles < mtile_upper_bound(static_cast<int64_t>(N) * k, E, m_tile))
+    return fail("permute: tile_map smaller than the m-tile upper bound");
   permute_kernel<<<n_wg, kPermThreads, 0, stream>>>(idx, N, k, E, m_tile, per_wg, words, counts,
-                                                    offsets, tile_off, sorted_slot, inv);
+                                                    offsets, tile_off, sorted_slot, inv,
+                                                    reinterpret_cast<int4*>(tile_map),
+                                                    static_cast<int>(max_tiles));
   return check_launch("permute");
 }
 
@@ -151,13 +166,15 @@ using namespace qmoe;
 
 extern "C" int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile,
                             int32_t* counts, int32_t* offsets, int32_t* tile_off,
-                            int32_t* sorted_slot, int32_t* inv, void* stream) {
+                            int32_t* sorted_slot, int32_t* inv, int32_t* tile_map,
+                            int64_t max_tiles, void* stream) {
   if (N <= 0 || k <= 0 || E <= 0 || E > 1024) return fail("qmoe_permute: need N,k > 0, 1 <= E <= 1024");
   if (N * k > (int64_t(1) << 30)) return fail("qmoe_permute: N*k too large");
   if (N > 196608) return fail("qmoe_permute: N above 196608 (6144 bitmap words per expert)");
   if (m_tile <= 0) return fail("qmoe_permute: m_tile must be positive");
   if (!idx || !counts || !offsets || !tile_off || !sorted_slot || !inv)
     return fail("qmoe_permute: null pointer");
+  if (max_tiles > (int64_t(1) << 30)) return fail("qmoe_permute: max_tiles too large");
   return launch_permute(idx, static_cast<int>(N), k, E, m_tile, counts, offsets, tile_off,
-                        sorted_slot, inv, static_cast<hipStream_t>(stream));
+                        sorted_slot, inv, tile_map, max_tiles, static_cast<hipStream_t>(stream));
 }

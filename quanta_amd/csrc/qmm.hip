@@ -41,7 +41,13 @@ __device__ __forceinline__ int find_segment(const int32_t* __restrict__ tile_off
 // (the grid is sized by an upper bound); uniform across the workgroup.
 __device__ __forceinline__ bool resolve_mtile(const QmmArgs& a, int mt, int m_tile, int& e,
                                               int& m0, int& m_cnt) {
-  if (a.offsets) {
+  if (a.tile_map) {
+    const int4 t = a.tile_map[mt];
+    if (t.x < 0) return false;
+    e = t.x;
+    m0 = t.y;
+    m_cnt = t.z;
+  } else if (a.offsets) {
     if (mt >= a.tile_off[a.n_experts]) return false;
     e = find_segment(a.tile_off, a.n_experts, mt);
     m0 = a.offsets[e] + (mt - a.tile_off[e]) * m_tile;
@@ -81,11 +87,24 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
 }
 
 // ============================================================================ small-M kernel
+// One wavefront = one 16-row weight tile job (two tiles, gate and up, for SwiGLU) over one
+// k-range of one 16-position m-tile. KSPLIT wavefronts of a workgroup share a job and split K;
+// their partial tiles are summed through LDS. WAVES = max(4, KSPLIT) wavefronts per workgroup.
+template <int FMT, int KSPLIT>
+struct SmallStage {
+  static constexpr int NT = 2;
+  u32x4 q[NT];    // int4: raw codes of one superblock / bf16: weight fragments of one 32-k step
+  uint2 sb[NT];   // int4 scale/bias of the superblock's two groups
+  u32x4 x[4];     // activation fragments
+};
+
 template <int FMT, int EPI, int KSPLIT>
-__global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
-  constexpr int JOBS_PER_WG = 4 / KSPLIT;
+__global__ void __launch_bounds__(KSPLIT > 4 ? 64 * KSPLIT : 256)
+qmm_small_kernel(QmmArgs a, int n_jobs) {
+  constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
+  constexpr int JOBS_PER_WG = WAVES / KSPLIT;
   constexpr int NT = (EPI == EPI_SWIGLU) ? 2 : 1;
-  __shared__ f32x4_t red[(KSPLIT > 1) ? 4 * NT * 64 : 1];
+  __shared__ f32x4_t red[(KSPLIT > 1) ? WAVES * NT * 64 : 1];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int e, m0, m_cnt;
@@ -99,7 +118,6 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
   int64_t arow = -1;
   if (mrow < m_cnt) arow = act_row(a, m0 + mrow);
   const bool row_ok = arow >= 0;
-  const uint32_t xmask = row_ok ? 0xFFFFFFFFu : 0u;   // rows past the segment read as zeros
   const uint16_t* xrow = a.act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
 
   f32x4_t acc[NT];
@@ -130,40 +148,55 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
         o[0] = o[1] = o[2] = o[3] = 0x3F803F80u;
       }
       const f32x4_t zero4{0.f, 0.f, 0.f, 0.f};
-
-      for (int p = p0; p < p1; ++p) {
-        u32x4 q[NT];
-        uint2 sbv[NT];
+      // Two register stages: the loads of superblock p+1 are in flight while p is computed.
+      SmallStage<FMT, KSPLIT> st[2];
+      auto load = [&](SmallStage<FMT, KSPLIT>& s, int p) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          q[t] = cp[t][p * 64];
-          sbv[t] = sp[t][p * 16];
+          s.q[t] = cp[t][p * 64];
+          s.sb[t] = sp[t][p * 16];
         }
-        // group 2p: k 16lg + 0..7 (step 0) and + 8..15 (step 1); group 2p+1 likewise, +64
-        u32x4 xv[4];
-        xv[0] = xp[p * 16 + 0] & xmask;
-        xv[1] = xp[p * 16 + 1] & xmask;
-        xv[2] = xp[p * 16 + 8] & xmask;
-        xv[3] = xp[p * 16 + 9] & xmask;
+        // group 2p: k 16lg + 0..7 (step 0) and + 8..15 (step 1); group 2p+1 likewise, +64.
+        // Only rows of the segment load; the rest of the 16-row tile is zeros.
+        if (row_ok) {
+          s.x[0] = xp[p * 16 + 0];
+          s.x[1] = xp[p * 16 + 1];
+          s.x[2] = xp[p * 16 + 8];
+          s.x[3] = xp[p * 16 + 9];
+        } else {
+          s.x[0] = s.x[1] = s.x[2] = s.x[3] = u32x4{0u, 0u, 0u, 0u};
+        }
+      };
+      auto compute = [&](const SmallStage<FMT, KSPLIT>& s) __attribute__((always_inline)) {
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
-          const bf16x8_t A0 = as_bf16x8(xv[2 * gg]);
-          const bf16x8_t A1 = as_bf16x8(xv[2 * gg + 1]);
+          const bf16x8_t A0 = as_bf16x8(s.x[2 * gg]);
+          const bf16x8_t A1 = as_bf16x8(s.x[2 * gg + 1]);
           f32x4_t xs = mfma16(A0, ones, zero4);
           xs = mfma16(A1, ones, xs);
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            const uint32_t w0 = gg ? q[t].z : q[t].x;
-            const uint32_t w1 = gg ? q[t].w : q[t].y;
+            const uint32_t w0 = gg ? s.q[t].z : s.q[t].x;
+            const uint32_t w1 = gg ? s.q[t].w : s.q[t].y;
             f32x4_t r = mfma16(A0, unpack_q128(w0), zero4);
             r = mfma16(A1, unpack_q128(w1), r);
-            const uint32_t sbw = gg ? sbv[t].y : sbv[t].x;
-            const float s = bf16lo_to_f32(sbw);
-            const float b = bf16hi_to_f32(sbw) - 128.0f * s;
+            const uint32_t sbw = gg ? s.sb[t].y : s.sb[t].x;
+            const float sc = bf16lo_to_f32(sbw);
+            const float bi = bf16hi_to_f32(sbw) - 128.0f * sc;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][j] = fmaf(s, r[j], fmaf(b, xs[j], acc[t][j]));
+            for (int j = 0; j < 4; ++j) acc[t][j] = fmaf(sc, r[j], fmaf(bi, xs[j], acc[t][j]));
           }
         }
+      };
+      int p = p0;
+      if (p < p1) load(st[0], p);
+      while (p < p1) {
+        if (p + 1 < p1) load(st[1], p + 1);
+        compute(st[0]);
+        if (++p >= p1) break;
+        if (p + 1 < p1) load(st[0], p + 1);
+        compute(st[1]);
+        ++p;
       }
     } else {  // FMT_BF16
       const int nks = a.K / 32;
@@ -180,7 +213,9 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
         u32x4 wv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) wv[t] = wp[t][c * 64];
-        const bf16x8_t A = as_bf16x8(xp[c * 4] & xmask);
+        u32x4 xv = u32x4{0u, 0u, 0u, 0u};
+        if (row_ok) xv = xp[c * 4];
+        const bf16x8_t A = as_bf16x8(xv);
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = mfma16(A, as_bf16x8(wv[t]), acc[t]);
       }
@@ -191,7 +226,7 @@ __global__ void __launch_bounds__(256) qmm_small_kernel(QmmArgs a, int n_jobs) {
     const int jl = wave / KSPLIT;
     if (kpart > 0) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) red[((wave) * NT + t) * 64 + lane] = acc[t];
+      for (int t = 0; t < NT; ++t) red[(wave * NT + t) * 64 + lane] = acc[t];
     }
     __syncthreads();
     if (kpart == 0) {
@@ -465,14 +500,24 @@ int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16,
 
 
 // ============================================================================ launcher
+template <int FMT, int EPI, int KSPLIT>
+static void launch_small_k(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
+  constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
+  const int n_jobs = (EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
+  const int jobs_per_wg = WAVES / KSPLIT;
+  dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mtiles));
+  qmm_small_kernel<FMT, EPI, KSPLIT><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
+}
+
 template <int FMT, int EPI>
 static void launch_small(const QmmArgs& a, int ksplit, int64_t mtiles, hipStream_t stream) {
-  const int n_jobs = (EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
-  const int jobs_per_wg = 4 / ksplit;
-  dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mtiles));
-  if (ksplit == 4) qmm_small_kernel<FMT, EPI, 4><<<grid, 256, 0, stream>>>(a, n_jobs);
-  else if (ksplit == 2) qmm_small_kernel<FMT, EPI, 2><<<grid, 256, 0, stream>>>(a, n_jobs);
-  else qmm_small_kernel<FMT, EPI, 1><<<grid, 256, 0, stream>>>(a, n_jobs);
+  switch (ksplit) {
+    case 16: launch_small_k<FMT, EPI, 16>(a, mtiles, stream); break;
+    case 8: launch_small_k<FMT, EPI, 8>(a, mtiles, stream); break;
+    case 4: launch_small_k<FMT, EPI, 4>(a, mtiles, stream); break;
+    case 2: launch_small_k<FMT, EPI, 2>(a, mtiles, stream); break;
+    default: launch_small_k<FMT, EPI, 1>(a, mtiles, stream); break;
+  }
 }
 
 template <int FMT, int EPI>
@@ -496,9 +541,17 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     if (fmt == FMT_INT4 && a.K % 128) return fail("qmm: int4 needs K % 128 == 0");
     if (fmt == FMT_BF16 && a.K % 32) return fail("qmm: bf16 needs K % 32 == 0");
     if (a.n_rows % (epi == EPI_SWIGLU ? 32 : 16)) return fail("qmm: weight rows not a tile multiple");
-    // Split-K depends on K only (never on the token count), so a row's summation order, and
-    // therefore its result, is the same at every batch size (batch invariance).
-    const int ksplit = (a.K >= 4096) ? 4 : (a.K >= 2048) ? 2 : 1;
+    // Split-K depends on the shape only (never on the token count), so a row's summation
+    // order, and therefore its result, is the same at every batch size (batch invariance).
+    // int4 wavefronts keep >= 8 superblocks each; bf16 (router, shared expert) wavefronts
+    // keep ~8 32-deep steps, which spreads the few dense row tiles over enough wavefronts.
+    int ksplit;
+    if (fmt == FMT_INT4) {
+      ksplit = (a.K >= 4096) ? 4 : (a.K >= 2048) ? 2 : 1;
+    } else {
+      const int nks = a.K / 32;
+      ksplit = (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
+    }
 #define QMOE_SMALL(F, P) launch_small<F, P>(a, ksplit, mtile_bound, stream)
     if (fmt == FMT_INT4) {
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT4, EPI_SWIGLU);

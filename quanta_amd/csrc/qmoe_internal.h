@@ -147,7 +147,7 @@ int launch_topk(const float* logits, int ld_logits, const float* bias, int N, in
                 hipStream_t stream);
 int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,
                    int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
-                   hipStream_t stream);
+                   int32_t* tile_map, int64_t max_tiles, hipStream_t stream);
 
 struct QmmArgs {
   const uint16_t* act;        // activation rows (bf16), row stride K
@@ -157,6 +157,7 @@ struct QmmArgs {
   int64_t n_slots;            // total sorted positions (bounds check on slot ids)
   const int32_t* offsets;     // [E+1] segment offsets (nullable: dense, one segment of M rows)
   const int32_t* tile_off;    // [E+1] m-tile prefix per segment (nullable in dense mode)
+  const int4* tile_map;       // per m-tile {expert, m0, rows} from permute (nullable: search)
   int64_t dense_rows;         // M for dense mode
   int n_experts;              // E (1 in dense mode)
   int K;                      // reduction length

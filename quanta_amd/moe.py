@@ -363,15 +363,17 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
     w_all.scatter_(1, idx.long(), w)
     regime = L.REGIME_SMALL if (n * E <= 256 * 16 or c.hidden % 256) else L.REGIME_LARGE
     m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
-    counts, offsets, tile_off, sorted_slot, inv = ops.permute(idx_all, E, m_tile)
+    counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(idx_all, E, m_tile)
     fmt = c.expert_format
     h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.inter, weight_format=fmt,
                         codes=pr.gu["codes"], sb=pr.gu["sb"], epilogue=L.EPI_SWIGLU,
                         out_rows=n * E, regime=regime, slot_of=sorted_slot, slot_div=E,
-                        n_slots=n * E, offsets=offsets, tile_off=tile_off, n_experts=E)
+                        n_slots=n * E, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
+                        n_experts=E)
     d = ops.grouped_qmm(h, K=c.inter, n_rows=c.hidden, weight_format=fmt, codes=pr.dn["codes"],
                         sb=pr.dn["sb"], epilogue=L.EPI_BF16, out_rows=n * E, regime=regime,
-                        n_slots=n * E, offsets=offsets, tile_off=tile_off, n_experts=E)
+                        n_slots=n * E, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
+                        n_experts=E)
     sh_out = None
     if c.shared_inter > 0:
         sreg = _dense_regime(n, c.hidden)

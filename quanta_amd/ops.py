@@ -151,7 +151,8 @@ def router_topk(logits: torch.Tensor, n_experts: int, k: int, *, scoring: int = 
 
 
 def permute(idx: torch.Tensor, n_experts: int, m_tile: int = L.SMALL_M_TILE):
-    """Stable permute of idx [N, k] by expert -> (counts, offsets, tile_off, sorted_slot, inv)."""
+    """Stable permute of idx [N, k] by expert -> (counts, offsets, tile_off, sorted_slot, inv,
+    tile_map)."""
     _need(idx, torch.int32, "idx")
     N, k = idx.shape
     dev = idx.device
@@ -160,17 +161,20 @@ def permute(idx: torch.Tensor, n_experts: int, m_tile: int = L.SMALL_M_TILE):
     tile_off = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
     sorted_slot = torch.empty(N * k, dtype=torch.int32, device=dev)
     inv = torch.empty(N * k, dtype=torch.int32, device=dev)
+    max_tiles = L.mtile_upper_bound(N * k, n_experts, m_tile)
+    tile_map = torch.empty(max_tiles, 4, dtype=torch.int32, device=dev)
     L.check(L.load().qmoe_permute(_p(idx), N, k, n_experts, m_tile, _p(counts), _p(offsets),
-                                  _p(tile_off), _p(sorted_slot), _p(inv), _stream(dev)),
-            "qmoe_permute")
-    return counts, offsets, tile_off, sorted_slot, inv
+                                  _p(tile_off), _p(sorted_slot), _p(inv), _p(tile_map), max_tiles,
+                                  _stream(dev)), "qmoe_permute")
+    return counts, offsets, tile_off, sorted_slot, inv, tile_map
 
 
 def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
                 codes: torch.Tensor, sb: torch.Tensor | None, epilogue: int, out_rows: int,
                 regime: int, slot_of: torch.Tensor | None = None, slot_div: int = 1,
                 n_slots: int = 0, offsets: torch.Tensor | None = None,
-                tile_off: torch.Tensor | None = None, n_experts: int = 1,
+                tile_off: torch.Tensor | None = None, tile_map: torch.Tensor | None = None,
+                n_experts: int = 1,
                 dense_rows: int = 0, out: torch.Tensor | None = None,
                 ws: torch.Tensor | None = None) -> torch.Tensor:
     """Grouped matmul over expert segments (see qmoe_grouped_qmm). Returns out [out_rows, cols]
@@ -183,7 +187,8 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
         _need(sb, torch.bfloat16, "sb")
     else:
         _need(codes, torch.bfloat16, "codes")
-    for t, nm in ((slot_of, "slot_of"), (offsets, "offsets"), (tile_off, "tile_off")):
+    for t, nm in ((slot_of, "slot_of"), (offsets, "offsets"), (tile_off, "tile_off"),
+                  (tile_map, "tile_map")):
         if t is not None:
             _need(t, torch.int32, nm)
     cols = n_rows // 2 if epilogue == L.EPI_SWIGLU else n_rows
@@ -198,8 +203,13 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     need = int(lib.qmoe_grouped_qmm_workspace(act.shape[0], K, weight_format, regime))
     if need and (ws is None or ws.numel() < need):
         ws = torch.empty(need, dtype=torch.uint8, device=act.device)
+    if tile_map is not None and offsets is not None:
+        m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
+        if tile_map.shape[0] < L.mtile_upper_bound(n_slots, n_experts, m_tile):
+            raise ValueError("grouped_qmm: tile_map was built for a different m-tile")
     L.check(lib.qmoe_grouped_qmm(_p(act), act.shape[0], _p(slot_of), slot_div, n_slots,
-                                 _p(offsets), _p(tile_off), n_experts, dense_rows, K, n_rows,
+                                 _p(offsets), _p(tile_off), _p(tile_map), n_experts, dense_rows,
+                                 K, n_rows,
                                  weight_format, _p(codes), _p(sb), epilogue, _p(out), cols,
                                  regime, _p(ws) if need else None, ws.numel() if need else 0,
                                  _stream(act.device)), "qmoe_grouped_qmm")

@@ -44,8 +44,10 @@ def _last_error() -> str:
     (lambda lib: lib.qmoe_dequant(None, None, None, 4, 100, 4, 64, None, None), "in_features"),
     (lambda lib: lib.qmoe_tile_int4(None, None, None, 1, 15, 128, 64, None, None, None), "rows % 16"),
     (lambda lib: lib.qmoe_tile_bf16(None, 1, 16, 33, None, None), "in_features % 32"),
-    (lambda lib: lib.qmoe_permute(None, 0, 2, 16, 16, None, None, None, None, None, None), "N,k"),
-    (lambda lib: lib.qmoe_permute(None, 4, 2, 2000, 16, None, None, None, None, None, None), "E <= 1024"),
+    (lambda lib: lib.qmoe_permute(None, 0, 2, 16, 16, None, None, None, None, None, None, 0, None),
+     "N,k"),
+    (lambda lib: lib.qmoe_permute(None, 4, 2, 2000, 16, None, None, None, None, None, None, 0, None),
+     "E <= 1024"),
     (lambda lib: lib.qmoe_router_topk(None, 16, None, 4, 16, 17, 0, 1, 1, 1, 1.0, 0, None, None, None,
                                       None), "k <= min"),
     (lambda lib: lib.qmoe_router_topk(None, 16, None, 4, 16, 2, 0, 3, 1, 1, 1.0, 0, None, None, None,
@@ -53,8 +55,8 @@ def _last_error() -> str:
     (lambda lib: lib.qmoe_router_topk(None, 16, None, 4, 16, 8, 1, 8, 2, 1, 1.0, 0, None, None, None,
                                       None), "kept groups"),
     (lambda lib: lib.qmoe_combine(None, None, None, 4, 2, 100, None, None, None, None), "H % 8"),
-    (lambda lib: lib.qmoe_grouped_qmm(None, 1, None, 1, 1, None, None, 1, 1, 128, 16, 0, None, None,
-                                      0, None, 16, 1, None, 0, None), "null pointer"),
+    (lambda lib: lib.qmoe_grouped_qmm(None, 1, None, 1, 1, None, None, None, 1, 1, 128, 16, 0, None,
+                                      None, 0, None, 16, 1, None, 0, None), "null pointer"),
 ])
 def test_invalid_arguments_rejected(call, fragment):
     rc = call(L.load())

@@ -159,7 +159,8 @@ def test_permute_bit_exact(gpu, N, k, E, m_tile):
     else:
         idx = np.stack([rng.permutation(E)[:k] for _ in range(N)])
     idx = idx.astype(np.int32)
-    counts, offsets, tile_off, sorted_slot, inv = ops.permute(torch.from_numpy(idx).to(gpu), E, m_tile)
+    counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(
+        torch.from_numpy(idx).to(gpu), E, m_tile)
     c_o, off_o, order_o, inv_o = om.permute(idx, E)
     assert np.array_equal(counts.cpu().numpy(), c_o)
     assert np.array_equal(offsets.cpu().numpy(), off_o)
@@ -167,11 +168,16 @@ def test_permute_bit_exact(gpu, N, k, E, m_tile):
     assert np.array_equal(inv.cpu().numpy(), inv_o)
     tiles = (c_o + m_tile - 1) // m_tile
     assert np.array_equal(tile_off.cpu().numpy(), np.concatenate([[0], np.cumsum(tiles)]))
+    want = [[e, off_o[e] + i * m_tile, min(m_tile, c_o[e] - i * m_tile), 0]
+            for e in range(E) for i in range(tiles[e])]
+    tm = tile_map.cpu().numpy()
+    assert np.array_equal(tm[:len(want)], np.array(want, dtype=np.int32).reshape(-1, 4))
+    assert np.all(tm[len(want):, 0] == -1)
 
 
 def test_permute_ignores_out_of_range_ids(gpu):
     idx = np.array([[0, 3], [5, 1], [-1, 2]], np.int32)   # 5 and -1 are outside [0, 4)
-    counts, offsets, _, sorted_slot, inv = ops.permute(torch.from_numpy(idx).to(gpu), 4, 16)
+    counts, offsets, _, sorted_slot, inv, _ = ops.permute(torch.from_numpy(idx).to(gpu), 4, 16)
     assert counts.cpu().tolist() == [1, 1, 1, 1]
     assert offsets.cpu().tolist() == [0, 1, 2, 3, 4]
     inv = inv.cpu().numpy()
@@ -196,16 +202,17 @@ def _qmm_problem(rng, N, k, E, H, rows, fmt):
 @pytest.mark.parametrize("fmt", [L.FMT_INT4_G64, L.FMT_BF16])
 @pytest.mark.parametrize("regime", [L.REGIME_SMALL, L.REGIME_LARGE])
 @pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
-@pytest.mark.parametrize("N,k,E,H,rows", [(7, 3, 6, 256, 256), (40, 2, 5, 512, 384),
-                                          (1, 4, 8, 4096, 256), (200, 4, 4, 1024, 128),
-                                          (300, 3, 5, 768, 512), (129, 2, 3, 256, 768)])
-def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows):
+@pytest.mark.parametrize("N,k,E,H,rows,use_map", [(7, 3, 6, 256, 256, True), (40, 2, 5, 512, 384, False),
+                                                  (1, 4, 8, 4096, 256, True), (200, 4, 4, 1024, 128, True),
+                                                  (300, 3, 5, 768, 512, True), (129, 2, 3, 256, 768, False)])
+def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows, use_map):
     if regime == L.REGIME_LARGE and rows % 256:
         pytest.skip("the large regime tiles 256 weight rows")
     rng = np.random.default_rng(N * 13 + E + H + rows + fmt)
     idx, x, w, dense = _qmm_problem(rng, N, k, E, H, rows, fmt)
     m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
-    counts, offsets, tile_off, sorted_slot, inv = ops.permute(torch.from_numpy(idx).to(gpu), E, m_tile)
+    counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(
+        torch.from_numpy(idx).to(gpu), E, m_tile)
     if fmt == L.FMT_INT4_G64:
         codes, sb = ops.tile_int4(words_dev(w[0], gpu), bf16_dev(w[1], gpu), bf16_dev(w[2], gpu))
     else:
@@ -214,7 +221,7 @@ def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows):
     out = ops.grouped_qmm(xd, K=H, n_rows=rows, weight_format=fmt, codes=codes, sb=sb,
                           epilogue=epi, out_rows=N * k, regime=regime, slot_of=sorted_slot,
                           slot_div=k, n_slots=N * k, offsets=offsets, tile_off=tile_off,
-                          n_experts=E)
+                          tile_map=tile_map if use_map else None, n_experts=E)
     order = sorted_slot.cpu().numpy()
     exp_sorted = idx.reshape(-1)[order]
     tok_sorted = order // k
