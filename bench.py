@@ -193,9 +193,10 @@ def main():
 
     # ------------------------------------------------------------------ measured copy peak
     # device-to-device copy of 2 GiB (read + write bytes), the practical HBM ceiling next to
-    # the 8 TB/s vendor figure
+    # the 8 TB/s vendor figure; in the `--only kernel` profiling mode it is also the copy of
+    # known size that FETCH_SIZE / WRITE_SIZE counter passes are calibrated against
     copy_gbps = None
-    if args.only == "":
+    if args.only in ("", "kernel"):
         src = torch.empty(1 << 30, dtype=torch.int16, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
