@@ -38,7 +38,11 @@ def parse():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--layers", type=int, default=8, help="layer copies rotated for cold HBM")
     ap.add_argument("--pool", type=int, default=16, help="distinct input batches rotated")
-    ap.add_argument("--sweep", default="1,8,128,4096", help="extra batch sizes ('' = none)")
+    ap.add_argument("--sweep", default="1,8,128", help="extra decode batch sizes ('' = none)")
+    ap.add_argument("--prefill", type=int, default=4096,
+                    help="tokens of the c4 Zipf prefill line (0 = none)")
+    ap.add_argument("--zipf", action="store_true",
+                    help="headline workload with c4's Zipf(1.1) routing (profiling the prefill)")
     ap.add_argument("--kernel-reps", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
@@ -96,9 +100,15 @@ def main():
     torch.cuda.synchronize()
     log(f"{args.layers} resident layer copies ready ({time.time() - t0:.1f}s)")
 
-    def run_batch(N, steps, warmup, pool, regime=L.REGIME_AUTO):
-        xs = [synth.make_inputs(args.config, N, device=dev, seed=100 + i) for i in range(pool)]
-        preps = [prepare(p, cfg, regime=regime) for p in layers]
+    def run_batch(N, steps, warmup, pool, regime=L.REGIME_AUTO, zipf=False):
+        # zipf: the c4 workload (the same shape, Zipf(1.1) expert popularity through router
+        # column 0 and x[:, 0] = 1.0), on the resident experts of the headline config
+        src = "c4" if zipf else args.config
+        xs = [synth.make_inputs(src, N, device=dev, seed=100 + i) for i in range(pool)]
+        lays = layers
+        if zipf:
+            lays = [dict(p, gate=synth.zipf_router(p["gate"])) for p in layers]
+        preps = [prepare(p, cfg, regime=regime) for p in lays]
         ws = torch.empty(ops.forward_workspace(preps[0].cfg, N), dtype=torch.uint8, device=dev)
         out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
 
@@ -119,7 +129,7 @@ def main():
         # distinct experts per batch (U) for the algorithmic byte count
         us = []
         for x in xs:
-            idx, _ = qwen35_route(x, layers[0]["gate"], cfg)
+            idx, _ = qwen35_route(x, lays[0]["gate"], cfg)
             us.append(int(torch.unique(idx).numel()))
         return ms, us, xs, preps
 
@@ -129,7 +139,7 @@ def main():
         steps_layer = 1
     else:
         steps_layer = args.steps
-    ms, us, xs, preps = run_batch(N, steps_layer, args.warmup, args.pool)
+    ms, us, xs, preps = run_batch(N, steps_layer, args.warmup, args.pool, zipf=args.zipf)
     U = sum(us) / len(us)
     layer_bytes = synth.algorithmic_bytes(cfg, U, N)
     log(f"N={N}: {ms * 1e3:.1f} us/step, U={U:.1f}, layer {layer_bytes / ms / 1e6:.0f} GB/s")
@@ -141,8 +151,9 @@ def main():
         regime = L.REGIME_SMALL if N <= 256 else L.REGIME_LARGE
         m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
         inputs = []
+        gate0 = synth.zipf_router(layers[0]["gate"]) if args.zipf else layers[0]["gate"]
         for x in xs[:4]:
-            idx, _ = qwen35_route(x, layers[0]["gate"], cfg)
+            idx, _ = qwen35_route(x, gate0, cfg)
             counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(idx, E, m_tile)
             inputs.append((x, offsets, tile_off, sorted_slot, tile_map, int((counts > 0).sum())))
         h = torch.empty(N * k, I, dtype=torch.bfloat16, device=dev)
@@ -171,19 +182,26 @@ def main():
         per_expert = 2 * I * H * 9 // 16                   # int4 codes + bf16 scale/bias per 64
         kbytes = u_k * per_expert + N * H * 2 + N * k * I * 2
         kern = dict(name=f"qmm_small_kernel<int4,swiglu,ksplit>" if regime == L.REGIME_SMALL
-                    else "qmm_large_kernel<int4,swiglu>", us=kms * 1e3, bytes=kbytes, U=u_k)
+                    else "act_to_f16 + qmm_large_kernel<int4,swiglu>", us=kms * 1e3, bytes=kbytes,
+                    U=u_k, mfma=regime == L.REGIME_LARGE, flops=2 * N * k * 2 * I * H)
         log(f"gate_up kernel: {kms * 1e3:.1f} us, {kbytes / kms / 1e6:.0f} GB/s")
 
     # ------------------------------------------------------------------ sweep
     sweep = []
-    if args.only == "" and args.sweep:
-        for n2 in [int(v) for v in args.sweep.split(",") if v]:
+    runs = []
+    if args.only == "":
+        runs = [(int(v), False) for v in args.sweep.split(",") if v]
+        if args.prefill > 0:
+            runs.append((args.prefill, True))
+    if runs:
+        for n2, zipf in runs:
             st = max(10, args.steps // 4) if n2 <= 256 else max(5, args.steps // 20)
-            m2, u2, _, _ = run_batch(n2, st, 3, min(args.pool, 8))
+            m2, u2, _, _ = run_batch(n2, st, 3, min(args.pool, 8), zipf=zipf)
             U2 = sum(u2) / len(u2)
             b2 = synth.algorithmic_bytes(cfg, U2, n2)
             f2 = synth.algorithmic_flops(cfg, n2)
-            rec = dict(N=n2, ms_per_step=round(m2, 5), tokens_per_s=round(n2 / (m2 / 1e3), 1),
+            rec = dict(workload=f"c4-prefill-N{n2}-zipf" if zipf else f"{args.config}-N{n2}",
+                       N=n2, ms_per_step=round(m2, 5), tokens_per_s=round(n2 / (m2 / 1e3), 1),
                        distinct_experts=round(U2, 1), hbm_gbps=round(b2 / m2 / 1e6, 1),
                        hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4),
                        tflops=round(f2 / m2 / 1e9, 2),
@@ -232,11 +250,19 @@ def main():
 
     roofline = None
     if kern is not None:
-        achieved = kern["bytes"] / (kern["us"] * 1e-6) / 1e9
-        roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
-                        frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
-                        kernel=kern["name"], kernel_us=round(kern["us"], 2),
-                        bytes_per_launch=int(kern["bytes"]), distinct_experts=round(kern["U"], 1))
+        if kern["mfma"]:
+            # prefill: FLOPs of the routed gate_up per launch (2 * N*k * 2I * H) per second
+            achieved = kern["flops"] / (kern["us"] * 1e-6) / 1e12
+            roofline = dict(bound="mfma", achieved=round(achieved, 1), peak=BF16_PEAK_TFLOPS,
+                            unit="TFLOP/s", frac=round(achieved / BF16_PEAK_TFLOPS, 4),
+                            traffic=None, kernel=kern["name"], kernel_us=round(kern["us"], 2),
+                            flops_per_launch=int(kern["flops"]), distinct_experts=round(kern["U"], 1))
+        else:
+            achieved = kern["bytes"] / (kern["us"] * 1e-6) / 1e9
+            roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                            frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
+                            kernel=kern["name"], kernel_us=round(kern["us"], 2),
+                            bytes_per_launch=int(kern["bytes"]), distinct_experts=round(kern["U"], 1))
     line = {
         "metric": METRIC,
         "value": round(N / (ms / 1e3), 1),
@@ -250,7 +276,8 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}-decode-N{N}" if N <= 256 else f"{args.config}-prefill-N{N}",
+        "config": {"workload": ("c4-prefill-zipf" if args.zipf else
+                                f"{args.config}-decode" if N <= 256 else f"{args.config}-prefill") + f"-N{N}",
                    "hidden": H, "experts": E, "top_k": k, "inter": I, "shared_inter": Is,
                    "batch_tokens": N, "weights": "int4-g64 affine, bf16 scale/bias",
                    "layer_copies": args.layers, "input_pool": args.pool},

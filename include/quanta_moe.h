@@ -50,7 +50,7 @@ extern "C" {
 /* grouped-qmm regimes */
 #define QMOE_REGIME_AUTO 0
 #define QMOE_REGIME_SMALL 1 /* 16-token m-tiles, weights streamed to registers (decode) */
-#define QMOE_REGIME_LARGE 2 /* 128x256 tiles, fp16-dequantised LDS tiles, 32x32 MFMA (prefill) */
+#define QMOE_REGIME_LARGE 2 /* 128x256 tiles, register-dequantised fp16 weights (prefill) */
 
 /* grouped-qmm epilogues */
 #define QMOE_EPI_SWIGLU 0 /* out[:, j] = bf16(silu(bf16(gate_j)) * bf16(up_j)), rows = [gate; up] */

@@ -8,6 +8,8 @@
 // output is deterministic.
 #include <string>
 
+#include <algorithm>
+
 #include "qmoe_internal.h"
 #include "../../include/quanta_moe.h"
 
@@ -96,9 +98,9 @@ int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int t
 
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
-  size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, sorted, inv, h, d, sh_h,
-      sh_out, x16, x_sinv, h16, h_sinv, total;
-  int64_t max_tiles;
+  size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, tile_map_big, sorted, inv, h,
+      d, sh_h, sh_out, x16, x_sinv, h16, h_sinv, total;
+  int64_t max_tiles, max_tiles_big;
 };
 
 static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
@@ -121,6 +123,9 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   // tile descriptors for whichever m-tile the regime uses (16 needs the most entries)
   L.max_tiles = mtile_upper_bound(mc, c.n_experts, kSmallMTile);
   L.tile_map = take(static_cast<size_t>(L.max_tiles) * 16);
+  // large-M regime: 128-row tiles of the experts above the hybrid split
+  L.max_tiles_big = mtile_upper_bound(mc, c.n_experts, kLargeMTile);
+  L.tile_map_big = take(static_cast<size_t>(L.max_tiles_big) * 16);
   L.sorted = take(static_cast<size_t>(mc) * 4);
   L.inv = take(static_cast<size_t>(mc) * 4);
   L.h = take(static_cast<size_t>(mc) * c.inter * 2);
@@ -295,7 +300,18 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   const int n = static_cast<int>(N);
   const int64_t mc = N * c.top_k;
   const int regime = pick_regime(c, N);
-  const int m_tile = (regime == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
+  // Large-M regime = hybrid: experts with more than kHybridSplitRows rows run on the large
+  // kernel (128-row tiles), the rest on the small kernel (16-row tiles). A handful of rows
+  // cannot amortise a 128-row tile's weight dequant; under skewed routing most experts are
+  // that small while a few carry thousands of rows.
+  const bool hybrid = (regime == QMOE_REGIME_LARGE);
+  int32_t* tile_map_big = reinterpret_cast<int32_t*>(base + L.tile_map_big);
+  const int64_t bound_small = mtile_upper_bound(mc, c.n_experts, kSmallMTile);
+  const int64_t cold_bound =
+      std::min<int64_t>(bound_small, static_cast<int64_t>(c.n_experts) *
+                                         ((kHybridSplitRows + kSmallMTile - 1) / kSmallMTile));
+  const int64_t hot_bound = (mc + kLargeMTile - 1) / kLargeMTile +
+                            std::min<int64_t>(c.n_experts, mc / (kHybridSplitRows + 1));
   const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4 : FMT_BF16;
   const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
 
@@ -320,26 +336,35 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
                    c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream);
   if (rc) return rc;
-  // 3. stable permute by expert
-  const int64_t bound = mtile_upper_bound(mc, c.n_experts, m_tile);
-  rc = launch_permute(idx, n, c.top_k, c.n_experts, m_tile, counts, offsets, tile_off, sorted, inv,
-                      tile_map, bound, stream);
+  // 3. stable permute by expert (16-row tiles; hybrid: hot experts' 128-row tiles separately)
+  rc = launch_permute(idx, n, c.top_k, c.n_experts, kSmallMTile, counts, offsets, tile_off, sorted,
+                      inv, tile_map, bound_small, stream, kHybridSplitRows, kLargeMTile,
+                      hybrid ? tile_map_big : nullptr, L.max_tiles_big);
   if (rc) return rc;
-  const bool f16_acts = (regime == QMOE_REGIME_LARGE && wfmt == FMT_INT4);
+  const bool f16_acts = (hybrid && wfmt == FMT_INT4);
+  // routed grouped matmul over the permuted rows: small kernel over the (cold) 16-row tiles,
+  // large kernel over the hot experts' tiles
+  auto routed = [&](QmmArgs a, int epi, const uint16_t* act16, const float* sinv) {
+    a.tile_map = reinterpret_cast<const int4*>(tile_map);
+    int r = launch_qmm(a, wfmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : bound_small, stream);
+    if (r || !hybrid) return r;
+    a.tile_map = reinterpret_cast<const int4*>(tile_map_big);
+    a.act16 = act16;
+    a.row_sinv = sinv;
+    return launch_qmm(a, wfmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
+  };
   // 4. routed gate_up + SwiGLU -> h (sorted order)
   {
     QmmArgs a{};
     a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
-    a.tile_map = reinterpret_cast<const int4*>(tile_map);
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
     a.out = h; a.ld_out = c.inter;
     if (f16_acts) {
       rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, stream);
       if (rc) return rc;
-      a.act16 = x16; a.row_sinv = x_sinv;
     }
-    rc = launch_qmm(a, wfmt, EPI_SWIGLU, regime, bound, stream);
+    rc = routed(a, EPI_SWIGLU, x16, x_sinv);
     if (rc) return rc;
   }
   // 5. shared expert gate_up + SwiGLU
@@ -358,15 +383,13 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     QmmArgs a{};
     a.act = h; a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
-    a.tile_map = reinterpret_cast<const int4*>(tile_map);
     a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
     a.out = d; a.ld_out = c.hidden;
     if (f16_acts) {
       rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);
       if (rc) return rc;
-      a.act16 = h16; a.row_sinv = h_sinv;
     }
-    rc = launch_qmm(a, wfmt, EPI_BF16, regime, bound, stream);
+    rc = routed(a, EPI_BF16, h16, h_sinv);
     if (rc) return rc;
   }
   // 7. shared expert down

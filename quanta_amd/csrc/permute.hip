@@ -45,11 +45,14 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* 
   return warp_sums[16 + wid] + incl - v;
 }
 
+// Optional split tile maps (hybrid regime): experts with more than `split_rows` rows get
+// m-tiles of `m_tile_big` rows in tile_map_big; the others keep m_tile-row tiles in tile_map.
 __global__ void __launch_bounds__(kPermThreads) permute_kernel(
     const int32_t* __restrict__ idx, int N, int k, int E, int m_tile, int experts_per_wg,
     int words_per_expert, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ inv,
-    int4* __restrict__ tile_map, int max_tiles) {
+    int4* __restrict__ tile_map, int max_tiles, int split_rows, int m_tile_big,
+    int4* __restrict__ tile_map_big, int max_tiles_big) {
   __shared__ int hist[1024];
   __shared__ int offs[1025];
   __shared__ int scan_tmp[40];
@@ -87,6 +90,18 @@ __global__ void __launch_bounds__(kPermThreads) permute_kernel(
   __syncthreads();
   const int tiles = (c + m_tile - 1) / m_tile;
   const int tex = block_exclusive_scan(tiles, scan_tmp, &scan_tmp[38]);
+  // hybrid split: small-tile map over the experts at or below split_rows, big-tile map over
+  // the rest (block-uniform condition: tile_map_big is a kernel argument)
+  int s_tiles = tiles, s_ex = tex, s_total = 0, b_tiles = 0, b_ex = 0, b_total = 0;
+  if (tile_map_big) {
+    const bool big = c > split_rows;
+    s_tiles = big ? 0 : tiles;
+    b_tiles = big ? (c + m_tile_big - 1) / m_tile_big : 0;
+    s_ex = block_exclusive_scan(s_tiles, scan_tmp, &scan_tmp[37]);
+    s_total = scan_tmp[37];
+    b_ex = block_exclusive_scan(b_tiles, scan_tmp, &scan_tmp[36]);
+    b_total = scan_tmp[36];
+  }
   if (blockIdx.x == 0) {
     if (tid < E) {
       counts[tid] = c;
@@ -100,12 +115,24 @@ __global__ void __launch_bounds__(kPermThreads) permute_kernel(
     // Per-tile descriptors {expert, first sorted position, rows, 0} for the grouped-qmm grid,
     // and a -1 sentinel in every unused entry up to max_tiles, so a workgroup resolves its tile
     // with one 16-byte load.
-    if (tile_map) {
+    if (tile_map && !tile_map_big) {
       if (tid < E)
         for (int i = 0; i < tiles; ++i)
           tile_map[tex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
       for (int t = scan_tmp[38] + tid; t < max_tiles; t += kPermThreads)
         tile_map[t] = make_int4(-1, 0, 0, 0);
+    }
+    if (tile_map_big) {
+      if (tid < E) {
+        for (int i = 0; i < s_tiles; ++i)
+          tile_map[s_ex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
+        for (int i = 0; i < b_tiles; ++i)
+          tile_map_big[b_ex + i] =
+              make_int4(tid, ex + i * m_tile_big, min(m_tile_big, c - i * m_tile_big), 0);
+      }
+      for (int t = s_total + tid; t < max_tiles; t += kPermThreads) tile_map[t] = make_int4(-1, 0, 0, 0);
+      for (int t = b_total + tid; t < max_tiles_big; t += kPermThreads)
+        tile_map_big[t] = make_int4(-1, 0, 0, 0);
     }
   }
 
@@ -145,7 +172,8 @@ __global__ void __launch_bounds__(kPermThreads) permute_kernel(
 
 int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,
                    int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
-                   int32_t* tile_map, int64_t max_tiles, hipStream_t stream) {
+                   int32_t* tile_map, int64_t max_tiles, hipStream_t stream, int split_rows,
+                   int m_tile_big, int32_t* tile_map_big, int64_t max_tiles_big) {
   const int words = (N + 31) / 32;
   int per_wg = (kPermLdsWords / 2) / words;
   if (per_wg < 1) return fail("permute: N too large for the LDS token bitmap");
@@ -153,10 +181,13 @@ int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t*
   const int n_wg = (E + per_wg - 1) / per_wg;
   if (tile_map && max_tiles < mtile_upper_bound(static_cast<int64_t>(N) * k, E, m_tile))
     return fail("permute: tile_map smaller than the m-tile upper bound");
-  permute_kernel<<<n_wg, kPermThreads, 0, stream>>>(idx, N, k, E, m_tile, per_wg, words, counts,
-                                                    offsets, tile_off, sorted_slot, inv,
-                                                    reinterpret_cast<int4*>(tile_map),
-                                                    static_cast<int>(max_tiles));
+  if (tile_map_big && (!tile_map || m_tile_big <= 0 ||
+                       max_tiles_big < mtile_upper_bound(static_cast<int64_t>(N) * k, E, m_tile_big)))
+    return fail("permute: split tile maps need both maps sized to their m-tile bounds");
+  permute_kernel<<<n_wg, kPermThreads, 0, stream>>>(
+      idx, N, k, E, m_tile, per_wg, words, counts, offsets, tile_off, sorted_slot, inv,
+      reinterpret_cast<int4*>(tile_map), static_cast<int>(max_tiles), split_rows, m_tile_big,
+      reinterpret_cast<int4*>(tile_map_big), static_cast<int>(max_tiles_big));
   return check_launch("permute");
 }
 

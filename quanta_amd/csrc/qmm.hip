@@ -11,18 +11,22 @@
 // expert's dense bf16 matmuls src/quanta/qwen35/moe.py:145-151; router logits
 // src/quanta/qwen35/moe.py:47.
 //
-// Two regimes, both on v_mfma_f32_16x16x32_bf16 with activations as the A operand
-// (16 token rows) and weights as the B operand (16 weight rows as columns):
+// Two regimes, both on 16x16x32 MFMAs with activations as the A operand (16 token rows) and
+// weights as the B operand (16 weight rows as columns):
 //  * small-M ("decode"): 16-token m-tiles; each wavefront streams one 16-row weight tile (two
 //    for SwiGLU) straight from HBM into registers with one contiguous 1 KiB dwordx4 load per
 //    superblock, and never materialises a dequantised weight. For int4 it multiplies the raw
-//    codes (as bf16 128+q, exact) and applies the per-group affine map on the 16x16 result:
+//    codes (as bf16 128+q, exact) on v_mfma_f32_16x16x32_bf16 and applies the per-group affine
+//    map on the 16x16 result:
 //      sum_k x_k (s q_k + b) = s * sum_k x_k (128+q_k) + (b - 128 s) * sum_k x_k,
 //    with sum_k x_k from one extra MFMA against a ones fragment. Optional split-K across the
 //    workgroup's wavefronts, reduced through LDS.
-//  * large-M ("prefill"): 128x128 workgroup tiles; each 128-deep k-step is dequantised
-//    cooperatively into LDS as bf16 (one dequant per weight element per workgroup, shared by
-//    128 tokens), activations gathered by token id into LDS, then 2x2 wavefronts of 64x64.
+//  * large-M ("prefill"): 128-position x 256-weight-row workgroup tiles, 8 wavefronts; int4
+//    weights are dequantised to fp16 in registers straight from their tiled global layout and
+//    multiplied on v_mfma_f32_16x16x32_f16 against an exactly scaled fp16 copy of the
+//    activations, staged through double-buffered LDS.
+#include <type_traits>
+
 #include "qmoe_internal.h"
 #include "../../include/quanta_moe.h"
 
@@ -252,194 +256,315 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
 
 // ============================================================================ large-M kernel
 // Workgroup tile: 128 sorted positions x 256 weight rows (SwiGLU: 128 gate + 128 up rows ->
-// 128 h columns), one 128-deep k-step (one int4 superblock) per iteration. 4 wavefronts in a
-// 2x2 arrangement, each owning 64 positions x 128 weight rows as 2x4 blocks of
-// v_mfma_f32_32x32x16 (f16 for int4 weights, bf16 for bf16 weights).
+// 128 h columns), one 128-deep k superblock per iteration. 8 wavefronts side by side along the
+// weight rows: wavefront w owns all 128 positions (8 m-blocks of 16) and two 16-row weight tiles
+// (SwiGLU: gate tile w and its up tile), on v_mfma_f32_16x16x32 (f16 for int4 weights, bf16 for
+// bf16 weights). Every weight is dequantized exactly once per workgroup; two wavefronts per SIMD.
 //
-// int4 weights are dequantized in registers, right after their global load and while the
-// previous step's MFMAs run, with packed fp16 FMAs (fp16(s*q + b), one rounding; 11-bit
-// mantissa), and activations come from the fp16 per-row-scaled copy (act16), so the step is an
-// exact-input fp16 product with fp32 accumulation. Outputs are rescaled per row by row_sinv.
-// bf16 weights (shared expert, router) are copied as they are, against bf16 activations.
-//
-// LDS (dynamic, 96 KiB): A [4 m-blocks of 32][8 k-steps of 16][64 lanes] and
-// B [8 n-blocks of 32][8][64], 16 B per entry, each entry one lane's MFMA fragment (lane l:
-// row l%32, k 8*(l/32)..+8 of the 16-k step), so fragment reads are conflict-free 16-byte loads.
-constexpr int kLgThreads = 256;
-constexpr size_t kLgLdsBytes = (2048 + 4096) * 16;
+// All streaming loads go global -> LDS directly (global_load_lds_dwordx4 / _dword), two
+// superblocks ahead of the MFMAs, into rings of three LDS slots:
+//  * A (activations): 32 KiB per slot, [m-block][step][64 lanes] x 16 B; wavefront w loads
+//    m-block w, lane l fetching row l%16's 8-k chunk that MFMA lane l consumes, so fragment
+//    reads are 64 consecutive 16-byte slots.
+//  * int4 weights: per wavefront and slot, its two tiles' 1 KiB code blocks (verbatim copies of
+//    the tiled layout, each lane's 16 bytes being its B fragments for the superblock's four
+//    32-k steps) and their 2 x 128 B of scale/bias.
+// Every wavefront waits for its own loads of the next superblock (explicit vmcnt: the loads are
+// issued from inline assembly, so the compiler neither tracks them nor serialises LDS reads
+// behind them), then one barrier publishes the superblock. Weights are dequantized from the
+// LDS copy in registers with packed fp16 FMAs (fp16(s*q + b), one rounding); activations come
+// from the fp16 per-row-scaled copy (act16), so each step is an exact-input fp16 product with
+// fp32 accumulation; the epilogue rescales rows by row_sinv. bf16 weights (shared expert,
+// router) are read into registers one superblock ahead, against bf16 activations.
+// A partly filled tile computes only its first 2, 4 or 8 m-blocks (three compiled variants of
+// the loop, chosen once per workgroup).
+constexpr int kLgThreads = 512;
+constexpr int kLgNBuf = 3;
+constexpr int kLgABytes = 8 * 4 * 64 * 16;                // one A slot: 32 KiB
+constexpr int kLgBWaveBytes = 2 * 1024 + 2 * 128;         // one wavefront's int4 weight slot
+constexpr int kLgBBytes = 8 * kLgBWaveBytes;              // 18 KiB
+constexpr size_t kLgLdsBytes = kLgNBuf * (kLgABytes + kLgBBytes);   // 150 KiB
+
+// 16-byte k-chunk (of 16 in a superblock) that MFMA step s consumes in lane group g: int4 weight
+// fragments follow the tiled code words, bf16 ones the natural 32-k chunks.
+template <int FMT>
+__device__ __forceinline__ int lg_chunk(int s, int g) {
+  return FMT == FMT_INT4 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
+}
+__device__ __forceinline__ f32x4_t mfma16_f16(u32x4 a, u32x4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+// LDS byte offset of a pointer into the kernel's dynamic LDS (the low 32 bits of its generic
+// address), made wave-uniform for M0
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
+// Global -> LDS copy: each lane's 16 (or 4) bytes at src land at lds_off + 16 (or 4) * lane.
+// M0 is saved and restored around the copy.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_off) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(src), "s"(lds_off) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds_off) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+               "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(src), "s"(lds_off) : "memory");
+}
+// Wait until at most n of this wavefront's vector-memory operations are outstanding (they
+// complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+// Workgroup barrier for the load rings: this wavefront's LDS reads drained (lgkmcnt 0), then
+// s_barrier. Unlike __syncthreads() it carries no release fence, whose vmcnt(0) would also wait
+// for the loads still in flight for later superblocks; the data each barrier publishes has been
+// waited for explicitly (wait_vmcnt) by the wavefront that loaded it.
+__device__ __forceinline__ void lg_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// bf16-weight superblock registers of a wavefront: 2 tiles x 4 steps of B fragments.
+struct LgStageBf {
+  u32x4 q[2][4];
+};
 
 template <int FMT, int EPI>
 __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   extern __shared__ u32x4 lds[];
-  u32x4* la = lds;
-  u32x4* lb = lds + 2048;
-
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  char* lds_c = reinterpret_cast<char*>(lds);
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave index as a scalar: per-wave decisions are uniform (scalar) branches
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int e, m0, m_cnt;
-  if (!resolve_mtile(a, blockIdx.y, kLargeMTile, e, m0, m_cnt)) return;
-  const int cb = blockIdx.x;
-  const int tiles_per_expert = a.n_rows / 16;
-  const int64_t ebase = static_cast<int64_t>(e) * tiles_per_expert;
+  // XCD-aware tile order. Workgroups are dispatched round-robin over the 8 XCDs, so linear id
+  // i runs on XCD i % 8 as that XCD's (i / 8)-th workgroup. Each XCD takes groups of G m-tiles
+  // x all nb weight-row blocks (G * nb <= 32, one workgroup per CU of the XCD): the nb blocks
+  // of an m-tile share its activation slices through the XCD's L2, and the G m-tiles share the
+  // weight slices, instead of every XCD streaming every activation row from MALL.
+  const int nbk = a.n_rows / 256;
+  const int G = (nbk >= 32) ? 1 : 32 / nbk;
+  const int wi = blockIdx.x, xcd = wi & 7, kx = wi >> 3;
+  const int gk = kx / (G * nbk), rk = kx - gk * (G * nbk);
+  const int mt = (gk * 8 + xcd) * G + rk / nbk;
+  const int cb = rk % nbk;
+  if (mt >= a.mtiles || !resolve_mtile(a, mt, kLargeMTile, e, m0, m_cnt)) return;
+  const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
   const int nsb = a.K / 128;
-  const int nks32 = a.K / 32;
+  const int mb_act = __builtin_amdgcn_readfirstlane((m_cnt + 15) >> 4);   // 1..8
 
-  // 16-row global tile of local tile lt (0..15)
-  auto gtile = [&](int lt) -> int {
-    if (EPI == EPI_SWIGLU) return (lt < 8) ? 8 * cb + lt : a.n_rows / 32 + 8 * cb + (lt - 8);
-    return 16 * cb + lt;
-  };
-
-  // ---- activation staging: thread -> row ar (0..127), 64-wide k half ah
-  const int ar = tid & 127, ah = tid >> 7;
-  int64_t arow = -1;
-  if (ar < m_cnt) arow = act_row(a, m0 + ar);
-  const uint32_t xmask = (arow >= 0) ? 0xFFFFFFFFu : 0u;
-  const uint16_t* abase = (FMT == FMT_INT4) ? a.act16 : a.act;
-  const u32x4* asrc =
-      reinterpret_cast<const u32x4*>(abase + (arow >= 0 ? arow : 0) * static_cast<int64_t>(a.K)) +
-      ah * 8;
-  // chunk i covers k 64ah + 8i: 16-k step 4ah + i/2, half (i&1)
-  u32x4* adst = la + ((ar >> 5) * 8 + 4 * ah) * 64 + (ar & 31);
-
-  // ---- weight staging pointers
-  const u32x4* cptr[4];
-  const uint2* sptr[4];
-  int bdst[4];
-  if (FMT == FMT_INT4) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int slot = tid + 256 * i, lt = slot >> 6, L = slot & 63;
-      const int64_t tb = (ebase + gtile(lt)) * nsb;
-      cptr[i] = static_cast<const u32x4*>(a.codes) + tb * 64 + L;
-      sptr[i] = reinterpret_cast<const uint2*>(a.sb) + tb * 16 + (L & 15);
-      const int rb = 16 * lt + (L & 15), g = L >> 4;
-      bdst[i] = ((rb >> 5) * 8 + g) * 64 + (rb & 31);   // + word-dependent offsets below
-    }
+  // ---- activation source: this wavefront loads m-block `wave`; lane -> row lane%16 of the
+  // block, k-chunk lg_chunk(s, lane/16) of step s. Rows past the tile and rows whose activation
+  // row is invalid read activation row 0 (the former are never stored, the latter are written
+  // as zeros by the epilogue). A wavefront whose m-block lies past the tile loads no A.
+  const bool a_on = wave < mb_act;
+  const char* arow_ptr;
+  {
+    const int r = 16 * wave + (lane & 15);
+    const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
+    const uint16_t* abase = (FMT == FMT_INT4) ? a.act16 : a.act;
+    arow_ptr = reinterpret_cast<const char*>(abase + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
+               16 * lg_chunk<FMT>(0, lane >> 4);
   }
-  const u32x4* wbase = nullptr;
-  if (FMT == FMT_BF16) {
-    // thread owns lane slot (k32 chunk (tid>>6)&3, lane tid&63) of local tiles 0..15
-    wbase = static_cast<const u32x4*>(a.codes) + ((tid >> 6) & 3) * 64 + (tid & 63);
-  }
+  const uint32_t lds_base = lds_offset(lds);
+  auto a_slot = [&](int p) { return (p % kLgNBuf) * kLgABytes; };
+  auto b_slot = [&](int p) { return kLgNBuf * kLgABytes + (p % kLgNBuf) * kLgBBytes + wave * kLgBWaveBytes; };
 
-  f32x16_t acc[2][4];
+  // ---- this wavefront's two weight tiles
+  const char* wcode[2];
+  const char* wsb[2];
+  const u32x4* wp[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int wm = wave >> 1, wn = wave & 1;
-  int wtl[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    wtl[j] = (EPI == EPI_SWIGLU) ? ((j < 2) ? 2 * wn + j : 4 + 2 * wn + (j - 2)) : 4 * wn + j;
-
-  u32x4 xv[8];
-  u32x4 bq[FMT == FMT_INT4 ? 4 : 16];   // raw codes (int4) or bf16 weight fragments
-  uint2 bs[4];
-  u32x4 dq[16];                         // dequantized fp16 weights (int4)
-
-  auto load_step = [&](int p) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = asrc[p * 16 + i] & xmask;
+  for (int t = 0; t < 2; ++t) {
+    const int tl = (EPI == EPI_SWIGLU) ? (t == 0 ? 8 * cb + wave : a.n_rows / 32 + 8 * cb + wave)
+                                       : 16 * cb + 2 * wave + t;
     if (FMT == FMT_INT4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        bq[i] = cptr[i][p * 64];
-        bs[i] = sptr[i][p * 16];
-      }
+      const int64_t tb = (ebase + tl) * nsb;
+      wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
+      wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
+      wp[t] = nullptr;
     } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        bq[i] = wbase[((ebase + gtile(i)) * nks32 + 4 * p) * 64];
+      wcode[t] = wsb[t] = nullptr;
+      wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
     }
-  };
-  auto dequant_step = [&]() __attribute__((always_inline)) {
-    if (FMT == FMT_INT4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int gg = 0; gg < 2; ++gg) {
-          const uint32_t sbw = gg ? bs[i].y : bs[i].x;
-          const _Float16 s = static_cast<_Float16>(bf16lo_to_f32(sbw));
-          const _Float16 b = static_cast<_Float16>(bf16hi_to_f32(sbw));
-          const f16x2_t s2 = {s, s}, b2 = {b, b};
-          dq[4 * i + 2 * gg + 0] = dequant_word_f16(gg ? bq[i].z : bq[i].x, s2, b2);
-          dq[4 * i + 2 * gg + 1] = dequant_word_f16(gg ? bq[i].w : bq[i].y, s2, b2);
-        }
-      }
-    }
-  };
-
-  load_step(0);
-  dequant_step();
-  for (int p = 0; p < nsb; ++p) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) adst[(i >> 1) * 64 + 32 * (i & 1)] = xv[i];
-    if (FMT == FMT_INT4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          // word t: group gg = t>>1 (k 64gg..), step s = t&1 -> 16-k step 4gg + g, half s
-          const int gg = t >> 1, s = t & 1;
-          lb[bdst[i] + (4 * gg) * 64 + 32 * s] = dq[4 * i + t];
-        }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        // tile i, k32 chunk cc = (tid>>6)&3, lane L = tid&63: row 16i + L%16, k 32cc + 8(L/16)
-        const int L = tid & 63, cc = (tid >> 6) & 3;
-        const int rb = 16 * i + (L & 15), kk = 32 * cc + 8 * (L >> 4);
-        lb[((rb >> 5) * 8 + (kk >> 4)) * 64 + 32 * ((kk >> 3) & 1) + (rb & 31)] = bq[i];
-      }
-    }
-    __syncthreads();
-    const bool more = p + 1 < nsb;
-    if (more) load_step(p + 1);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      u32x4 A[2], B[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) A[i] = la[((2 * wm + i) * 8 + ks) * 64 + lane];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) B[j] = lb[(wtl[j] * 8 + ks) * 64 + lane];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = (FMT == FMT_INT4) ? mfma32_f16(A[i], B[j], acc[i][j])
-                                        : mfma32_bf16(A[i], B[j], acc[i][j]);
-    }
-    if (more) dequant_step();
   }
+  // scale/bias copy: lanes 0-31 take tile 0's 128 B, lanes 32-63 tile 1's, 4 B each
+  const char* sb_src = (FMT == FMT_INT4) ? wsb[lane >> 5] + 4 * (lane & 31) : nullptr;
 
-  // ---- epilogue: lane holds C[row 8(r/4) + 4(lane/32) + r%4][col lane%32] of each block
+  // issue all loads of superblock p (A: 4 instructions when a_on; int4 weights: 3)
+  auto issue = [&](int p) __attribute__((always_inline)) {
+    if (a_on) {
+      const char* src = arow_ptr + 256 * p;
+      const uint32_t dst = lds_base + a_slot(p) + wave * 4 * 1024;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+      for (int s = 0; s < 4; ++s) {
+        const int off = 16 * ((FMT == FMT_INT4) ? 8 * (s >> 1) + (s & 1) : 4 * s);
+        dma16(src + off, dst + s * 1024);
+      }
+    }
+    if (FMT == FMT_INT4) {
+      const uint32_t dst = lds_base + b_slot(p);
+      dma16(wcode[0] + static_cast<int64_t>(p) * 1024, dst);
+      dma16(wcode[1] + static_cast<int64_t>(p) * 1024, dst + 1024);
+      dma4(sb_src + static_cast<int64_t>(p) * 128, dst + 2048);
+    }
+  };
+
+  f32x4_t acc[8][2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int mr = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      if (mr >= m_cnt) continue;
-      float rs = 1.0f;
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // One superblock: four 32-k MFMA steps, software-pipelined by hand. Step s is MB slots; slot
+  // i issues the two MFMAs of m-block i, the read of m-block i's A fragment for step s+1 and
+  // 1/MB of step s+1's weight dequant, and a scheduling barrier keeps that order, so LDS reads
+  // have a full step to land and the dequant VALU work is spread between the MFMAs.
+  const uint32_t exp_bits = 0x64006400u;
+  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  auto compute = [&](int p, const LgStageBf& gb, auto mbc) __attribute__((always_inline)) {
+    constexpr int MB = decltype(mbc)::value;
+    constexpr int UPS = 8 / MB;                 // dequant units (nibble pairs) per slot
+    const u32x4* la = reinterpret_cast<const u32x4*>(lds_c + a_slot(p)) + lane;
+    u32x4 q[2];
+    uint2 sbv[2];
+    if (FMT == FMT_INT4) {
+      const char* lb = lds_c + b_slot(p);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
+        sbv[t] = reinterpret_cast<const uint2*>(lb + 2048 + t * 128)[lane & 15];
+      }
+    }
+    f16x2_t s2[2], b2[2];
+    auto sb_conv = [&](int grp) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t sbw = grp ? sbv[t].y : sbv[t].x;
+        const _Float16 sv = static_cast<_Float16>(bf16lo_to_f32(sbw));
+        const _Float16 bv = static_cast<_Float16>(bf16hi_to_f32(sbw));
+        s2[t] = f16x2_t{sv, sv};
+        b2[t] = f16x2_t{bv, bv};
+      }
+    };
+    // dequant unit u (0..7) of step s: tile u/4, nibble pair u%4 -> one packed fp16 register
+    auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
+      const int t = u >> 2, j = u & 3;
       if (FMT == FMT_INT4) {
-        const int64_t ar2 = act_row(a, m0 + mr);
-        rs = (ar2 >= 0) ? a.row_sinv[ar2] : 0.0f;
+        uint32_t r;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q[t][s] >> (4 * j)), "s"(0x000F000Fu),
+            "v"(exp_bits));
+        const f16x2_t qq = __builtin_bit_cast(f16x2_t, r) - k1024;
+        bfo[t][j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qq, s2[t], b2[t]));
+      } else if (j == 0) {
+        bfo[t] = gb.q[t][s];
       }
-      if (EPI == EPI_SWIGLU) {
+    };
+    u32x4 bf[2][2], A[2][MB];
+    if (FMT == FMT_INT4) sb_conv(0);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int col = 128 * cb + 64 * wn + 32 * t + (lane & 31);
-          store_out<EPI>(a, m0 + mr, col, acc[i][t][r] * rs, acc[i][2 + t][r] * rs);
+    for (int u = 0; u < 8; ++u) deq_unit(0, u, bf[0]);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) A[0][i] = la[256 * i];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = s & 1;
+      if (FMT == FMT_INT4 && s == 1) sb_conv(1);      // group 1 feeds steps 2 and 3
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          acc[i][t] = (FMT == FMT_INT4) ? mfma16_f16(A[c][i], bf[c][t], acc[i][t])
+                                        : mfma16(as_bf16x8(A[c][i]), as_bf16x8(bf[c][t]), acc[i][t]);
+        if (s < 3) {
+          A[c ^ 1][i] = la[256 * i + 64 * (s + 1)];
+#pragma unroll
+          for (int v = 0; v < UPS; ++v) deq_unit(s + 1, i * UPS + v, bf[c ^ 1]);
         }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  // bf16 weights: registers, one superblock ahead
+  LgStageBf gbf[2];
+  auto load_bf = [&](int p, LgStageBf& g) __attribute__((always_inline)) {
+    if (FMT == FMT_BF16) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) g.q[t][s] = wp[t][(4 * p + s) * 64];
+    }
+  };
+
+  // Loads in flight per wavefront and superblock: NA (A, when a_on) + NB (int4 weights).
+  // Before the barrier that publishes superblock p+1, a wavefront waits until only the loads
+  // of p+2 remain outstanding.
+  constexpr int NB = (FMT == FMT_INT4) ? 3 : 0;
+  auto run = [&](auto mbc) __attribute__((always_inline)) {
+    auto wait_next = [&](bool far) __attribute__((always_inline)) {
+      // loads of the superblock after the next one, if issued, may stay in flight
+      if (a_on) {
+        if (far) wait_vmcnt<4 + NB>(); else wait_vmcnt<0>();
+      } else {
+        if (far) wait_vmcnt<NB>(); else wait_vmcnt<0>();
+      }
+    };
+    issue(0);
+    if (nsb > 1) issue(1);
+    load_bf(0, gbf[0]);
+    wait_next(nsb > 1);
+    lg_barrier();
+    auto iter = [&](int p, const LgStageBf& cur, LgStageBf& nxt) __attribute__((always_inline)) {
+      const bool far = p + 2 < nsb;
+      if (far) issue(p + 2);
+      load_bf(p + 1, nxt);
+      compute(p, cur, mbc);
+      wait_next(far);
+      lg_barrier();
+    };
+    int p = 0;
+    for (; p + 2 < nsb; p += 2) {
+      iter(p, gbf[0], gbf[1]);
+      iter(p + 1, gbf[1], gbf[0]);
+    }
+    if (p + 1 < nsb) {
+      iter(p, gbf[0], gbf[1]);
+      compute(p + 1, gbf[1], mbc);
+    } else {
+      compute(p, gbf[0], mbc);
+    }
+  };
+  if (mb_act <= 2) run(std::integral_constant<int, 2>{});
+  else if (mb_act <= 4) run(std::integral_constant<int, 4>{});
+  else run(std::integral_constant<int, 8>{});
+
+  // ---- epilogue: lane holds C[row 4(lane/16) + j][col lane%16] of each 16x16 block
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i >= mb_act) break;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int mr = 16 * i + 4 * (lane >> 4) + j;
+      if (mr >= m_cnt) continue;
+      // rows whose activation row is invalid read as zeros (their A data was row 0's)
+      const int64_t ar2 = act_row(a, m0 + mr);
+      const bool ok = ar2 >= 0;
+      const float rs = (FMT == FMT_INT4 && ok) ? a.row_sinv[ar2] : 1.0f;
+      if (EPI == EPI_SWIGLU) {
+        const int col = 128 * cb + 16 * wave + (lane & 15);
+        store_out<EPI>(a, m0 + mr, col, ok ? acc[i][0][j] * rs : 0.f, ok ? acc[i][1][j] * rs : 0.f);
       } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int col = 256 * cb + 32 * (4 * wn + t) + (lane & 31);
-          store_out<EPI>(a, m0 + mr, col, acc[i][t][r] * rs, 0.f);
+        for (int t = 0; t < 2; ++t) {
+          const int col = 256 * cb + 32 * wave + 16 * t + (lane & 15);
+          store_out<EPI>(a, m0 + mr, col, ok ? acc[i][t][j] * rs : 0.f, 0.f);
         }
       }
     }
@@ -522,13 +647,19 @@ static void launch_small(const QmmArgs& a, int ksplit, int64_t mtiles, hipStream
 
 template <int FMT, int EPI>
 static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
-  // 96 KiB of dynamic LDS is above the default per-kernel limit; set it for the current device
+  // 150 KiB of dynamic LDS is above the default per-kernel limit; set it for the current device
   const hipError_t err =
       hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_large_kernel<FMT, EPI>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLgLdsBytes));
   if (err != hipSuccess) return fail(std::string("qmm(large): LDS attribute: ") + hipGetErrorString(err));
-  dim3 grid(a.n_rows / 256, static_cast<unsigned>(mtiles));
-  qmm_large_kernel<FMT, EPI><<<grid, kLgThreads, kLgLdsBytes, stream>>>(a);
+  // 1-D grid in the XCD-grouped order the kernel decodes: m-tiles padded to whole groups of
+  // 8 XCDs x G m-tiles; workgroups past `mtiles` exit at once
+  const int nbk = a.n_rows / 256;
+  const int G = (nbk >= 32) ? 1 : 32 / nbk;
+  const int64_t mpad = (mtiles + 8 * G - 1) / (8 * G) * (8 * G);
+  QmmArgs b = a;
+  b.mtiles = static_cast<int>(mtiles);
+  qmm_large_kernel<FMT, EPI><<<dim3(static_cast<unsigned>(mpad * nbk)), kLgThreads, kLgLdsBytes, stream>>>(b);
   return 0;
 }
 

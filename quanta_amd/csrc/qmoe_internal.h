@@ -130,6 +130,23 @@ __device__ __forceinline__ u32x4 dequant_word_f16(uint32_t w, f16x2_t s2, f16x2_
   return out;
 }
 
+// Same result as dequant_word_f16; the nibble pair extraction is one v_and_or_b32 per pair (mask
+// and exponent bits as register operands, which gfx9-family VOP3 encodings require) instead of
+// the separate and + or the compiler otherwise emits for two literal constants.
+__device__ __forceinline__ u32x4 dequant_word_f16_ao(uint32_t w, f16x2_t s2, f16x2_t b2,
+                                                     uint32_t exp_bits) {
+  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  u32x4 out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w >> (4 * j)), "s"(0x000F000Fu), "v"(exp_bits));
+    const f16x2_t q = __builtin_bit_cast(f16x2_t, r) - k1024;
+    out[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
+  }
+  return out;
+}
+
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 
 // Upper bound on the number of m-tiles a permuted (token, slot) list can produce.
@@ -145,9 +162,12 @@ int launch_topk(const float* logits, int ld_logits, const float* bias, int N, in
                 int scoring, int n_group, int topk_group, int norm_topk, float scale,
                 int has_shared_gate, int32_t* idx, float* w, float* shared_gate_out,
                 hipStream_t stream);
+// With tile_map_big: experts of more than split_rows rows get m_tile_big-row tiles there and
+// none in tile_map (the hybrid regime); without it, every expert's tiles go to tile_map.
 int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,
                    int32_t* offsets, int32_t* tile_off, int32_t* sorted_slot, int32_t* inv,
-                   int32_t* tile_map, int64_t max_tiles, hipStream_t stream);
+                   int32_t* tile_map, int64_t max_tiles, hipStream_t stream, int split_rows = 0,
+                   int m_tile_big = 0, int32_t* tile_map_big = nullptr, int64_t max_tiles_big = 0);
 
 struct QmmArgs {
   const uint16_t* act;        // activation rows (bf16), row stride K
@@ -168,6 +188,7 @@ struct QmmArgs {
   int ld_out;                 // output row stride (elements)
   const uint16_t* act16;      // large int4 regime: fp16 copy of act, row r scaled by 1/row_sinv[r]
   const float* row_sinv;      // large int4 regime: per activation row inverse scale (2^e)
+  int mtiles;                 // large regime: m-tiles in the grid (entries of tile_map it reads)
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1 };
@@ -189,5 +210,8 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 
 constexpr int kSmallMTile = 16;
 constexpr int kLargeMTile = 128;
+// Large-M (prefill) regime: experts routed more rows than this use 128-row tiles on the large
+// kernel, the others 16-row tiles on the small kernel.
+constexpr int kHybridSplitRows = 32;
 
 }  // namespace qmoe

@@ -102,6 +102,16 @@ def zipf_logit_bias(E: int, g: torch.Generator, device) -> torch.Tensor:
     return -ZIPF_S * ZIPF_TAU * torch.log(rank)
 
 
+def zipf_router(gate: torch.Tensor, seed: int = 4) -> torch.Tensor:
+    """A copy of a router weight [E, H] whose column 0 carries the c4 Zipf popularity bias (used
+    with inputs whose channel 0 is 1.0), turning a c2 layer into the c4 prefill workload without
+    regenerating its experts."""
+    g = _gen(gate.device, (1000 + seed) * 1009 + 7)
+    out = gate.clone()
+    out[:, 0] = zipf_logit_bias(gate.shape[0], g, gate.device).to(gate.dtype)
+    return out
+
+
 def make_layer(name: str | SynthSpec, *, device="cuda", seed: int | None = None,
                layer: int = 0) -> dict:
     """Parameter dict with the reference keys (src/quanta/qwen35/moe.py:159-161); routed experts as
