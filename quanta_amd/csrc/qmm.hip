@@ -91,23 +91,24 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
 }
 
 // ============================================================================ small-M kernel
-// One wavefront = one 16-row weight tile job (two tiles, gate and up, for SwiGLU) over one
-// k-range of one 16-position m-tile. KSPLIT wavefronts of a workgroup share a job and split K;
-// their partial tiles are summed through LDS. WAVES = max(4, KSPLIT) wavefronts per workgroup.
-template <int FMT, int KSPLIT>
+// One wavefront = JPW consecutive 16-row weight tile jobs (each two tiles, gate and up, for
+// SwiGLU) over one k-range of one 16-position m-tile; the jobs share the wavefront's activation
+// fragments, so activation loads are amortised over JPW times the weight bytes. KSPLIT
+// wavefronts of a workgroup share the jobs and split K; their partial tiles are summed through
+// LDS. WAVES = max(4, KSPLIT) wavefronts per workgroup.
+template <int NT>
 struct SmallStage {
-  static constexpr int NT = 2;
   u32x4 q[NT];    // int4: raw codes of one superblock / bf16: weight fragments of one 32-k step
   uint2 sb[NT];   // int4 scale/bias of the superblock's two groups
   u32x4 x[4];     // activation fragments
 };
 
-template <int FMT, int EPI, int KSPLIT>
+template <int FMT, int EPI, int KSPLIT, int JPW>
 __global__ void __launch_bounds__(KSPLIT > 4 ? 64 * KSPLIT : 256)
 qmm_small_kernel(QmmArgs a, int n_jobs) {
   constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
   constexpr int JOBS_PER_WG = WAVES / KSPLIT;
-  constexpr int NT = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int NT = ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW;
   __shared__ f32x4_t red[(KSPLIT > 1) ? WAVES * NT * 64 : 1];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -129,9 +130,14 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
   for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int tiles_per_expert = a.n_rows / 16;
+  // tiles of this wavefront's jobs: job j covers tile j (SwiGLU: gate tile j and up tile
+  // j + n_rows/32, the up half starting at row I = n_rows/2); SwiGLU keeps gates first
   int tile[NT];
-  tile[0] = job;
-  if (NT == 2) tile[NT - 1] = job + a.n_rows / 32;   // up half starts at row I = n_rows/2
+#pragma unroll
+  for (int jp = 0; jp < JPW; ++jp) {
+    tile[jp] = job * JPW + jp;
+    if (EPI == EPI_SWIGLU) tile[JPW + jp] = job * JPW + jp + a.n_rows / 32;
+  }
 
   if (job_ok) {
     if (FMT == FMT_INT4) {
@@ -153,12 +159,15 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
       }
       const f32x4_t zero4{0.f, 0.f, 0.f, 0.f};
       // Two register stages: the loads of superblock p+1 are in flight while p is computed.
-      SmallStage<FMT, KSPLIT> st[2];
-      auto load = [&](SmallStage<FMT, KSPLIT>& s, int p) __attribute__((always_inline)) {
+      SmallStage<NT> st[2];
+      auto load = [&](SmallStage<NT>& s, int p) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          s.q[t] = cp[t][p * 64];
-          s.sb[t] = sp[t][p * 16];
+          // weights are streamed once per call: nontemporal loads keep them out of the way of
+          // the activations that every job of the m-tile re-reads
+          s.q[t] = __builtin_nontemporal_load(cp[t] + p * 64);
+          const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(sp[t] + p * 16));
+          s.sb[t] = uint2{v.x, v.y};
         }
         // group 2p: k 16lg + 0..7 (step 0) and + 8..15 (step 1); group 2p+1 likewise, +64.
         // Only rows of the segment load; the rest of the 16-row tile is zeros.
@@ -171,7 +180,7 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
           s.x[0] = s.x[1] = s.x[2] = s.x[3] = u32x4{0u, 0u, 0u, 0u};
         }
       };
-      auto compute = [&](const SmallStage<FMT, KSPLIT>& s) __attribute__((always_inline)) {
+      auto compute = [&](const SmallStage<NT>& s) __attribute__((always_inline)) {
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
           const bf16x8_t A0 = as_bf16x8(s.x[2 * gg]);
@@ -246,11 +255,15 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
   }
   if (!job_ok || kpart != 0) return;
 
-  const int col = job * 16 + (lane & 15);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int mr = 4 * lg + j;
-    if (mr < m_cnt) store_out<EPI>(a, m0 + mr, col, acc[0][j], acc[NT - 1][j]);
+  for (int jp = 0; jp < JPW; ++jp) {
+    const int col = (job * JPW + jp) * 16 + (lane & 15);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int mr = 4 * lg + j;
+      if (mr < m_cnt)
+        store_out<EPI>(a, m0 + mr, col, acc[jp][j], acc[(EPI == EPI_SWIGLU) ? JPW + jp : jp][j]);
+    }
   }
 }
 
@@ -625,23 +638,42 @@ int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16,
 
 
 // ============================================================================ launcher
-template <int FMT, int EPI, int KSPLIT>
+// Fewest small-kernel workgroups (over the m-tile bound) for which several jobs per wavefront
+// are used: below it, one job per wavefront keeps more wavefronts streaming.
+constexpr int64_t kSmallMinWgs = 4096;
+template <int FMT, int EPI, int KSPLIT, int JPW>
 static void launch_small_k(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
-  const int n_jobs = (EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
+  const int n_jobs = ((EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16) / JPW;
   const int jobs_per_wg = WAVES / KSPLIT;
   dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mtiles));
-  qmm_small_kernel<FMT, EPI, KSPLIT><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
+  qmm_small_kernel<FMT, EPI, KSPLIT, JPW><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
+}
+
+// Jobs per wavefront: int4 weights take several tiles per wavefront (sharing its activation
+// fragments) when the grid stays large enough to fill the chip; bf16 weights take one.
+template <int FMT, int EPI, int KSPLIT>
+static void launch_small_j(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
+  constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
+  const int jobs = (EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
+  auto wgs = [&](int jpw) { return mtiles * ((jobs / jpw + WAVES / KSPLIT - 1) / (WAVES / KSPLIT)); };
+  // (SwiGLU wavefronts hold two tiles per job: four jobs would exceed the register budget)
+  if (FMT == FMT_INT4 && EPI != EPI_SWIGLU && jobs % 4 == 0 && wgs(4) >= kSmallMinWgs)
+    launch_small_k<FMT, EPI, KSPLIT, (EPI == EPI_SWIGLU) ? 2 : 4>(a, mtiles, stream);
+  else if (FMT == FMT_INT4 && jobs % 2 == 0 && wgs(2) >= kSmallMinWgs)
+    launch_small_k<FMT, EPI, KSPLIT, 2>(a, mtiles, stream);
+  else
+    launch_small_k<FMT, EPI, KSPLIT, 1>(a, mtiles, stream);
 }
 
 template <int FMT, int EPI>
 static void launch_small(const QmmArgs& a, int ksplit, int64_t mtiles, hipStream_t stream) {
   switch (ksplit) {
-    case 16: launch_small_k<FMT, EPI, 16>(a, mtiles, stream); break;
-    case 8: launch_small_k<FMT, EPI, 8>(a, mtiles, stream); break;
-    case 4: launch_small_k<FMT, EPI, 4>(a, mtiles, stream); break;
-    case 2: launch_small_k<FMT, EPI, 2>(a, mtiles, stream); break;
-    default: launch_small_k<FMT, EPI, 1>(a, mtiles, stream); break;
+    case 16: launch_small_j<FMT, EPI, 16>(a, mtiles, stream); break;
+    case 8: launch_small_j<FMT, EPI, 8>(a, mtiles, stream); break;
+    case 4: launch_small_j<FMT, EPI, 4>(a, mtiles, stream); break;
+    case 2: launch_small_j<FMT, EPI, 2>(a, mtiles, stream); break;
+    default: launch_small_j<FMT, EPI, 1>(a, mtiles, stream); break;
   }
 }
 

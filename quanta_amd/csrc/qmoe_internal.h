@@ -29,6 +29,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 // Native 16-byte vector (HIP's uint4 is a struct whose copies lower to memcpy, which can
 // pin arrays of it in scratch); used for all raw 16-byte global/LDS traffic in the kernels.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------ error reporting
 void set_error(const std::string& msg);

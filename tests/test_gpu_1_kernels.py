@@ -202,9 +202,12 @@ def _qmm_problem(rng, N, k, E, H, rows, fmt):
 @pytest.mark.parametrize("fmt", [L.FMT_INT4_G64, L.FMT_BF16])
 @pytest.mark.parametrize("regime", [L.REGIME_SMALL, L.REGIME_LARGE])
 @pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
+# (1024, 4, 32, 256, 1024): enough m-tiles that the small kernel runs several jobs per
+# wavefront (2 for SwiGLU, 4 otherwise)
 @pytest.mark.parametrize("N,k,E,H,rows,use_map", [(7, 3, 6, 256, 256, True), (40, 2, 5, 512, 384, False),
                                                   (1, 4, 8, 4096, 256, True), (200, 4, 4, 1024, 128, True),
-                                                  (300, 3, 5, 768, 512, True), (129, 2, 3, 256, 768, False)])
+                                                  (300, 3, 5, 768, 512, True), (129, 2, 3, 256, 768, False),
+                                                  (1024, 4, 32, 256, 1024, True)])
 def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows, use_map):
     if regime == L.REGIME_LARGE and rows % 256:
         pytest.skip("the large regime tiles 256 weight rows")
