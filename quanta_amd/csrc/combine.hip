@@ -6,9 +6,10 @@
 // y = bf16(routed + f32(shared_out) * sigmoid(x . g)) (src/quanta/qwen35/moe.py:145-151,201-202).
 // The combine gathers each slot's row through inv (no atomics), summing in slot order, so the
 // output is deterministic.
-#include <string>
-
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <string>
 
 #include "qmoe_internal.h"
 #include "../../include/quanta_moe.h"
@@ -95,6 +96,43 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 }
 
 int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int topk_group);
+
+// ------------------------------------------------------------------ auxiliary stream
+// The shared expert depends only on x, so qmoe_forward runs it on a library-owned stream
+// (created once per device, default priority) concurrently with the router -> top-k ->
+// permute -> routed chain: a fork event records the caller's stream at entry and the caller's
+// stream waits on a join event right before the combine. The mutex is held from the fork record
+// until the join wait is enqueued, so concurrent calls on different streams cannot exchange
+// the events.
+struct AuxStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::mutex g_aux_mu;
+constexpr int64_t kAuxMinTokens = 8;
+static std::map<int, AuxStream> g_aux;
+
+static int aux_stream(hipStream_t caller, AuxStream** out) {
+  int dev = 0;
+  hipError_t err = hipStreamGetDevice(caller, &dev);
+  if (err != hipSuccess) return fail(std::string("forward: stream device: ") + hipGetErrorString(err));
+  AuxStream& a = g_aux[dev];
+  if (!a.s) {
+    int cur = 0;
+    err = hipGetDevice(&cur);
+    if (err == hipSuccess && cur != dev) err = hipSetDevice(dev);
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&a.s, hipStreamNonBlocking);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&a.fork, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&a.join, hipEventDisableTiming);
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (err != hipSuccess) {
+      a = AuxStream{};
+      return fail(std::string("forward: auxiliary stream: ") + hipGetErrorString(err));
+    }
+  }
+  *out = &a;
+  return 0;
+}
 
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
@@ -315,7 +353,44 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4 : FMT_BF16;
   const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
 
-  // 1. router logits (+ the shared-expert gate logit in column E)
+  // fork the shared expert onto the auxiliary stream (held until its join is enqueued below)
+  // (below kAuxMinTokens the cross-stream synchronisation costs more than the overlap saves)
+  std::unique_lock<std::mutex> aux_lock;
+  AuxStream* aux = nullptr;
+  hipStream_t sstream = stream;
+  if (c.shared_inter > 0 && N >= kAuxMinTokens) {
+    aux_lock = std::unique_lock<std::mutex>(g_aux_mu);
+    rc = aux_stream(stream, &aux);
+    if (rc) return rc;
+    hipError_t err = hipEventRecord(aux->fork, stream);
+    if (err == hipSuccess) err = hipStreamWaitEvent(aux->s, aux->fork, 0);
+    if (err != hipSuccess) return fail(std::string("forward: fork: ") + hipGetErrorString(err));
+    sstream = aux->s;
+  }
+
+  // 1. shared expert (gate_up + SwiGLU, then down) on the auxiliary stream
+  const int sreg = dense_regime(c, N);
+  const int st = (sreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
+  if (c.shared_inter > 0) {
+    QmmArgs a{};
+    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
+    a.K = c.hidden; a.n_rows = 2 * c.shared_inter; a.codes = wts->sh_gu; a.out = sh_h;
+    a.ld_out = c.shared_inter;
+    rc = launch_qmm(a, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
+    if (rc) return rc;
+    QmmArgs b{};
+    b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
+    b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = wts->sh_dn; b.out = sh_out;
+    b.ld_out = c.hidden;
+    rc = launch_qmm(b, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, sstream);
+    if (rc) return rc;
+    if (aux) {
+      const hipError_t err = hipEventRecord(aux->join, aux->s);
+      if (err != hipSuccess) return fail(std::string("forward: join record: ") + hipGetErrorString(err));
+    }
+  }
+
+  // 2. router logits (+ the shared-expert gate logit in column E)
   int ld = 0;
   if (c.router_format == QMOE_ROUTER_F32) {
     ld = c.n_experts + 1;
@@ -332,11 +407,11 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     rc = launch_qmm(a, FMT_BF16, EPI_F32, rreg, (N + rt - 1) / rt, stream);
   }
   if (rc) return rc;
-  // 2. top-k
+  // 3. top-k
   rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
                    c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream);
   if (rc) return rc;
-  // 3. stable permute by expert (16-row tiles; hybrid: hot experts' 128-row tiles separately)
+  // 4. stable permute by expert (16-row tiles; hybrid: hot experts' 128-row tiles separately)
   rc = launch_permute(idx, n, c.top_k, c.n_experts, kSmallMTile, counts, offsets, tile_off, sorted,
                       inv, tile_map, bound_small, stream, kHybridSplitRows, kLargeMTile,
                       hybrid ? tile_map_big : nullptr, L.max_tiles_big);
@@ -353,7 +428,7 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     a.row_sinv = sinv;
     return launch_qmm(a, wfmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
   };
-  // 4. routed gate_up + SwiGLU -> h (sorted order)
+  // 5. routed gate_up + SwiGLU -> h (sorted order)
   {
     QmmArgs a{};
     a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
@@ -365,17 +440,6 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
       if (rc) return rc;
     }
     rc = routed(a, EPI_SWIGLU, x16, x_sinv);
-    if (rc) return rc;
-  }
-  // 5. shared expert gate_up + SwiGLU
-  const int sreg = dense_regime(c, N);
-  const int st = (sreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
-  if (c.shared_inter > 0) {
-    QmmArgs a{};
-    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
-    a.K = c.hidden; a.n_rows = 2 * c.shared_inter; a.codes = wts->sh_gu; a.out = sh_h;
-    a.ld_out = c.shared_inter;
-    rc = launch_qmm(a, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, stream);
     if (rc) return rc;
   }
   // 6. routed down -> d (sorted order)
@@ -392,16 +456,11 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     rc = routed(a, EPI_BF16, h16, h_sinv);
     if (rc) return rc;
   }
-  // 7. shared expert down
-  if (c.shared_inter > 0) {
-    QmmArgs a{};
-    a.act = sh_h; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
-    a.K = c.shared_inter; a.n_rows = c.hidden; a.codes = wts->sh_dn; a.out = sh_out;
-    a.ld_out = c.hidden;
-    rc = launch_qmm(a, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, stream);
-    if (rc) return rc;
+  if (aux) {
+    const hipError_t err = hipStreamWaitEvent(stream, aux->join, 0);
+    if (err != hipSuccess) return fail(std::string("forward: join wait: ") + hipGetErrorString(err));
   }
-  // 8. unpermute + weighted combine + gated shared + bf16
+  // 7. unpermute + weighted combine + gated shared + bf16
   return launch_combine(d, inv, wv, n, c.top_k, c.hidden, c.shared_inter > 0 ? sh_out : nullptr,
                         has_sg ? sg : nullptr, y, stream);
 }
