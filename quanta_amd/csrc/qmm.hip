@@ -93,9 +93,14 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
 // ============================================================================ small-M kernel
 // One wavefront = JPW consecutive 16-row weight tile jobs (each two tiles, gate and up, for
 // SwiGLU) over one k-range of one 16-position m-tile; the jobs share the wavefront's activation
-// fragments, so activation loads are amortised over JPW times the weight bytes. KSPLIT
-// wavefronts of a workgroup share the jobs and split K; their partial tiles are summed through
-// LDS. WAVES = max(4, KSPLIT) wavefronts per workgroup.
+// fragments, so activation loads are amortised over JPW times the weight bytes.
+//
+// Summation order: K is cut into CH = W * CPW equal chunks (CH depends on K only); each chunk is
+// summed from zero over its superblocks, and the chunk sums are added in chunk order,
+// ((c0 + c1) + c2) + ... . W wavefronts of a workgroup share a job, each summing CPW consecutive
+// chunks; chunk sums meet in LDS. How many wavefronts share the chunks (W) varies with the
+// launch size, but the arithmetic does not, so every output is bit-identical at every batch size.
+// WAVES = max(4, W) wavefronts per workgroup.
 template <int NT>
 struct SmallStage {
   u32x4 q[NT];    // int4: raw codes of one superblock / bf16: weight fragments of one 32-k step
@@ -103,20 +108,24 @@ struct SmallStage {
   u32x4 x[4];     // activation fragments
 };
 
-template <int FMT, int EPI, int KSPLIT, int JPW>
-__global__ void __launch_bounds__(KSPLIT > 4 ? 64 * KSPLIT : 256)
+template <int FMT, int EPI, int W, int CPW, int JPW>
+__global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
 qmm_small_kernel(QmmArgs a, int n_jobs) {
-  constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
-  constexpr int JOBS_PER_WG = WAVES / KSPLIT;
+  constexpr int WAVES = W > 4 ? W : 4;
+  constexpr int JOBS_PER_WG = WAVES / W;
   constexpr int NT = ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW;
-  __shared__ f32x4_t red[(KSPLIT > 1) ? WAVES * NT * 64 : 1];
+  constexpr int CH = W * CPW;
+  static_assert(FMT == FMT_INT4 || CPW == 1, "bf16 weights use one chunk per wavefront");
+  // chunk sums: [wave][chunk of the wave][tile][lane]
+  constexpr bool kRed = CH > 1;
+  __shared__ f32x4_t red[kRed ? WAVES * CPW * NT * 64 : 1];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int e, m0, m_cnt;
   if (!resolve_mtile(a, blockIdx.y, kSmallMTile, e, m0, m_cnt)) return;
 
-  const int job = blockIdx.x * JOBS_PER_WG + wave / KSPLIT;
-  const int kpart = wave % KSPLIT;
+  const int job = blockIdx.x * JOBS_PER_WG + wave / W;
+  const int kpart = wave % W;
   const bool job_ok = job < n_jobs;
   const int mrow = lane & 15, lg = lane >> 4;
 
@@ -142,7 +151,9 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
   if (job_ok) {
     if (FMT == FMT_INT4) {
       const int nsb = a.K / 128;
-      const int p0 = kpart * nsb / KSPLIT, p1 = (kpart + 1) * nsb / KSPLIT;
+      // chunk c = superblocks [c * nsb / CH, (c + 1) * nsb / CH); this wavefront: CPW chunks
+      const int p0 = kpart * CPW * nsb / CH, p1 = (kpart + 1) * CPW * nsb / CH;
+      const int pmid = (kpart * CPW + 1) * nsb / CH;   // end of the first chunk (CPW == 2)
       const u32x4* cp[NT];
       const uint2* sp[NT];
 #pragma unroll
@@ -201,19 +212,30 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
           }
         }
       };
+      // the first chunk's sum goes to LDS and the accumulators restart from zero
+      auto chunk_end = [&](int pdone) __attribute__((always_inline)) {
+        if (CPW == 2 && pdone == pmid) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            red[((wave * CPW) * NT + t) * 64 + lane] = acc[t];
+            acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      };
       int p = p0;
       if (p < p1) load(st[0], p);
       while (p < p1) {
         if (p + 1 < p1) load(st[1], p + 1);
         compute(st[0]);
-        if (++p >= p1) break;
+        chunk_end(++p);
+        if (p >= p1) break;
         if (p + 1 < p1) load(st[0], p + 1);
         compute(st[1]);
-        ++p;
+        chunk_end(++p);
       }
     } else {  // FMT_BF16
       const int nks = a.K / 32;
-      const int k0 = kpart * nks / KSPLIT, k1 = (kpart + 1) * nks / KSPLIT;
+      const int k0 = kpart * nks / W, k1 = (kpart + 1) * nks / W;
       const u32x4* wp[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -235,22 +257,35 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
     }
   }
 
-  if (KSPLIT > 1) {
-    const int jl = wave / KSPLIT;
+  if (kRed) {
+    // the wavefront's last chunk stays in registers for kpart 0 and goes to LDS for the others;
+    // kpart 0 then adds the chunks in order: its own first chunk (CPW == 2) + its last, then
+    // every chunk of wavefronts 1 .. W-1
+    const int jl = wave / W;
     if (kpart > 0) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) red[(wave * NT + t) * 64 + lane] = acc[t];
+      for (int t = 0; t < NT; ++t) red[((wave * CPW + CPW - 1) * NT + t) * 64 + lane] = acc[t];
     }
-    __syncthreads();
+    if (W > 1) __syncthreads();
     if (kpart == 0) {
-#pragma unroll
-      for (int kp = 1; kp < KSPLIT; ++kp)
+      if (CPW == 2) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f32x4_t o = red[((jl * KSPLIT + kp) * NT + t) * 64 + lane];
+          const f32x4_t o = red[((wave * CPW) * NT + t) * 64 + lane];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[t][j] += o[j];
+          for (int j = 0; j < 4; ++j) acc[t][j] = o[j] + acc[t][j];
         }
+      }
+#pragma unroll
+      for (int kp = 1; kp < W; ++kp)
+#pragma unroll
+        for (int ci = 0; ci < CPW; ++ci)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const f32x4_t o = red[(((jl * W + kp) * CPW + ci) * NT + t) * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][j] += o[j];
+          }
     }
   }
   if (!job_ok || kpart != 0) return;
@@ -638,42 +673,85 @@ int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16,
 
 
 // ============================================================================ launcher
-// Fewest small-kernel workgroups (over the m-tile bound) for which several jobs per wavefront
-// are used: below it, one job per wavefront keeps more wavefronts streaming.
-constexpr int64_t kSmallMinWgs = 4096;
-template <int FMT, int EPI, int KSPLIT, int JPW>
+// Small-kernel launch shape. The chunk count CH depends on K only (the summation order); the
+// launch picks how many 16-row tiles a wavefront streams (JPW) and how many wavefronts share a
+// job's chunks (W = CH or CH / 2, so CPW = 1 or 2): the most work per wavefront that still
+// leaves kSmallMinWaves wavefronts, else the most wavefronts.
+constexpr int64_t kSmallMinWaves = 5120;
+template <int FMT, int EPI, int W, int CPW, int JPW>
 static void launch_small_k(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
-  constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
+  constexpr int WAVES = W > 4 ? W : 4;
   const int n_jobs = ((EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16) / JPW;
-  const int jobs_per_wg = WAVES / KSPLIT;
+  const int jobs_per_wg = WAVES / W;
   dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mtiles));
-  qmm_small_kernel<FMT, EPI, KSPLIT, JPW><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
+  qmm_small_kernel<FMT, EPI, W, CPW, JPW><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
 }
 
-// Jobs per wavefront: int4 weights take several tiles per wavefront (sharing its activation
-// fragments) when the grid stays large enough to fill the chip; bf16 weights take one.
-template <int FMT, int EPI, int KSPLIT>
-static void launch_small_j(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
-  constexpr int WAVES = KSPLIT > 4 ? KSPLIT : 4;
-  const int jobs = (EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
-  auto wgs = [&](int jpw) { return mtiles * ((jobs / jpw + WAVES / KSPLIT - 1) / (WAVES / KSPLIT)); };
-  // (SwiGLU wavefronts hold two tiles per job: four jobs would exceed the register budget)
-  if (FMT == FMT_INT4 && EPI != EPI_SWIGLU && jobs % 4 == 0 && wgs(4) >= kSmallMinWgs)
-    launch_small_k<FMT, EPI, KSPLIT, (EPI == EPI_SWIGLU) ? 2 : 4>(a, mtiles, stream);
-  else if (FMT == FMT_INT4 && jobs % 2 == 0 && wgs(2) >= kSmallMinWgs)
-    launch_small_k<FMT, EPI, KSPLIT, 2>(a, mtiles, stream);
-  else
-    launch_small_k<FMT, EPI, KSPLIT, 1>(a, mtiles, stream);
+struct SmallShape {
+  int jpw, w, cpw;
+};
+
+// (SwiGLU wavefronts hold two tiles per job: JPW 4 would exceed the register budget)
+static SmallShape pick_small_shape(int fmt, int epi, int ch, int64_t mtiles, int jobs) {
+  if (fmt != FMT_INT4) return SmallShape{1, ch, 1};
+  const int jmax = (epi == EPI_SWIGLU) ? 2 : 4;
+  SmallShape best{1, ch, 1};
+  int64_t best_waves = mtiles * jobs * ch, best_work = 1;
+  bool best_ok = best_waves >= kSmallMinWaves;
+  for (int jpw = 1; jpw <= jmax; jpw *= 2) {
+    if (jobs % jpw) continue;
+    for (int cpw = 1; cpw <= 2 && cpw <= ch; cpw *= 2) {
+      const int w = ch / cpw;
+      const int64_t waves = mtiles * (jobs / jpw) * w;
+      const int64_t work = static_cast<int64_t>(jpw) * cpw;
+      const bool ok = waves >= kSmallMinWaves;
+      const bool better = ok ? (!best_ok || work > best_work || (work == best_work && jpw > best.jpw))
+                             : (!best_ok && waves > best_waves);
+      if (better) {
+        best = SmallShape{jpw, w, cpw};
+        best_waves = waves;
+        best_work = work;
+        best_ok = ok;
+      }
+    }
+  }
+  return best;
+}
+
+template <int FMT, int EPI, int W, int CPW>
+static void launch_small_j(const QmmArgs& a, int jpw, int64_t mtiles, hipStream_t stream) {
+  if constexpr (FMT == FMT_INT4) {
+    if (EPI != EPI_SWIGLU && jpw == 4)
+      launch_small_k<FMT, EPI, W, CPW, (EPI == EPI_SWIGLU) ? 2 : 4>(a, mtiles, stream);
+    else if (jpw == 2)
+      launch_small_k<FMT, EPI, W, CPW, 2>(a, mtiles, stream);
+    else
+      launch_small_k<FMT, EPI, W, CPW, 1>(a, mtiles, stream);
+  } else {
+    launch_small_k<FMT, EPI, W, 1, 1>(a, mtiles, stream);
+  }
 }
 
 template <int FMT, int EPI>
-static void launch_small(const QmmArgs& a, int ksplit, int64_t mtiles, hipStream_t stream) {
-  switch (ksplit) {
-    case 16: launch_small_j<FMT, EPI, 16>(a, mtiles, stream); break;
-    case 8: launch_small_j<FMT, EPI, 8>(a, mtiles, stream); break;
-    case 4: launch_small_j<FMT, EPI, 4>(a, mtiles, stream); break;
-    case 2: launch_small_j<FMT, EPI, 2>(a, mtiles, stream); break;
-    default: launch_small_j<FMT, EPI, 1>(a, mtiles, stream); break;
+static void launch_small(const QmmArgs& a, const SmallShape& sh, int64_t mtiles,
+                         hipStream_t stream) {
+  if constexpr (FMT == FMT_INT4) {
+    if (sh.cpw == 2) {
+      if (sh.w == 2) launch_small_j<FMT, EPI, 2, 2>(a, sh.jpw, mtiles, stream);
+      else launch_small_j<FMT, EPI, 1, 2>(a, sh.jpw, mtiles, stream);
+    } else {
+      if (sh.w == 4) launch_small_j<FMT, EPI, 4, 1>(a, sh.jpw, mtiles, stream);
+      else if (sh.w == 2) launch_small_j<FMT, EPI, 2, 1>(a, sh.jpw, mtiles, stream);
+      else launch_small_j<FMT, EPI, 1, 1>(a, sh.jpw, mtiles, stream);
+    }
+  } else {
+    switch (sh.w) {
+      case 16: launch_small_j<FMT, EPI, 16, 1>(a, sh.jpw, mtiles, stream); break;
+      case 8: launch_small_j<FMT, EPI, 8, 1>(a, sh.jpw, mtiles, stream); break;
+      case 4: launch_small_j<FMT, EPI, 4, 1>(a, sh.jpw, mtiles, stream); break;
+      case 2: launch_small_j<FMT, EPI, 2, 1>(a, sh.jpw, mtiles, stream); break;
+      default: launch_small_j<FMT, EPI, 1, 1>(a, sh.jpw, mtiles, stream); break;
+    }
   }
 }
 
@@ -704,18 +782,22 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     if (fmt == FMT_INT4 && a.K % 128) return fail("qmm: int4 needs K % 128 == 0");
     if (fmt == FMT_BF16 && a.K % 32) return fail("qmm: bf16 needs K % 32 == 0");
     if (a.n_rows % (epi == EPI_SWIGLU ? 32 : 16)) return fail("qmm: weight rows not a tile multiple");
-    // Split-K depends on the shape only (never on the token count), so a row's summation
-    // order, and therefore its result, is the same at every batch size (batch invariance).
-    // int4 wavefronts keep >= 8 superblocks each; bf16 (router, shared expert) wavefronts
-    // keep ~8 32-deep steps, which spreads the few dense row tiles over enough wavefronts.
-    int ksplit;
+    // The chunk count depends on the shape only (never on the token count), so a row's
+    // summation order, and therefore its result, is the same at every batch size (batch
+    // invariance). int4 chunks hold >= 4 superblocks; bf16 (router, shared expert) chunks
+    // ~8 32-deep steps, one wavefront each, which spreads the few dense row tiles over enough
+    // wavefronts.
+    int ch;
     if (fmt == FMT_INT4) {
-      ksplit = (a.K >= 4096) ? 4 : (a.K >= 2048) ? 2 : 1;
+      const int nsb = a.K / 128;
+      ch = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;
     } else {
       const int nks = a.K / 32;
-      ksplit = (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
+      ch = (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
     }
-#define QMOE_SMALL(F, P) launch_small<F, P>(a, ksplit, mtile_bound, stream)
+    const int jobs = (epi == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
+    const SmallShape sh = pick_small_shape(fmt, epi, ch, mtile_bound, jobs);
+#define QMOE_SMALL(F, P) launch_small<F, P>(a, sh, mtile_bound, stream)
     if (fmt == FMT_INT4) {
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT4, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT4, EPI_BF16);

@@ -211,6 +211,20 @@ def test_block_full_size(gpu, name, N):
     assert_close(f64(y)[toks], want, f"{name} N={N} tokens {toks}")
 
 
+@pytest.mark.parametrize("name,N", [("c2", 128), ("c3", 64)])
+def test_batch_invariance_full_size(gpu, name, N):
+    """Large decode batches stream each job's K chunks on fewer wavefronts than single tokens do;
+    the chunk sums are still added in one fixed order, so every token's output is bit-identical
+    to its output when it is the only token of the call."""
+    cfg = synth.spec(name).cfg
+    p = _layer(name, gpu)
+    x = synth.make_inputs(name, N, device=gpu, seed=N)
+    full = qwen35_moe(x[None], p, cfg)[0]
+    for t in (0, N // 3, N - 1):
+        single = qwen35_moe(x[t:t + 1][None], p, cfg)[0, 0]
+        assert torch.equal(single, full[t]), f"{name} token {t} of {N}"
+
+
 def test_prefill_zipf_c4(gpu):
     cfg = synth.spec("c4").cfg
     p = _layer("c4", gpu)
