@@ -1,0 +1,392 @@
+// Device building blocks of the routing stage: the per-token top-k of one wavefront and the
+// stable-permute body of one workgroup (kept apart from their kernels so that any kernel
+// embedding them computes bit-identical ids, weights and permutations).
+//
+// Reference: top-k softmax routing src/quanta/qwen35/moe.py:36-56 (softmax over all experts,
+// top-k, renorm with +1e-20); sigmoid + correction bias, bias-free weights and
+// routed_scaling_factor src/quanta/modeling/moe.py:33-44 and src/quanta/glm/moe.py:44-55; the
+// stable permute order = argsort(exp) (stable), inv = argsort(order)
+// src/quanta/modeling/moe.py:81-85.
+#pragma once
+
+#include <math.h>
+
+#include "qmoe_internal.h"
+#include "../../include/quanta_moe.h"
+
+namespace qmoe {
+
+// Wavefront reductions from ROCm's device library (declared by HIP's own headers only under an
+// opt-in macro); used by the group-limited selection only.
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(
+    unsigned long long);
+
+// ---------------------------------------------------------------- wavefront reductions
+// Butterfly over each 16-lane row with DPP (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror), then the four row results combined in a fixed order. Every
+// step pairs two lanes that combine the same two partial results, so all lanes of a row hold
+// bitwise-identical values and the result is the same on every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Order-preserving map of a float onto uint32 (larger float -> larger integer).
+__device__ __forceinline__ uint32_t orderable(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// Group selection key: value first, then the lower group id wins a tie.
+__device__ __forceinline__ unsigned long long sel_key(float v, int id) {
+  return (static_cast<unsigned long long>(orderable(v)) << 32) |
+         static_cast<unsigned long long>(0xFFFFFFFFu - static_cast<uint32_t>(id));
+}
+__device__ __forceinline__ int key_id(unsigned long long key) {
+  return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key));
+}
+
+struct TopkParams {
+  const float* bias;   // [E] selection-only correction bias (nullable)
+  int E, k, scoring, n_group, topk_group, norm_topk, has_sg;
+  float scale;
+};
+
+// Top-k of one token's logits row, by one wavefront. Lane l holds experts l*VPL .. l*VPL+VPL-1
+// (contiguous, so a group of E/n_group experts spans whole lanes when VPL divides the group
+// size). Selection order is canonical: choice value descending, lower expert id first on
+// ties (the reference's argpartition returns the same set in an unspecified order). Each lane
+// keeps its best remaining candidate (the lowest of its ids among its largest values); a round
+// takes the wavefront max of those values and the lowest lane holding it, which owns the
+// lowest id of that value. Lane r < k returns the r-th expert and its final weight.
+template <int VPL>
+__device__ __forceinline__ void topk_token(const float* __restrict__ row, const TopkParams& P,
+                                           int lane, int& out_id, float& out_w) {
+  const float NEG_INF = -INFINITY;
+  const int E = P.E;
+  const int e_base = lane * VPL;
+  // Branch-free throughout (per-element predicates become selects, loads are clamped in
+  // bounds): the selection is a serial chain on one wavefront, so branches would dominate it.
+  float lg[VPL], sc[VPL], ch[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const float v = row[min(e_base + i, E - 1)];
+    lg[i] = (e_base + i < E) ? v : NEG_INF;
+  }
+  if (P.scoring == QMOE_SCORE_SOFTMAX) {
+    float m = NEG_INF;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) m = fmaxf(m, lg[i]);
+    m = wave_max_f32(m);
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      sc[i] = (e_base + i < E) ? expf(lg[i] - m) : 0.f;
+      z += sc[i];
+    }
+    z = wave_sum_f32(z);
+    const float inv = 1.0f / z;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) sc[i] *= inv;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      sc[i] = (e_base + i < E) ? 1.0f / (1.0f + expf(-lg[i])) : 0.f;
+  }
+  // Without a bias, softmax selection by probability equals selection by logit (monotone); the
+  // logit avoids ties manufactured by rounding exp(). Sigmoid selects on the score.
+  const bool by_logit = (P.scoring == QMOE_SCORE_SOFTMAX);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int e = e_base + i;
+    float c = by_logit ? lg[i] : sc[i];
+    if (P.bias) c = sc[i] + P.bias[min(e, E - 1)];
+    c = (e < E) ? c : NEG_INF;
+    ch[i] = (c != c) ? NEG_INF : c;   // a NaN never outranks a number
+  }
+
+  if (P.n_group > 1) {
+    const int gsize = E / P.n_group;
+    // group score = sum of the group's two largest choice values; gkey holds one selection key
+    // per group (on the lane holding the group's first expert, or on lane gamma in the generic
+    // path), 0 elsewhere
+    unsigned long long gkey = 0ull;
+    if (gsize % VPL == 0) {
+      const int lanes_per_group = gsize / VPL;   // a power of two for power-of-two E, n_group
+      float b1 = NEG_INF, b2 = NEG_INF;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const float v = ch[i];
+        if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) { b2 = v; }
+      }
+      for (int off = 1; off < lanes_per_group; off <<= 1) {
+        const float o1 = __shfl_xor(b1, off), o2 = __shfl_xor(b2, off);
+        const float n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
+        b1 = fmaxf(b1, o1);
+        b2 = n2;
+      }
+      if (e_base < E && e_base % gsize == 0) gkey = sel_key(b1 + b2, e_base / gsize);
+    } else {
+      for (int gam = 0; gam < P.n_group; ++gam) {
+        float b1 = NEG_INF, b2 = NEG_INF;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+          const int e = e_base + i;
+          if (e < E && e / gsize == gam) {
+            const float v = ch[i];
+            if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) { b2 = v; }
+          }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+          const float o1 = __shfl_xor(b1, off), o2 = __shfl_xor(b2, off);
+          const float n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
+          b1 = fmaxf(b1, o1);
+          b2 = n2;
+        }
+        if (lane == gam) gkey = sel_key(b1 + b2, gam);
+      }
+    }
+    unsigned long long keep = 0ull;
+    for (int r = 0; r < P.topk_group; ++r) {
+      const unsigned long long best = __ockl_wfred_max_u64(gkey);
+      keep |= 1ull << key_id(best);
+      if (gkey == best) gkey = 0ull;   // keys are unique (they embed the group id)
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = e_base + i;
+      if (e < E && !((keep >> (e / gsize)) & 1ull)) ch[i] = NEG_INF;
+    }
+  }
+
+  // remaining candidates of this lane (bit i = expert e_base + i) and the lane's best of them
+  uint32_t avail = 0u;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+    if (e_base + i < E) avail |= 1u << i;
+  float hv = NEG_INF, hs = 0.f;
+  int hi = -1;
+  auto head = [&]() __attribute__((always_inline)) {
+    hv = NEG_INF;
+    hi = -1;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const bool take = ((avail >> i) & 1u) & ((hi < 0) | (ch[i] > hv));
+      hv = take ? ch[i] : hv;
+      hs = take ? sc[i] : hs;
+      hi = take ? i : hi;
+    }
+  };
+  head();
+
+  int my_id = 0;
+  float my_w = 0.f;
+  for (int r = 0; r < P.k; ++r) {
+    const bool has = hi >= 0;
+    const float m = wave_max_f32(has ? hv : NEG_INF);
+    unsigned long long win = __ballot(has & (hv == m));
+    win = win ? win : __ballot(has);   // the fallback is unreachable while k <= E
+    const int owner = static_cast<int>(__builtin_ctzll(win));
+    const int id = __builtin_amdgcn_readlane(e_base + hi, owner);
+    const float s_win = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
+    // the owner drops its winner and recomputes its best remaining candidate
+    avail = (lane == owner) ? (avail & ~(1u << (hi & 31))) : avail;
+    head();
+    my_id = (lane == r) ? id : my_id;
+    my_w = (lane == r) ? s_win : my_w;
+  }
+  const float tot = wave_sum_f32(lane < P.k ? my_w : 0.f);
+  if (P.norm_topk) my_w = my_w / (tot + 1e-20f);
+  out_id = my_id;
+  out_w = my_w * P.scale;
+}
+
+// ---------------------------------------------------------------- stable permute body
+// Stable permute of the (token, slot) list by expert: histogram, exclusive scans and scatter in
+// LDS, with the stable rank taken from a per-expert token bitmap, so the result equals a stable
+// argsort without ordered atomics. Stable rank of slot m = t*k + s routed to expert e = the
+// number of earlier slots with the same expert; top-k routing selects distinct experts per
+// token, so that equals the number of tokens t' < t that chose e: popcount of e's token bitmap
+// below bit t. The workgroup owns experts [e0, e1) (their bitmaps in LDS), recomputes the full
+// histogram for the offsets, and scatters only its own experts' slots. Workgroup 0 (is_first)
+// writes counts, offsets, the m-tile prefix and the tile descriptors.
+struct PermuteLds {
+  int* hist;        // [1024]
+  int* offs;        // [1025]
+  int* scan_tmp;    // [40]
+  uint32_t* bits;   // [(e1 - e0) * words_per_expert]
+  uint32_t* pref;   // same size
+};
+
+// Exclusive scan across a 1024-thread workgroup (16 wavefronts of 64).
+__device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) warp_sums[wid] = incl;
+  __syncthreads();
+  if (wid == 0) {
+    int s = (lane < 16) ? warp_sums[lane] : 0;
+    int si = s;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      int o = __shfl_up(si, off);
+      if (lane >= off) si += o;
+    }
+    if (lane < 16) warp_sums[16 + lane] = si - s;   // exclusive prefix of wave totals
+    if (lane == 15) *total = si;
+  }
+  __syncthreads();
+  return warp_sums[16 + wid] + incl - v;
+}
+
+// Optional split tile maps (hybrid regime): experts with more than `split_rows` rows get
+// m-tiles of `m_tile_big` rows in tile_map_big; the others keep m_tile-row tiles in tile_map.
+// Must be called by all 1024 threads of the workgroup.
+__device__ __forceinline__ void permute_body(
+    const int32_t* idx, int N, int k, int E, int m_tile, int e0, int e1, int words_per_expert,
+    bool is_first, const PermuteLds& S, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ tile_off,
+    int32_t* __restrict__ sorted_slot, int32_t* __restrict__ inv, int4* __restrict__ tile_map,
+    int max_tiles, int split_rows, int m_tile_big, int4* __restrict__ tile_map_big,
+    int max_tiles_big) {
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int mc = N * k;
+  const int nbits = (e1 - e0) * words_per_expert;
+  int* hist = S.hist;
+  int* offs = S.offs;
+  int* scan_tmp = S.scan_tmp;
+  uint32_t* bits = S.bits;
+  uint32_t* pref = S.pref;
+
+  for (int i = tid; i < 1024; i += nthr) hist[i] = 0;
+  for (int i = tid; i < nbits; i += nthr) bits[i] = 0u;
+  __syncthreads();
+
+  for (int m = tid; m < mc; m += nthr) {
+    const int e = idx[m];
+    if (e < 0 || e >= E) continue;
+    atomicAdd(&hist[e], 1);
+    if (e >= e0 && e < e1) {
+      const int t = m / k;
+      atomicOr(&bits[(e - e0) * words_per_expert + (t >> 5)], 1u << (t & 31));
+    }
+  }
+  __syncthreads();
+
+  // Offsets (exclusive scan of counts) and the m-tile prefix.
+  const int c = (tid < E) ? hist[tid] : 0;
+  const int ex = block_exclusive_scan(c, scan_tmp, &scan_tmp[39]);
+  const int total = scan_tmp[39];
+  if (tid < E) offs[tid] = ex;
+  if (tid == 0) offs[E] = total;
+  __syncthreads();
+  const int tiles = (c + m_tile - 1) / m_tile;
+  const int tex = block_exclusive_scan(tiles, scan_tmp, &scan_tmp[38]);
+  // hybrid split: small-tile map over the experts at or below split_rows, big-tile map over
+  // the rest (block-uniform condition: tile_map_big is a kernel argument)
+  int s_tiles = tiles, s_ex = tex, s_total = 0, b_tiles = 0, b_ex = 0, b_total = 0;
+  if (tile_map_big) {
+    const bool big = c > split_rows;
+    s_tiles = big ? 0 : tiles;
+    b_tiles = big ? (c + m_tile_big - 1) / m_tile_big : 0;
+    s_ex = block_exclusive_scan(s_tiles, scan_tmp, &scan_tmp[37]);
+    s_total = scan_tmp[37];
+    b_ex = block_exclusive_scan(b_tiles, scan_tmp, &scan_tmp[36]);
+    b_total = scan_tmp[36];
+  }
+  if (is_first) {
+    if (tid < E) {
+      counts[tid] = c;
+      offsets[tid] = ex;
+      tile_off[tid] = tex;
+    }
+    if (tid == 0) {
+      offsets[E] = total;
+      tile_off[E] = scan_tmp[38];
+    }
+    // Per-tile descriptors {expert, first sorted position, rows, 0} for the grouped-qmm grid,
+    // and a -1 sentinel in every unused entry up to max_tiles, so a workgroup resolves its tile
+    // with one 16-byte load.
+    if (tile_map && !tile_map_big) {
+      if (tid < E)
+        for (int i = 0; i < tiles; ++i)
+          tile_map[tex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
+      for (int t = scan_tmp[38] + tid; t < max_tiles; t += nthr) tile_map[t] = make_int4(-1, 0, 0, 0);
+    }
+    if (tile_map_big) {
+      if (tid < E) {
+        for (int i = 0; i < s_tiles; ++i)
+          tile_map[s_ex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
+        for (int i = 0; i < b_tiles; ++i)
+          tile_map_big[b_ex + i] =
+              make_int4(tid, ex + i * m_tile_big, min(m_tile_big, c - i * m_tile_big), 0);
+      }
+      for (int t = s_total + tid; t < max_tiles; t += nthr) tile_map[t] = make_int4(-1, 0, 0, 0);
+      for (int t = b_total + tid; t < max_tiles_big; t += nthr)
+        tile_map_big[t] = make_int4(-1, 0, 0, 0);
+    }
+  }
+
+  // Per-expert exclusive popcount prefix over the token bitmap words.
+  for (int i = tid; i < nbits; i += nthr) pref[i] = __popc(bits[i]);
+  __syncthreads();
+  for (int el = tid; el < e1 - e0; el += nthr) {
+    uint32_t run = 0;
+    uint32_t* p = pref + el * words_per_expert;
+    for (int w = 0; w < words_per_expert; ++w) {
+      const uint32_t v = p[w];
+      p[w] = run;
+      run += v;
+    }
+  }
+  // Own output segment starts as -1 so a malformed idx (duplicate experts within a token)
+  // leaves detectable holes instead of stale data.
+  if (e1 > e0)
+    for (int p = offs[e0] + tid; p < offs[e1]; p += nthr) sorted_slot[p] = -1;
+  __syncthreads();
+
+  for (int m = tid; m < mc; m += nthr) {
+    const int e = idx[m];
+    if (e < 0 || e >= E) {
+      if (is_first) inv[m] = -1;
+      continue;
+    }
+    if (e < e0 || e >= e1) continue;
+    const int t = m / k;
+    const int wi = (e - e0) * words_per_expert + (t >> 5);
+    const uint32_t below = bits[wi] & ((1u << (t & 31)) - 1u);
+    const int pos = offs[e] + static_cast<int>(pref[wi]) + __popc(below);
+    sorted_slot[pos] = m;
+    inv[m] = pos;
+  }
+}
+
+}  // namespace qmoe

@@ -13,6 +13,7 @@
 #include <math.h>
 
 #include "qmoe_internal.h"
+#include "route_common.h"
 #include "../../include/quanta_moe.h"
 
 namespace qmoe {
@@ -55,183 +56,49 @@ int launch_router_f32(const uint16_t* x, const float* wr, const float* shared_ga
   return check_launch("router_f32");
 }
 
-// ---------------------------------------------------------------- top-k in wavefront registers
-// Wavefront reductions from ROCm's device library (declared by HIP's own headers only under an
-// opt-in macro). They return the reduction over all active lanes to every lane.
-extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(
-    unsigned long long);
-extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
-extern "C" __device__ __attribute__((const)) float __ockl_wfred_add_f32(float);
-
-// Order-preserving map of a float onto uint32 (larger float -> larger integer).
-__device__ __forceinline__ uint32_t orderable(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-// Selection key: value first, then the lower id wins a tie.
-__device__ __forceinline__ unsigned long long sel_key(float v, int id) {
-  return (static_cast<unsigned long long>(orderable(v)) << 32) |
-         static_cast<unsigned long long>(0xFFFFFFFFu - static_cast<uint32_t>(id));
-}
-__device__ __forceinline__ int key_id(unsigned long long key) {
-  return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key));
-}
-
-// One wavefront per token. Lane l holds experts l*VPL .. l*VPL+VPL-1 (contiguous, so a group
-// of E/n_group experts spans whole lanes when VPL divides the group size). Each lane keeps the
-// key of its best remaining expert; every round takes one wavefront max-reduction, and only the
-// winning lane rescans its VPL values.
+// ---------------------------------------------------------------- top-k
+// One wavefront per token (topk_token in route_common.h).
 template <int VPL>
-__global__ void __launch_bounds__(256) topk_kernel(
-    const float* __restrict__ logits, int ld, const float* __restrict__ bias, int N, int E, int k,
-    int scoring, int n_group, int topk_group, int norm_topk, float scale, int has_sg,
-    int32_t* __restrict__ idx_out, float* __restrict__ w_out, float* __restrict__ sg_out) {
+__global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ logits, int ld,
+                                                   TopkParams P, int N,
+                                                   int32_t* __restrict__ idx_out,
+                                                   float* __restrict__ w_out,
+                                                   float* __restrict__ sg_out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;  // whole wavefront exits together; no block barriers below
-  const float NEG_INF = -INFINITY;
   const float* row = logits + static_cast<int64_t>(t) * ld;
-  const int e_base = lane * VPL;
+  int id;
+  float w;
+  topk_token<VPL>(row, P, lane, id, w);
+  if (lane < P.k) {
+    idx_out[static_cast<int64_t>(t) * P.k + lane] = id;
+    w_out[static_cast<int64_t>(t) * P.k + lane] = w;
+  }
+  if (P.has_sg && lane == 0) sg_out[t] = 1.0f / (1.0f + expf(-row[P.E]));
+}
 
-  float lg[VPL], sc[VPL], ch[VPL];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) lg[i] = (e_base + i < E) ? row[e_base + i] : NEG_INF;
-  if (scoring == QMOE_SCORE_SOFTMAX) {
-    float m = NEG_INF;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) m = fmaxf(m, lg[i]);
-    m = __ockl_wfred_max_f32(m);
-    float z = 0.f;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      sc[i] = (e_base + i < E) ? expf(lg[i] - m) : 0.f;
-      z += sc[i];
-    }
-    z = __ockl_wfred_add_f32(z);
-    const float inv = 1.0f / z;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) sc[i] *= inv;
-  } else {
-#pragma unroll
-    for (int i = 0; i < VPL; ++i)
-      sc[i] = (e_base + i < E) ? 1.0f / (1.0f + expf(-lg[i])) : 0.f;
-  }
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int e = e_base + i;
-    if (e >= E) {
-      ch[i] = NEG_INF;
-    } else if (bias) {
-      ch[i] = sc[i] + bias[e];
-    } else {
-      // Without a bias, softmax selection by probability equals selection by logit (monotone);
-      // the logit avoids ties manufactured by rounding exp(). Sigmoid selects on the score.
-      ch[i] = (scoring == QMOE_SCORE_SOFTMAX) ? lg[i] : sc[i];
-    }
-  }
-
-  if (n_group > 1) {
-    const int gsize = E / n_group;
-    // group score = sum of the group's two largest choice values; gkey holds one selection key
-    // per group (on the lane holding the group's first expert, or on lane gamma in the generic
-    // path), 0 elsewhere
-    unsigned long long gkey = 0ull;
-    if (gsize % VPL == 0) {
-      const int lanes_per_group = gsize / VPL;   // a power of two for power-of-two E, n_group
-      float b1 = NEG_INF, b2 = NEG_INF;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const float v = ch[i];
-        if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) { b2 = v; }
-      }
-      for (int off = 1; off < lanes_per_group; off <<= 1) {
-        const float o1 = __shfl_xor(b1, off), o2 = __shfl_xor(b2, off);
-        const float n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
-        b1 = fmaxf(b1, o1);
-        b2 = n2;
-      }
-      if (e_base < E && e_base % gsize == 0) gkey = sel_key(b1 + b2, e_base / gsize);
-    } else {
-      for (int gam = 0; gam < n_group; ++gam) {
-        float b1 = NEG_INF, b2 = NEG_INF;
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-          const int e = e_base + i;
-          if (e < E && e / gsize == gam) {
-            const float v = ch[i];
-            if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) { b2 = v; }
-          }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-          const float o1 = __shfl_xor(b1, off), o2 = __shfl_xor(b2, off);
-          const float n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
-          b1 = fmaxf(b1, o1);
-          b2 = n2;
-        }
-        if (lane == gam) gkey = sel_key(b1 + b2, gam);
-      }
-    }
-    unsigned long long keep = 0ull;
-    for (int r = 0; r < topk_group; ++r) {
-      const unsigned long long best = __ockl_wfred_max_u64(gkey);
-      keep |= 1ull << key_id(best);
-      if (gkey == best) gkey = 0ull;   // keys are unique (they embed the group id)
-    }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int e = e_base + i;
-      if (e < E && !((keep >> (e / gsize)) & 1ull)) ch[i] = NEG_INF;
-    }
-  }
-
-  // lane's best remaining candidate
-  unsigned long long keys[VPL];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) keys[i] = (e_base + i < E) ? sel_key(ch[i], e_base + i) : 0ull;
-  unsigned long long mine = 0ull;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) mine = keys[i] > mine ? keys[i] : mine;
-
-  int my_id = 0;
-  float my_w = 0.f;
-  for (int r = 0; r < k; ++r) {
-    const unsigned long long best = __ockl_wfred_max_u64(mine);
-    const int id = key_id(best);
-    const int owner = id / VPL;
-    float s_win = 0.f;
-    if (lane == owner) {
-      unsigned long long nb = 0ull;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        if (e_base + i == id) {
-          s_win = sc[i];
-          keys[i] = 0ull;
-        }
-        nb = keys[i] > nb ? keys[i] : nb;
-      }
-      mine = nb;
-    }
-    s_win = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s_win), owner));
-    if (lane == r) { my_id = id; my_w = s_win; }
-  }
-  const float tot = __ockl_wfred_add_f32(lane < k ? my_w : 0.f);
-  if (norm_topk) my_w = my_w / (tot + 1e-20f);
-  my_w *= scale;
-  if (lane < k) {
-    idx_out[static_cast<int64_t>(t) * k + lane] = my_id;
-    w_out[static_cast<int64_t>(t) * k + lane] = my_w;
-  }
-  if (has_sg && lane == 0) sg_out[t] = 1.0f / (1.0f + expf(-row[E]));
+static TopkParams topk_params(const float* bias, int E, int k, int scoring, int n_group,
+                              int topk_group, int norm_topk, float scale, int has_sg) {
+  TopkParams P;
+  P.bias = bias;
+  P.E = E;
+  P.k = k;
+  P.scoring = scoring;
+  P.n_group = n_group;
+  P.topk_group = topk_group;
+  P.norm_topk = norm_topk;
+  P.has_sg = has_sg;
+  P.scale = scale;
+  return P;
 }
 
 int launch_topk(const float* logits, int ld, const float* bias, int N, int E, int k, int scoring,
                 int n_group, int topk_group, int norm_topk, float scale, int has_sg,
                 int32_t* idx, float* w, float* sg_out, hipStream_t stream) {
+  const TopkParams P = topk_params(bias, E, k, scoring, n_group, topk_group, norm_topk, scale, has_sg);
   dim3 grid((N + 3) / 4);
-#define QMOE_TOPK(V)                                                                         \
-  topk_kernel<V><<<grid, 256, 0, stream>>>(logits, ld, bias, N, E, k, scoring, n_group,       \
-                                           topk_group, norm_topk, scale, has_sg, idx, w, sg_out)
+#define QMOE_TOPK(V) topk_kernel<V><<<grid, 256, 0, stream>>>(logits, ld, P, N, idx, w, sg_out)
   if (E <= 64) QMOE_TOPK(1);
   else if (E <= 128) QMOE_TOPK(2);
   else if (E <= 256) QMOE_TOPK(4);
