@@ -98,15 +98,20 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int topk_group);
 
 // ------------------------------------------------------------------ auxiliary stream
-// The shared expert depends only on x, so qmoe_forward runs it on a library-owned stream
-// (created once per device, default priority) concurrently with the router -> top-k ->
-// permute -> routed chain: a fork event records the caller's stream at entry and the caller's
-// stream waits on a join event right before the combine. The mutex is held from the fork record
-// until the join wait is enqueued, so concurrent calls on different streams cannot exchange
-// the events.
+// qmoe_forward runs independent work on a library-owned stream (created once per device,
+// default priority) concurrently with the caller's stream:
+//  * the shared expert, which depends only on x, beside the router -> top-k -> permute ->
+//    routed chain;
+//  * in the hybrid large-M regime, the cold experts' grouped matmuls (small kernel, bound by
+//    HBM) beside the hot experts' (large kernel, bound by MFMA).
+// A fork event records the caller's stream at entry, `perm` publishes the permute to the
+// auxiliary stream, `cold` returns the cold gate_up (h complete), `hready` publishes the fp16
+// copy of h, and the caller's stream waits on `join` right before the combine. The mutex is held
+// from the fork record until the join wait is enqueued, so concurrent calls on different streams
+// cannot exchange the events.
 struct AuxStream {
   hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr, perm = nullptr, cold = nullptr, hready = nullptr;
 };
 static std::mutex g_aux_mu;
 constexpr int64_t kAuxMinTokens = 8;
@@ -124,6 +129,9 @@ static int aux_stream(hipStream_t caller, AuxStream** out) {
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&a.s, hipStreamNonBlocking);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&a.fork, hipEventDisableTiming);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&a.join, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&a.perm, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&a.cold, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&a.hready, hipEventDisableTiming);
     if (cur != dev) (void)hipSetDevice(cur);
     if (err != hipSuccess) {
       a = AuxStream{};
@@ -353,19 +361,25 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4 : FMT_BF16;
   const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
 
-  // fork the shared expert onto the auxiliary stream (held until its join is enqueued below)
+  // fork onto the auxiliary stream (held until its join is enqueued below): the shared expert
   // (below kAuxMinTokens the cross-stream synchronisation costs more than the overlap saves)
+  // and, in the hybrid regime, the cold experts' grouped matmuls
   std::unique_lock<std::mutex> aux_lock;
   AuxStream* aux = nullptr;
   hipStream_t sstream = stream;
-  if (c.shared_inter > 0 && N >= kAuxMinTokens) {
+  const bool shared_aux = c.shared_inter > 0 && N >= kAuxMinTokens;
+  auto link = [&](hipEvent_t ev, hipStream_t from, hipStream_t to, const char* what) {
+    hipError_t err = hipEventRecord(ev, from);
+    if (err == hipSuccess) err = hipStreamWaitEvent(to, ev, 0);
+    return err == hipSuccess ? 0 : fail(std::string("forward: ") + what + ": " + hipGetErrorString(err));
+  };
+  if (shared_aux || hybrid) {
     aux_lock = std::unique_lock<std::mutex>(g_aux_mu);
     rc = aux_stream(stream, &aux);
     if (rc) return rc;
-    hipError_t err = hipEventRecord(aux->fork, stream);
-    if (err == hipSuccess) err = hipStreamWaitEvent(aux->s, aux->fork, 0);
-    if (err != hipSuccess) return fail(std::string("forward: fork: ") + hipGetErrorString(err));
-    sstream = aux->s;
+    rc = link(aux->fork, stream, aux->s, "fork");
+    if (rc) return rc;
+    if (shared_aux) sstream = aux->s;
   }
 
   // 1. shared expert (gate_up + SwiGLU, then down) on the auxiliary stream
@@ -384,10 +398,6 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     b.ld_out = c.hidden;
     rc = launch_qmm(b, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, sstream);
     if (rc) return rc;
-    if (aux) {
-      const hipError_t err = hipEventRecord(aux->join, aux->s);
-      if (err != hipSuccess) return fail(std::string("forward: join record: ") + hipGetErrorString(err));
-    }
   }
 
   // 2. router logits (+ the shared-expert gate logit in column E)
@@ -417,11 +427,19 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
                       hybrid ? tile_map_big : nullptr, L.max_tiles_big);
   if (rc) return rc;
   const bool f16_acts = (hybrid && wfmt == FMT_INT4);
+  // the cold experts' tiles wait for the permute on the auxiliary stream
+  hipStream_t cstream = stream;
+  if (hybrid) {
+    rc = link(aux->perm, stream, aux->s, "permute to auxiliary stream");
+    if (rc) return rc;
+    cstream = aux->s;
+  }
   // routed grouped matmul over the permuted rows: small kernel over the (cold) 16-row tiles,
-  // large kernel over the hot experts' tiles
+  // large kernel over the hot experts' tiles (hybrid: the two on different streams; hot and
+  // cold experts own disjoint rows of the output)
   auto routed = [&](QmmArgs a, int epi, const uint16_t* act16, const float* sinv) {
     a.tile_map = reinterpret_cast<const int4*>(tile_map);
-    int r = launch_qmm(a, wfmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : bound_small, stream);
+    int r = launch_qmm(a, wfmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : bound_small, cstream);
     if (r || !hybrid) return r;
     a.tile_map = reinterpret_cast<const int4*>(tile_map_big);
     a.act16 = act16;
@@ -441,6 +459,10 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     }
     rc = routed(a, EPI_SWIGLU, x16, x_sinv);
     if (rc) return rc;
+    if (hybrid) {   // h complete (cold rows from the auxiliary stream) before its fp16 copy
+      rc = link(aux->cold, aux->s, stream, "cold gate_up");
+      if (rc) return rc;
+    }
   }
   // 6. routed down -> d (sorted order)
   {
@@ -453,12 +475,16 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
       rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);
       if (rc) return rc;
     }
+    if (hybrid) {   // the cold down reads bf16 h, complete since the cold gate_up join
+      rc = link(aux->hready, stream, aux->s, "h to auxiliary stream");
+      if (rc) return rc;
+    }
     rc = routed(a, EPI_BF16, h16, h_sinv);
     if (rc) return rc;
   }
   if (aux) {
-    const hipError_t err = hipStreamWaitEvent(stream, aux->join, 0);
-    if (err != hipSuccess) return fail(std::string("forward: join wait: ") + hipGetErrorString(err));
+    rc = link(aux->join, aux->s, stream, "join");
+    if (rc) return rc;
   }
   // 7. unpermute + weighted combine + gated shared + bf16
   return launch_combine(d, inv, wv, n, c.top_k, c.hidden, c.shared_inter > 0 ? sh_out : nullptr,
