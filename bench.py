@@ -14,6 +14,16 @@ Printed (one JSON line): whole-layer tokens/s (`value`), per-step time, the domi
 roofline (routed gate_up+SwiGLU: algorithmic bytes per launch / its average duration, HIP events
 on the launch stream), a sweep over the other decode batches and the 4096-token prefill, and the
 CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host cores, bounded sample).
+
+`roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
+profiles/hbm_traffic.json, written from two rocprofv3 counter passes over `--only kernel` runs:
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d F -o pmc -- python bench.py --only kernel
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d W -o pmc -- python bench.py --only kernel
+    python bench.py --write-traffic F W
+
+Each counter is scaled by what it reads for the 2 GiB device copy of the same run (the copy's
+known read and write bytes divided by its counter values).
 """
 
 from __future__ import annotations
@@ -47,7 +57,65 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
+    ap.add_argument("--write-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 counter runs into profiles/hbm_traffic.json")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+COPY_BYTES = 2 << 30          # the 2 GiB device copy of the `--only kernel` run
+
+
+def kernel_key(workload, regime_small):
+    """Counter-CSV kernel name prefix of the routed gate_up+SwiGLU launch."""
+    return "qmm_small_kernel<0, 0," if regime_small else "qmm_large_kernel<0, 0>"
+
+
+def write_traffic(fetch_dir, write_dir, workload="c2-decode-N32", regime_small=True):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant kernel, scaled by the copy."""
+    import csv
+    import glob
+
+    def read(d, counter):
+        f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not f:
+            sys.exit(f"bench.py: no counter_collection.csv under {d}")
+        kern, copy, name = [], [], None
+        for r in csv.DictReader(open(f[0])):
+            if r.get("Counter_Name") != counter:
+                continue
+            v = float(r["Counter_Value"])
+            if "copyBuffer" in r["Kernel_Name"]:
+                copy.append(v)
+            elif kernel_key(workload, regime_small) in r["Kernel_Name"]:
+                kern.append(v)
+                name = r["Kernel_Name"]
+        if not kern or not copy:
+            sys.exit(f"bench.py: {counter}: kernel or copy dispatches missing in {d}")
+        return sum(kern) / len(kern), max(copy), name, len(kern)
+
+    fk, fcopy, name, n1 = read(fetch_dir, "FETCH_SIZE")
+    wk, wcopy, _, n2 = read(write_dir, "WRITE_SIZE")
+    fs, ws = COPY_BYTES / 1024 / fcopy, COPY_BYTES / 1024 / wcopy
+    rec = dict(workload=workload, kernel=name, dispatches=[n1, n2], fetch_kib=round(fk, 1),
+               write_kib=round(wk, 1), copy_fetch_kib=round(fcopy, 1), copy_write_kib=round(wcopy, 1),
+               fetch_scale=round(fs, 4), write_scale=round(ws, 4),
+               traffic_bytes=int(round((fk * fs + wk * ws) * 1024)))
+    data = {}
+    if os.path.exists(TRAFFIC_FILE):
+        data = json.load(open(TRAFFIC_FILE))
+    data[workload] = rec
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(data, f, indent=1)
+        f.write("\n")
+    print(json.dumps(rec))
+
+
+def measured_traffic(workload):
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    rec = json.load(open(TRAFFIC_FILE)).get(workload)
+    return rec["traffic_bytes"] if rec else None
 
 
 def log(msg):
@@ -56,6 +124,9 @@ def log(msg):
 
 def main():
     args = parse()
+    if args.write_traffic:
+        write_traffic(*args.write_traffic)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
               f"--gpus {args.gpus} is not supported. Multi-GPU sharding is a design note "
@@ -248,6 +319,9 @@ def main():
                           f"(torch-CPU fp32 port, oracle/torch_cpu.py), {dt:.1f}s")
         log(f"cpu baseline: {cpu}")
 
+    workload = (("c4-prefill-zipf" if args.zipf else
+                 f"{args.config}-decode" if N <= 256 else f"{args.config}-prefill") + f"-N{N}")
+    traffic = measured_traffic(workload)
     roofline = None
     if kern is not None:
         if kern["mfma"]:
@@ -260,7 +334,7 @@ def main():
         else:
             achieved = kern["bytes"] / (kern["us"] * 1e-6) / 1e9
             roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
-                            frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
+                            frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=traffic,
                             kernel=kern["name"], kernel_us=round(kern["us"], 2),
                             bytes_per_launch=int(kern["bytes"]), distinct_experts=round(kern["U"], 1))
     line = {
@@ -276,8 +350,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": ("c4-prefill-zipf" if args.zipf else
-                                f"{args.config}-decode" if N <= 256 else f"{args.config}-prefill") + f"-N{N}",
+        "config": {"workload": workload,
                    "hidden": H, "experts": E, "top_k": k, "inter": I, "shared_inter": Is,
                    "batch_tokens": N, "weights": "int4-g64 affine, bf16 scale/bias",
                    "layer_copies": args.layers, "input_pool": args.pool},

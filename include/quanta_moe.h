@@ -16,8 +16,11 @@
  *  - Return value: QMOE_OK (0), QMOE_EINVAL (-1, bad argument, nothing enqueued) or
  *    QMOE_EHIP (-2, HIP launch error). qmoe_last_error() holds a thread-local message.
  *  - bf16 tensors are passed as uint16_t bit patterns, packed int4 codes as uint32 words.
- *  - No global mutable state besides the thread-local error string: calls on different
- *    streams are independent; calls sharing workspace must be ordered by the caller.
+ *  - Calls on different streams are independent; calls sharing workspace must be ordered by
+ *    the caller. Library state: the thread-local error string, and for qmoe_forward one
+ *    auxiliary stream per device (default priority, created with its events on first use)
+ *    that runs independent parts of the block concurrently, forked from and joined back into
+ *    `stream` with events; a mutex serialises the enqueue of concurrent calls.
  */
 #ifndef QUANTA_MOE_H_
 #define QUANTA_MOE_H_
@@ -50,7 +53,8 @@ extern "C" {
 /* grouped-qmm regimes */
 #define QMOE_REGIME_AUTO 0
 #define QMOE_REGIME_SMALL 1 /* 16-token m-tiles, weights streamed to registers (decode) */
-#define QMOE_REGIME_LARGE 2 /* 128x256 tiles, register-dequantised fp16 weights (prefill) */
+#define QMOE_REGIME_LARGE 2 /* prefill: experts of > 32 rows on 128x256 LDS-staged fp16 tiles,
+                               the others on 16-token m-tiles */
 
 /* grouped-qmm epilogues */
 #define QMOE_EPI_SWIGLU 0 /* out[:, j] = bf16(silu(bf16(gate_j)) * bf16(up_j)), rows = [gate; up] */
