@@ -410,9 +410,13 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   } else {
     ld = c.router_rows;
     QmmArgs a{};
-    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
-    a.K = c.hidden; a.n_rows = c.router_rows; a.codes = wts->router_w; a.out = logits; a.ld_out = ld;
     const int rreg = dense_regime(c, N);
+    // the decode kernel stops at the 16-row tile holding logit E (the rows up to router_rows
+    // are padding for the large kernel's 256-row tiles)
+    const int live_rows = (c.n_experts + has_sg + 15) / 16 * 16;
+    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
+    a.K = c.hidden; a.n_rows = (rreg == QMOE_REGIME_SMALL) ? std::min(live_rows, c.router_rows) : c.router_rows;
+    a.codes = wts->router_w; a.out = logits; a.ld_out = ld;
     const int rt = (rreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
     rc = launch_qmm(a, FMT_BF16, EPI_F32, rreg, (N + rt - 1) / rt, stream);
   }

@@ -53,6 +53,24 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+// Same butterfly on unsigned integers (0 is max's identity, so the DPP moves fold into the
+// max instructions).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u<0xB1>(v));
+  v = max(v, dpp_u<0x4E>(v));
+  v = max(v, dpp_u<0x141>(v));
+  v = max(v, dpp_u<0x140>(v));
+  const uint32_t r0 = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t r1 = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t r3 = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
 // Order-preserving map of a float onto uint32 (larger float -> larger integer).
 __device__ __forceinline__ uint32_t orderable(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -79,7 +97,9 @@ struct TopkParams {
 // ties (the reference's argpartition returns the same set in an unspecified order). Each lane
 // keeps its best remaining candidate (the lowest of its ids among its largest values); a round
 // takes the wavefront max of those values and the lowest lane holding it, which owns the
-// lowest id of that value. Lane r < k returns the r-th expert and its final weight.
+// lowest id of that value (a lane's candidates are taken in id order, and only a strictly
+// larger value replaces the current best). Lane r < k returns the r-th expert and its final
+// weight.
 template <int VPL>
 __device__ __forceinline__ void topk_token(const float* __restrict__ row, const TopkParams& P,
                                            int lane, int& out_id, float& out_w) {
@@ -181,20 +201,26 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
     }
   }
 
+  // Selection runs on order-preserving integer keys of the choice values (-0 folded into +0,
+  // which compare equal); every real key is above 0, the "no candidate" value.
+  uint32_t key[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) key[i] = orderable(ch[i] + 0.0f);
   // remaining candidates of this lane (bit i = expert e_base + i) and the lane's best of them
   uint32_t avail = 0u;
 #pragma unroll
   for (int i = 0; i < VPL; ++i)
     if (e_base + i < E) avail |= 1u << i;
-  float hv = NEG_INF, hs = 0.f;
+  uint32_t hk = 0u;
+  float hs = 0.f;
   int hi = -1;
   auto head = [&]() __attribute__((always_inline)) {
-    hv = NEG_INF;
+    hk = 0u;
     hi = -1;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const bool take = ((avail >> i) & 1u) & ((hi < 0) | (ch[i] > hv));
-      hv = take ? ch[i] : hv;
+      const bool take = ((avail >> i) & 1u) & (key[i] > hk);
+      hk = take ? key[i] : hk;
       hs = take ? sc[i] : hs;
       hi = take ? i : hi;
     }
@@ -204,10 +230,9 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
   int my_id = 0;
   float my_w = 0.f;
   for (int r = 0; r < P.k; ++r) {
-    const bool has = hi >= 0;
-    const float m = wave_max_f32(has ? hv : NEG_INF);
-    unsigned long long win = __ballot(has & (hv == m));
-    win = win ? win : __ballot(has);   // the fallback is unreachable while k <= E
+    const uint32_t m = wave_max_u32(hk);
+    unsigned long long win = __ballot((hi >= 0) & (hk == m));
+    win = win ? win : __ballot(hi >= 0);   // the fallback is unreachable while k <= E
     const int owner = static_cast<int>(__builtin_ctzll(win));
     const int id = __builtin_amdgcn_readlane(e_base + hi, owner);
     const float s_win = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
