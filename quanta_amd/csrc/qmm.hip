@@ -110,6 +110,7 @@ struct SmallStage {
 
 template <int FMT, int EPI, int W, int CPW, int JPW>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
+__attribute__((amdgpu_waves_per_eu((FMT == FMT_INT4 && ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW >= 4) ? 3 : 1)))
 qmm_small_kernel(QmmArgs a, int n_jobs) {
   constexpr int WAVES = W > 4 ? W : 4;
   constexpr int JOBS_PER_WG = WAVES / W;
@@ -120,7 +121,8 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
   constexpr bool kRed = CH > 1;
   __shared__ f32x4_t red[kRed ? WAVES * CPW * NT * 64 : 1];
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave index as a scalar, so per-wavefront quantities (job, k-range) stay in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   int e, m0, m_cnt;
   if (!resolve_mtile(a, blockIdx.y, kSmallMTile, e, m0, m_cnt)) return;
 
@@ -132,7 +134,11 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
   int64_t arow = -1;
   if (mrow < m_cnt) arow = act_row(a, m0 + mrow);
   const bool row_ok = arow >= 0;
+  // Rows past the segment and rows whose slot is invalid read activation row 0, so every load
+  // is unconditional (a load under a branch makes the compiler wait for all loads in flight);
+  // the former are never stored, the latter are stored as zeros.
   const uint16_t* xrow = a.act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
+  const uint32_t rows_ok = static_cast<uint32_t>(__ballot(row_ok)) & 0xFFFFu;   // lanes 0-15
 
   f32x4_t acc[NT];
 #pragma unroll
@@ -154,14 +160,18 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
       // chunk c = superblocks [c * nsb / CH, (c + 1) * nsb / CH); this wavefront: CPW chunks
       const int p0 = kpart * CPW * nsb / CH, p1 = (kpart + 1) * CPW * nsb / CH;
       const int pmid = (kpart * CPW + 1) * nsb / CH;   // end of the first chunk (CPW == 2)
-      const u32x4* cp[NT];
-      const uint2* sp[NT];
+      // tile bases are wave-uniform (scalar registers); every stream adds one shared per-lane
+      // offset, so the loads use scalar-base + 32-bit vector-offset addressing
+      const char* cb[NT];
+      const char* sbb[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int64_t tb = (static_cast<int64_t>(e) * tiles_per_expert + tile[t]) * nsb;
-        cp[t] = static_cast<const u32x4*>(a.codes) + tb * 64 + lane;
-        sp[t] = reinterpret_cast<const uint2*>(a.sb) + tb * 16 + (lane & 15);
+        cb[t] = static_cast<const char*>(a.codes) + tb * 1024;
+        sbb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       }
+      const uint32_t lane_c = static_cast<uint32_t>(lane) * 16u;
+      const uint32_t lane_s = static_cast<uint32_t>(lane & 15) * 8u;
       const u32x4* xp = reinterpret_cast<const u32x4*>(xrow) + 2 * lg;   // 16 lg bf16
       bf16x8_t ones;
       {
@@ -176,20 +186,17 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
         for (int t = 0; t < NT; ++t) {
           // weights are streamed once per call: nontemporal loads keep them out of the way of
           // the activations that every job of the m-tile re-reads
-          s.q[t] = __builtin_nontemporal_load(cp[t] + p * 64);
-          const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(sp[t] + p * 16));
+          s.q[t] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(cb[t] + static_cast<int64_t>(p) * 1024 + lane_c));
+          const u32x2 v = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x2*>(sbb[t] + static_cast<int64_t>(p) * 128 + lane_s));
           s.sb[t] = uint2{v.x, v.y};
         }
-        // group 2p: k 16lg + 0..7 (step 0) and + 8..15 (step 1); group 2p+1 likewise, +64.
-        // Only rows of the segment load; the rest of the 16-row tile is zeros.
-        if (row_ok) {
-          s.x[0] = xp[p * 16 + 0];
-          s.x[1] = xp[p * 16 + 1];
-          s.x[2] = xp[p * 16 + 8];
-          s.x[3] = xp[p * 16 + 9];
-        } else {
-          s.x[0] = s.x[1] = s.x[2] = s.x[3] = u32x4{0u, 0u, 0u, 0u};
-        }
+        // group 2p: k 16lg + 0..7 (step 0) and + 8..15 (step 1); group 2p+1 likewise, +64
+        s.x[0] = xp[p * 16 + 0];
+        s.x[1] = xp[p * 16 + 1];
+        s.x[2] = xp[p * 16 + 8];
+        s.x[3] = xp[p * 16 + 9];
       };
       auto compute = [&](const SmallStage<NT>& s) __attribute__((always_inline)) {
 #pragma unroll
@@ -222,16 +229,33 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
           }
         }
       };
+      // Steady state: two superblocks per iteration with every load unconditional, so the
+      // compiler waits only for the stage about to be computed; then a one- or two-superblock
+      // tail (p1 - p0 >= 1).
+      // (the scheduling barriers keep each stage's loads issued before the MFMAs that wait for
+      // the previous stage)
       int p = p0;
-      if (p < p1) load(st[0], p);
-      while (p < p1) {
-        if (p + 1 < p1) load(st[1], p + 1);
+      load(st[0], p);
+      for (; p + 2 < p1; p += 2) {
+        load(st[1], p + 1);
+        __builtin_amdgcn_sched_barrier(0);
         compute(st[0]);
-        chunk_end(++p);
-        if (p >= p1) break;
-        if (p + 1 < p1) load(st[0], p + 1);
+        chunk_end(p + 1);
+        load(st[0], p + 2);
+        __builtin_amdgcn_sched_barrier(0);
         compute(st[1]);
-        chunk_end(++p);
+        chunk_end(p + 2);
+      }
+      if (p + 1 < p1) {
+        load(st[1], p + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(st[0]);
+        chunk_end(p + 1);
+        compute(st[1]);
+        chunk_end(p + 2);
+      } else {
+        compute(st[0]);
+        chunk_end(p + 1);
       }
     } else {  // FMT_BF16
       const int nks = a.K / 32;
@@ -248,9 +272,7 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
         u32x4 wv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) wv[t] = wp[t][c * 64];
-        u32x4 xv = u32x4{0u, 0u, 0u, 0u};
-        if (row_ok) xv = xp[c * 4];
-        const bf16x8_t A = as_bf16x8(xv);
+        const bf16x8_t A = as_bf16x8(xp[c * 4]);
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = mfma16(A, as_bf16x8(wv[t]), acc[t]);
       }
@@ -296,8 +318,10 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int mr = 4 * lg + j;
+      const bool ok = (rows_ok >> mr) & 1u;
       if (mr < m_cnt)
-        store_out<EPI>(a, m0 + mr, col, acc[jp][j], acc[(EPI == EPI_SWIGLU) ? JPW + jp : jp][j]);
+        store_out<EPI>(a, m0 + mr, col, ok ? acc[jp][j] : 0.f,
+                       ok ? acc[(EPI == EPI_SWIGLU) ? JPW + jp : jp][j] : 0.f);
     }
   }
 }
