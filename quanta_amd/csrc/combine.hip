@@ -95,15 +95,103 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
   return check_launch("combine");
 }
 
+// ------------------------------------------------------------------ combine + shared down
+// Decode form of the combine with the shared expert's down projection fused in. A workgroup
+// owns 16 output features f and a block of up to kCsTokens tokens:
+//   sh[t, f] = bf16(sh_h[t] . Wd[f])                      (the reference's bf16 matmul output)
+//   y[t, f]  = bf16(sum_s w[t,s] * f32(d[inv[t,s], f]) + g[t] * f32(sh[t, f]))
+// sh is computed on v_mfma_f32_16x16x32_bf16 (16 tokens x 16 features per m-tile) with K cut
+// into the same chunks as the standalone small-regime bf16 product (bf16_chunks, one wavefront
+// each, summed from zero and added in chunk order; the other wavefronts add exact zeros), so
+// the result is bit-identical to the unfused shared down and independent of the other tokens.
+// Wd is the tiled bf16 [H/16][Is/32][64][8].
+constexpr int kCsWaves = 8;
+constexpr int kCsTokens = 16;   // tokens per workgroup (one m-tile)
+__global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
+    const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
+    int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ sh_h, int Is, int nch,
+    const u32x4* __restrict__ wd, const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
+  __shared__ f32x4_t part[kCsWaves][64];
+  __shared__ float sh[16][17];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int fb = blockIdx.x;
+  const int t_begin = blockIdx.y * kCsTokens;
+  const int t_end = min(N, t_begin + kCsTokens);
+  const int nks = Is / 32;
+  const int c0 = (wave < nch) ? wave * nks / nch : 0, c1 = (wave < nch) ? (wave + 1) * nks / nch : 0;
+  const u32x4* wp = wd + static_cast<int64_t>(fb) * nks * 64 + lane;
+  const int f = threadIdx.x & 15, tl = threadIdx.x >> 4;   // combine phase: (token, feature)
+  const int col = fb * 16 + f;
+  for (int tm = t_begin; tm < t_end; tm += 16) {
+    // shared down for tokens tm .. tm+15 (rows past N read token tm: computed, never used)
+    const int tr = tm + (lane & 15);
+    const uint16_t* xr = sh_h + static_cast<int64_t>(tr < N ? tr : tm) * Is + 8 * (lane >> 4);
+    f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+    for (int c = c0; c < c1; ++c) {
+      const u32x4 wv = wp[c * 64];
+      const u32x4 xv = *reinterpret_cast<const u32x4*>(xr + 32 * c);
+      acc = mfma16(as_bf16x8(xv), as_bf16x8(wv), acc);
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      f32x4_t s4 = part[0][lane];
+#pragma unroll
+      for (int q = 1; q < kCsWaves; ++q) {
+        const f32x4_t o = part[q][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s4[j] += o[j];
+      }
+      // lane holds tokens 4*(lane/16) + j, feature lane%16
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sh[4 * (lane >> 4) + j][lane & 15] = bf16_to_f32(f32_to_bf16(s4[j]));
+    }
+    __syncthreads();
+    // weighted combine of the routed slots (slot order) + gated shared, for 16 x 16 outputs
+    if (tl < 16) {
+      const int t = tm + tl;
+      if (t < N) {
+        float acc1 = 0.f;
+        const int64_t m0 = static_cast<int64_t>(t) * k;
+        for (int s0 = 0; s0 < k; ++s0) {
+          const int pos = inv[m0 + s0];
+          if (pos >= 0 && pos < n_pos)
+            acc1 = fmaf(bf16_to_f32(d[static_cast<int64_t>(pos) * H + col]), w[m0 + s0], acc1);
+        }
+        const float g = shared_gate ? shared_gate[t] : 1.0f;
+        acc1 = fmaf(sh[tl][f], g, acc1);
+        y[static_cast<int64_t>(t) * H + col] = f32_to_bf16(acc1);
+      }
+    }
+    // part / sh are rewritten by the next m-tile only after every thread has read them
+    __syncthreads();
+  }
+}
+
+int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
+                          int H, const uint16_t* sh_h, int Is, const uint16_t* wd,
+                          const float* shared_gate, uint16_t* y, hipStream_t stream) {
+  const int nch = bf16_chunks(Is);
+  if (H % 16 || Is % 32 || Is <= 0 || nch > kCsWaves)
+    return fail("combine: fused shared down needs H % 16 == 0, Is % 32 == 0, Is < 4096");
+  dim3 grid(H / 16, (N + kCsTokens - 1) / kCsTokens);
+  combine_shared_kernel<<<grid, 64 * kCsWaves, 0, stream>>>(
+      d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
+      reinterpret_cast<const u32x4*>(wd), shared_gate, y);
+  return check_launch("combine_shared");
+}
+
 int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int topk_group);
 
 // ------------------------------------------------------------------ auxiliary stream
-// qmoe_forward runs independent work on a library-owned stream (created once per device,
-// default priority) concurrently with the caller's stream:
+// qmoe_forward runs independent work on a library-owned stream (created
+// once per device, default priority) concurrently with the caller's stream:
 //  * the shared expert, which depends only on x, beside the router -> top-k -> permute ->
-//    routed chain;
-//  * in the hybrid large-M regime, the cold experts' grouped matmuls (small kernel, bound by
-//    HBM) beside the hot experts' (large kernel, bound by MFMA).
+//    routed chain (small decode batches instead fuse it into the router and combine launches:
+//    there a join, which costs a launch that does not overlap the previous kernel, costs more
+//    than the shared expert's bytes);
+//  * in the hybrid regime, the cold experts' grouped matmuls (small kernel, bound by HBM)
+//    beside the hot experts' (large kernel, bound by MFMA).
 // A fork event records the caller's stream at entry, `perm` publishes the permute to the
 // auxiliary stream, `cold` returns the cold gate_up (h complete), `hready` publishes the fp16
 // copy of h, and the caller's stream waits on `join` right before the combine. The mutex is held
@@ -114,7 +202,7 @@ struct AuxStream {
   hipEvent_t fork = nullptr, join = nullptr, perm = nullptr, cold = nullptr, hready = nullptr;
 };
 static std::mutex g_aux_mu;
-constexpr int64_t kAuxMinTokens = 8;
+constexpr int64_t kFuseSharedMaxTokens = 64;
 static std::map<int, AuxStream> g_aux;
 
 static int aux_stream(hipStream_t caller, AuxStream** out) {
@@ -361,13 +449,22 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4 : FMT_BF16;
   const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
 
-  // fork onto the auxiliary stream (held until its join is enqueued below): the shared expert
-  // (below kAuxMinTokens the cross-stream synchronisation costs more than the overlap saves)
-  // and, in the hybrid regime, the cold experts' grouped matmuls
+  const int sreg = dense_regime(c, N);
+  const bool decode = (sreg == QMOE_REGIME_SMALL);
+  // Small decode batches: the shared expert rides in the neighbouring launches, its gate_up with
+  // the router logits and its down projection in the combine, so no launch or stream event of
+  // its own. Otherwise the shared expert and, in the hybrid regime, the cold experts' grouped
+  // matmuls run on the auxiliary stream (held until its join is enqueued below).
+  const bool shared = c.shared_inter > 0;
+  // (the fused launches give bit-identical results; above kFuseSharedMaxTokens the shared
+  // expert's re-read weights cost more than the auxiliary stream's join)
+  const bool fuse = decode && shared && N <= kFuseSharedMaxTokens;
+  const bool fuse_gu = fuse && c.router_format == QMOE_ROUTER_BF16_TILED;
+  const bool fuse_dn = fuse && bf16_chunks(c.shared_inter) <= 8;
   std::unique_lock<std::mutex> aux_lock;
   AuxStream* aux = nullptr;
   hipStream_t sstream = stream;
-  const bool shared_aux = c.shared_inter > 0 && N >= kAuxMinTokens;
+  const bool shared_aux = shared && !fuse;
   auto link = [&](hipEvent_t ev, hipStream_t from, hipStream_t to, const char* what) {
     hipError_t err = hipEventRecord(ev, from);
     if (err == hipSuccess) err = hipStreamWaitEvent(to, ev, 0);
@@ -382,22 +479,26 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     if (shared_aux) sstream = aux->s;
   }
 
-  // 1. shared expert (gate_up + SwiGLU, then down) on the auxiliary stream
-  const int sreg = dense_regime(c, N);
-  const int st = (sreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
-  if (c.shared_inter > 0) {
-    QmmArgs a{};
-    a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
-    a.K = c.hidden; a.n_rows = 2 * c.shared_inter; a.codes = wts->sh_gu; a.out = sh_h;
-    a.ld_out = c.shared_inter;
-    rc = launch_qmm(a, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
-    if (rc) return rc;
-    QmmArgs b{};
-    b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
-    b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = wts->sh_dn; b.out = sh_out;
-    b.ld_out = c.hidden;
-    rc = launch_qmm(b, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, sstream);
-    if (rc) return rc;
+  // 1. shared expert gate_up + SwiGLU -> sh_h (fused with the router below when decoding)
+  const int st = decode ? kSmallMTile : kLargeMTile;
+  QmmArgs sgu{};
+  if (shared) {
+    sgu.act = x; sgu.act_rows = N; sgu.slot_div = 1; sgu.dense_rows = N; sgu.n_experts = 1;
+    sgu.K = c.hidden; sgu.n_rows = 2 * c.shared_inter; sgu.codes = wts->sh_gu; sgu.out = sh_h;
+    sgu.ld_out = c.shared_inter;
+    if (!fuse_gu) {
+      rc = launch_qmm(sgu, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
+      if (rc) return rc;
+    }
+    // shared down -> sh_out (fused into the combine when decoding)
+    if (!fuse_dn) {
+      QmmArgs b{};
+      b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
+      b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = wts->sh_dn; b.out = sh_out;
+      b.ld_out = c.hidden;
+      rc = launch_qmm(b, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, sstream);
+      if (rc) return rc;
+    }
   }
 
   // 2. router logits (+ the shared-expert gate logit in column E)
@@ -410,15 +511,16 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   } else {
     ld = c.router_rows;
     QmmArgs a{};
-    const int rreg = dense_regime(c, N);
     // the decode kernel stops at the 16-row tile holding logit E (the rows up to router_rows
     // are padding for the large kernel's 256-row tiles)
     const int live_rows = (c.n_experts + has_sg + 15) / 16 * 16;
     a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
-    a.K = c.hidden; a.n_rows = (rreg == QMOE_REGIME_SMALL) ? std::min(live_rows, c.router_rows) : c.router_rows;
+    a.K = c.hidden; a.n_rows = decode ? std::min(live_rows, c.router_rows) : c.router_rows;
     a.codes = wts->router_w; a.out = logits; a.ld_out = ld;
-    const int rt = (rreg == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
-    rc = launch_qmm(a, FMT_BF16, EPI_F32, rreg, (N + rt - 1) / rt, stream);
+    if (fuse_gu)
+      rc = launch_qmm_pair_bf16(a, sgu, stream);
+    else
+      rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + st - 1) / st, stream);
   }
   if (rc) return rc;
   // 3. top-k
@@ -490,7 +592,10 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
     rc = link(aux->join, aux->s, stream, "join");
     if (rc) return rc;
   }
-  // 7. unpermute + weighted combine + gated shared + bf16
-  return launch_combine(d, inv, wv, n, c.top_k, c.hidden, c.shared_inter > 0 ? sh_out : nullptr,
+  // 7. unpermute + weighted combine + gated shared (its down projection fused when decoding) + bf16
+  if (fuse_dn)
+    return launch_combine_shared(d, inv, wv, n, c.top_k, c.hidden, sh_h, c.shared_inter, wts->sh_dn,
+                                 has_sg ? sg : nullptr, y, stream);
+  return launch_combine(d, inv, wv, n, c.top_k, c.hidden, shared ? sh_out : nullptr,
                         has_sg ? sg : nullptr, y, stream);
 }

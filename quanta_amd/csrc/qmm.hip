@@ -109,24 +109,34 @@ struct SmallStage {
 };
 
 template <int FMT, int EPI, int W, int CPW, int JPW>
-__global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
-__attribute__((amdgpu_waves_per_eu((FMT == FMT_INT4 && ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW >= 4) ? 3 : 1)))
-qmm_small_kernel(QmmArgs a, int n_jobs) {
-  constexpr int WAVES = W > 4 ? W : 4;
-  constexpr int JOBS_PER_WG = WAVES / W;
-  constexpr int NT = ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW;
-  constexpr int CH = W * CPW;
-  static_assert(FMT == FMT_INT4 || CPW == 1, "bf16 weights use one chunk per wavefront");
+struct SmallCfg {
+  static constexpr int WAVES = W > 4 ? W : 4;
+  static constexpr int JOBS_PER_WG = WAVES / W;
+  static constexpr int NT = ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW;
+  static constexpr int CH = W * CPW;
   // chunk sums: [wave][chunk of the wave][tile][lane]
+  static constexpr int RED = (CH > 1) ? WAVES * CPW * NT * 64 : 1;
+  // the four-tile variants are held to 3 wavefronts per SIMD (168 VGPRs)
+  static constexpr int WPE = (FMT == FMT_INT4 && NT >= 4) ? 3 : 1;
+};
+
+// Body of one workgroup: job block `bx` of m-tile `by`, chunk sums in `red` (LDS).
+template <int FMT, int EPI, int W, int CPW, int JPW>
+__device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx, int by,
+                                           f32x4_t* red) {
+  using C = SmallCfg<FMT, EPI, W, CPW, JPW>;
+  constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
+  constexpr int NT = C::NT;
+  constexpr int CH = C::CH;
+  static_assert(FMT == FMT_INT4 || CPW == 1, "bf16 weights use one chunk per wavefront");
   constexpr bool kRed = CH > 1;
-  __shared__ f32x4_t red[kRed ? WAVES * CPW * NT * 64 : 1];
 
   // wave index as a scalar, so per-wavefront quantities (job, k-range) stay in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   int e, m0, m_cnt;
-  if (!resolve_mtile(a, blockIdx.y, kSmallMTile, e, m0, m_cnt)) return;
+  if (!resolve_mtile(a, by, kSmallMTile, e, m0, m_cnt)) return;
 
-  const int job = blockIdx.x * JOBS_PER_WG + wave / W;
+  const int job = bx * JOBS_PER_WG + wave / W;
   const int kpart = wave % W;
   const bool job_ok = job < n_jobs;
   const int mrow = lane & 15, lg = lane >> 4;
@@ -324,6 +334,28 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
                        ok ? acc[(EPI == EPI_SWIGLU) ? JPW + jp : jp][j] : 0.f);
     }
   }
+}
+
+template <int FMT, int EPI, int W, int CPW, int JPW>
+__global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
+__attribute__((amdgpu_waves_per_eu(SmallCfg<FMT, EPI, W, CPW, JPW>::WPE)))
+qmm_small_kernel(QmmArgs a, int n_jobs) {
+  __shared__ f32x4_t red[SmallCfg<FMT, EPI, W, CPW, JPW>::RED];
+  small_body<FMT, EPI, W, CPW, JPW>(a, n_jobs, blockIdx.x, blockIdx.y, red);
+}
+
+// Two dense bf16 products over the same activation rows in one launch (the router logits and
+// the shared expert's gate_up): job blocks [0, gx1) run the first, the rest the second. Both
+// use the same K, so the same chunking W, and each keeps the arithmetic of its own launch.
+template <int EPI1, int EPI2, int W>
+__global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
+qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2) {
+  constexpr int R1 = SmallCfg<FMT_BF16, EPI1, W, 1, 1>::RED, R2 = SmallCfg<FMT_BF16, EPI2, W, 1, 1>::RED;
+  __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
+  if (static_cast<int>(blockIdx.x) < gx1)
+    small_body<FMT_BF16, EPI1, W, 1, 1>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
+  else
+    small_body<FMT_BF16, EPI2, W, 1, 1>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
 }
 
 // ============================================================================ large-M kernel
@@ -797,6 +829,32 @@ static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   return 0;
 }
 
+template <int W>
+static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream) {
+  constexpr int WAVES = W > 4 ? W : 4;
+  constexpr int JPWG = WAVES / W;
+  const int n1 = a1.n_rows / 16, n2 = a2.n_rows / 32;   // fp32 epilogue jobs, SwiGLU jobs
+  const int gx1 = (n1 + JPWG - 1) / JPWG, gx2 = (n2 + JPWG - 1) / JPWG;
+  qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W>
+      <<<dim3(gx1 + gx2, static_cast<unsigned>(mtiles)), 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+}
+
+int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream) {
+  if (a1.offsets || a2.offsets || a1.dense_rows != a2.dense_rows || a1.K != a2.K || a1.K % 32 ||
+      a1.n_rows % 16 || a2.n_rows % 32 || a1.dense_rows <= 0)
+    return fail("qmm pair: two dense bf16 products over the same rows and K required");
+  const int64_t mtiles = (a1.dense_rows + kSmallMTile - 1) / kSmallMTile;
+  if (mtiles > 65535) return fail("qmm pair: too many m-tiles for one launch");
+  switch (bf16_chunks(a1.K)) {
+    case 16: launch_pair_w<16>(a1, a2, mtiles, stream); break;
+    case 8: launch_pair_w<8>(a1, a2, mtiles, stream); break;
+    case 4: launch_pair_w<4>(a1, a2, mtiles, stream); break;
+    case 2: launch_pair_w<2>(a1, a2, mtiles, stream); break;
+    default: launch_pair_w<1>(a1, a2, mtiles, stream); break;
+  }
+  return check_launch("qmm pair");
+}
+
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,
                hipStream_t stream) {
   if (a.K <= 0 || a.n_rows <= 0) return fail("qmm: empty problem");
@@ -816,8 +874,7 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       const int nsb = a.K / 128;
       ch = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;
     } else {
-      const int nks = a.K / 32;
-      ch = (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
+      ch = bf16_chunks(a.K);
     }
     const int jobs = (epi == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16;
     const SmallShape sh = pick_small_shape(fmt, epi, ch, mtile_bound, jobs);

@@ -197,6 +197,19 @@ enum { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,
                hipStream_t stream);
+// Chunk count of the small-regime bf16 products over K: ~8 32-deep steps per chunk, one
+// wavefront per chunk, chunk sums added in chunk order.
+inline int bf16_chunks(int K) {
+  const int nks = K / 32;
+  return (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
+}
+// One launch of two dense bf16 small-regime products over the same rows and K: a1 with the
+// fp32 epilogue (router logits), a2 with SwiGLU (shared expert gate_up).
+int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream);
+// Decode combine with the shared expert's down projection fused in (wd: tiled bf16 [H, Is]).
+int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
+                          int H, const uint16_t* sh_h, int Is, const uint16_t* wd,
+                          const float* shared_gate, uint16_t* y, hipStream_t stream);
 // act [rows][K] bf16 -> act16 fp16 with a per-row power-of-two scale (exact for bf16 values
 // within 2^28 of the row's largest magnitude); row_sinv[r] = the inverse scale.
 int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16, float* row_sinv,

@@ -225,6 +225,19 @@ def test_batch_invariance_full_size(gpu, name, N):
         assert torch.equal(single, full[t]), f"{name} token {t} of {N}"
 
 
+@pytest.mark.parametrize("name", ["c1", "c2", "c3"])
+def test_fused_shared_expert_matches_unfused(gpu, name):
+    """Up to 64 tokens the shared expert runs inside the router and combine launches; above, as
+    its own launches on the auxiliary stream. Both use the same chunked summation, so the first
+    64 tokens of a 65-token call equal a 64-token call bit for bit."""
+    cfg = synth.spec(name).cfg
+    p = _layer(name, gpu)
+    x = synth.make_inputs(name, 65, device=gpu, seed=65)
+    y65 = qwen35_moe(x[None], p, cfg)[0]
+    y64 = qwen35_moe(x[:64][None], p, cfg)[0]
+    assert torch.equal(y64, y65[:64])
+
+
 def test_prefill_zipf_c4(gpu):
     cfg = synth.spec("c4").cfg
     p = _layer("c4", gpu)
