@@ -53,7 +53,7 @@ extern "C" {
 /* grouped-qmm regimes */
 #define QMOE_REGIME_AUTO 0
 #define QMOE_REGIME_SMALL 1 /* 16-token m-tiles, weights streamed to registers (decode) */
-#define QMOE_REGIME_LARGE 2 /* prefill: experts of > 32 rows on 128x256 LDS-staged fp16 tiles,
+#define QMOE_REGIME_LARGE 2 /* prefill: experts of > 16 rows on 128x256 LDS-staged fp16 tiles,
                                the others on 16-token m-tiles */
 
 /* grouped-qmm epilogues */

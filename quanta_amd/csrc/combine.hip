@@ -106,24 +106,42 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 // the result is bit-identical to the unfused shared down and independent of the other tokens.
 // Wd is the tiled bf16 [H/16][Is/32][64][8].
 constexpr int kCsWaves = 8;
-constexpr int kCsTokens = 16;   // tokens per workgroup (one m-tile)
+constexpr int kCsTokens = 16;   // tokens per workgroup: one m-tile
 __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
     int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ sh_h, int Is, int nch,
     const u32x4* __restrict__ wd, const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
   __shared__ f32x4_t part[kCsWaves][64];
   __shared__ float sh[16][17];
+  __shared__ float routed[16][17];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int fb = blockIdx.x;
-  const int t_begin = blockIdx.y * kCsTokens;
-  const int t_end = min(N, t_begin + kCsTokens);
+  const int tm = blockIdx.y * kCsTokens;
   const int nks = Is / 32;
   const int c0 = (wave < nch) ? wave * nks / nch : 0, c1 = (wave < nch) ? (wave + 1) * nks / nch : 0;
   const u32x4* wp = wd + static_cast<int64_t>(fb) * nks * 64 + lane;
-  const int f = threadIdx.x & 15, tl = threadIdx.x >> 4;   // combine phase: (token, feature)
+  // the routed gather-sum of (token tl, feature f) runs on wavefronts 4-7 while wavefronts 0-3
+  // compute the shared down (when it has at most 4 chunks), else after it
+  const int rt = threadIdx.x & 255;
+  const int f = rt & 15, tl = rt >> 4;
   const int col = fb * 16 + f;
-  for (int tm = t_begin; tm < t_end; tm += 16) {
-    // shared down for tokens tm .. tm+15 (rows past N read token tm: computed, never used)
+  const bool gather_early = nch <= 4;
+  auto routed_sum = [&]() __attribute__((always_inline)) {
+    const int t = tm + tl;
+    float acc1 = 0.f;
+    if (t < N) {
+      const int64_t m0 = static_cast<int64_t>(t) * k;
+      for (int s0 = 0; s0 < k; ++s0) {
+        const int pos = inv[m0 + s0];
+        if (pos >= 0 && pos < n_pos)
+          acc1 = fmaf(bf16_to_f32(d[static_cast<int64_t>(pos) * H + col]), w[m0 + s0], acc1);
+      }
+    }
+    routed[tl][f] = acc1;
+  };
+  if (gather_early && wave >= 4) routed_sum();
+  // shared down for tokens tm .. tm+15 (rows past N read token tm: computed, never used)
+  {
     const int tr = tm + (lane & 15);
     const uint16_t* xr = sh_h + static_cast<int64_t>(tr < N ? tr : tm) * Is + 8 * (lane >> 4);
     f32x4_t acc{0.f, 0.f, 0.f, 0.f};
@@ -133,38 +151,29 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
       acc = mfma16(as_bf16x8(xv), as_bf16x8(wv), acc);
     }
     part[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-      f32x4_t s4 = part[0][lane];
+  }
+  if (!gather_early && wave < 4) routed_sum();
+  __syncthreads();
+  if (wave == 0) {
+    f32x4_t s4 = part[0][lane];
 #pragma unroll
-      for (int q = 1; q < kCsWaves; ++q) {
-        const f32x4_t o = part[q][lane];
+    for (int q = 1; q < kCsWaves; ++q) {
+      const f32x4_t o = part[q][lane];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s4[j] += o[j];
-      }
-      // lane holds tokens 4*(lane/16) + j, feature lane%16
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sh[4 * (lane >> 4) + j][lane & 15] = bf16_to_f32(f32_to_bf16(s4[j]));
+      for (int j = 0; j < 4; ++j) s4[j] += o[j];
     }
-    __syncthreads();
-    // weighted combine of the routed slots (slot order) + gated shared, for 16 x 16 outputs
-    if (tl < 16) {
-      const int t = tm + tl;
-      if (t < N) {
-        float acc1 = 0.f;
-        const int64_t m0 = static_cast<int64_t>(t) * k;
-        for (int s0 = 0; s0 < k; ++s0) {
-          const int pos = inv[m0 + s0];
-          if (pos >= 0 && pos < n_pos)
-            acc1 = fmaf(bf16_to_f32(d[static_cast<int64_t>(pos) * H + col]), w[m0 + s0], acc1);
-        }
-        const float g = shared_gate ? shared_gate[t] : 1.0f;
-        acc1 = fmaf(sh[tl][f], g, acc1);
-        y[static_cast<int64_t>(t) * H + col] = f32_to_bf16(acc1);
-      }
+    // lane holds tokens 4*(lane/16) + j, feature lane%16
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sh[4 * (lane >> 4) + j][lane & 15] = bf16_to_f32(f32_to_bf16(s4[j]));
+  }
+  __syncthreads();
+  // routed sum (slot order) + gated shared, rounded once to bf16
+  if (threadIdx.x < 256) {
+    const int t = tm + tl;
+    if (t < N) {
+      const float g = shared_gate ? shared_gate[t] : 1.0f;
+      y[static_cast<int64_t>(t) * H + col] = f32_to_bf16(fmaf(sh[tl][f], g, routed[tl][f]));
     }
-    // part / sh are rewritten by the next m-tile only after every thread has read them
-    __syncthreads();
   }
 }
 

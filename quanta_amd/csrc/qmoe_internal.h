@@ -226,6 +226,6 @@ constexpr int kSmallMTile = 16;
 constexpr int kLargeMTile = 128;
 // Large-M (prefill) regime: experts routed more rows than this use 128-row tiles on the large
 // kernel, the others 16-row tiles on the small kernel.
-constexpr int kHybridSplitRows = 32;
+constexpr int kHybridSplitRows = 16;
 
 }  // namespace qmoe
