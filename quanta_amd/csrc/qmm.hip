@@ -530,8 +530,12 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // i issues the two MFMAs of m-block i, the read of m-block i's A fragment for step s+1 and
   // 1/MB of step s+1's weight dequant, and a scheduling barrier keeps that order, so LDS reads
   // have a full step to land and the dequant VALU work is spread between the MFMAs.
-  const uint32_t exp_bits = 0x64006400u;
+  // fp16 bit insertion: nibble pair 0 (2) of a word OR'd into 1024.0 (0x6400, mantissa LSB 1)
+  // gives 1024 + q; pair 1 (3), masked in place at bits 4-7, into 64.0 (0x5400, mantissa LSB
+  // 1/16) gives 64 + q. Pairs 2 and 3 share one 8-bit shift. Subtracting 1024 or 64 is exact.
+  const uint32_t exp_lo = 0x64006400u, exp_hi = 0x54005400u;
   const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  const f16x2_t k64 = {static_cast<_Float16>(64.0f), static_cast<_Float16>(64.0f)};
   auto compute = [&](int p, const LgStageBf& gb, auto mbc) __attribute__((always_inline)) {
     constexpr int MB = decltype(mbc)::value;
     constexpr int UPS = 8 / MB;                 // dequant units (nibble pairs) per slot
@@ -562,9 +566,10 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       const int t = u >> 2, j = u & 3;
       if (FMT == FMT_INT4) {
         uint32_t r;
-        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q[t][s] >> (4 * j)), "s"(0x000F000Fu),
-            "v"(exp_bits));
-        const f16x2_t qq = __builtin_bit_cast(f16x2_t, r) - k1024;
+        const uint32_t src = (j >= 2) ? (q[t][s] >> 8) : q[t][s];
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(src),
+            "s"((j & 1) ? 0x00F000F0u : 0x000F000Fu), "v"((j & 1) ? exp_hi : exp_lo));
+        const f16x2_t qq = __builtin_bit_cast(f16x2_t, r) - ((j & 1) ? k64 : k1024);
         bfo[t][j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qq, s2[t], b2[t]));
       } else if (j == 0) {
         bfo[t] = gb.q[t][s];
