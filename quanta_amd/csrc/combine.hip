@@ -145,10 +145,19 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     const int tr = tm + (lane & 15);
     const uint16_t* xr = sh_h + static_cast<int64_t>(tr < N ? tr : tm) * Is + 8 * (lane >> 4);
     f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-    for (int c = c0; c < c1; ++c) {
-      const u32x4 wv = wp[c * 64];
-      const u32x4 xv = *reinterpret_cast<const u32x4*>(xr + 32 * c);
-      acc = mfma16(as_bf16x8(xv), as_bf16x8(wv), acc);
+    // batches of 8 steps, all loads first (clamped indices), MFMAs in step order
+    constexpr int BS = 8;
+    for (int cb = c0; cb < c1; cb += BS) {
+      u32x4 wv[BS], xv[BS];
+#pragma unroll
+      for (int i = 0; i < BS; ++i) {
+        const int c = min(cb + i, c1 - 1);
+        wv[i] = wp[c * 64];
+        xv[i] = *reinterpret_cast<const u32x4*>(xr + 32 * c);
+      }
+#pragma unroll
+      for (int i = 0; i < BS; ++i)
+        if (cb + i < c1) acc = mfma16(as_bf16x8(xv[i]), as_bf16x8(wv[i]), acc);
     }
     part[wave][lane] = acc;
   }

@@ -277,14 +277,25 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         wp[t] = static_cast<const u32x4*>(a.codes) + tb * 64 + lane;
       }
       const u32x4* xp = reinterpret_cast<const u32x4*>(xrow) + lg;   // 8 lg bf16
-#pragma unroll 4
-      for (int c = k0; c < k1; ++c) {
-        u32x4 wv[NT];
+      // Batches of 8 steps: all loads of a batch issue before its MFMAs (indices clamped into
+      // the range, so no load is conditional); the MFMAs run in step order.
+      constexpr int BS = 8;
+      for (int cb = k0; cb < k1; cb += BS) {
+        u32x4 wv[BS][NT], xv[BS];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) wv[t] = wp[t][c * 64];
-        const bf16x8_t A = as_bf16x8(xp[c * 4]);
+        for (int i = 0; i < BS; ++i) {
+          const int c = min(cb + i, k1 - 1);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] = mfma16(A, as_bf16x8(wv[t]), acc[t]);
+          for (int t = 0; t < NT; ++t) wv[i][t] = wp[t][c * 64];
+          xv[i] = xp[c * 4];
+        }
+#pragma unroll
+        for (int i = 0; i < BS; ++i) {
+          if (cb + i < k1) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = mfma16(as_bf16x8(xv[i]), as_bf16x8(wv[i][t]), acc[t]);
+          }
+        }
       }
     }
   }
