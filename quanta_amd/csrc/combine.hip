@@ -221,6 +221,8 @@ struct AuxStream {
 };
 static std::mutex g_aux_mu;
 constexpr int64_t kFuseSharedMaxTokens = 64;
+// Largest batch routed slot-major (no permute launch).
+constexpr int64_t kSlotMajorMaxTokens = 2;
 static std::map<int, AuxStream> g_aux;
 
 static int aux_stream(hipStream_t caller, AuxStream** out) {
@@ -479,6 +481,9 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   const bool fuse = decode && shared && N <= kFuseSharedMaxTokens;
   const bool fuse_gu = fuse && c.router_format == QMOE_ROUTER_BF16_TILED;
   const bool fuse_dn = fuse && bf16_chunks(c.shared_inter) <= 8;
+  // one or two tokens: slot-major routing written by the top-k, no permute launch (each slot
+  // its own m-tile; an expert two tokens share is read twice, cheaper than the launch)
+  const bool slot_major = !hybrid && N <= kSlotMajorMaxTokens;
   std::unique_lock<std::mutex> aux_lock;
   AuxStream* aux = nullptr;
   hipStream_t sstream = stream;
@@ -541,15 +546,23 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + st - 1) / st, stream);
   }
   if (rc) return rc;
-  // 3. top-k
-  rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
-                   c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream);
-  if (rc) return rc;
-  // 4. stable permute by expert (16-row tiles; hybrid: hot experts' 128-row tiles separately)
-  rc = launch_permute(idx, n, c.top_k, c.n_experts, kSmallMTile, counts, offsets, tile_off, sorted,
-                      inv, tile_map, bound_small, stream, kHybridSplitRows, kLargeMTile,
-                      hybrid ? tile_map_big : nullptr, L.max_tiles_big);
-  if (rc) return rc;
+  if (slot_major) {
+    // 3-4. top-k with the slot-major tile map
+    rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
+                     c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream,
+                     tile_map, bound_small, sorted, inv);
+    if (rc) return rc;
+  } else {
+    // 3. top-k
+    rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
+                     c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream);
+    if (rc) return rc;
+    // 4. stable permute by expert (16-row tiles; hybrid: hot experts' 128-row tiles separately)
+    rc = launch_permute(idx, n, c.top_k, c.n_experts, kSmallMTile, counts, offsets, tile_off,
+                        sorted, inv, tile_map, bound_small, stream, kHybridSplitRows, kLargeMTile,
+                        hybrid ? tile_map_big : nullptr, L.max_tiles_big);
+    if (rc) return rc;
+  }
   const bool f16_acts = (hybrid && wfmt == FMT_INT4);
   // the cold experts' tiles wait for the permute on the auxiliary stream
   hipStream_t cstream = stream;

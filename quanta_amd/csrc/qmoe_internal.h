@@ -159,10 +159,13 @@ inline int64_t mtile_upper_bound(int64_t mc, int64_t n_experts, int64_t m_tile) 
 // Launchers shared between entry points (defined in the .hip files).
 int launch_router_f32(const uint16_t* x, const float* wr, const float* shared_gate, int N, int H,
                       int E, float* logits, int ld_logits, hipStream_t stream);
+// With tile_map: slot-major routing (each slot its own one-row m-tile, identity sorted/inv)
+// in place of the permute; max_tiles >= N*k.
 int launch_topk(const float* logits, int ld_logits, const float* bias, int N, int E, int k,
-                int scoring, int n_group, int topk_group, int norm_topk, float scale,
-                int has_shared_gate, int32_t* idx, float* w, float* shared_gate_out,
-                hipStream_t stream);
+                int scoring, int n_group, int topk_group, int norm_topk, float scale, int has_sg,
+                int32_t* idx, float* w, float* sg_out, hipStream_t stream,
+                int32_t* tile_map = nullptr, int64_t max_tiles = 0, int32_t* sorted = nullptr,
+                int32_t* inv = nullptr);
 // With tile_map_big: experts of more than split_rows rows get m_tile_big-row tiles there and
 // none in tile_map (the hybrid regime); without it, every expert's tiles go to tile_map.
 int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,

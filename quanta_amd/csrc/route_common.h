@@ -248,6 +248,45 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
   out_w = my_w * P.scale;
 }
 
+inline TopkParams topk_params(const float* bias, int E, int k, int scoring, int n_group,
+                              int topk_group, int norm_topk, float scale, int has_sg) {
+  TopkParams P;
+  P.bias = bias;
+  P.E = E;
+  P.k = k;
+  P.scoring = scoring;
+  P.n_group = n_group;
+  P.topk_group = topk_group;
+  P.norm_topk = norm_topk;
+  P.has_sg = has_sg;
+  P.scale = scale;
+  return P;
+}
+
+// Experts per lane of the top-k wavefront for E experts.
+inline int topk_vpl(int E) {
+  return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+}
+
+// Top-k of token t by one wavefront, stored as idx/w rows of k and the shared-expert gate
+// sigmoid(logit E); returns lane r's expert (r < k).
+template <int VPL>
+__device__ __forceinline__ int topk_store(const float* __restrict__ logits, int ld,
+                                           const TopkParams& P, int t, int lane,
+                                           int32_t* __restrict__ idx_out,
+                                           float* __restrict__ w_out, float* __restrict__ sg_out) {
+  const float* row = logits + static_cast<int64_t>(t) * ld;
+  int id;
+  float w;
+  topk_token<VPL>(row, P, lane, id, w);
+  if (lane < P.k) {
+    idx_out[static_cast<int64_t>(t) * P.k + lane] = id;
+    w_out[static_cast<int64_t>(t) * P.k + lane] = w;
+  }
+  if (P.has_sg && lane == 0) sg_out[t] = 1.0f / (1.0f + expf(-row[P.E]));
+  return id;
+}
+
 // ---------------------------------------------------------------- stable permute body
 // Stable permute of the (token, slot) list by expert: histogram, exclusive scans and scatter in
 // LDS, with the stable rank taken from a per-expert token bitmap, so the result equals a stable

@@ -58,52 +58,59 @@ int launch_router_f32(const uint16_t* x, const float* wr, const float* shared_ga
 
 // ---------------------------------------------------------------- top-k
 // One wavefront per token (topk_token in route_common.h).
+// With tile_map (SlotMap), also the slot-major routing of a few tokens: slot m = t*k + s is its
+// own one-row m-tile {idx[m], m, 1, 0} and sorted/inv are the identity, in place of the stable
+// permute. Every output row is computed independently of the other rows of its m-tile, so the
+// results equal those of the sorted order; an expert chosen by two tokens is read twice.
+struct SlotMap {
+  int4* tile_map;
+  int max_tiles;
+  int32_t* sorted;
+  int32_t* inv;
+};
+
 template <int VPL>
 __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ logits, int ld,
                                                    TopkParams P, int N,
                                                    int32_t* __restrict__ idx_out,
                                                    float* __restrict__ w_out,
-                                                   float* __restrict__ sg_out) {
+                                                   float* __restrict__ sg_out, SlotMap sm) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;  // whole wavefront exits together; no block barriers below
-  const float* row = logits + static_cast<int64_t>(t) * ld;
-  int id;
-  float w;
-  topk_token<VPL>(row, P, lane, id, w);
-  if (lane < P.k) {
-    idx_out[static_cast<int64_t>(t) * P.k + lane] = id;
-    w_out[static_cast<int64_t>(t) * P.k + lane] = w;
+  const int id = topk_store<VPL>(logits, ld, P, t, lane, idx_out, w_out, sg_out);
+  if (sm.tile_map) {
+    const int m = t * P.k + lane;
+    if (lane < P.k) {
+      sm.tile_map[m] = make_int4(id, m, 1, 0);
+      sm.sorted[m] = m;
+      sm.inv[m] = m;
+    }
+    if (t == 0)
+      for (int i = N * P.k + lane; i < sm.max_tiles; i += 64) sm.tile_map[i] = make_int4(-1, 0, 0, 0);
   }
-  if (P.has_sg && lane == 0) sg_out[t] = 1.0f / (1.0f + expf(-row[P.E]));
-}
-
-static TopkParams topk_params(const float* bias, int E, int k, int scoring, int n_group,
-                              int topk_group, int norm_topk, float scale, int has_sg) {
-  TopkParams P;
-  P.bias = bias;
-  P.E = E;
-  P.k = k;
-  P.scoring = scoring;
-  P.n_group = n_group;
-  P.topk_group = topk_group;
-  P.norm_topk = norm_topk;
-  P.has_sg = has_sg;
-  P.scale = scale;
-  return P;
 }
 
 int launch_topk(const float* logits, int ld, const float* bias, int N, int E, int k, int scoring,
                 int n_group, int topk_group, int norm_topk, float scale, int has_sg,
-                int32_t* idx, float* w, float* sg_out, hipStream_t stream) {
+                int32_t* idx, float* w, float* sg_out, hipStream_t stream, int32_t* tile_map,
+                int64_t max_tiles, int32_t* sorted, int32_t* inv) {
   const TopkParams P = topk_params(bias, E, k, scoring, n_group, topk_group, norm_topk, scale, has_sg);
+  SlotMap sm{};
+  if (tile_map) {
+    if (!sorted || !inv || max_tiles < static_cast<int64_t>(N) * k || max_tiles > (int64_t(1) << 30))
+      return fail("topk: slot-major routing needs sorted, inv and N*k tiles");
+    sm = SlotMap{reinterpret_cast<int4*>(tile_map), static_cast<int>(max_tiles), sorted, inv};
+  }
   dim3 grid((N + 3) / 4);
-#define QMOE_TOPK(V) topk_kernel<V><<<grid, 256, 0, stream>>>(logits, ld, P, N, idx, w, sg_out)
-  if (E <= 64) QMOE_TOPK(1);
-  else if (E <= 128) QMOE_TOPK(2);
-  else if (E <= 256) QMOE_TOPK(4);
-  else if (E <= 512) QMOE_TOPK(8);
-  else QMOE_TOPK(16);
+#define QMOE_TOPK(V) topk_kernel<V><<<grid, 256, 0, stream>>>(logits, ld, P, N, idx, w, sg_out, sm)
+  switch (topk_vpl(E)) {
+    case 1: QMOE_TOPK(1); break;
+    case 2: QMOE_TOPK(2); break;
+    case 4: QMOE_TOPK(4); break;
+    case 8: QMOE_TOPK(8); break;
+    default: QMOE_TOPK(16); break;
+  }
 #undef QMOE_TOPK
   return check_launch("topk");
 }
