@@ -419,16 +419,42 @@ __device__ __forceinline__ void permute_body(
     }
   }
 
-  // Per-expert exclusive popcount prefix over the token bitmap words.
+  // Per-expert exclusive popcount prefix over the token bitmap words: one thread per expert
+  // for a few words; for long bitmaps 16 lanes per expert, each over a run of words, with the
+  // run totals scanned across the 16 lanes.
   for (int i = tid; i < nbits; i += nthr) pref[i] = __popc(bits[i]);
   __syncthreads();
-  for (int el = tid; el < e1 - e0; el += nthr) {
-    uint32_t run = 0;
-    uint32_t* p = pref + el * words_per_expert;
-    for (int w = 0; w < words_per_expert; ++w) {
-      const uint32_t v = p[w];
-      p[w] = run;
-      run += v;
+  if (words_per_expert <= 4) {
+    for (int el = tid; el < e1 - e0; el += nthr) {
+      uint32_t run = 0;
+      uint32_t* p = pref + el * words_per_expert;
+      for (int w = 0; w < words_per_expert; ++w) {
+        const uint32_t v = p[w];
+        p[w] = run;
+        run += v;
+      }
+    }
+  } else {
+    const int l16 = tid & 15;
+    const int per = (words_per_expert + 15) / 16;
+    const int w0 = min(l16 * per, words_per_expert), w1 = min(w0 + per, words_per_expert);
+    // the 16 lanes of a group share el, so the shuffles stay within active lanes
+    for (int el = tid >> 4; el < e1 - e0; el += nthr >> 4) {
+      uint32_t* p = pref + el * words_per_expert;
+      uint32_t sum = 0;
+      for (int w = w0; w < w1; ++w) sum += p[w];
+      uint32_t incl = sum;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off, 16);
+        if (l16 >= off) incl += o;
+      }
+      uint32_t run = incl - sum;
+      for (int w = w0; w < w1; ++w) {
+        const uint32_t v = p[w];
+        p[w] = run;
+        run += v;
+      }
     }
   }
   // Own output segment starts as -1 so a malformed idx (duplicate experts within a token)

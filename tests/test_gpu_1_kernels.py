@@ -149,6 +149,7 @@ def test_router_bf16_mfma_logits(gpu):
 @pytest.mark.parametrize("N,k,E,m_tile", [
     (1, 10, 512, 16), (8, 2, 16, 16), (128, 10, 512, 16), (300, 8, 256, 16), (4096, 10, 512, 128),
     (5, 1, 1, 16), (64, 64, 64, 16), (8192, 8, 256, 128), (1000, 3, 1024, 128),
+    (2500, 4, 64, 16),
 ])
 def test_permute_bit_exact(gpu, N, k, E, m_tile):
     rng = np.random.default_rng(N + k + E)
