@@ -97,7 +97,8 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 
 // ------------------------------------------------------------------ combine + shared down
 // Decode form of the combine with the shared expert's down projection fused in. A workgroup
-// owns 16 output features f and a block of up to kCsTokens tokens:
+// owns 16 output features f and a block of 16*MT tokens (MT m-tiles, each weight fragment
+// feeding MT MFMAs):
 //   sh[t, f] = bf16(sh_h[t] . Wd[f])                      (the reference's bf16 matmul output)
 //   y[t, f]  = bf16(sum_s w[t,s] * f32(d[inv[t,s], f]) + g[t] * f32(sh[t, f]))
 // sh is computed on v_mfma_f32_16x16x32_bf16 (16 tokens x 16 features per m-tile) with K cut
@@ -106,78 +107,98 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 // the result is bit-identical to the unfused shared down and independent of the other tokens.
 // Wd is the tiled bf16 [H/16][Is/32][64][8].
 constexpr int kCsWaves = 8;
-constexpr int kCsTokens = 16;   // tokens per workgroup: one m-tile
+template <int MT>
 __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
     int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ sh_h, int Is, int nch,
     const u32x4* __restrict__ wd, const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
-  __shared__ f32x4_t part[kCsWaves][64];
-  __shared__ float sh[16][17];
-  __shared__ float routed[16][17];
+  constexpr int TOK = 16 * MT;   // tokens per workgroup
+  __shared__ f32x4_t part[kCsWaves][MT][64];
+  __shared__ float sh[TOK][17];
+  __shared__ float routed[TOK][17];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int fb = blockIdx.x;
-  const int tm = blockIdx.y * kCsTokens;
+  const int tm = blockIdx.y * TOK;
   const int nks = Is / 32;
   const int c0 = (wave < nch) ? wave * nks / nch : 0, c1 = (wave < nch) ? (wave + 1) * nks / nch : 0;
   const u32x4* wp = wd + static_cast<int64_t>(fb) * nks * 64 + lane;
   // the routed gather-sum of (token tl, feature f) runs on wavefronts 4-7 while wavefronts 0-3
-  // compute the shared down (when it has at most 4 chunks), else after it
+  // compute the shared down (when it has at most 4 chunks), else after it; 256 threads, MT
+  // tokens each
   const int rt = threadIdx.x & 255;
-  const int f = rt & 15, tl = rt >> 4;
+  const int f = rt & 15;
   const int col = fb * 16 + f;
   const bool gather_early = nch <= 4;
   auto routed_sum = [&]() __attribute__((always_inline)) {
-    const int t = tm + tl;
-    float acc1 = 0.f;
-    if (t < N) {
-      const int64_t m0 = static_cast<int64_t>(t) * k;
-      for (int s0 = 0; s0 < k; ++s0) {
-        const int pos = inv[m0 + s0];
-        if (pos >= 0 && pos < n_pos)
-          acc1 = fmaf(bf16_to_f32(d[static_cast<int64_t>(pos) * H + col]), w[m0 + s0], acc1);
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int tl = (rt >> 4) + 16 * u;
+      const int t = tm + tl;
+      float acc1 = 0.f;
+      if (t < N) {
+        const int64_t m0 = static_cast<int64_t>(t) * k;
+        for (int s0 = 0; s0 < k; ++s0) {
+          const int pos = inv[m0 + s0];
+          if (pos >= 0 && pos < n_pos)
+            acc1 = fmaf(bf16_to_f32(d[static_cast<int64_t>(pos) * H + col]), w[m0 + s0], acc1);
+        }
       }
+      routed[tl][f] = acc1;
     }
-    routed[tl][f] = acc1;
   };
   if (gather_early && wave >= 4) routed_sum();
-  // shared down for tokens tm .. tm+15 (rows past N read token tm: computed, never used)
+  // shared down for tokens tm .. tm+TOK-1 (rows past N read token tm: computed, never used)
   {
-    const int tr = tm + (lane & 15);
-    const uint16_t* xr = sh_h + static_cast<int64_t>(tr < N ? tr : tm) * Is + 8 * (lane >> 4);
-    f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-    // batches of 8 steps, all loads first (clamped indices), MFMAs in step order
+    const uint16_t* xr[MT];
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int tr = tm + 16 * u + (lane & 15);
+      xr[u] = sh_h + static_cast<int64_t>(tr < N ? tr : tm) * Is + 8 * (lane >> 4);
+    }
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int u = 0; u < MT; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // batches of steps, all loads first (clamped indices), MFMAs in step order
     constexpr int BS = 8;
     for (int cb = c0; cb < c1; cb += BS) {
-      u32x4 wv[BS], xv[BS];
+      u32x4 wv[BS], xv[BS][MT];
 #pragma unroll
       for (int i = 0; i < BS; ++i) {
         const int c = min(cb + i, c1 - 1);
         wv[i] = wp[c * 64];
-        xv[i] = *reinterpret_cast<const u32x4*>(xr + 32 * c);
+#pragma unroll
+        for (int u = 0; u < MT; ++u) xv[i][u] = *reinterpret_cast<const u32x4*>(xr[u] + 32 * c);
       }
 #pragma unroll
       for (int i = 0; i < BS; ++i)
-        if (cb + i < c1) acc = mfma16(as_bf16x8(xv[i]), as_bf16x8(wv[i]), acc);
+        if (cb + i < c1) {
+#pragma unroll
+          for (int u = 0; u < MT; ++u) acc[u] = mfma16(as_bf16x8(xv[i][u]), as_bf16x8(wv[i]), acc[u]);
+        }
     }
-    part[wave][lane] = acc;
+#pragma unroll
+    for (int u = 0; u < MT; ++u) part[wave][u][lane] = acc[u];
   }
   if (!gather_early && wave < 4) routed_sum();
   __syncthreads();
-  if (wave == 0) {
-    f32x4_t s4 = part[0][lane];
+  if (wave < MT) {
+    const int u = wave;
+    f32x4_t s4 = part[0][u][lane];
 #pragma unroll
     for (int q = 1; q < kCsWaves; ++q) {
-      const f32x4_t o = part[q][lane];
+      const f32x4_t o = part[q][u][lane];
 #pragma unroll
       for (int j = 0; j < 4; ++j) s4[j] += o[j];
     }
-    // lane holds tokens 4*(lane/16) + j, feature lane%16
+    // lane holds tokens 4*(lane/16) + j of m-tile u, feature lane%16
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sh[4 * (lane >> 4) + j][lane & 15] = bf16_to_f32(f32_to_bf16(s4[j]));
+    for (int j = 0; j < 4; ++j)
+      sh[16 * u + 4 * (lane >> 4) + j][lane & 15] = bf16_to_f32(f32_to_bf16(s4[j]));
   }
   __syncthreads();
   // routed sum (slot order) + gated shared, rounded once to bf16
-  if (threadIdx.x < 256) {
+  if (threadIdx.x < 16 * TOK) {
+    const int tl = threadIdx.x >> 4;
     const int t = tm + tl;
     if (t < N) {
       const float g = shared_gate ? shared_gate[t] : 1.0f;
@@ -192,10 +213,19 @@ int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w,
   const int nch = bf16_chunks(Is);
   if (H % 16 || Is % 32 || Is <= 0 || nch > kCsWaves)
     return fail("combine: fused shared down needs H % 16 == 0, Is % 32 == 0, Is < 4096");
-  dim3 grid(H / 16, (N + kCsTokens - 1) / kCsTokens);
-  combine_shared_kernel<<<grid, 64 * kCsWaves, 0, stream>>>(
-      d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
-      reinterpret_cast<const u32x4*>(wd), shared_gate, y);
+  // above 48 tokens, 32 per workgroup: the shared down weights are read once per 32 tokens
+  // (below that the halved grid leaves CUs idle)
+  if (N > 48) {
+    dim3 grid(H / 16, (N + 31) / 32);
+    combine_shared_kernel<2><<<grid, 64 * kCsWaves, 0, stream>>>(
+        d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
+        reinterpret_cast<const u32x4*>(wd), shared_gate, y);
+  } else {
+    dim3 grid(H / 16, (N + 15) / 16);
+    combine_shared_kernel<1><<<grid, 64 * kCsWaves, 0, stream>>>(
+        d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
+        reinterpret_cast<const u32x4*>(wd), shared_gate, y);
+  }
   return check_launch("combine_shared");
 }
 

@@ -108,23 +108,26 @@ struct SmallStage {
   u32x4 x[4];     // activation fragments
 };
 
-template <int FMT, int EPI, int W, int CPW, int JPW>
+template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1>
 struct SmallCfg {
   static constexpr int WAVES = W > 4 ? W : 4;
   static constexpr int JOBS_PER_WG = WAVES / W;
   static constexpr int NT = ((EPI == EPI_SWIGLU) ? 2 : 1) * JPW;
   static constexpr int CH = W * CPW;
-  // chunk sums: [wave][chunk of the wave][tile][lane]
-  static constexpr int RED = (CH > 1) ? WAVES * CPW * NT * 64 : 1;
+  // chunk sums: [wave][chunk of the wave][m-tile][tile][lane]
+  static constexpr int RED = (CH > 1) ? WAVES * CPW * MT * NT * 64 : 1;
   // the four-tile variants are held to 3 wavefronts per SIMD (168 VGPRs)
   static constexpr int WPE = (FMT == FMT_INT4 && NT >= 4) ? 3 : 1;
 };
 
-// Body of one workgroup: job block `bx` of m-tile `by`, chunk sums in `red` (LDS).
-template <int FMT, int EPI, int W, int CPW, int JPW>
+// Body of one workgroup: job block `bx` of m-tile `by` (MT > 1, dense bf16 products only:
+// m-tiles by*MT .. by*MT+MT-1, every weight fragment feeding MT MFMAs), chunk sums in `red`
+// (LDS).
+template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1>
 __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx, int by,
                                            f32x4_t* red) {
-  using C = SmallCfg<FMT, EPI, W, CPW, JPW>;
+  using C = SmallCfg<FMT, EPI, W, CPW, JPW, MT>;
+  static_assert(MT == 1 || FMT == FMT_BF16, "several m-tiles per wavefront: bf16 weights only");
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
   constexpr int NT = C::NT;
   constexpr int CH = C::CH;
@@ -133,26 +136,45 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
 
   // wave index as a scalar, so per-wavefront quantities (job, k-range) stay in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  int e, m0, m_cnt;
-  if (!resolve_mtile(a, by, kSmallMTile, e, m0, m_cnt)) return;
+  int e, mt0[MT], mtc[MT];
+  if (MT == 1) {
+    if (!resolve_mtile(a, by, kSmallMTile, e, mt0[0], mtc[0])) return;
+  } else {   // dense rows (the launcher guarantees no segments)
+    e = 0;
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      mt0[u] = (by * MT + u) * kSmallMTile;
+      mtc[u] = static_cast<int>(max<int64_t>(0, min<int64_t>(kSmallMTile, a.dense_rows - mt0[u])));
+    }
+    if (mtc[0] <= 0) return;
+  }
 
   const int job = bx * JOBS_PER_WG + wave / W;
   const int kpart = wave % W;
   const bool job_ok = job < n_jobs;
   const int mrow = lane & 15, lg = lane >> 4;
 
-  int64_t arow = -1;
-  if (mrow < m_cnt) arow = act_row(a, m0 + mrow);
-  const bool row_ok = arow >= 0;
   // Rows past the segment and rows whose slot is invalid read activation row 0, so every load
   // is unconditional (a load under a branch makes the compiler wait for all loads in flight);
   // the former are never stored, the latter are stored as zeros.
-  const uint16_t* xrow = a.act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
-  const uint32_t rows_ok = static_cast<uint32_t>(__ballot(row_ok)) & 0xFFFFu;   // lanes 0-15
-
-  f32x4_t acc[NT];
+  const uint16_t* xrows[MT];
+  uint32_t rows_okm[MT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < MT; ++u) {
+    int64_t arow = -1;
+    if (mrow < mtc[u]) arow = act_row(a, mt0[u] + mrow);
+    const bool row_ok = arow >= 0;
+    xrows[u] = a.act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
+    rows_okm[u] = static_cast<uint32_t>(__ballot(row_ok)) & 0xFFFFu;   // lanes 0-15
+  }
+  const uint16_t* xrow = xrows[0];
+
+  f32x4_t accm[MT][NT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) accm[u][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x4_t (&acc)[NT] = accm[0];
 
   const int tiles_per_expert = a.n_rows / 16;
   // tiles of this wavefront's jobs: job j covers tile j (SwiGLU: gate tile j and up tile
@@ -276,24 +298,30 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         const int64_t tb = (static_cast<int64_t>(e) * tiles_per_expert + tile[t]) * nks;
         wp[t] = static_cast<const u32x4*>(a.codes) + tb * 64 + lane;
       }
-      const u32x4* xp = reinterpret_cast<const u32x4*>(xrow) + lg;   // 8 lg bf16
-      // Batches of 8 steps: all loads of a batch issue before its MFMAs (indices clamped into
+      const u32x4* xp[MT];
+#pragma unroll
+      for (int u = 0; u < MT; ++u) xp[u] = reinterpret_cast<const u32x4*>(xrows[u]) + lg;   // 8 lg bf16
+      // Batches of steps: all loads of a batch issue before its MFMAs (indices clamped into
       // the range, so no load is conditional); the MFMAs run in step order.
-      constexpr int BS = 8;
+      constexpr int BS = (MT > 1) ? 4 : 8;
       for (int cb = k0; cb < k1; cb += BS) {
-        u32x4 wv[BS][NT], xv[BS];
+        u32x4 wv[BS][NT], xv[BS][MT];
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           const int c = min(cb + i, k1 - 1);
 #pragma unroll
           for (int t = 0; t < NT; ++t) wv[i][t] = wp[t][c * 64];
-          xv[i] = xp[c * 4];
+#pragma unroll
+          for (int u = 0; u < MT; ++u) xv[i][u] = xp[u][c * 4];
         }
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           if (cb + i < k1) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] = mfma16(as_bf16x8(xv[i]), as_bf16x8(wv[i][t]), acc[t]);
+            for (int u = 0; u < MT; ++u)
+#pragma unroll
+              for (int t = 0; t < NT; ++t)
+                accm[u][t] = mfma16(as_bf16x8(xv[i][u]), as_bf16x8(wv[i][t]), accm[u][t]);
           }
         }
       }
@@ -305,16 +333,19 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
     // kpart 0 then adds the chunks in order: its own first chunk (CPW == 2) + its last, then
     // every chunk of wavefronts 1 .. W-1
     const int jl = wave / W;
+    auto ri = [&](int wc, int u, int t) { return ((wc * MT + u) * NT + t) * 64 + lane; };
     if (kpart > 0) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) red[((wave * CPW + CPW - 1) * NT + t) * 64 + lane] = acc[t];
+      for (int u = 0; u < MT; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) red[ri(wave * CPW + CPW - 1, u, t)] = accm[u][t];
     }
     if (W > 1) __syncthreads();
     if (kpart == 0) {
       if (CPW == 2) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f32x4_t o = red[((wave * CPW) * NT + t) * 64 + lane];
+          const f32x4_t o = red[ri(wave * CPW, 0, t)];
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[t][j] = o[j] + acc[t][j];
         }
@@ -324,49 +355,55 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
 #pragma unroll
         for (int ci = 0; ci < CPW; ++ci)
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const f32x4_t o = red[(((jl * W + kp) * CPW + ci) * NT + t) * 64 + lane];
+          for (int u = 0; u < MT; ++u)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][j] += o[j];
-          }
+            for (int t = 0; t < NT; ++t) {
+              const f32x4_t o = red[ri((jl * W + kp) * CPW + ci, u, t)];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) accm[u][t][j] += o[j];
+            }
     }
   }
   if (!job_ok || kpart != 0) return;
 
 #pragma unroll
-  for (int jp = 0; jp < JPW; ++jp) {
-    const int col = (job * JPW + jp) * 16 + (lane & 15);
+  for (int u = 0; u < MT; ++u) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int mr = 4 * lg + j;
-      const bool ok = (rows_ok >> mr) & 1u;
-      if (mr < m_cnt)
-        store_out<EPI>(a, m0 + mr, col, ok ? acc[jp][j] : 0.f,
-                       ok ? acc[(EPI == EPI_SWIGLU) ? JPW + jp : jp][j] : 0.f);
+    for (int jp = 0; jp < JPW; ++jp) {
+      const int col = (job * JPW + jp) * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int mr = 4 * lg + j;
+        const bool ok = (rows_okm[u] >> mr) & 1u;
+        if (mr < mtc[u])
+          store_out<EPI>(a, mt0[u] + mr, col, ok ? accm[u][jp][j] : 0.f,
+                         ok ? accm[u][(EPI == EPI_SWIGLU) ? JPW + jp : jp][j] : 0.f);
+      }
     }
   }
 }
 
-template <int FMT, int EPI, int W, int CPW, int JPW>
+template <int FMT, int EPI, int W, int CPW, int JPW, int MT>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
 __attribute__((amdgpu_waves_per_eu(SmallCfg<FMT, EPI, W, CPW, JPW>::WPE)))
 qmm_small_kernel(QmmArgs a, int n_jobs) {
-  __shared__ f32x4_t red[SmallCfg<FMT, EPI, W, CPW, JPW>::RED];
-  small_body<FMT, EPI, W, CPW, JPW>(a, n_jobs, blockIdx.x, blockIdx.y, red);
+  __shared__ f32x4_t red[SmallCfg<FMT, EPI, W, CPW, JPW, MT>::RED];
+  small_body<FMT, EPI, W, CPW, JPW, MT>(a, n_jobs, blockIdx.x, blockIdx.y, red);
 }
 
 // Two dense bf16 products over the same activation rows in one launch (the router logits and
 // the shared expert's gate_up): job blocks [0, gx1) run the first, the rest the second. Both
 // use the same K, so the same chunking W, and each keeps the arithmetic of its own launch.
-template <int EPI1, int EPI2, int W>
+template <int EPI1, int EPI2, int W, int MT>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
 qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2) {
-  constexpr int R1 = SmallCfg<FMT_BF16, EPI1, W, 1, 1>::RED, R2 = SmallCfg<FMT_BF16, EPI2, W, 1, 1>::RED;
+  constexpr int R1 = SmallCfg<FMT_BF16, EPI1, W, 1, 1, MT>::RED;
+  constexpr int R2 = SmallCfg<FMT_BF16, EPI2, W, 1, 1, MT>::RED;
   __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
   if (static_cast<int>(blockIdx.x) < gx1)
-    small_body<FMT_BF16, EPI1, W, 1, 1>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
+    small_body<FMT_BF16, EPI1, W, 1, 1, MT>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
   else
-    small_body<FMT_BF16, EPI2, W, 1, 1>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
+    small_body<FMT_BF16, EPI2, W, 1, 1, MT>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
 }
 
 // ============================================================================ large-M kernel
@@ -750,13 +787,24 @@ int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16,
 // job's chunks (W = CH or CH / 2, so CPW = 1 or 2): the most work per wavefront that still
 // leaves kSmallMinWaves wavefronts, else the most wavefronts.
 constexpr int64_t kSmallMinWaves = 5120;
+// Fewest m-tiles for which dense bf16 products run two m-tiles per wavefront.
+constexpr int64_t kSmallMt2MinTiles = 4;
 template <int FMT, int EPI, int W, int CPW, int JPW>
 static void launch_small_k(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   constexpr int WAVES = W > 4 ? W : 4;
   const int n_jobs = ((EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16) / JPW;
   const int jobs_per_wg = WAVES / W;
+  // dense bf16 products over kSmallMt2MinTiles or more m-tiles: two per wavefront (weights
+  // read once per 32 rows; below that, halving the grid leaves CUs idle)
+  if constexpr (FMT == FMT_BF16) {
+    if (mtiles >= kSmallMt2MinTiles && !a.offsets && !a.tile_map) {
+      dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>((mtiles + 1) / 2));
+      qmm_small_kernel<FMT, EPI, W, CPW, JPW, 2><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
+      return;
+    }
+  }
   dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mtiles));
-  qmm_small_kernel<FMT, EPI, W, CPW, JPW><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
+  qmm_small_kernel<FMT, EPI, W, CPW, JPW, 1><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
 }
 
 struct SmallShape {
@@ -851,8 +899,13 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
   constexpr int JPWG = WAVES / W;
   const int n1 = a1.n_rows / 16, n2 = a2.n_rows / 32;   // fp32 epilogue jobs, SwiGLU jobs
   const int gx1 = (n1 + JPWG - 1) / JPWG, gx2 = (n2 + JPWG - 1) / JPWG;
-  qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W>
-      <<<dim3(gx1 + gx2, static_cast<unsigned>(mtiles)), 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+  if (mtiles >= kSmallMt2MinTiles)   // two m-tiles per wavefront, as in launch_small_k
+    qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2>
+        <<<dim3(gx1 + gx2, static_cast<unsigned>((mtiles + 1) / 2)), 64 * WAVES, 0, stream>>>(
+            a1, n1, gx1, a2, n2);
+  else
+    qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1>
+        <<<dim3(gx1 + gx2, static_cast<unsigned>(mtiles)), 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
 }
 
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream) {
