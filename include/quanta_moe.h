@@ -165,9 +165,10 @@ size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format, in
 int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* w, int64_t N, int k, int H,
                  const uint16_t* shared_out, const float* shared_gate, uint16_t* y, void* stream);
 
-/* Bit-exact dequant of a native affine int4-g64 stack: out[rows, in] bf16 =
- * bf16(fma(scale, code, bias)). Replaces mx.dequantize (src/quanta/bake/quant.py:32-36;
- * src/quanta/qwen35/artifact.py:105-115). */
+/* Bit-exact dequant of a native affine int4-g64 or int8-g64 stack: out[rows, in] bf16 =
+ * bf16(fma(scale, code, bias)), codes LSB-first (8 or 4 per u32 word). Replaces mx.dequantize
+ * (src/quanta/bake/quant.py:32-36; src/quanta/qwen35/artifact.py:105-115); int8 g64 is the
+ * bake's shared-expert format (src/quanta/qwen35/bake.py:106-110, 143-151). */
 int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias, int64_t rows,
                  int64_t in_features, int bits, int group_size, uint16_t* out, void* stream);
 

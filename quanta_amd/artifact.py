@@ -1,0 +1,220 @@
+"""Reader of the MoE blocks of a quanta artifact (the reference's baked model format) into the
+tensors quanta_amd takes, so real bakes feed the kernels.
+
+Format (written by the reference's ArtifactWriter, src/quanta/bake/artifact.py:44-85; read by
+Qwen35Artifact, src/quanta/qwen35/artifact.py:35-229):
+  * `model.safetensors.index.json`: {"weight_map": {tensor name: shard file name}};
+  * `manifest.json`: {"format": "quanta", "tensors": {key: entry}} with entry
+    {"format": "affine_packed", "bits", "group_size"} for a quantized weight stored at
+    `key.weight_packed` (uint32 codes, LSB-first, [.., out, in*bits/32]) plus `key.weight_scale`
+    and `key.weight_bias` ([.., out, in/group_size]), or {"format": "dense", "dtype"} for a tensor
+    stored verbatim under `key`;
+  * `config.json`: the source model config, decoder fields under `text_config`
+    (src/quanta/qwen35/config.py:258-364);
+  * the shards: safetensors files.
+MoE keys of layer i (src/quanta/qwen35/loader.py:49,74; src/quanta/qwen35/bake.py:143-155):
+`model.language_model.layers.{i}.mlp.` + `gate.weight` (dense), `shared_expert_gate.weight`
+(dense), `shared_expert.{gate,up,down}_proj` (int8 g64 affine, or dense),
+`experts.gate_up_proj` / `experts.down_proj` (int4 g64 affine, pre-stacked [E, out, in]).
+
+Shards are memory-mapped: a tensor is a view of the mapping (no host copy) until it is copied to
+the device. Resolution and errors follow Qwen35Artifact: an unknown manifest format raises
+ValueError, a missing key KeyError, a non-quanta directory ValueError. Quantized weights that the
+block reads as bf16 (the shared expert) are dequantized on the GPU by `qmoe_dequant` (int4 or int8,
+group 64); the routed expert stacks stay packed.
+"""
+
+from __future__ import annotations
+
+import json
+import struct
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from quanta_amd import ops
+from quanta_amd.moe import MoEConfig, Qwen35MoEModule
+
+LM_PREFIX = "model.language_model."                       # src/quanta/qwen35/loader.py:49
+SHARED_EXPERT_PROJS = ("gate_proj", "up_proj", "down_proj")   # src/quanta/qwen35/loader.py:74
+_WEIGHT_SUFFIX = ".weight"
+
+# safetensors dtype -> (numpy storage dtype, torch view dtype or None)
+_ST_DTYPES = {
+    "BF16": (np.uint16, torch.bfloat16),
+    "F16": (np.float16, None),
+    "F32": (np.float32, None),
+    "F64": (np.float64, None),
+    "U8": (np.uint8, None),
+    "I8": (np.int8, None),
+    "I16": (np.int16, None),
+    "U16": (np.uint16, torch.uint16),
+    "I32": (np.int32, None),
+    "U32": (np.uint32, torch.uint32),
+    "I64": (np.int64, None),
+    "BOOL": (np.bool_, None),
+}
+
+
+class _Shard:
+    """One safetensors file, mapped: 8-byte little-endian header length, JSON header
+    {name: {dtype, shape, data_offsets}}, then the data section."""
+
+    def __init__(self, path: Path) -> None:
+        with open(path, "rb") as f:
+            n = struct.unpack("<Q", f.read(8))[0]
+            header = json.loads(f.read(n))
+        self.path = path
+        self.meta = {k: v for k, v in header.items() if k != "__metadata__"}
+        self.base = 8 + n
+        # copy-on-write mapping: torch needs a writable array, nothing is written back
+        self.mm = np.memmap(path, dtype=np.uint8, mode="c")
+
+    def tensor(self, name: str) -> torch.Tensor:
+        m = self.meta[name]
+        if m["dtype"] not in _ST_DTYPES:
+            raise ValueError(f"{self.path.name}: {name}: unsupported safetensors dtype {m['dtype']}")
+        npdt, tdt = _ST_DTYPES[m["dtype"]]
+        b, e = m["data_offsets"]
+        raw = self.mm[self.base + b:self.base + e]
+        if (self.base + b) % np.dtype(npdt).itemsize:
+            raw = np.array(raw)   # unaligned in the file: one host copy
+        arr = raw.view(npdt).reshape(m["shape"])
+        t = torch.from_numpy(arr)
+        return t.view(tdt) if tdt is not None else t
+
+
+class QuantaArtifact:
+    """Lazy reader over a quanta artifact directory (src/quanta/qwen35/artifact.py:38-50)."""
+
+    def __init__(self, art_dir: str | Path) -> None:
+        self.dir = Path(art_dir)
+        self.weight_map: dict[str, str] = json.loads(
+            (self.dir / "model.safetensors.index.json").read_text())["weight_map"]
+        man = json.loads((self.dir / "manifest.json").read_text())
+        if man.get("format") != "quanta":
+            raise ValueError(f"{self.dir}: not a quanta artifact (format={man.get('format')!r})")
+        self.manifest: dict[str, dict] = man["tensors"]
+        cfg_path = self.dir / "config.json"
+        self.config: dict = json.loads(cfg_path.read_text()) if cfg_path.exists() else {}
+        self._shards: dict[str, _Shard] = {}
+
+    # --- tensors --------------------------------------------------------------------------
+    def get(self, name: str) -> torch.Tensor:
+        """One tensor verbatim by its exact key, as a host view of the mapped shard
+        (src/quanta/qwen35/artifact.py:54-63)."""
+        if name not in self.weight_map:
+            raise KeyError(f"tensor not in artifact index: {name}")
+        fn = self.weight_map[name]
+        shard = self._shards.get(fn)
+        if shard is None:
+            shard = self._shards[fn] = _Shard(self.dir / fn)
+        return shard.tensor(name)
+
+    def has(self, key: str) -> bool:
+        """True iff a logical key resolves: a dense entry, or a quantized base
+        (src/quanta/qwen35/artifact.py:65-70)."""
+        if key in self.weight_map:
+            return True
+        base = key[:-len(_WEIGHT_SUFFIX)] if key.endswith(_WEIGHT_SUFFIX) else key
+        return self.manifest.get(base, {}).get("format") == "affine_packed"
+
+    def release(self) -> None:
+        """Drop the shard mappings (src/quanta/qwen35/artifact.py:72-74)."""
+        self._shards.clear()
+
+    def _meta(self, key: str) -> tuple[str, dict]:
+        """A logical key -> (base, manifest entry): a dense entry at the full key, else the
+        affine_packed base (the key without a trailing `.weight`)
+        (src/quanta/qwen35/artifact.py:77-94)."""
+        meta = self.manifest.get(key)
+        if meta is not None and meta.get("format") == "dense":
+            return key, meta
+        base = key[:-len(_WEIGHT_SUFFIX)] if key.endswith(_WEIGHT_SUFFIX) else key
+        bmeta = self.manifest.get(base)
+        if bmeta is not None and bmeta.get("format") == "affine_packed":
+            return base, bmeta
+        for cand, cmeta in ((key, meta), (base, bmeta)):
+            if cmeta is not None:
+                raise ValueError(f"{cand}: unknown manifest format {cmeta.get('format')!r}")
+        raise KeyError(f"{key}: not in artifact manifest (no dense entry, no quantized base {base!r})")
+
+    def read(self, key: str, device: torch.device | str) -> torch.Tensor:
+        """A bf16 weight on `device` for a logical key: a dense tensor cast to bf16, or an
+        affine_packed one dequantized on the GPU (src/quanta/qwen35/artifact.py:96-123)."""
+        base, meta = self._meta(key)
+        if meta["format"] == "dense":
+            return self.get(base).to(device).to(torch.bfloat16)
+        tr = self.packed_triplet(base, device)
+        if tr["group_size"] != 64 or tr["bits"] not in (4, 8):
+            raise ValueError(f"{base}: dequant of bits={tr['bits']} group_size={tr['group_size']} "
+                             "is not supported (int4 or int8, group 64)")
+        return ops.dequant(tr["packed"], tr["scale"], tr["bias"], bits=tr["bits"],
+                           group_size=tr["group_size"])
+
+    def packed_triplet(self, base: str, device: torch.device | str) -> dict:
+        """The packed affine triplet {packed, scale, bias, group_size, bits} of `base`, verbatim,
+        on `device`; the decode width comes from the manifest
+        (src/quanta/qwen35/artifact.py:187-203). Not an affine_packed weight: ValueError."""
+        meta = self.manifest.get(base)
+        if meta is None or meta.get("format") != "affine_packed":
+            raise ValueError(f"{base}: not an affine_packed weight (format="
+                             f"{None if meta is None else meta.get('format')!r})")
+        packed = self.get(base + ".weight_packed")
+        if packed.dtype == torch.uint32:
+            packed = packed.view(torch.int32)
+        return {"packed": packed.to(device),
+                "scale": self.get(base + ".weight_scale").to(device),
+                "bias": self.get(base + ".weight_bias").to(device),
+                "group_size": int(meta["group_size"]),
+                "bits": int(meta["bits"])}
+
+    # --- the MoE block --------------------------------------------------------------------
+    def moe_packed(self, i: int, device: torch.device | str, *, prefix: str = LM_PREFIX) -> dict:
+        """The parameter dict of layer i's MoE block for `qwen35_moe`: the routed experts as packed
+        triplets, the router gate, the shared expert and its gate in bf16
+        (src/quanta/qwen35/artifact.py:205-229). A block without a shared expert omits its keys."""
+        p = f"{prefix}layers.{i}.mlp."
+        out: dict[str, object] = {
+            "gate": self.read(p + "gate.weight", device),
+            "experts_gate_up": self.packed_triplet(p + "experts.gate_up_proj", device),
+            "experts_down": self.packed_triplet(p + "experts.down_proj", device),
+        }
+        if self.has(p + "shared_expert.gate_proj.weight"):
+            for proj in SHARED_EXPERT_PROJS:
+                out[f"shared_{proj}"] = self.read(p + f"shared_expert.{proj}.weight", device)
+            if self.has(p + "shared_expert_gate.weight"):
+                out["shared_expert_gate"] = self.read(p + "shared_expert_gate.weight", device)
+        return out
+
+    def moe_config(self) -> MoEConfig:
+        """The MoE fields of the artifact's config.json (`text_config` when nested), with the
+        reference's defaults (src/quanta/qwen35/config.py:340-364)."""
+        tc = self.config.get("text_config", self.config)
+        return MoEConfig(
+            hidden_size=int(tc["hidden_size"]),
+            num_experts=int(tc["num_experts"]),
+            num_experts_per_tok=int(tc["num_experts_per_tok"]),
+            moe_intermediate_size=int(tc["moe_intermediate_size"]),
+            shared_expert_intermediate_size=int(tc.get("shared_expert_intermediate_size", 0)),
+            norm_topk_prob=bool(tc.get("norm_topk_prob", True)),
+        )
+
+    def moe_module(self, i: int, device: torch.device | str, *,
+                   prefix: str = LM_PREFIX) -> Qwen35MoEModule:
+        """A Qwen35MoEModule holding layer i's MoE block, as the reference loader builds it
+        (src/quanta/qwen35/loader.py:178-188)."""
+        p = self.moe_packed(i, device, prefix=prefix)
+        m = Qwen35MoEModule(self.moe_config(), device=device)
+        with torch.no_grad():
+            m.gate.copy_(p["gate"])
+            for proj in SHARED_EXPERT_PROJS:
+                if f"shared_{proj}" in p:
+                    getattr(m, f"shared_{proj}").copy_(p[f"shared_{proj}"])
+            if "shared_expert_gate" in p:
+                m.shared_expert_gate.copy_(p["shared_expert_gate"])
+            else:   # an ungated shared expert
+                m.shared_expert_gate = None
+        m.set_experts_packed(p["experts_gate_up"], p["experts_down"])
+        return m

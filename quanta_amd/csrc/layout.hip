@@ -36,6 +36,31 @@ __global__ void __launch_bounds__(256) dequant_native_kernel(
   out[i] = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// int8: one thread per packed word, 4 byte codes -> 4 bf16 (one 8-byte store), same rounding
+// (s*c exact in float32: 8-bit x 8-bit mantissas). Reference: the int8 g64 shared expert and
+// non-expert weights of the bake (src/quanta/qwen35/bake.py:106-110, 143-151).
+__global__ void __launch_bounds__(256) dequant_native8_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ bias, int64_t n_words, int words_per_row, int groups_per_row,
+    uint2* __restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_words) return;
+  int64_t row = i / words_per_row;
+  int wr = static_cast<int>(i - row * words_per_row);
+  int64_t g = row * groups_per_row + wr / 16;    // 16 words per 64-code group
+  float s = bf16_to_f32(scale[g]);
+  float b = bf16_to_f32(bias[g]);
+  uint32_t w = packed[i];
+  uint32_t o[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float v0 = fmaf(s, static_cast<float>((w >> (16 * j)) & 0xFFu), b);
+    float v1 = fmaf(s, static_cast<float>((w >> (16 * j + 8)) & 0xFFu), b);
+    o[j] = pack_bf16x2(v0, v1);
+  }
+  out[i] = make_uint2(o[0], o[1]);
+}
+
 // Tiled int4 -> natural bf16 [mats][rows][K]; checks the tiled transform is lossless (it undoes
 // the nibble interleave of the stored words).
 __global__ void __launch_bounds__(256) dequant_tiled_kernel(
@@ -136,15 +161,22 @@ using namespace qmoe;
 extern "C" int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                             int64_t rows, int64_t in_features, int bits, int group_size,
                             uint16_t* out, void* stream) {
-  if (bits != 4 || group_size != 64) return fail("qmoe_dequant: only bits=4, group_size=64");
+  if ((bits != 4 && bits != 8) || group_size != 64)
+    return fail("qmoe_dequant: bits 4 or 8 with group_size 64 only");
   if (rows <= 0 || in_features <= 0 || in_features % 64)
     return fail("qmoe_dequant: rows > 0 and in_features % 64 == 0 required");
   if (!packed || !scale || !bias || !out) return fail("qmoe_dequant: null pointer");
-  int64_t n_words = rows * (in_features / 8);
+  const int per_word = 32 / bits;
+  int64_t n_words = rows * (in_features / per_word);
   if (n_words >= (int64_t(1) << 40)) return fail("qmoe_dequant: tensor too large");
-  dequant_native_kernel<<<grid_for(n_words, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
-      packed, scale, bias, n_words, static_cast<int>(in_features / 8),
-      static_cast<int>(in_features / 64), reinterpret_cast<uint4*>(out));
+  if (bits == 4)
+    dequant_native_kernel<<<grid_for(n_words, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        packed, scale, bias, n_words, static_cast<int>(in_features / 8),
+        static_cast<int>(in_features / 64), reinterpret_cast<uint4*>(out));
+  else
+    dequant_native8_kernel<<<grid_for(n_words, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        packed, scale, bias, n_words, static_cast<int>(in_features / 4),
+        static_cast<int>(in_features / 64), reinterpret_cast<uint2*>(out));
   return check_launch("qmoe_dequant");
 }
 

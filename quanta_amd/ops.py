@@ -47,12 +47,14 @@ def _words(t: torch.Tensor, name: str) -> torch.Tensor:
 
 def dequant(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *, bits: int = 4,
             group_size: int = 64) -> torch.Tensor:
-    """Native affine int4-g64 stack [..., rows, K/8] -> bf16 [..., rows, K] (bit-exact:
-    bf16(fma(s, q, b)))."""
+    """Native affine int4-g64 (or int8-g64, bits=8) stack [..., rows, K*bits/32] -> bf16
+    [..., rows, K] (bit-exact: bf16(fma(s, q, b)))."""
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
-    K = packed.shape[-1] * 8
+    if bits not in (4, 8):
+        raise ValueError("dequant: bits must be 4 or 8")
+    K = packed.shape[-1] * (32 // bits)
     if scale.shape != bias.shape or scale.shape[:-1] != packed.shape[:-1] or scale.shape[-1] * 64 != K:
         raise ValueError("dequant: shape mismatch between packed words and scale/bias")
     rows = packed.numel() // packed.shape[-1]
