@@ -144,12 +144,13 @@ def test_quantizer_error_bound_and_product_equality():
     assert np.array_equal(qb.view(torch.int16).numpy().astype(np.uint16), b_bits)
 
 
-def test_dequant_exact_rational():
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_exact_rational(bits):
     """bf16(fp32(s)*q + fp32(b)) checked with exact rationals (independent of numpy rounding)."""
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(5 + bits)
     w = (rng.standard_normal((3, 128)) * 0.05).astype(np.float32)
-    packed, s_bits, b_bits, codes = oq.quantize_rtn(w, 4, 64)
-    got = oq.dequant_bf16_bits(packed, s_bits, b_bits, 128)
+    packed, s_bits, b_bits, codes = oq.quantize_rtn(w, bits, 64)
+    got = oq.dequant_bf16_bits(packed, s_bits, b_bits, 128, bits=bits)
     sf = oq.bf16_bits_to_f32(s_bits)
     bf = oq.bf16_bits_to_f32(b_bits)
     for r, c in itertools.product(range(3), range(128)):
@@ -159,13 +160,15 @@ def test_dequant_exact_rational():
         assert Fraction(float(oq.bf16_bits_to_f32(got[r, c]))) == want, (r, c)
 
 
-def test_dequant_special_codes():
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_special_codes(bits):
+    top = (1 << bits) - 1
     s_bits = oq.f32_to_bf16_bits(np.full((1, 1), 0.0625, np.float32))
     b_bits = oq.f32_to_bf16_bits(np.full((1, 1), -0.5, np.float32))
-    codes = np.array([[0] * 32 + [15] * 32], np.uint32)
-    words = oq.pack_affine(codes, 4)
-    vals = oq.bf16_bits_to_f32(oq.dequant_bf16_bits(words, s_bits, b_bits, 64))
-    assert np.all(vals[0, :32] == -0.5) and np.all(vals[0, 32:] == 15 * 0.0625 - 0.5)
+    codes = np.array([[0] * 32 + [top] * 32], np.uint32)
+    words = oq.pack_affine(codes, bits)
+    vals = oq.bf16_bits_to_f32(oq.dequant_bf16_bits(words, s_bits, b_bits, 64, bits=bits))
+    assert np.all(vals[0, :32] == -0.5) and np.all(vals[0, 32:] == top * 0.0625 - 0.5)
 
 
 # ----------------------------------------------------------------------------------- routing
