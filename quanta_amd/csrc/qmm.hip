@@ -21,10 +21,11 @@
 //      sum_k x_k (s q_k + b) = s * sum_k x_k (128+q_k) + (b - 128 s) * sum_k x_k,
 //    with sum_k x_k from one extra MFMA against a ones fragment. Optional split-K across the
 //    workgroup's wavefronts, reduced through LDS.
-//  * large-M ("prefill"): 128-position x 256-weight-row workgroup tiles, 8 wavefronts; int4
-//    weights are dequantised to fp16 in registers straight from their tiled global layout and
-//    multiplied on v_mfma_f32_16x16x32_f16 against an exactly scaled fp16 copy of the
-//    activations, staged through double-buffered LDS.
+//  * large-M ("prefill"): int4 weights are dequantised to fp16 in registers from an LDS copy of
+//    their tiled layout and multiplied on v_mfma_f32_16x16x32_f16 against an exactly scaled fp16
+//    copy of the activations, staged through LDS. Weight-row counts in 512-row blocks take the
+//    wide kernel (128-position x 512-weight-row workgroup tiles, each wavefront 128 x 64);
+//    others, and bf16 weights, the 128 x 256 kernel (each wavefront 128 x 32).
 #include <type_traits>
 
 #include "qmoe_internal.h"
@@ -728,6 +729,218 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   }
 }
 
+// ============================================================================ wide prefill kernel
+// int4 weights, large-M regime, for weight-row counts that are multiples of 512 (SwiGLU: gate
+// halves that are multiples of 256). Workgroup tile: 128 sorted positions x 512 weight rows
+// (SwiGLU: 256 gate + 256 up rows -> 256 h columns), 8 wavefronts side by side along the
+// weight rows. Wavefront w owns all 128 positions (8 m-blocks of 16) and four 16-row weight
+// tiles (SwiGLU: two gate tiles and their up tiles), so each A fragment read from LDS feeds four
+// MFMAs and every dequantised B fragment feeds eight: half the LDS bytes per MFMA of the
+// 256-row tile, at the same dequant cost per MFMA. Accumulators: 8 x 4 16x16 blocks (128 VGPRs).
+//
+// LDS: two slots of one superblock each, A 32 KiB ([m-block][step][64 lanes] x 16 B, as in the
+// 256-row kernel) + int4 weights 8 x 4.5 KiB (per wavefront its four tiles' 1 KiB code blocks
+// and 4 x 128 B of scale/bias), 136 KiB in all. One barrier per superblock: at the end of
+// superblock p every wavefront waits for its own loads of p+1 (the only ones in flight), the
+// barrier publishes slot p+1 and retires slot p, and the loads of p+2 are issued into slot p at
+// once, landing while p+1 is computed.
+//
+// Per output the summation is the 256-row kernel's (k-steps in order within a superblock,
+// superblocks in order, one fp32 accumulator), so both kernels give identical results.
+constexpr int kWdThreads = 512;
+constexpr int kWdABytes = 8 * 4 * 64 * 16;                 // 32 KiB
+constexpr int kWdBWaveBytes = 4 * 1024 + 4 * 128;          // 4.5 KiB
+constexpr int kWdSlotBytes = kWdABytes + 8 * kWdBWaveBytes; // 68 KiB
+constexpr size_t kWdLdsBytes = 2 * kWdSlotBytes;            // 136 KiB
+
+template <int EPI>
+__global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
+  extern __shared__ u32x4 lds[];
+  char* lds_c = reinterpret_cast<char*>(lds);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int e, m0, m_cnt;
+  // XCD-aware tile order, as in the 256-row kernel (groups of G m-tiles x all nbk weight-row
+  // blocks per XCD, G * nbk <= 32)
+  const int nbk = a.n_rows / 512;
+  const int G = (nbk >= 32) ? 1 : 32 / nbk;
+  const int wi = blockIdx.x, xcd = wi & 7, kx = wi >> 3;
+  const int gk = kx / (G * nbk), rk = kx - gk * (G * nbk);
+  const int mt = (gk * 8 + xcd) * G + rk / nbk;
+  const int cb = rk % nbk;
+  if (mt >= a.mtiles || !resolve_mtile(a, mt, kLargeMTile, e, m0, m_cnt)) return;
+  const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
+  const int nsb = a.K / 128;
+  const int mb_act = __builtin_amdgcn_readfirstlane((m_cnt + 15) >> 4);   // 1..8
+
+  // activation source: wavefront w loads m-block w (see qmm_large_kernel)
+  const bool a_on = wave < mb_act;
+  const char* arow_ptr;
+  {
+    const int r = 16 * wave + (lane & 15);
+    const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
+    arow_ptr = reinterpret_cast<const char*>(a.act16 + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
+               16 * lg_chunk<FMT_INT4>(0, lane >> 4);
+  }
+  const uint32_t lds_base = lds_offset(lds);
+  auto a_slot = [&](int p) { return (p & 1) * kWdSlotBytes; };
+  auto b_slot = [&](int p) { return (p & 1) * kWdSlotBytes + kWdABytes + wave * kWdBWaveBytes; };
+
+  // this wavefront's four weight tiles (SwiGLU: gate tiles first, then their up tiles)
+  const char* wcode[4];
+  const char* wsb[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int tl = (EPI == EPI_SWIGLU)
+                       ? ((t < 2) ? 16 * cb + 2 * wave + t : a.n_rows / 32 + 16 * cb + 2 * wave + (t - 2))
+                       : 32 * cb + 4 * wave + t;
+    const int64_t tb = (ebase + tl) * nsb;
+    wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
+    wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
+  }
+  // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
+  const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
+  const char* sb_src1 = wsb[2 + (lane >> 5)] + 4 * (lane & 31);
+
+  // all loads of superblock p: A 4 (when a_on) + codes 4 + scale/bias 2
+  auto issue = [&](int p) __attribute__((always_inline)) {
+    if (a_on) {
+      const char* src = arow_ptr + 256 * p;
+      const uint32_t dst = lds_base + a_slot(p) + wave * 4 * 1024;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) dma16(src + 16 * (8 * (s >> 1) + (s & 1)), dst + s * 1024);
+    }
+    const uint32_t dst = lds_base + b_slot(p);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dma16(wcode[t] + static_cast<int64_t>(p) * 1024, dst + t * 1024);
+    dma4(sb_src0 + static_cast<int64_t>(p) * 128, dst + 4096);
+    dma4(sb_src1 + static_cast<int64_t>(p) * 128, dst + 4096 + 256);
+  };
+
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t exp_lo = 0x64006400u, exp_hi = 0x54005400u;
+  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  const f16x2_t k64 = {static_cast<_Float16>(64.0f), static_cast<_Float16>(64.0f)};
+  // One superblock: four 32-k steps. Step s is MB slots; slot i issues the four MFMAs of
+  // m-block i, the LDS read of the A fragment two slots ahead, and 16/MB of step s+1's weight
+  // dequant units (tile u/4, nibble pair u%4), in that order (scheduling barriers).
+  auto compute = [&](int p, auto mbc) __attribute__((always_inline)) {
+    constexpr int MB = decltype(mbc)::value;
+    constexpr int UPS = 16 / MB;
+    constexpr int NI = 4 * MB;                 // A fragments (slots) per superblock
+    const u32x4* la = reinterpret_cast<const u32x4*>(lds_c + a_slot(p)) + lane;
+    const char* lb = lds_c + b_slot(p);
+    u32x4 q[4];
+    uint2 sbv[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
+      sbv[t] = reinterpret_cast<const uint2*>(lb + 4096 + t * 128)[lane & 15];
+    }
+    f16x2_t s2[4], b2[4];
+    auto sb_conv = [&](int grp) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t sbw = grp ? sbv[t].y : sbv[t].x;
+        const _Float16 sv = static_cast<_Float16>(bf16lo_to_f32(sbw));
+        const _Float16 bv = static_cast<_Float16>(bf16hi_to_f32(sbw));
+        s2[t] = f16x2_t{sv, sv};
+        b2[t] = f16x2_t{bv, bv};
+      }
+    };
+    auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
+      const int t = u >> 2, j = u & 3;
+      uint32_t r;
+      const uint32_t src = (j >= 2) ? (q[t][s] >> 8) : q[t][s];
+      asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(src),
+          "s"((j & 1) ? 0x00F000F0u : 0x000F000Fu), "v"((j & 1) ? exp_hi : exp_lo));
+      const f16x2_t qq = __builtin_bit_cast(f16x2_t, r) - ((j & 1) ? k64 : k1024);
+      bfo[t][j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qq, s2[t], b2[t]));
+    };
+    u32x4 bf[2][4];
+    u32x4 A[NI];
+    sb_conv(0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) deq_unit(0, u, bf[0]);
+    A[0] = la[0];
+    if (NI > 1) A[1] = la[(MB > 1) ? 256 : 64];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = s & 1;
+      if (s == 1) sb_conv(1);      // group 1 feeds steps 2 and 3
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const int n = s * MB + i;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[i][t] = mfma16_f16(A[n], bf[c][t], acc[i][t]);
+        if (n + 2 < NI) {
+          const int n2 = n + 2, s2i = n2 / MB, i2 = n2 % MB;
+          A[n2] = la[256 * i2 + 64 * s2i];
+        }
+        if (s < 3) {
+#pragma unroll
+          for (int v = 0; v < UPS; ++v) deq_unit(s + 1, i * UPS + v, bf[c ^ 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  auto run = [&](auto mbc) __attribute__((always_inline)) {
+    issue(0);
+    if (nsb > 1) {
+      issue(1);
+      if (a_on) wait_vmcnt<10>(); else wait_vmcnt<6>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lg_barrier();
+    for (int p = 0; p < nsb; ++p) {
+      compute(p, mbc);
+      if (p + 1 < nsb) {
+        wait_vmcnt<0>();
+        lg_barrier();
+        if (p + 2 < nsb) issue(p + 2);
+      }
+    }
+  };
+  if (mb_act <= 2) run(std::integral_constant<int, 2>{});
+  else if (mb_act <= 4) run(std::integral_constant<int, 4>{});
+  else run(std::integral_constant<int, 8>{});
+
+  // epilogue: lane holds C[row 4(lane/16) + j][col lane%16] of each 16x16 block
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i >= mb_act) break;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int mr = 16 * i + 4 * (lane >> 4) + j;
+      if (mr >= m_cnt) continue;
+      const int64_t ar2 = act_row(a, m0 + mr);
+      const bool ok = ar2 >= 0;
+      const float rs = ok ? a.row_sinv[ar2] : 1.0f;
+      if (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int col = 256 * cb + 32 * wave + 16 * t + (lane & 15);
+          store_out<EPI>(a, m0 + mr, col, ok ? acc[i][t][j] * rs : 0.f, ok ? acc[i][t + 2][j] * rs : 0.f);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int col = 512 * cb + 64 * wave + 16 * t + (lane & 15);
+          store_out<EPI>(a, m0 + mr, col, ok ? acc[i][t][j] * rs : 0.f, 0.f);
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- fp16 activation copy
 // One workgroup per row: absmax, then act16 = fp16(act * 2^(14 - e)) with 2^(e-1) <= absmax < 2^e,
 // so every value sits below 2^14 and all bf16 values within 2^28 of the row maximum convert
@@ -893,6 +1106,23 @@ static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   return 0;
 }
 
+// 1-D grid in the XCD-grouped order the wide kernel decodes (as in launch_large, with 512-row
+// weight blocks)
+template <int EPI>
+static int launch_wide(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
+  const hipError_t err =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_wide_kernel<EPI>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kWdLdsBytes));
+  if (err != hipSuccess) return fail(std::string("qmm(wide): LDS attribute: ") + hipGetErrorString(err));
+  const int nbk = a.n_rows / 512;
+  const int G = (nbk >= 32) ? 1 : 32 / nbk;
+  const int64_t mpad = (mtiles + 8 * G - 1) / (8 * G) * (8 * G);
+  QmmArgs b = a;
+  b.mtiles = static_cast<int>(mtiles);
+  qmm_wide_kernel<EPI><<<dim3(static_cast<unsigned>(mpad * nbk)), kWdThreads, kWdLdsBytes, stream>>>(b);
+  return 0;
+}
+
 template <int W>
 static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream) {
   constexpr int WAVES = W > 4 ? W : 4;
@@ -965,7 +1195,12 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       return fail("qmm(large): int4 weights need the fp16 activation copy");
     int rc;
 #define QMOE_LARGE(F, P) rc = launch_large<F, P>(a, mtile_bound, stream)
-    if (fmt == FMT_INT4) {
+    // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves) take the wide kernel
+    if (fmt == FMT_INT4 && a.n_rows % 512 == 0) {
+      if (epi == EPI_SWIGLU) rc = launch_wide<EPI_SWIGLU>(a, mtile_bound, stream);
+      else if (epi == EPI_BF16) rc = launch_wide<EPI_BF16>(a, mtile_bound, stream);
+      else rc = launch_wide<EPI_F32>(a, mtile_bound, stream);
+    } else if (fmt == FMT_INT4) {
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT4, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT4, EPI_BF16);
       else QMOE_LARGE(FMT_INT4, EPI_F32);
