@@ -253,7 +253,7 @@ def main():
         per_expert = 2 * I * H * 9 // 16                   # int4 codes + bf16 scale/bias per 64
         kbytes = u_k * per_expert + N * H * 2 + N * k * I * 2
         kern = dict(name="qmm_small_kernel<int4,swiglu,W,CPW,JPW>" if regime == L.REGIME_SMALL
-                    else "act_to_f16 + qmm_large_kernel<int4,swiglu>", us=kms * 1e3, bytes=kbytes,
+                    else "act_to_f16 + qmm_wide_kernel<swiglu>", us=kms * 1e3, bytes=kbytes,
                     U=u_k, mfma=regime == L.REGIME_LARGE, flops=2 * N * k * 2 * I * H)
         log(f"gate_up kernel: {kms * 1e3:.1f} us, {kbytes / kms / 1e6:.0f} GB/s")
 

@@ -53,7 +53,8 @@ extern "C" {
 /* grouped-qmm regimes */
 #define QMOE_REGIME_AUTO 0
 #define QMOE_REGIME_SMALL 1 /* 16-token m-tiles, weights streamed to registers (decode) */
-#define QMOE_REGIME_LARGE 2 /* prefill: experts of > 16 rows on 128x256 LDS-staged fp16 tiles,
+#define QMOE_REGIME_LARGE 2 /* prefill: experts of > 16 rows on 128-row LDS-staged fp16 tiles
+                               (128x512 for int4 weights in 512-row blocks, else 128x256),
                                the others on 16-token m-tiles */
 
 /* grouped-qmm epilogues */
