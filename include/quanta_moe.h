@@ -107,6 +107,26 @@ size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N);
 int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x, int64_t N,
                  uint16_t* y, void* ws, size_t ws_bytes, void* stream);
 
+/* The block with the decoder layer's steps either side of it, as the layer calls it:
+ *   y = bf16(x + bf16(block(rmsnorm(x))))
+ * Replaces post_attention_layernorm -> mlp -> residual add, x = x + mlp(
+ * post_attention_layernorm(x)) (src/quanta/qwen35/model.py:104-105; the batched decode step
+ * src/quanta/qwen35/batched_runtime.py:304-306). rmsnorm(x) = bf16(norm_w * (x * rsqrt(mean(x^2)
+ * + eps))) in fp32, norm_w [H] bf16 being nn.RMSNorm's resident weight (source weight + 1,
+ * src/quanta/qwen35/runtime.py:57-63). The normalised rows live in the workspace; the residual
+ * add is fused into the block's final combine; y may alias x. */
+size_t qmoe_forward_residual_workspace(const qmoe_config_t* cfg, int64_t N);
+int qmoe_forward_residual(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x,
+                          const uint16_t* norm_w, float eps, int64_t N, uint16_t* y, void* ws,
+                          size_t ws_bytes, void* stream);
+
+/* RMSNorm rows alone (the same arithmetic as qmoe_forward_residual's norm):
+ * out[t] = bf16(w * (x[t] * rsqrt(mean(x[t]^2) + eps))), fp32 math, H % 8 == 0. Replaces
+ * nn.RMSNorm / mx.fast.rms_norm as the reference restates it (src/quanta/qwen35/
+ * attention.py:113-117; src/quanta/qwen35/mtp.py:40-42). */
+int qmoe_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float eps, uint16_t* out,
+                 void* stream);
+
 /* Top-k selection from router logits [N, ld_logits] (fp32): softmax or sigmoid scores,
  * optional correction bias [E] for selection, group-limited selection when n_group > 1,
  * renormalisation (+1e-20) and routed_scale. Outputs idx[N,k] (int32, canonical order:

@@ -31,6 +31,27 @@ def _sigmoid(v: np.ndarray) -> np.ndarray:
     return 1.0 / (1.0 + np.exp(-v))
 
 
+# ----------------------------------------------------------------------------- layer norm
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """The decoder layer's post_attention_layernorm in front of the block
+    (`src/quanta/qwen35/model.py:104-105`): w * (x * rsqrt(mean(x^2) + eps)) over the last dim, as
+    the reference restates its norms (`src/quanta/qwen35/attention.py:113-117`,
+    `src/quanta/qwen35/mtp.py:40-42`: fp32 math, one rounding to the input dtype). Here in
+    float64 and unrounded; `w` is nn.RMSNorm's resident weight (checkpoint weight + 1,
+    `src/quanta/qwen35/runtime.py:57-63`). MLX's own reduction order inside mx.fast.rms_norm is
+    parity unpinned at the MLX boundary (a last-bit difference in bf16 at most)."""
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return w * (x * r)
+
+
+def residual_add(x: np.ndarray, block_out_bf16: np.ndarray) -> np.ndarray:
+    """x + mlp(...) of the decoder layer (`src/quanta/qwen35/model.py:104-105`): both bf16, the
+    sum rounded once to bf16 (an fp32 add of two bf16 values then RNE)."""
+    return round_bf16(x + block_out_bf16)
+
+
 # ----------------------------------------------------------------------------- routing
 
 

@@ -6,10 +6,12 @@ include/quanta_moe.h (`quanta_amd/_qmoe.so`, built by `python -m quanta_amd.buil
 """
 
 from quanta_amd.moe import (MoEConfig, Qwen35MoEModule, TiledExperts, prepare, qwen35_moe,
-                            qwen35_route, tile_experts_bf16, tile_experts_packed)
+                            qwen35_moe_residual, qwen35_route, tile_experts_bf16,
+                            tile_experts_packed)
 from quanta_amd.quant import pack_affine, quantize_affine, unpack_affine
 
 __all__ = [
-    "MoEConfig", "Qwen35MoEModule", "TiledExperts", "prepare", "qwen35_moe", "qwen35_route",
+    "MoEConfig", "Qwen35MoEModule", "TiledExperts", "prepare", "qwen35_moe", "qwen35_moe_residual",
+    "qwen35_route",
     "tile_experts_bf16", "tile_experts_packed", "pack_affine", "quantize_affine", "unpack_affine",
 ]

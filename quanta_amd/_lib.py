@@ -74,6 +74,10 @@ SIGNATURES = {
     "qmoe_forward_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),
     "qmoe_forward": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _I64, _P, _P,
                           ctypes.c_size_t, _P]),
+    "qmoe_forward_residual_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),
+    "qmoe_forward_residual": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _P, _F,
+                                   _I64, _P, _P, ctypes.c_size_t, _P]),
+    "qmoe_rmsnorm": (_I, [_P, _P, _I64, _I, _F, _P, _P]),
     "qmoe_router_topk": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P]),
     "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
     "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),

@@ -199,7 +199,16 @@ class QuantaArtifact:
             moe_intermediate_size=int(tc["moe_intermediate_size"]),
             shared_expert_intermediate_size=int(tc.get("shared_expert_intermediate_size", 0)),
             norm_topk_prob=bool(tc.get("norm_topk_prob", True)),
+            norm_eps=float(tc.get("rms_norm_eps", 1e-6)),
         )
+
+    def post_attention_norm(self, i: int, device: torch.device | str, *,
+                            prefix: str = LM_PREFIX) -> torch.Tensor:
+        """Layer i's post_attention_layernorm weight in its resident form, source + 1 in bf16, as
+        the reference wires it into nn.RMSNorm (key: src/quanta/qwen35/loader.py:136-142; the +1:
+        src/quanta/qwen35/runtime.py:57-63,121): the `norm_weight` of `qwen35_moe_residual`."""
+        w = self.read(f"{prefix}layers.{i}.post_attention_layernorm.weight", device)
+        return (w.to(torch.bfloat16) + 1.0).to(torch.bfloat16)
 
     def moe_module(self, i: int, device: torch.device | str, *,
                    prefix: str = LM_PREFIX) -> Qwen35MoEModule:

@@ -36,10 +36,19 @@ int check_launch(const char* what) {
 
 // One 64-thread workgroup per (token, 512 features): the k slot rows are gathered through inv
 // with their loads issued together (8 at a time), then summed in slot order.
+// With resid (the block entry that carries the decoder layer's residual add), the bf16 block
+// output is added to the residual row and rounded again: y = bf16(resid + bf16(moe)), the
+// reference's bf16 `x + mlp(...)`; y may then alias resid (each element is read and written by
+// the same thread).
+__device__ __forceinline__ uint32_t add_resid(uint32_t packed_moe, uint32_t r) {
+  return pack_bf16x2(bf16lo_to_f32(r) + bf16lo_to_f32(packed_moe),
+                     bf16hi_to_f32(r) + bf16hi_to_f32(packed_moe));
+}
+
 __global__ void __launch_bounds__(64) combine_kernel(
     const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
     int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ shared_out,
-    const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
+    const float* __restrict__ shared_gate, const uint16_t* resid, uint16_t* y) {
   const int t = blockIdx.y;
   const int h8 = (blockIdx.x * 64 + threadIdx.x) * 8;
   if (h8 >= H) return;
@@ -83,15 +92,20 @@ __global__ void __launch_bounds__(64) combine_kernel(
   o[1] = pack_bf16x2(acc[2], acc[3]);
   o[2] = pack_bf16x2(acc[4], acc[5]);
   o[3] = pack_bf16x2(acc[6], acc[7]);
+  if (resid) {
+    const u32x4 r = *reinterpret_cast<const u32x4*>(resid + static_cast<int64_t>(t) * H + h8);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = add_resid(o[q], r[q]);
+  }
   *reinterpret_cast<u32x4*>(y + static_cast<int64_t>(t) * H + h8) = o;
 }
 
 int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
                    const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
-                   hipStream_t stream) {
+                   hipStream_t stream, const uint16_t* resid) {
   dim3 grid((H + 511) / 512, N);
   combine_kernel<<<grid, 64, 0, stream>>>(d, inv, w, N, k, H, static_cast<int64_t>(N) * k,
-                                          shared_out, shared_gate, y);
+                                          shared_out, shared_gate, resid, y);
   return check_launch("combine");
 }
 
@@ -111,7 +125,8 @@ template <int MT>
 __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
     int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ sh_h, int Is, int nch,
-    const u32x4* __restrict__ wd, const float* __restrict__ shared_gate, uint16_t* __restrict__ y) {
+    const u32x4* __restrict__ wd, const float* __restrict__ shared_gate, const uint16_t* resid,
+    uint16_t* y) {
   constexpr int TOK = 16 * MT;   // tokens per workgroup
   __shared__ f32x4_t part[kCsWaves][MT][64];
   __shared__ float sh[TOK][17];
@@ -202,14 +217,18 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     const int t = tm + tl;
     if (t < N) {
       const float g = shared_gate ? shared_gate[t] : 1.0f;
-      y[static_cast<int64_t>(t) * H + col] = f32_to_bf16(fmaf(sh[tl][f], g, routed[tl][f]));
+      const int64_t o = static_cast<int64_t>(t) * H + col;
+      uint16_t v = f32_to_bf16(fmaf(sh[tl][f], g, routed[tl][f]));
+      if (resid) v = f32_to_bf16(bf16_to_f32(resid[o]) + bf16_to_f32(v));   // see add_resid
+      y[o] = v;
     }
   }
 }
 
 int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
                           int H, const uint16_t* sh_h, int Is, const uint16_t* wd,
-                          const float* shared_gate, uint16_t* y, hipStream_t stream) {
+                          const float* shared_gate, uint16_t* y, hipStream_t stream,
+                          const uint16_t* resid) {
   const int nch = bf16_chunks(Is);
   if (H % 16 || Is % 32 || Is <= 0 || nch > kCsWaves)
     return fail("combine: fused shared down needs H % 16 == 0, Is % 32 == 0, Is < 4096");
@@ -219,12 +238,12 @@ int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w,
     dim3 grid(H / 16, (N + 31) / 32);
     combine_shared_kernel<2><<<grid, 64 * kCsWaves, 0, stream>>>(
         d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
-        reinterpret_cast<const u32x4*>(wd), shared_gate, y);
+        reinterpret_cast<const u32x4*>(wd), shared_gate, resid, y);
   } else {
     dim3 grid(H / 16, (N + 15) / 16);
     combine_shared_kernel<1><<<grid, 64 * kCsWaves, 0, stream>>>(
         d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
-        reinterpret_cast<const u32x4*>(wd), shared_gate, y);
+        reinterpret_cast<const u32x4*>(wd), shared_gate, resid, y);
   }
   return check_launch("combine_shared");
 }
@@ -444,8 +463,10 @@ static int pick_regime(const qmoe_config_t& c, int64_t N) {
   return dense_regime(c, N);
 }
 
-extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
-                            int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream_) {
+// The block on x; with resid, the combine adds the decoder layer's residual row.
+static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
+                        int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream_,
+                        const uint16_t* resid) {
   if (!cfg || !wts || !x || !y || !ws) return fail("qmoe_forward: null pointer");
   const qmoe_config_t& c = *cfg;
   int rc = validate_config(c);
@@ -656,7 +677,36 @@ extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
   // 7. unpermute + weighted combine + gated shared (its down projection fused when decoding) + bf16
   if (fuse_dn)
     return launch_combine_shared(d, inv, wv, n, c.top_k, c.hidden, sh_h, c.shared_inter, wts->sh_dn,
-                                 has_sg ? sg : nullptr, y, stream);
+                                 has_sg ? sg : nullptr, y, stream, resid);
   return launch_combine(d, inv, wv, n, c.top_k, c.hidden, shared ? sh_out : nullptr,
-                        has_sg ? sg : nullptr, y, stream);
+                        has_sg ? sg : nullptr, y, stream, resid);
+}
+
+extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
+                            int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
+  return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream, nullptr);
+}
+
+// The block with the decoder layer's steps either side of it: the normalised rows go to the
+// end of the workspace, the block runs on them, and the combine adds the residual.
+extern "C" size_t qmoe_forward_residual_workspace(const qmoe_config_t* cfg, int64_t N) {
+  if (!cfg || N <= 0 || N > 65535 || cfg->hidden <= 0) return 0;
+  return ws_layout(*cfg, N).total + align256(static_cast<size_t>(N) * cfg->hidden * 2);
+}
+
+extern "C" int qmoe_forward_residual(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
+                                     const uint16_t* x, const uint16_t* norm_w, float eps,
+                                     int64_t N, uint16_t* y, void* ws, size_t ws_bytes,
+                                     void* stream) {
+  if (!cfg || !wts || !x || !norm_w || !y || !ws) return fail("qmoe_forward_residual: null pointer");
+  int rc = validate_config(*cfg);
+  if (rc) return rc;
+  if (N <= 0 || N > 65535) return fail("qmoe_forward_residual: 0 < N <= 65535 tokens per call");
+  const size_t main = ws_layout(*cfg, N).total;
+  if (ws_bytes < qmoe_forward_residual_workspace(cfg, N))
+    return fail("qmoe_forward_residual: workspace too small");
+  uint16_t* xn = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + main);
+  rc = launch_rmsnorm(x, norm_w, N, cfg->hidden, eps, xn, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  return forward_impl(cfg, wts, xn, N, y, ws, main, stream, x);
 }

@@ -210,9 +210,11 @@ inline int bf16_chunks(int K) {
 // fp32 epilogue (router logits), a2 with SwiGLU (shared expert gate_up).
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream);
 // Decode combine with the shared expert's down projection fused in (wd: tiled bf16 [H, Is]).
+// resid (nullable): the decoder layer's residual row, y = bf16(resid + bf16(block output)).
 int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
                           int H, const uint16_t* sh_h, int Is, const uint16_t* wd,
-                          const float* shared_gate, uint16_t* y, hipStream_t stream);
+                          const float* shared_gate, uint16_t* y, hipStream_t stream,
+                          const uint16_t* resid = nullptr);
 // act [rows][K] bf16 -> act16 fp16 with a per-row power-of-two scale (exact for bf16 values
 // within 2^28 of the row's largest magnitude); row_sinv[r] = the inverse scale.
 int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16, float* row_sinv,
@@ -223,6 +225,9 @@ inline size_t act16_ws_bytes(int64_t rows, int K) {
 }
 int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
                    const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
+                   hipStream_t stream, const uint16_t* resid = nullptr);
+// RMSNorm rows: out = bf16(w * (x * rsqrt(mean(x^2) + eps))) in fp32 (norm.hip).
+int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float eps, uint16_t* out,
                    hipStream_t stream);
 
 constexpr int kSmallMTile = 16;

@@ -45,6 +45,7 @@ class MoEConfig:
     n_group: int = 1
     topk_group: int = 1
     routed_scaling_factor: float = 1.0
+    norm_eps: float = 1e-6
 
     @property
     def moe_gate_up_out(self) -> int:
@@ -429,6 +430,54 @@ def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chun
     return y.reshape(b, s, hidden)
 
 
+def qwen35_moe_residual(x: torch.Tensor, p: dict, cfg, norm_weight: torch.Tensor, *,
+                        eps: float | None = None, sparse: bool = True, token_chunk: int = 8192,
+                        topk_override: int | None = None,
+                        regime: int = L.REGIME_AUTO) -> torch.Tensor:
+    """The decoder layer's MoE half, x + qwen35_moe(post_attention_layernorm(x)), as one call.
+
+    Mirrors `x = x + self.mlp(self.post_attention_layernorm(x), ...)`
+    (src/quanta/qwen35/model.py:104-105; src/quanta/qwen35/batched_runtime.py:304-306).
+    `norm_weight` [H] bf16 is nn.RMSNorm's resident weight (the checkpoint weight + 1,
+    src/quanta/qwen35/runtime.py:57-63); `eps` defaults to the config's `norm_eps`. The norm is
+    fp32 math rounded once to bf16 (the reference's own restatement, src/quanta/qwen35/
+    attention.py:113-117), the block runs on the normalised rows, and the bf16 residual add is
+    fused into the block's combine: y = bf16(x + bf16(block)). `sparse=False` runs the same norm
+    and add around the run-every-expert oracle path.
+    """
+    if x.dim() != 3:
+        raise ValueError("x must be [B, S, hidden]")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bf16 (got {x.dtype}); the block computes on bf16 activations")
+    b, s, hidden = x.shape
+    if norm_weight.dtype != torch.bfloat16 or tuple(norm_weight.shape) != (hidden,):
+        raise ValueError("norm_weight must be bf16 [hidden]")
+    eps = float(_cfg(cfg, "norm_eps", 1e-6) if eps is None else eps)
+    n = b * s
+    if not sparse or n == 0:
+        xf = x.reshape(n, hidden).contiguous()
+        xn = ops.rmsnorm(xf, norm_weight.contiguous(), eps) if n else xf
+        y = qwen35_moe(xn.reshape(b, s, hidden), p, cfg, sparse=sparse, token_chunk=token_chunk,
+                       topk_override=topk_override, regime=regime)
+        return (x.float() + y.float()).to(torch.bfloat16)
+    k_max = int(_cfg(cfg, "num_experts_per_tok"))
+    topk = topk_override if topk_override is not None else k_max
+    if topk < 1 or topk > k_max:
+        raise ValueError(f"topk_override {topk_override} must be in [1, {k_max}]")
+    pr = prepare(p, cfg, topk=topk, regime=regime)
+    xf = x.reshape(n, hidden).contiguous()
+    nw = norm_weight.contiguous()
+    chunk = token_chunk if token_chunk and token_chunk > 0 else n
+    chunk = min(chunk, 65535)
+    y = torch.empty_like(xf)
+    ws = torch.empty(max(ops.forward_residual_workspace(pr.cfg, min(n, chunk)), 1),
+                     dtype=torch.uint8, device=x.device)
+    for c0 in range(0, n, chunk):
+        c1 = min(c0 + chunk, n)
+        ops.forward_residual(pr.cfg, pr.weights, xf[c0:c1], nw, eps, out=y[c0:c1], ws=ws)
+    return y.reshape(b, s, hidden)
+
+
 class Qwen35MoEModule(torch.nn.Module):
     """Module wrapper over :func:`qwen35_moe` holding the router, expert and shared params
     (src/quanta/qwen35/model.py:28-70).
@@ -486,3 +535,10 @@ class Qwen35MoEModule(torch.nn.Module):
                 topk_override: int | None = None) -> torch.Tensor:
         return qwen35_moe(x, self._params(), self.cfg, sparse=sparse, token_chunk=self.token_chunk,
                           topk_override=topk_override)
+
+    def forward_residual(self, x: torch.Tensor, norm_weight: torch.Tensor, *,
+                         eps: float | None = None, sparse: bool = True,
+                         topk_override: int | None = None) -> torch.Tensor:
+        """x + self(post_attention_layernorm(x)) in one call (:func:`qwen35_moe_residual`)."""
+        return qwen35_moe_residual(x, self._params(), self.cfg, norm_weight, eps=eps, sparse=sparse,
+                                   token_chunk=self.token_chunk, topk_override=topk_override)

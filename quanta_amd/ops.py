@@ -256,3 +256,43 @@ def forward(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
     L.check(L.load().qmoe_forward(ctypes.byref(cfg), ctypes.byref(weights), _p(x), N, _p(out),
                                   _p(ws), ws.numel(), _stream(x.device)), "qmoe_forward")
     return out
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm rows of x [N, H] bf16 with the resident bf16 weight [H] (qmoe_rmsnorm):
+    bf16(weight * (x * rsqrt(mean(x^2) + eps))) in fp32."""
+    _need(x, torch.bfloat16, "x")
+    _need(weight, torch.bfloat16, "weight")
+    if x.dim() != 2 or weight.shape != (x.shape[1],):
+        raise ValueError("rmsnorm: x must be [N, H] and weight [H]")
+    if out is None:
+        out = torch.empty_like(x)
+    L.check(L.load().qmoe_rmsnorm(_p(x), _p(weight), x.shape[0], x.shape[1], float(eps), _p(out),
+                                  _stream(x.device)), "qmoe_rmsnorm")
+    return out
+
+
+def forward_residual_workspace(cfg: L.QmoeConfig, N: int) -> int:
+    return int(L.load().qmoe_forward_residual_workspace(ctypes.byref(cfg), N))
+
+
+def forward_residual(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
+                     norm_weight: torch.Tensor, eps: float, out: torch.Tensor | None = None,
+                     ws: torch.Tensor | None = None) -> torch.Tensor:
+    """x + block(rmsnorm(x)) on the residual rows x [N, H] bf16 (qmoe_forward_residual). `out`
+    may be x itself (in-place residual update)."""
+    _need(x, torch.bfloat16, "x")
+    _need(norm_weight, torch.bfloat16, "norm_weight")
+    N, H = x.shape
+    if H != cfg.hidden or norm_weight.shape != (H,):
+        raise ValueError("forward_residual: x / norm_weight do not match the config's hidden size")
+    need = forward_residual_workspace(cfg, N)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty(N, H, dtype=torch.bfloat16, device=x.device)
+    L.check(L.load().qmoe_forward_residual(ctypes.byref(cfg), ctypes.byref(weights), _p(x),
+                                           _p(norm_weight), float(eps), N, _p(out), _p(ws),
+                                           ws.numel(), _stream(x.device)), "qmoe_forward_residual")
+    return out

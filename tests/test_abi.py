@@ -86,6 +86,11 @@ def test_workspace_grows_with_tokens():
     assert 0 < a < b
     # h (mc*I bf16) + d (mc*H bf16) dominate
     assert b >= 128 * 10 * (1024 + 4096) * 2
+    # the residual entry adds the normalised rows (N*H bf16, 256-byte aligned) after them
+    for n in (1, 3, 128):
+        assert (lib.qmoe_forward_residual_workspace(ctypes.byref(cfg), n)
+                == lib.qmoe_forward_workspace(ctypes.byref(cfg), n) + (n * 4096 * 2 + 255) // 256 * 256)
+    assert lib.qmoe_forward_residual_workspace(ctypes.byref(cfg), 0) == 0
 
 
 def test_ops_refuse_cpu_tensors():

@@ -387,3 +387,38 @@ def test_route_margin_flags_ties():
     choice = np.array([[3.0, 1.0, 1.0, 0.5], [4.0, 3.0, 2.0, 1.0]])
     m = om.route_margin(choice, 2)
     assert m[0] == 0.0 and m[1] == 1.0
+
+
+# ----------------------------------------------------------------------------- layer norm
+def test_rmsnorm_matches_torch_rms_norm():
+    """oracle rmsnorm == torch.nn.functional.rms_norm (float64), i.e. x * rsqrt(mean(x^2) + eps)
+    * w over the last dim; a dropped eps, a sum in place of the mean or the weight applied twice
+    all fail here."""
+    rng = np.random.default_rng(11)
+    for H, eps in ((64, 1e-6), (4096, 1e-6), (96, 0.5)):
+        x = oq.round_bf16(rng.standard_normal((7, H)) * 3.0)
+        w = oq.round_bf16(1.0 + 0.1 * rng.standard_normal(H))
+        want = torch.nn.functional.rms_norm(torch.from_numpy(x), (H,), weight=torch.from_numpy(w),
+                                            eps=eps).numpy()
+        np.testing.assert_allclose(om.rmsnorm(x, w, eps), want, rtol=1e-12, atol=1e-12)
+
+
+def test_rmsnorm_closed_forms():
+    """A constant row c gives w * c / sqrt(c^2 + eps); with eps = 0 the norm is invariant under
+    positive scaling of the row and every normalised row has mean square 1 (w = 1)."""
+    c, eps = -2.5, 1e-2
+    w = np.array([1.0, 0.5, 2.0, -1.0])
+    got = om.rmsnorm(np.full((1, 4), c), w, eps)
+    np.testing.assert_allclose(got, w[None] * c / np.sqrt(c * c + eps), rtol=1e-15)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 33))
+    ones = np.ones(33)
+    np.testing.assert_allclose(om.rmsnorm(7.25 * x, ones, 0.0), om.rmsnorm(x, ones, 0.0), rtol=1e-13)
+    np.testing.assert_allclose(np.mean(om.rmsnorm(x, ones, 0.0) ** 2, axis=-1), 1.0, rtol=1e-13)
+
+
+def test_residual_add_rounds_once():
+    """bf16 + bf16 rounds once to bf16: exact sums stay, a tie rounds to even."""
+    a = np.array([1.0, 1.0, 256.0])
+    b = np.array([2.0, 2.0 ** -8, 1.0])     # 1 + 2^-8: tie between 1 and 1+2^-7 -> 1 (even)
+    np.testing.assert_array_equal(om.residual_add(a, b), [3.0, 1.0, 256.0])
