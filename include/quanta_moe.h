@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 1
+#define QMOE_ABI_VERSION 2
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -56,6 +56,16 @@ extern "C" {
 #define QMOE_REGIME_LARGE 2 /* prefill: experts of > 16 rows on 128-row LDS-staged fp16 tiles
                                (128x512 for int4 weights in 512-row blocks, else 128x256),
                                the others on 16-token m-tiles */
+
+/* gated activation of the SwiGLU epilogue, h = act(gate, up) on the bf16 gate/up values in fp32:
+ *  SILU        silu(g) * u                                (src/quanta/qwen35/moe.py:59-63)
+ *  SILU_CLAMP  silu(min(g, L)) * clip(u, -L, L)           (src/quanta/dsv4/moe.py:74-77, L = swiglu_limit)
+ *  SWIGLU_OAI  (clip(u, -L, L) + 1) * g' * sigmoid(alpha * g'), g' = min(g, L)
+ *                                                         (src/quanta/minimax/model_m3.py:112-128,
+ *                                                          alpha 1.702, L 7.0) */
+#define QMOE_ACT_SILU 0
+#define QMOE_ACT_SILU_CLAMP 1
+#define QMOE_ACT_SWIGLU_OAI 2
 
 /* grouped-qmm epilogues */
 #define QMOE_EPI_SWIGLU 0 /* out[:, j] = bf16(silu(bf16(gate_j)) * bf16(up_j)), rows = [gate; up] */
@@ -81,6 +91,9 @@ typedef struct {
   int32_t router_rows;   /* rows of the tiled bf16 router (>= E + shared_gated, % 256 == 0) */
   int32_t shared_gated;  /* 1: shared output scaled by sigmoid(x . shared_expert_gate) */
   int32_t regime;        /* QMOE_REGIME_* for the routed experts (AUTO: small for N <= 256) */
+  int32_t act;           /* QMOE_ACT_* of the routed and shared experts' SwiGLU */
+  float act_alpha;       /* SWIGLU_OAI's alpha */
+  float act_limit;       /* SILU_CLAMP / SWIGLU_OAI's clamp L (> 0; +inf = none) */
 } qmoe_config_t;
 
 /* Prepared (resident) weights of one block; every array is device memory. */
@@ -165,7 +178,9 @@ int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_
  * QMOE_REGIME_LARGE), with row(p) = slot_of[p] / slot_div (slot_of NULL: row(p) = p). With
  * offsets == NULL the call is one dense segment of dense_rows rows. W is tiled int4-g64
  * (codes + sb) or tiled bf16 (codes), [n_experts][n_rows][K]. Epilogue QMOE_EPI_SWIGLU treats
- * rows [0, n_rows/2) as gate and [n_rows/2, n_rows) as up.
+ * rows [0, n_rows/2) as gate and [n_rows/2, n_rows) as up, with the gated activation `glu`
+ * (QMOE_ACT_*; glu_alpha and glu_limit as act_alpha and act_limit of qmoe_config_t; other
+ * epilogues ignore them).
  * Replaces mx.gather_qmm(..., transpose=True, group_size=64, bits=4)
  * (src/quanta/qwen35/moe.py:117-123, src/quanta/dsv4/moe.py:119-124) with the SwiGLU of
  * src/quanta/qwen35/moe.py:59-63 fused, and mx.gather_mm (src/quanta/qwen35/moe.py:79-81). */
@@ -173,7 +188,8 @@ int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_
                      int64_t n_slots, const int32_t* offsets, const int32_t* tile_off,
                      const int32_t* tile_map, int n_experts, int64_t dense_rows, int K,
                      int n_rows, int weight_format,
-                     const void* codes, const uint16_t* sb, int epilogue, void* out, int ld_out,
+                     const void* codes, const uint16_t* sb, int epilogue, int glu,
+                     float glu_alpha, float glu_limit, void* out, int ld_out,
                      int regime, void* ws, size_t ws_bytes, void* stream);
 /* Workspace qmoe_grouped_qmm needs: the large-M int4 regime stages an fp16 copy of the
  * activations (per-row power-of-two scaled, exact for bf16 inputs); otherwise 0. */
@@ -186,16 +202,19 @@ size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format, in
 int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* w, int64_t N, int k, int H,
                  const uint16_t* shared_out, const float* shared_gate, uint16_t* y, void* stream);
 
-/* Bit-exact dequant of a native affine int4-g64 or int8-g64 stack: out[rows, in] bf16 =
- * bf16(fma(scale, code, bias)), codes LSB-first (8 or 4 per u32 word). Replaces mx.dequantize
+/* Bit-exact dequant of a native affine int4 or int8 stack, group 64 or 128: out[rows, in] bf16
+ * = bf16(fma(scale, code, bias)), codes LSB-first (8 or 4 per u32 word). Replaces mx.dequantize
  * (src/quanta/bake/quant.py:32-36; src/quanta/qwen35/artifact.py:105-115); int8 g64 is the
  * bake's shared-expert format (src/quanta/qwen35/bake.py:106-110, 143-151). */
 int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias, int64_t rows,
                  int64_t in_features, int bits, int group_size, uint16_t* out, void* stream);
 
-/* One-time layout transform of a native int4-g64 stack [n_mats][rows][in] (packed u32
- * [.., in/8], scale/bias bf16 [.., in/64]) into the MFMA-tiled layout (codes: same byte count;
- * sb: [n_mats][rows/16][in/128][16][2][2] bf16). rows % 16 == 0, in % 128 == 0. Stands in for
+/* One-time layout transform of a native int4 stack [n_mats][rows][in] (packed u32 [.., in/8],
+ * scale/bias bf16 [.., in/group_size], group_size 64 or 128) into the MFMA-tiled layout
+ * (codes: same byte count; sb: [n_mats][rows/16][in/128][16][2][2] bf16, one (scale, bias) per
+ * 64 columns: a 128-column group's pair is written for both of its halves, so every kernel
+ * reads one layout). rows % 16 == 0, in % 128 == 0. Group 128 is the layout of Kimi's
+ * QuantizedSparseMoE stacks (src/quanta/modeling/quantized.py:29-34). Stands in for
  * holding the packed triplet verbatim (Qwen35MoEModule.set_experts_packed,
  * src/quanta/qwen35/model.py:49-55; Qwen35Artifact.moe_packed,
  * src/quanta/qwen35/artifact.py:205-229). */

@@ -152,7 +152,7 @@ def permute(idx: np.ndarray, n_experts: int):
 
 def gather_qmm(xrows: np.ndarray, experts: np.ndarray, packed: np.ndarray, scale: np.ndarray,
                bias: np.ndarray, in_features: int, *, round_out: bool = True,
-               round_weights: bool = False) -> np.ndarray:
+               round_weights: bool = False, group_size: int = 64) -> np.ndarray:
     """y[m] = x[m] . (s*q + b)[experts[m]]^T per row, float64, rounded to bf16.
 
     Restates `mx.gather_qmm(x, packed, scale, bias, rhs_indices=exp, transpose=True)`
@@ -168,7 +168,7 @@ def gather_qmm(xrows: np.ndarray, experts: np.ndarray, packed: np.ndarray, scale
     out = np.zeros((xrows.shape[0], packed.shape[1]), dtype=np.float64)
     for e in np.unique(experts):
         sel = experts == e
-        w = dequant_exact(packed[e], scale[e], bias[e], in_features)
+        w = dequant_exact(packed[e], scale[e], bias[e], in_features, group_size=group_size)
         if round_weights:
             w = round_bf16(w)
         out[sel] = xrows[sel].astype(np.float64) @ w.T
@@ -185,12 +185,31 @@ def gather_mm(xrows: np.ndarray, experts: np.ndarray, stack: np.ndarray) -> np.n
     return round_bf16(out)
 
 
-def swiglu(gu: np.ndarray, inter: int) -> np.ndarray:
+def glu(g: np.ndarray, u: np.ndarray, act: str = "silu", alpha: float = 1.702,
+        limit: float = 0.0) -> np.ndarray:
+    """The gated activation on bf16 gate/up values, unrounded:
+      "silu"       silu(g) * u (`src/quanta/qwen35/moe.py:59-63`), clamped when limit > 0 as
+                   g = min(g, L), u = clip(u, -L, L) (`src/quanta/dsv4/moe.py:74-77`);
+      "swigluoai"  g = min(g, L), u = clip(u, -L, L), (u + 1) * g * sigmoid(alpha * g)
+                   (`src/quanta/minimax/model_m3.py:112-128`, transformers GptOssExperts)."""
+    if limit > 0:
+        g = np.minimum(g, limit)
+        u = np.clip(u, -limit, limit)
+    if act == "swigluoai":
+        return (u + 1.0) * (g * _sigmoid(alpha * g))
+    if act != "silu":
+        raise ValueError(f"unknown act {act!r}")
+    return _silu(g) * u
+
+
+def swiglu(gu: np.ndarray, inter: int, act: str = "silu", alpha: float = 1.702,
+           limit: float = 0.0) -> np.ndarray:
     """SwiGLU on the fused gate|up activation (`src/quanta/qwen35/moe.py:59-63`):
-    gate = first `inter` columns, up = the rest; h = bf16(silu(g) * u)."""
+    gate = first `inter` columns, up = the rest; h = bf16(glu(g, u)) (the MiniMax M3 split is
+    the same, `src/quanta/minimax/model_m3.py:407-408`)."""
     g = gu[:, :inter]
     u = gu[:, inter:]
-    return round_bf16(_silu(g) * u)
+    return round_bf16(glu(g, u, act, alpha, limit))
 
 
 def combine(d: np.ndarray, w: np.ndarray) -> np.ndarray:
@@ -200,7 +219,8 @@ def combine(d: np.ndarray, w: np.ndarray) -> np.ndarray:
 
 
 def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
-                  gate: np.ndarray | None):
+                  gate: np.ndarray | None, act: str = "silu", alpha: float = 1.702,
+                  limit: float = 0.0):
     """Shared SwiGLU expert (`src/quanta/qwen35/moe.py:145-151`): bf16 chain
     out = bf16(bf16(silu(bf16(x Wg^T)) * bf16(x Wu^T)) Wd^T), then times
     sg = sigmoid(x_f32 . g_f32) when a gate is given (Qwen); DeepSeek/GLM shared experts are
@@ -208,7 +228,7 @@ def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
     x = x.astype(np.float64)
     g = round_bf16(x @ wg.astype(np.float64).T)
     u = round_bf16(x @ wu.astype(np.float64).T)
-    h = round_bf16(_silu(g) * u)
+    h = round_bf16(glu(g, u, act, alpha, limit))
     out = round_bf16(h @ wd.astype(np.float64).T)
     if gate is None:
         return out, out, None
@@ -221,7 +241,8 @@ def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
 
 def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "softmax",
                 norm_topk: bool = True, n_group: int = 1, topk_group: int = 1,
-                scale: float = 1.0, round_weights: bool = False):
+                scale: float = 1.0, round_weights: bool = False, act: str = "silu",
+                alpha: float = 1.702, limit: float = 0.0, group_size: int = 64):
     """Whole block y = bf16(routed + shared) for x [N, H] (`src/quanta/qwen35/moe.py:154-202`).
 
     `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
@@ -239,16 +260,17 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
     exp = idx.reshape(-1)
     tok = np.repeat(np.arange(n), k)
     gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim,
-                    round_weights=round_weights)
-    h = swiglu(gu, inter)
+                    round_weights=round_weights, group_size=group_size)
+    h = swiglu(gu, inter, act, alpha, limit)
     d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
-                   round_weights=round_weights)
+                   round_weights=round_weights, group_size=group_size)
     routed = combine(d, w)
     y = routed.copy()
     sh = None
     if p.get("shared_gate_proj") is not None:
         sh, sh_out, sg = shared_expert(x, p["shared_gate_proj"], p["shared_up_proj"],
-                                       p["shared_down_proj"], p.get("shared_expert_gate"))
+                                       p["shared_down_proj"], p.get("shared_expert_gate"),
+                                       act, alpha, limit)
         y = y + sh
     inter_d = dict(idx=idx, w=w, logits=logits, scores=scores, choice=choice, gu=gu, h=h, d=d,
                    routed=routed, shared=sh, y_exact=y)

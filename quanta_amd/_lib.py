@@ -20,7 +20,9 @@ FMT_INT4_G64, FMT_BF16 = 0, 1
 ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
 REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
+ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
+ABI_VERSION = 2
 
 
 def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
@@ -45,6 +47,9 @@ class QmoeConfig(ctypes.Structure):
         ("router_rows", ctypes.c_int32),
         ("shared_gated", ctypes.c_int32),
         ("regime", ctypes.c_int32),
+        ("act", ctypes.c_int32),
+        ("act_alpha", ctypes.c_float),
+        ("act_limit", ctypes.c_float),
     ]
 
 
@@ -82,7 +87,7 @@ SIGNATURES = {
     "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
     "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _I,
-                              _P, _I, _I, _P, ctypes.c_size_t, _P]),
+                              _I, _F, _F, _P, _I, _I, _P, ctypes.c_size_t, _P]),
     "qmoe_grouped_qmm_workspace": (ctypes.c_size_t, [_I64, _I, _I, _I]),
     "qmoe_combine": (_I, [_P, _P, _P, _I64, _I, _I, _P, _P, _P, _P]),
     "qmoe_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
@@ -119,7 +124,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.qmoe_abi_version() != 1:
+        if lib.qmoe_abi_version() != ABI_VERSION:
             raise RuntimeError("quanta_amd: ABI version mismatch; rebuild the extension")
         _lib = lib
     return _lib

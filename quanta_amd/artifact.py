@@ -200,6 +200,9 @@ class QuantaArtifact:
             shared_expert_intermediate_size=int(tc.get("shared_expert_intermediate_size", 0)),
             norm_topk_prob=bool(tc.get("norm_topk_prob", True)),
             norm_eps=float(tc.get("rms_norm_eps", 1e-6)),
+            hidden_act=str(tc.get("hidden_act", "silu")),
+            swiglu_alpha=float(tc.get("swiglu_alpha", 1.702)),
+            swiglu_limit=float(tc.get("swiglu_limit", 0.0) or 0.0),
         )
 
     def post_attention_norm(self, i: int, device: torch.device | str, *,

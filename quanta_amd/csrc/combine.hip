@@ -6,6 +6,8 @@
 // y = bf16(routed + f32(shared_out) * sigmoid(x . g)) (src/quanta/qwen35/moe.py:145-151,201-202).
 // The combine gathers each slot's row through inv (no atomics), summing in slot order, so the
 // output is deterministic.
+#include <math.h>
+
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -344,6 +346,15 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   return L;
 }
 
+// Gated activation of the SwiGLU epilogue: QMOE_ACT_SILU ignores alpha and limit; the clamped
+// forms need limit > 0 (+inf: no clamp) and a finite alpha.
+static int validate_glu(int act, float alpha, float limit) {
+  if (act < QMOE_ACT_SILU || act > QMOE_ACT_SWIGLU_OAI) return fail("config: unknown act");
+  if (act != QMOE_ACT_SILU && !(limit > 0.f)) return fail("config: act_limit must be > 0 (+inf: none)");
+  if (act == QMOE_ACT_SWIGLU_OAI && !isfinite(alpha)) return fail("config: act_alpha must be finite");
+  return 0;
+}
+
 static int validate_config(const qmoe_config_t& c) {
   const int rc = validate_routing(1, c.hidden, c.n_experts, c.top_k, c.scoring, c.n_group,
                                   c.topk_group);
@@ -362,7 +373,7 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: unknown router_format");
   }
   if (c.regime < QMOE_REGIME_AUTO || c.regime > QMOE_REGIME_LARGE) return fail("config: bad regime");
-  return 0;
+  return validate_glu(c.act, c.act_alpha, c.act_limit);
 }
 
 }  // namespace qmoe
@@ -394,9 +405,14 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
                                 int slot_div, int64_t n_slots, const int32_t* offsets,
                                 const int32_t* tile_off, const int32_t* tile_map, int n_experts,
                                 int64_t dense_rows, int K, int n_rows, int weight_format,
-                                const void* codes, const uint16_t* sb, int epilogue, void* out,
+                                const void* codes, const uint16_t* sb, int epilogue, int glu,
+                                float glu_alpha, float glu_limit, void* out,
                                 int ld_out, int regime, void* ws, size_t ws_bytes, void* stream) {
   if (!act || !codes || !out) return fail("qmoe_grouped_qmm: null pointer");
+  if (epilogue == QMOE_EPI_SWIGLU) {
+    const int rc = validate_glu(glu, glu_alpha, glu_limit);
+    if (rc) return rc;
+  }
   if (weight_format == QMOE_FMT_INT4_G64 && !sb) return fail("qmoe_grouped_qmm: int4 needs sb");
   if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16)
     return fail("qmoe_grouped_qmm: bad weight_format");
@@ -423,6 +439,9 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
   a.sb = sb;
   a.out = out;
   a.ld_out = ld_out;
+  a.glu = glu;
+  a.glu_alpha = glu_alpha;
+  a.glu_limit = glu_limit;
   const int m_tile = (regime == QMOE_REGIME_SMALL) ? kSmallMTile : kLargeMTile;
   int64_t bound;
   if (offsets) {
@@ -560,6 +579,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     sgu.act = x; sgu.act_rows = N; sgu.slot_div = 1; sgu.dense_rows = N; sgu.n_experts = 1;
     sgu.K = c.hidden; sgu.n_rows = 2 * c.shared_inter; sgu.codes = wts->sh_gu; sgu.out = sh_h;
     sgu.ld_out = c.shared_inter;
+    sgu.glu = c.act; sgu.glu_alpha = c.act_alpha; sgu.glu_limit = c.act_limit;
     if (!fuse_gu) {
       rc = launch_qmm(sgu, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
       if (rc) return rc;
@@ -641,6 +661,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
     a.out = h; a.ld_out = c.inter;
+    a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
     if (f16_acts) {
       rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, stream);
       if (rc) return rc;

@@ -4,7 +4,8 @@
 // Reference format: src/quanta/bake/quant.py:48-73 (LSB-first nibbles, code i of a row in word
 // i/8 at bits 4*(i%8)), src/quanta/qwen35/bake.py:113-124 (stacks [E, out, in], bf16 scale and
 // bias per 64 along `in`), src/quanta/qwen35/artifact.py:187-229 (the {packed, scale, bias}
-// triplet the resident runtime holds).
+// triplet the resident runtime holds); group 128 along `in`: Kimi's QuantizedSparseMoE stacks
+// (src/quanta/modeling/quantized.py:29-34).
 #include "qmoe_internal.h"
 #include "../../include/quanta_moe.h"
 
@@ -17,12 +18,12 @@ namespace qmoe {
 __global__ void __launch_bounds__(256) dequant_native_kernel(
     const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
     const uint16_t* __restrict__ bias, int64_t n_words, int words_per_row, int groups_per_row,
-    uint4* __restrict__ out) {
+    int words_per_group, uint4* __restrict__ out) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n_words) return;
   int64_t row = i / words_per_row;
   int wr = static_cast<int>(i - row * words_per_row);
-  int64_t g = row * groups_per_row + wr / 8;     // 8 words per 64-code group
+  int64_t g = row * groups_per_row + wr / words_per_group;   // 8 words per 64-code group
   float s = bf16_to_f32(scale[g]);
   float b = bf16_to_f32(bias[g]);
   uint32_t w = packed[i];
@@ -42,12 +43,12 @@ __global__ void __launch_bounds__(256) dequant_native_kernel(
 __global__ void __launch_bounds__(256) dequant_native8_kernel(
     const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
     const uint16_t* __restrict__ bias, int64_t n_words, int words_per_row, int groups_per_row,
-    uint2* __restrict__ out) {
+    int words_per_group, uint2* __restrict__ out) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n_words) return;
   int64_t row = i / words_per_row;
   int wr = static_cast<int>(i - row * words_per_row);
-  int64_t g = row * groups_per_row + wr / 16;    // 16 words per 64-code group
+  int64_t g = row * groups_per_row + wr / words_per_group;   // 16 words per 64-code group
   float s = bf16_to_f32(scale[g]);
   float b = bf16_to_f32(bias[g]);
   uint32_t w = packed[i];
@@ -105,10 +106,10 @@ __global__ void __launch_bounds__(256) dequant_tiled_kernel(
 __global__ void __launch_bounds__(256) tile_int4_kernel(
     const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
     const uint16_t* __restrict__ bias, int64_t n_lanes_total, int K, int rows,
-    uint4* __restrict__ codes, uint16_t* __restrict__ sb) {
+    int halves_per_group, uint4* __restrict__ codes, uint16_t* __restrict__ sb) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n_lanes_total) return;
-  const int nsb = K / 128, wpr = K / 8, gpr = K / 64;
+  const int nsb = K / 128, wpr = K / 8, gpr = K / (64 * halves_per_group);
   int lane = static_cast<int>(i & 63);
   int64_t blk = i >> 6;
   int p = static_cast<int>(blk % nsb);
@@ -122,12 +123,14 @@ __global__ void __launch_bounds__(256) tile_int4_kernel(
   codes[i] = make_uint4(interleave_nibbles(src[2 * g]), interleave_nibbles(src[2 * g + 1]),
                         interleave_nibbles(src[8 + 2 * g]), interleave_nibbles(src[8 + 2 * g + 1]));
   if (g == 0) {
+    // one (scale, bias) per 64 columns: a 128-column group's pair serves both of its halves
     uint16_t* d = sb + ((blk * 16 + r) * 2) * 2;
-    int64_t gi = row * gpr + 2 * p;
-    d[0] = scale[gi];
-    d[1] = bias[gi];
-    d[2] = scale[gi + 1];
-    d[3] = bias[gi + 1];
+    const int64_t g0 = row * gpr + (2 * p) / halves_per_group;
+    const int64_t g1 = row * gpr + (2 * p + 1) / halves_per_group;
+    d[0] = scale[g0];
+    d[1] = bias[g0];
+    d[2] = scale[g1];
+    d[3] = bias[g1];
   }
 }
 
@@ -161,10 +164,10 @@ using namespace qmoe;
 extern "C" int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                             int64_t rows, int64_t in_features, int bits, int group_size,
                             uint16_t* out, void* stream) {
-  if ((bits != 4 && bits != 8) || group_size != 64)
-    return fail("qmoe_dequant: bits 4 or 8 with group_size 64 only");
-  if (rows <= 0 || in_features <= 0 || in_features % 64)
-    return fail("qmoe_dequant: rows > 0 and in_features % 64 == 0 required");
+  if ((bits != 4 && bits != 8) || (group_size != 64 && group_size != 128))
+    return fail("qmoe_dequant: bits 4 or 8 with group_size 64 or 128 only");
+  if (rows <= 0 || in_features <= 0 || in_features % group_size)
+    return fail("qmoe_dequant: rows > 0 and in_features % group_size == 0 required");
   if (!packed || !scale || !bias || !out) return fail("qmoe_dequant: null pointer");
   const int per_word = 32 / bits;
   int64_t n_words = rows * (in_features / per_word);
@@ -172,18 +175,18 @@ extern "C" int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const
   if (bits == 4)
     dequant_native_kernel<<<grid_for(n_words, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
         packed, scale, bias, n_words, static_cast<int>(in_features / 8),
-        static_cast<int>(in_features / 64), reinterpret_cast<uint4*>(out));
+        static_cast<int>(in_features / group_size), group_size / 8, reinterpret_cast<uint4*>(out));
   else
     dequant_native8_kernel<<<grid_for(n_words, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
         packed, scale, bias, n_words, static_cast<int>(in_features / 4),
-        static_cast<int>(in_features / 64), reinterpret_cast<uint2*>(out));
+        static_cast<int>(in_features / group_size), group_size / 4, reinterpret_cast<uint2*>(out));
   return check_launch("qmoe_dequant");
 }
 
 extern "C" int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                               int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
                               uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream) {
-  if (group_size != 64) return fail("qmoe_tile_int4: group_size must be 64");
+  if (group_size != 64 && group_size != 128) return fail("qmoe_tile_int4: group_size must be 64 or 128");
   if (n_mats <= 0 || rows <= 0 || rows % 16 || in_features <= 0 || in_features % 128)
     return fail("qmoe_tile_int4: need rows % 16 == 0 and in_features % 128 == 0");
   if (!packed || !scale || !bias || !tiled_codes || !tiled_sb)
@@ -192,7 +195,7 @@ extern "C" int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, con
   int64_t lanes = n_mats * rows * (in_features / 128) * 4;   // 16 rows x 64 lanes per 16 rows
   tile_int4_kernel<<<grid_for(lanes, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
       packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
-      reinterpret_cast<uint4*>(tiled_codes), tiled_sb);
+      group_size / 64, reinterpret_cast<uint4*>(tiled_codes), tiled_sb);
   return check_launch("qmoe_tile_int4");
 }
 

@@ -80,10 +80,21 @@ template <int EPI>
 __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, float v, float v_up) {
   const int64_t off = static_cast<int64_t>(row) * a.ld_out + col;
   if (EPI == EPI_SWIGLU) {
-    // gate/up are bf16 tensors in the reference's flow; SwiGLU then rounds once to bf16.
+    // gate/up are bf16 tensors in the reference's flow; the gated activation runs on them in
+    // fp32 and rounds once to bf16 (QMOE_ACT_*: the clamped forms of src/quanta/dsv4/moe.py:74-77
+    // and src/quanta/minimax/model_m3.py:112-128)
     const float g = bf16_to_f32(f32_to_bf16(v));
     const float u = bf16_to_f32(f32_to_bf16(v_up));
-    static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(silu_f(g) * u);
+    float h;
+    if (a.glu == QMOE_ACT_SILU) {
+      h = silu_f(g) * u;
+    } else {
+      const float gc = fminf(g, a.glu_limit);
+      const float uc = fminf(fmaxf(u, -a.glu_limit), a.glu_limit);
+      h = (a.glu == QMOE_ACT_SILU_CLAMP) ? silu_f(gc) * uc
+                                         : (uc + 1.0f) * (gc / (1.0f + __expf(-a.glu_alpha * gc)));
+    }
+    static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(h);
   } else if (EPI == EPI_BF16) {
     static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(v);
   } else {

@@ -193,6 +193,9 @@ struct QmmArgs {
   const uint16_t* act16;      // large int4 regime: fp16 copy of act, row r scaled by 1/row_sinv[r]
   const float* row_sinv;      // large int4 regime: per activation row inverse scale (2^e)
   int mtiles;                 // large regime: m-tiles in the grid (entries of tile_map it reads)
+  int glu;                    // SwiGLU epilogue: gated activation (QMOE_ACT_*)
+  float glu_alpha;            // SWIGLU_OAI alpha
+  float glu_limit;            // clamp of SILU_CLAMP / SWIGLU_OAI
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1 };

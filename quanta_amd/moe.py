@@ -46,6 +46,9 @@ class MoEConfig:
     topk_group: int = 1
     routed_scaling_factor: float = 1.0
     norm_eps: float = 1e-6
+    hidden_act: str = "silu"
+    swiglu_alpha: float = 1.702
+    swiglu_limit: float = 0.0
 
     @property
     def moe_gate_up_out(self) -> int:
@@ -80,14 +83,15 @@ class TiledExperts(dict):
 
 
 def tile_experts_packed(d: dict) -> TiledExperts:
-    """Reference packed triplet -> TiledExperts. Fails loud unless bits == 4 and group_size == 64
-    (the kernels' format; the manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
+    """Reference packed triplet -> TiledExperts. Fails loud unless bits == 4 and group_size is 64
+    or 128 (the kernels' format: 128-column groups are tiled as two 64-column halves with the same
+    scale and bias; the manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
     if isinstance(d, TiledExperts):
         return d
     bits, gs = int(d["bits"]), int(d["group_size"])
-    if bits != 4 or gs != 64:
-        raise ValueError(f"packed experts must be affine int4 with group_size 64 (got bits={bits}, "
-                         f"group_size={gs})")
+    if bits != 4 or gs not in (64, 128):
+        raise ValueError(f"packed experts must be affine int4 with group_size 64 or 128 (got "
+                         f"bits={bits}, group_size={gs})")
     packed, scale, bias = d["packed"], d["scale"], d["bias"]
     if scale.dtype != torch.bfloat16 or bias.dtype != torch.bfloat16:
         raise TypeError("packed experts need bf16 scale and bias")
@@ -221,6 +225,22 @@ def _prepare_shared(p: dict, H: int, Is: int):
     return ops.tile_bf16(gu), ops.tile_bf16(wd.contiguous())
 
 
+def gated_activation(cfg) -> tuple[int, float, float]:
+    """(act, alpha, limit) of the experts' SwiGLU from the config: `hidden_act` "silu" is the
+    Qwen SwiGLU (src/quanta/qwen35/moe.py:59-63), clamped by `swiglu_limit` > 0 as DeepSeek-V4
+    does (src/quanta/dsv4/moe.py:74-77); "swigluoai" is the clamped SwiGLU-OAI of MiniMax M3
+    (src/quanta/minimax/model_m3.py:112-128; `swiglu_alpha`, `swiglu_limit`)."""
+    act = str(_cfg(cfg, "hidden_act", "silu"))
+    limit = float(_cfg(cfg, "swiglu_limit", 0.0) or 0.0)
+    alpha = float(_cfg(cfg, "swiglu_alpha", 1.702))
+    inf = float("inf")
+    if act == "swigluoai":
+        return L.ACT_SWIGLU_OAI, alpha, (limit if limit > 0 else inf)
+    if act in ("silu", "swish"):
+        return (L.ACT_SILU_CLAMP, 1.0, limit) if limit > 0 else (L.ACT_SILU, 1.0, inf)
+    raise ValueError(f"hidden_act {act!r} not supported (silu | swigluoai)")
+
+
 def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUTO) -> Prepared:
     """Resolve the parameter dict `p` (reference keys, src/quanta/qwen35/moe.py:159-161) into the
     resident kernel form. Conversions are cached on the source tensors."""
@@ -273,6 +293,7 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     c.router_rows = rrows
     c.shared_gated = int(sgate is not None)
     c.regime = regime
+    c.act, c.act_alpha, c.act_limit = gated_activation(cfg)
 
     w = L.QmoeWeights()
     w.router_w = rw.data_ptr()
@@ -370,7 +391,7 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
                         codes=pr.gu["codes"], sb=pr.gu["sb"], epilogue=L.EPI_SWIGLU,
                         out_rows=n * E, regime=regime, slot_of=sorted_slot, slot_div=E,
                         n_slots=n * E, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
-                        n_experts=E)
+                        n_experts=E, glu=c.act, glu_alpha=c.act_alpha, glu_limit=c.act_limit)
     d = ops.grouped_qmm(h, K=c.inter, n_rows=c.hidden, weight_format=fmt, codes=pr.dn["codes"],
                         sb=pr.dn["sb"], epilogue=L.EPI_BF16, out_rows=n * E, regime=regime,
                         n_slots=n * E, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
@@ -380,7 +401,8 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
         sreg = _dense_regime(n, c.hidden)
         sh_h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.shared_inter, weight_format=L.FMT_BF16,
                                codes=pr.sh_gu, sb=None, epilogue=L.EPI_SWIGLU, out_rows=n,
-                               regime=sreg, dense_rows=n)
+                               regime=sreg, dense_rows=n, glu=c.act, glu_alpha=c.act_alpha,
+                               glu_limit=c.act_limit)
         sh_out = ops.grouped_qmm(sh_h, K=c.shared_inter, n_rows=c.hidden, weight_format=L.FMT_BF16,
                                  codes=pr.sh_dn, sb=None, epilogue=L.EPI_BF16, out_rows=n,
                                  regime=sreg, dense_rows=n)

@@ -47,15 +47,15 @@ def _words(t: torch.Tensor, name: str) -> torch.Tensor:
 
 def dequant(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *, bits: int = 4,
             group_size: int = 64) -> torch.Tensor:
-    """Native affine int4-g64 (or int8-g64, bits=8) stack [..., rows, K*bits/32] -> bf16
-    [..., rows, K] (bit-exact: bf16(fma(s, q, b)))."""
+    """Native affine int4 (or int8, bits=8) stack [..., rows, K*bits/32], group 64 or 128 ->
+    bf16 [..., rows, K] (bit-exact: bf16(fma(s, q, b)))."""
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
     if bits not in (4, 8):
         raise ValueError("dequant: bits must be 4 or 8")
     K = packed.shape[-1] * (32 // bits)
-    if scale.shape != bias.shape or scale.shape[:-1] != packed.shape[:-1] or scale.shape[-1] * 64 != K:
+    if scale.shape != bias.shape or scale.shape[:-1] != packed.shape[:-1] or scale.shape[-1] * group_size != K:
         raise ValueError("dequant: shape mismatch between packed words and scale/bias")
     rows = packed.numel() // packed.shape[-1]
     out = torch.empty(*packed.shape[:-1], K, dtype=torch.bfloat16, device=packed.device)
@@ -66,7 +66,8 @@ def dequant(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *, bi
 
 def tile_int4(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
               group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
-    """Native stack [E, rows, K/8] (+ scale/bias [E, rows, K/64]) -> MFMA-tiled (codes, sb)."""
+    """Native stack [E, rows, K/8] (+ scale/bias [E, rows, K/group_size], group 64 or 128) ->
+    MFMA-tiled (codes, sb); sb holds one (scale, bias) per 64 columns either way."""
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
@@ -76,8 +77,10 @@ def tile_int4(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
         raise ValueError("tile_int4: expected [E, rows, K/8]")
     E, rows, W = packed.shape
     K = W * 8
-    if scale.shape != (E, rows, K // 64) or bias.shape != scale.shape:
-        raise ValueError("tile_int4: scale/bias must be [E, rows, K/64]")
+    if group_size not in (64, 128):
+        raise ValueError("tile_int4: group_size must be 64 or 128")
+    if scale.shape != (E, rows, K // group_size) or bias.shape != scale.shape:
+        raise ValueError(f"tile_int4: scale/bias must be [E, rows, K/{group_size}]")
     codes = torch.empty(E * rows * W, dtype=torch.int32, device=packed.device)
     sb = torch.empty(E * rows * (K // 64) * 2, dtype=torch.bfloat16, device=packed.device)
     L.check(L.load().qmoe_tile_int4(_p(packed), _p(scale), _p(bias), E, rows, K, group_size,
@@ -178,9 +181,11 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
                 tile_off: torch.Tensor | None = None, tile_map: torch.Tensor | None = None,
                 n_experts: int = 1,
                 dense_rows: int = 0, out: torch.Tensor | None = None,
-                ws: torch.Tensor | None = None) -> torch.Tensor:
+                ws: torch.Tensor | None = None, glu: int = L.ACT_SILU, glu_alpha: float = 1.0,
+                glu_limit: float = float("inf")) -> torch.Tensor:
     """Grouped matmul over expert segments (see qmoe_grouped_qmm). Returns out [out_rows, cols]
-    (bf16, or fp32 for EPI_F32); cols = n_rows/2 for SwiGLU else n_rows."""
+    (bf16, or fp32 for EPI_F32); cols = n_rows/2 for SwiGLU else n_rows. `glu`, `glu_alpha`,
+    `glu_limit`: the SwiGLU epilogue's gated activation (L.ACT_*)."""
     _need(act, torch.bfloat16, "act")
     if act.dim() != 2 or act.shape[1] != K:
         raise ValueError("grouped_qmm: act must be [rows, K]")
@@ -212,7 +217,8 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     L.check(lib.qmoe_grouped_qmm(_p(act), act.shape[0], _p(slot_of), slot_div, n_slots,
                                  _p(offsets), _p(tile_off), _p(tile_map), n_experts, dense_rows,
                                  K, n_rows,
-                                 weight_format, _p(codes), _p(sb), epilogue, _p(out), cols,
+                                 weight_format, _p(codes), _p(sb), epilogue, int(glu),
+                                 float(glu_alpha), float(glu_limit), _p(out), cols,
                                  regime, _p(ws) if need else None, ws.numel() if need else 0,
                                  _stream(act.device)), "qmoe_grouped_qmm")
     return out

@@ -1,0 +1,126 @@
+"""GPU tier: other expert formats on the same kernels.
+
+- int4 (and int8) stacks with 128-column groups (Kimi's QuantizedSparseMoE layout,
+  src/quanta/modeling/quantized.py:29-34): dequant bit-exact, the tiled layout lossless, and the
+  block against the oracle at decode and prefill sizes.
+- the clamped gated activations of the SwiGLU epilogue: DeepSeek-V4's clamped silu
+  (src/quanta/dsv4/moe.py:74-77) and MiniMax M3's SwiGLU-OAI (src/quanta/minimax/
+  model_m3.py:112-128), on routed and shared experts, against the oracle in every regime.
+
+Bars: dequant and tiling bit-exact; the block within the BASELINE gates (max-abs 2e-2 scaled,
+relative L2 5e-3).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from oracle import quant as oq
+from quanta_amd import _lib as L
+from quanta_amd import ops
+from quanta_amd.moe import MoEConfig, qwen35_moe
+from quanta_amd.quant import quantize_affine
+from tests._util import assert_close, bf16_dev, bits_np, f64, oracle_params_from_torch, words_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_group128_bit_exact(gpu, bits):
+    rng = np.random.default_rng(bits)
+    rows, K = 48, 512
+    codes = rng.integers(0, 1 << bits, size=(rows, K))
+    words = oq.pack_affine(codes, bits)
+    s = oq.f32_to_bf16_bits((rng.random((rows, K // 128)) * 0.05 + 1e-3).astype(np.float32))
+    b = oq.f32_to_bf16_bits((rng.standard_normal((rows, K // 128)) * 0.3).astype(np.float32))
+    got = ops.dequant(words_dev(words, gpu), bf16_dev(s, gpu), bf16_dev(b, gpu), bits=bits,
+                      group_size=128)
+    want = oq.dequant_bf16_bits(words, s, b, K, bits=bits, group_size=128)
+    assert np.array_equal(bits_np(got), want)
+
+
+def test_tile_group128_lossless(gpu):
+    rng = np.random.default_rng(5)
+    E, rows, K = 3, 32, 384
+    w = torch.from_numpy(rng.standard_normal((E, rows, K)).astype(np.float32) * 0.02).to(gpu)
+    packed, s, b = quantize_affine(w, 4, group_size=128)
+    codes, sb = ops.tile_int4(packed, s, b, group_size=128)
+    back = ops.dequant_tiled(codes, sb, E, rows, K)
+    assert torch.equal(back, ops.dequant(packed, s, b, bits=4, group_size=128))
+
+
+def _layer(dev, gs, seed, H=512, E=8, I=256, Is=256, gated=True):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    nrm = lambda *shape: torch.randn(*shape, generator=g) * 0.02
+    p = {"gate": nrm(E, H).to(torch.bfloat16).to(dev)}
+    for key, shape in (("experts_gate_up", (E, 2 * I, H)), ("experts_down", (E, H, I))):
+        packed, s, b = quantize_affine(nrm(*shape).to(dev), 4, group_size=gs)
+        p[key] = {"packed": packed, "scale": s, "bias": b, "group_size": gs, "bits": 4}
+    for key, shape in (("shared_gate_proj", (Is, H)), ("shared_up_proj", (Is, H)),
+                       ("shared_down_proj", (H, Is))):
+        p[key] = nrm(*shape).to(torch.bfloat16).to(dev)
+    if gated:
+        p["shared_expert_gate"] = nrm(1, H).to(torch.bfloat16).to(dev)
+    return p
+
+
+def _inputs(dev, N, H, seed, scale=4.0):
+    g = torch.Generator(device="cpu").manual_seed(1000 + seed)
+    return (torch.randn(N, H, generator=g) * scale).to(torch.bfloat16).to(dev)
+
+
+def _check(p, cfg, x, what, *, act="silu", alpha=1.702, limit=0.0, gs=64):
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=cfg.num_experts_per_tok,
+                           inter=cfg.moe_intermediate_size, act=act, alpha=alpha, limit=limit,
+                           group_size=gs)
+    assert_close(f64(y), it["y_exact"], what)
+    return y, it
+
+
+@pytest.mark.parametrize("N", [1, 5, 40, 300])
+def test_block_group128_vs_oracle(gpu, N):
+    """128-column groups through every regime (slot-major, decode, hybrid prefill)."""
+    cfg = MoEConfig(512, 8, 2, 256, 256)
+    p = _layer(gpu, 128, seed=N)
+    _check(p, cfg, _inputs(gpu, N, 512, N), f"group 128 N={N}", gs=128)
+
+
+@pytest.mark.parametrize("act,alpha,limit", [("swigluoai", 1.702, 1.5), ("silu", 1.0, 0.75),
+                                             ("swigluoai", 1.702, 0.0)])
+@pytest.mark.parametrize("N", [2, 20, 70, 300])
+def test_block_gated_activation_vs_oracle(gpu, act, alpha, limit, N):
+    """The clamped activations on routed and shared experts: slot-major (N <= 2), fused shared
+    expert (N <= 64), auxiliary-stream shared expert and hybrid prefill (N > 256). The limits are
+    small enough that the clamps bind on part of the gate/up values."""
+    cfg = MoEConfig(512, 8, 2, 256, 256, hidden_act=act, swiglu_alpha=alpha, swiglu_limit=limit)
+    p = _layer(gpu, 64, seed=7 * N)
+    x = _inputs(gpu, N, 512, N)
+    _, it = _check(p, cfg, x, f"{act} limit={limit} N={N}", act=act, alpha=alpha, limit=limit)
+    if limit > 0 and N >= 20:
+        gu = it["gu"]
+        assert np.any(gu > limit), "the clamp must bind somewhere for the test to mean anything"
+
+
+def test_gated_activation_dense_path_and_errors(gpu):
+    """sparse=False (bf16 stacks, run-every-expert) takes the same activation; unknown
+    activations and a non-positive clamp are refused."""
+    cfg = MoEConfig(512, 8, 2, 256, 256, hidden_act="swigluoai", swiglu_alpha=1.702, swiglu_limit=1.5)
+    p = _layer(gpu, 64, seed=3)
+    x = _inputs(gpu, 9, 512, 3)
+    gu, dn = p["experts_gate_up"], p["experts_down"]
+    p16 = dict(p, experts_gate_up=ops.dequant(gu["packed"], gu["scale"], gu["bias"]),
+               experts_down=ops.dequant(dn["packed"], dn["scale"], dn["bias"]))
+    y_sparse = f64(qwen35_moe(x[None], p16, cfg))
+    y_dense = f64(qwen35_moe(x[None], p16, cfg, sparse=False))
+    assert_close(y_dense, y_sparse, "swigluoai dense vs sparse")
+    with pytest.raises(ValueError, match="hidden_act"):
+        qwen35_moe(x[None], p, MoEConfig(512, 8, 2, 256, 256, hidden_act="gelu"))
+    codes, sb = ops.tile_int4(gu["packed"], gu["scale"], gu["bias"])
+    with pytest.raises(ValueError, match="act_limit"):
+        ops.grouped_qmm(x, K=512, n_rows=512, weight_format=L.FMT_INT4_G64, codes=codes, sb=sb,
+                        epilogue=L.EPI_SWIGLU, out_rows=9, regime=L.REGIME_SMALL, dense_rows=9,
+                        glu=L.ACT_SILU_CLAMP, glu_limit=0.0)

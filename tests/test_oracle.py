@@ -422,3 +422,53 @@ def test_residual_add_rounds_once():
     a = np.array([1.0, 1.0, 256.0])
     b = np.array([2.0, 2.0 ** -8, 1.0])     # 1 + 2^-8: tie between 1 and 1+2^-7 -> 1 (even)
     np.testing.assert_array_equal(om.residual_add(a, b), [3.0, 1.0, 256.0])
+
+
+# ----------------------------------------------------------------------------- gated activations
+def test_swigluoai_matches_transformers_gpt_oss():
+    """glu("swigluoai") == transformers GptOssExperts._apply_gate (float64), which the reference's
+    swigluoai is written against (src/quanta/minimax/model_m3.py:112-128). GPT-OSS interleaves
+    gate/up columns; the reference (and this build) splits halves, so the input is interleaved
+    for transformers and the halves compared."""
+    from types import SimpleNamespace
+
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssExperts
+
+    rng = np.random.default_rng(21)
+    g = oq.round_bf16(rng.standard_normal((6, 40)) * 6.0)
+    u = oq.round_bf16(rng.standard_normal((6, 40)) * 6.0)
+    inter = np.empty((6, 80))
+    inter[:, ::2], inter[:, 1::2] = g, u
+    want = GptOssExperts._apply_gate(SimpleNamespace(alpha=1.702, limit=7.0),
+                                     torch.from_numpy(inter)).numpy()
+    np.testing.assert_allclose(om.glu(g, u, "swigluoai", 1.702, 7.0), want, rtol=1e-12, atol=1e-12)
+    assert np.any(g > 7.0) and np.any(np.abs(u) > 7.0)       # the clamps are exercised
+
+
+def test_clamped_silu_known_answers():
+    """The DeepSeek-V4 clamp (src/quanta/dsv4/moe.py:74-77): the gate is clamped from above only,
+    the up branch both ways; limit 0 is the plain silu(g) * u."""
+    g = np.array([10.0, -10.0, 3.0])
+    u = np.array([10.0, -10.0, 0.5])
+    L = 7.0
+    silu = lambda v: v / (1.0 + np.exp(-v))
+    np.testing.assert_allclose(om.glu(g, u, "silu", limit=L),
+                               [silu(7.0) * 7.0, silu(-10.0) * -7.0, silu(3.0) * 0.5], rtol=1e-15)
+    np.testing.assert_allclose(om.glu(g, u, "silu", limit=0.0), silu(g) * u, rtol=1e-15)
+    np.testing.assert_allclose(om.glu(g, u, "swigluoai", 1.0, 0.0), silu(g) * (u + 1.0), rtol=1e-15)
+
+
+def test_dequant_group128_explicit_loop():
+    """group_size 128 (Kimi's stacks, src/quanta/modeling/quantized.py:29-34): one (scale, bias)
+    per 128 codes, checked element by element."""
+    rng = np.random.default_rng(8)
+    rows, K = 3, 256
+    codes = rng.integers(0, 16, size=(rows, K))
+    words = oq.pack_affine(codes, 4)
+    sb = oq.f32_to_bf16_bits(rng.standard_normal((rows, K // 128)).astype(np.float32) * 0.1)
+    bb = oq.f32_to_bf16_bits(rng.standard_normal((rows, K // 128)).astype(np.float32))
+    got = oq.dequant_exact(words, sb, bb, K, group_size=128)
+    s, b = oq.bf16_bits_to_f32(sb).astype(np.float64), oq.bf16_bits_to_f32(bb).astype(np.float64)
+    for r in range(rows):
+        for k in range(K):
+            assert got[r, k] == s[r, k // 128] * codes[r, k] + b[r, k // 128]
