@@ -45,6 +45,8 @@ extern "C" {
 /* expert weight formats, both in this library's MFMA-tiled layout (see qmoe_tile_*) */
 #define QMOE_FMT_INT4_G64 0
 #define QMOE_FMT_BF16 1
+#define QMOE_FMT_INT6_G64 2 /* affine int6 codes, bf16 scale/bias per 64 (MiniMax M3 experts,
+                               src/quanta/minimax/model_m3.py:414-450); small regime only */
 
 /* router weight storage */
 #define QMOE_ROUTER_BF16_TILED 0 /* bf16 [router_rows, H] tiled; row E = shared-expert gate */
@@ -202,8 +204,8 @@ size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format, in
 int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* w, int64_t N, int k, int H,
                  const uint16_t* shared_out, const float* shared_gate, uint16_t* y, void* stream);
 
-/* Bit-exact dequant of a native affine int4 or int8 stack, group 64 or 128: out[rows, in] bf16
- * = bf16(fma(scale, code, bias)), codes LSB-first (8 or 4 per u32 word). Replaces mx.dequantize
+/* Bit-exact dequant of a native affine int4, int6 or int8 stack, group 64 or 128: out[rows, in]
+ * bf16 = bf16(fma(scale, code, bias)), codes LSB-first (8 per word, 16 per 3 words, 4 per word). Replaces mx.dequantize
  * (src/quanta/bake/quant.py:32-36; src/quanta/qwen35/artifact.py:105-115); int8 g64 is the
  * bake's shared-expert format (src/quanta/qwen35/bake.py:106-110, 143-151). */
 int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias, int64_t rows,
@@ -219,6 +221,17 @@ int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* 
  * src/quanta/qwen35/model.py:49-55; Qwen35Artifact.moe_packed,
  * src/quanta/qwen35/artifact.py:205-229). */
 int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                   int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                   uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
+
+/* One-time layout transform of a native int6 stack [n_mats][rows][in] (packed u32 [.., in*6/32],
+ * the bake's LSB-first bitstream, src/quanta/bake/quant.py:48-63; scale/bias bf16
+ * [.., in/group_size], group 64 or 128) into the tiled int6 layout the decode kernel streams: per
+ * 16-row tile and 128-deep superblock a 1 KiB plane of the codes' low nibbles, laid out as the int4
+ * tiles, then a 512-byte plane of their high two bits (same byte count as the native codes); sb as
+ * qmoe_tile_int4. Stands in for holding MiniMax M3's int6 triplets verbatim
+ * (src/quanta/minimax/model_m3.py:414-450). */
+int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                    int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
                    uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
 

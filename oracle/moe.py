@@ -152,7 +152,7 @@ def permute(idx: np.ndarray, n_experts: int):
 
 def gather_qmm(xrows: np.ndarray, experts: np.ndarray, packed: np.ndarray, scale: np.ndarray,
                bias: np.ndarray, in_features: int, *, round_out: bool = True,
-               round_weights: bool = False, group_size: int = 64) -> np.ndarray:
+               round_weights: bool = False, group_size: int = 64, bits: int = 4) -> np.ndarray:
     """y[m] = x[m] . (s*q + b)[experts[m]]^T per row, float64, rounded to bf16.
 
     Restates `mx.gather_qmm(x, packed, scale, bias, rhs_indices=exp, transpose=True)`
@@ -168,7 +168,8 @@ def gather_qmm(xrows: np.ndarray, experts: np.ndarray, packed: np.ndarray, scale
     out = np.zeros((xrows.shape[0], packed.shape[1]), dtype=np.float64)
     for e in np.unique(experts):
         sel = experts == e
-        w = dequant_exact(packed[e], scale[e], bias[e], in_features, group_size=group_size)
+        w = dequant_exact(packed[e], scale[e], bias[e], in_features, bits=bits,
+                          group_size=group_size)
         if round_weights:
             w = round_bf16(w)
         out[sel] = xrows[sel].astype(np.float64) @ w.T
@@ -242,7 +243,7 @@ def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
 def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "softmax",
                 norm_topk: bool = True, n_group: int = 1, topk_group: int = 1,
                 scale: float = 1.0, round_weights: bool = False, act: str = "silu",
-                alpha: float = 1.702, limit: float = 0.0, group_size: int = 64):
+                alpha: float = 1.702, limit: float = 0.0, group_size: int = 64, bits: int = 4):
     """Whole block y = bf16(routed + shared) for x [N, H] (`src/quanta/qwen35/moe.py:154-202`).
 
     `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
@@ -260,10 +261,10 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
     exp = idx.reshape(-1)
     tok = np.repeat(np.arange(n), k)
     gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim,
-                    round_weights=round_weights, group_size=group_size)
+                    round_weights=round_weights, group_size=group_size, bits=bits)
     h = swiglu(gu, inter, act, alpha, limit)
     d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
-                   round_weights=round_weights, group_size=group_size)
+                   round_weights=round_weights, group_size=group_size, bits=bits)
     routed = combine(d, w)
     y = routed.copy()
     sh = None

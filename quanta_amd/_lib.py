@@ -16,7 +16,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "quanta_moe.h"
 
 QMOE_OK, QMOE_EINVAL, QMOE_EHIP = 0, -1, -2
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
-FMT_INT4_G64, FMT_BF16 = 0, 1
+FMT_INT4_G64, FMT_BF16, FMT_INT6_G64 = 0, 1, 2
 ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
 REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
@@ -93,6 +93,7 @@ SIGNATURES = {
     "qmoe_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "qmoe_tile_int4": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_dequant_tiled": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "qmoe_tile_int6": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_bf16": (_I, [_P, _I64, _I64, _I64, _P, _P]),
 }
 

@@ -364,8 +364,11 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: the large-M regime needs hidden % 256 == 0");
   if (c.inter <= 0 || c.inter % 128) return fail("config: inter % 128 == 0 required");
   if (c.shared_inter < 0 || c.shared_inter % 128) return fail("config: shared_inter % 128 == 0 required");
-  if (c.expert_format != QMOE_FMT_INT4_G64 && c.expert_format != QMOE_FMT_BF16)
-    return fail("config: expert_format must be int4-g64 (0) or bf16 (1)");
+  if (c.expert_format != QMOE_FMT_INT4_G64 && c.expert_format != QMOE_FMT_BF16 &&
+      c.expert_format != QMOE_FMT_INT6_G64)
+    return fail("config: expert_format must be int4-g64 (0), bf16 (1) or int6-g64 (2)");
+  if (c.expert_format == QMOE_FMT_INT6_G64 && c.regime == QMOE_REGIME_LARGE)
+    return fail("config: int6 experts run in the small regime only");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {
     if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 256)
       return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 256");
@@ -413,9 +416,10 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
     const int rc = validate_glu(glu, glu_alpha, glu_limit);
     if (rc) return rc;
   }
-  if (weight_format == QMOE_FMT_INT4_G64 && !sb) return fail("qmoe_grouped_qmm: int4 needs sb");
-  if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16)
+  if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16 &&
+      weight_format != QMOE_FMT_INT6_G64)
     return fail("qmoe_grouped_qmm: bad weight_format");
+  if (weight_format != QMOE_FMT_BF16 && !sb) return fail("qmoe_grouped_qmm: int4/int6 need sb");
   if (epilogue < QMOE_EPI_SWIGLU || epilogue > QMOE_EPI_F32) return fail("qmoe_grouped_qmm: bad epilogue");
   if (regime != QMOE_REGIME_SMALL && regime != QMOE_REGIME_LARGE)
     return fail("qmoe_grouped_qmm: regime must be small (1) or large (2)");
@@ -479,6 +483,7 @@ static int dense_regime(const qmoe_config_t& c, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
+  if (c.expert_format == QMOE_FMT_INT6_G64) return QMOE_REGIME_SMALL;   // no large int6 kernel
   return dense_regime(c, N);
 }
 
@@ -494,8 +499,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   const WsLayout L = ws_layout(c, N);
   if (ws_bytes < L.total) return fail("qmoe_forward: workspace too small");
   if (!wts->router_w || !wts->gu_codes || !wts->dn_codes) return fail("qmoe_forward: missing weights");
-  if (c.expert_format == QMOE_FMT_INT4_G64 && (!wts->gu_sb || !wts->dn_sb))
-    return fail("qmoe_forward: int4 experts need scale/bias");
+  if (c.expert_format != QMOE_FMT_BF16 && (!wts->gu_sb || !wts->dn_sb))
+    return fail("qmoe_forward: int4/int6 experts need scale/bias");
   if (c.shared_inter > 0 && (!wts->sh_gu || !wts->sh_dn)) return fail("qmoe_forward: missing shared expert");
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
@@ -536,7 +541,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                                          ((kHybridSplitRows + kSmallMTile - 1) / kSmallMTile));
   const int64_t hot_bound = (mc + kLargeMTile - 1) / kLargeMTile +
                             std::min<int64_t>(c.n_experts, mc / (kHybridSplitRows + 1));
-  const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4 : FMT_BF16;
+  const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4
+                   : (c.expert_format == QMOE_FMT_INT6_G64) ? FMT_INT6 : FMT_BF16;
   const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
 
   const int sreg = dense_regime(c, N);

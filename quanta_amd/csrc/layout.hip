@@ -62,6 +62,95 @@ __global__ void __launch_bounds__(256) dequant_native8_kernel(
   out[i] = make_uint2(o[0], o[1]);
 }
 
+// Code k (6 bits) of a native int6 row (LSB-first bitstream: code k at bits 6k .. 6k+5).
+__device__ __forceinline__ uint32_t int6_code(const uint32_t* __restrict__ row_words, int k) {
+  const int bit = 6 * k, w = bit >> 5, sh = bit & 31;
+  uint32_t v = row_words[w] >> sh;
+  if (sh > 26) v |= row_words[w + 1] << (32 - sh);
+  return v & 63u;
+}
+
+// int6: one thread per 3 packed words = 16 codes of one row, written as two 16-byte stores;
+// same rounding (s*c exact in float32: 8-bit x 6-bit mantissas). Reference: the int6 expert
+// stacks of MiniMax M3 (src/quanta/minimax/model_m3.py:414-450), packed as the bake's bitstream
+// (src/quanta/bake/quant.py:48-63).
+__global__ void __launch_bounds__(256) dequant_native6_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ bias, int64_t n_chunks, int chunks_per_row, int groups_per_row,
+    int chunks_per_group, uint4* __restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_chunks) return;
+  int64_t row = i / chunks_per_row;
+  int cr = static_cast<int>(i - row * chunks_per_row);
+  int64_t g = row * groups_per_row + cr / chunks_per_group;
+  float s = bf16_to_f32(scale[g]);
+  float b = bf16_to_f32(bias[g]);
+  const uint32_t w[3] = {packed[3 * i], packed[3 * i + 1], packed[3 * i + 2]};
+  uint32_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    o[j] = pack_bf16x2(fmaf(s, static_cast<float>(int6_code(w, 2 * j)), b),
+                       fmaf(s, static_cast<float>(int6_code(w, 2 * j + 1)), b));
+  out[2 * i] = make_uint4(o[0], o[1], o[2], o[3]);
+  out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// Native int6 -> tiled int6: per 16-row tile and 128-deep superblock, a 1 KiB plane of the codes'
+// low nibbles laid out exactly as the int4 tiles (lane l: row l%16, words {2g, 2g+1} of each of
+// the two 64-column groups, g = l/16, nibbles interleaved) and a 512-byte plane of their high two
+// bits, lane l's 8 bytes being one word per group: the high bits of the lane's 8-code half h,
+// pair j (codes 2j, 2j+1 of the half) at bits 2j + 8h and 16 + 2j + 8h, so a shift by 2j + 8h and a
+// mask of 0x00030003 puts them beside the pair's nibbles. Scale/bias as the int4 tiling. One
+// thread per 16-byte lane slot of the nibble plane.
+__global__ void __launch_bounds__(256) tile_int6_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ bias, int64_t n_lanes_total, int K, int rows,
+    int halves_per_group, uint32_t* __restrict__ codes, uint16_t* __restrict__ sb) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_lanes_total) return;
+  const int nsb = K / 128, wpr = K * 6 / 32, gpr = K / (64 * halves_per_group);
+  int lane = static_cast<int>(i & 63);
+  int64_t blk = i >> 6;
+  int p = static_cast<int>(blk % nsb);
+  int64_t mr = blk / nsb;
+  int rt = rows / 16;
+  int64_t mat = mr / rt;
+  int R = static_cast<int>(mr - mat * rt);
+  int r = lane & 15, g = lane >> 4;
+  int64_t row = mat * rows + R * 16 + r;
+  const uint32_t* src = packed + row * wpr;
+  uint32_t nib[4], hi[2];
+#pragma unroll
+  for (int grp = 0; grp < 2; ++grp) {
+    hi[grp] = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t code = int6_code(src, 128 * p + 64 * grp + 16 * g + 8 * h + c);
+        w |= (code & 15u) << (4 * c);                 // natural order, interleaved below
+        const int j = c >> 1;
+        hi[grp] |= (code >> 4) << ((c & 1) ? 16 + 2 * j + 8 * h : 2 * j + 8 * h);
+      }
+      nib[2 * grp + h] = interleave_nibbles(w);
+    }
+  }
+  // superblock tile block: 1 KiB nibble plane then 512 B high-bit plane
+  uint32_t* blkp = codes + blk * 384;
+  reinterpret_cast<uint4*>(blkp)[lane] = make_uint4(nib[0], nib[1], nib[2], nib[3]);
+  reinterpret_cast<uint2*>(blkp + 256)[lane] = make_uint2(hi[0], hi[1]);
+  if (g == 0) {
+    uint16_t* d = sb + ((blk * 16 + r) * 2) * 2;
+    const int64_t g0 = row * gpr + (2 * p) / halves_per_group;
+    const int64_t g1 = row * gpr + (2 * p + 1) / halves_per_group;
+    d[0] = scale[g0];
+    d[1] = bias[g0];
+    d[2] = scale[g1];
+    d[3] = bias[g1];
+  }
+}
+
 // Tiled int4 -> natural bf16 [mats][rows][K]; checks the tiled transform is lossless (it undoes
 // the nibble interleave of the stored words).
 __global__ void __launch_bounds__(256) dequant_tiled_kernel(
@@ -164,11 +253,19 @@ using namespace qmoe;
 extern "C" int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                             int64_t rows, int64_t in_features, int bits, int group_size,
                             uint16_t* out, void* stream) {
-  if ((bits != 4 && bits != 8) || (group_size != 64 && group_size != 128))
-    return fail("qmoe_dequant: bits 4 or 8 with group_size 64 or 128 only");
+  if ((bits != 4 && bits != 6 && bits != 8) || (group_size != 64 && group_size != 128))
+    return fail("qmoe_dequant: bits 4, 6 or 8 with group_size 64 or 128 only");
   if (rows <= 0 || in_features <= 0 || in_features % group_size)
     return fail("qmoe_dequant: rows > 0 and in_features % group_size == 0 required");
   if (!packed || !scale || !bias || !out) return fail("qmoe_dequant: null pointer");
+  if (bits == 6) {
+    const int64_t n_chunks = rows * (in_features / 16);
+    if (n_chunks >= (int64_t(1) << 40)) return fail("qmoe_dequant: tensor too large");
+    dequant_native6_kernel<<<grid_for(n_chunks, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        packed, scale, bias, n_chunks, static_cast<int>(in_features / 16),
+        static_cast<int>(in_features / group_size), group_size / 16, reinterpret_cast<uint4*>(out));
+    return check_launch("qmoe_dequant");
+  }
   const int per_word = 32 / bits;
   int64_t n_words = rows * (in_features / per_word);
   if (n_words >= (int64_t(1) << 40)) return fail("qmoe_dequant: tensor too large");
@@ -197,6 +294,22 @@ extern "C" int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, con
       packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
       group_size / 64, reinterpret_cast<uint4*>(tiled_codes), tiled_sb);
   return check_launch("qmoe_tile_int4");
+}
+
+extern "C" int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                              int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                              uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream) {
+  if (group_size != 64 && group_size != 128) return fail("qmoe_tile_int6: group_size must be 64 or 128");
+  if (n_mats <= 0 || rows <= 0 || rows % 16 || in_features <= 0 || in_features % 128)
+    return fail("qmoe_tile_int6: need rows % 16 == 0 and in_features % 128 == 0");
+  if (!packed || !scale || !bias || !tiled_codes || !tiled_sb)
+    return fail("qmoe_tile_int6: null pointer");
+  if (rows > (1 << 30) || in_features > (1 << 30)) return fail("qmoe_tile_int6: dims too large");
+  int64_t lanes = n_mats * rows * (in_features / 128) * 4;
+  tile_int6_kernel<<<grid_for(lanes, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
+      group_size / 64, tiled_codes, tiled_sb);
+  return check_launch("qmoe_tile_int6");
 }
 
 extern "C" int qmoe_dequant_tiled(const uint32_t* tiled_codes, const uint16_t* tiled_sb,

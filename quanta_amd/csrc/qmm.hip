@@ -113,10 +113,11 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
 // chunks; chunk sums meet in LDS. How many wavefronts share the chunks (W) varies with the
 // launch size, but the arithmetic does not, so every output is bit-identical at every batch size.
 // WAVES = max(4, W) wavefronts per workgroup.
-template <int NT>
+template <int NT, int FMT>
 struct SmallStage {
-  u32x4 q[NT];    // int4: raw codes of one superblock / bf16: weight fragments of one 32-k step
-  uint2 sb[NT];   // int4 scale/bias of the superblock's two groups
+  u32x4 q[NT];    // int4/int6: the codes' nibbles of one superblock / bf16: weight fragments of one 32-k step
+  uint2 sb[NT];   // int4/int6 scale/bias of the superblock's two groups
+  u32x2 hq[(FMT == FMT_INT6) ? NT : 1];   // int6: the codes' high two bits (one word per group)
   u32x4 x[4];     // activation fragments
 };
 
@@ -129,7 +130,7 @@ struct SmallCfg {
   // chunk sums: [wave][chunk of the wave][m-tile][tile][lane]
   static constexpr int RED = (CH > 1) ? WAVES * CPW * MT * NT * 64 : 1;
   // the four-tile variants are held to 3 wavefronts per SIMD (168 VGPRs)
-  static constexpr int WPE = (FMT == FMT_INT4 && NT >= 4) ? 3 : 1;
+  static constexpr int WPE = (fmt_quant(FMT) && NT >= 4) ? 3 : 1;
 };
 
 // Body of one workgroup: job block `bx` of m-tile `by` (MT > 1, dense bf16 products only:
@@ -143,7 +144,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
   constexpr int NT = C::NT;
   constexpr int CH = C::CH;
-  static_assert(FMT == FMT_INT4 || CPW == 1, "bf16 weights use one chunk per wavefront");
+  static_assert(fmt_quant(FMT) || CPW == 1, "bf16 weights use one chunk per wavefront");
   constexpr bool kRed = CH > 1;
 
   // wave index as a scalar, so per-wavefront quantities (job, k-range) stay in SGPRs
@@ -199,7 +200,9 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
   }
 
   if (job_ok) {
-    if (FMT == FMT_INT4) {
+    if (fmt_quant(FMT)) {
+      // tile superblock: int4 1 KiB of codes; int6 1 KiB of nibbles + 512 B of high bits
+      constexpr int SBB = (FMT == FMT_INT6) ? 1536 : 1024;
       const int nsb = a.K / 128;
       // chunk c = superblocks [c * nsb / CH, (c + 1) * nsb / CH); this wavefront: CPW chunks
       const int p0 = kpart * CPW * nsb / CH, p1 = (kpart + 1) * CPW * nsb / CH;
@@ -211,7 +214,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int64_t tb = (static_cast<int64_t>(e) * tiles_per_expert + tile[t]) * nsb;
-        cb[t] = static_cast<const char*>(a.codes) + tb * 1024;
+        cb[t] = static_cast<const char*>(a.codes) + tb * SBB;
         sbb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       }
       const uint32_t lane_c = static_cast<uint32_t>(lane) * 16u;
@@ -224,14 +227,17 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       }
       const f32x4_t zero4{0.f, 0.f, 0.f, 0.f};
       // Two register stages: the loads of superblock p+1 are in flight while p is computed.
-      SmallStage<NT> st[2];
-      auto load = [&](SmallStage<NT>& s, int p) __attribute__((always_inline)) {
+      SmallStage<NT, FMT> st[2];
+      auto load = [&](SmallStage<NT, FMT>& s, int p) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           // weights are streamed once per call: nontemporal loads keep them out of the way of
           // the activations that every job of the m-tile re-reads
           s.q[t] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(cb[t] + static_cast<int64_t>(p) * 1024 + lane_c));
+              reinterpret_cast<const u32x4*>(cb[t] + static_cast<int64_t>(p) * SBB + lane_c));
+          if constexpr (FMT == FMT_INT6)
+            s.hq[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(
+                cb[t] + static_cast<int64_t>(p) * SBB + 1024 + 8 * lane));
           const u32x2 v = __builtin_nontemporal_load(
               reinterpret_cast<const u32x2*>(sbb[t] + static_cast<int64_t>(p) * 128 + lane_s));
           s.sb[t] = uint2{v.x, v.y};
@@ -242,7 +248,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         s.x[2] = xp[p * 16 + 8];
         s.x[3] = xp[p * 16 + 9];
       };
-      auto compute = [&](const SmallStage<NT>& s) __attribute__((always_inline)) {
+      auto compute = [&](const SmallStage<NT, FMT>& s) __attribute__((always_inline)) {
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
           const bf16x8_t A0 = as_bf16x8(s.x[2 * gg]);
@@ -253,8 +259,15 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
           for (int t = 0; t < NT; ++t) {
             const uint32_t w0 = gg ? s.q[t].z : s.q[t].x;
             const uint32_t w1 = gg ? s.q[t].w : s.q[t].y;
-            f32x4_t r = mfma16(A0, unpack_q128(w0), zero4);
-            r = mfma16(A1, unpack_q128(w1), r);
+            f32x4_t r;
+            if constexpr (FMT == FMT_INT6) {
+              const uint32_t hw = gg ? s.hq[t].y : s.hq[t].x;
+              r = mfma16(A0, unpack_q128_6(w0, hw, 0), zero4);
+              r = mfma16(A1, unpack_q128_6(w1, hw, 1), r);
+            } else {
+              r = mfma16(A0, unpack_q128(w0), zero4);
+              r = mfma16(A1, unpack_q128(w1), r);
+            }
             const uint32_t sbw = gg ? s.sb[t].y : s.sb[t].x;
             const float sc = bf16lo_to_f32(sbw);
             const float bi = bf16hi_to_f32(sbw) - 128.0f * sc;
@@ -1036,9 +1049,10 @@ struct SmallShape {
 };
 
 // (SwiGLU wavefronts hold two tiles per job: JPW 4 would exceed the register budget)
+// (int6 wavefronts hold at most two tiles: four spill at the three-wavefront register budget)
 static SmallShape pick_small_shape(int fmt, int epi, int ch, int64_t mtiles, int jobs) {
-  if (fmt != FMT_INT4) return SmallShape{1, ch, 1};
-  const int jmax = (epi == EPI_SWIGLU) ? 2 : 4;
+  if (!fmt_quant(fmt)) return SmallShape{1, ch, 1};
+  const int jmax = (fmt == FMT_INT6) ? ((epi == EPI_SWIGLU) ? 1 : 2) : ((epi == EPI_SWIGLU) ? 2 : 4);
   SmallShape best{1, ch, 1};
   int64_t best_waves = mtiles * jobs * ch, best_work = 1;
   bool best_ok = best_waves >= kSmallMinWaves;
@@ -1064,7 +1078,12 @@ static SmallShape pick_small_shape(int fmt, int epi, int ch, int64_t mtiles, int
 
 template <int FMT, int EPI, int W, int CPW>
 static void launch_small_j(const QmmArgs& a, int jpw, int64_t mtiles, hipStream_t stream) {
-  if constexpr (FMT == FMT_INT4) {
+  if constexpr (FMT == FMT_INT6) {
+    if (EPI != EPI_SWIGLU && jpw == 2)
+      launch_small_k<FMT, EPI, W, CPW, (EPI == EPI_SWIGLU) ? 1 : 2>(a, mtiles, stream);
+    else
+      launch_small_k<FMT, EPI, W, CPW, 1>(a, mtiles, stream);
+  } else if constexpr (FMT == FMT_INT4) {
     if (EPI != EPI_SWIGLU && jpw == 4)
       launch_small_k<FMT, EPI, W, CPW, (EPI == EPI_SWIGLU) ? 2 : 4>(a, mtiles, stream);
     else if (jpw == 2)
@@ -1079,7 +1098,7 @@ static void launch_small_j(const QmmArgs& a, int jpw, int64_t mtiles, hipStream_
 template <int FMT, int EPI>
 static void launch_small(const QmmArgs& a, const SmallShape& sh, int64_t mtiles,
                          hipStream_t stream) {
-  if constexpr (FMT == FMT_INT4) {
+  if constexpr (fmt_quant(FMT)) {
     if (sh.cpw == 2) {
       if (sh.w == 2) launch_small_j<FMT, EPI, 2, 2>(a, sh.jpw, mtiles, stream);
       else launch_small_j<FMT, EPI, 1, 2>(a, sh.jpw, mtiles, stream);
@@ -1171,7 +1190,7 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (mtile_bound <= 0) return 0;
   if (mtile_bound > 65535) return fail("qmm: too many m-tiles for one launch");
   if (regime == QMOE_REGIME_SMALL) {
-    if (fmt == FMT_INT4 && a.K % 128) return fail("qmm: int4 needs K % 128 == 0");
+    if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int4/int6 need K % 128 == 0");
     if (fmt == FMT_BF16 && a.K % 32) return fail("qmm: bf16 needs K % 32 == 0");
     if (a.n_rows % (epi == EPI_SWIGLU ? 32 : 16)) return fail("qmm: weight rows not a tile multiple");
     // The chunk count depends on the shape only (never on the token count), so a row's
@@ -1193,6 +1212,10 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT4, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT4, EPI_BF16);
       else QMOE_SMALL(FMT_INT4, EPI_F32);
+    } else if (fmt == FMT_INT6) {
+      if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT6, EPI_SWIGLU);
+      else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT6, EPI_BF16);
+      else QMOE_SMALL(FMT_INT6, EPI_F32);
     } else {
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_BF16, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_BF16, EPI_BF16);
@@ -1200,6 +1223,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     }
 #undef QMOE_SMALL
   } else {
+    if (fmt == FMT_INT6)
+      return fail("qmm(large): int6 weights run in the small regime only (a 1.5 KiB int6 tile "
+                  "superblock does not fit the large kernels' LDS slots)");
     if (a.K % 128) return fail("qmm(large): K % 128 == 0 required");
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
     if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))

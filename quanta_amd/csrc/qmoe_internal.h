@@ -90,6 +90,19 @@ __device__ __forceinline__ bf16x8_t unpack_q128(uint32_t w) {
   return v;
 }
 
+// int6 tiles: the low nibbles as unpack_q128, the high two bits from the lane's high-bit word of
+// the group (the word's half h holds pair j's two high-bit pairs at bits 2j + 8h and 16 + 2j + 8h).
+// 128 + q (q < 64) is exact in bf16.
+__device__ __forceinline__ bf16x8_t unpack_q128_6(uint32_t w, uint32_t hw, int h) {
+  const uint32_t m = 0x000F000Fu, o = 0x43004300u, mh = 0x00030003u;
+  bf16x8_t v;
+  uint32_t* p = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    p[j] = ((w >> (4 * j)) & m) | (((hw >> (2 * j + 8 * h)) & mh) << 4) | o;
+  return v;
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 q) {
   bf16x8_t v;
   __builtin_memcpy(&v, &q, 16);
@@ -198,7 +211,9 @@ struct QmmArgs {
   float glu_limit;            // clamp of SILU_CLAMP / SWIGLU_OAI
 };
 
-enum { FMT_INT4 = 0, FMT_BF16 = 1 };
+enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2 };
+// affine-quantized weight formats (int4 or int6 codes with per-64 scale/bias)
+constexpr bool fmt_quant(int fmt) { return fmt == FMT_INT4 || fmt == FMT_INT6; }
 enum { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,

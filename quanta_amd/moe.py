@@ -71,7 +71,8 @@ def _cfg(cfg, name, default=None):
 class TiledExperts(dict):
     """A routed expert stack resident in the MFMA-tiled layout.
 
-    Keys: "format" ("int4_g64" | "bf16"), "codes" (tiled int4 words / tiled bf16), "sb" (tiled
+    Keys: "format" ("int4_g64" | "int6_g64" | "bf16"), "codes" (tiled int4 or int6 words / tiled
+    bf16), "sb" (tiled
     scale+bias, int4 only), "shape" (E, rows, K), "group_size", "bits". Produced from the
     reference's packed triplet {packed, scale, bias, group_size, bits}
     (src/quanta/qwen35/artifact.py:199-203) or from a bf16 [E, rows, K] stack.
@@ -79,28 +80,29 @@ class TiledExperts(dict):
 
     @property
     def is_packed(self) -> bool:
-        return self["format"] == "int4_g64"
+        return self["format"] in ("int4_g64", "int6_g64")
 
 
 def tile_experts_packed(d: dict) -> TiledExperts:
-    """Reference packed triplet -> TiledExperts. Fails loud unless bits == 4 and group_size is 64
-    or 128 (the kernels' format: 128-column groups are tiled as two 64-column halves with the same
-    scale and bias; the manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
+    """Reference packed triplet -> TiledExperts. Fails loud unless bits is 4 or 6 and group_size
+    is 64 or 128 (the kernels' formats: 128-column groups are tiled as two 64-column halves with
+    the same scale and bias; int6 is MiniMax M3's expert format, src/quanta/minimax/
+    model_m3.py:414-450; the manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
     if isinstance(d, TiledExperts):
         return d
     bits, gs = int(d["bits"]), int(d["group_size"])
-    if bits != 4 or gs not in (64, 128):
-        raise ValueError(f"packed experts must be affine int4 with group_size 64 or 128 (got "
-                         f"bits={bits}, group_size={gs})")
+    if bits not in (4, 6) or gs not in (64, 128):
+        raise ValueError(f"packed experts must be affine int4 or int6 with group_size 64 or 128 "
+                         f"(got bits={bits}, group_size={gs})")
     packed, scale, bias = d["packed"], d["scale"], d["bias"]
     if scale.dtype != torch.bfloat16 or bias.dtype != torch.bfloat16:
         raise TypeError("packed experts need bf16 scale and bias")
     if packed.dim() != 3:
         raise ValueError("packed experts must be a stacked [E, out, in*bits/32] tensor")
     E, rows, W = packed.shape
-    codes, sb = ops.tile_int4(packed.contiguous(), scale.contiguous(), bias.contiguous(),
-                              group_size=gs)
-    return TiledExperts(format="int4_g64", codes=codes, sb=sb, shape=(E, rows, W * 8),
+    tile = ops.tile_int4 if bits == 4 else ops.tile_int6
+    codes, sb = tile(packed.contiguous(), scale.contiguous(), bias.contiguous(), group_size=gs)
+    return TiledExperts(format=f"int{bits}_g64", codes=codes, sb=sb, shape=(E, rows, W * 32 // bits),
                         group_size=gs, bits=bits)
 
 
@@ -288,7 +290,10 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     c.n_group = int(_cfg(cfg, "n_group", 1))
     c.topk_group = int(_cfg(cfg, "topk_group", 1))
     c.routed_scale = float(_cfg(cfg, "routed_scaling_factor", 1.0))
-    c.expert_format = L.FMT_INT4_G64 if packed else L.FMT_BF16
+    if packed and gu["format"] != dn["format"]:
+        raise ValueError("experts_gate_up and experts_down must use the same bit width")
+    c.expert_format = (L.FMT_BF16 if not packed else
+                       L.FMT_INT6_G64 if gu["format"] == "int6_g64" else L.FMT_INT4_G64)
     c.router_format = L.ROUTER_BF16_TILED if rkind == "bf16" else L.ROUTER_F32
     c.router_rows = rrows
     c.shared_gated = int(sgate is not None)

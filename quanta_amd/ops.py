@@ -47,14 +47,16 @@ def _words(t: torch.Tensor, name: str) -> torch.Tensor:
 
 def dequant(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *, bits: int = 4,
             group_size: int = 64) -> torch.Tensor:
-    """Native affine int4 (or int8, bits=8) stack [..., rows, K*bits/32], group 64 or 128 ->
+    """Native affine int4 (or int6 / int8, bits=6 / 8) stack [..., rows, K*bits/32], group 64 or 128 ->
     bf16 [..., rows, K] (bit-exact: bf16(fma(s, q, b)))."""
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
-    if bits not in (4, 8):
-        raise ValueError("dequant: bits must be 4 or 8")
-    K = packed.shape[-1] * (32 // bits)
+    if bits not in (4, 6, 8):
+        raise ValueError("dequant: bits must be 4, 6 or 8")
+    if (packed.shape[-1] * 32) % bits:
+        raise ValueError("dequant: packed words do not hold a whole number of codes")
+    K = packed.shape[-1] * 32 // bits
     if scale.shape != bias.shape or scale.shape[:-1] != packed.shape[:-1] or scale.shape[-1] * group_size != K:
         raise ValueError("dequant: shape mismatch between packed words and scale/bias")
     rows = packed.numel() // packed.shape[-1]
@@ -85,6 +87,33 @@ def tile_int4(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
     sb = torch.empty(E * rows * (K // 64) * 2, dtype=torch.bfloat16, device=packed.device)
     L.check(L.load().qmoe_tile_int4(_p(packed), _p(scale), _p(bias), E, rows, K, group_size,
                                     _p(codes), _p(sb), _stream(packed.device)), "qmoe_tile_int4")
+    return codes, sb
+
+
+def tile_int6(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
+              group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native int6 stack [E, rows, K*6/32] (+ scale/bias [E, rows, K/group_size]) -> the tiled
+    int6 layout of the decode kernel (codes: nibble plane + high-bit plane per tile superblock,
+    the same byte count; sb as tile_int4)."""
+    packed = _words(packed, "packed")
+    _need(scale, torch.bfloat16, "scale")
+    _need(bias, torch.bfloat16, "bias")
+    if packed.dim() == 2:
+        packed, scale, bias = packed[None], scale[None], bias[None]
+    if packed.dim() != 3:
+        raise ValueError("tile_int6: expected [E, rows, K*6/32]")
+    E, rows, W = packed.shape
+    if (W * 32) % 6:
+        raise ValueError("tile_int6: packed words do not hold a whole number of codes")
+    K = W * 32 // 6
+    if group_size not in (64, 128):
+        raise ValueError("tile_int6: group_size must be 64 or 128")
+    if scale.shape != (E, rows, K // group_size) or bias.shape != scale.shape:
+        raise ValueError(f"tile_int6: scale/bias must be [E, rows, K/{group_size}]")
+    codes = torch.empty(E * rows * W, dtype=torch.int32, device=packed.device)
+    sb = torch.empty(E * rows * (K // 64) * 2, dtype=torch.bfloat16, device=packed.device)
+    L.check(L.load().qmoe_tile_int6(_p(packed), _p(scale), _p(bias), E, rows, K, group_size,
+                                    _p(codes), _p(sb), _stream(packed.device)), "qmoe_tile_int6")
     return codes, sb
 
 
@@ -189,7 +218,7 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     _need(act, torch.bfloat16, "act")
     if act.dim() != 2 or act.shape[1] != K:
         raise ValueError("grouped_qmm: act must be [rows, K]")
-    if weight_format == L.FMT_INT4_G64:
+    if weight_format in (L.FMT_INT4_G64, L.FMT_INT6_G64):
         codes = _words(codes, "codes")
         _need(sb, torch.bfloat16, "sb")
     else:

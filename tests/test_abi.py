@@ -43,7 +43,8 @@ _DUMMY = ctypes.c_void_p(16)   # never dereferenced: each call fails validation 
 
 
 @pytest.mark.parametrize("call, fragment", [
-    (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 3, 64, None, None), "bits 4 or 8"),
+    (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 3, 64, None, None), "bits 4, 6 or 8"),
+    (lambda lib: lib.qmoe_tile_int6(None, None, None, 1, 16, 100, 64, None, None, None), "in_features % 128"),
     (lambda lib: lib.qmoe_dequant(None, None, None, 4, 100, 4, 64, None, None), "in_features"),
     (lambda lib: lib.qmoe_tile_int4(None, None, None, 1, 15, 128, 64, None, None, None), "rows % 16"),
     (lambda lib: lib.qmoe_tile_bf16(None, 1, 16, 33, None, None), "in_features % 32"),

@@ -1,5 +1,7 @@
 """GPU tier: other expert formats on the same kernels.
 
+- int6 expert stacks (MiniMax M3, src/quanta/minimax/model_m3.py:414-450) on the decode kernel:
+  dequant bit-exact, the grouped matmul and the block against the oracle.
 - int4 (and int8) stacks with 128-column groups (Kimi's QuantizedSparseMoE layout,
   src/quanta/modeling/quantized.py:29-34): dequant bit-exact, the tiled layout lossless, and the
   block against the oracle at decode and prefill sizes.
@@ -23,7 +25,8 @@ from quanta_amd import _lib as L
 from quanta_amd import ops
 from quanta_amd.moe import MoEConfig, qwen35_moe
 from quanta_amd.quant import quantize_affine
-from tests._util import assert_close, bf16_dev, bits_np, f64, oracle_params_from_torch, words_dev
+from tests._util import (assert_close, bf16_dev, bits_np, f64, oracle_params_from_torch, words_dev,
+                         words_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -72,11 +75,11 @@ def _inputs(dev, N, H, seed, scale=4.0):
     return (torch.randn(N, H, generator=g) * scale).to(torch.bfloat16).to(dev)
 
 
-def _check(p, cfg, x, what, *, act="silu", alpha=1.702, limit=0.0, gs=64):
+def _check(p, cfg, x, what, *, act="silu", alpha=1.702, limit=0.0, gs=64, bits=4):
     y = qwen35_moe(x[None], p, cfg)[0]
     _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=cfg.num_experts_per_tok,
                            inter=cfg.moe_intermediate_size, act=act, alpha=alpha, limit=limit,
-                           group_size=gs)
+                           group_size=gs, bits=bits)
     assert_close(f64(y), it["y_exact"], what)
     return y, it
 
@@ -124,3 +127,74 @@ def test_gated_activation_dense_path_and_errors(gpu):
         ops.grouped_qmm(x, K=512, n_rows=512, weight_format=L.FMT_INT4_G64, codes=codes, sb=sb,
                         epilogue=L.EPI_SWIGLU, out_rows=9, regime=L.REGIME_SMALL, dense_rows=9,
                         glu=L.ACT_SILU_CLAMP, glu_limit=0.0)
+
+
+# ------------------------------------------------------------------------------------ int6
+@pytest.mark.parametrize("gs", [64, 128])
+def test_dequant_int6_bit_exact(gpu, gs):
+    rng = np.random.default_rng(gs + 6)
+    rows, K = 40, 384
+    codes = rng.integers(0, 64, size=(rows, K))
+    words = oq.pack_affine(codes, 6)
+    s = oq.f32_to_bf16_bits((rng.random((rows, K // gs)) * 0.05 + 1e-3).astype(np.float32))
+    b = oq.f32_to_bf16_bits((rng.standard_normal((rows, K // gs)) * 0.3).astype(np.float32))
+    got = ops.dequant(words_dev(words, gpu), bf16_dev(s, gpu), bf16_dev(b, gpu), bits=6, group_size=gs)
+    assert np.array_equal(bits_np(got), oq.dequant_bf16_bits(words, s, b, K, bits=6, group_size=gs))
+
+
+@pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
+@pytest.mark.parametrize("N,k,E,H,rows", [(1, 4, 8, 4096, 256), (7, 3, 6, 256, 256),
+                                          (200, 4, 4, 1024, 128), (1024, 4, 32, 256, 512)])
+def test_grouped_qmm_int6_vs_oracle(gpu, epi, N, k, E, H, rows):
+    """The decode kernel's int6 path (tiled nibble + high-bit planes) against the oracle's exact
+    affine weights, through several launch shapes (chunks per wavefront, tiles per wavefront)."""
+    rng = np.random.default_rng(N + E + H + rows)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(N)]).astype(np.int32)
+    x = oq.round_bf16(rng.standard_normal((N, H)))
+    w = torch.from_numpy(rng.standard_normal((E, rows, H)).astype(np.float32) * 0.05).to(gpu)
+    packed, s, b = quantize_affine(w, 6, group_size=64)
+    dense = oq.dequant_exact(words_np(packed), bits_np(s), bits_np(b), H, bits=6)
+    counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(torch.from_numpy(idx).to(gpu), E,
+                                                                        L.SMALL_M_TILE)
+    codes, sb = ops.tile_int6(packed, s, b)
+    out = ops.grouped_qmm(bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu), K=H, n_rows=rows,
+                          weight_format=L.FMT_INT6_G64, codes=codes, sb=sb, epilogue=epi,
+                          out_rows=N * k, regime=L.REGIME_SMALL, slot_of=sorted_slot, slot_div=k,
+                          n_slots=N * k, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
+                          n_experts=E)
+    order = sorted_slot.cpu().numpy()
+    full = np.einsum("mh,moh->mo", x[order // k], dense[idx.reshape(-1)[order]])
+    want = oq.round_bf16(full)
+    if epi == L.EPI_SWIGLU:
+        want = om.swiglu(want, rows // 2)
+    assert_close(f64(out), want, f"int6 qmm epi={epi} N={N} E={E} H={H} rows={rows}", rel_l2=4e-3)
+
+
+def _layer6(dev, gs, seed, H=512, E=8, I=256, Is=256):
+    p = _layer(dev, gs, seed, H, E, I, Is)
+    g = torch.Generator(device="cpu").manual_seed(seed + 1)
+    for key, shape in (("experts_gate_up", (E, 2 * I, H)), ("experts_down", (E, H, I))):
+        packed, s, b = quantize_affine((torch.randn(*shape, generator=g) * 0.02).to(dev), 6, group_size=gs)
+        p[key] = {"packed": packed, "scale": s, "bias": b, "group_size": gs, "bits": 6}
+    return p
+
+
+@pytest.mark.parametrize("gs,act", [(64, "silu"), (64, "swigluoai"), (128, "swigluoai")])
+@pytest.mark.parametrize("N", [1, 8, 40, 300])
+def test_block_int6_vs_oracle(gpu, gs, act, N):
+    """int6 experts through the block (MiniMax M3's combination is int6 + SwiGLU-OAI): slot-major,
+    fused shared expert, auxiliary-stream shared expert, and above 256 tokens the decode kernel
+    (int6 has no large-regime kernel)."""
+    limit = 1.5 if act == "swigluoai" else 0.0
+    cfg = MoEConfig(512, 8, 2, 256, 256, hidden_act=act, swiglu_alpha=1.702, swiglu_limit=limit)
+    p = _layer6(gpu, gs, seed=11 * N + gs)
+    _check(p, cfg, _inputs(gpu, N, 512, N), f"int6 g{gs} {act} N={N}", act=act, limit=limit,
+           gs=gs, bits=6)
+
+
+def test_int6_large_regime_refused(gpu):
+    cfg = MoEConfig(512, 8, 2, 256, 256)
+    p = _layer6(gpu, 64, seed=1)
+    x = _inputs(gpu, 300, 512, 1)
+    with pytest.raises(ValueError, match="int6"):
+        qwen35_moe(x[None], p, cfg, regime=L.REGIME_LARGE)

@@ -472,3 +472,22 @@ def test_dequant_group128_explicit_loop():
     for r in range(rows):
         for k in range(K):
             assert got[r, k] == s[r, k // 128] * codes[r, k] + b[r, k // 128]
+
+
+def test_dequant_int6_explicit_loop():
+    """int6 codes (MiniMax M3's expert format, src/quanta/minimax/model_m3.py:414-450) packed as the
+    LSB-first bitstream (src/quanta/bake/quant.py:48-63; pack_affine is pinned bit by bit above),
+    dequantized element by element for groups of 64 and 128."""
+    rng = np.random.default_rng(6)
+    rows, K = 2, 256
+    codes = rng.integers(0, 64, size=(rows, K))
+    words = oq.pack_affine(codes, 6)
+    assert words.shape == (rows, K * 6 // 32)
+    for gs in (64, 128):
+        sb = oq.f32_to_bf16_bits(rng.standard_normal((rows, K // gs)).astype(np.float32) * 0.1)
+        bb = oq.f32_to_bf16_bits(rng.standard_normal((rows, K // gs)).astype(np.float32))
+        got = oq.dequant_exact(words, sb, bb, K, bits=6, group_size=gs)
+        s, b = oq.bf16_bits_to_f32(sb).astype(np.float64), oq.bf16_bits_to_f32(bb).astype(np.float64)
+        for r in range(rows):
+            for k in range(K):
+                assert got[r, k] == s[r, k // gs] * codes[r, k] + b[r, k // gs]
