@@ -12,8 +12,11 @@ routed experts change every step).
 
 Printed (one JSON line): whole-layer tokens/s (`value`), per-step time, the dominant kernel's
 roofline (routed gate_up+SwiGLU: algorithmic bytes per launch / its average duration, HIP events
-on the launch stream), a sweep over the other decode batches and the 4096-token prefill, and the
-CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host cores, bounded sample).
+on the launch stream), a sweep over the other decode batches and the 4096-token prefill, the
+widened rows at the headline batch (`--extra`: the block with the decoder layer's RMSNorm and
+residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, rotating
+two int6 copies), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
+cores, bounded sample).
 
 `roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
 profiles/hbm_traffic.json, written from two rocprofv3 counter passes over `--only kernel` runs:
@@ -54,6 +57,8 @@ def parse():
     ap.add_argument("--zipf", action="store_true",
                     help="headline workload with c4's Zipf(1.1) routing (profiling the prefill)")
     ap.add_argument("--kernel-reps", type=int, default=64)
+    ap.add_argument("--extra", default="residual,int6",
+                    help="widened rows timed at the headline batch ('' = none): residual, int6")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
@@ -171,21 +176,28 @@ def main():
     torch.cuda.synchronize()
     log(f"{args.layers} resident layer copies ready ({time.time() - t0:.1f}s)")
 
-    def run_batch(N, steps, warmup, pool, regime=L.REGIME_AUTO, zipf=False):
+    def run_batch(N, steps, warmup, pool, regime=L.REGIME_AUTO, zipf=False, lays=None,
+                  residual=False):
         # zipf: the c4 workload (the same shape, Zipf(1.1) expert popularity through router
         # column 0 and x[:, 0] = 1.0), on the resident experts of the headline config
+        # residual: the block with the layer's RMSNorm in front and the residual add fused
         src = "c4" if zipf else args.config
         xs = [synth.make_inputs(src, N, device=dev, seed=100 + i) for i in range(pool)]
-        lays = layers
+        lays = layers if lays is None else lays
         if zipf:
-            lays = [dict(p, gate=synth.zipf_router(p["gate"])) for p in layers]
+            lays = [dict(p, gate=synth.zipf_router(p["gate"])) for p in lays]
         preps = [prepare(p, cfg, regime=regime) for p in lays]
-        ws = torch.empty(ops.forward_workspace(preps[0].cfg, N), dtype=torch.uint8, device=dev)
+        wsz = (ops.forward_residual_workspace if residual else ops.forward_workspace)(preps[0].cfg, N)
+        ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
         out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+        norm_w = (1.0 + 0.1 * torch.randn(H, device=dev)).to(torch.bfloat16)
 
         def step(i):
             pr = preps[i % len(preps)]
-            ops.forward(pr.cfg, pr.weights, xs[i % pool], out=out, ws=ws)
+            if residual:
+                ops.forward_residual(pr.cfg, pr.weights, xs[i % pool], norm_w, 1e-6, out=out, ws=ws)
+            else:
+                ops.forward(pr.cfg, pr.weights, xs[i % pool], out=out, ws=ws)
 
         for i in range(warmup):
             step(i)
@@ -200,7 +212,8 @@ def main():
         # distinct experts per batch (U) for the algorithmic byte count
         us = []
         for x in xs:
-            idx, _ = qwen35_route(x, lays[0]["gate"], cfg)
+            xr = ops.rmsnorm(x, norm_w, 1e-6) if residual else x
+            idx, _ = qwen35_route(xr, lays[0]["gate"], cfg)
             us.append(int(torch.unique(idx).numel()))
         return ms, us, xs, preps
 
@@ -279,6 +292,35 @@ def main():
                        mfma_frac=round(f2 / m2 / 1e9 / BF16_PEAK_TFLOPS, 4))
             sweep.append(rec)
             log(f"sweep {rec}")
+
+    # ------------------------------------------------------------------ widened rows
+    # the block with the decoder layer's norm and residual add (qmoe_forward_residual), and the
+    # layer with int6 experts (MiniMax M3's format), at the headline batch
+    if args.only == "" and N <= 256:
+        def record(name, m2, u2, bits=4, extra_bytes=0):
+            U2 = sum(u2) / len(u2)
+            b2 = synth.algorithmic_bytes(cfg, U2, N, bits=bits) + extra_bytes
+            rec = dict(workload=name, N=N, ms_per_step=round(m2, 5),
+                       tokens_per_s=round(N / (m2 / 1e3), 1), distinct_experts=round(U2, 1),
+                       hbm_gbps=round(b2 / m2 / 1e6, 1), hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4))
+            sweep.append(rec)
+            log(f"sweep {rec}")
+
+        if "residual" in args.extra:
+            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), residual=True)
+            record(f"{args.config}-N{N}-residual", m2, u2, extra_bytes=2 * H)
+        if "int6" in args.extra:
+            # two int6 copies suffice to stream from HBM: one step touches U experts x 10 MB
+            lays6 = []
+            for li in range(2):
+                p6 = synth.make_layer(args.config, device=dev, layer=li, bits=6)
+                p6["experts_gate_up"] = TiledExperts(**tile_experts_packed(p6["experts_gate_up"]))
+                p6["experts_down"] = TiledExperts(**tile_experts_packed(p6["experts_down"]))
+                lays6.append(p6)
+            torch.cuda.synchronize()
+            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays6)
+            record(f"{args.config}-N{N}-int6", m2, u2, bits=6)
+            del lays6
 
     # ------------------------------------------------------------------ measured copy peak
     # device-to-device copy of 2 GiB (read + write bytes), the practical HBM ceiling next to
