@@ -14,8 +14,9 @@ Printed (one JSON line): whole-layer tokens/s (`value`), per-step time, the domi
 roofline (routed gate_up+SwiGLU: algorithmic bytes per launch / its average duration, HIP events
 on the launch stream), a sweep over the other decode batches and the 4096-token prefill, the
 widened rows at the headline batch (`--extra`: the block with the decoder layer's RMSNorm and
-residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, rotating
-two int6 copies), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
+residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, and with
+Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies), and the CPU
+baseline (the torch-CPU port in oracle/torch_cpu.py on the host
 cores, bounded sample).
 
 `roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
@@ -57,8 +58,8 @@ def parse():
     ap.add_argument("--zipf", action="store_true",
                     help="headline workload with c4's Zipf(1.1) routing (profiling the prefill)")
     ap.add_argument("--kernel-reps", type=int, default=64)
-    ap.add_argument("--extra", default="residual,int6",
-                    help="widened rows timed at the headline batch ('' = none): residual, int6")
+    ap.add_argument("--extra", default="residual,int6,int3",
+                    help="widened rows timed at the headline batch ('' = none): residual, int6, int3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
@@ -297,9 +298,9 @@ def main():
     # the block with the decoder layer's norm and residual add (qmoe_forward_residual), and the
     # layer with int6 experts (MiniMax M3's format), at the headline batch
     if args.only == "" and N <= 256:
-        def record(name, m2, u2, bits=4, extra_bytes=0):
+        def record(name, m2, u2, extra_bytes=0, **fmt):
             U2 = sum(u2) / len(u2)
-            b2 = synth.algorithmic_bytes(cfg, U2, N, bits=bits) + extra_bytes
+            b2 = synth.algorithmic_bytes(cfg, U2, N, **fmt) + extra_bytes
             rec = dict(workload=name, N=N, ms_per_step=round(m2, 5),
                        tokens_per_s=round(N / (m2 / 1e3), 1), distinct_experts=round(U2, 1),
                        hbm_gbps=round(b2 / m2 / 1e6, 1), hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4))
@@ -309,18 +310,21 @@ def main():
         if "residual" in args.extra:
             m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), residual=True)
             record(f"{args.config}-N{N}-residual", m2, u2, extra_bytes=2 * H)
-        if "int6" in args.extra:
-            # two int6 copies suffice to stream from HBM: one step touches U experts x 10 MB
-            lays6 = []
+        # int6: MiniMax M3's experts; int3: Kimi's widths (gate_up int3 + down int4, group 128).
+        # Two copies suffice to stream from HBM: one step touches U experts x 6-10 MB.
+        for tag, fmt in (("int6", dict(bits=6)), ("int3", dict(bits=3, down_bits=4, group_size=128))):
+            if tag not in args.extra:
+                continue
+            lays_f = []
             for li in range(2):
-                p6 = synth.make_layer(args.config, device=dev, layer=li, bits=6)
-                p6["experts_gate_up"] = TiledExperts(**tile_experts_packed(p6["experts_gate_up"]))
-                p6["experts_down"] = TiledExperts(**tile_experts_packed(p6["experts_down"]))
-                lays6.append(p6)
+                pf = synth.make_layer(args.config, device=dev, layer=li, **fmt)
+                pf["experts_gate_up"] = TiledExperts(**tile_experts_packed(pf["experts_gate_up"]))
+                pf["experts_down"] = TiledExperts(**tile_experts_packed(pf["experts_down"]))
+                lays_f.append(pf)
             torch.cuda.synchronize()
-            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays6)
-            record(f"{args.config}-N{N}-int6", m2, u2, bits=6)
-            del lays6
+            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_f)
+            record(f"{args.config}-N{N}-{tag}", m2, u2, **fmt)
+            del lays_f
 
     # ------------------------------------------------------------------ measured copy peak
     # device-to-device copy of 2 GiB (read + write bytes), the practical HBM ceiling next to

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 2
+#define QMOE_ABI_VERSION 3
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -47,6 +47,8 @@ extern "C" {
 #define QMOE_FMT_BF16 1
 #define QMOE_FMT_INT6_G64 2 /* affine int6 codes, bf16 scale/bias per 64 (MiniMax M3 experts,
                                src/quanta/minimax/model_m3.py:414-450); small regime only */
+#define QMOE_FMT_INT3_G64 3 /* affine int3 codes, bf16 scale/bias per 64 (Kimi's int3 gate/up
+                               stacks, src/quanta/modeling/quantized.py:1-84); small regime only */
 
 /* router weight storage */
 #define QMOE_ROUTER_BF16_TILED 0 /* bf16 [router_rows, H] tiled; row E = shared-expert gate */
@@ -96,6 +98,9 @@ typedef struct {
   int32_t act;           /* QMOE_ACT_* of the routed and shared experts' SwiGLU */
   float act_alpha;       /* SWIGLU_OAI's alpha */
   float act_limit;       /* SILU_CLAMP / SWIGLU_OAI's clamp L (> 0; +inf = none) */
+  int32_t down_format;   /* QMOE_FMT_* of the routed down projection (gate_up: expert_format);
+                            both quantized or both bf16 (Kimi: gate/up int3, down int4,
+                            src/quanta/modeling/quantized.py:4-7) */
 } qmoe_config_t;
 
 /* Prepared (resident) weights of one block; every array is device memory. */
@@ -204,8 +209,9 @@ size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format, in
 int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* w, int64_t N, int k, int H,
                  const uint16_t* shared_out, const float* shared_gate, uint16_t* y, void* stream);
 
-/* Bit-exact dequant of a native affine int4, int6 or int8 stack, group 64 or 128: out[rows, in]
- * bf16 = bf16(fma(scale, code, bias)), codes LSB-first (8 per word, 16 per 3 words, 4 per word). Replaces mx.dequantize
+/* Bit-exact dequant of a native affine int3, int4, int6 or int8 stack, group 64 or 128:
+ * out[rows, in] bf16 = bf16(fma(scale, code, bias)), codes LSB-first (32 per 3 words, 8 per word,
+ * 16 per 3 words, 4 per word). Replaces mx.dequantize
  * (src/quanta/bake/quant.py:32-36; src/quanta/qwen35/artifact.py:105-115); int8 g64 is the
  * bake's shared-expert format (src/quanta/qwen35/bake.py:106-110, 143-151). */
 int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias, int64_t rows,
@@ -221,6 +227,16 @@ int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* 
  * src/quanta/qwen35/model.py:49-55; Qwen35Artifact.moe_packed,
  * src/quanta/qwen35/artifact.py:205-229). */
 int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                   int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                   uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
+
+/* One-time layout transform of a native int3 stack [n_mats][rows][in] (packed u32 [.., in*3/32],
+ * LSB-first bitstream; scale/bias bf16 [.., in/group_size], group 64 or 128) into the tiled int3
+ * layout the decode kernel streams: per 16-row tile and 128-deep superblock a 512-byte plane of
+ * the codes' low two bits then a 256-byte plane of their top bits (same byte count as the native
+ * codes); sb as qmoe_tile_int4. Stands in for holding Kimi's int3 stacks verbatim
+ * (QuantizedSparseMoE.set_experts, src/quanta/modeling/quantized.py:38-49). */
+int qmoe_tile_int3(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                    int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
                    uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
 

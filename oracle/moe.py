@@ -243,7 +243,8 @@ def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
 def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "softmax",
                 norm_topk: bool = True, n_group: int = 1, topk_group: int = 1,
                 scale: float = 1.0, round_weights: bool = False, act: str = "silu",
-                alpha: float = 1.702, limit: float = 0.0, group_size: int = 64, bits: int = 4):
+                alpha: float = 1.702, limit: float = 0.0, group_size: int = 64, bits: int = 4,
+                down_bits: int | None = None):
     """Whole block y = bf16(routed + shared) for x [N, H] (`src/quanta/qwen35/moe.py:154-202`).
 
     `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
@@ -264,7 +265,8 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
                     round_weights=round_weights, group_size=group_size, bits=bits)
     h = swiglu(gu, inter, act, alpha, limit)
     d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
-                   round_weights=round_weights, group_size=group_size, bits=bits)
+                   round_weights=round_weights, group_size=group_size,
+                   bits=bits if down_bits is None else down_bits)
     routed = combine(d, w)
     y = routed.copy()
     sh = None

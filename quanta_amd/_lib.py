@@ -16,13 +16,13 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "quanta_moe.h"
 
 QMOE_OK, QMOE_EINVAL, QMOE_EHIP = 0, -1, -2
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
-FMT_INT4_G64, FMT_BF16, FMT_INT6_G64 = 0, 1, 2
+FMT_INT4_G64, FMT_BF16, FMT_INT6_G64, FMT_INT3_G64 = 0, 1, 2, 3
 ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
 REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
@@ -50,6 +50,7 @@ class QmoeConfig(ctypes.Structure):
         ("act", ctypes.c_int32),
         ("act_alpha", ctypes.c_float),
         ("act_limit", ctypes.c_float),
+        ("down_format", ctypes.c_int32),
     ]
 
 
@@ -94,6 +95,7 @@ SIGNATURES = {
     "qmoe_tile_int4": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_dequant_tiled": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "qmoe_tile_int6": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "qmoe_tile_int3": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_bf16": (_I, [_P, _I64, _I64, _I64, _P, _P]),
 }
 

@@ -355,6 +355,17 @@ static int validate_glu(int act, float alpha, float limit) {
   return 0;
 }
 
+// Kernel format of a QMOE_FMT_* value.
+static int kernel_fmt(int f) {
+  return f == QMOE_FMT_INT4_G64 ? FMT_INT4 : f == QMOE_FMT_INT6_G64 ? FMT_INT6
+         : f == QMOE_FMT_INT3_G64 ? FMT_INT3 : FMT_BF16;
+}
+// int3 or int6 codes on either projection: the large-M kernels stage int4 superblocks only.
+static bool narrow_codes(const qmoe_config_t& c) {
+  return c.expert_format == QMOE_FMT_INT6_G64 || c.expert_format == QMOE_FMT_INT3_G64 ||
+         c.down_format == QMOE_FMT_INT6_G64 || c.down_format == QMOE_FMT_INT3_G64;
+}
+
 static int validate_config(const qmoe_config_t& c) {
   const int rc = validate_routing(1, c.hidden, c.n_experts, c.top_k, c.scoring, c.n_group,
                                   c.topk_group);
@@ -364,11 +375,13 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: the large-M regime needs hidden % 256 == 0");
   if (c.inter <= 0 || c.inter % 128) return fail("config: inter % 128 == 0 required");
   if (c.shared_inter < 0 || c.shared_inter % 128) return fail("config: shared_inter % 128 == 0 required");
-  if (c.expert_format != QMOE_FMT_INT4_G64 && c.expert_format != QMOE_FMT_BF16 &&
-      c.expert_format != QMOE_FMT_INT6_G64)
-    return fail("config: expert_format must be int4-g64 (0), bf16 (1) or int6-g64 (2)");
-  if (c.expert_format == QMOE_FMT_INT6_G64 && c.regime == QMOE_REGIME_LARGE)
-    return fail("config: int6 experts run in the small regime only");
+  if (c.expert_format < QMOE_FMT_INT4_G64 || c.expert_format > QMOE_FMT_INT3_G64 ||
+      c.down_format < QMOE_FMT_INT4_G64 || c.down_format > QMOE_FMT_INT3_G64)
+    return fail("config: expert_format / down_format must be int4-g64 (0), bf16 (1), int6-g64 (2) or int3-g64 (3)");
+  if ((c.expert_format == QMOE_FMT_BF16) != (c.down_format == QMOE_FMT_BF16))
+    return fail("config: gate_up and down must both be quantized or both bf16");
+  if (narrow_codes(c) && c.regime == QMOE_REGIME_LARGE)
+    return fail("config: int3/int6 experts run in the small regime only");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {
     if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 256)
       return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 256");
@@ -416,10 +429,9 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
     const int rc = validate_glu(glu, glu_alpha, glu_limit);
     if (rc) return rc;
   }
-  if (weight_format != QMOE_FMT_INT4_G64 && weight_format != QMOE_FMT_BF16 &&
-      weight_format != QMOE_FMT_INT6_G64)
+  if (weight_format < QMOE_FMT_INT4_G64 || weight_format > QMOE_FMT_INT3_G64)
     return fail("qmoe_grouped_qmm: bad weight_format");
-  if (weight_format != QMOE_FMT_BF16 && !sb) return fail("qmoe_grouped_qmm: int4/int6 need sb");
+  if (weight_format != QMOE_FMT_BF16 && !sb) return fail("qmoe_grouped_qmm: quantized weights need sb");
   if (epilogue < QMOE_EPI_SWIGLU || epilogue > QMOE_EPI_F32) return fail("qmoe_grouped_qmm: bad epilogue");
   if (regime != QMOE_REGIME_SMALL && regime != QMOE_REGIME_LARGE)
     return fail("qmoe_grouped_qmm: regime must be small (1) or large (2)");
@@ -483,7 +495,7 @@ static int dense_regime(const qmoe_config_t& c, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  if (c.expert_format == QMOE_FMT_INT6_G64) return QMOE_REGIME_SMALL;   // no large int6 kernel
+  if (narrow_codes(c)) return QMOE_REGIME_SMALL;   // no large int3/int6 kernel
   return dense_regime(c, N);
 }
 
@@ -500,7 +512,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   if (ws_bytes < L.total) return fail("qmoe_forward: workspace too small");
   if (!wts->router_w || !wts->gu_codes || !wts->dn_codes) return fail("qmoe_forward: missing weights");
   if (c.expert_format != QMOE_FMT_BF16 && (!wts->gu_sb || !wts->dn_sb))
-    return fail("qmoe_forward: int4/int6 experts need scale/bias");
+    return fail("qmoe_forward: quantized experts need scale/bias");
   if (c.shared_inter > 0 && (!wts->sh_gu || !wts->sh_dn)) return fail("qmoe_forward: missing shared expert");
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
@@ -541,8 +553,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                                          ((kHybridSplitRows + kSmallMTile - 1) / kSmallMTile));
   const int64_t hot_bound = (mc + kLargeMTile - 1) / kLargeMTile +
                             std::min<int64_t>(c.n_experts, mc / (kHybridSplitRows + 1));
-  const int wfmt = (c.expert_format == QMOE_FMT_INT4_G64) ? FMT_INT4
-                   : (c.expert_format == QMOE_FMT_INT6_G64) ? FMT_INT6 : FMT_BF16;
+  const int gfmt = kernel_fmt(c.expert_format), dfmt = kernel_fmt(c.down_format);
   const int has_sg = (c.shared_inter > 0 && c.shared_gated) ? 1 : 0;
 
   const int sreg = dense_regime(c, N);
@@ -640,7 +651,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                         hybrid ? tile_map_big : nullptr, L.max_tiles_big);
     if (rc) return rc;
   }
-  const bool f16_acts = (hybrid && wfmt == FMT_INT4);
+  const bool f16_acts = (hybrid && gfmt == FMT_INT4);   // hybrid implies int4 or bf16 experts
   // the cold experts' tiles wait for the permute on the auxiliary stream
   hipStream_t cstream = stream;
   if (hybrid) {
@@ -651,14 +662,14 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // routed grouped matmul over the permuted rows: small kernel over the (cold) 16-row tiles,
   // large kernel over the hot experts' tiles (hybrid: the two on different streams; hot and
   // cold experts own disjoint rows of the output)
-  auto routed = [&](QmmArgs a, int epi, const uint16_t* act16, const float* sinv) {
+  auto routed = [&](QmmArgs a, int fmt, int epi, const uint16_t* act16, const float* sinv) {
     a.tile_map = reinterpret_cast<const int4*>(tile_map);
-    int r = launch_qmm(a, wfmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : bound_small, cstream);
+    int r = launch_qmm(a, fmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : bound_small, cstream);
     if (r || !hybrid) return r;
     a.tile_map = reinterpret_cast<const int4*>(tile_map_big);
     a.act16 = act16;
     a.row_sinv = sinv;
-    return launch_qmm(a, wfmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
+    return launch_qmm(a, fmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
   };
   // 5. routed gate_up + SwiGLU -> h (sorted order)
   {
@@ -672,7 +683,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, stream);
       if (rc) return rc;
     }
-    rc = routed(a, EPI_SWIGLU, x16, x_sinv);
+    rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
     if (rc) return rc;
     if (hybrid) {   // h complete (cold rows from the auxiliary stream) before its fp16 copy
       rc = link(aux->cold, aux->s, stream, "cold gate_up");
@@ -694,7 +705,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = link(aux->hready, stream, aux->s, "h to auxiliary stream");
       if (rc) return rc;
     }
-    rc = routed(a, EPI_BF16, h16, h_sinv);
+    rc = routed(a, dfmt, EPI_BF16, h16, h_sinv);
     if (rc) return rc;
   }
   if (aux) {

@@ -95,6 +95,91 @@ __global__ void __launch_bounds__(256) dequant_native6_kernel(
   out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
+// Code k (3 bits) of a native int3 row (LSB-first bitstream: code k at bits 3k .. 3k+2).
+__device__ __forceinline__ uint32_t int3_code(const uint32_t* __restrict__ row_words, int k) {
+  const int bit = 3 * k, w = bit >> 5, sh = bit & 31;
+  uint32_t v = row_words[w] >> sh;
+  if (sh > 29) v |= row_words[w + 1] << (32 - sh);
+  return v & 7u;
+}
+
+// int3: one thread per 3 packed words = 32 codes of one row (Kimi's int3 expert stacks,
+// src/quanta/modeling/quantized.py:29-84, packed as the bake's bitstream,
+// src/quanta/bake/quant.py:48-63), written as four 16-byte stores; same rounding.
+__global__ void __launch_bounds__(256) dequant_native3_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ bias, int64_t n_chunks, int chunks_per_row, int groups_per_row,
+    int chunks_per_group, uint4* __restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_chunks) return;
+  int64_t row = i / chunks_per_row;
+  int cr = static_cast<int>(i - row * chunks_per_row);
+  int64_t g = row * groups_per_row + cr / chunks_per_group;
+  float s = bf16_to_f32(scale[g]);
+  float b = bf16_to_f32(bias[g]);
+  const uint32_t w[3] = {packed[3 * i], packed[3 * i + 1], packed[3 * i + 2]};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16x2(fmaf(s, static_cast<float>(int3_code(w, 8 * q + 2 * j)), b),
+                         fmaf(s, static_cast<float>(int3_code(w, 8 * q + 2 * j + 1)), b));
+    out[4 * i + q] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// Native int3 -> tiled int3: per 16-row tile and 128-deep superblock 768 B, three words per lane
+// (lane l: row l%16, the codes 16g .. 16g+15 of each 64-column group, g = l/16). The lane's 32
+// codes form 16 pairs, pair q = 8c + 4h + j being codes 2j and 2j + 1 of half h (codes 8h .. 8h+7)
+// of group c; pair q < 15 sits in word q / 5 at bits 3(q % 5) and 16 + 3(q % 5), pair 15 keeps bit
+// i of its two codes in bits 15 and 31 of word i. Scale/bias as the int4 tiling. One thread per
+// lane slot.
+__global__ void __launch_bounds__(256) tile_int3_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ bias, int64_t n_lanes_total, int K, int rows,
+    int halves_per_group, uint32_t* __restrict__ codes, uint16_t* __restrict__ sb) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_lanes_total) return;
+  const int nsb = K / 128, wpr = K * 3 / 32, gpr = K / (64 * halves_per_group);
+  int lane = static_cast<int>(i & 63);
+  int64_t blk = i >> 6;
+  int p = static_cast<int>(blk % nsb);
+  int64_t mr = blk / nsb;
+  int rt = rows / 16;
+  int64_t mat = mr / rt;
+  int R = static_cast<int>(mr - mat * rt);
+  int r = lane & 15, g = lane >> 4;
+  int64_t row = mat * rows + R * 16 + r;
+  const uint32_t* src = packed + row * wpr;
+  uint32_t w[3] = {0u, 0u, 0u};
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int c = q >> 3, h = (q >> 2) & 1, j = q & 3;
+    const int k0 = 128 * p + 64 * c + 16 * g + 8 * h + 2 * j;
+    const uint32_t lo = int3_code(src, k0), hi = int3_code(src, k0 + 1);
+    if (q < 15) {
+      w[q / 5] |= (lo << (3 * (q % 5))) | (hi << (16 + 3 * (q % 5)));
+    } else {
+#pragma unroll
+      for (int b = 0; b < 3; ++b) w[b] |= (((lo >> b) & 1u) << 15) | (((hi >> b) & 1u) << 31);
+    }
+  }
+  uint32_t* blkp = codes + blk * 192 + 3 * lane;
+  blkp[0] = w[0];
+  blkp[1] = w[1];
+  blkp[2] = w[2];
+  if (g == 0) {
+    uint16_t* d = sb + ((blk * 16 + r) * 2) * 2;
+    const int64_t g0 = row * gpr + (2 * p) / halves_per_group;
+    const int64_t g1 = row * gpr + (2 * p + 1) / halves_per_group;
+    d[0] = scale[g0];
+    d[1] = bias[g0];
+    d[2] = scale[g1];
+    d[3] = bias[g1];
+  }
+}
+
 // Native int6 -> tiled int6: per 16-row tile and 128-deep superblock, a 1 KiB plane of the codes'
 // low nibbles laid out exactly as the int4 tiles (lane l: row l%16, words {2g, 2g+1} of each of
 // the two 64-column groups, g = l/16, nibbles interleaved) and a 512-byte plane of their high two
@@ -253,11 +338,20 @@ using namespace qmoe;
 extern "C" int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                             int64_t rows, int64_t in_features, int bits, int group_size,
                             uint16_t* out, void* stream) {
-  if ((bits != 4 && bits != 6 && bits != 8) || (group_size != 64 && group_size != 128))
-    return fail("qmoe_dequant: bits 4, 6 or 8 with group_size 64 or 128 only");
+  if ((bits != 3 && bits != 4 && bits != 6 && bits != 8) || (group_size != 64 && group_size != 128))
+    return fail("qmoe_dequant: bits 3, 4, 6 or 8 with group_size 64 or 128 only");
   if (rows <= 0 || in_features <= 0 || in_features % group_size)
     return fail("qmoe_dequant: rows > 0 and in_features % group_size == 0 required");
   if (!packed || !scale || !bias || !out) return fail("qmoe_dequant: null pointer");
+  if (bits == 3) {
+    const int64_t n_chunks = rows * (in_features / 32);
+    if (in_features % 32) return fail("qmoe_dequant: int3 needs in_features % 32 == 0");
+    if (n_chunks >= (int64_t(1) << 40)) return fail("qmoe_dequant: tensor too large");
+    dequant_native3_kernel<<<grid_for(n_chunks, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        packed, scale, bias, n_chunks, static_cast<int>(in_features / 32),
+        static_cast<int>(in_features / group_size), group_size / 32, reinterpret_cast<uint4*>(out));
+    return check_launch("qmoe_dequant");
+  }
   if (bits == 6) {
     const int64_t n_chunks = rows * (in_features / 16);
     if (n_chunks >= (int64_t(1) << 40)) return fail("qmoe_dequant: tensor too large");
@@ -294,6 +388,22 @@ extern "C" int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, con
       packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
       group_size / 64, reinterpret_cast<uint4*>(tiled_codes), tiled_sb);
   return check_launch("qmoe_tile_int4");
+}
+
+extern "C" int qmoe_tile_int3(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                              int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                              uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream) {
+  if (group_size != 64 && group_size != 128) return fail("qmoe_tile_int3: group_size must be 64 or 128");
+  if (n_mats <= 0 || rows <= 0 || rows % 16 || in_features <= 0 || in_features % 128)
+    return fail("qmoe_tile_int3: need rows % 16 == 0 and in_features % 128 == 0");
+  if (!packed || !scale || !bias || !tiled_codes || !tiled_sb)
+    return fail("qmoe_tile_int3: null pointer");
+  if (rows > (1 << 30) || in_features > (1 << 30)) return fail("qmoe_tile_int3: dims too large");
+  int64_t lanes = n_mats * rows * (in_features / 128) * 4;
+  tile_int3_kernel<<<grid_for(lanes, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
+      group_size / 64, tiled_codes, tiled_sb);
+  return check_launch("qmoe_tile_int3");
 }
 
 extern "C" int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,

@@ -201,8 +201,9 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
 
   if (job_ok) {
     if (fmt_quant(FMT)) {
-      // tile superblock: int4 1 KiB of codes; int6 1 KiB of nibbles + 512 B of high bits
-      constexpr int SBB = (FMT == FMT_INT6) ? 1536 : 1024;
+      // tile superblock: int4 1 KiB of codes; int6 1 KiB of nibbles + 512 B of high bits; int3
+      // 768 B, three words per lane
+      constexpr int SBB = (FMT == FMT_INT6) ? 1536 : (FMT == FMT_INT3) ? 768 : 1024;
       const int nsb = a.K / 128;
       // chunk c = superblocks [c * nsb / CH, (c + 1) * nsb / CH); this wavefront: CPW chunks
       const int p0 = kpart * CPW * nsb / CH, p1 = (kpart + 1) * CPW * nsb / CH;
@@ -233,8 +234,16 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         for (int t = 0; t < NT; ++t) {
           // weights are streamed once per call: nontemporal loads keep them out of the way of
           // the activations that every job of the m-tile re-reads
-          s.q[t] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(cb[t] + static_cast<int64_t>(p) * SBB + lane_c));
+          if constexpr (FMT == FMT_INT3) {
+            // the lane's three code words (one dwordx3 load)
+            const uint32_t* w3 = reinterpret_cast<const uint32_t*>(
+                cb[t] + static_cast<int64_t>(p) * SBB + 12 * lane);
+            s.q[t] = u32x4{__builtin_nontemporal_load(w3), __builtin_nontemporal_load(w3 + 1),
+                           __builtin_nontemporal_load(w3 + 2), 0u};
+          } else {
+            s.q[t] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(cb[t] + static_cast<int64_t>(p) * SBB + lane_c));
+          }
           if constexpr (FMT == FMT_INT6)
             s.hq[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(
                 cb[t] + static_cast<int64_t>(p) * SBB + 1024 + 8 * lane));
@@ -264,6 +273,9 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
               const uint32_t hw = gg ? s.hq[t].y : s.hq[t].x;
               r = mfma16(A0, unpack_q128_6(w0, hw, 0), zero4);
               r = mfma16(A1, unpack_q128_6(w1, hw, 1), r);
+            } else if constexpr (FMT == FMT_INT3) {
+              r = mfma16(A0, unpack_q128_3(s.q[t].x, s.q[t].y, s.q[t].z, gg, 0), zero4);
+              r = mfma16(A1, unpack_q128_3(s.q[t].x, s.q[t].y, s.q[t].z, gg, 1), r);
             } else {
               r = mfma16(A0, unpack_q128(w0), zero4);
               r = mfma16(A1, unpack_q128(w1), r);
@@ -1083,7 +1095,7 @@ static void launch_small_j(const QmmArgs& a, int jpw, int64_t mtiles, hipStream_
       launch_small_k<FMT, EPI, W, CPW, (EPI == EPI_SWIGLU) ? 1 : 2>(a, mtiles, stream);
     else
       launch_small_k<FMT, EPI, W, CPW, 1>(a, mtiles, stream);
-  } else if constexpr (FMT == FMT_INT4) {
+  } else if constexpr (FMT == FMT_INT4 || FMT == FMT_INT3) {
     if (EPI != EPI_SWIGLU && jpw == 4)
       launch_small_k<FMT, EPI, W, CPW, (EPI == EPI_SWIGLU) ? 2 : 4>(a, mtiles, stream);
     else if (jpw == 2)
@@ -1190,18 +1202,19 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (mtile_bound <= 0) return 0;
   if (mtile_bound > 65535) return fail("qmm: too many m-tiles for one launch");
   if (regime == QMOE_REGIME_SMALL) {
-    if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int4/int6 need K % 128 == 0");
+    if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int3/int4/int6 need K % 128 == 0");
     if (fmt == FMT_BF16 && a.K % 32) return fail("qmm: bf16 needs K % 32 == 0");
     if (a.n_rows % (epi == EPI_SWIGLU ? 32 : 16)) return fail("qmm: weight rows not a tile multiple");
     // The chunk count depends on the shape only (never on the token count), so a row's
     // summation order, and therefore its result, is the same at every batch size (batch
-    // invariance). int4 chunks hold >= 4 superblocks; bf16 (router, shared expert) chunks
-    // ~8 32-deep steps, one wavefront each, which spreads the few dense row tiles over enough
-    // wavefronts.
+    // invariance). int3/int4/int6 chunks hold >= 4 superblocks (int3, whose superblocks are
+    // 3/4 the bytes of int4's: >= 16 at K = 4096, where two chunks measured faster than four);
+    // bf16 (router, shared expert) chunks ~8 32-deep steps, one wavefront each, which spreads
+    // the few dense row tiles over enough wavefronts.
     int ch;
-    if (fmt == FMT_INT4) {
+    if (fmt_quant(fmt)) {
       const int nsb = a.K / 128;
-      ch = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;
+      ch = (nsb >= (fmt == FMT_INT3 ? 64 : 32)) ? 4 : (nsb >= 8) ? 2 : 1;
     } else {
       ch = bf16_chunks(a.K);
     }
@@ -1216,6 +1229,10 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT6, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT6, EPI_BF16);
       else QMOE_SMALL(FMT_INT6, EPI_F32);
+    } else if (fmt == FMT_INT3) {
+      if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT3, EPI_SWIGLU);
+      else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT3, EPI_BF16);
+      else QMOE_SMALL(FMT_INT3, EPI_F32);
     } else {
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_BF16, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_BF16, EPI_BF16);
@@ -1223,9 +1240,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     }
 #undef QMOE_SMALL
   } else {
-    if (fmt == FMT_INT6)
-      return fail("qmm(large): int6 weights run in the small regime only (a 1.5 KiB int6 tile "
-                  "superblock does not fit the large kernels' LDS slots)");
+    if (fmt == FMT_INT6 || fmt == FMT_INT3)
+      return fail("qmm(large): int3/int6 weights run in the small regime only (the large kernels "
+                  "stage int4 tile superblocks)");
     if (a.K % 128) return fail("qmm(large): K % 128 == 0 required");
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
     if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))

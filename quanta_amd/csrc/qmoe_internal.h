@@ -103,6 +103,28 @@ __device__ __forceinline__ bf16x8_t unpack_q128_6(uint32_t w, uint32_t hw, int h
   return v;
 }
 
+// int3 tiles: the lane's three words w0..w2 hold its 32 codes as 16 pairs; pair q = 8c + 4h + j
+// (group c, half h, pair j of the half: codes 2j and 2j + 1) sits, for q < 15, in word q / 5 at
+// bits 3(q % 5) .. +2 and 16 + 3(q % 5) .. +2, so one shift and one and-or make the bf16 pair
+// 128 + code; pair 15 keeps bit i of each code in bit 15 / bit 31 of word i. 128 + q (q < 8) is
+// exact in bf16.
+__device__ __forceinline__ bf16x8_t unpack_q128_3(uint32_t w0, uint32_t w1, uint32_t w2, int c,
+                                                  int h) {
+  const uint32_t o = 0x43004300u;
+  const uint32_t w[3] = {w0, w1, w2};
+  bf16x8_t v;
+  uint32_t* p = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = 8 * c + 4 * h + j;
+    if (q < 15)
+      p[j] = ((w[q / 5] >> (3 * (q % 5))) & 0x00070007u) | o;
+    else
+      p[j] = ((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) | ((w2 >> 13) & 0x00040004u) | o;
+  }
+  return v;
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 q) {
   bf16x8_t v;
   __builtin_memcpy(&v, &q, 16);
@@ -211,9 +233,9 @@ struct QmmArgs {
   float glu_limit;            // clamp of SILU_CLAMP / SWIGLU_OAI
 };
 
-enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2 };
-// affine-quantized weight formats (int4 or int6 codes with per-64 scale/bias)
-constexpr bool fmt_quant(int fmt) { return fmt == FMT_INT4 || fmt == FMT_INT6; }
+enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3 };
+// affine-quantized weight formats (int3, int4 or int6 codes with per-64 scale/bias)
+constexpr bool fmt_quant(int fmt) { return fmt == FMT_INT4 || fmt == FMT_INT6 || fmt == FMT_INT3; }
 enum { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,

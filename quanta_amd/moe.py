@@ -71,8 +71,8 @@ def _cfg(cfg, name, default=None):
 class TiledExperts(dict):
     """A routed expert stack resident in the MFMA-tiled layout.
 
-    Keys: "format" ("int4_g64" | "int6_g64" | "bf16"), "codes" (tiled int4 or int6 words / tiled
-    bf16), "sb" (tiled
+    Keys: "format" ("int4_g64" | "int6_g64" | "int3_g64" | "bf16"), "codes" (tiled int4 / int6 /
+    int3 words or tiled bf16), "sb" (tiled
     scale+bias, int4 only), "shape" (E, rows, K), "group_size", "bits". Produced from the
     reference's packed triplet {packed, scale, bias, group_size, bits}
     (src/quanta/qwen35/artifact.py:199-203) or from a bf16 [E, rows, K] stack.
@@ -80,27 +80,28 @@ class TiledExperts(dict):
 
     @property
     def is_packed(self) -> bool:
-        return self["format"] in ("int4_g64", "int6_g64")
+        return self["format"] in ("int4_g64", "int6_g64", "int3_g64")
 
 
 def tile_experts_packed(d: dict) -> TiledExperts:
-    """Reference packed triplet -> TiledExperts. Fails loud unless bits is 4 or 6 and group_size
+    """Reference packed triplet -> TiledExperts. Fails loud unless bits is 3, 4 or 6 and group_size
     is 64 or 128 (the kernels' formats: 128-column groups are tiled as two 64-column halves with
     the same scale and bias; int6 is MiniMax M3's expert format, src/quanta/minimax/
-    model_m3.py:414-450; the manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
+    model_m3.py:414-450; int3 Kimi's gate/up width, src/quanta/modeling/quantized.py:4-7; the
+    manifest is the source of truth, src/quanta/qwen35/artifact.py:194)."""
     if isinstance(d, TiledExperts):
         return d
     bits, gs = int(d["bits"]), int(d["group_size"])
-    if bits not in (4, 6) or gs not in (64, 128):
-        raise ValueError(f"packed experts must be affine int4 or int6 with group_size 64 or 128 "
-                         f"(got bits={bits}, group_size={gs})")
+    if bits not in (3, 4, 6) or gs not in (64, 128):
+        raise ValueError(f"packed experts must be affine int3, int4 or int6 with group_size 64 or "
+                         f"128 (got bits={bits}, group_size={gs})")
     packed, scale, bias = d["packed"], d["scale"], d["bias"]
     if scale.dtype != torch.bfloat16 or bias.dtype != torch.bfloat16:
         raise TypeError("packed experts need bf16 scale and bias")
     if packed.dim() != 3:
         raise ValueError("packed experts must be a stacked [E, out, in*bits/32] tensor")
     E, rows, W = packed.shape
-    tile = ops.tile_int4 if bits == 4 else ops.tile_int6
+    tile = {4: ops.tile_int4, 6: ops.tile_int6, 3: ops.tile_int3}[bits]
     codes, sb = tile(packed.contiguous(), scale.contiguous(), bias.contiguous(), group_size=gs)
     return TiledExperts(format=f"int{bits}_g64", codes=codes, sb=sb, shape=(E, rows, W * 32 // bits),
                         group_size=gs, bits=bits)
@@ -290,10 +291,11 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     c.n_group = int(_cfg(cfg, "n_group", 1))
     c.topk_group = int(_cfg(cfg, "topk_group", 1))
     c.routed_scale = float(_cfg(cfg, "routed_scaling_factor", 1.0))
-    if packed and gu["format"] != dn["format"]:
-        raise ValueError("experts_gate_up and experts_down must use the same bit width")
-    c.expert_format = (L.FMT_BF16 if not packed else
-                       L.FMT_INT6_G64 if gu["format"] == "int6_g64" else L.FMT_INT4_G64)
+    fmts = {"int4_g64": L.FMT_INT4_G64, "int6_g64": L.FMT_INT6_G64, "int3_g64": L.FMT_INT3_G64,
+            "bf16": L.FMT_BF16}
+    # gate_up and down may differ in width (Kimi: gate/up int3, down int4,
+    # src/quanta/modeling/quantized.py:4-7)
+    c.expert_format, c.down_format = fmts[gu["format"]], fmts[dn["format"]]
     c.router_format = L.ROUTER_BF16_TILED if rkind == "bf16" else L.ROUTER_F32
     c.router_rows = rrows
     c.shared_gated = int(sgate is not None)

@@ -52,8 +52,8 @@ def dequant(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *, bi
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
-    if bits not in (4, 6, 8):
-        raise ValueError("dequant: bits must be 4, 6 or 8")
+    if bits not in (3, 4, 6, 8):
+        raise ValueError("dequant: bits must be 3, 4, 6 or 8")
     if (packed.shape[-1] * 32) % bits:
         raise ValueError("dequant: packed words do not hold a whole number of codes")
     K = packed.shape[-1] * 32 // bits
@@ -90,31 +90,44 @@ def tile_int4(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
     return codes, sb
 
 
-def tile_int6(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
-              group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
-    """Native int6 stack [E, rows, K*6/32] (+ scale/bias [E, rows, K/group_size]) -> the tiled
-    int6 layout of the decode kernel (codes: nibble plane + high-bit plane per tile superblock,
-    the same byte count; sb as tile_int4)."""
+def _tile_narrow(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, bits: int,
+                 group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native int3/int6 stack [E, rows, K*bits/32] (+ scale/bias [E, rows, K/group_size]) -> the
+    tiled layout of the decode kernel (codes: the planes of the code bits per tile superblock, the
+    same byte count; sb as tile_int4)."""
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
     if packed.dim() == 2:
         packed, scale, bias = packed[None], scale[None], bias[None]
     if packed.dim() != 3:
-        raise ValueError("tile_int6: expected [E, rows, K*6/32]")
+        raise ValueError(f"tile_int{bits}: expected [E, rows, K*{bits}/32]")
     E, rows, W = packed.shape
-    if (W * 32) % 6:
-        raise ValueError("tile_int6: packed words do not hold a whole number of codes")
-    K = W * 32 // 6
+    if (W * 32) % bits:
+        raise ValueError(f"tile_int{bits}: packed words do not hold a whole number of codes")
+    K = W * 32 // bits
     if group_size not in (64, 128):
-        raise ValueError("tile_int6: group_size must be 64 or 128")
+        raise ValueError(f"tile_int{bits}: group_size must be 64 or 128")
     if scale.shape != (E, rows, K // group_size) or bias.shape != scale.shape:
-        raise ValueError(f"tile_int6: scale/bias must be [E, rows, K/{group_size}]")
+        raise ValueError(f"tile_int{bits}: scale/bias must be [E, rows, K/{group_size}]")
     codes = torch.empty(E * rows * W, dtype=torch.int32, device=packed.device)
     sb = torch.empty(E * rows * (K // 64) * 2, dtype=torch.bfloat16, device=packed.device)
-    L.check(L.load().qmoe_tile_int6(_p(packed), _p(scale), _p(bias), E, rows, K, group_size,
-                                    _p(codes), _p(sb), _stream(packed.device)), "qmoe_tile_int6")
+    fn = L.load().qmoe_tile_int6 if bits == 6 else L.load().qmoe_tile_int3
+    L.check(fn(_p(packed), _p(scale), _p(bias), E, rows, K, group_size, _p(codes), _p(sb),
+               _stream(packed.device)), f"qmoe_tile_int{bits}")
     return codes, sb
+
+
+def tile_int6(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
+              group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native int6 stack -> the decode kernel's tiled int6 layout (qmoe_tile_int6)."""
+    return _tile_narrow(packed, scale, bias, 6, group_size)
+
+
+def tile_int3(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
+              group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native int3 stack -> the decode kernel's tiled int3 layout (qmoe_tile_int3)."""
+    return _tile_narrow(packed, scale, bias, 3, group_size)
 
 
 def dequant_tiled(codes: torch.Tensor, sb: torch.Tensor, n_mats: int, rows: int,
@@ -218,7 +231,7 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     _need(act, torch.bfloat16, "act")
     if act.dim() != 2 or act.shape[1] != K:
         raise ValueError("grouped_qmm: act must be [rows, K]")
-    if weight_format in (L.FMT_INT4_G64, L.FMT_INT6_G64):
+    if weight_format in (L.FMT_INT4_G64, L.FMT_INT6_G64, L.FMT_INT3_G64):
         codes = _words(codes, "codes")
         _need(sb, torch.bfloat16, "sb")
     else:

@@ -80,19 +80,19 @@ def _normal(shape, std, g, device, dtype=torch.float32):
     return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std).to(dtype)
 
 
-def _quantized_stack(E, rows, K, g, device, chunk_elems=1 << 28, bits=4):
-    """Stack of E experts [rows, K] ~ N(0, 0.02) bf16, RTN int`bits` g64 -> packed triplet dict."""
+def _quantized_stack(E, rows, K, g, device, chunk_elems=1 << 28, bits=4, group_size=64):
+    """Stack of E experts [rows, K] ~ N(0, 0.02) bf16, RTN int`bits` -> packed triplet dict."""
     packed = torch.empty(E, rows, K * bits // 32, dtype=torch.int32, device=device)
-    scale = torch.empty(E, rows, K // 64, dtype=torch.bfloat16, device=device)
+    scale = torch.empty(E, rows, K // group_size, dtype=torch.bfloat16, device=device)
     bias = torch.empty_like(scale)
     per = max(1, chunk_elems // (rows * K))
     for e0 in range(0, E, per):
         e1 = min(E, e0 + per)
         w = _normal((e1 - e0, rows, K), 0.02, g, device, torch.bfloat16)
-        q, s, b = quantize_affine(w, bits, 64, scale_dtype=torch.bfloat16)
+        q, s, b = quantize_affine(w, bits, group_size, scale_dtype=torch.bfloat16)
         packed[e0:e1], scale[e0:e1], bias[e0:e1] = q, s, b
         del w, q, s, b
-    return {"packed": packed, "scale": scale, "bias": bias, "group_size": 64, "bits": bits}
+    return {"packed": packed, "scale": scale, "bias": bias, "group_size": group_size, "bits": bits}
 
 
 def zipf_logit_bias(E: int, g: torch.Generator, device) -> torch.Tensor:
@@ -113,9 +113,11 @@ def zipf_router(gate: torch.Tensor, seed: int = 4) -> torch.Tensor:
 
 
 def make_layer(name: str | SynthSpec, *, device="cuda", seed: int | None = None,
-               layer: int = 0, bits: int = 4) -> dict:
+               layer: int = 0, bits: int = 4, down_bits: int | None = None,
+               group_size: int = 64) -> dict:
     """Parameter dict with the reference keys (src/quanta/qwen35/moe.py:159-161); routed experts as
-    packed triplets (int`bits`, group 64) in the reference's native layout."""
+    packed triplets in the reference's native layout (gate_up int`bits`, down int`down_bits`,
+    default the same width)."""
     s = SPECS[name] if isinstance(name, str) else name
     c = s.cfg
     cid = int(name[1]) if isinstance(name, str) else 9
@@ -126,8 +128,9 @@ def make_layer(name: str | SynthSpec, *, device="cuda", seed: int | None = None,
     if s.zipf:
         gate[:, 0] = zipf_logit_bias(E, g, device)
     p["gate"] = gate if s.router_fp32 else gate.to(torch.bfloat16)
-    p["experts_gate_up"] = _quantized_stack(E, 2 * I, H, g, device, bits=bits)
-    p["experts_down"] = _quantized_stack(E, H, I, g, device, bits=bits)
+    p["experts_gate_up"] = _quantized_stack(E, 2 * I, H, g, device, bits=bits, group_size=group_size)
+    p["experts_down"] = _quantized_stack(E, H, I, g, device, group_size=group_size,
+                                         bits=bits if down_bits is None else down_bits)
     if Is > 0:
         p["shared_gate_proj"] = _normal((Is, H), 0.02, g, device, torch.bfloat16)
         p["shared_up_proj"] = _normal((Is, H), 0.02, g, device, torch.bfloat16)
@@ -150,13 +153,15 @@ def make_inputs(name: str | SynthSpec, N: int, *, device="cuda", seed: int = 0) 
 
 
 def algorithmic_bytes(cfg, distinct_experts: int, N: int, router_bytes_per_elem: int = 2,
-                      bits: int = 4) -> int:
-    """Bytes a layer call must move at minimum: U*B_e + S + R + A with B_e = 3*I*H*(bits/8 + 1/16)
-    (codes + bf16 scale and bias per 64: 0.5625 B per weight for int4, 0.8125 for int6),
+                      bits: int = 4, down_bits: int | None = None, group_size: int = 64) -> int:
+    """Bytes a layer call must move at minimum: U*B_e + S + R + A with
+    B_e = 2*I*H*(bits/8 + 4/g) + I*H*(down_bits/8 + 4/g) (codes + a bf16 scale and bias per group
+    of g: 0.5625 B per weight for int4 g64, 0.8125 for int6 g64, 0.40625 for int3 g128),
     S = 3*Is*H*2, R = E*H*elem, A = 4*N*H (bf16 in and out)."""
     H, E, I = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size
     Is = cfg.shared_expert_intermediate_size
-    be = 3 * I * H * (8 * bits + 4) // 64
+    db = bits if down_bits is None else down_bits
+    be = (2 * I * H * (bits * group_size + 32) + I * H * (db * group_size + 32)) // (8 * group_size)
     return distinct_experts * be + 3 * Is * H * 2 + E * H * router_bytes_per_elem + 4 * N * H
 
 

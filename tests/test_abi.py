@@ -13,7 +13,7 @@ from quanta_amd import _lib as L
 
 def test_library_loads_and_abi_version():
     lib = L.load()
-    assert lib.qmoe_abi_version() == L.ABI_VERSION == 2
+    assert lib.qmoe_abi_version() == L.ABI_VERSION == 3
 
 
 def test_every_header_symbol_is_exported_and_bound():
@@ -43,7 +43,8 @@ _DUMMY = ctypes.c_void_p(16)   # never dereferenced: each call fails validation 
 
 
 @pytest.mark.parametrize("call, fragment", [
-    (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 3, 64, None, None), "bits 4, 6 or 8"),
+    (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 5, 64, None, None), "bits 3, 4, 6 or 8"),
+    (lambda lib: lib.qmoe_tile_int3(None, None, None, 1, 16, 96, 64, None, None, None), "in_features % 128"),
     (lambda lib: lib.qmoe_tile_int6(None, None, None, 1, 16, 100, 64, None, None, None), "in_features % 128"),
     (lambda lib: lib.qmoe_dequant(None, None, None, 4, 100, 4, 64, None, None), "in_features"),
     (lambda lib: lib.qmoe_tile_int4(None, None, None, 1, 15, 128, 64, None, None, None), "rows % 16"),
@@ -111,3 +112,24 @@ def test_ops_refuse_cpu_tensors():
 
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.tile_bf16(torch.zeros(16, 32, dtype=torch.bfloat16))
+
+
+def test_forward_rejects_mixed_bf16_and_unknown_down_format():
+    lib = L.load()
+    base = dict(hidden=512, n_experts=16, top_k=2, inter=128, shared_inter=0, scoring=0, norm_topk=1,
+                n_group=1, topk_group=1, routed_scale=1.0, router_format=1, router_rows=0,
+                shared_gated=0, regime=0)
+    w = L.QmoeWeights()
+    dummy = ctypes.c_void_p(16)
+    for ef, df, frag in ((L.FMT_INT3_G64, L.FMT_BF16, "both be quantized or both bf16"),
+                         (L.FMT_INT4_G64, 7, "down_format must be"),
+                         (L.FMT_INT3_G64, L.FMT_INT4_G64, None)):
+        cfg = L.QmoeConfig(expert_format=ef, down_format=df, **base)
+        if frag is None:   # a valid mix: the workspace query accepts it
+            assert lib.qmoe_forward_workspace(ctypes.byref(cfg), 4) > 0
+            cfg.regime = L.REGIME_LARGE
+            rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
+            assert rc == L.QMOE_EINVAL and "small regime only" in _last_error()
+            continue
+        rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
+        assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()

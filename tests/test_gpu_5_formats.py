@@ -2,6 +2,9 @@
 
 - int6 expert stacks (MiniMax M3, src/quanta/minimax/model_m3.py:414-450) on the decode kernel:
   dequant bit-exact, the grouped matmul and the block against the oracle.
+- int3 expert stacks, alone and as Kimi's per-projection widths (gate/up int3 + down int4, group
+  128; src/quanta/modeling/quantized.py:4-7) on the decode kernel: dequant bit-exact, the grouped
+  matmul and the block against the oracle.
 - int4 (and int8) stacks with 128-column groups (Kimi's QuantizedSparseMoE layout,
   src/quanta/modeling/quantized.py:29-34): dequant bit-exact, the tiled layout lossless, and the
   block against the oracle at decode and prefill sizes.
@@ -75,11 +78,11 @@ def _inputs(dev, N, H, seed, scale=4.0):
     return (torch.randn(N, H, generator=g) * scale).to(torch.bfloat16).to(dev)
 
 
-def _check(p, cfg, x, what, *, act="silu", alpha=1.702, limit=0.0, gs=64, bits=4):
+def _check(p, cfg, x, what, *, act="silu", alpha=1.702, limit=0.0, gs=64, bits=4, down_bits=None):
     y = qwen35_moe(x[None], p, cfg)[0]
     _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=cfg.num_experts_per_tok,
                            inter=cfg.moe_intermediate_size, act=act, alpha=alpha, limit=limit,
-                           group_size=gs, bits=bits)
+                           group_size=gs, bits=bits, down_bits=down_bits)
     assert_close(f64(y), it["y_exact"], what)
     return y, it
 
@@ -198,3 +201,96 @@ def test_int6_large_regime_refused(gpu):
     x = _inputs(gpu, 300, 512, 1)
     with pytest.raises(ValueError, match="int6"):
         qwen35_moe(x[None], p, cfg, regime=L.REGIME_LARGE)
+
+
+
+# ------------------------------------------------------------------------------------ int3
+@pytest.mark.parametrize("gs", [64, 128])
+def test_dequant_int3_bit_exact(gpu, gs):
+    rng = np.random.default_rng(gs + 3)
+    rows, K = 40, 384
+    codes = rng.integers(0, 8, size=(rows, K))
+    words = oq.pack_affine(codes, 3)
+    s = oq.f32_to_bf16_bits((rng.random((rows, K // gs)) * 0.05 + 1e-3).astype(np.float32))
+    b = oq.f32_to_bf16_bits((rng.standard_normal((rows, K // gs)) * 0.3).astype(np.float32))
+    got = ops.dequant(words_dev(words, gpu), bf16_dev(s, gpu), bf16_dev(b, gpu), bits=3, group_size=gs)
+    assert np.array_equal(bits_np(got), oq.dequant_bf16_bits(words, s, b, K, bits=3, group_size=gs))
+
+
+@pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
+@pytest.mark.parametrize("N,k,E,H,rows", [(1, 4, 8, 4096, 256), (7, 3, 6, 256, 256),
+                                          (200, 4, 4, 1024, 128), (1024, 4, 32, 256, 512)])
+def test_grouped_qmm_int3_vs_oracle(gpu, epi, N, k, E, H, rows):
+    """The decode kernel's int3 path (tiled 2-bit + top-bit planes) against the oracle's exact
+    affine weights, through several launch shapes."""
+    rng = np.random.default_rng(3 * N + E + H + rows)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(N)]).astype(np.int32)
+    x = oq.round_bf16(rng.standard_normal((N, H)))
+    w = torch.from_numpy(rng.standard_normal((E, rows, H)).astype(np.float32) * 0.05).to(gpu)
+    packed, s, b = quantize_affine(w, 3, group_size=64)
+    dense = oq.dequant_exact(words_np(packed), bits_np(s), bits_np(b), H, bits=3)
+    counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(torch.from_numpy(idx).to(gpu), E,
+                                                                        L.SMALL_M_TILE)
+    codes, sb = ops.tile_int3(packed, s, b)
+    out = ops.grouped_qmm(bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu), K=H, n_rows=rows,
+                          weight_format=L.FMT_INT3_G64, codes=codes, sb=sb, epilogue=epi,
+                          out_rows=N * k, regime=L.REGIME_SMALL, slot_of=sorted_slot, slot_div=k,
+                          n_slots=N * k, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
+                          n_experts=E)
+    order = sorted_slot.cpu().numpy()
+    full = np.einsum("mh,moh->mo", x[order // k], dense[idx.reshape(-1)[order]])
+    want = oq.round_bf16(full)
+    if epi == L.EPI_SWIGLU:
+        want = om.swiglu(want, rows // 2)
+    assert_close(f64(out), want, f"int3 qmm epi={epi} N={N} E={E} H={H} rows={rows}", rel_l2=4e-3)
+
+
+def _layer_widths(dev, gs, seed, gu_bits, dn_bits, H=512, E=8, I=256, Is=256):
+    p = _layer(dev, gs, seed, H, E, I, Is)
+    g = torch.Generator(device="cpu").manual_seed(seed + 1)
+    for key, shape, bits in (("experts_gate_up", (E, 2 * I, H), gu_bits), ("experts_down", (E, H, I), dn_bits)):
+        packed, s, b = quantize_affine((torch.randn(*shape, generator=g) * 0.02).to(dev), bits, group_size=gs)
+        p[key] = {"packed": packed, "scale": s, "bias": b, "group_size": gs, "bits": bits}
+    return p
+
+
+@pytest.mark.parametrize("gs,gu_bits,dn_bits", [(128, 3, 4), (64, 3, 3), (128, 6, 4), (64, 4, 6)])
+@pytest.mark.parametrize("N", [1, 8, 40, 300])
+def test_block_mixed_widths_vs_oracle(gpu, gs, gu_bits, dn_bits, N):
+    """Per-projection widths through the block: Kimi's gate/up int3 + down int4 at group 128, int3
+    throughout, and the other mixes of the decode kernel's formats. Slot-major, fused shared
+    expert, auxiliary-stream shared expert, and above 256 tokens the decode kernel (no narrow
+    format has a large-regime kernel, so the block keeps such layers on the decode kernel)."""
+    cfg = MoEConfig(512, 8, 2, 256, 256)
+    p = _layer_widths(gpu, gs, 13 * N + gs + gu_bits, gu_bits, dn_bits)
+    _check(p, cfg, _inputs(gpu, N, 512, N), f"gate_up int{gu_bits} down int{dn_bits} g{gs} N={N}",
+           gs=gs, bits=gu_bits, down_bits=dn_bits)
+
+
+def test_int3_large_regime_refused(gpu):
+    cfg = MoEConfig(512, 8, 2, 256, 256)
+    p = _layer_widths(gpu, 128, 1, 3, 4)
+    x = _inputs(gpu, 300, 512, 1)
+    with pytest.raises(ValueError, match="int3|int6|narrow|large"):
+        qwen35_moe(x[None], p, cfg, regime=L.REGIME_LARGE)
+
+
+@pytest.mark.parametrize("fmt", [dict(bits=3, down_bits=4, group_size=128), dict(bits=6)],
+                         ids=["int3+int4-g128", "int6"])
+def test_narrow_formats_batch_invariance_full_size(gpu, fmt):
+    """The K-chunk count of the int3/int6 decode kernel follows the weight shape only, so a token's
+    output at 128 tokens (few wavefronts per job, two chunks each) is bit-identical to its output
+    alone (one chunk per wavefront), at the c2 shapes (K = 4096 gate_up, K = 1024 down)."""
+    from quanta_amd import synth
+    from quanta_amd.moe import TiledExperts, tile_experts_packed
+
+    cfg = synth.spec("c2").cfg
+    p = synth.make_layer("c2", device=gpu, **fmt)
+    p["experts_gate_up"] = TiledExperts(**tile_experts_packed(p["experts_gate_up"]))
+    p["experts_down"] = TiledExperts(**tile_experts_packed(p["experts_down"]))
+    N = 128
+    x = synth.make_inputs("c2", N, device=gpu, seed=N)
+    full = qwen35_moe(x[None], p, cfg)[0]
+    for t in (0, N // 3, N - 1):
+        single = qwen35_moe(x[t:t + 1][None], p, cfg)[0, 0]
+        assert torch.equal(single, full[t]), f"token {t} of {N}"

@@ -491,3 +491,25 @@ def test_dequant_int6_explicit_loop():
         for r in range(rows):
             for k in range(K):
                 assert got[r, k] == s[r, k // gs] * codes[r, k] + b[r, k // gs]
+
+
+def test_dequant_int3_explicit_loop():
+    """int3 codes (Kimi's gate/up width, src/quanta/modeling/quantized.py:4-7) packed as the
+    LSB-first bitstream (codes straddle word boundaries: code 10 holds bits 30..32), dequantized
+    element by element for groups of 64 and 128."""
+    rng = np.random.default_rng(3)
+    rows, K = 2, 256
+    codes = rng.integers(0, 8, size=(rows, K))
+    words = oq.pack_affine(codes, 3)
+    assert words.shape == (rows, K * 3 // 32)
+    # code 10 of row 0: bits 30, 31 of word 0 and bit 0 of word 1
+    c10 = ((int(words[0, 0]) >> 30) & 3) | ((int(words[0, 1]) & 1) << 2)
+    assert c10 == codes[0, 10]
+    for gs in (64, 128):
+        sb = oq.f32_to_bf16_bits(rng.standard_normal((rows, K // gs)).astype(np.float32) * 0.1)
+        bb = oq.f32_to_bf16_bits(rng.standard_normal((rows, K // gs)).astype(np.float32))
+        got = oq.dequant_exact(words, sb, bb, K, bits=3, group_size=gs)
+        s, b = oq.bf16_bits_to_f32(sb).astype(np.float64), oq.bf16_bits_to_f32(bb).astype(np.float64)
+        for r in range(rows):
+            for k in range(K):
+                assert got[r, k] == s[r, k // gs] * codes[r, k] + b[r, k // gs]
