@@ -15,8 +15,8 @@ roofline (routed gate_up+SwiGLU: algorithmic bytes per launch / its average dura
 on the launch stream), a sweep over the other decode batches and the 4096-token prefill, the
 widened rows at the headline batch (`--extra`: the block with the decoder layer's RMSNorm and
 residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, and with
-Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies), and the CPU
-baseline (the torch-CPU port in oracle/torch_cpu.py on the host
+Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies; and with
+DeepSeek-V4's activation-aware expert scales on the int4 experts), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
 cores, bounded sample).
 
 `roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
@@ -58,8 +58,9 @@ def parse():
     ap.add_argument("--zipf", action="store_true",
                     help="headline workload with c4's Zipf(1.1) routing (profiling the prefill)")
     ap.add_argument("--kernel-reps", type=int, default=64)
-    ap.add_argument("--extra", default="residual,int6,int3",
-                    help="widened rows timed at the headline batch ('' = none): residual, int6, int3")
+    ap.add_argument("--extra", default="residual,int6,int3,awq",
+                    help="widened rows timed at the headline batch ('' = none): residual, int6, "
+                         "int3, awq")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
@@ -298,9 +299,9 @@ def main():
     # the block with the decoder layer's norm and residual add (qmoe_forward_residual), and the
     # layer with int6 experts (MiniMax M3's format), at the headline batch
     if args.only == "" and N <= 256:
-        def record(name, m2, u2, extra_bytes=0, **fmt):
+        def record(name, m2, u2, extra_bytes=0, per_expert_bytes=0, **fmt):
             U2 = sum(u2) / len(u2)
-            b2 = synth.algorithmic_bytes(cfg, U2, N, **fmt) + extra_bytes
+            b2 = synth.algorithmic_bytes(cfg, U2, N, **fmt) + extra_bytes + U2 * per_expert_bytes
             rec = dict(workload=name, N=N, ms_per_step=round(m2, 5),
                        tokens_per_s=round(N / (m2 / 1e3), 1), distinct_experts=round(U2, 1),
                        hbm_gbps=round(b2 / m2 / 1e6, 1), hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4))
@@ -325,6 +326,25 @@ def main():
             m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_f)
             record(f"{args.config}-N{N}-{tag}", m2, u2, **fmt)
             del lays_f
+        if "awq" in args.extra:
+            # DeepSeek-V4's activation-aware scales on the int4 experts: each routed row's
+            # activation divided per input channel before gate, up and down (bf16 scales [E,2,H]
+            # and [E,I], read per distinct expert)
+            lays_a = []   # the resident int4 layer copies, with scales
+            for li, pl in enumerate(layers):
+                pa = dict(pl)
+                g = torch.Generator(device="cpu").manual_seed(77 + li)
+                E_, I_ = cfg.num_experts, cfg.moe_intermediate_size
+                s_gu = (2.0 ** (torch.rand(E_, 2, H, generator=g) * 2 - 1)).to(torch.bfloat16).to(dev)
+                s_dn = (2.0 ** (torch.rand(E_, I_, generator=g) * 2 - 1)).to(torch.bfloat16).to(dev)
+                pa["experts_gate_up"] = TiledExperts(dict(pa["experts_gate_up"], awq_scale=s_gu))
+                pa["experts_down"] = TiledExperts(dict(pa["experts_down"], awq_scale=s_dn))
+                lays_a.append(pa)
+            torch.cuda.synchronize()
+            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_a)
+            record(f"{args.config}-N{N}-awq", m2, u2,
+                   per_expert_bytes=(2 * H + cfg.moe_intermediate_size) * 2)
+            del lays_a
 
     # ------------------------------------------------------------------ measured copy peak
     # device-to-device copy of 2 GiB (read + write bytes), the practical HBM ceiling next to

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 3
+#define QMOE_ABI_VERSION 4
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -101,6 +101,10 @@ typedef struct {
   int32_t down_format;   /* QMOE_FMT_* of the routed down projection (gate_up: expert_format);
                             both quantized or both bf16 (Kimi: gate/up int3, down int4,
                             src/quanta/modeling/quantized.py:4-7) */
+  int32_t awq;           /* 1: the quantized experts carry activation-aware scales (weights'
+                            awq_gu / awq_dn, DeepSeek-V4, src/quanta/dsv4/moe.py:112-137): the
+                            activation is divided by the expert's per-input-channel scale before
+                            each projection; small regime only */
 } qmoe_config_t;
 
 /* Prepared (resident) weights of one block; every array is device memory. */
@@ -114,6 +118,9 @@ typedef struct {
   const uint16_t* dn_sb;
   const uint16_t* sh_gu;          /* shared gate|up [2*Is, H] tiled bf16 */
   const uint16_t* sh_dn;          /* shared down [H, Is] tiled bf16 */
+  const uint16_t* awq_gu;         /* config awq: bf16 [E, 2, H] input-channel scales of the gate
+                                     (row 0) and up (row 1) projections, else NULL */
+  const uint16_t* awq_dn;         /* config awq: bf16 [E, I] scales of the down projection */
 } qmoe_weights_t;
 
 int qmoe_abi_version(void);

@@ -213,6 +213,35 @@ def swiglu(gu: np.ndarray, inter: int, act: str = "silu", alpha: float = 1.702,
     return round_bf16(glu(g, u, act, alpha, limit))
 
 
+def awq_divide(x: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """bf16(fp32(x / s)) for bf16-valued x and s: the fp32 division rounded once to bf16 by the
+    matmul's bf16 input (`src/quanta/dsv4/moe.py:112-137`). The float64 quotient of two bf16
+    values rounds to fp32 as the correctly rounded fp32 division does (an 8-bit by 8-bit quotient
+    is never an fp32 rounding midpoint), so round_bf16's fp32 step is that division."""
+    return round_bf16(x / s)
+
+
+def awq_expert_rows(xrows: np.ndarray, exp: np.ndarray, p: dict, inter: int, hdim: int, *,
+                    act: str = "silu", alpha: float = 1.702, limit: float = 0.0,
+                    round_weights: bool = False, group_size: int = 64, bits: int = 4):
+    """DeepSeek-V4's packed routed SwiGLU with activation-aware scales
+    (`src/quanta/dsv4/moe.py:112-137`): g = qmm(bf16(x / s_w1[e])), u = qmm(bf16(x / s_w3[e])),
+    both bf16; h = bf16(glu(g, u) / s_w2[e]) with the gated activation unrounded. The fused
+    gate_up stack holds w1 in rows [0, I) and w3 in rows [I, 2I). Returns (gu [M, 2I], h)."""
+    exp = np.asarray(exp).reshape(-1)
+    s_gu, s_dn = p["gu_awq"], p["dn_awq"]
+    outs = []
+    for half in (0, 1):
+        rows = slice(half * inter, (half + 1) * inter)
+        xs = awq_divide(xrows, s_gu[exp, half])
+        outs.append(gather_qmm(xs, exp, p["gu_packed"][:, rows], p["gu_scale"][:, rows],
+                               p["gu_bias"][:, rows], hdim, round_weights=round_weights,
+                               group_size=group_size, bits=bits))
+    g, u = outs
+    h = awq_divide(glu(g, u, act, alpha, limit), s_dn[exp])
+    return np.concatenate([g, u], axis=1), h
+
+
 def combine(d: np.ndarray, w: np.ndarray) -> np.ndarray:
     """routed[t] = sum_s d[t*k+s] * w[t,s] (`src/quanta/qwen35/moe.py:191`), float64."""
     n, k = w.shape
@@ -251,7 +280,8 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
       gate [E,H]; gu_packed [E,2I,H/8], gu_scale/gu_bias [E,2I,H/64] (bf16 bits);
       dn_packed [E,H,I/8], dn_scale/dn_bias [E,H,I/64]; optional e_score_correction_bias [E];
       optional shared_gate_proj [Is,H], shared_up_proj [Is,H], shared_down_proj [H,Is],
-      shared_expert_gate [1,H].
+      shared_expert_gate [1,H]; optional gu_awq [E,2,H] and dn_awq [E,I] (bf16 values): the
+      activation-aware scales of DeepSeek-V4's packed experts (see awq_expert_rows).
     Returns (y bf16-valued float64 [N,H], dict of intermediates).
     """
     n, hdim = x.shape
@@ -261,9 +291,13 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
         scale=scale)
     exp = idx.reshape(-1)
     tok = np.repeat(np.arange(n), k)
-    gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim,
-                    round_weights=round_weights, group_size=group_size, bits=bits)
-    h = swiglu(gu, inter, act, alpha, limit)
+    if p.get("gu_awq") is not None:
+        gu, h = awq_expert_rows(x[tok], exp, p, inter, hdim, act=act, alpha=alpha, limit=limit,
+                                round_weights=round_weights, group_size=group_size, bits=bits)
+    else:
+        gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim,
+                        round_weights=round_weights, group_size=group_size, bits=bits)
+        h = swiglu(gu, inter, act, alpha, limit)
     d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
                    round_weights=round_weights, group_size=group_size,
                    bits=bits if down_bits is None else down_bits)

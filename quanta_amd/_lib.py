@@ -22,7 +22,7 @@ REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
@@ -51,6 +51,7 @@ class QmoeConfig(ctypes.Structure):
         ("act_alpha", ctypes.c_float),
         ("act_limit", ctypes.c_float),
         ("down_format", ctypes.c_int32),
+        ("awq", ctypes.c_int32),
     ]
 
 
@@ -65,6 +66,8 @@ class QmoeWeights(ctypes.Structure):
         ("dn_sb", ctypes.c_void_p),
         ("sh_gu", ctypes.c_void_p),
         ("sh_dn", ctypes.c_void_p),
+        ("awq_gu", ctypes.c_void_p),
+        ("awq_dn", ctypes.c_void_p),
     ]
 
 

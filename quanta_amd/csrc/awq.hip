@@ -1,0 +1,105 @@
+// Activation-aware (AWQ) expert scales around the routed grouped matmuls.
+//
+// Reference: DeepSeek-V4's packed experts hold the codes of W·diag(s) with a per-expert,
+// per-input-channel awq_scale s for each projection; the routed SwiGLU divides the gathered
+// activation by s before each quantized matmul: g = qmm(x / s_w1), u = qmm(x / s_w3),
+// h = silu(clamp(g)) * clamp(u), d = qmm(h / s_w2), the divisions in fp32 and the quotients
+// rounded to bf16 by the matmul's bf16 input (src/quanta/dsv4/moe.py:112-137; the scales come
+// from the artifact's {key}.awq_scale, src/quanta/dsv4/artifact.py:252-290, all ones for RTN
+// experts).
+//
+// The gate and up projections of one row then read different activations, so they cannot share
+// the decode kernel's activation fragments: the block runs gate_up with the bf16 epilogue, the
+// gate half's wavefronts reading the rows prescaled for the gate and the up half's those for the
+// up projection (QmmArgs::act_hi), and the gated activation with the down projection's division
+// as one pass between gate_up and down.
+#include "qmoe_internal.h"
+
+namespace qmoe {
+
+// Owner of sorted row m: the last expert e with offsets[e] <= m (empty experts share their
+// offset with the next one, which is the owner).
+__device__ __forceinline__ int expert_of_row(const int32_t* __restrict__ offsets, int E, int64_t m) {
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= m) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// One workgroup per sorted row; each thread 8 channels at a time.
+__global__ void __launch_bounds__(256) awq_prescale_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ offsets, int E, int k, int H, const uint16_t* __restrict__ s_gu,
+    uint16_t* __restrict__ xg, uint16_t* __restrict__ xu) {
+  const int64_t m = blockIdx.x;
+  const int e = expert_of_row(offsets, E, m);
+  const int64_t tok = sorted[m] / k;
+  const u32x4* xs = reinterpret_cast<const u32x4*>(x + tok * H);
+  const u32x4* sg = reinterpret_cast<const u32x4*>(s_gu + static_cast<int64_t>(e) * 2 * H);
+  const u32x4* su = sg + H / 8;
+  u32x4* og = reinterpret_cast<u32x4*>(xg + m * H);
+  u32x4* ou = reinterpret_cast<u32x4*>(xu + m * H);
+  for (int i = threadIdx.x; i < H / 8; i += 256) {
+    const u32x4 v = xs[i], a = sg[i], b = su[i];
+    u32x4 rg, ru;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16lo_to_f32(v[j]), hi = bf16hi_to_f32(v[j]);
+      // correctly rounded fp32 quotients (hipcc's default division), then one bf16 rounding
+      rg[j] = pack_bf16x2(lo / bf16lo_to_f32(a[j]), hi / bf16hi_to_f32(a[j]));
+      ru[j] = pack_bf16x2(lo / bf16lo_to_f32(b[j]), hi / bf16hi_to_f32(b[j]));
+    }
+    og[i] = rg;
+    ou[i] = ru;
+  }
+}
+
+__global__ void __launch_bounds__(256) awq_glu_kernel(
+    const uint16_t* __restrict__ gu, const int32_t* __restrict__ offsets, int E, int I,
+    const uint16_t* __restrict__ s_dn, int act, float alpha, float limit, uint16_t* __restrict__ h) {
+  const int64_t m = blockIdx.x;
+  const int e = expert_of_row(offsets, E, m);
+  const u32x4* g4 = reinterpret_cast<const u32x4*>(gu + m * 2 * I);
+  const u32x4* u4 = g4 + I / 8;
+  const u32x4* s4 = reinterpret_cast<const u32x4*>(s_dn + static_cast<int64_t>(e) * I);
+  u32x4* o4 = reinterpret_cast<u32x4*>(h + m * I);
+  for (int i = threadIdx.x; i < I / 8; i += 256) {
+    const u32x4 g = g4[i], u = u4[i], s = s4[i];
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = glu_f(bf16lo_to_f32(g[j]), bf16lo_to_f32(u[j]), act, alpha, limit);
+      const float hi = glu_f(bf16hi_to_f32(g[j]), bf16hi_to_f32(u[j]), act, alpha, limit);
+      o[j] = pack_bf16x2(lo / bf16lo_to_f32(s[j]), hi / bf16hi_to_f32(s[j]));
+    }
+    o4[i] = o;
+  }
+}
+
+int launch_awq_prescale(const uint16_t* x, const int32_t* sorted, const int32_t* offsets, int E,
+                        int k, int64_t mc, int H, const uint16_t* s_gu, uint16_t* xg, uint16_t* xu,
+                        hipStream_t stream) {
+  if (mc <= 0) return 0;
+  if (H <= 0 || H % 8) return fail("awq prescale: H % 8 == 0 required");
+  if (E <= 0 || k <= 0) return fail("awq prescale: E, k > 0 required");
+  if (mc > 0x7fffffff) return fail("awq prescale: too many rows");
+  awq_prescale_kernel<<<static_cast<unsigned>(mc), 256, 0, stream>>>(x, sorted, offsets, E, k, H,
+                                                                      s_gu, xg, xu);
+  return check_launch("awq prescale");
+}
+
+int launch_awq_glu(const uint16_t* gu, const int32_t* offsets, int E, int64_t mc, int I,
+                   const uint16_t* s_dn, int act, float alpha, float limit, uint16_t* h,
+                   hipStream_t stream) {
+  if (mc <= 0) return 0;
+  if (I <= 0 || I % 8) return fail("awq glu: I % 8 == 0 required");
+  if (mc > 0x7fffffff) return fail("awq glu: too many rows");
+  awq_glu_kernel<<<static_cast<unsigned>(mc), 256, 0, stream>>>(gu, offsets, E, I, s_dn, act, alpha,
+                                                                 limit, h);
+  return check_launch("awq glu");
+}
+
+}  // namespace qmoe

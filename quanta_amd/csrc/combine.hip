@@ -304,7 +304,7 @@ static int aux_stream(hipStream_t caller, AuxStream** out) {
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
   size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, tile_map_big, sorted, inv, h,
-      d, sh_h, sh_out, x16, x_sinv, h16, h_sinv, total;
+      d, sh_h, sh_out, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, total;
   int64_t max_tiles, max_tiles_big;
 };
 
@@ -342,6 +342,9 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.x_sinv = take(static_cast<size_t>(N) * 4);
   L.h16 = take(static_cast<size_t>(mc) * c.inter * 2);
   L.h_sinv = take(static_cast<size_t>(mc) * 4);
+  // AWQ: the gate and up projections' prescaled rows [2][mc][H] and their outputs [mc][2I]
+  L.awq_x = take(c.awq ? static_cast<size_t>(2) * mc * c.hidden * 2 : 0);
+  L.awq_gu = take(c.awq ? static_cast<size_t>(mc) * 2 * c.inter * 2 : 0);
   L.total = o;
   return L;
 }
@@ -382,6 +385,11 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: gate_up and down must both be quantized or both bf16");
   if (narrow_codes(c) && c.regime == QMOE_REGIME_LARGE)
     return fail("config: int3/int6 experts run in the small regime only");
+  if (c.awq != 0 && c.awq != 1) return fail("config: awq must be 0 or 1");
+  if (c.awq && c.expert_format == QMOE_FMT_BF16)
+    return fail("config: awq scales need quantized experts");
+  if (c.awq && c.regime == QMOE_REGIME_LARGE)
+    return fail("config: experts with awq scales run in the small regime only");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {
     if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 256)
       return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 256");
@@ -495,7 +503,7 @@ static int dense_regime(const qmoe_config_t& c, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  if (narrow_codes(c)) return QMOE_REGIME_SMALL;   // no large int3/int6 kernel
+  if (narrow_codes(c) || c.awq) return QMOE_REGIME_SMALL;   // no large int3/int6/AWQ kernel
   return dense_regime(c, N);
 }
 
@@ -516,6 +524,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   if (c.shared_inter > 0 && (!wts->sh_gu || !wts->sh_dn)) return fail("qmoe_forward: missing shared expert");
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
+  if (c.awq && (!wts->awq_gu || !wts->awq_dn)) return fail("qmoe_forward: awq needs awq_gu and awq_dn");
 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* base = static_cast<char*>(ws);
@@ -570,7 +579,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   const bool fuse_dn = fuse && bf16_chunks(c.shared_inter) <= 8;
   // one or two tokens: slot-major routing written by the top-k, no permute launch (each slot
   // its own m-tile; an expert two tokens share is read twice, cheaper than the launch)
-  const bool slot_major = !hybrid && N <= kSlotMajorMaxTokens;
+  // (AWQ prescaling finds each row's expert from the permute's segment offsets)
+  const bool slot_major = !hybrid && N <= kSlotMajorMaxTokens && !c.awq;
   std::unique_lock<std::mutex> aux_lock;
   AuxStream* aux = nullptr;
   hipStream_t sstream = stream;
@@ -672,7 +682,27 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     return launch_qmm(a, fmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
   };
   // 5. routed gate_up + SwiGLU -> h (sorted order)
-  {
+  if (c.awq) {
+    // AWQ: gate and up on their own prescaled rows (one launch over all 2I rows of each expert,
+    // the up half's tiles reading the up rows) into awq_gu, then h = bf16(glu / s_dn)
+    uint16_t* xg = reinterpret_cast<uint16_t*>(base + L.awq_x);
+    uint16_t* xu = xg + mc * c.hidden;
+    uint16_t* gu = reinterpret_cast<uint16_t*>(base + L.awq_gu);
+    rc = launch_awq_prescale(x, sorted, offsets, c.n_experts, c.top_k, mc, c.hidden, wts->awq_gu,
+                             xg, xu, stream);
+    if (rc) return rc;
+    QmmArgs a{};
+    a.act = xg; a.act_hi = xu; a.split_tile = c.inter / 16;
+    a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
+    a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+    a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
+    a.out = gu; a.ld_out = 2 * c.inter;
+    rc = routed(a, gfmt, EPI_BF16, nullptr, nullptr);
+    if (rc) return rc;
+    rc = launch_awq_glu(gu, offsets, c.n_experts, mc, c.inter, wts->awq_dn, c.act, c.act_alpha,
+                        c.act_limit, h, stream);
+    if (rc) return rc;
+  } else {
     QmmArgs a{};
     a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;

@@ -85,16 +85,7 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
     // and src/quanta/minimax/model_m3.py:112-128)
     const float g = bf16_to_f32(f32_to_bf16(v));
     const float u = bf16_to_f32(f32_to_bf16(v_up));
-    float h;
-    if (a.glu == QMOE_ACT_SILU) {
-      h = silu_f(g) * u;
-    } else {
-      const float gc = fminf(g, a.glu_limit);
-      const float uc = fminf(fmaxf(u, -a.glu_limit), a.glu_limit);
-      h = (a.glu == QMOE_ACT_SILU_CLAMP) ? silu_f(gc) * uc
-                                         : (uc + 1.0f) * (gc / (1.0f + __expf(-a.glu_alpha * gc)));
-    }
-    static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(h);
+    static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(glu_f(g, u, a.glu, a.glu_alpha, a.glu_limit));
   } else if (EPI == EPI_BF16) {
     static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(v);
   } else {
@@ -170,6 +161,8 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
   // Rows past the segment and rows whose slot is invalid read activation row 0, so every load
   // is unconditional (a load under a branch makes the compiler wait for all loads in flight);
   // the former are never stored, the latter are stored as zeros.
+  // (act_hi: the wavefront's JPW tiles lie on one side of split_tile, a multiple of 4)
+  const uint16_t* act = (fmt_quant(FMT) && a.act_hi && job * JPW >= a.split_tile) ? a.act_hi : a.act;
   const uint16_t* xrows[MT];
   uint32_t rows_okm[MT];
 #pragma unroll
@@ -177,7 +170,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
     int64_t arow = -1;
     if (mrow < mtc[u]) arow = act_row(a, mt0[u] + mrow);
     const bool row_ok = arow >= 0;
-    xrows[u] = a.act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
+    xrows[u] = act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
     rows_okm[u] = static_cast<uint32_t>(__ballot(row_ok)) & 0xFFFFu;   // lanes 0-15
   }
   const uint16_t* xrow = xrows[0];
@@ -1206,6 +1199,13 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (a.K <= 0 || a.n_rows <= 0) return fail("qmm: empty problem");
   if (mtile_bound <= 0) return 0;
   if (mtile_bound > 65535) return fail("qmm: too many m-tiles for one launch");
+  if (a.act_hi) {
+    if (regime != QMOE_REGIME_SMALL || !fmt_quant(fmt) || epi == EPI_SWIGLU || a.slot_of)
+      return fail("qmm: a second activation needs quantized weights, the small regime, a "
+                  "non-SwiGLU epilogue and rows by sorted position");
+    if (a.split_tile <= 0 || a.split_tile % 4 || a.split_tile >= a.n_rows / 16)
+      return fail("qmm: split_tile must be a positive multiple of 4 inside the weight tiles");
+  }
   if (regime == QMOE_REGIME_SMALL) {
     if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int3/int4/int6 need K % 128 == 0");
     if (fmt == FMT_BF16 && a.K % 32) return fail("qmm: bf16 needs K % 32 == 0");

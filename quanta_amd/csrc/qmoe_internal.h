@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
+#include "../../include/quanta_moe.h"
 
 namespace qmoe {
 
@@ -184,6 +185,15 @@ __device__ __forceinline__ u32x4 dequant_word_f16_ao(uint32_t w, f16x2_t s2, f16
 }
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+// The gated activation on (bf16-valued) gate/up values, fp32 (QMOE_ACT_*: silu(g)*u; its clamped
+// form, src/quanta/dsv4/moe.py:74-77; SwiGLU-OAI, src/quanta/minimax/model_m3.py:112-128).
+__device__ __forceinline__ float glu_f(float g, float u, int act, float alpha, float limit) {
+  if (act == QMOE_ACT_SILU) return silu_f(g) * u;
+  const float gc = fminf(g, limit);
+  const float uc = fminf(fmaxf(u, -limit), limit);
+  return (act == QMOE_ACT_SILU_CLAMP) ? silu_f(gc) * uc
+                                      : (uc + 1.0f) * (gc / (1.0f + __expf(-alpha * gc)));
+}
 
 // Upper bound on the number of m-tiles a permuted (token, slot) list can produce.
 inline int64_t mtile_upper_bound(int64_t mc, int64_t n_experts, int64_t m_tile) {
@@ -231,6 +241,10 @@ struct QmmArgs {
   int glu;                    // SwiGLU epilogue: gated activation (QMOE_ACT_*)
   float glu_alpha;            // SWIGLU_OAI alpha
   float glu_limit;            // clamp of SILU_CLAMP / SWIGLU_OAI
+  const uint16_t* act_hi;     // small quantized regime, nullable: the activation rows of the
+                              // weight tiles from split_tile on (AWQ: the up half of gate_up
+                              // reads rows prescaled for the up projection)
+  int split_tile;             // first 16-row tile that reads act_hi (a multiple of 4)
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3 };
@@ -267,6 +281,16 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
                    const uint16_t* shared_out, const float* shared_gate, uint16_t* y,
                    hipStream_t stream, const uint16_t* resid = nullptr);
 // RMSNorm rows: out = bf16(w * (x * rsqrt(mean(x^2) + eps))) in fp32 (norm.hip).
+// Activation-aware (AWQ) expert scales (src/quanta/dsv4/moe.py:112-137): per sorted row m of
+// expert e (offsets), xg[m] = bf16(x[tok] / s_gu[e][0]) and xu[m] = bf16(x[tok] / s_gu[e][1]),
+// tok = sorted[m] / k; s_gu bf16 [E][2][H].
+int launch_awq_prescale(const uint16_t* x, const int32_t* sorted, const int32_t* offsets, int E,
+                        int k, int64_t mc, int H, const uint16_t* s_gu, uint16_t* xg, uint16_t* xu,
+                        hipStream_t stream);
+// h[m] = bf16(glu(g, u) / s_dn[e]) over gu [mc][2I] (gate | up, bf16) with s_dn bf16 [E][I].
+int launch_awq_glu(const uint16_t* gu, const int32_t* offsets, int E, int64_t mc, int I,
+                   const uint16_t* s_dn, int act, float alpha, float limit, uint16_t* h,
+                   hipStream_t stream);
 int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float eps, uint16_t* out,
                    hipStream_t stream);
 

@@ -73,9 +73,11 @@ class TiledExperts(dict):
 
     Keys: "format" ("int4_g64" | "int6_g64" | "int3_g64" | "bf16"), "codes" (tiled int4 / int6 /
     int3 words or tiled bf16), "sb" (tiled
-    scale+bias, int4 only), "shape" (E, rows, K), "group_size", "bits". Produced from the
-    reference's packed triplet {packed, scale, bias, group_size, bits}
-    (src/quanta/qwen35/artifact.py:199-203) or from a bf16 [E, rows, K] stack.
+    scale+bias, int4 only), "shape" (E, rows, K), "group_size", "bits", and "awq_scale" (bf16
+    per-input-channel activation scales, or None). Produced from the reference's packed triplet
+    {packed, scale, bias, group_size, bits} (src/quanta/qwen35/artifact.py:199-203; DeepSeek-V4's
+    packed experts add awq_scale, src/quanta/dsv4/artifact.py:252-290) or from a bf16
+    [E, rows, K] stack.
     """
 
     @property
@@ -103,8 +105,11 @@ def tile_experts_packed(d: dict) -> TiledExperts:
     E, rows, W = packed.shape
     tile = {4: ops.tile_int4, 6: ops.tile_int6, 3: ops.tile_int3}[bits]
     codes, sb = tile(packed.contiguous(), scale.contiguous(), bias.contiguous(), group_size=gs)
+    awq = d.get("awq_scale")
+    if awq is not None:
+        awq = awq.to(device=packed.device, dtype=torch.bfloat16).contiguous()
     return TiledExperts(format=f"int{bits}_g64", codes=codes, sb=sb, shape=(E, rows, W * 32 // bits),
-                        group_size=gs, bits=bits)
+                        group_size=gs, bits=bits, awq_scale=awq)
 
 
 def tile_experts_bf16(stack: torch.Tensor) -> TiledExperts:
@@ -301,6 +306,16 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     c.shared_gated = int(sgate is not None)
     c.regime = regime
     c.act, c.act_alpha, c.act_limit = gated_activation(cfg)
+    # DeepSeek-V4's activation-aware scales (src/quanta/dsv4/moe.py:112-137): gate and up
+    # scales of the fused gate_up stack as [E, 2, H] (w1 row 0, w3 row 1), down [E, I]
+    awq_gu, awq_dn = gu.get("awq_scale"), dn.get("awq_scale")
+    if (awq_gu is None) != (awq_dn is None):
+        raise ValueError("awq_scale must be given on both experts_gate_up and experts_down")
+    if awq_gu is not None:
+        if tuple(awq_gu.shape) != (E, 2, H) or tuple(awq_dn.shape) != (E, I):
+            raise ValueError(f"awq_scale must be gate_up [{E}, 2, {H}] and down [{E}, {I}] "
+                             f"(got {tuple(awq_gu.shape)} and {tuple(awq_dn.shape)})")
+        c.awq = 1
 
     w = L.QmoeWeights()
     w.router_w = rw.data_ptr()
@@ -312,7 +327,9 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     w.dn_sb = dn["sb"].data_ptr() if dn["sb"] is not None else None
     w.sh_gu = sh_gu.data_ptr() if sh_gu is not None else None
     w.sh_dn = sh_dn.data_ptr() if sh_dn is not None else None
-    keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn)
+    w.awq_gu = awq_gu.data_ptr() if awq_gu is not None else None
+    w.awq_dn = awq_dn.data_ptr() if awq_dn is not None else None
+    keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn, awq_gu, awq_dn)
     return Prepared(c, w, keep, rw if rkind == "bf16" else None, rw if rkind == "f32" else None,
                     sg32, gu, dn, sh_gu, sh_dn, bias)
 

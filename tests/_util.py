@@ -70,6 +70,9 @@ def oracle_params_from_torch(p: dict) -> dict:
             out[k] = f64(p[k])
     if p.get("e_score_correction_bias") is not None:
         out["e_score_correction_bias"] = f64(p["e_score_correction_bias"])
+    for pre, key in (("gu", "experts_gate_up"), ("dn", "experts_down")):
+        if p[key].get("awq_scale") is not None:
+            out[f"{pre}_awq"] = f64(p[key]["awq_scale"])
     return out
 
 

@@ -13,7 +13,7 @@ from quanta_amd import _lib as L
 
 def test_library_loads_and_abi_version():
     lib = L.load()
-    assert lib.qmoe_abi_version() == L.ABI_VERSION == 3
+    assert lib.qmoe_abi_version() == L.ABI_VERSION == 4
 
 
 def test_every_header_symbol_is_exported_and_bound():
@@ -133,3 +133,25 @@ def test_forward_rejects_mixed_bf16_and_unknown_down_format():
             continue
         rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
         assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()
+
+
+def test_forward_rejects_bad_awq_config():
+    lib = L.load()
+    base = dict(hidden=512, n_experts=16, top_k=2, inter=128, shared_inter=0, scoring=0, norm_topk=1,
+                n_group=1, topk_group=1, routed_scale=1.0, router_format=1, router_rows=0,
+                shared_gated=0)
+    dummy = ctypes.c_void_p(16)
+    w = L.QmoeWeights()
+    for kw, frag in ((dict(expert_format=L.FMT_BF16, down_format=L.FMT_BF16, awq=1, regime=0),
+                      "awq scales need quantized experts"),
+                     (dict(expert_format=0, down_format=0, awq=1, regime=L.REGIME_LARGE),
+                      "awq scales run in the small regime only"),
+                     (dict(expert_format=0, down_format=0, awq=2, regime=0), "awq must be 0 or 1")):
+        cfg = L.QmoeConfig(**kw, **base)
+        rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
+        assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()
+    # awq adds the prescaled rows [2][mc][H] and the gate|up outputs [mc][2I] to the workspace
+    cfg0 = L.QmoeConfig(expert_format=0, down_format=0, awq=0, regime=0, **base)
+    cfg1 = L.QmoeConfig(expert_format=0, down_format=0, awq=1, regime=0, **base)
+    extra = lib.qmoe_forward_workspace(ctypes.byref(cfg1), 5) - lib.qmoe_forward_workspace(ctypes.byref(cfg0), 5)
+    assert extra >= 2 * 10 * 512 * 2 + 10 * 256 * 2

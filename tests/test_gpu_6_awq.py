@@ -1,0 +1,100 @@
+"""GPU tier: DeepSeek-V4's activation-aware (AWQ) expert scales (src/quanta/dsv4/moe.py:112-137).
+
+The block divides each routed row's activation by its expert's per-input-channel scale before
+the gate, the up and the down projection (qmoe_config_t.awq; kernels in awq.hip, the gate and up
+halves of the fused gate_up stack as two launches).
+
+Bars: unit scales give the plain path's output bit for bit (same per-output arithmetic); random
+scales within the BASELINE gates of the oracle (max-abs 2e-2 scaled, relative L2 5e-3) at every
+batch regime the AWQ path uses; batch invariance bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from quanta_amd import _lib as L
+from quanta_amd.moe import MoEConfig, qwen35_moe
+from tests._util import assert_close, f64, oracle_params_from_torch
+from tests.test_gpu_5_formats import _inputs, _layer, _layer_widths
+
+pytestmark = pytest.mark.gpu
+
+LIMIT = 2.0   # DeepSeek-V4's clamped SwiGLU, small enough to bind on part of the values
+
+
+def _cfg(**kw):
+    return MoEConfig(512, 8, 2, 256, 256, scoring_func="sigmoid", norm_topk_prob=True,
+                     routed_scaling_factor=1.5, hidden_act="silu", swiglu_limit=LIMIT, **kw)
+
+
+def _with_awq(p, dev, seed, E=8, H=512, I=256, unit=False):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    if unit:
+        s_gu, s_dn = torch.ones(E, 2, H), torch.ones(E, I)
+    else:
+        s_gu = 2.0 ** (torch.rand(E, 2, H, generator=g) * 2 - 1)
+        s_dn = 2.0 ** (torch.rand(E, I, generator=g) * 2 - 1)
+    q = dict(p)
+    q["experts_gate_up"] = dict(p["experts_gate_up"], awq_scale=s_gu.to(torch.bfloat16).to(dev))
+    q["experts_down"] = dict(p["experts_down"], awq_scale=s_dn.to(torch.bfloat16).to(dev))
+    return q
+
+
+@pytest.mark.parametrize("N", [1, 8, 40, 300])
+def test_awq_unit_scales_equal_plain_path(gpu, N):
+    """All-ones scales: prescaling is exact and the gated activation divides by one, so the two
+    half-stack launches plus the AWQ activation pass reproduce the fused SwiGLU launch bit for bit
+    (the K chunks and their order depend on the shape only)."""
+    cfg = _cfg()
+    p = _layer(gpu, 64, seed=3 * N, gated=False)
+    x = _inputs(gpu, N, 512, N)
+    y_plain = qwen35_moe(x[None], p, cfg, regime=L.REGIME_SMALL)[0]
+    y_awq = qwen35_moe(x[None], _with_awq(p, gpu, N, unit=True), cfg)[0]
+    assert torch.equal(y_awq, y_plain)
+
+
+@pytest.mark.parametrize("gs,gu_bits,dn_bits", [(64, 4, 4), (128, 4, 4), (128, 3, 4)])
+@pytest.mark.parametrize("N", [1, 8, 40, 300])
+def test_awq_block_vs_oracle(gpu, gs, gu_bits, dn_bits, N):
+    cfg = _cfg()
+    base = (_layer(gpu, gs, seed=5 * N + gs, gated=False) if (gu_bits, dn_bits) == (4, 4) else
+            _layer_widths(gpu, gs, 5 * N + gs, gu_bits, dn_bits))
+    base.pop("shared_expert_gate", None)   # DeepSeek-V4's shared expert is ungated
+    p = _with_awq(base, gpu, seed=7 * N + gs)
+    x = _inputs(gpu, N, 512, N)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=2, inter=256, scoring="sigmoid",
+                           norm_topk=True, scale=1.5, act="silu", limit=LIMIT, group_size=gs,
+                           bits=gu_bits, down_bits=dn_bits)
+    assert_close(f64(y), it["y_exact"], f"awq int{gu_bits}/int{dn_bits} g{gs} N={N}")
+    if N >= 40:
+        g = it["gu"][:, :256]
+        assert np.any(g > LIMIT), "the clamp must bind somewhere for the test to mean anything"
+
+
+def test_awq_batch_invariance(gpu):
+    cfg = _cfg()
+    p = _with_awq(_layer(gpu, 64, seed=11, gated=False), gpu, seed=12)
+    x = _inputs(gpu, 40, 512, 13)
+    full = qwen35_moe(x[None], p, cfg)[0]
+    for t in (0, 17, 39):
+        assert torch.equal(qwen35_moe(x[t:t + 1][None], p, cfg)[0, 0], full[t]), f"token {t}"
+
+
+def test_awq_argument_errors(gpu):
+    cfg = _cfg()
+    p = _layer(gpu, 64, seed=1, gated=False)
+    q = _with_awq(p, gpu, seed=2)
+    x = _inputs(gpu, 4, 512, 1)
+    one_sided = dict(q, experts_down=p["experts_down"])
+    with pytest.raises(ValueError, match="both experts_gate_up and experts_down"):
+        qwen35_moe(x[None], one_sided, cfg)
+    bad = dict(q, experts_down=dict(q["experts_down"], awq_scale=q["experts_down"]["awq_scale"][:, :128]))
+    with pytest.raises(ValueError, match="awq_scale must be"):
+        qwen35_moe(x[None], bad, cfg)
+    with pytest.raises(ValueError, match="small regime only"):
+        qwen35_moe(x[None], q, cfg, regime=L.REGIME_LARGE)

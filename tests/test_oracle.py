@@ -513,3 +513,62 @@ def test_dequant_int3_explicit_loop():
         for r in range(rows):
             for k in range(K):
                 assert got[r, k] == s[r, k // gs] * codes[r, k] + b[r, k // gs]
+
+
+# ----------------------------------------------------------------------------------- AWQ scales
+
+
+def test_awq_divide_is_fp32_division_rounded_to_bf16():
+    """awq_divide (float64 quotient -> fp32 -> bf16) against numpy's IEEE float32 division then
+    the bf16 rounding, over every finite bf16 numerator and a spread of positive bf16 scales."""
+    num = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    num = num[np.isfinite(oq.bf16_bits_to_f32(num))]
+    rng = np.random.default_rng(0)
+    den = oq.f32_to_bf16_bits((2.0 ** rng.uniform(-6, 6, 96)).astype(np.float32))
+    x = oq.bf16_bits_to_f32(num)[:, None].astype(np.float32)
+    s = oq.bf16_bits_to_f32(den)[None, :].astype(np.float32)
+    with np.errstate(over="ignore", under="ignore"):
+        want = oq.bf16_bits_to_f32(oq.f32_to_bf16_bits(x / s))
+        got = om.awq_divide(x.astype(np.float64), s.astype(np.float64))
+    assert np.array_equal(got.astype(np.float32), want, equal_nan=True)
+
+
+def _awq_case(seed, E=4, H=128, I=128):
+    rng = np.random.default_rng(seed)
+    gu_w = rng.standard_normal((E, 2 * I, H)) * 0.05
+    dn_w = rng.standard_normal((E, H, I)) * 0.05
+    p = {}
+    for pre, w in (("gu", gu_w), ("dn", dn_w)):
+        packed, sb, bb, _ = oq.quantize_rtn(w, 4, 64)
+        p[f"{pre}_packed"], p[f"{pre}_scale"], p[f"{pre}_bias"] = packed, sb, bb
+    x = oq.round_bf16(rng.standard_normal((6, H)))
+    exp = rng.integers(0, E, 6)
+    return p, x, exp, rng
+
+
+def test_awq_rows_reduce_to_the_plain_path_with_unit_scales():
+    p, x, exp, _ = _awq_case(1)
+    E, I, H = 4, 128, 128
+    q = dict(p, gu_awq=np.ones((E, 2, H)), dn_awq=np.ones((E, I)))
+    gu, h = om.awq_expert_rows(x, exp, q, I, H, act="silu", limit=7.0)
+    gu_plain = om.gather_qmm(x, exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], H)
+    assert np.array_equal(gu, gu_plain)
+    assert np.array_equal(h, om.swiglu(gu_plain, I, "silu", limit=7.0))
+
+
+def test_awq_rows_power_of_two_scales():
+    """Scales 2^j per (expert, projection) divide exactly and commute with bf16 rounding, so
+    g, u and h are the unit-scale values times 2^-j: pins which half of the gate_up stack takes
+    which scale row and that every row takes its own expert's scales."""
+    p, x, exp, rng = _awq_case(2)
+    E, I, H = 4, 128, 128
+    jg = rng.integers(-3, 4, (E, 2))
+    jd = rng.integers(-3, 4, E)
+    s_gu = np.broadcast_to((2.0 ** jg)[:, :, None], (E, 2, H)).copy()
+    s_dn = np.broadcast_to((2.0 ** jd)[:, None], (E, I)).copy()
+    gu, h = om.awq_expert_rows(x, exp, dict(p, gu_awq=s_gu, dn_awq=s_dn), I, H)
+    gu1, _ = om.awq_expert_rows(x, exp, dict(p, gu_awq=np.ones((E, 2, H)), dn_awq=np.ones((E, I))), I, H)
+    assert np.array_equal(gu[:, :I], gu1[:, :I] * 2.0 ** -jg[exp, 0][:, None])
+    assert np.array_equal(gu[:, I:], gu1[:, I:] * 2.0 ** -jg[exp, 1][:, None])
+    want_h = oq.round_bf16(om.glu(gu[:, :I], gu[:, I:])) * 2.0 ** -jd[exp][:, None]
+    assert np.array_equal(h, want_h)
