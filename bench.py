@@ -16,7 +16,8 @@ on the launch stream), a sweep over the other decode batches and the 4096-token 
 widened rows at the headline batch (`--extra`: the block with the decoder layer's RMSNorm and
 residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, and with
 Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies; and with
-DeepSeek-V4's activation-aware expert scales on the int4 experts), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
+DeepSeek-V4's activation-aware expert scales on the int4 experts; with Kimi's widths drawn per
+(expert, projection)), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
 cores, bounded sample).
 
 `roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
@@ -58,9 +59,9 @@ def parse():
     ap.add_argument("--zipf", action="store_true",
                     help="headline workload with c4's Zipf(1.1) routing (profiling the prefill)")
     ap.add_argument("--kernel-reps", type=int, default=64)
-    ap.add_argument("--extra", default="residual,int6,int3,awq",
+    ap.add_argument("--extra", default="residual,int6,int3,mixed,awq",
                     help="widened rows timed at the headline batch ('' = none): residual, int6, "
-                         "int3, awq")
+                         "int3, mixed, awq")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
@@ -199,7 +200,7 @@ def main():
             if residual:
                 ops.forward_residual(pr.cfg, pr.weights, xs[i % pool], norm_w, 1e-6, out=out, ws=ws)
             else:
-                ops.forward(pr.cfg, pr.weights, xs[i % pool], out=out, ws=ws)
+                ops.forward(pr.cfg, pr.weights, xs[i % pool], out=out, ws=ws, mixed=pr.mixed)
 
         for i in range(warmup):
             step(i)
@@ -326,6 +327,24 @@ def main():
             m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_f)
             record(f"{args.config}-N{N}-{tag}", m2, u2, **fmt)
             del lays_f
+        if "mixed" in args.extra:
+            # Kimi's per-(expert, projection) widths, int3 or int4 at group 128 drawn per expert
+            # and projection: one launch per (projection, width); two copies
+            from quanta_amd.moe import tile_experts_mixed
+            lays_m, be = [], 0.0
+            for li in range(2):
+                src = synth.make_mixed_experts(args.config, device=dev, seed=li)
+                be = synth.mixed_expert_bytes(src, cfg)
+                pm = {kk: v for kk, v in layers[li].items() if not kk.startswith("experts_")}
+                pm["experts_mixed"] = tile_experts_mixed(src["stacks"], src["pbits"], src["pslot"])
+                del src
+                lays_m.append(pm)
+            torch.cuda.synchronize()
+            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_m)
+            # bytes: the int4-g64 figure with the mixed layer's mean bytes per expert in its place
+            be4 = 3 * cfg.moe_intermediate_size * H * 36 / 64
+            record(f"{args.config}-N{N}-mixed34", m2, u2, per_expert_bytes=be - be4)
+            del lays_m
         if "awq" in args.extra:
             # DeepSeek-V4's activation-aware scales on the int4 experts: each routed row's
             # activation divided per input channel before gate, up and down (bf16 scales [E,2,H]

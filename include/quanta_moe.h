@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 4
+#define QMOE_ABI_VERSION 5
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -105,6 +105,8 @@ typedef struct {
                             awq_gu / awq_dn, DeepSeek-V4, src/quanta/dsv4/moe.py:112-137): the
                             activation is divided by the expert's per-input-channel scale before
                             each projection; small regime only */
+  int32_t mixed;         /* 1: routed experts of mixed widths per (expert, projection), passed to
+                            qmoe_forward_mixed (weights' gu/dn fields unused); small regime only */
 } qmoe_config_t;
 
 /* Prepared (resident) weights of one block; every array is device memory. */
@@ -133,6 +135,36 @@ const char* qmoe_last_error(void);
 size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N);
 int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x, int64_t N,
                  uint16_t* y, void* ws, size_t ws_bytes, void* stream);
+
+/* Routed experts whose widths vary per (expert, projection) (Kimi's QuantizedSparseMoE,
+ * src/quanta/modeling/quantized.py:40-84: one packed stack per projection and width, each expert
+ * carrying per projection its width and its slot in that width's stack). Each stack is tiled as
+ * the uniform stacks (qmoe_tile_int3/int4/int6; gate and up [E_w, I, H], down [E_w, H, I]) and
+ * names, per expert, the slot it holds in the stack or -1. Every expert must be in exactly one
+ * stack per projection (the library cannot check the device maps). The gate and up projections
+ * are separate stacks, as in the reference. */
+#define QMOE_PROJ_GATE 0
+#define QMOE_PROJ_UP 1
+#define QMOE_PROJ_DOWN 2
+#define QMOE_MAX_STACKS 12
+typedef struct {
+  int32_t proj;                /* QMOE_PROJ_* */
+  int32_t format;              /* QMOE_FMT_INT3_G64 / INT4_G64 / INT6_G64 */
+  const uint32_t* codes;       /* tiled codes */
+  const uint16_t* sb;          /* tiled scale/bias */
+  const int32_t* expert_slot;  /* [E] device: the expert's slot in this stack, or -1 */
+} qmoe_stack_t;
+typedef struct {
+  int32_t n_stacks;            /* 3 .. QMOE_MAX_STACKS, every projection at least once */
+  qmoe_stack_t stacks[QMOE_MAX_STACKS];
+} qmoe_mixed_t;
+
+/* qmoe_forward with the routed experts of mixed (cfg->mixed = 1); workspace as
+ * qmoe_forward_workspace. No counterpart beyond QuantizedSparseMoE.__call__ (quantized.py:68-84):
+ * gate and up by width into one [N*k, 2I] buffer, h = bf16(silu(g) * u), down by width. */
+int qmoe_forward_mixed(const qmoe_config_t* cfg, const qmoe_weights_t* w, const qmoe_mixed_t* mixed,
+                       const uint16_t* x, int64_t N, uint16_t* y, void* ws, size_t ws_bytes,
+                       void* stream);
 
 /* The block with the decoder layer's steps either side of it, as the layer calls it:
  *   y = bf16(x + bf16(block(rmsnorm(x))))

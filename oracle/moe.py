@@ -242,6 +242,28 @@ def awq_expert_rows(xrows: np.ndarray, exp: np.ndarray, p: dict, inter: int, hdi
     return np.concatenate([g, u], axis=1), h
 
 
+def mixed_proj(xrows: np.ndarray, exp: np.ndarray, m: dict, proj: str, in_features: int) -> np.ndarray:
+    """One projection over routed rows whose experts have per-(expert, projection) widths
+    (`src/quanta/modeling/quantized.py:53-66`): row r uses expert e = exp[r]'s width
+    b = pbits[proj][e] and its slot pslot[proj][e] in the width-b stack; y = bf16(x . W^T).
+    `m`: {"stacks": {proj: {bits: (packed, scale, bias)}}, "pbits": {proj: [E]},
+    "pslot": {proj: [E]}, "group_size": g}."""
+    exp = np.asarray(exp).reshape(-1)
+    pb = np.asarray(m["pbits"][proj])[exp]
+    ps = np.asarray(m["pslot"][proj])[exp]
+    out = None
+    for bits, (packed, scale, bias) in sorted(m["stacks"][proj].items()):
+        sel = pb == bits
+        if not sel.any():
+            continue
+        o = gather_qmm(xrows[sel], ps[sel], packed, scale, bias, in_features,
+                       group_size=m["group_size"], bits=bits)
+        if out is None:
+            out = np.zeros((exp.size, o.shape[1]))
+        out[sel] = o
+    return out
+
+
 def combine(d: np.ndarray, w: np.ndarray) -> np.ndarray:
     """routed[t] = sum_s d[t*k+s] * w[t,s] (`src/quanta/qwen35/moe.py:191`), float64."""
     n, k = w.shape
@@ -281,7 +303,8 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
       dn_packed [E,H,I/8], dn_scale/dn_bias [E,H,I/64]; optional e_score_correction_bias [E];
       optional shared_gate_proj [Is,H], shared_up_proj [Is,H], shared_down_proj [H,Is],
       shared_expert_gate [1,H]; optional gu_awq [E,2,H] and dn_awq [E,I] (bf16 values): the
-      activation-aware scales of DeepSeek-V4's packed experts (see awq_expert_rows).
+      activation-aware scales of DeepSeek-V4's packed experts (see awq_expert_rows); or, in
+      place of the gu_/dn_ stacks, "mixed" (per-(expert, projection) widths, see mixed_proj).
     Returns (y bf16-valued float64 [N,H], dict of intermediates).
     """
     n, hdim = x.shape
@@ -291,16 +314,26 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
         scale=scale)
     exp = idx.reshape(-1)
     tok = np.repeat(np.arange(n), k)
-    if p.get("gu_awq") is not None:
+    if p.get("mixed") is not None:
+        # Kimi's QuantizedSparseMoE (`src/quanta/modeling/quantized.py:68-84`): gate and up by
+        # width, h = silu(g) * u (rounded once to bf16 here), down by width
+        g = mixed_proj(x[tok], exp, p["mixed"], "gate", hdim)
+        u = mixed_proj(x[tok], exp, p["mixed"], "up", hdim)
+        gu = np.concatenate([g, u], axis=1)
+        h = swiglu(gu, inter, act, alpha, limit)
+    elif p.get("gu_awq") is not None:
         gu, h = awq_expert_rows(x[tok], exp, p, inter, hdim, act=act, alpha=alpha, limit=limit,
                                 round_weights=round_weights, group_size=group_size, bits=bits)
     else:
         gu = gather_qmm(x[tok], exp, p["gu_packed"], p["gu_scale"], p["gu_bias"], hdim,
                         round_weights=round_weights, group_size=group_size, bits=bits)
         h = swiglu(gu, inter, act, alpha, limit)
-    d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
-                   round_weights=round_weights, group_size=group_size,
-                   bits=bits if down_bits is None else down_bits)
+    if p.get("mixed") is not None:
+        d = mixed_proj(h, exp, p["mixed"], "down", inter)
+    else:
+        d = gather_qmm(h, exp, p["dn_packed"], p["dn_scale"], p["dn_bias"], inter,
+                       round_weights=round_weights, group_size=group_size,
+                       bits=bits if down_bits is None else down_bits)
     routed = combine(d, w)
     y = routed.copy()
     sh = None

@@ -22,7 +22,7 @@ REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
@@ -52,6 +52,7 @@ class QmoeConfig(ctypes.Structure):
         ("act_limit", ctypes.c_float),
         ("down_format", ctypes.c_int32),
         ("awq", ctypes.c_int32),
+        ("mixed", ctypes.c_int32),
     ]
 
 
@@ -71,6 +72,27 @@ class QmoeWeights(ctypes.Structure):
     ]
 
 
+PROJ_GATE, PROJ_UP, PROJ_DOWN = 0, 1, 2
+MAX_STACKS = 12
+
+
+class QmoeStack(ctypes.Structure):
+    _fields_ = [
+        ("proj", ctypes.c_int32),
+        ("format", ctypes.c_int32),
+        ("codes", ctypes.c_void_p),
+        ("sb", ctypes.c_void_p),
+        ("expert_slot", ctypes.c_void_p),
+    ]
+
+
+class QmoeMixed(ctypes.Structure):
+    _fields_ = [
+        ("n_stacks", ctypes.c_int32),
+        ("stacks", QmoeStack * MAX_STACKS),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
@@ -83,6 +105,8 @@ SIGNATURES = {
     "qmoe_forward_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),
     "qmoe_forward": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _I64, _P, _P,
                           ctypes.c_size_t, _P]),
+    "qmoe_forward_mixed": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights),
+                                ctypes.POINTER(QmoeMixed), _P, _I64, _P, _P, ctypes.c_size_t, _P]),
     "qmoe_forward_residual_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),
     "qmoe_forward_residual": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _P, _F,
                                    _I64, _P, _P, ctypes.c_size_t, _P]),

@@ -61,11 +61,23 @@ __global__ void __launch_bounds__(256) awq_glu_kernel(
     const uint16_t* __restrict__ gu, const int32_t* __restrict__ offsets, int E, int I,
     const uint16_t* __restrict__ s_dn, int act, float alpha, float limit, uint16_t* __restrict__ h) {
   const int64_t m = blockIdx.x;
-  const int e = expert_of_row(offsets, E, m);
   const u32x4* g4 = reinterpret_cast<const u32x4*>(gu + m * 2 * I);
   const u32x4* u4 = g4 + I / 8;
-  const u32x4* s4 = reinterpret_cast<const u32x4*>(s_dn + static_cast<int64_t>(e) * I);
   u32x4* o4 = reinterpret_cast<u32x4*>(h + m * I);
+  if (!s_dn) {   // no down-projection scales (experts of mixed widths): h = bf16(glu(g, u))
+    for (int i = threadIdx.x; i < I / 8; i += 256) {
+      const u32x4 g = g4[i], u = u4[i];
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16x2(glu_f(bf16lo_to_f32(g[j]), bf16lo_to_f32(u[j]), act, alpha, limit),
+                           glu_f(bf16hi_to_f32(g[j]), bf16hi_to_f32(u[j]), act, alpha, limit));
+      o4[i] = o;
+    }
+    return;
+  }
+  const int e = expert_of_row(offsets, E, m);
+  const u32x4* s4 = reinterpret_cast<const u32x4*>(s_dn + static_cast<int64_t>(e) * I);
   for (int i = threadIdx.x; i < I / 8; i += 256) {
     const u32x4 g = g4[i], u = u4[i], s = s4[i];
     u32x4 o;

@@ -344,7 +344,8 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.h_sinv = take(static_cast<size_t>(mc) * 4);
   // AWQ: the gate and up projections' prescaled rows [2][mc][H] and their outputs [mc][2I]
   L.awq_x = take(c.awq ? static_cast<size_t>(2) * mc * c.hidden * 2 : 0);
-  L.awq_gu = take(c.awq ? static_cast<size_t>(mc) * 2 * c.inter * 2 : 0);
+  // (mixed widths also route gate and up through awq_gu)
+  L.awq_gu = take((c.awq || c.mixed) ? static_cast<size_t>(mc) * 2 * c.inter * 2 : 0);
   L.total = o;
   return L;
 }
@@ -369,6 +370,22 @@ static bool narrow_codes(const qmoe_config_t& c) {
          c.down_format == QMOE_FMT_INT6_G64 || c.down_format == QMOE_FMT_INT3_G64;
 }
 
+static int validate_mixed(const qmoe_mixed_t& m) {
+  if (m.n_stacks < 3 || m.n_stacks > QMOE_MAX_STACKS)
+    return fail("mixed: 3 <= n_stacks <= QMOE_MAX_STACKS required");
+  int seen[3] = {0, 0, 0};
+  for (int i = 0; i < m.n_stacks; ++i) {
+    const qmoe_stack_t& st = m.stacks[i];
+    if (st.proj < QMOE_PROJ_GATE || st.proj > QMOE_PROJ_DOWN) return fail("mixed: unknown proj");
+    if (st.format != QMOE_FMT_INT4_G64 && st.format != QMOE_FMT_INT6_G64 && st.format != QMOE_FMT_INT3_G64)
+      return fail("mixed: stack formats must be int3, int4 or int6");
+    if (!st.codes || !st.sb || !st.expert_slot) return fail("mixed: null stack pointer");
+    seen[st.proj] = 1;
+  }
+  if (!seen[0] || !seen[1] || !seen[2]) return fail("mixed: every projection needs a stack");
+  return 0;
+}
+
 static int validate_config(const qmoe_config_t& c) {
   const int rc = validate_routing(1, c.hidden, c.n_experts, c.top_k, c.scoring, c.n_group,
                                   c.topk_group);
@@ -390,6 +407,9 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: awq scales need quantized experts");
   if (c.awq && c.regime == QMOE_REGIME_LARGE)
     return fail("config: experts with awq scales run in the small regime only");
+  if (c.mixed != 0 && c.mixed != 1) return fail("config: mixed must be 0 or 1");
+  if (c.mixed && (c.awq || c.regime == QMOE_REGIME_LARGE))
+    return fail("config: mixed-width experts run in the small regime, without awq scales");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {
     if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 256)
       return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 256");
@@ -503,23 +523,31 @@ static int dense_regime(const qmoe_config_t& c, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  if (narrow_codes(c) || c.awq) return QMOE_REGIME_SMALL;   // no large int3/int6/AWQ kernel
+  // no large-regime kernel for int3/int6, AWQ scales or mixed widths
+  if (narrow_codes(c) || c.awq || c.mixed) return QMOE_REGIME_SMALL;
   return dense_regime(c, N);
 }
 
 // The block on x; with resid, the combine adds the decoder layer's residual row.
 static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
                         int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream_,
-                        const uint16_t* resid) {
+                        const uint16_t* resid, const qmoe_mixed_t* mixed = nullptr) {
   if (!cfg || !wts || !x || !y || !ws) return fail("qmoe_forward: null pointer");
   const qmoe_config_t& c = *cfg;
   int rc = validate_config(c);
   if (rc) return rc;
+  if (c.mixed != (mixed != nullptr))
+    return fail("qmoe_forward: mixed-width experts go through qmoe_forward_mixed (config mixed = 1)");
+  if (mixed) {
+    rc = validate_mixed(*mixed);
+    if (rc) return rc;
+  }
   if (N <= 0 || N > 65535) return fail("qmoe_forward: 0 < N <= 65535 tokens per call");
   const WsLayout L = ws_layout(c, N);
   if (ws_bytes < L.total) return fail("qmoe_forward: workspace too small");
-  if (!wts->router_w || !wts->gu_codes || !wts->dn_codes) return fail("qmoe_forward: missing weights");
-  if (c.expert_format != QMOE_FMT_BF16 && (!wts->gu_sb || !wts->dn_sb))
+  if (!wts->router_w || (!mixed && (!wts->gu_codes || !wts->dn_codes)))
+    return fail("qmoe_forward: missing weights");
+  if (!mixed && c.expert_format != QMOE_FMT_BF16 && (!wts->gu_sb || !wts->dn_sb))
     return fail("qmoe_forward: quantized experts need scale/bias");
   if (c.shared_inter > 0 && (!wts->sh_gu || !wts->sh_dn)) return fail("qmoe_forward: missing shared expert");
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
@@ -682,7 +710,25 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     return launch_qmm(a, fmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
   };
   // 5. routed gate_up + SwiGLU -> h (sorted order)
-  if (c.awq) {
+  if (mixed) {
+    // widths per (expert, projection): gate and up by width into awq_gu, then h = bf16(glu)
+    uint16_t* gu = reinterpret_cast<uint16_t*>(base + L.awq_gu);
+    for (int i = 0; i < mixed->n_stacks; ++i) {
+      const qmoe_stack_t& st = mixed->stacks[i];
+      if (st.proj == QMOE_PROJ_DOWN) continue;
+      QmmArgs a{};
+      a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
+      a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+      a.K = c.hidden; a.n_rows = c.inter; a.codes = st.codes; a.sb = st.sb;
+      a.expert_map = st.expert_slot;
+      a.out = gu + (st.proj == QMOE_PROJ_UP ? c.inter : 0); a.ld_out = 2 * c.inter;
+      rc = routed(a, kernel_fmt(st.format), EPI_BF16, nullptr, nullptr);
+      if (rc) return rc;
+    }
+    rc = launch_awq_glu(gu, offsets, c.n_experts, mc, c.inter, nullptr, c.act, c.act_alpha,
+                        c.act_limit, h, stream);
+    if (rc) return rc;
+  } else if (c.awq) {
     // AWQ: gate and up on their own prescaled rows (one launch over all 2I rows of each expert,
     // the up half's tiles reading the up rows) into awq_gu, then h = bf16(glu / s_dn)
     uint16_t* xg = reinterpret_cast<uint16_t*>(base + L.awq_x);
@@ -735,8 +781,18 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = link(aux->hready, stream, aux->s, "h to auxiliary stream");
       if (rc) return rc;
     }
-    rc = routed(a, dfmt, EPI_BF16, h16, h_sinv);
-    if (rc) return rc;
+    if (mixed) {
+      for (int i = 0; i < mixed->n_stacks; ++i) {
+        const qmoe_stack_t& st = mixed->stacks[i];
+        if (st.proj != QMOE_PROJ_DOWN) continue;
+        a.codes = st.codes; a.sb = st.sb; a.expert_map = st.expert_slot;
+        rc = routed(a, kernel_fmt(st.format), EPI_BF16, nullptr, nullptr);
+        if (rc) return rc;
+      }
+    } else {
+      rc = routed(a, dfmt, EPI_BF16, h16, h_sinv);
+      if (rc) return rc;
+    }
   }
   if (aux) {
     rc = link(aux->join, aux->s, stream, "join");
@@ -753,6 +809,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
 extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
                             int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
   return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream, nullptr);
+}
+
+extern "C" int qmoe_forward_mixed(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
+                                  const qmoe_mixed_t* mixed, const uint16_t* x, int64_t N,
+                                  uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
+  if (!mixed) return fail("qmoe_forward_mixed: null pointer");
+  return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream, nullptr, mixed);
 }
 
 // The block with the decoder layer's steps either side of it: the normalised rows go to the

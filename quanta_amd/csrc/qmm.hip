@@ -143,6 +143,12 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
   int e, mt0[MT], mtc[MT];
   if (MT == 1) {
     if (!resolve_mtile(a, by, kSmallMTile, e, mt0[0], mtc[0])) return;
+    // (one stack of a projection whose experts have different widths: the others' m-tiles exit;
+    // every wavefront of the workgroup resolves the same m-tile)
+    if (a.expert_map) {
+      e = a.expert_map[e];
+      if (e < 0) return;
+    }
   } else {   // dense rows (the launcher guarantees no segments)
     e = 0;
 #pragma unroll
@@ -1199,6 +1205,8 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (a.K <= 0 || a.n_rows <= 0) return fail("qmm: empty problem");
   if (mtile_bound <= 0) return 0;
   if (mtile_bound > 65535) return fail("qmm: too many m-tiles for one launch");
+  if (a.expert_map && regime != QMOE_REGIME_SMALL)
+    return fail("qmm: an expert map needs the small regime");
   if (a.act_hi) {
     if (regime != QMOE_REGIME_SMALL || !fmt_quant(fmt) || epi == EPI_SWIGLU || a.slot_of)
       return fail("qmm: a second activation needs quantized weights, the small regime, a "

@@ -245,6 +245,8 @@ struct QmmArgs {
                               // weight tiles from split_tile on (AWQ: the up half of gate_up
                               // reads rows prescaled for the up projection)
   int split_tile;             // first 16-row tile that reads act_hi (a multiple of 4)
+  const int32_t* expert_map;  // small regime, nullable: expert -> its slot in this launch's
+                              // weight stack, -1 when it is not in the stack (its m-tiles exit)
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3 };
@@ -287,7 +289,8 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 int launch_awq_prescale(const uint16_t* x, const int32_t* sorted, const int32_t* offsets, int E,
                         int k, int64_t mc, int H, const uint16_t* s_gu, uint16_t* xg, uint16_t* xu,
                         hipStream_t stream);
-// h[m] = bf16(glu(g, u) / s_dn[e]) over gu [mc][2I] (gate | up, bf16) with s_dn bf16 [E][I].
+// h[m] = bf16(glu(g, u) / s_dn[e]) over gu [mc][2I] (gate | up, bf16) with s_dn bf16 [E][I];
+// s_dn NULL: h[m] = bf16(glu(g, u)) (offsets unused).
 int launch_awq_glu(const uint16_t* gu, const int32_t* offsets, int E, int64_t mc, int I,
                    const uint16_t* s_dn, int act, float alpha, float limit, uint16_t* h,
                    hipStream_t stream);

@@ -124,6 +124,47 @@ def tile_experts_bf16(stack: torch.Tensor) -> TiledExperts:
                         shape=tuple(stack.shape), group_size=0, bits=16)
 
 
+PROJS = ("gate", "up", "down")
+
+
+class MixedExperts(dict):
+    """Routed experts whose widths vary per (expert, projection), resident: "stacks" is a list of
+    (projection, TiledExperts, expert map [E] int32 on the device: the expert's slot in that
+    stack or -1), "n_experts" E. Built by tile_experts_mixed."""
+
+
+def tile_experts_mixed(stacks: dict, pbits: dict, pslot: dict, *, group_size: int = 128) -> MixedExperts:
+    """Kimi's per-(expert, projection) widths (QuantizedSparseMoE.set_experts,
+    src/quanta/modeling/quantized.py:40-51) -> MixedExperts. `stacks[proj][bits]` is the packed
+    stack {packed, scale, bias} of that projection and width ("gate", "up" [E_w, I, H], "down"
+    [E_w, H, I]); `pbits[proj]` / `pslot[proj]` [E]: each expert's width and its slot in that
+    width's stack. Checked here, on the host: every expert's width has a stack and its slot lies
+    in it (the kernels read the maps without checks)."""
+    if isinstance(stacks, MixedExperts):
+        return stacks
+    out, E = [], None
+    for proj in PROJS:
+        pb = torch.as_tensor(pbits[proj]).to("cpu", torch.int64).reshape(-1)
+        ps = torch.as_tensor(pslot[proj]).to("cpu", torch.int64).reshape(-1)
+        if E is None:
+            E = pb.numel()
+        if pb.numel() != E or ps.numel() != E:
+            raise ValueError(f"pbits/pslot[{proj!r}] must have one entry per expert ({E})")
+        have = {int(b) for b in stacks[proj]}
+        missing = sorted(set(pb.tolist()) - have)
+        if missing:
+            raise ValueError(f"{proj}: experts of width {missing} have no stack")
+        for bits in sorted(have):
+            st = stacks[proj][bits]
+            te = tile_experts_packed(dict(st, bits=bits, group_size=int(st.get("group_size", group_size))))
+            mine = pb == bits
+            if bool(mine.any()) and (int(ps[mine].min()) < 0 or int(ps[mine].max()) >= te["shape"][0]):
+                raise ValueError(f"{proj}: slots of width {bits} outside its stack of {te['shape'][0]}")
+            emap = torch.where(mine, ps, torch.full_like(ps, -1)).to(torch.int32).to(te["codes"].device)
+            out.append((proj, te, emap))
+    return MixedExperts(stacks=out, n_experts=E)
+
+
 def _is_packed(v) -> bool:
     """Auto-detection of packed experts, as the reference does with isinstance(dict)
     (src/quanta/qwen35/moe.py:181)."""
@@ -198,6 +239,7 @@ class Prepared:
     sh_gu: torch.Tensor | None
     sh_dn: torch.Tensor | None
     bias: torch.Tensor | None
+    mixed: L.QmoeMixed | None = None
 
 
 def _prepare_router(gate: torch.Tensor, sgate: torch.Tensor | None, E: int, H: int):
@@ -261,6 +303,8 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     if scoring not in ("softmax", "sigmoid"):
         raise ValueError(f"scoring_func {scoring!r} not supported (softmax | sigmoid)")
 
+    if p.get("experts_mixed") is not None:
+        return _prepare_mixed(p, cfg, topk=topk, regime=regime)
     gu_src, dn_src = p["experts_gate_up"], p["experts_down"]
     packed = _is_packed(gu_src)
     if packed != _is_packed(dn_src):
@@ -321,9 +365,10 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     w.router_w = rw.data_ptr()
     w.router_bias = bias.data_ptr() if bias is not None else None
     w.shared_gate_w = sg32.data_ptr() if sg32 is not None else None
-    w.gu_codes = gu["codes"].data_ptr()
+    # (codes None: the shape-only placeholder of a mixed-width layer, see _prepare_mixed)
+    w.gu_codes = gu["codes"].data_ptr() if gu["codes"] is not None else None
     w.gu_sb = gu["sb"].data_ptr() if gu["sb"] is not None else None
-    w.dn_codes = dn["codes"].data_ptr()
+    w.dn_codes = dn["codes"].data_ptr() if dn["codes"] is not None else None
     w.dn_sb = dn["sb"].data_ptr() if dn["sb"] is not None else None
     w.sh_gu = sh_gu.data_ptr() if sh_gu is not None else None
     w.sh_dn = sh_dn.data_ptr() if sh_dn is not None else None
@@ -332,6 +377,43 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn, awq_gu, awq_dn)
     return Prepared(c, w, keep, rw if rkind == "bf16" else None, rw if rkind == "f32" else None,
                     sg32, gu, dn, sh_gu, sh_dn, bias)
+
+
+def _prepare_mixed(p: dict, cfg, *, topk, regime) -> Prepared:
+    """prepare() for p["experts_mixed"] (MixedExperts, or the reference's (stacks, pbits, pslot)
+    as a dict with those keys): the rest of the block as for uniform stacks, the routed experts
+    through qmoe_forward_mixed."""
+    H, E = int(_cfg(cfg, "hidden_size")), int(_cfg(cfg, "num_experts"))
+    I = int(_cfg(cfg, "moe_intermediate_size"))
+    src = p["experts_mixed"]
+    mx = _cached("mixed", (src,), lambda: src if isinstance(src, MixedExperts) else
+                 tile_experts_mixed(src["stacks"], src["pbits"], src["pslot"],
+                                    group_size=int(src.get("group_size", 128))))
+    if mx["n_experts"] != E:
+        raise ValueError(f"mixed experts: {mx['n_experts']} experts for a {E}-expert config")
+    if len(mx["stacks"]) > L.MAX_STACKS:
+        raise ValueError(f"mixed experts: at most {L.MAX_STACKS} (projection, width) stacks")
+    m = L.QmoeMixed()
+    m.n_stacks = len(mx["stacks"])
+    fmts = {"int4_g64": L.FMT_INT4_G64, "int6_g64": L.FMT_INT6_G64, "int3_g64": L.FMT_INT3_G64}
+    for i, (proj, te, emap) in enumerate(mx["stacks"]):
+        want = (I, H) if proj != "down" else (H, I)
+        if tuple(te["shape"][1:]) != want:
+            raise ValueError(f"mixed experts: {proj} stacks must be [E_w, {want[0]}, {want[1]}] "
+                             f"(got {tuple(te['shape'])})")
+        m.stacks[i] = L.QmoeStack(PROJS.index(proj), fmts[te["format"]], te["codes"].data_ptr(),
+                                  te["sb"].data_ptr(), emap.data_ptr())
+    # the rest of the block: a placeholder uniform stack pair supplies nothing but the shapes
+    q = {kk: v for kk, v in p.items() if kk != "experts_mixed"}
+    q["experts_gate_up"] = TiledExperts(format="int4_g64", codes=None, sb=None, shape=(E, 2 * I, H),
+                                        group_size=64, bits=4)
+    q["experts_down"] = TiledExperts(format="int4_g64", codes=None, sb=None, shape=(E, H, I),
+                                     group_size=64, bits=4)
+    pr = prepare(q, cfg, topk=topk, regime=regime)
+    pr.cfg.mixed = 1
+    pr.mixed = m
+    pr.keep = pr.keep + (mx,)
+    return pr
 
 
 # ----------------------------------------------------------------------------------- routing
@@ -455,7 +537,7 @@ def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chun
     topk = topk_override if topk_override is not None else k_max
     if topk < 1 or topk > k_max:
         raise ValueError(f"topk_override {topk_override} must be in [1, {k_max}]")
-    packed = _is_packed(p["experts_gate_up"])
+    packed = p.get("experts_mixed") is not None or _is_packed(p["experts_gate_up"])
     if not sparse and packed:
         raise ValueError("qwen35_moe(sparse=False) is the bf16 dense oracle; packed int4 experts "
                          "require sparse=True (gather_qmm). Refusing to dequant silently.")
@@ -472,7 +554,7 @@ def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chun
                      device=x.device)
     for c0 in range(0, n, chunk):
         c1 = min(c0 + chunk, n)
-        ops.forward(pr.cfg, pr.weights, xf[c0:c1], out=y[c0:c1], ws=ws)
+        ops.forward(pr.cfg, pr.weights, xf[c0:c1], out=y[c0:c1], ws=ws, mixed=pr.mixed)
     return y.reshape(b, s, hidden)
 
 
@@ -545,6 +627,7 @@ class Qwen35MoEModule(torch.nn.Module):
         self.gate = torch.zeros(e, h, dtype=dtype, device=dev)
         self.experts_gate_up = None
         self.experts_down = None
+        self.experts_mixed = None
         self.shared_gate_proj = torch.zeros(si, h, dtype=dtype, device=dev)
         self.shared_up_proj = torch.zeros(si, h, dtype=dtype, device=dev)
         self.shared_down_proj = torch.zeros(h, si, dtype=dtype, device=dev)
@@ -555,19 +638,28 @@ class Qwen35MoEModule(torch.nn.Module):
     def set_experts(self, gate_up: torch.Tensor, down: torch.Tensor) -> None:
         """bf16 expert stacks [E,2I,H] / [E,H,I] (src/quanta/qwen35/model.py:46-47)."""
         self.experts_gate_up, self.experts_down = tile_experts_bf16(gate_up), tile_experts_bf16(down)
+        self.experts_mixed = None
 
     def set_experts_packed(self, gate_up: dict, down: dict) -> None:
         """Packed int4 triplets {packed, scale, bias, group_size, bits}
         (src/quanta/qwen35/model.py:49-55); converted once to the tiled resident layout."""
         self.experts_gate_up, self.experts_down = tile_experts_packed(gate_up), tile_experts_packed(down)
+        self.experts_mixed = None
+
+    def set_experts_mixed(self, stacks: dict, pbits: dict, pslot: dict, *, group_size: int = 128) -> None:
+        """Widths per (expert, projection), as QuantizedSparseMoE.set_experts(stacks, pbits, pslot)
+        (src/quanta/modeling/quantized.py:40-51); converted once to tiled stacks."""
+        self.experts_mixed = tile_experts_mixed(stacks, pbits, pslot, group_size=group_size)
+        self.experts_gate_up = self.experts_down = None
 
     def _params(self) -> dict:
-        if self.experts_gate_up is None or self.experts_down is None:
-            raise ValueError("experts not set: call set_experts or set_experts_packed first")
+        if self.experts_mixed is None and (self.experts_gate_up is None or self.experts_down is None):
+            raise ValueError("experts not set: call set_experts, set_experts_packed or set_experts_mixed first")
+        experts = ({"experts_mixed": self.experts_mixed} if self.experts_mixed is not None else
+                   {"experts_gate_up": self.experts_gate_up, "experts_down": self.experts_down})
         p = {
             "gate": self.gate,
-            "experts_gate_up": self.experts_gate_up,
-            "experts_down": self.experts_down,
+            **experts,
             "shared_gate_proj": self.shared_gate_proj,
             "shared_up_proj": self.shared_up_proj,
             "shared_down_proj": self.shared_down_proj,

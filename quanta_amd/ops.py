@@ -290,8 +290,10 @@ def forward_workspace(cfg: L.QmoeConfig, N: int) -> int:
 
 
 def forward(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
-            out: torch.Tensor | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
-    """Whole block on x [N, H] bf16 (qmoe_forward). `ws` may be a preallocated uint8 buffer."""
+            out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+            mixed: L.QmoeMixed | None = None) -> torch.Tensor:
+    """Whole block on x [N, H] bf16 (qmoe_forward; with `mixed`, the routed experts of mixed
+    widths, qmoe_forward_mixed). `ws` may be a preallocated uint8 buffer."""
     _need(x, torch.bfloat16, "x")
     N, H = x.shape
     if H != cfg.hidden:
@@ -301,6 +303,11 @@ def forward(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
         ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     if out is None:
         out = torch.empty(N, H, dtype=torch.bfloat16, device=x.device)
+    if mixed is not None:
+        L.check(L.load().qmoe_forward_mixed(ctypes.byref(cfg), ctypes.byref(weights), ctypes.byref(mixed),
+                                            _p(x), N, _p(out), _p(ws), ws.numel(), _stream(x.device)),
+                "qmoe_forward_mixed")
+        return out
     L.check(L.load().qmoe_forward(ctypes.byref(cfg), ctypes.byref(weights), _p(x), N, _p(out),
                                   _p(ws), ws.numel(), _stream(x.device)), "qmoe_forward")
     return out

@@ -26,6 +26,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from quanta_amd.moe import MoEConfig
@@ -93,6 +94,37 @@ def _quantized_stack(E, rows, K, g, device, chunk_elems=1 << 28, bits=4, group_s
         packed[e0:e1], scale[e0:e1], bias[e0:e1] = q, s, b
         del w, q, s, b
     return {"packed": packed, "scale": scale, "bias": bias, "group_size": group_size, "bits": bits}
+
+
+def make_mixed_experts(name: str, *, device="cuda", seed: int = 0, choices=(3, 4),
+                       group_size: int = 128) -> dict:
+    """Routed experts of widths drawn per (expert, projection) from `choices` (Kimi's
+    per-projection bake, src/quanta/modeling/quantized.py:40-51), as the reference's
+    (stacks, pbits, pslot): one stack per (projection, width), experts in id order."""
+    c = SPECS[name].cfg
+    E, H, I = c.num_experts, c.hidden_size, c.moe_intermediate_size
+    g = _gen(device, seed * 1009 + 7)
+    rng = np.random.default_rng(seed)
+    stacks, pbits, pslot = {}, {}, {}
+    for proj in ("gate", "up", "down"):
+        rows, K = (I, H) if proj != "down" else (H, I)
+        pb = rng.choice(np.asarray(choices), E)
+        ps = np.zeros(E, np.int64)
+        stacks[proj] = {}
+        for b in sorted(set(pb.tolist())):
+            ids = np.flatnonzero(pb == b)
+            ps[ids] = np.arange(ids.size)
+            stacks[proj][b] = _quantized_stack(ids.size, rows, K, g, device, bits=b, group_size=group_size)
+        pbits[proj], pslot[proj] = pb, ps
+    return {"stacks": stacks, "pbits": pbits, "pslot": pslot, "group_size": group_size}
+
+
+def mixed_expert_bytes(mixed: dict, cfg) -> float:
+    """Mean bytes per expert of a mixed-width layer (codes + a bf16 scale and bias per group)."""
+    H, I, gs = cfg.hidden_size, cfg.moe_intermediate_size, mixed["group_size"]
+    tot = sum(I * H * (np.asarray(mixed["pbits"][proj]) * gs + 32) / (8 * gs)
+              for proj in ("gate", "up", "down"))
+    return float(np.mean(tot))
 
 
 def zipf_logit_bias(E: int, g: torch.Generator, device) -> torch.Tensor:

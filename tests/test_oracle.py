@@ -572,3 +572,37 @@ def test_awq_rows_power_of_two_scales():
     assert np.array_equal(gu[:, I:], gu1[:, I:] * 2.0 ** -jg[exp, 1][:, None])
     want_h = oq.round_bf16(om.glu(gu[:, :I], gu[:, I:])) * 2.0 ** -jd[exp][:, None]
     assert np.array_equal(h, want_h)
+
+
+# ----------------------------------------------------------------------------------- mixed widths
+
+
+def test_mixed_proj_widths_and_slots():
+    """mixed_proj against a per-row loop: each row's expert picks its width's stack and its slot in
+    it (slots permuted, so a slot/expert mix-up fails); with one width and identity slots it is
+    gather_qmm on that stack."""
+    rng = np.random.default_rng(8)
+    E, rows, K, gs = 6, 32, 256, 128
+    pbits = np.array([3, 4, 4, 3, 6, 4])
+    stacks, pslot = {}, np.zeros(E, np.int64)
+    for b in (3, 4, 6):
+        ids = np.flatnonzero(pbits == b)
+        perm = rng.permutation(ids.size)
+        pslot[ids] = perm
+        w = rng.standard_normal((ids.size, rows, K)) * 0.05
+        packed, sb, bb, _ = oq.quantize_rtn(w, b, gs)
+        stacks[b] = (packed, sb, bb)
+    m = {"stacks": {"gate": stacks}, "pbits": {"gate": pbits}, "pslot": {"gate": pslot}, "group_size": gs}
+    x = oq.round_bf16(rng.standard_normal((9, K)))
+    exp = rng.integers(0, E, 9)
+    got = om.mixed_proj(x, exp, m, "gate", K)
+    for r in range(9):
+        e = exp[r]
+        packed, sb, bb = stacks[pbits[e]]
+        w = oq.dequant_exact(packed[pslot[e]], sb[pslot[e]], bb[pslot[e]], K, bits=int(pbits[e]), group_size=gs)
+        assert np.array_equal(got[r], oq.round_bf16(w @ x[r]))
+    uni = {"stacks": {"gate": {4: stacks[4]}}, "pbits": {"gate": np.full(2, 4)},
+           "pslot": {"gate": np.arange(2)}, "group_size": gs}
+    e2 = rng.integers(0, 2, 5)
+    assert np.array_equal(om.mixed_proj(x[:5], e2, uni, "gate", K),
+                          om.gather_qmm(x[:5], e2, *stacks[4], K, group_size=gs, bits=4))
