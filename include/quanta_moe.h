@@ -41,6 +41,7 @@ extern "C" {
 /* scoring functions (cfg.scoring_func, src/quanta/qwen35/config.py:129) */
 #define QMOE_SCORE_SOFTMAX 0
 #define QMOE_SCORE_SIGMOID 1
+#define QMOE_SCORE_SQRTSOFTPLUS 2   /* DeepSeek-V4: sqrt(softplus(logit)), src/quanta/dsv4/moe.py:37-57 */
 
 /* expert weight formats, both in this library's MFMA-tiled layout (see qmoe_tile_*) */
 #define QMOE_FMT_INT4_G64 0

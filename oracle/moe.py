@@ -95,6 +95,8 @@ def route(x: np.ndarray, wr: np.ndarray, *, k: int, scoring: str = "softmax",
     sigmoid + correction bias (`src/quanta/modeling/moe.py:36-43`, `src/quanta/glm/moe.py:48-55`):
     scores = sigmoid(logits); select by scores + bias (optionally group-limited); weights are
     the bias-free scores, renormalised, then times `scale` (routed_scaling_factor).
+    sqrtsoftplus (DeepSeek-V4, `src/quanta/dsv4/moe.py:37-57`): scores = sqrt(log(1 + e^logits)),
+    then as sigmoid.
     """
     logits = x.astype(np.float64) @ wr.astype(np.float64).T
     if scoring == "softmax":
@@ -103,6 +105,8 @@ def route(x: np.ndarray, wr: np.ndarray, *, k: int, scoring: str = "softmax",
         scores = p / p.sum(axis=-1, keepdims=True)
     elif scoring == "sigmoid":
         scores = _sigmoid(logits)
+    elif scoring == "sqrtsoftplus":
+        scores = np.sqrt(np.logaddexp(0.0, logits))
     else:
         raise ValueError(scoring)
     choice = scores + bias[None, :].astype(np.float64) if bias is not None else scores.copy()

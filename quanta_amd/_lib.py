@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().with_name("_qmoe.so")
 HEADER = Path(__file__).resolve().parent.parent / "include" / "quanta_moe.h"
 
 QMOE_OK, QMOE_EINVAL, QMOE_EHIP = 0, -1, -2
-SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
 FMT_INT4_G64, FMT_BF16, FMT_INT6_G64, FMT_INT3_G64 = 0, 1, 2, 3
 ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
 REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2

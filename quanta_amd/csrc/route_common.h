@@ -129,13 +129,18 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
     const float inv = 1.0f / z;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) sc[i] *= inv;
-  } else {
+  } else if (P.scoring == QMOE_SCORE_SIGMOID) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
       sc[i] = (e_base + i < E) ? 1.0f / (1.0f + expf(-lg[i])) : 0.f;
+  } else {   // sqrt(softplus), softplus(l) = log(1 + e^l) = max(l, 0) + log1p(e^-|l|)
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      sc[i] = (e_base + i < E) ? sqrtf(fmaxf(lg[i], 0.f) + log1pf(expf(-fabsf(lg[i])))) : 0.f;
   }
   // Without a bias, softmax selection by probability equals selection by logit (monotone); the
-  // logit avoids ties manufactured by rounding exp(). Sigmoid selects on the score.
+  // logit avoids ties manufactured by rounding exp(). Sigmoid and sqrt-softplus select on the
+  // score, as the reference does.
   const bool by_logit = (P.scoring == QMOE_SCORE_SOFTMAX);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {

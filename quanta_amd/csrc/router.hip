@@ -119,8 +119,9 @@ int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int t
   if (N <= 0 || H <= 0) return fail("router: N and H must be positive");
   if (E < 1 || E > 1024) return fail("router: 1 <= E <= 1024 required");
   if (k < 1 || k > E || k > 64) return fail("router: 1 <= k <= min(E, 64) required");
-  if (scoring != QMOE_SCORE_SOFTMAX && scoring != QMOE_SCORE_SIGMOID)
-    return fail("router: scoring must be softmax (0) or sigmoid (1)");
+  if (scoring != QMOE_SCORE_SOFTMAX && scoring != QMOE_SCORE_SIGMOID &&
+      scoring != QMOE_SCORE_SQRTSOFTPLUS)
+    return fail("router: scoring must be softmax (0), sigmoid (1) or sqrtsoftplus (2)");
   if (n_group < 1 || n_group > 64 || E % n_group) return fail("router: E % n_group == 0, n_group <= 64");
   if (n_group > 1) {
     if (E / n_group < 2) return fail("router: group-limited routing needs >= 2 experts per group");

@@ -125,6 +125,9 @@ def tile_experts_bf16(stack: torch.Tensor) -> TiledExperts:
 
 
 PROJS = ("gate", "up", "down")
+# router score functions: Qwen softmax; DeepSeek-V3/GLM sigmoid; DeepSeek-V4 sqrt(softplus)
+# (src/quanta/dsv4/moe.py:37-57)
+_SCORING = {"softmax": L.SCORE_SOFTMAX, "sigmoid": L.SCORE_SIGMOID, "sqrtsoftplus": L.SCORE_SQRTSOFTPLUS}
 
 
 class MixedExperts(dict):
@@ -300,8 +303,8 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     Is = int(_cfg(cfg, "shared_expert_intermediate_size", 0))
     k = int(topk if topk is not None else _cfg(cfg, "num_experts_per_tok"))
     scoring = str(_cfg(cfg, "scoring_func", "softmax"))
-    if scoring not in ("softmax", "sigmoid"):
-        raise ValueError(f"scoring_func {scoring!r} not supported (softmax | sigmoid)")
+    if scoring not in _SCORING:
+        raise ValueError(f"scoring_func {scoring!r} not supported (softmax | sigmoid | sqrtsoftplus)")
 
     if p.get("experts_mixed") is not None:
         return _prepare_mixed(p, cfg, topk=topk, regime=regime)
@@ -335,7 +338,7 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     c = L.QmoeConfig()
     c.hidden, c.n_experts, c.top_k, c.inter = H, E, k, I
     c.shared_inter = Is if has_shared else 0
-    c.scoring = L.SCORE_SOFTMAX if scoring == "softmax" else L.SCORE_SIGMOID
+    c.scoring = _SCORING[scoring]
     c.norm_topk = int(bool(_cfg(cfg, "norm_topk_prob", True)))
     c.n_group = int(_cfg(cfg, "n_group", 1))
     c.topk_group = int(_cfg(cfg, "topk_group", 1))
@@ -465,7 +468,7 @@ def qwen35_route(xf: torch.Tensor, gate_w: torch.Tensor, cfg, *, topk_override: 
         logits = ops.grouped_qmm(xf, K=H, n_rows=rows, weight_format=L.FMT_BF16, codes=rw, sb=None,
                                  epilogue=L.EPI_F32, out_rows=n, regime=_dense_regime(n, H),
                                  dense_rows=n)
-    scoring = L.SCORE_SOFTMAX if _cfg(cfg, "scoring_func", "softmax") == "softmax" else L.SCORE_SIGMOID
+    scoring = _SCORING[str(_cfg(cfg, "scoring_func", "softmax"))]
     bias = None if e_score_correction_bias is None else e_score_correction_bias.float().reshape(E).contiguous()
     idx, w, _ = ops.router_topk(logits, E, k, scoring=scoring, bias=bias,
                                 n_group=int(_cfg(cfg, "n_group", 1)),

@@ -74,7 +74,7 @@ def _route_case(rng, N, E, H, k, scoring, bias=False, n_group=1, topk_group=1, s
 def _check_route(gpu, x, wr, kw, logits_dev, E):
     idx_o, w_o, logits_o, scores_o, choice_o = om.route(x, wr, **kw)
     k = kw["k"]
-    idx, w, _ = ops.router_topk(logits_dev, E, k, scoring=0 if kw["scoring"] == "softmax" else 1,
+    idx, w, _ = ops.router_topk(logits_dev, E, k, scoring={"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}[kw["scoring"]],
                                 bias=None if kw["bias"] is None else
                                 torch.tensor(kw["bias"], dtype=torch.float32, device=gpu),
                                 n_group=kw["n_group"], topk_group=kw["topk_group"],
@@ -107,6 +107,8 @@ def _check_route(gpu, x, wr, kw, logits_dev, E):
     dict(N=64, E=256, H=7168, k=8, scoring="sigmoid", bias=True, n_group=8, topk_group=4, scale=2.5),
     dict(N=5, E=64, H=256, k=1, scoring="sigmoid", bias=True, norm=False),
     dict(N=3, E=1024, H=256, k=16, scoring="softmax"),
+    dict(N=40, E=256, H=1024, k=6, scoring="sqrtsoftplus", bias=True, scale=1.5),
+    dict(N=9, E=384, H=512, k=8, scoring="sqrtsoftplus"),
 ])
 def test_router_topk_vs_oracle(gpu, case):
     rng = np.random.default_rng(case["N"] * 31 + case["E"])

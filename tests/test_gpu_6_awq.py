@@ -1,8 +1,8 @@
 """GPU tier: DeepSeek-V4's activation-aware (AWQ) expert scales (src/quanta/dsv4/moe.py:112-137).
 
 The block divides each routed row's activation by its expert's per-input-channel scale before
-the gate, the up and the down projection (qmoe_config_t.awq; kernels in awq.hip, the gate and up
-halves of the fused gate_up stack as two launches).
+the gate, the up and the down projection (qmoe_config_t.awq; kernels in awq.hip; gate_up as one
+launch whose up-half wavefronts read the rows prescaled for the up projection).
 
 Bars: unit scales give the plain path's output bit for bit (same per-output arithmetic); random
 scales within the BASELINE gates of the oracle (max-abs 2e-2 scaled, relative L2 5e-3) at every
@@ -46,9 +46,9 @@ def _with_awq(p, dev, seed, E=8, H=512, I=256, unit=False):
 
 @pytest.mark.parametrize("N", [1, 8, 40, 300])
 def test_awq_unit_scales_equal_plain_path(gpu, N):
-    """All-ones scales: prescaling is exact and the gated activation divides by one, so the two
-    half-stack launches plus the AWQ activation pass reproduce the fused SwiGLU launch bit for bit
-    (the K chunks and their order depend on the shape only)."""
+    """All-ones scales: prescaling is exact and the gated activation divides by one, so the
+    bf16-epilogue gate_up launch plus the AWQ activation pass reproduce the fused SwiGLU launch
+    bit for bit (the K chunks and their order depend on the shape only)."""
     cfg = _cfg()
     p = _layer(gpu, 64, seed=3 * N, gated=False)
     x = _inputs(gpu, N, 512, N)
@@ -74,6 +74,24 @@ def test_awq_block_vs_oracle(gpu, gs, gu_bits, dn_bits, N):
     if N >= 40:
         g = it["gu"][:, :256]
         assert np.any(g > LIMIT), "the clamp must bind somewhere for the test to mean anything"
+
+
+@pytest.mark.parametrize("N", [1, 8, 40, 300])
+def test_dsv4_block_vs_oracle(gpu, N):
+    """DeepSeek-V4's block as the reference composes it (src/quanta/dsv4/moe.py:140-173):
+    sqrt-softplus scores with the selection bias, normalised weights times 1.5, clamped SwiGLU,
+    AWQ-scaled int4 experts and an ungated shared expert."""
+    cfg = MoEConfig(512, 8, 2, 256, 256, scoring_func="sqrtsoftplus", norm_topk_prob=True,
+                    routed_scaling_factor=1.5, hidden_act="silu", swiglu_limit=LIMIT)
+    base = _layer(gpu, 128, seed=23 * N, gated=False)
+    g = torch.Generator(device="cpu").manual_seed(N)
+    base["e_score_correction_bias"] = (torch.randn(8, generator=g) * 0.05).to(gpu)
+    p = _with_awq(base, gpu, seed=29 * N)
+    x = _inputs(gpu, N, 512, N)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=2, inter=256, scoring="sqrtsoftplus",
+                           norm_topk=True, scale=1.5, act="silu", limit=LIMIT, group_size=128)
+    assert_close(f64(y), it["y_exact"], f"dsv4 N={N}")
 
 
 def test_awq_batch_invariance(gpu):

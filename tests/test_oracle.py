@@ -606,3 +606,23 @@ def test_mixed_proj_widths_and_slots():
     e2 = rng.integers(0, 2, 5)
     assert np.array_equal(om.mixed_proj(x[:5], e2, uni, "gate", K),
                           om.gather_qmm(x[:5], e2, *stacks[4], K, group_size=gs, bits=4))
+
+
+def test_route_sqrtsoftplus_matches_torch_softplus():
+    """DeepSeek-V4's scores sqrt(softplus(logits)) against torch's softplus, and the selection
+    on score + bias with the bias-free, renormalised, scaled weights (src/quanta/dsv4/moe.py:37-57),
+    including large logits where log(1 + e^l) must not overflow."""
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((7, 64))
+    wr = rng.standard_normal((32, 64)) * 0.3
+    wr[3] *= 400.0                      # logits of several hundred for expert 3
+    bias = rng.standard_normal(32) * 0.1
+    idx, w, logits, scores, choice = om.route(x, wr, k=4, scoring="sqrtsoftplus", bias=bias, scale=1.5)
+    want = torch.sqrt(torch.nn.functional.softplus(torch.from_numpy(logits))).numpy()
+    assert np.all(np.isfinite(scores))
+    assert np.allclose(scores, want, rtol=1e-12, atol=0)
+    for r in range(7):
+        order = sorted(range(32), key=lambda e: (-(scores[r, e] + bias[e]), e))[:4]
+        assert list(idx[r]) == order
+        sel = scores[r, order]
+        assert np.allclose(w[r], sel / (sel.sum() + 1e-20) * 1.5, rtol=1e-14)
