@@ -147,6 +147,9 @@ int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16
 #define QMOE_PROJ_GATE 0
 #define QMOE_PROJ_UP 1
 #define QMOE_PROJ_DOWN 2
+#define QMOE_PROJ_GATE_UP 3   /* gate and up fused per width ([E_w, 2I, H], gate rows first), when
+                                 every expert's gate and up share width and slot; then no GATE or
+                                 UP stacks */
 #define QMOE_MAX_STACKS 12
 typedef struct {
   int32_t proj;                /* QMOE_PROJ_* */
@@ -156,7 +159,7 @@ typedef struct {
   const int32_t* expert_slot;  /* [E] device: the expert's slot in this stack, or -1 */
 } qmoe_stack_t;
 typedef struct {
-  int32_t n_stacks;            /* 3 .. QMOE_MAX_STACKS, every projection at least once */
+  int32_t n_stacks;            /* 2 .. QMOE_MAX_STACKS, every projection at least once */
   qmoe_stack_t stacks[QMOE_MAX_STACKS];
 } qmoe_mixed_t;
 

@@ -72,7 +72,7 @@ class QmoeWeights(ctypes.Structure):
     ]
 
 
-PROJ_GATE, PROJ_UP, PROJ_DOWN = 0, 1, 2
+PROJ_GATE, PROJ_UP, PROJ_DOWN, PROJ_GATE_UP = 0, 1, 2, 3
 MAX_STACKS = 12
 
 

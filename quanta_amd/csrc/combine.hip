@@ -370,19 +370,28 @@ static bool narrow_codes(const qmoe_config_t& c) {
          c.down_format == QMOE_FMT_INT6_G64 || c.down_format == QMOE_FMT_INT3_G64;
 }
 
+static bool has_split(const qmoe_mixed_t& m) {
+  for (int i = 0; i < m.n_stacks; ++i)
+    if (m.stacks[i].proj == QMOE_PROJ_GATE || m.stacks[i].proj == QMOE_PROJ_UP) return true;
+  return false;
+}
+
 static int validate_mixed(const qmoe_mixed_t& m) {
-  if (m.n_stacks < 3 || m.n_stacks > QMOE_MAX_STACKS)
-    return fail("mixed: 3 <= n_stacks <= QMOE_MAX_STACKS required");
-  int seen[3] = {0, 0, 0};
+  if (m.n_stacks < 2 || m.n_stacks > QMOE_MAX_STACKS)
+    return fail("mixed: 2 <= n_stacks <= QMOE_MAX_STACKS required");
+  int seen[4] = {0, 0, 0, 0};
   for (int i = 0; i < m.n_stacks; ++i) {
     const qmoe_stack_t& st = m.stacks[i];
-    if (st.proj < QMOE_PROJ_GATE || st.proj > QMOE_PROJ_DOWN) return fail("mixed: unknown proj");
+    if (st.proj < QMOE_PROJ_GATE || st.proj > QMOE_PROJ_GATE_UP) return fail("mixed: unknown proj");
     if (st.format != QMOE_FMT_INT4_G64 && st.format != QMOE_FMT_INT6_G64 && st.format != QMOE_FMT_INT3_G64)
       return fail("mixed: stack formats must be int3, int4 or int6");
     if (!st.codes || !st.sb || !st.expert_slot) return fail("mixed: null stack pointer");
     seen[st.proj] = 1;
   }
-  if (!seen[0] || !seen[1] || !seen[2]) return fail("mixed: every projection needs a stack");
+  const bool split = seen[QMOE_PROJ_GATE] || seen[QMOE_PROJ_UP];
+  if (!seen[QMOE_PROJ_DOWN] || (split ? (!seen[QMOE_PROJ_GATE] || !seen[QMOE_PROJ_UP] || seen[QMOE_PROJ_GATE_UP])
+                                      : !seen[QMOE_PROJ_GATE_UP]))
+    return fail("mixed: every projection needs a stack (gate and up, or fused gate_up)");
   return 0;
 }
 
@@ -710,12 +719,26 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     return launch_qmm(a, fmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
   };
   // 5. routed gate_up + SwiGLU -> h (sorted order)
-  if (mixed) {
+  if (mixed && !has_split(*mixed)) {
+    // fused gate_up stacks by width: SwiGLU in the epilogue, straight into h
+    for (int i = 0; i < mixed->n_stacks; ++i) {
+      const qmoe_stack_t& st = mixed->stacks[i];
+      if (st.proj != QMOE_PROJ_GATE_UP) continue;
+      QmmArgs a{};
+      a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
+      a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
+      a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = st.codes; a.sb = st.sb;
+      a.expert_map = st.expert_slot; a.out = h; a.ld_out = c.inter;
+      a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
+      rc = routed(a, kernel_fmt(st.format), EPI_SWIGLU, nullptr, nullptr);
+      if (rc) return rc;
+    }
+  } else if (mixed) {
     // widths per (expert, projection): gate and up by width into awq_gu, then h = bf16(glu)
     uint16_t* gu = reinterpret_cast<uint16_t*>(base + L.awq_gu);
     for (int i = 0; i < mixed->n_stacks; ++i) {
       const qmoe_stack_t& st = mixed->stacks[i];
-      if (st.proj == QMOE_PROJ_DOWN) continue;
+      if (st.proj != QMOE_PROJ_GATE && st.proj != QMOE_PROJ_UP) continue;
       QmmArgs a{};
       a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
       a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;

@@ -133,7 +133,8 @@ _SCORING = {"softmax": L.SCORE_SOFTMAX, "sigmoid": L.SCORE_SIGMOID, "sqrtsoftplu
 class MixedExperts(dict):
     """Routed experts whose widths vary per (expert, projection), resident: "stacks" is a list of
     (projection, TiledExperts, expert map [E] int32 on the device: the expert's slot in that
-    stack or -1), "n_experts" E. Built by tile_experts_mixed."""
+    stack or -1), "n_experts" E; projection "gate_up" when gate and up are fused per width.
+    Built by tile_experts_mixed."""
 
 
 def tile_experts_mixed(stacks: dict, pbits: dict, pslot: dict, *, group_size: int = 128) -> MixedExperts:
@@ -146,7 +147,20 @@ def tile_experts_mixed(stacks: dict, pbits: dict, pslot: dict, *, group_size: in
     if isinstance(stacks, MixedExperts):
         return stacks
     out, E = [], None
-    for proj in PROJS:
+    # every expert's gate and up of one width and slot: fuse them per width (gate rows first),
+    # so gate_up runs as the uniform stacks do, SwiGLU in the matmul's epilogue
+    host = lambda v: torch.as_tensor(v).to("cpu", torch.int64).reshape(-1)
+    fuse = (torch.equal(host(pbits["gate"]), host(pbits["up"])) and
+            torch.equal(host(pslot["gate"]), host(pslot["up"])) and
+            all(stacks["gate"][b]["packed"].shape == stacks["up"][b]["packed"].shape
+                for b in stacks["gate"] if b in stacks["up"]) and
+            set(stacks["gate"]) == set(stacks["up"]))
+    if fuse:
+        stacks = dict(stacks, gate_up={b: {key: torch.cat([stacks["gate"][b][key], stacks["up"][b][key]], dim=1)
+                                           for key in ("packed", "scale", "bias")}
+                                       for b in stacks["gate"]})
+        pbits, pslot = dict(pbits, gate_up=pbits["gate"]), dict(pslot, gate_up=pslot["gate"])
+    for proj in (("gate_up", "down") if fuse else PROJS):
         pb = torch.as_tensor(pbits[proj]).to("cpu", torch.int64).reshape(-1)
         ps = torch.as_tensor(pslot[proj]).to("cpu", torch.int64).reshape(-1)
         if E is None:
@@ -399,12 +413,13 @@ def _prepare_mixed(p: dict, cfg, *, topk, regime) -> Prepared:
     m = L.QmoeMixed()
     m.n_stacks = len(mx["stacks"])
     fmts = {"int4_g64": L.FMT_INT4_G64, "int6_g64": L.FMT_INT6_G64, "int3_g64": L.FMT_INT3_G64}
+    proj_id = {"gate": L.PROJ_GATE, "up": L.PROJ_UP, "down": L.PROJ_DOWN, "gate_up": L.PROJ_GATE_UP}
     for i, (proj, te, emap) in enumerate(mx["stacks"]):
-        want = (I, H) if proj != "down" else (H, I)
+        want = {"down": (H, I), "gate_up": (2 * I, H)}.get(proj, (I, H))
         if tuple(te["shape"][1:]) != want:
             raise ValueError(f"mixed experts: {proj} stacks must be [E_w, {want[0]}, {want[1]}] "
                              f"(got {tuple(te['shape'])})")
-        m.stacks[i] = L.QmoeStack(PROJS.index(proj), fmts[te["format"]], te["codes"].data_ptr(),
+        m.stacks[i] = L.QmoeStack(proj_id[proj], fmts[te["format"]], te["codes"].data_ptr(),
                                   te["sb"].data_ptr(), emap.data_ptr())
     # the rest of the block: a placeholder uniform stack pair supplies nothing but the shapes
     q = {kk: v for kk, v in p.items() if kk != "experts_mixed"}

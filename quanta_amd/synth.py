@@ -98,17 +98,19 @@ def _quantized_stack(E, rows, K, g, device, chunk_elems=1 << 28, bits=4, group_s
 
 def make_mixed_experts(name: str, *, device="cuda", seed: int = 0, choices=(3, 4),
                        group_size: int = 128) -> dict:
-    """Routed experts of widths drawn per (expert, projection) from `choices` (Kimi's
-    per-projection bake, src/quanta/modeling/quantized.py:40-51), as the reference's
+    """Routed experts of widths drawn per expert from `choices`, one draw for gate and up
+    together and one for down (Kimi's per-projection bake, src/quanta/modeling/quantized.py:
+    40-51, whose canonical split is gate/up int3 + down int4), as the reference's
     (stacks, pbits, pslot): one stack per (projection, width), experts in id order."""
     c = SPECS[name].cfg
     E, H, I = c.num_experts, c.hidden_size, c.moe_intermediate_size
     g = _gen(device, seed * 1009 + 7)
     rng = np.random.default_rng(seed)
     stacks, pbits, pslot = {}, {}, {}
+    pb_gu = rng.choice(np.asarray(choices), E)
     for proj in ("gate", "up", "down"):
         rows, K = (I, H) if proj != "down" else (H, I)
-        pb = rng.choice(np.asarray(choices), E)
+        pb = pb_gu if proj != "down" else rng.choice(np.asarray(choices), E)
         ps = np.zeros(E, np.int64)
         stacks[proj] = {}
         for b in sorted(set(pb.tolist())):
