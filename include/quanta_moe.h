@@ -163,9 +163,11 @@ typedef struct {
   qmoe_stack_t stacks[QMOE_MAX_STACKS];
 } qmoe_mixed_t;
 
-/* qmoe_forward with the routed experts of mixed (cfg->mixed = 1); workspace as
- * qmoe_forward_workspace. No counterpart beyond QuantizedSparseMoE.__call__ (quantized.py:68-84):
- * gate and up by width into one [N*k, 2I] buffer, h = bf16(silu(g) * u), down by width. */
+/* qmoe_forward with the routed experts of mixed widths (cfg->mixed = 1); workspace as
+ * qmoe_forward_workspace. Replaces QuantizedSparseMoE.__call__ (src/quanta/modeling/
+ * quantized.py:68-84): gate and up by width (fused per width with the SwiGLU epilogue when a
+ * QMOE_PROJ_GATE_UP stack holds them, else into one [N*k, 2I] buffer and h = bf16(silu(g) * u)),
+ * then down by width. */
 int qmoe_forward_mixed(const qmoe_config_t* cfg, const qmoe_weights_t* w, const qmoe_mixed_t* mixed,
                        const uint16_t* x, int64_t N, uint16_t* y, void* ws, size_t ws_bytes,
                        void* stream);
