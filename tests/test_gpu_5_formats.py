@@ -294,3 +294,24 @@ def test_narrow_formats_batch_invariance_full_size(gpu, fmt):
     for t in (0, N // 3, N - 1):
         single = qwen35_moe(x[t:t + 1][None], p, cfg)[0, 0]
         assert torch.equal(single, full[t]), f"token {t} of {N}"
+
+
+# ------------------------------------------------------------------------------ edge sizes
+@pytest.mark.parametrize("E,k,N", [(1024, 16, 2), (64, 64, 3), (16, 16, 5), (1024, 8, 300)])
+def test_block_router_limits_vs_oracle(gpu, E, k, N):
+    """The router's limits through the whole block: the largest expert count (1024), the
+    largest top-k (64), k = E (every expert on every token), at decode and prefill sizes."""
+    cfg = MoEConfig(256, E, k, 128, 128)
+    p = _layer(gpu, 64, seed=E + k + N, H=256, E=E, I=128, Is=128)
+    x = _inputs(gpu, N, 256, N)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=k, inter=128)
+    assert_close(f64(y), it["y_exact"], f"E={E} k={k} N={N}")
+
+
+def test_block_empty_input(gpu):
+    cfg = MoEConfig(512, 8, 2, 256, 256)
+    p = _layer(gpu, 64, seed=2)
+    x = torch.empty(1, 0, 512, dtype=torch.bfloat16, device=gpu)
+    y = qwen35_moe(x, p, cfg)
+    assert y.shape == (1, 0, 512) and y.dtype == torch.bfloat16
