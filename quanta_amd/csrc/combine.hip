@@ -268,7 +268,8 @@ int validate_routing(int N, int H, int E, int k, int scoring, int n_group, int t
 // cannot exchange the events.
 struct AuxStream {
   hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr, perm = nullptr, cold = nullptr, hready = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr, perm = nullptr, cold = nullptr, hready = nullptr,
+             xready = nullptr;
 };
 static std::mutex g_aux_mu;
 constexpr int64_t kFuseSharedMaxTokens = 64;
@@ -291,6 +292,7 @@ static int aux_stream(hipStream_t caller, AuxStream** out) {
     if (err == hipSuccess) err = hipEventCreateWithFlags(&a.perm, hipEventDisableTiming);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&a.cold, hipEventDisableTiming);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&a.hready, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&a.xready, hipEventDisableTiming);
     if (cur != dev) (void)hipSetDevice(cur);
     if (err != hipSuccess) {
       a = AuxStream{};
@@ -635,6 +637,15 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (rc) return rc;
     if (shared_aux) sstream = aux->s;
   }
+  // hybrid prefill with int4 experts: the hot experts' gate_up reads an fp16 copy of x, made
+  // first on the auxiliary stream, beside the routing chain (hybrid implies int4 or bf16 experts)
+  const bool f16_acts = (hybrid && gfmt == FMT_INT4);
+  if (f16_acts) {
+    rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, aux->s);
+    if (rc) return rc;
+    const hipError_t err = hipEventRecord(aux->xready, aux->s);
+    if (err != hipSuccess) return fail(std::string("forward: x16 record: ") + hipGetErrorString(err));
+  }
 
   // 1. shared expert gate_up + SwiGLU -> sh_h (fused with the router below when decoding)
   const int st = decode ? kSmallMTile : kLargeMTile;
@@ -698,7 +709,6 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                         hybrid ? tile_map_big : nullptr, L.max_tiles_big);
     if (rc) return rc;
   }
-  const bool f16_acts = (hybrid && gfmt == FMT_INT4);   // hybrid implies int4 or bf16 experts
   // the cold experts' tiles wait for the permute on the auxiliary stream
   hipStream_t cstream = stream;
   if (hybrid) {
@@ -778,9 +788,9 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
     a.out = h; a.ld_out = c.inter;
     a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
-    if (f16_acts) {
-      rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, stream);
-      if (rc) return rc;
+    if (f16_acts) {   // the fp16 copy of x, made on the auxiliary stream at the fork
+      const hipError_t err = hipStreamWaitEvent(stream, aux->xready, 0);
+      if (err != hipSuccess) return fail(std::string("forward: x16 wait: ") + hipGetErrorString(err));
     }
     rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
     if (rc) return rc;
