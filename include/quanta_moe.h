@@ -43,6 +43,17 @@ extern "C" {
 #define QMOE_SCORE_SIGMOID 1
 #define QMOE_SCORE_SQRTSOFTPLUS 2   /* DeepSeek-V4: sqrt(softplus(logit)), src/quanta/dsv4/moe.py:37-57 */
 
+/* renormalisation of the k routing weights, w /= sum(w) + 1e-20 (the config's norm_topk):
+ *  NONE    never
+ *  ALWAYS  whenever set, k = 1 included (qwen35_route, src/quanta/qwen35/moe.py:53-54; DeepSeek-V4
+ *          renormalises its non-softmax scores unconditionally, src/quanta/dsv4/moe.py:54-55)
+ *  MULTI   only when k > 1 (the sigmoid + correction-bias MoEGate routers,
+ *          src/quanta/modeling/moe.py:41-42, src/quanta/glm/moe.py:53-54,
+ *          src/quanta/minimax/moe.py:54-55: a single expert keeps its score) */
+#define QMOE_NORM_NONE 0
+#define QMOE_NORM_ALWAYS 1
+#define QMOE_NORM_MULTI 2
+
 /* expert weight formats, both in this library's MFMA-tiled layout (see qmoe_tile_*) */
 #define QMOE_FMT_INT4_G64 0
 #define QMOE_FMT_BF16 1
@@ -87,7 +98,7 @@ typedef struct {
   int32_t inter;         /* I, multiple of 128 */
   int32_t shared_inter;  /* Is, 0 = no shared expert, else multiple of 128 */
   int32_t scoring;       /* QMOE_SCORE_* */
-  int32_t norm_topk;     /* renormalise the k weights: w /= sum(w) + 1e-20 */
+  int32_t norm_topk;     /* QMOE_NORM_*: renormalise the k weights, w /= sum(w) + 1e-20 */
   int32_t n_group;       /* expert groups (1 = plain top-k) */
   int32_t topk_group;    /* groups kept when n_group > 1 */
   float routed_scale;    /* routed_scaling_factor applied after renormalisation */
@@ -194,7 +205,7 @@ int qmoe_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float e
 
 /* Top-k selection from router logits [N, ld_logits] (fp32): softmax or sigmoid scores,
  * optional correction bias [E] for selection, group-limited selection when n_group > 1,
- * renormalisation (+1e-20) and routed_scale. Outputs idx[N,k] (int32, canonical order:
+ * renormalisation (norm_topk: QMOE_NORM_*, +1e-20) and routed_scale. Outputs idx[N,k] (int32, canonical order:
  * choice value descending, id ascending) and w[N,k] (fp32). With has_shared_gate, column E
  * holds the shared-gate logit and shared_gate_out[N] = sigmoid(logit).
  * Replaces qwen35_route (src/quanta/qwen35/moe.py:36-56) and MoEGate.__call__

@@ -86,7 +86,7 @@ def group_limit(choice: np.ndarray, n_group: int, topk_group: int) -> np.ndarray
 
 def route(x: np.ndarray, wr: np.ndarray, *, k: int, scoring: str = "softmax",
           norm_topk: bool = True, bias: np.ndarray | None = None, n_group: int = 1,
-          topk_group: int = 1, scale: float = 1.0):
+          topk_group: int = 1, scale: float = 1.0, norm_single: bool = True):
     """Router -> (idx [N,k] int32, w [N,k] float64, logits, scores).
 
     softmax (`src/quanta/qwen35/moe.py:47-55`): logits = x . Wr^T in float (here float64),
@@ -97,6 +97,10 @@ def route(x: np.ndarray, wr: np.ndarray, *, k: int, scoring: str = "softmax",
     the bias-free scores, renormalised, then times `scale` (routed_scaling_factor).
     sqrtsoftplus (DeepSeek-V4, `src/quanta/dsv4/moe.py:37-57`): scores = sqrt(log(1 + e^logits)),
     then as sigmoid.
+    Renormalisation at k = 1: qwen35_route divides a single weight by itself too
+    (`src/quanta/qwen35/moe.py:53-54`, norm_single=True); the MoEGate routers keep a single
+    expert's score (`topk > 1 and norm_topk_prob`, `src/quanta/modeling/moe.py:41`,
+    `src/quanta/glm/moe.py:53`, norm_single=False).
     """
     logits = x.astype(np.float64) @ wr.astype(np.float64).T
     if scoring == "softmax":
@@ -114,7 +118,7 @@ def route(x: np.ndarray, wr: np.ndarray, *, k: int, scoring: str = "softmax",
         choice = group_limit(choice, n_group, topk_group)
     idx = topk_canonical(choice, k)
     w = np.take_along_axis(scores, idx, axis=-1)
-    if norm_topk:
+    if norm_topk and (k > 1 or norm_single):
         w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
     w = w * scale
     return idx.astype(np.int32), w, logits, scores, choice
@@ -250,18 +254,20 @@ def mixed_proj(xrows: np.ndarray, exp: np.ndarray, m: dict, proj: str, in_featur
     """One projection over routed rows whose experts have per-(expert, projection) widths
     (`src/quanta/modeling/quantized.py:53-66`): row r uses expert e = exp[r]'s width
     b = pbits[proj][e] and its slot pslot[proj][e] in the width-b stack; y = bf16(x . W^T).
-    `m`: {"stacks": {proj: {bits: (packed, scale, bias)}}, "pbits": {proj: [E]},
-    "pslot": {proj: [E]}, "group_size": g}."""
+    `m`: {"stacks": {proj: {bits: (packed, scale, bias[, group_size])}}, "pbits": {proj: [E]},
+    "pslot": {proj: [E]}, "group_size": g}; a stack's own group size, when given, overrides g."""
     exp = np.asarray(exp).reshape(-1)
     pb = np.asarray(m["pbits"][proj])[exp]
     ps = np.asarray(m["pslot"][proj])[exp]
     out = None
-    for bits, (packed, scale, bias) in sorted(m["stacks"][proj].items()):
+    for bits, st in sorted(m["stacks"][proj].items()):
+        packed, scale, bias = st[:3]
+        gs = st[3] if len(st) > 3 else m["group_size"]
         sel = pb == bits
         if not sel.any():
             continue
         o = gather_qmm(xrows[sel], ps[sel], packed, scale, bias, in_features,
-                       group_size=m["group_size"], bits=bits)
+                       group_size=gs, bits=bits)
         if out is None:
             out = np.zeros((exp.size, o.shape[1]))
         out[sel] = o
@@ -299,7 +305,7 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
                 norm_topk: bool = True, n_group: int = 1, topk_group: int = 1,
                 scale: float = 1.0, round_weights: bool = False, act: str = "silu",
                 alpha: float = 1.702, limit: float = 0.0, group_size: int = 64, bits: int = 4,
-                down_bits: int | None = None):
+                down_bits: int | None = None, norm_single: bool = True):
     """Whole block y = bf16(routed + shared) for x [N, H] (`src/quanta/qwen35/moe.py:154-202`).
 
     `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
@@ -315,7 +321,7 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
     idx, w, logits, scores, choice = route(
         x, p["gate"], k=k, scoring=scoring, norm_topk=norm_topk,
         bias=p.get("e_score_correction_bias"), n_group=n_group, topk_group=topk_group,
-        scale=scale)
+        scale=scale, norm_single=norm_single)
     exp = idx.reshape(-1)
     tok = np.repeat(np.arange(n), k)
     if p.get("mixed") is not None:

@@ -43,7 +43,10 @@ def route(x: torch.Tensor, gate: torch.Tensor, cfg, k: int, bias=None):
         choice = choice.masked_fill(~mask, float("-inf"))
     idx = choice.topk(k, dim=-1).indices
     w = scores.gather(1, idx)
-    if cfg.norm_topk_prob:
+    # a sigmoid + correction-bias router (MoEGate) keeps a single expert's score
+    # (src/quanta/modeling/moe.py:41); qwen35_route renormalises it too (moe.py:53-54)
+    moegate = cfg.scoring_func == "sigmoid" and bias is not None
+    if cfg.norm_topk_prob and (k > 1 or not moegate):
         w = w / (w.sum(-1, keepdim=True) + 1e-20)
     return idx, w * cfg.routed_scaling_factor
 

@@ -16,6 +16,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "quanta_moe.h"
 
 QMOE_OK, QMOE_EINVAL, QMOE_EHIP = 0, -1, -2
 SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
+NORM_NONE, NORM_ALWAYS, NORM_MULTI = 0, 1, 2
 FMT_INT4_G64, FMT_BF16, FMT_INT6_G64, FMT_INT3_G64 = 0, 1, 2, 3
 ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
 REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2

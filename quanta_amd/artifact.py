@@ -85,60 +85,100 @@ class _Shard:
         return t.view(tdt) if tdt is not None else t
 
 
+class _Manifest:
+    """What an artifact directory declares, indexed once when it is opened.
+
+    The writer (src/quanta/bake/artifact.py:51-77) stores a dense tensor verbatim under its own
+    key and records {"format": "dense"} at that key; it stores a quantized weight as three tensors
+    `<stem>.weight_packed/_scale/_bias` and records {"format": "affine_packed", bits,
+    group_size} at the stem, the weight's key without its ".weight" suffix. A reader therefore
+    resolves a weight key by this rule (the one Qwen35Artifact applies,
+    src/quanta/qwen35/artifact.py:77-94):
+      1. a dense record at the key itself wins;
+      2. else an affine_packed record at the stem;
+      3. a record at either place in any other format is an error (ValueError): decoding it at a
+         guessed width would be silently wrong;
+      4. no record at all is a missing weight (KeyError).
+    """
+
+    def __init__(self, root: Path) -> None:
+        index = json.loads((root / "model.safetensors.index.json").read_text())
+        self.shard_of: dict[str, str] = dict(index["weight_map"])
+        doc = json.loads((root / "manifest.json").read_text())
+        if doc.get("format") != "quanta":
+            raise ValueError(f"{root}: manifest.json declares format={doc.get('format')!r}, so this is not a quanta artifact")
+        self.entries: dict[str, dict] = doc["tensors"]
+        self.dense = {k for k, e in self.entries.items() if e.get("format") == "dense"}
+        self.packed = {k: (int(e["bits"]), int(e["group_size"]))
+                       for k, e in self.entries.items() if e.get("format") == "affine_packed"}
+
+    @staticmethod
+    def stem(key: str) -> str:
+        return key[:-len(_WEIGHT_SUFFIX)] if key.endswith(_WEIGHT_SUFFIX) else key
+
+    def resolve(self, key: str) -> tuple[str, str]:
+        """A weight key -> (stored key, "dense" | "affine_packed"), by the rule above."""
+        if key in self.dense:
+            return key, "dense"
+        stem = self.stem(key)
+        if stem in self.packed:
+            return stem, "affine_packed"
+        for where in (key, stem):
+            if where in self.entries:
+                raise ValueError(f"{where}: unknown manifest format "
+                                 f"{self.entries[where].get('format')!r} (a reader decodes dense "
+                                 "and affine_packed records only)")
+        raise KeyError(f"{key}: the manifest records neither a dense tensor at this key nor an "
+                       f"affine_packed weight at {stem!r}")
+
+
 class QuantaArtifact:
-    """Lazy reader over a quanta artifact directory (src/quanta/qwen35/artifact.py:38-50)."""
+    """Lazy reader over a quanta artifact directory: the manifest indexed at open time, each
+    shard mapped on first use (the reference's reader: src/quanta/qwen35/artifact.py:38-123)."""
 
     def __init__(self, art_dir: str | Path) -> None:
         self.dir = Path(art_dir)
-        self.weight_map: dict[str, str] = json.loads(
-            (self.dir / "model.safetensors.index.json").read_text())["weight_map"]
-        man = json.loads((self.dir / "manifest.json").read_text())
-        if man.get("format") != "quanta":
-            raise ValueError(f"{self.dir}: not a quanta artifact (format={man.get('format')!r})")
-        self.manifest: dict[str, dict] = man["tensors"]
-        cfg_path = self.dir / "config.json"
-        self.config: dict = json.loads(cfg_path.read_text()) if cfg_path.exists() else {}
-        self._shards: dict[str, _Shard] = {}
+        self._man = _Manifest(self.dir)
+        cfg_file = self.dir / "config.json"
+        self.config: dict = json.loads(cfg_file.read_text()) if cfg_file.exists() else {}
+        self._open: dict[str, _Shard] = {}
+
+    @property
+    def weight_map(self) -> dict[str, str]:
+        """Stored tensor name -> shard file (the index's weight_map)."""
+        return self._man.shard_of
+
+    @property
+    def manifest(self) -> dict[str, dict]:
+        """Manifest records by key."""
+        return self._man.entries
+
+    @property
+    def _shards(self) -> dict[str, _Shard]:
+        return self._open
 
     # --- tensors --------------------------------------------------------------------------
     def get(self, name: str) -> torch.Tensor:
-        """One tensor verbatim by its exact key, as a host view of the mapped shard
-        (src/quanta/qwen35/artifact.py:54-63)."""
-        if name not in self.weight_map:
-            raise KeyError(f"tensor not in artifact index: {name}")
-        fn = self.weight_map[name]
-        shard = self._shards.get(fn)
-        if shard is None:
-            shard = self._shards[fn] = _Shard(self.dir / fn)
-        return shard.tensor(name)
+        """The stored tensor `name` (exact key) as a host view of its mapped shard."""
+        fn = self._man.shard_of.get(name)
+        if fn is None:
+            raise KeyError(f"{name}: no such tensor in the artifact index")
+        if fn not in self._open:
+            self._open[fn] = _Shard(self.dir / fn)
+        return self._open[fn].tensor(name)
 
     def has(self, key: str) -> bool:
-        """True iff a logical key resolves: a dense entry, or a quantized base
-        (src/quanta/qwen35/artifact.py:65-70)."""
-        if key in self.weight_map:
-            return True
-        base = key[:-len(_WEIGHT_SUFFIX)] if key.endswith(_WEIGHT_SUFFIX) else key
-        return self.manifest.get(base, {}).get("format") == "affine_packed"
+        """Whether a weight key is stored verbatim or resolves to an affine_packed weight."""
+        return key in self._man.shard_of or self._man.stem(key) in self._man.packed
 
     def release(self) -> None:
-        """Drop the shard mappings (src/quanta/qwen35/artifact.py:72-74)."""
-        self._shards.clear()
+        """Unmap every shard; tensors already copied elsewhere are unaffected."""
+        self._open = {}
 
     def _meta(self, key: str) -> tuple[str, dict]:
-        """A logical key -> (base, manifest entry): a dense entry at the full key, else the
-        affine_packed base (the key without a trailing `.weight`)
-        (src/quanta/qwen35/artifact.py:77-94)."""
-        meta = self.manifest.get(key)
-        if meta is not None and meta.get("format") == "dense":
-            return key, meta
-        base = key[:-len(_WEIGHT_SUFFIX)] if key.endswith(_WEIGHT_SUFFIX) else key
-        bmeta = self.manifest.get(base)
-        if bmeta is not None and bmeta.get("format") == "affine_packed":
-            return base, bmeta
-        for cand, cmeta in ((key, meta), (base, bmeta)):
-            if cmeta is not None:
-                raise ValueError(f"{cand}: unknown manifest format {cmeta.get('format')!r}")
-        raise KeyError(f"{key}: not in artifact manifest (no dense entry, no quantized base {base!r})")
+        """(stored key, manifest record) of a weight key; see _Manifest.resolve."""
+        where, _ = self._man.resolve(key)
+        return where, self._man.entries[where]
 
     def read(self, key: str, device: torch.device | str) -> torch.Tensor:
         """A bf16 weight on `device` for a logical key: a dense tensor cast to bf16, or an
@@ -181,6 +221,11 @@ class QuantaArtifact:
             "experts_gate_up": self.packed_triplet(p + "experts.gate_up_proj", device),
             "experts_down": self.packed_triplet(p + "experts.down_proj", device),
         }
+        # a sigmoid router's selection bias, where the bake stores one (the HF key of the
+        # DeepSeek/GLM gates, src/quanta/loader.py:50)
+        if self.has(p + "gate.e_score_correction_bias"):
+            out["e_score_correction_bias"] = self.get(p + "gate.e_score_correction_bias").to(
+                device).to(torch.float32)
         if self.has(p + "shared_expert.gate_proj.weight"):
             for proj in SHARED_EXPERT_PROJS:
                 out[f"shared_{proj}"] = self.read(p + f"shared_expert.{proj}.weight", device)
@@ -190,14 +235,24 @@ class QuantaArtifact:
 
     def moe_config(self) -> MoEConfig:
         """The MoE fields of the artifact's config.json (`text_config` when nested), with the
-        reference's defaults (src/quanta/qwen35/config.py:340-364)."""
+        reference's defaults (src/quanta/qwen35/config.py:340-364): the router's scoring_func
+        (:361, softmax unless stated) and, where present, the DeepSeek/GLM router fields n_group,
+        topk_group and routed_scaling_factor (src/quanta/glm/config.py:65-69)."""
         tc = self.config.get("text_config", self.config)
+        scoring = str(tc.get("scoring_func", "softmax"))
+        if scoring not in ("softmax", "sigmoid"):
+            raise ValueError(f"config.json: scoring_func {scoring!r} is not a Qwen3.5 router "
+                             "(softmax | sigmoid)")
         return MoEConfig(
             hidden_size=int(tc["hidden_size"]),
             num_experts=int(tc["num_experts"]),
             num_experts_per_tok=int(tc["num_experts_per_tok"]),
             moe_intermediate_size=int(tc["moe_intermediate_size"]),
             shared_expert_intermediate_size=int(tc.get("shared_expert_intermediate_size", 0)),
+            scoring_func=scoring,
+            n_group=int(tc.get("n_group", 1) or 1),
+            topk_group=int(tc.get("topk_group", 1) or 1),
+            routed_scaling_factor=float(tc.get("routed_scaling_factor", 1.0) or 1.0),
             norm_topk_prob=bool(tc.get("norm_topk_prob", True)),
             norm_eps=float(tc.get("rms_norm_eps", 1e-6)),
             hidden_act=str(tc.get("hidden_act", "silu")),
@@ -228,5 +283,7 @@ class QuantaArtifact:
                 m.shared_expert_gate.copy_(p["shared_expert_gate"])
             else:   # an ungated shared expert
                 m.shared_expert_gate = None
+        if "e_score_correction_bias" in p:
+            m.e_score_correction_bias = p["e_score_correction_bias"]
         m.set_experts_packed(p["experts_gate_up"], p["experts_down"])
         return m

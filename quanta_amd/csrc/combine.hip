@@ -327,8 +327,11 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.counts = take(static_cast<size_t>(c.n_experts) * 4);
   L.offsets = take(static_cast<size_t>(c.n_experts + 1) * 4);
   L.tile_off = take(static_cast<size_t>(c.n_experts + 1) * 4);
-  // tile descriptors for whichever m-tile the regime uses (16 needs the most entries)
+  // tile descriptors for whichever m-tile the regime uses (16 needs the most entries); the
+  // slot-major map of one or two tokens has one tile per slot, which can exceed that bound when
+  // k > E / 2
   L.max_tiles = mtile_upper_bound(mc, c.n_experts, kSmallMTile);
+  if (N <= kSlotMajorMaxTokens) L.max_tiles = std::max<int64_t>(L.max_tiles, mc);
   L.tile_map = take(static_cast<size_t>(L.max_tiles) * 16);
   // large-M regime: 128-row tiles of the experts above the hybrid split
   L.max_tiles_big = mtile_upper_bound(mc, c.n_experts, kLargeMTile);
@@ -402,6 +405,8 @@ static int validate_config(const qmoe_config_t& c) {
                                   c.topk_group);
   if (rc) return rc;
   if (c.hidden % 128) return fail("config: hidden % 128 == 0 required");
+  if (c.norm_topk < QMOE_NORM_NONE || c.norm_topk > QMOE_NORM_MULTI)
+    return fail("config: norm_topk must be QMOE_NORM_NONE, _ALWAYS or _MULTI");
   if (c.regime == QMOE_REGIME_LARGE && c.hidden % 256)
     return fail("config: the large-M regime needs hidden % 256 == 0");
   if (c.inter <= 0 || c.inter % 128) return fail("config: inter % 128 == 0 required");
@@ -620,6 +625,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // its own m-tile; an expert two tokens share is read twice, cheaper than the launch)
   // (AWQ prescaling finds each row's expert from the permute's segment offsets)
   const bool slot_major = !hybrid && N <= kSlotMajorMaxTokens && !c.awq;
+  // m-tiles of the small-kernel launches: one per slot when slot-major
+  const int64_t tiles_small = slot_major ? std::max<int64_t>(bound_small, mc) : bound_small;
   std::unique_lock<std::mutex> aux_lock;
   AuxStream* aux = nullptr;
   hipStream_t sstream = stream;
@@ -696,7 +703,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     // 3-4. top-k with the slot-major tile map
     rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
                      c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream,
-                     tile_map, bound_small, sorted, inv);
+                     tile_map, tiles_small, sorted, inv);
     if (rc) return rc;
   } else {
     // 3. top-k
@@ -721,7 +728,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // cold experts own disjoint rows of the output)
   auto routed = [&](QmmArgs a, int fmt, int epi, const uint16_t* act16, const float* sinv) {
     a.tile_map = reinterpret_cast<const int4*>(tile_map);
-    int r = launch_qmm(a, fmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : bound_small, cstream);
+    int r = launch_qmm(a, fmt, epi, QMOE_REGIME_SMALL, hybrid ? cold_bound : tiles_small, cstream);
     if (r || !hybrid) return r;
     a.tile_map = reinterpret_cast<const int4*>(tile_map_big);
     a.act16 = act16;

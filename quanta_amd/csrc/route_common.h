@@ -248,7 +248,9 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
     my_w = (lane == r) ? s_win : my_w;
   }
   const float tot = wave_sum_f32(lane < P.k ? my_w : 0.f);
-  if (P.norm_topk) my_w = my_w / (tot + 1e-20f);
+  // QMOE_NORM_ALWAYS, or QMOE_NORM_MULTI with more than one expert (a MoEGate keeps a single
+  // expert's score as it is)
+  if (P.norm_topk == 1 || (P.norm_topk == 2 && P.k > 1)) my_w = my_w / (tot + 1e-20f);
   out_id = my_id;
   out_w = my_w * P.scale;
 }

@@ -142,6 +142,8 @@ extern "C" int qmoe_router_topk(const float* logits, int64_t ld_logits, const fl
   int rc = validate_routing(static_cast<int>(N), 1, E, k, scoring, n_group, topk_group);
   if (rc) return rc;
   if (N > (int64_t(1) << 30)) return fail("qmoe_router_topk: N too large");
+  if (norm_topk < QMOE_NORM_NONE || norm_topk > QMOE_NORM_MULTI)
+    return fail("qmoe_router_topk: norm_topk must be QMOE_NORM_NONE, _ALWAYS or _MULTI");
   if (ld_logits < E + (has_shared_gate ? 1 : 0)) return fail("qmoe_router_topk: ld_logits too small");
   if (!logits || !idx || !w || (has_shared_gate && !shared_gate_out))
     return fail("qmoe_router_topk: null pointer");

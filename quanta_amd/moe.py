@@ -15,13 +15,13 @@ API; held directly by the module).
 
 from __future__ import annotations
 
-import collections
 import ctypes
 import math
 import weakref
 from dataclasses import dataclass
 
 import torch
+from torch.utils.weak import WeakIdKeyDictionary
 
 from quanta_amd import _lib as L
 from quanta_amd import ops
@@ -49,6 +49,9 @@ class MoEConfig:
     hidden_act: str = "silu"
     swiglu_alpha: float = 1.702
     swiglu_limit: float = 0.0
+    # renormalise a single routed expert's weight (k = 1) when norm_topk_prob is set; None picks
+    # the reference router's own rule (see norm_mode)
+    norm_topk_single: bool | None = None
 
     @property
     def moe_gate_up_out(self) -> int:
@@ -63,6 +66,25 @@ class MoEConfig:
 def _cfg(cfg, name, default=None):
     v = getattr(cfg, name, default)
     return default if v is None else v
+
+
+def norm_mode(cfg, scoring: str, has_bias: bool) -> int:
+    """QMOE_NORM_* mode of the router's renormalisation.
+
+    qwen35_route renormalises whenever norm_topk_prob is set, a single expert included
+    (src/quanta/qwen35/moe.py:53-54). The MoEGate routers, which select on sigmoid scores plus
+    e_score_correction_bias, renormalise only when more than one expert is kept
+    (src/quanta/modeling/moe.py:41-42, src/quanta/glm/moe.py:53-54, src/quanta/minimax/moe.py:54-55).
+    DeepSeek-V4 renormalises its sqrt-softplus scores whatever norm_topk_prob says
+    (src/quanta/dsv4/moe.py:54-55). `cfg.norm_topk_single`, when set, overrides the k = 1 rule."""
+    if scoring == "sqrtsoftplus":
+        return L.NORM_ALWAYS
+    if not bool(_cfg(cfg, "norm_topk_prob", True)):
+        return L.NORM_NONE
+    single = getattr(cfg, "norm_topk_single", None)
+    if single is None:
+        single = not (scoring == "sigmoid" and has_bias)
+    return L.NORM_ALWAYS if single else L.NORM_MULTI
 
 
 # ----------------------------------------------------------------------------------- tiled experts
@@ -150,14 +172,16 @@ def tile_experts_mixed(stacks: dict, pbits: dict, pslot: dict, *, group_size: in
     # every expert's gate and up of one width and slot: fuse them per width (gate rows first),
     # so gate_up runs as the uniform stacks do, SwiGLU in the matmul's epilogue
     host = lambda v: torch.as_tensor(v).to("cpu", torch.int64).reshape(-1)
-    fuse = (torch.equal(host(pbits["gate"]), host(pbits["up"])) and
+    gsz = lambda st: int(st.get("group_size", group_size))
+    fuse = (set(stacks["gate"]) == set(stacks["up"]) and
+            torch.equal(host(pbits["gate"]), host(pbits["up"])) and
             torch.equal(host(pslot["gate"]), host(pslot["up"])) and
-            all(stacks["gate"][b]["packed"].shape == stacks["up"][b]["packed"].shape
-                for b in stacks["gate"] if b in stacks["up"]) and
-            set(stacks["gate"]) == set(stacks["up"]))
+            all(stacks["gate"][b]["packed"].shape == stacks["up"][b]["packed"].shape and
+                gsz(stacks["gate"][b]) == gsz(stacks["up"][b]) for b in stacks["gate"]))
     if fuse:
-        stacks = dict(stacks, gate_up={b: {key: torch.cat([stacks["gate"][b][key], stacks["up"][b][key]], dim=1)
-                                           for key in ("packed", "scale", "bias")}
+        stacks = dict(stacks, gate_up={b: dict({key: torch.cat([stacks["gate"][b][key], stacks["up"][b][key]], dim=1)
+                                                for key in ("packed", "scale", "bias")},
+                                               group_size=gsz(stacks["gate"][b]))
                                        for b in stacks["gate"]})
         pbits, pslot = dict(pbits, gate_up=pbits["gate"]), dict(pslot, gate_up=pslot["gate"])
     for proj in (("gate_up", "down") if fuse else PROJS):
@@ -190,52 +214,101 @@ def _is_packed(v) -> bool:
     return isinstance(v, dict)
 
 
-# ----------------------------------------------------------------------------------- cache
+# ----------------------------------------------------------------------------------- resident forms
 
-_CACHE: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
-_CACHE_MAX = 64
-
-
-def _tkey(t):
-    if t is None:
-        return None
-    if isinstance(t, dict):   # tensors by identity/version, other fields (bits, group_size) by value
-        return tuple((k, _tkey(v) if isinstance(v, torch.Tensor) else repr(v))
-                     for k, v in sorted(t.items()))
-    return (t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device)
+# The resident (tiled) forms the kernels read are derived once per layer and memoised on the
+# caller's own tensors: each memo entry hangs off an "anchor" tensor of the layer (the router
+# gate, a native expert stack, the shared gate_proj) through a weak key, so it lives exactly as
+# long as the layer's weights do. There is no size limit to overflow at model scale (a 60-layer
+# decode loop hits on every call), and a dropped layer takes its entries with it. An entry is
+# reused only while every source it was built from is the same object at the same version.
+# (keyed by tensor identity: a plain WeakKeyDictionary would compare tensors with ==)
+_MEMO: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
 
 
-def _cached(kind: str, tensors: tuple, build):
-    """Memoise a weight preparation on the identity and version of its source tensors. Entries
-    hold weak references, so a freed source never matches a new tensor at the same address."""
-    key = (kind,) + tuple(_tkey(t) for t in tensors)
-    hit = _CACHE.get(key)
-    if hit is not None:
-        refs, value = hit
-        if all(r() is t for r, t in zip(refs, _flat(tensors))):
-            _CACHE.move_to_end(key)
-            return value
-    value = build()
-    for dead in [kk for kk, (refs, _) in _CACHE.items() if any(r() is None for r in refs)]:
-        del _CACHE[dead]
-    _CACHE[key] = (tuple(weakref.ref(t) for t in _flat(tensors)), value)
-    while len(_CACHE) > _CACHE_MAX:
-        _CACHE.popitem(last=False)
-    return value
-
-
-def _flat(tensors):
-    out = []
-    for t in tensors:
-        if isinstance(t, dict):
-            out.extend(v for k, v in sorted(t.items()) if isinstance(v, torch.Tensor))
-        elif t is not None:
-            out.append(t)
+def _leaves(o, out: list) -> list:
+    """Flatten a parameter value into identity leaves (tensors, arrays, resident forms) and value
+    leaves (keys, bits, group sizes, shapes)."""
+    if isinstance(o, (torch.Tensor, TiledExperts, MixedExperts)) or type(o).__name__ == "ndarray":
+        out.append(o)
+    elif isinstance(o, dict):
+        for k in sorted(o, key=str):
+            out.append(("k", str(k)))
+            _leaves(o[k], out)
+    elif isinstance(o, (list, tuple)):
+        out.append(("n", len(o)))
+        for v in o:
+            _leaves(v, out)
+    else:
+        out.append(("v", o))
     return out
 
 
+def _version(o) -> int:
+    return o._version if isinstance(o, torch.Tensor) else 0
+
+
+def _signature(sources) -> tuple:
+    sig = []
+    for leaf in _leaves(list(sources), []):
+        if isinstance(leaf, tuple):
+            sig.append(leaf)
+        else:
+            sig.append((weakref.ref(leaf), _version(leaf)))
+    return tuple(sig)
+
+
+def _matches(sig: tuple, sources) -> bool:
+    leaves = _leaves(list(sources), [])
+    if len(leaves) != len(sig):
+        return False
+    for leaf, want in zip(leaves, sig):
+        if isinstance(leaf, tuple):
+            if leaf != want:
+                return False
+        elif not (isinstance(want[0], weakref.ref) and want[0]() is leaf and want[1] == _version(leaf)):
+            return False
+    return True
+
+
+def _memo(anchor: torch.Tensor, kind, sources, build):
+    """The value `build()` derives from `sources`, memoised on `anchor` (a weak key). The value
+    must not hold `anchor` itself, or the entry would keep its own key alive."""
+    entries = _MEMO.get(anchor)
+    if entries is None:
+        entries = _MEMO[anchor] = {}
+    hit = entries.get(kind)
+    if hit is not None and _matches(hit[0], sources):
+        return hit[1]
+    value = build()
+    entries[kind] = (_signature(sources), value)
+    return value
+
+
 def clear_cache() -> None:
-    _CACHE.clear()
+    """Drop every memoised resident form (they are rebuilt on the next call)."""
+    _MEMO.clear()
+
+
+def resident_experts(v):
+    """The resident (tiled) form of an expert stack: a packed triplet dict or a bf16 [E, out, in]
+    stack, converted once (memoised on the native tensors); a TiledExperts is returned as is."""
+    if v is None or isinstance(v, TiledExperts):
+        return v
+    if isinstance(v, dict):
+        return _memo(v["packed"], "tiled", (v,), lambda: tile_experts_packed(v))
+    return _memo(v, "tiled16", (v,), lambda: tile_experts_bf16(v))
+
+
+def resident_params(p: dict) -> dict:
+    """A copy of the parameter dict `p` whose expert stacks are their resident tiled forms. A
+    caller that keeps this dict and drops its native triplets holds each layer once on the GPU
+    (the module's set_experts_packed does the same). Other entries are passed through."""
+    q = dict(p)
+    for key in ("experts_gate_up", "experts_down"):
+        if q.get(key) is not None:
+            q[key] = resident_experts(q[key])
+    return q
 
 
 # ----------------------------------------------------------------------------------- prepare
@@ -277,6 +350,8 @@ def _prepare_router(gate: torch.Tensor, sgate: torch.Tensor | None, E: int, H: i
             full[E] = sgate.reshape(H)
         return ("bf16", ops.tile_bf16(full), rows, None)
     wr = gate.to(torch.float32).contiguous()
+    if wr is gate:   # an fp32 gate: its own copy, so the memo entry does not hold its weak key
+        wr = gate.clone()
     sg = sgate.to(torch.float32).reshape(H).contiguous() if gated else None
     return ("f32", wr, E + 1, sg)
 
@@ -308,9 +383,26 @@ def gated_activation(cfg) -> tuple[int, float, float]:
     raise ValueError(f"hidden_act {act!r} not supported (silu | swigluoai)")
 
 
+# parameter-dict keys and config fields a prepared block depends on
+_PARAM_KEYS = ("gate", "experts_gate_up", "experts_down", "experts_mixed", "shared_gate_proj",
+               "shared_up_proj", "shared_down_proj", "shared_expert_gate", "e_score_correction_bias")
+_CFG_FIELDS = ("hidden_size", "num_experts", "num_experts_per_tok", "moe_intermediate_size",
+               "shared_expert_intermediate_size", "scoring_func", "norm_topk_prob", "n_group",
+               "topk_group", "routed_scaling_factor", "hidden_act", "swiglu_alpha", "swiglu_limit",
+               "norm_topk_single")
+
+
 def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUTO) -> Prepared:
     """Resolve the parameter dict `p` (reference keys, src/quanta/qwen35/moe.py:159-161) into the
-    resident kernel form. Conversions are cached on the source tensors."""
+    resident kernel form. The result is memoised per layer on p["gate"], and each weight's tiled
+    form on that weight, so a model's layers are converted once however many there are."""
+    sig = tuple(getattr(cfg, f, None) for f in _CFG_FIELDS)
+    sources = [p.get(k) for k in _PARAM_KEYS]
+    return _memo(p["gate"], ("block", topk, regime, sig), sources,
+                 lambda: _build_prepared(p, cfg, topk=topk, regime=regime))
+
+
+def _build_prepared(p: dict, cfg, *, topk: int | None, regime: int) -> Prepared:
     H = int(_cfg(cfg, "hidden_size"))
     E = int(_cfg(cfg, "num_experts"))
     I = int(_cfg(cfg, "moe_intermediate_size"))
@@ -326,12 +418,7 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     packed = _is_packed(gu_src)
     if packed != _is_packed(dn_src):
         raise ValueError("experts_gate_up and experts_down must both be packed or both bf16")
-    if packed:
-        gu = _cached("gu", (gu_src,), lambda: tile_experts_packed(gu_src))
-        dn = _cached("dn", (dn_src,), lambda: tile_experts_packed(dn_src))
-    else:
-        gu = _cached("gu16", (gu_src,), lambda: tile_experts_bf16(gu_src))
-        dn = _cached("dn16", (dn_src,), lambda: tile_experts_bf16(dn_src))
+    gu, dn = resident_experts(gu_src), resident_experts(dn_src)
     if tuple(gu["shape"]) != (E, 2 * I, H) or tuple(dn["shape"]) != (E, H, I):
         raise ValueError(f"expert stacks must be gate_up [{E},{2 * I},{H}] and down [{E},{H},{I}] "
                          f"(got {gu['shape']} and {dn['shape']})")
@@ -339,12 +426,12 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     has_shared = Is > 0 and p.get("shared_gate_proj") is not None
     sgate = p.get("shared_expert_gate") if has_shared else None
     gate = p["gate"]
-    rkind, rw, rrows, sg32 = _cached("router", (gate, sgate), lambda: _prepare_router(gate, sgate, E, H))
+    rkind, rw, rrows, sg32 = _memo(gate, ("router", sgate is not None), (gate, sgate),
+                                   lambda: _prepare_router(gate, sgate, E, H))
     sh_gu = sh_dn = None
     if has_shared:
-        sh_gu, sh_dn = _cached("shared", (p["shared_gate_proj"], p["shared_up_proj"],
-                                          p["shared_down_proj"]),
-                               lambda: _prepare_shared(p, H, Is))
+        shw = (p["shared_gate_proj"], p["shared_up_proj"], p["shared_down_proj"])
+        sh_gu, sh_dn = _memo(shw[0], "shared", shw, lambda: _prepare_shared(p, H, Is))
     bias = p.get("e_score_correction_bias")
     if bias is not None:
         bias = bias.to(torch.float32).reshape(E).contiguous()
@@ -353,7 +440,7 @@ def prepare(p: dict, cfg, *, topk: int | None = None, regime: int = L.REGIME_AUT
     c.hidden, c.n_experts, c.top_k, c.inter = H, E, k, I
     c.shared_inter = Is if has_shared else 0
     c.scoring = _SCORING[scoring]
-    c.norm_topk = int(bool(_cfg(cfg, "norm_topk_prob", True)))
+    c.norm_topk = norm_mode(cfg, scoring, bias is not None)
     c.n_group = int(_cfg(cfg, "n_group", 1))
     c.topk_group = int(_cfg(cfg, "topk_group", 1))
     c.routed_scale = float(_cfg(cfg, "routed_scaling_factor", 1.0))
@@ -403,9 +490,10 @@ def _prepare_mixed(p: dict, cfg, *, topk, regime) -> Prepared:
     H, E = int(_cfg(cfg, "hidden_size")), int(_cfg(cfg, "num_experts"))
     I = int(_cfg(cfg, "moe_intermediate_size"))
     src = p["experts_mixed"]
-    mx = _cached("mixed", (src,), lambda: src if isinstance(src, MixedExperts) else
-                 tile_experts_mixed(src["stacks"], src["pbits"], src["pslot"],
-                                    group_size=int(src.get("group_size", 128))))
+    mx = src if isinstance(src, MixedExperts) else _memo(
+        p["gate"], "mixed", (src,),
+        lambda: tile_experts_mixed(src["stacks"], src["pbits"], src["pslot"],
+                                   group_size=int(src.get("group_size", 128))))
     if mx["n_experts"] != E:
         raise ValueError(f"mixed experts: {mx['n_experts']} experts for a {E}-expert config")
     if len(mx["stacks"]) > L.MAX_STACKS:
@@ -427,7 +515,7 @@ def _prepare_mixed(p: dict, cfg, *, topk, regime) -> Prepared:
                                         group_size=64, bits=4)
     q["experts_down"] = TiledExperts(format="int4_g64", codes=None, sb=None, shape=(E, H, I),
                                      group_size=64, bits=4)
-    pr = prepare(q, cfg, topk=topk, regime=regime)
+    pr = _build_prepared(q, cfg, topk=topk, regime=regime)
     pr.cfg.mixed = 1
     pr.mixed = m
     pr.keep = pr.keep + (mx,)
@@ -456,7 +544,7 @@ def _router_logits(xf: torch.Tensor, pr: Prepared) -> torch.Tensor:
 def _topk(logits: torch.Tensor, pr: Prepared, k: int):
     c = pr.cfg
     return ops.router_topk(logits, c.n_experts, k, scoring=c.scoring, bias=pr.bias,
-                           n_group=c.n_group, topk_group=c.topk_group, norm_topk=bool(c.norm_topk),
+                           n_group=c.n_group, topk_group=c.topk_group, norm_topk=c.norm_topk,
                            routed_scale=c.routed_scale, has_shared_gate=bool(c.shared_gated))
 
 
@@ -474,7 +562,8 @@ def qwen35_route(xf: torch.Tensor, gate_w: torch.Tensor, cfg, *, topk_override: 
         raise TypeError("qwen35_route: x must be bf16")
     E, H = int(_cfg(cfg, "num_experts")), int(_cfg(cfg, "hidden_size"))
     k = topk_override if topk_override is not None else int(_cfg(cfg, "num_experts_per_tok"))
-    kind, rw, rows, _ = _cached("router", (gate_w, None), lambda: _prepare_router(gate_w, None, E, H))
+    kind, rw, rows, _ = _memo(gate_w, ("router", False), (gate_w, None),
+                              lambda: _prepare_router(gate_w, None, E, H))
     xf = xf.contiguous()
     n = xf.shape[0]
     if kind == "f32":
@@ -483,12 +572,13 @@ def qwen35_route(xf: torch.Tensor, gate_w: torch.Tensor, cfg, *, topk_override: 
         logits = ops.grouped_qmm(xf, K=H, n_rows=rows, weight_format=L.FMT_BF16, codes=rw, sb=None,
                                  epilogue=L.EPI_F32, out_rows=n, regime=_dense_regime(n, H),
                                  dense_rows=n)
-    scoring = _SCORING[str(_cfg(cfg, "scoring_func", "softmax"))]
+    sname = str(_cfg(cfg, "scoring_func", "softmax"))
+    scoring = _SCORING[sname]
     bias = None if e_score_correction_bias is None else e_score_correction_bias.float().reshape(E).contiguous()
     idx, w, _ = ops.router_topk(logits, E, k, scoring=scoring, bias=bias,
                                 n_group=int(_cfg(cfg, "n_group", 1)),
                                 topk_group=int(_cfg(cfg, "topk_group", 1)),
-                                norm_topk=bool(_cfg(cfg, "norm_topk_prob", True)),
+                                norm_topk=norm_mode(cfg, sname, bias is not None),
                                 routed_scale=float(_cfg(cfg, "routed_scaling_factor", 1.0)))
     return idx, w
 

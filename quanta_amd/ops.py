@@ -179,8 +179,10 @@ def router_logits_f32(x: torch.Tensor, wr: torch.Tensor,
 
 def router_topk(logits: torch.Tensor, n_experts: int, k: int, *, scoring: int = L.SCORE_SOFTMAX,
                 bias: torch.Tensor | None = None, n_group: int = 1, topk_group: int = 1,
-                norm_topk: bool = True, routed_scale: float = 1.0, has_shared_gate: bool = False):
-    """Top-k over router logits [N, ld] -> (idx [N,k] int32, w [N,k] fp32, sg [N] fp32 or None)."""
+                norm_topk: int = L.NORM_ALWAYS, routed_scale: float = 1.0,
+                has_shared_gate: bool = False):
+    """Top-k over router logits [N, ld] -> (idx [N,k] int32, w [N,k] fp32, sg [N] fp32 or None).
+    `norm_topk` is a QMOE_NORM_* mode (True / False mean always / never)."""
     _need(logits, torch.float32, "logits")
     N, ld = logits.shape
     if bias is not None:

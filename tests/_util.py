@@ -49,11 +49,20 @@ def metrics(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
     return max_abs, rel
 
 
+def raw_max_abs(got, want) -> float:
+    """The unscaled max |got - want|, reported beside the scaled gate figure."""
+    d = np.asarray(got, np.float64) - np.asarray(want, np.float64)
+    return float(np.max(np.abs(d))) if d.size else 0.0
+
+
 def assert_close(got, want, what="", max_abs=MAX_ABS, rel_l2=REL_L2):
     """`want` should be the oracle's unrounded (float64) result: the GPU's bf16 output then
     carries exactly one rounding, not two."""
     ma, rl = metrics(got, want)
-    print(f"[parity] {what}: max_abs(scaled)={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    raw = raw_max_abs(got, want)
+    peak = float(np.max(np.abs(want))) if np.size(want) else 0.0
+    print(f"[parity] {what}: max_abs(scaled)={ma:.3e} max_abs(raw)={raw:.3e} max|want|={peak:.3g} "
+          f"rel_l2={rl:.3e}", flush=True)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     assert ma <= max_abs and rl <= rel_l2, f"{what}: max_abs={ma:.3e} rel_l2={rl:.3e}"
 
@@ -85,5 +94,5 @@ def route_sets_equal(a: np.ndarray, b: np.ndarray) -> bool:
     return all(set(x) == set(y) for x, y in zip(a.tolist(), b.tolist()))
 
 
-__all__ = ["bf16_dev", "words_dev", "bits_np", "f64", "words_np", "metrics", "assert_close",
+__all__ = ["bf16_dev", "words_dev", "bits_np", "f64", "words_np", "metrics", "raw_max_abs", "assert_close",
            "oracle_params_from_torch", "near_tie_rows", "route_sets_equal", "oq"]

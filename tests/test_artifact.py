@@ -72,6 +72,51 @@ def test_moe_packed_and_config(tmp_path):
     cfg = art.moe_config()
     assert (cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size,
             cfg.shared_expert_intermediate_size, cfg.norm_topk_prob) == (128, 4, 2, 64, 64, False)
+    assert (cfg.scoring_func, cfg.n_group, cfg.topk_group, cfg.routed_scaling_factor) == \
+        ("softmax", 1, 1, 1.0)
+
+
+def test_moe_config_router_fields(tmp_path):
+    """scoring_func (src/quanta/qwen35/config.py:361) and the DeepSeek/GLM router fields are read
+    from config.json; a scoring function the block does not run is refused."""
+    rng = torch.Generator().manual_seed(4)
+    b, _ = _block(rng)
+    cj = moe_config_json(128, 4, 2, 64, 64)
+    cj["text_config"].update(scoring_func="sigmoid", n_group=2, topk_group=1,
+                             routed_scaling_factor=2.5)
+    cfg = QuantaArtifact(b.write(tmp_path / "a", cj)).moe_config()
+    assert (cfg.scoring_func, cfg.n_group, cfg.topk_group, cfg.routed_scaling_factor) == \
+        ("sigmoid", 2, 1, 2.5)
+    cj["text_config"]["scoring_func"] = "argmax"
+    with pytest.raises(ValueError, match="scoring_func"):
+        QuantaArtifact(b.write(tmp_path / "b", cj)).moe_config()
+
+
+def test_manifest_resolution_rule(tmp_path):
+    """The four cases of the manifest rule: a dense record at the key wins over an affine_packed
+    stem, an affine_packed stem resolves the .weight key, another format at either place is a
+    ValueError, and no record is a KeyError."""
+    rng = torch.Generator().manual_seed(5)
+    b, _ = _block(rng)
+    p = LM_PREFIX + "layers.0.mlp."
+    # both a dense record at "twin.weight" and an affine_packed one at "twin": dense wins
+    b.add_dense(p + "twin.weight", torch.ones(2, 64).to(torch.bfloat16))
+    b.add_quantized(p + "twin", u32(np.zeros((2, 8), np.uint32)), torch.ones(2, 1).to(torch.bfloat16),
+                    torch.zeros(2, 1).to(torch.bfloat16), bits=4, group_size=64)
+    b.manifest[p + "weird.weight"] = {"format": "fp3"}
+    b.tensors[p + "weird.weight"] = torch.zeros(2)
+    art = QuantaArtifact(b.write(tmp_path / "a", moe_config_json(128, 4, 2, 64, 64)))
+    assert art._meta(p + "twin.weight") == (p + "twin.weight", {"format": "dense", "dtype": "bfloat16"})
+    base, meta = art._meta(p + "experts.down_proj.weight")
+    assert base == p + "experts.down_proj" and meta["format"] == "affine_packed"
+    assert art._meta(p + "experts.down_proj")[0] == p + "experts.down_proj"
+    with pytest.raises(ValueError, match="fp3"):
+        art._meta(p + "weird.weight")
+    with pytest.raises(KeyError):
+        art._meta(p + "absent.weight")
+    assert art.has(p + "twin") and art.has(p + "weird.weight") and not art.has(p + "absent.weight")
+    art.release()
+    assert not art._shards
 
 
 def test_reader_errors_follow_the_reference(tmp_path):

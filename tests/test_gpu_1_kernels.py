@@ -63,12 +63,13 @@ def test_tile_bf16_layout(gpu):
 
 
 def _route_case(rng, N, E, H, k, scoring, bias=False, n_group=1, topk_group=1, scale=1.0,
-                norm=True):
+                norm=True, norm_single=True):
     x = oq.round_bf16(rng.standard_normal((N, H)))
     wr = oq.round_bf16(rng.standard_normal((E, H)) * 0.02)
     bvec = rng.standard_normal(E) * 0.01 if bias else None
     return x, wr, bvec, dict(k=k, scoring=scoring, bias=bvec, n_group=n_group,
-                             topk_group=topk_group, scale=scale, norm_topk=norm)
+                             topk_group=topk_group, scale=scale, norm_topk=norm,
+                             norm_single=norm_single)
 
 
 def _check_route(gpu, x, wr, kw, logits_dev, E):
@@ -78,7 +79,9 @@ def _check_route(gpu, x, wr, kw, logits_dev, E):
                                 bias=None if kw["bias"] is None else
                                 torch.tensor(kw["bias"], dtype=torch.float32, device=gpu),
                                 n_group=kw["n_group"], topk_group=kw["topk_group"],
-                                norm_topk=kw["norm_topk"], routed_scale=kw["scale"])
+                                norm_topk=(L.NORM_NONE if not kw["norm_topk"] else
+                                           L.NORM_ALWAYS if kw["norm_single"] else L.NORM_MULTI),
+                                routed_scale=kw["scale"])
     idx, w = idx.cpu().numpy(), w.cpu().numpy().astype(np.float64)
     # float32 logits carry ~|x||w| * 2^-24 * sqrt(H) error: rows whose selection gap is below a
     # generous bound of that are reported and compared as sets only.
@@ -106,6 +109,9 @@ def _check_route(gpu, x, wr, kw, logits_dev, E):
     dict(N=20, E=128, H=1024, k=6, scoring="sigmoid"),
     dict(N=64, E=256, H=7168, k=8, scoring="sigmoid", bias=True, n_group=8, topk_group=4, scale=2.5),
     dict(N=5, E=64, H=256, k=1, scoring="sigmoid", bias=True, norm=False),
+    # k = 1 with renormalisation: a MoEGate keeps the score (x 2.5), qwen35_route gives 1
+    dict(N=7, E=64, H=256, k=1, scoring="sigmoid", bias=True, scale=2.5, norm_single=False),
+    dict(N=6, E=64, H=256, k=1, scoring="softmax"),
     dict(N=3, E=1024, H=256, k=16, scoring="softmax"),
     dict(N=40, E=256, H=1024, k=6, scoring="sqrtsoftplus", bias=True, scale=1.5),
     dict(N=9, E=384, H=512, k=8, scoring="sqrtsoftplus"),
@@ -115,7 +121,7 @@ def test_router_topk_vs_oracle(gpu, case):
     x, wr, bvec, kw = _route_case(rng, case["N"], case["E"], case["H"], case["k"], case["scoring"],
                                   case.get("bias", False), case.get("n_group", 1),
                                   case.get("topk_group", 1), case.get("scale", 1.0),
-                                  case.get("norm", True))
+                                  case.get("norm", True), case.get("norm_single", True))
     logits = ops.router_logits_f32(bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu),
                                    torch.tensor(wr, dtype=torch.float32, device=gpu))
     lg = f64(logits)[:, :case["E"]]

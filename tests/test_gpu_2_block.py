@@ -101,6 +101,32 @@ def test_topk_override_and_errors(gpu):
         qwen35_moe(x[None], dict(p, experts_gate_up=bad), cfg)
 
 
+def test_topk_override_one_moegate_keeps_score(gpu):
+    """A sigmoid + correction-bias router (MoEGate) at k = 1 keeps the expert's score times the
+    routed scale instead of renormalising it to 1 (`topk > 1 and norm_topk_prob`,
+    src/quanta/modeling/moe.py:41, src/quanta/glm/moe.py:53)."""
+    a, cfg, p, x = _fixture("c3mini", gpu)
+    assert cfg.scoring_func == "sigmoid" and cfg.norm_topk_prob
+    op = oracle_params_from_torch(p)
+    xf = f64(x)
+    kw = dict(k=1, inter=cfg.moe_intermediate_size, scoring="sigmoid", norm_topk=True,
+              n_group=cfg.n_group, topk_group=cfg.topk_group, scale=cfg.routed_scaling_factor)
+    _, keep = om.moe_forward(xf, op, norm_single=False, **kw)
+    _, renorm = om.moe_forward(xf, op, norm_single=True, **kw)
+    assert not np.allclose(keep["w"], renorm["w"])
+    y = qwen35_moe(x[None], p, cfg, topk_override=1)[0]
+    assert_close(f64(y), keep["y_exact"], "c3mini MoEGate k=1")
+    idx, w = qwen35_route(x, p["gate"], cfg, topk_override=1,
+                          e_score_correction_bias=p["e_score_correction_bias"])
+    ok = om.route_margin(keep["choice"], 1) > 1e-5
+    assert np.array_equal(idx.cpu().numpy()[ok], keep["idx"][ok])
+    assert np.allclose(w.cpu().numpy()[ok], keep["w"][ok], rtol=1e-5, atol=1e-7)
+    # the explicit override restores qwen35_route's rule
+    cfg1 = MoEConfig(**{**cfg.__dict__, "norm_topk_single": True})
+    y1 = qwen35_moe(x[None], p, cfg1, topk_override=1)[0]
+    assert_close(f64(y1), renorm["y_exact"], "c3mini k=1 renormalised")
+
+
 def test_token_chunking_and_batch_invariance(gpu):
     a, cfg, p, x = _fixture("c1mini", gpu)
     full = qwen35_moe(x[None], p, cfg, token_chunk=8192)

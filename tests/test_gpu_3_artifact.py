@@ -99,3 +99,41 @@ def test_block_from_artifact(gpu, tmp_path, shared_int8):
         assert_close(f64(y), a["y_exact"], "c1mini from artifact")
     m = art.moe_module(0, gpu)
     assert torch.equal(m(x[None])[0], y)
+
+
+def test_sigmoid_router_from_artifact(gpu, tmp_path):
+    """A bake whose config.json declares a sigmoid router with groups and a routed scale (the
+    c3mini golden block: sigmoid + correction bias, 8 groups keep 4, x2.5): moe_config reads
+    scoring_func (src/quanta/qwen35/config.py:361) and the DeepSeek/GLM fields, moe_packed picks
+    up the stored selection bias, and the block matches the golden output. With scoring_func
+    left out of the config, the same weights route with softmax and the output differs."""
+    a = dict(np.load(GOLDEN / "c3mini.npz"))
+    H, E, k, I, Is, ng, tg, norm, sig = a["dims"].tolist()
+    assert sig and ng > 1
+    p = LM_PREFIX + "layers.0.mlp."
+    b = ArtifactBuilder()
+    b.add_dense(p + "gate.weight", bf16_from_bits(a["gate"]))
+    b.add_dense(p + "gate.e_score_correction_bias", torch.from_numpy(a["e_score_correction_bias"]))
+    for proj in ("gate_proj", "up_proj", "down_proj"):
+        b.add_dense(p + f"shared_expert.{proj}.weight", bf16_from_bits(a[f"shared_{proj}"]))
+    for key, pre in (("experts.gate_up_proj", "gu"), ("experts.down_proj", "dn")):
+        b.add_quantized(p + key, u32(a[f"{pre}_packed"]), bf16_from_bits(a[f"{pre}_scale"]),
+                        bf16_from_bits(a[f"{pre}_bias"]), bits=4, group_size=64)
+    cfg_json = moe_config_json(H, E, k, I, Is, bool(norm))
+    cfg_json["text_config"].update(scoring_func="sigmoid", n_group=ng, topk_group=tg,
+                                   routed_scaling_factor=float(a["routed_scale"][0]))
+    art = QuantaArtifact(b.write(tmp_path / "sig", cfg_json))
+    cfg = art.moe_config()
+    assert (cfg.scoring_func, cfg.n_group, cfg.topk_group, cfg.routed_scaling_factor) == \
+        ("sigmoid", ng, tg, float(a["routed_scale"][0]))
+    x = bf16_dev(a["x"], gpu)
+    pk = art.moe_packed(0, gpu)
+    assert "e_score_correction_bias" in pk and "shared_expert_gate" not in pk
+    y = qwen35_moe(x[None], pk, cfg)[0]
+    assert_close(f64(y), a["y_exact"], "c3mini (sigmoid router) from artifact")
+    assert torch.equal(art.moe_module(0, gpu)(x[None])[0], y)
+    del cfg_json["text_config"]["scoring_func"]
+    soft = QuantaArtifact(b.write(tmp_path / "soft", cfg_json))
+    assert soft.moe_config().scoring_func == "softmax"
+    y_soft = qwen35_moe(x[None], soft.moe_packed(0, gpu), soft.moe_config())[0]
+    assert not torch.equal(y_soft, y)

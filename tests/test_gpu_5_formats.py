@@ -297,10 +297,13 @@ def test_narrow_formats_batch_invariance_full_size(gpu, fmt):
 
 
 # ------------------------------------------------------------------------------ edge sizes
-@pytest.mark.parametrize("E,k,N", [(1024, 16, 2), (64, 64, 3), (16, 16, 5), (1024, 8, 300)])
+@pytest.mark.parametrize("E,k,N", [(1024, 16, 2), (64, 64, 3), (16, 16, 5), (1024, 8, 300),
+                                   (16, 16, 2), (64, 64, 2), (64, 64, 1), (16, 12, 2)])
 def test_block_router_limits_vs_oracle(gpu, E, k, N):
     """The router's limits through the whole block: the largest expert count (1024), the
-    largest top-k (64), k = E (every expert on every token), at decode and prefill sizes."""
+    largest top-k (64), k = E (every expert on every token), at decode and prefill sizes. One
+    or two tokens route slot-major, one m-tile per slot: with k > E / 2 that is more tiles than
+    the permute's bound, so the tile map is sized for N * k."""
     cfg = MoEConfig(256, E, k, 128, 128)
     p = _layer(gpu, 64, seed=E + k + N, H=256, E=E, I=128, Is=128)
     x = _inputs(gpu, N, 256, N)

@@ -27,13 +27,16 @@ H, E, I = 512, 8, 256
 GS = 128
 
 
-def _mixed(dev, seed, widths, permute=True):
-    """widths[proj] [E] -> (p["experts_mixed"] source dict, the oracle's "mixed" dict)."""
+def _mixed(dev, seed, widths, permute=True, tie_slots=False, group_sizes=None):
+    """widths[proj] [E] -> (p["experts_mixed"] source dict, the oracle's "mixed" dict).
+    tie_slots: up takes gate's slots (with equal widths, the layout that fuses gate and up);
+    group_sizes[proj]: that projection's stacks' group size (default GS)."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     rng = np.random.default_rng(seed)
     stacks, pslot, ostacks = {}, {}, {}
     for proj in ("gate", "up", "down"):
         rows, K = (I, H) if proj != "down" else (H, I)
+        gs = (group_sizes or {}).get(proj, GS)
         pb = np.asarray(widths[proj])
         ps = np.zeros(E, np.int64)
         stacks[proj], ostacks[proj] = {}, {}
@@ -41,19 +44,21 @@ def _mixed(dev, seed, widths, permute=True):
             ids = np.flatnonzero(pb == b)
             ps[ids] = rng.permutation(ids.size) if permute else np.arange(ids.size)
             w = (torch.randn(ids.size, rows, K, generator=g) * 0.02).to(dev)
-            packed, s, bb = quantize_affine(w, b, group_size=GS)
-            stacks[proj][b] = {"packed": packed, "scale": s, "bias": bb}
-            ostacks[proj][b] = (words_np(packed), bits_np(s), bits_np(bb))
+            packed, s, bb = quantize_affine(w, b, group_size=gs)
+            stacks[proj][b] = {"packed": packed, "scale": s, "bias": bb, "group_size": gs}
+            ostacks[proj][b] = (words_np(packed), bits_np(s), bits_np(bb), gs)
+        if tie_slots and proj == "up":
+            ps = pslot["gate"].copy()
         pslot[proj] = ps
     pbits = {k: np.asarray(v) for k, v in widths.items()}
     src = {"stacks": stacks, "pbits": pbits, "pslot": pslot, "group_size": GS}
     return src, {"stacks": ostacks, "pbits": pbits, "pslot": pslot, "group_size": GS}
 
 
-def _layer_mixed(dev, seed, widths, permute=True):
+def _layer_mixed(dev, seed, widths, permute=True, **kw):
     p = _layer(dev, GS, seed)
     del p["experts_gate_up"], p["experts_down"]
-    src, om_mixed = _mixed(dev, seed, widths, permute)
+    src, om_mixed = _mixed(dev, seed, widths, permute, **kw)
     p["experts_mixed"] = src
     return p, om_mixed
 
@@ -104,6 +109,30 @@ def test_mixed_vs_oracle(gpu, case, N):
     y = qwen35_moe(x[None], p, cfg)[0]
     _, it = om.moe_forward(f64(x), _oracle(p, om_mixed), k=2, inter=I)
     assert_close(f64(y), it["y_exact"], f"mixed {case} N={N}")
+
+
+@pytest.mark.parametrize("case", ["fused34", "fused346", "g64_g128"])
+@pytest.mark.parametrize("N", [1, 8, 40, 300])
+def test_mixed_gate_up_drawn_together_vs_oracle(gpu, case, N):
+    """gate and up share each expert's width and slot, over two or three widths: gate and up are
+    then fused per width (SwiGLU in the epilogue) unless their group sizes differ, which keeps
+    them apart. Both against the oracle."""
+    from quanta_amd.moe import tile_experts_mixed
+
+    rng = np.random.default_rng(100 + N)
+    gu = rng.choice([3, 4, 6] if case == "fused346" else [3, 4], E)
+    widths = {"gate": gu, "up": gu.copy(), "down": rng.choice([3, 4], E)}
+    gsz = {"gate": 64, "up": 128} if case == "g64_g128" else None
+    cfg = MoEConfig(H, E, 2, I, 256)
+    p, om_mixed = _layer_mixed(gpu, 29 * N + len(case), widths, tie_slots=True, group_sizes=gsz)
+    src = p["experts_mixed"]
+    mx = tile_experts_mixed(src["stacks"], src["pbits"], src["pslot"])
+    fused = any(proj == "gate_up" for proj, _, _ in mx["stacks"])
+    assert fused == (case != "g64_g128")
+    x = _inputs(gpu, N, H, N)
+    y = qwen35_moe(x[None], dict(p, experts_mixed=mx), cfg)[0]
+    _, it = om.moe_forward(f64(x), _oracle(p, om_mixed), k=2, inter=I)
+    assert_close(f64(y), it["y_exact"], f"mixed gate/up together {case} N={N}")
 
 
 def test_mixed_argument_errors(gpu):

@@ -174,7 +174,8 @@ def test_dequant_special_codes(bits):
 # ----------------------------------------------------------------------------------- routing
 
 
-def _brute_route(x, wr, k, scoring, bias=None, n_group=1, topk_group=1, norm=True, scale=1.0):
+def _brute_route(x, wr, k, scoring, bias=None, n_group=1, topk_group=1, norm=True, scale=1.0,
+                 norm_single=True):
     out_idx, out_w = [], []
     for t in range(x.shape[0]):
         logit = [float(np.dot(x[t].astype(np.float64), wr[e].astype(np.float64)))
@@ -194,7 +195,7 @@ def _brute_route(x, wr, k, scoring, bias=None, n_group=1, topk_group=1, norm=Tru
             allowed = {e for e in range(len(sc)) if e // gs in keep}
         sel = sorted(allowed, key=lambda e: (-ch[e], e))[:k]
         w = [sc[e] for e in sel]
-        if norm:
+        if norm and (len(sel) > 1 or norm_single):
             tot = sum(w) + 1e-20
             w = [v / tot for v in w]
         out_idx.append(sel)
@@ -207,21 +208,35 @@ def _brute_route(x, wr, k, scoring, bias=None, n_group=1, topk_group=1, norm=Tru
     dict(scoring="sigmoid"),
     dict(scoring="sigmoid", bias=True, n_group=4, topk_group=2, scale=2.5),
     dict(scoring="sigmoid", bias=True, norm=False),
+    # k = 1: qwen35_route divides the single weight by itself, a MoEGate keeps the score
+    dict(scoring="softmax", k=1),
+    dict(scoring="sigmoid", bias=True, scale=2.5, k=1, norm_single=False),
+    dict(scoring="sigmoid", bias=True, scale=2.5, k=1, norm_single=True),
 ])
 def test_route_brute_force(case):
     rng = np.random.default_rng(6)
-    E, H, N, k = 16, 24, 9, 3
+    E, H, N = 16, 24, 9
+    k = case.get("k", 3)
     x = rng.standard_normal((N, H))
     wr = rng.standard_normal((E, H)) * 0.3
     bias = rng.standard_normal(E) * 0.1 if case.get("bias") else None
     kw = dict(scoring=case["scoring"], bias=bias, n_group=case.get("n_group", 1),
               topk_group=case.get("topk_group", 1), norm=case.get("norm", True),
-              scale=case.get("scale", 1.0))
+              scale=case.get("scale", 1.0), norm_single=case.get("norm_single", True))
     bi, bw = _brute_route(x, wr, k, **kw)
     idx, w, *_ = om.route(x, wr, k=k, scoring=kw["scoring"], norm_topk=kw["norm"], bias=bias,
-                          n_group=kw["n_group"], topk_group=kw["topk_group"], scale=kw["scale"])
+                          n_group=kw["n_group"], topk_group=kw["topk_group"], scale=kw["scale"],
+                          norm_single=kw["norm_single"])
     assert np.array_equal(idx, bi)
     assert np.allclose(w, bw, rtol=1e-12, atol=0)
+    if k == 1 and kw["norm"]:
+        # closed forms: a renormalised single weight is 1 (times the scale); a kept score is
+        # sigmoid(x . wr[e]) times the scale
+        if kw["norm_single"]:
+            assert np.allclose(w, kw["scale"], rtol=1e-12)
+        else:
+            want = kw["scale"] / (1 + np.exp(-np.einsum("nh,nh->n", x, wr[idx[:, 0]])))
+            assert np.allclose(w[:, 0], want, rtol=1e-12)
 
 
 def test_route_softmax_matches_torch_topk():
