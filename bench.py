@@ -54,6 +54,11 @@ def parse():
     ap.add_argument("--layers", type=int, default=8, help="layer copies rotated for cold HBM")
     ap.add_argument("--pool", type=int, default=16, help="distinct input batches rotated")
     ap.add_argument("--sweep", default="1,8,128", help="extra decode batch sizes ('' = none)")
+    ap.add_argument("--configs-sweep", default="c1:1,8,32,64;c3:1,16,64",
+                    help="decode lines of the other BASELINE configs, 'cfg:N,N;cfg:N' ('' = none)")
+    ap.add_argument("--warmup-ms", type=float, default=150.0,
+                    help="each timed loop's warm-up runs at least --warmup steps and at least this "
+                         "many ms of steps: the clocks settle only after ~30 ms of sustained load")
     ap.add_argument("--prefill", type=int, default=4096,
                     help="tokens of the c4 Zipf prefill line (0 = none)")
     ap.add_argument("--zipf", action="store_true",
@@ -157,43 +162,63 @@ def main():
     H, E, k, I = cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size
     Is = cfg.shared_expert_intermediate_size
 
-    t0 = time.time()
-    base = synth.make_layer(args.config, device=dev)
-    log(f"generated {args.config} layer in {time.time() - t0:.1f}s")
-    # resident (tiled) layer copies at distinct addresses; the native stacks are dropped
-    layers = []
-    gu0 = TiledExperts(**tile_experts_packed(base["experts_gate_up"]))
-    dn0 = TiledExperts(**tile_experts_packed(base["experts_down"]))
-    native_cpu = None
-    if not args.no_cpu_baseline:
-        native_cpu = {kk: ({q: (v.cpu() if isinstance(v, torch.Tensor) else v) for q, v in vv.items()}
-                           if isinstance(vv, dict) else vv.cpu()) for kk, vv in base.items()}
-    del base["experts_gate_up"], base["experts_down"]
-    for li in range(args.layers):
-        def cp(te):
-            return TiledExperts({q: (v.clone() if isinstance(v, torch.Tensor) else v) for q, v in te.items()})
-        p = {kk: v.clone() for kk, v in base.items()}
-        p["experts_gate_up"] = gu0 if li == 0 else cp(gu0)
-        p["experts_down"] = dn0 if li == 0 else cp(dn0)
-        layers.append(p)
-    torch.cuda.synchronize()
-    log(f"{args.layers} resident layer copies ready ({time.time() - t0:.1f}s)")
+    def resident_layers(name, copies):
+        """`copies` resident (tiled) copies of config `name`'s synthetic layer at distinct
+        addresses, and the native layer on the host (for the CPU baseline) or None."""
+        t0 = time.time()
+        base = synth.make_layer(name, device=dev)
+        gu0 = TiledExperts(**tile_experts_packed(base["experts_gate_up"]))
+        dn0 = TiledExperts(**tile_experts_packed(base["experts_down"]))
+        native = {kk: ({q: (v.cpu() if isinstance(v, torch.Tensor) else v) for q, v in vv.items()}
+                       if isinstance(vv, dict) else vv.cpu()) for kk, vv in base.items()}
+        del base["experts_gate_up"], base["experts_down"]
+        out = []
+        for li in range(copies):
+            def cp(te):
+                return TiledExperts({q: (v.clone() if isinstance(v, torch.Tensor) else v) for q, v in te.items()})
+            p = {kk: v.clone() for kk, v in base.items()}
+            p["experts_gate_up"] = gu0 if li == 0 else cp(gu0)
+            p["experts_down"] = dn0 if li == 0 else cp(dn0)
+            out.append(p)
+        torch.cuda.synchronize()
+        log(f"{name}: {copies} resident layer copies ready ({time.time() - t0:.1f}s)")
+        return out, native
+
+    layers, native = resident_layers(args.config, args.layers)
+    native_cpu = None if args.no_cpu_baseline else native
+    warm_runs = []
+
+    def warm(step, warmup):
+        """At least `warmup` steps and at least --warmup-ms of steps, then a synchronize. From
+        idle, the chip runs the first ~5 steps fast, the next ~100 up to 17% slower and then
+        settles (a power-management transient); sustained load removes it, so the timed loop
+        starts from the steady state a serving loop runs in."""
+        t0 = time.perf_counter()
+        n = 0
+        while n < warmup or (time.perf_counter() - t0) * 1e3 < args.warmup_ms:
+            for _ in range(max(warmup - n, 16)):   # enqueued back to back: sustained load
+                step(n)
+                n += 1
+            torch.cuda.synchronize()
+        warm_runs.append(n)
+        return n
 
     def run_batch(N, steps, warmup, pool, regime=L.REGIME_AUTO, zipf=False, lays=None,
-                  residual=False):
+                  residual=False, cfg_=None):
         # zipf: the c4 workload (the same shape, Zipf(1.1) expert popularity through router
         # column 0 and x[:, 0] = 1.0), on the resident experts of the headline config
         # residual: the block with the layer's RMSNorm in front and the residual add fused
-        src = "c4" if zipf else args.config
+        src = "c4" if zipf else (cfg_ or args.config)
+        c_ = synth.spec(src).cfg
         xs = [synth.make_inputs(src, N, device=dev, seed=100 + i) for i in range(pool)]
         lays = layers if lays is None else lays
         if zipf:
             lays = [dict(p, gate=synth.zipf_router(p["gate"])) for p in lays]
-        preps = [prepare(p, cfg, regime=regime) for p in lays]
+        preps = [prepare(p, c_, regime=regime) for p in lays]
         wsz = (ops.forward_residual_workspace if residual else ops.forward_workspace)(preps[0].cfg, N)
         ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
-        out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
-        norm_w = (1.0 + 0.1 * torch.randn(H, device=dev)).to(torch.bfloat16)
+        out = torch.empty(N, c_.hidden_size, dtype=torch.bfloat16, device=dev)
+        norm_w = (1.0 + 0.1 * torch.randn(c_.hidden_size, device=dev)).to(torch.bfloat16)
 
         def step(i):
             pr = preps[i % len(preps)]
@@ -202,9 +227,7 @@ def main():
             else:
                 ops.forward(pr.cfg, pr.weights, xs[i % pool], out=out, ws=ws, mixed=pr.mixed)
 
-        for i in range(warmup):
-            step(i)
-        torch.cuda.synchronize()
+        warm(step, warmup)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for i in range(steps):
@@ -216,7 +239,8 @@ def main():
         us = []
         for x in xs:
             xr = ops.rmsnorm(x, norm_w, 1e-6) if residual else x
-            idx, _ = qwen35_route(xr, lays[0]["gate"], cfg)
+            idx, _ = qwen35_route(xr, lays[0]["gate"], c_,
+                                  e_score_correction_bias=lays[0].get("e_score_correction_bias"))
             us.append(int(torch.unique(idx).numel()))
         return ms, us, xs, preps
 
@@ -249,14 +273,13 @@ def main():
             pr = preps[i % len(preps)]
             x, offsets, tile_off, sorted_slot, tile_map, _ = inputs[i % len(inputs)]
             ops.grouped_qmm(x, K=H, n_rows=2 * I, weight_format=L.FMT_INT4_G64,
-                            codes=pr.gu["codes"], sb=pr.gu["sb"], epilogue=L.EPI_SWIGLU,
+                            codes=pr.gu["codes"], sb=pr.gu["sb"], row_exp=pr.gu.get("rexp"),
+                            epilogue=L.EPI_SWIGLU,
                             out_rows=N * k, regime=regime, slot_of=sorted_slot, slot_div=k,
                             n_slots=N * k, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
                             n_experts=E, out=h)
 
-        for i in range(8):
-            launch(i)
-        torch.cuda.synchronize()
+        warm(launch, 8)
         reps = args.kernel_reps
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -282,7 +305,7 @@ def main():
             runs.append((args.prefill, True))
     if runs:
         for n2, zipf in runs:
-            st = max(10, args.steps // 4) if n2 <= 256 else max(5, args.steps // 20)
+            st = max(100, args.steps // 4) if n2 <= 256 else max(20, args.steps // 20)
             m2, u2, _, _ = run_batch(n2, st, 3, min(args.pool, 8), zipf=zipf)
             U2 = sum(u2) / len(u2)
             b2 = synth.algorithmic_bytes(cfg, U2, n2)
@@ -295,6 +318,30 @@ def main():
                        mfma_frac=round(f2 / m2 / 1e9 / BF16_PEAK_TFLOPS, 4))
             sweep.append(rec)
             log(f"sweep {rec}")
+
+    # ------------------------------------------------------------------ other BASELINE configs
+    # decode lines of configs 1 (Qwen3.6-35B-A3B shape) and 3 (DeepSeek-style sigmoid, groups),
+    # each on its own resident copies: enough of them that a step's weights come from HBM
+    if args.only == "" and args.configs_sweep:
+        for part in args.configs_sweep.split(";"):
+            name, ns = part.split(":")
+            c_ = synth.spec(name).cfg
+            layer_mb = synth.algorithmic_bytes(c_, c_.num_experts, 0) / 2**20
+            copies = max(2, min(8, int(2048 // layer_mb) + 1))
+            lays_c, _ = resident_layers(name, copies)
+            for n2 in (int(v) for v in ns.split(",") if v):
+                m2, u2, _, _ = run_batch(n2, max(100, args.steps // 4), 3, min(args.pool, 8),
+                                         lays=lays_c, cfg_=name)
+                U2 = sum(u2) / len(u2)
+                b2 = synth.algorithmic_bytes(c_, U2, n2)
+                rec = dict(workload=f"{name}-N{n2}", N=n2, ms_per_step=round(m2, 5),
+                           tokens_per_s=round(n2 / (m2 / 1e3), 1), distinct_experts=round(U2, 1),
+                           hbm_gbps=round(b2 / m2 / 1e6, 1),
+                           hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4), layer_copies=copies)
+                sweep.append(rec)
+                log(f"sweep {rec}")
+            del lays_c
+            torch.cuda.empty_cache()
 
     # ------------------------------------------------------------------ widened rows
     # the block with the decoder layer's norm and residual add (qmoe_forward_residual), and the
@@ -310,7 +357,7 @@ def main():
             log(f"sweep {rec}")
 
         if "residual" in args.extra:
-            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), residual=True)
+            m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), residual=True)
             record(f"{args.config}-N{N}-residual", m2, u2, extra_bytes=2 * H)
         # int6: MiniMax M3's experts; int3: Kimi's widths (gate_up int3 + down int4, group 128).
         # Two copies suffice to stream from HBM: one step touches U experts x 6-10 MB.
@@ -324,7 +371,7 @@ def main():
                 pf["experts_down"] = TiledExperts(**tile_experts_packed(pf["experts_down"]))
                 lays_f.append(pf)
             torch.cuda.synchronize()
-            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_f)
+            m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), lays=lays_f)
             record(f"{args.config}-N{N}-{tag}", m2, u2, **fmt)
             del lays_f
         if "mixed" in args.extra:
@@ -340,7 +387,7 @@ def main():
                 del src
                 lays_m.append(pm)
             torch.cuda.synchronize()
-            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_m)
+            m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), lays=lays_m)
             # bytes: the int4-g64 figure with the mixed layer's mean bytes per expert in its place
             be4 = 3 * cfg.moe_intermediate_size * H * 36 / 64
             record(f"{args.config}-N{N}-mixed34", m2, u2, per_expert_bytes=be - be4)
@@ -360,7 +407,7 @@ def main():
                 pa["experts_down"] = TiledExperts(dict(pa["experts_down"], awq_scale=s_dn))
                 lays_a.append(pa)
             torch.cuda.synchronize()
-            m2, u2, _, _ = run_batch(N, max(10, args.steps // 4), 3, min(args.pool, 8), lays=lays_a)
+            m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), lays=lays_a)
             record(f"{args.config}-N{N}-awq", m2, u2,
                    per_expert_bytes=(2 * H + cfg.moe_intermediate_size) * 2)
             del lays_a
@@ -429,6 +476,9 @@ def main():
         "n_gpus": 1,
         "steps": steps_layer,
         "warmup": args.warmup,
+        "warmup_policy": f"at least --warmup steps and {args.warmup_ms:g} ms of steps before each "
+                         "timed loop (the clocks settle ~30 ms into sustained load)",
+        "warmup_steps_run": warm_runs[0] if warm_runs else None,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",

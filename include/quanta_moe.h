@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 5
+#define QMOE_ABI_VERSION 6
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -135,6 +135,11 @@ typedef struct {
   const uint16_t* awq_gu;         /* config awq: bf16 [E, 2, H] input-channel scales of the gate
                                      (row 0) and up (row 1) projections, else NULL */
   const uint16_t* awq_dn;         /* config awq: bf16 [E, I] scales of the down projection */
+  const int8_t* gu_rexp;          /* int4 gate|up: per weight row [E, 2I] power-of-two exponent
+                                     (qmoe_row_exponents) for the prefill kernels' fp16 dequant,
+                                     or NULL (exponent 0: scales and biases must then lie in
+                                     fp16's normal range for full prefill precision) */
+  const int8_t* dn_rexp;          /* int4 down: per weight row [E, H], as gu_rexp */
 } qmoe_weights_t;
 
 int qmoe_abi_version(void);
@@ -240,7 +245,8 @@ int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_
  * p of expert e (offsets/tile_off from qmoe_permute; m_tile 16 for QMOE_REGIME_SMALL, 128 for
  * QMOE_REGIME_LARGE), with row(p) = slot_of[p] / slot_div (slot_of NULL: row(p) = p). With
  * offsets == NULL the call is one dense segment of dense_rows rows. W is tiled int4-g64
- * (codes + sb) or tiled bf16 (codes), [n_experts][n_rows][K]. Epilogue QMOE_EPI_SWIGLU treats
+ * (codes + sb) or tiled bf16 (codes), [n_experts][n_rows][K]; row_exp (int4, nullable) holds the
+ * per-row exponents of qmoe_row_exponents for the large regime's fp16 dequant. Epilogue QMOE_EPI_SWIGLU treats
  * rows [0, n_rows/2) as gate and [n_rows/2, n_rows) as up, with the gated activation `glu`
  * (QMOE_ACT_*; glu_alpha and glu_limit as act_alpha and act_limit of qmoe_config_t; other
  * epilogues ignore them).
@@ -251,7 +257,8 @@ int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int32_t* slot_
                      int64_t n_slots, const int32_t* offsets, const int32_t* tile_off,
                      const int32_t* tile_map, int n_experts, int64_t dense_rows, int K,
                      int n_rows, int weight_format,
-                     const void* codes, const uint16_t* sb, int epilogue, int glu,
+                     const void* codes, const uint16_t* sb, const int8_t* row_exp, int epilogue,
+                     int glu,
                      float glu_alpha, float glu_limit, void* out, int ld_out,
                      int regime, void* ws, size_t ws_bytes, void* stream);
 /* Workspace qmoe_grouped_qmm needs: the large-M int4 regime stages an fp16 copy of the
@@ -306,6 +313,18 @@ int qmoe_tile_int3(const uint32_t* packed, const uint16_t* scale, const uint16_t
 int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
                    int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
                    uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
+
+/* Per weight row of an affine stack [n_mats][rows][in] (native scale/bias bf16
+ * [.., in/group_size]): row_exp[r] = 14 - ex, 2^(ex-1) <= M_r < 2^ex, M_r the row's largest
+ * dequantized magnitude max_g max(|b_g|, |(2^bits - 1) s_g + b_g|); 0 for an all-zero row; within
+ * [-100, 100]. The prefill (large-regime) kernels dequantize int4 weights to fp16 as
+ * fp16(2^row_exp (s q + b)) and undo the power of two on the fp32 result, so rows of any
+ * magnitude keep fp16's full precision (scales far below fp16's normal range, 2^-14, would
+ * otherwise lose bits or vanish). No counterpart in the reference (MLX dequantizes in bf16);
+ * computed once per stack with the tiling. */
+int qmoe_row_exponents(const uint16_t* scale, const uint16_t* bias, int64_t n_mats, int64_t rows,
+                       int64_t in_features, int bits, int group_size, int8_t* row_exp,
+                       void* stream);
 
 /* Inverse check of qmoe_tile_int4: tiled stack -> bf16 [n_mats][rows][in], bit-identical to
  * qmoe_dequant of the native stack. Test/inspection entry point. */

@@ -23,7 +23,7 @@ REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
@@ -70,6 +70,8 @@ class QmoeWeights(ctypes.Structure):
         ("sh_dn", ctypes.c_void_p),
         ("awq_gu", ctypes.c_void_p),
         ("awq_dn", ctypes.c_void_p),
+        ("gu_rexp", ctypes.c_void_p),
+        ("dn_rexp", ctypes.c_void_p),
     ]
 
 
@@ -115,12 +117,13 @@ SIGNATURES = {
     "qmoe_router_topk": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P]),
     "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
     "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),
-    "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _I,
-                              _I, _F, _F, _P, _I, _I, _P, ctypes.c_size_t, _P]),
+    "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _P,
+                              _I, _I, _F, _F, _P, _I, _I, _P, ctypes.c_size_t, _P]),
     "qmoe_grouped_qmm_workspace": (ctypes.c_size_t, [_I64, _I, _I, _I]),
     "qmoe_combine": (_I, [_P, _P, _P, _I64, _I, _I, _P, _P, _P, _P]),
     "qmoe_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "qmoe_tile_int4": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "qmoe_row_exponents": (_I, [_P, _P, _I64, _I64, _I64, _I, _I, _P, _P]),
     "qmoe_dequant_tiled": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "qmoe_tile_int6": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_int3": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),

@@ -465,7 +465,8 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
                                 int slot_div, int64_t n_slots, const int32_t* offsets,
                                 const int32_t* tile_off, const int32_t* tile_map, int n_experts,
                                 int64_t dense_rows, int K, int n_rows, int weight_format,
-                                const void* codes, const uint16_t* sb, int epilogue, int glu,
+                                const void* codes, const uint16_t* sb, const int8_t* row_exp,
+                                int epilogue, int glu,
                                 float glu_alpha, float glu_limit, void* out,
                                 int ld_out, int regime, void* ws, size_t ws_bytes, void* stream) {
   if (!act || !codes || !out) return fail("qmoe_grouped_qmm: null pointer");
@@ -497,6 +498,7 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
   a.n_rows = n_rows;
   a.codes = codes;
   a.sb = sb;
+  a.row_exp = (weight_format == QMOE_FMT_INT4_G64) ? row_exp : nullptr;
   a.out = out;
   a.ld_out = ld_out;
   a.glu = glu;
@@ -793,6 +795,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
+    a.row_exp = (gfmt == FMT_INT4) ? wts->gu_rexp : nullptr;
     a.out = h; a.ld_out = c.inter;
     a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
     if (f16_acts) {   // the fp16 copy of x, made on the auxiliary stream at the fork
@@ -812,6 +815,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.act = h; a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
+    a.row_exp = (dfmt == FMT_INT4) ? wts->dn_rexp : nullptr;
     a.out = d; a.ld_out = c.hidden;
     if (f16_acts) {
       rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);

@@ -327,6 +327,34 @@ __global__ void __launch_bounds__(256) tile_bf16_kernel(const uint16_t* __restri
   out[i] = *src;
 }
 
+// ---------------------------------------------------------------------------- row exponents
+// One thread per weight row: M = the row's largest dequantized magnitude, max over its groups of
+// max(|b|, |qmax * s + b|) (the affine map is monotone in the code, so its extremes sit at codes
+// 0 and qmax), and row_exp = 14 - ex with 2^(ex-1) <= M < 2^ex, so every weight of the row times
+// 2^row_exp lies below 2^14 and fp16 holds it at full precision down to 2^-14 of that (2^28 of
+// dynamic range within the row). 0 for an all-zero or non-finite row; clamped to [-100, 100].
+__global__ void __launch_bounds__(256) row_exp_kernel(const uint16_t* __restrict__ scale,
+                                                      const uint16_t* __restrict__ bias,
+                                                      int64_t n_rows, int groups, float qmax,
+                                                      int8_t* __restrict__ row_exp) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  const uint16_t* sr = scale + r * groups;
+  const uint16_t* br = bias + r * groups;
+  float m = 0.f;
+  for (int g = 0; g < groups; ++g) {
+    const float sv = bf16_to_f32(sr[g]), bv = bf16_to_f32(br[g]);
+    m = fmaxf(m, fmaxf(fabsf(bv), fabsf(fmaf(qmax, sv, bv))));
+  }
+  int ex = 0;
+  if (m > 0.f && m <= 3.4e38f) {
+    frexpf(m, &ex);
+    ex = 14 - ex;
+    ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+  }
+  row_exp[r] = static_cast<int8_t>(ex);
+}
+
 static inline unsigned grid_for(int64_t n, int block) {
   return static_cast<unsigned>((n + block - 1) / block);
 }
@@ -372,6 +400,20 @@ extern "C" int qmoe_dequant(const uint32_t* packed, const uint16_t* scale, const
         packed, scale, bias, n_words, static_cast<int>(in_features / 4),
         static_cast<int>(in_features / group_size), group_size / 4, reinterpret_cast<uint2*>(out));
   return check_launch("qmoe_dequant");
+}
+
+extern "C" int qmoe_row_exponents(const uint16_t* scale, const uint16_t* bias, int64_t n_mats,
+                                  int64_t rows, int64_t in_features, int bits, int group_size,
+                                  int8_t* row_exp, void* stream) {
+  if (!scale || !bias || !row_exp) return fail("qmoe_row_exponents: null pointer");
+  if (n_mats <= 0 || rows <= 0 || in_features <= 0) return fail("qmoe_row_exponents: bad dims");
+  if (bits < 2 || bits > 8) return fail("qmoe_row_exponents: 2 <= bits <= 8");
+  if (group_size <= 0 || in_features % group_size) return fail("qmoe_row_exponents: in % group_size != 0");
+  const int64_t n = n_mats * rows;
+  row_exp_kernel<<<grid_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      scale, bias, n, static_cast<int>(in_features / group_size), static_cast<float>((1 << bits) - 1),
+      row_exp);
+  return check_launch("row_exponents");
 }
 
 extern "C" int qmoe_tile_int4(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,

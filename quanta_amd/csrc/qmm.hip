@@ -573,6 +573,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const char* wcode[2];
   const char* wsb[2];
   const u32x4* wp[2];
+  int rex[2] = {0, 0};   // int4: the lane's weight row of each tile, its power-of-two exponent
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int tl = (EPI == EPI_SWIGLU) ? (t == 0 ? 8 * cb + wave : a.n_rows / 32 + 8 * cb + wave)
@@ -582,6 +583,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
+      rex[t] = a.row_exp ? a.row_exp[(ebase + tl) * 16 + (lane & 15)] : 0;
     } else {
       wcode[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
@@ -640,12 +642,13 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       }
     }
     f16x2_t s2[2], b2[2];
+    // scale and bias of the row times 2^rex (exact), so the fp16 weights stay normal
     auto sb_conv = [&](int grp) __attribute__((always_inline)) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t sbw = grp ? sbv[t].y : sbv[t].x;
-        const _Float16 sv = static_cast<_Float16>(bf16lo_to_f32(sbw));
-        const _Float16 bv = static_cast<_Float16>(bf16hi_to_f32(sbw));
+        const _Float16 sv = static_cast<_Float16>(ldexpf(bf16lo_to_f32(sbw), rex[t]));
+        const _Float16 bv = static_cast<_Float16>(ldexpf(bf16hi_to_f32(sbw), rex[t]));
         s2[t] = f16x2_t{sv, sv};
         b2[t] = f16x2_t{bv, bv};
       }
@@ -755,14 +758,16 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       const int64_t ar2 = act_row(a, m0 + mr);
       const bool ok = ar2 >= 0;
       const float rs = (FMT == FMT_INT4 && ok) ? a.row_sinv[ar2] : 1.0f;
+      // undo both power-of-two scalings (activation row, int4 weight row): exact
+      auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {
         const int col = 128 * cb + 16 * wave + (lane & 15);
-        store_out<EPI>(a, m0 + mr, col, ok ? acc[i][0][j] * rs : 0.f, ok ? acc[i][1][j] * rs : 0.f);
+        store_out<EPI>(a, m0 + mr, col, val(0), val(1));
       } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int col = 256 * cb + 32 * wave + 16 * t + (lane & 15);
-          store_out<EPI>(a, m0 + mr, col, ok ? acc[i][t][j] * rs : 0.f, 0.f);
+          store_out<EPI>(a, m0 + mr, col, val(t), 0.f);
         }
       }
     }
@@ -829,6 +834,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
   // this wavefront's four weight tiles (SwiGLU: gate tiles first, then their up tiles)
   const char* wcode[4];
   const char* wsb[4];
+  int rex[4];   // the lane's weight row of each tile: its power-of-two exponent (row_exp)
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int tl = (EPI == EPI_SWIGLU)
@@ -837,6 +843,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     const int64_t tb = (ebase + tl) * nsb;
     wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
     wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
+    rex[t] = a.row_exp ? a.row_exp[(ebase + tl) * 16 + (lane & 15)] : 0;
   }
   // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
   const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
@@ -883,12 +890,13 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       sbv[t] = reinterpret_cast<const uint2*>(lb + 4096 + t * 128)[lane & 15];
     }
     f16x2_t s2[4], b2[4];
+    // scale and bias of the row times 2^rex (exact), so the fp16 weights stay normal
     auto sb_conv = [&](int grp) __attribute__((always_inline)) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t sbw = grp ? sbv[t].y : sbv[t].x;
-        const _Float16 sv = static_cast<_Float16>(bf16lo_to_f32(sbw));
-        const _Float16 bv = static_cast<_Float16>(bf16hi_to_f32(sbw));
+        const _Float16 sv = static_cast<_Float16>(ldexpf(bf16lo_to_f32(sbw), rex[t]));
+        const _Float16 bv = static_cast<_Float16>(ldexpf(bf16hi_to_f32(sbw), rex[t]));
         s2[t] = f16x2_t{sv, sv};
         b2[t] = f16x2_t{bv, bv};
       }
@@ -964,17 +972,19 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       const int64_t ar2 = act_row(a, m0 + mr);
       const bool ok = ar2 >= 0;
       const float rs = ok ? a.row_sinv[ar2] : 1.0f;
+      // undo both power-of-two scalings (activation row, weight row): exact
+      auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int col = 256 * cb + 32 * wave + 16 * t + (lane & 15);
-          store_out<EPI>(a, m0 + mr, col, ok ? acc[i][t][j] * rs : 0.f, ok ? acc[i][t + 2][j] * rs : 0.f);
+          store_out<EPI>(a, m0 + mr, col, val(t), val(t + 2));
         }
       } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int col = 512 * cb + 64 * wave + 16 * t + (lane & 15);
-          store_out<EPI>(a, m0 + mr, col, ok ? acc[i][t][j] * rs : 0.f, 0.f);
+          store_out<EPI>(a, m0 + mr, col, val(t), 0.f);
         }
       }
     }

@@ -247,6 +247,9 @@ struct QmmArgs {
   int split_tile;             // first 16-row tile that reads act_hi (a multiple of 4)
   const int32_t* expert_map;  // small regime, nullable: expert -> its slot in this launch's
                               // weight stack, -1 when it is not in the stack (its m-tiles exit)
+  const int8_t* row_exp;      // large int4 regime, nullable: per weight row [n_experts][n_rows]
+                              // the power of two 2^row_exp that brings the row's dequantized
+                              // weights into fp16's normal range (undone in the epilogue)
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3 };

@@ -94,9 +94,10 @@ class TiledExperts(dict):
     """A routed expert stack resident in the MFMA-tiled layout.
 
     Keys: "format" ("int4_g64" | "int6_g64" | "int3_g64" | "bf16"), "codes" (tiled int4 / int6 /
-    int3 words or tiled bf16), "sb" (tiled
-    scale+bias, int4 only), "shape" (E, rows, K), "group_size", "bits", and "awq_scale" (bf16
-    per-input-channel activation scales, or None). Produced from the reference's packed triplet
+    int3 words or tiled bf16), "sb" (tiled scale+bias of the quantized formats), "shape"
+    (E, rows, K), "group_size", "bits", "awq_scale" (bf16 per-input-channel activation scales, or
+    None) and "rexp" (int4: int8 [E, rows] per-row power-of-two exponents of the prefill
+    kernels' fp16 dequant, or None). Produced from the reference's packed triplet
     {packed, scale, bias, group_size, bits} (src/quanta/qwen35/artifact.py:199-203; DeepSeek-V4's
     packed experts add awq_scale, src/quanta/dsv4/artifact.py:252-290) or from a bf16
     [E, rows, K] stack.
@@ -127,11 +128,15 @@ def tile_experts_packed(d: dict) -> TiledExperts:
     E, rows, W = packed.shape
     tile = {4: ops.tile_int4, 6: ops.tile_int6, 3: ops.tile_int3}[bits]
     codes, sb = tile(packed.contiguous(), scale.contiguous(), bias.contiguous(), group_size=gs)
+    # int4 runs on the prefill kernels' fp16 dequant: per-row power-of-two exponents keep any
+    # row's weights in fp16's normal range
+    rexp = (ops.row_exponents(scale.contiguous(), bias.contiguous(), bits=bits, group_size=gs)
+            if bits == 4 else None)
     awq = d.get("awq_scale")
     if awq is not None:
         awq = awq.to(device=packed.device, dtype=torch.bfloat16).contiguous()
     return TiledExperts(format=f"int{bits}_g64", codes=codes, sb=sb, shape=(E, rows, W * 32 // bits),
-                        group_size=gs, bits=bits, awq_scale=awq)
+                        group_size=gs, bits=bits, awq_scale=awq, rexp=rexp)
 
 
 def tile_experts_bf16(stack: torch.Tensor) -> TiledExperts:
@@ -478,6 +483,9 @@ def _build_prepared(p: dict, cfg, *, topk: int | None, regime: int) -> Prepared:
     w.sh_dn = sh_dn.data_ptr() if sh_dn is not None else None
     w.awq_gu = awq_gu.data_ptr() if awq_gu is not None else None
     w.awq_dn = awq_dn.data_ptr() if awq_dn is not None else None
+    gu_rexp, dn_rexp = gu.get("rexp"), dn.get("rexp")
+    w.gu_rexp = gu_rexp.data_ptr() if gu_rexp is not None else None
+    w.dn_rexp = dn_rexp.data_ptr() if dn_rexp is not None else None
     keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn, awq_gu, awq_dn)
     return Prepared(c, w, keep, rw if rkind == "bf16" else None, rw if rkind == "f32" else None,
                     sg32, gu, dn, sh_gu, sh_dn, bias)

@@ -90,6 +90,25 @@ def tile_int4(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
     return codes, sb
 
 
+def row_exponents(scale: torch.Tensor, bias: torch.Tensor, *, bits: int = 4,
+                  group_size: int = 64) -> torch.Tensor:
+    """Per weight row of a native stack's scale/bias [E, rows, K/group_size] (bf16): the int8
+    power-of-two exponent the prefill kernels scale the row's fp16 weights by
+    (qmoe_row_exponents)."""
+    _need(scale, torch.bfloat16, "scale")
+    _need(bias, torch.bfloat16, "bias")
+    if scale.dim() == 2:
+        scale, bias = scale[None], bias[None]
+    if scale.dim() != 3 or bias.shape != scale.shape:
+        raise ValueError("row_exponents: scale/bias must be [E, rows, groups]")
+    E, rows, G = scale.shape
+    out = torch.empty(E, rows, dtype=torch.int8, device=scale.device)
+    L.check(L.load().qmoe_row_exponents(_p(scale), _p(bias), E, rows, G * group_size, bits,
+                                        group_size, _p(out), _stream(scale.device)),
+            "qmoe_row_exponents")
+    return out
+
+
 def _tile_narrow(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, bits: int,
                  group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Native int3/int6 stack [E, rows, K*bits/32] (+ scale/bias [E, rows, K/group_size]) -> the
@@ -226,10 +245,11 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
                 n_experts: int = 1,
                 dense_rows: int = 0, out: torch.Tensor | None = None,
                 ws: torch.Tensor | None = None, glu: int = L.ACT_SILU, glu_alpha: float = 1.0,
-                glu_limit: float = float("inf")) -> torch.Tensor:
+                glu_limit: float = float("inf"), row_exp: torch.Tensor | None = None) -> torch.Tensor:
     """Grouped matmul over expert segments (see qmoe_grouped_qmm). Returns out [out_rows, cols]
     (bf16, or fp32 for EPI_F32); cols = n_rows/2 for SwiGLU else n_rows. `glu`, `glu_alpha`,
-    `glu_limit`: the SwiGLU epilogue's gated activation (L.ACT_*)."""
+    `glu_limit`: the SwiGLU epilogue's gated activation (L.ACT_*). `row_exp`: int4 stacks' per-row
+    exponents (row_exponents) for the large regime's fp16 dequant."""
     _need(act, torch.bfloat16, "act")
     if act.dim() != 2 or act.shape[1] != K:
         raise ValueError("grouped_qmm: act must be [rows, K]")
@@ -242,6 +262,10 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
                   (tile_map, "tile_map")):
         if t is not None:
             _need(t, torch.int32, nm)
+    if row_exp is not None:
+        _need(row_exp, torch.int8, "row_exp")
+        if row_exp.numel() < n_experts * n_rows:
+            raise ValueError("grouped_qmm: row_exp must hold one exponent per weight row")
     cols = n_rows // 2 if epilogue == L.EPI_SWIGLU else n_rows
     dtype = torch.float32 if epilogue == L.EPI_F32 else torch.bfloat16
     if out is None:
@@ -261,7 +285,7 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     L.check(lib.qmoe_grouped_qmm(_p(act), act.shape[0], _p(slot_of), slot_div, n_slots,
                                  _p(offsets), _p(tile_off), _p(tile_map), n_experts, dense_rows,
                                  K, n_rows,
-                                 weight_format, _p(codes), _p(sb), epilogue, int(glu),
+                                 weight_format, _p(codes), _p(sb), _p(row_exp), epilogue, int(glu),
                                  float(glu_alpha), float(glu_limit), _p(out), cols,
                                  regime, _p(ws) if need else None, ws.numel() if need else 0,
                                  _stream(act.device)), "qmoe_grouped_qmm")

@@ -13,7 +13,7 @@ from quanta_amd import _lib as L
 
 def test_library_loads_and_abi_version():
     lib = L.load()
-    assert lib.qmoe_abi_version() == L.ABI_VERSION == 5
+    assert lib.qmoe_abi_version() == L.ABI_VERSION == 6
 
 
 def test_every_header_symbol_is_exported_and_bound():
@@ -61,13 +61,17 @@ _DUMMY = ctypes.c_void_p(16)   # never dereferenced: each call fails validation 
                                       None), "kept groups"),
     (lambda lib: lib.qmoe_combine(None, None, None, 4, 2, 100, None, None, None, None), "H % 8"),
     (lambda lib: lib.qmoe_grouped_qmm(None, 1, None, 1, 1, None, None, None, 1, 1, 128, 16, 0, None,
-                                      None, 0, 0, 1.0, 0.0, None, 16, 1, None, 0, None), "null pointer"),
+                                      None, None, 0, 0, 1.0, 0.0, None, 16, 1, None, 0, None),
+     "null pointer"),
     (lambda lib: lib.qmoe_grouped_qmm(_DUMMY, 1, None, 1, 1, None, None, None, 1, 1, 128, 32, 1,
-                                      _DUMMY, None, 0, 2, 1.0, 0.0, _DUMMY, 16, 1, None, 0, None),
-     "act_limit"),
+                                      _DUMMY, None, None, 0, 2, 1.0, 0.0, _DUMMY, 16, 1, None, 0,
+                                      None), "act_limit"),
     (lambda lib: lib.qmoe_grouped_qmm(_DUMMY, 1, None, 1, 1, None, None, None, 1, 1, 128, 32, 1,
-                                      _DUMMY, None, 0, 5, 1.0, 7.0, _DUMMY, 16, 1, None, 0, None),
-     "unknown act"),
+                                      _DUMMY, None, None, 0, 5, 1.0, 7.0, _DUMMY, 16, 1, None, 0,
+                                      None), "unknown act"),
+    (lambda lib: lib.qmoe_row_exponents(None, None, 1, 16, 128, 4, 64, None, None), "null pointer"),
+    (lambda lib: lib.qmoe_row_exponents(_DUMMY, _DUMMY, 1, 16, 100, 4, 64, _DUMMY, None),
+     "group_size"),
     (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 4, 32, None, None), "group_size 64 or 128"),
     (lambda lib: lib.qmoe_tile_int4(None, None, None, 1, 16, 128, 32, None, None, None), "64 or 128"),
 ])

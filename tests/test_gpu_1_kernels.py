@@ -225,12 +225,19 @@ def test_grouped_qmm_vs_oracle(gpu, fmt, regime, epi, N, k, E, H, rows, use_map)
     m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
     counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(
         torch.from_numpy(idx).to(gpu), E, m_tile)
+    rexp = None
     if fmt == L.FMT_INT4_G64:
         codes, sb = ops.tile_int4(words_dev(w[0], gpu), bf16_dev(w[1], gpu), bf16_dev(w[2], gpu))
+        rexp = ops.row_exponents(bf16_dev(w[1], gpu), bf16_dev(w[2], gpu))
+        # the defining property: each row's largest dequantized magnitude times 2^rexp lies in
+        # [2^13, 2^14)
+        peak = np.abs(dense).max(axis=-1) * np.exp2(rexp.cpu().numpy().astype(np.float64))
+        assert np.all((peak >= 2.0 ** 13) & (peak < 2.0 ** 14))
     else:
         codes, sb = ops.tile_bf16(bf16_dev(oq.f32_to_bf16_bits(w.astype(np.float32)), gpu)), None
     xd = bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu)
     out = ops.grouped_qmm(xd, K=H, n_rows=rows, weight_format=fmt, codes=codes, sb=sb,
+                          row_exp=rexp,
                           epilogue=epi, out_rows=N * k, regime=regime, slot_of=sorted_slot,
                           slot_div=k, n_slots=N * k, offsets=offsets, tile_off=tile_off,
                           tile_map=tile_map if use_map else None, n_experts=E)
