@@ -153,6 +153,18 @@ size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N);
 int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x, int64_t N,
                  uint16_t* y, void* ws, size_t ws_bytes, void* stream);
 
+/* qmoe_forward without allocation, for callers that cannot allocate: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference
+ * (MLX allocates inside its lazy graph). The workspace is a fixed device array inside the library,
+ * QMOE_NOALLOC_SCRATCH_BYTES (64 MiB) on each GPU the library runs on, held until the process
+ * ends; calls whose qmoe_forward_workspace exceeds it are refused (QMOE_EINVAL). Every launch
+ * goes on `stream` (no auxiliary stream or events are created). The call allocates nothing: no
+ * hipMalloc/hipFree, no allocating library routine. Calls that overlap on one GPU race on the
+ * shared scratch: order them on one stream. Same outputs as qmoe_forward, bit for bit. */
+#define QMOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int qmoe_forward_noalloc(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x,
+                         int64_t N, uint16_t* y, void* stream);
+
 /* Routed experts whose widths vary per (expert, projection) (Kimi's QuantizedSparseMoE,
  * src/quanta/modeling/quantized.py:40-84: one packed stack per projection and width, each expert
  * carrying per projection its width and its slot in that width's stack). Each stack is tiled as

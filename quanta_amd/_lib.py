@@ -24,6 +24,7 @@ EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
 ABI_VERSION = 6
+NOALLOC_SCRATCH_BYTES = 64 << 20   # QMOE_NOALLOC_SCRATCH_BYTES
 
 
 def mtile_upper_bound(mc: int, n_experts: int, m_tile: int) -> int:
@@ -108,6 +109,8 @@ SIGNATURES = {
     "qmoe_forward_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),
     "qmoe_forward": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _I64, _P, _P,
                           ctypes.c_size_t, _P]),
+    "qmoe_forward_noalloc": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights), _P, _I64,
+                                  _P, _P]),
     "qmoe_forward_mixed": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeWeights),
                                 ctypes.POINTER(QmoeMixed), _P, _I64, _P, _P, ctypes.c_size_t, _P]),
     "qmoe_forward_residual_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeConfig), _I64]),

@@ -547,9 +547,12 @@ static int pick_regime(const qmoe_config_t& c, int64_t N) {
 }
 
 // The block on x; with resid, the combine adds the decoder layer's residual row.
+// single_stream: every launch on the caller's stream (no auxiliary stream or events, which are
+// created on first use), for the entry point that allocates nothing.
 static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
                         int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream_,
-                        const uint16_t* resid, const qmoe_mixed_t* mixed = nullptr) {
+                        const uint16_t* resid, const qmoe_mixed_t* mixed = nullptr,
+                        bool single_stream = false) {
   if (!cfg || !wts || !x || !y || !ws) return fail("qmoe_forward: null pointer");
   const qmoe_config_t& c = *cfg;
   int rc = validate_config(c);
@@ -638,7 +641,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (err == hipSuccess) err = hipStreamWaitEvent(to, ev, 0);
     return err == hipSuccess ? 0 : fail(std::string("forward: ") + what + ": " + hipGetErrorString(err));
   };
-  if (shared_aux || hybrid) {
+  if ((shared_aux || hybrid) && !single_stream) {
     aux_lock = std::unique_lock<std::mutex>(g_aux_mu);
     rc = aux_stream(stream, &aux);
     if (rc) return rc;
@@ -650,10 +653,12 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // first on the auxiliary stream, beside the routing chain (hybrid implies int4 or bf16 experts)
   const bool f16_acts = (hybrid && gfmt == FMT_INT4);
   if (f16_acts) {
-    rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, aux->s);
+    rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, aux ? aux->s : stream);
     if (rc) return rc;
-    const hipError_t err = hipEventRecord(aux->xready, aux->s);
-    if (err != hipSuccess) return fail(std::string("forward: x16 record: ") + hipGetErrorString(err));
+    if (aux) {
+      const hipError_t err = hipEventRecord(aux->xready, aux->s);
+      if (err != hipSuccess) return fail(std::string("forward: x16 record: ") + hipGetErrorString(err));
+    }
   }
 
   // 1. shared expert gate_up + SwiGLU -> sh_h (fused with the router below when decoding)
@@ -720,7 +725,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   }
   // the cold experts' tiles wait for the permute on the auxiliary stream
   hipStream_t cstream = stream;
-  if (hybrid) {
+  if (hybrid && aux) {
     rc = link(aux->perm, stream, aux->s, "permute to auxiliary stream");
     if (rc) return rc;
     cstream = aux->s;
@@ -798,13 +803,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.row_exp = (gfmt == FMT_INT4) ? wts->gu_rexp : nullptr;
     a.out = h; a.ld_out = c.inter;
     a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
-    if (f16_acts) {   // the fp16 copy of x, made on the auxiliary stream at the fork
+    if (f16_acts && aux) {   // the fp16 copy of x, made on the auxiliary stream at the fork
       const hipError_t err = hipStreamWaitEvent(stream, aux->xready, 0);
       if (err != hipSuccess) return fail(std::string("forward: x16 wait: ") + hipGetErrorString(err));
     }
     rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
     if (rc) return rc;
-    if (hybrid) {   // h complete (cold rows from the auxiliary stream) before its fp16 copy
+    if (hybrid && aux) {   // h complete (cold rows from the auxiliary stream) before its fp16 copy
       rc = link(aux->cold, aux->s, stream, "cold gate_up");
       if (rc) return rc;
     }
@@ -821,7 +826,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);
       if (rc) return rc;
     }
-    if (hybrid) {   // the cold down reads bf16 h, complete since the cold gate_up join
+    if (hybrid && aux) {   // the cold down reads bf16 h, complete since the cold gate_up join
       rc = link(aux->hready, stream, aux->s, "h to auxiliary stream");
       if (rc) return rc;
     }
@@ -884,4 +889,60 @@ extern "C" int qmoe_forward_residual(const qmoe_config_t* cfg, const qmoe_weight
   rc = launch_rmsnorm(x, norm_w, N, cfg->hidden, eps, xn, static_cast<hipStream_t>(stream));
   if (rc) return rc;
   return forward_impl(cfg, wts, xn, N, y, ws, main, stream, x);
+}
+
+// ------------------------------------------------------------------ allocation-free entry point
+// qmoe_forward for callers that cannot allocate (HIP graph capture, serving loops, harnesses that
+// forbid hipMalloc): the per-call workspace is a file-scope device array of fixed size, one copy
+// per GPU the library runs on, held until the process ends, and every launch goes on the
+// caller's stream (no auxiliary stream or events, which qmoe_forward creates on first use).
+// The array's host-side name is not a device address: its address on each device comes from
+// hipGetSymbolAddress, taken once per device with that device current, and only that pointer is
+// handed to kernels. Calls on one GPU share the array, so calls that overlap on one GPU race;
+// nothing in it needs to start at zero (qmoe_forward takes uninitialised workspace too).
+constexpr size_t kScratchBytes = static_cast<size_t>(QMOE_NOALLOC_SCRATCH_BYTES);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kScratchMaxDevices = 64;
+static void* g_scratch_ptr[kScratchMaxDevices];   // per device: scratch's device address
+static std::mutex g_scratch_mu;
+
+static int scratch_on(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t err = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(std::string("qmoe_forward_noalloc: stream device: ") + hipGetErrorString(err));
+  if (dev < 0 || dev >= kScratchMaxDevices) return fail("qmoe_forward_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    err = hipGetDevice(&cur);
+    if (err == hipSuccess && cur != dev) err = hipSetDevice(dev);
+    void* p = nullptr;
+    if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (err != hipSuccess || !p)
+      return fail(std::string("qmoe_forward_noalloc: hipGetSymbolAddress(scratch): ") +
+                  (err != hipSuccess ? hipGetErrorString(err) : "null address"));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" int qmoe_forward_noalloc(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
+                                    const uint16_t* x, int64_t N, uint16_t* y, void* stream) {
+  if (!cfg || !wts || !x || !y) return fail("qmoe_forward_noalloc: null pointer");
+  int rc = validate_config(*cfg);
+  if (rc) return rc;
+  if (N <= 0 || N > 65535) return fail("qmoe_forward_noalloc: 0 < N <= 65535 tokens per call");
+  const size_t need = ws_layout(*cfg, N).total;
+  if (need > kScratchBytes)
+    return fail("qmoe_forward_noalloc: " + std::to_string(N) + " tokens need " +
+                std::to_string(need) + " bytes of workspace, more than the fixed " +
+                std::to_string(kScratchBytes) + "-byte scratch; call qmoe_forward with a "
+                "workspace, or pass fewer tokens per call");
+  void* ws = nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = scratch_on(st, &ws);
+  if (rc) return rc;
+  return forward_impl(cfg, wts, x, N, y, ws, kScratchBytes, stream, nullptr, nullptr, true);
 }

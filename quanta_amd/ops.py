@@ -339,6 +339,21 @@ def forward(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
     return out
 
 
+def forward_noalloc(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
+                    out: torch.Tensor) -> torch.Tensor:
+    """Whole block on x [N, H] bf16 into `out` (qmoe_forward_noalloc): the library's fixed
+    per-GPU scratch in place of a workspace, every launch on the current stream, nothing
+    allocated (the caller passes `out`)."""
+    _need(x, torch.bfloat16, "x")
+    _need(out, torch.bfloat16, "out")
+    N, H = x.shape
+    if H != cfg.hidden or out.shape != x.shape:
+        raise ValueError("forward_noalloc: x / out do not match the config's hidden size")
+    L.check(L.load().qmoe_forward_noalloc(ctypes.byref(cfg), ctypes.byref(weights), _p(x), N,
+                                          _p(out), _stream(x.device)), "qmoe_forward_noalloc")
+    return out
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
             out: torch.Tensor | None = None) -> torch.Tensor:
     """RMSNorm rows of x [N, H] bf16 with the resident bf16 weight [H] (qmoe_rmsnorm):

@@ -70,6 +70,7 @@ _DUMMY = ctypes.c_void_p(16)   # never dereferenced: each call fails validation 
                                       _DUMMY, None, None, 0, 5, 1.0, 7.0, _DUMMY, 16, 1, None, 0,
                                       None), "unknown act"),
     (lambda lib: lib.qmoe_row_exponents(None, None, 1, 16, 128, 4, 64, None, None), "null pointer"),
+    (lambda lib: lib.qmoe_forward_noalloc(None, None, None, 1, None, None), "null pointer"),
     (lambda lib: lib.qmoe_row_exponents(_DUMMY, _DUMMY, 1, 16, 100, 4, 64, _DUMMY, None),
      "group_size"),
     (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 4, 32, None, None), "group_size 64 or 128"),
