@@ -9,6 +9,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <mutex>
 #include <string>
@@ -273,8 +274,34 @@ struct AuxStream {
 };
 static std::mutex g_aux_mu;
 constexpr int64_t kFuseSharedMaxTokens = 64;
-// Largest batch routed slot-major (no permute launch).
-constexpr int64_t kSlotMajorMaxTokens = 2;
+// Slot-major routing (no permute launch) reads an expert once per slot that picks it, the
+// permute once per call; the permute launch costs about as much as streaming this many bytes.
+constexpr double kPermuteLaunchBytes = 24e6;
+constexpr int64_t kSlotMajorCapTokens = 16;
+
+// Routed expert bytes (gate_up + down) of one expert in the config's formats.
+static double expert_bytes(const qmoe_config_t& c) {
+  auto per_weight = [](int fmt) {
+    return fmt == QMOE_FMT_BF16 ? 2.0 : fmt == QMOE_FMT_INT6_G64 ? 6.5 / 8 :
+           fmt == QMOE_FMT_INT3_G64 ? 3.5 / 8 : 4.5 / 8;
+  };
+  const double iw = static_cast<double>(c.inter) * c.hidden;
+  return 2.0 * iw * per_weight(c.expert_format) + iw * per_weight(c.down_format);
+}
+
+// Largest batch routed slot-major: at least 2 tokens; more while the expected number of
+// duplicate expert reads under uniform routing, N*k - E*(1 - (1 - k/E)^N), costs fewer bytes
+// than the permute launch (c1's shape: 8 tokens and more; c2's: 5).
+static int64_t slot_major_max_tokens(const qmoe_config_t& c) {
+  const double k = c.top_k, E = c.n_experts, be = expert_bytes(c);
+  int64_t n = 2;
+  for (int64_t t = 3; t <= kSlotMajorCapTokens; ++t) {
+    const double dup = t * k - E * (1.0 - std::pow(1.0 - k / E, static_cast<double>(t)));
+    if (dup * be > kPermuteLaunchBytes) break;
+    n = t;
+  }
+  return n;
+}
 static std::map<int, AuxStream> g_aux;
 
 static int aux_stream(hipStream_t caller, AuxStream** out) {
@@ -328,10 +355,10 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.offsets = take(static_cast<size_t>(c.n_experts + 1) * 4);
   L.tile_off = take(static_cast<size_t>(c.n_experts + 1) * 4);
   // tile descriptors for whichever m-tile the regime uses (16 needs the most entries); the
-  // slot-major map of one or two tokens has one tile per slot, which can exceed that bound when
+  // slot-major map of a few tokens has one tile per slot, which can exceed that bound when
   // k > E / 2
   L.max_tiles = mtile_upper_bound(mc, c.n_experts, kSmallMTile);
-  if (N <= kSlotMajorMaxTokens) L.max_tiles = std::max<int64_t>(L.max_tiles, mc);
+  if (N <= slot_major_max_tokens(c)) L.max_tiles = std::max<int64_t>(L.max_tiles, mc);
   L.tile_map = take(static_cast<size_t>(L.max_tiles) * 16);
   // large-M regime: 128-row tiles of the experts above the hybrid split
   L.max_tiles_big = mtile_upper_bound(mc, c.n_experts, kLargeMTile);
@@ -549,11 +576,16 @@ static int pick_regime(const qmoe_config_t& c, int64_t N) {
 // The block on x; with resid, the combine adds the decoder layer's residual row.
 // single_stream: every launch on the caller's stream (no auxiliary stream or events, which are
 // created on first use), for the entry point that allocates nothing.
-static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
+// norm_w: the decoder layer's RMSNorm in front of the block (qmoe_forward_residual): x is the raw
+// residual row, the block runs on xn = rmsnorm(x) (written to `xn`, outside ws), and the combine
+// adds x back. For small decode batches the norm runs inside the router launch; otherwise it is
+// a launch of its own, first.
+static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x_in,
                         int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream_,
-                        const uint16_t* resid, const qmoe_mixed_t* mixed = nullptr,
-                        bool single_stream = false) {
-  if (!cfg || !wts || !x || !y || !ws) return fail("qmoe_forward: null pointer");
+                        const qmoe_mixed_t* mixed = nullptr, bool single_stream = false,
+                        const uint16_t* norm_w = nullptr, float norm_eps = 0.f,
+                        uint16_t* xn = nullptr) {
+  if (!cfg || !wts || !x_in || !y || !ws || (norm_w && !xn)) return fail("qmoe_forward: null pointer");
   const qmoe_config_t& c = *cfg;
   int rc = validate_config(c);
   if (rc) return rc;
@@ -625,11 +657,21 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // expert's re-read weights cost more than the auxiliary stream's join)
   const bool fuse = decode && shared && N <= kFuseSharedMaxTokens;
   const bool fuse_gu = fuse && c.router_format == QMOE_ROUTER_BF16_TILED;
+  // the block's input rows: x itself, or its RMSNorm (made inside the router launch when that is
+  // the fused pair, else by a launch of its own ahead of everything)
+  const uint16_t* resid = norm_w ? x_in : nullptr;
+  const uint16_t* x = norm_w ? xn : x_in;
+  // (the router launch normalises the rows when its shape allows, pair_norm_fusable)
+  const bool fuse_norm = norm_w && fuse_gu && pair_norm_fusable(c.hidden, N);
+  if (norm_w && !fuse_norm) {
+    rc = launch_rmsnorm(x_in, norm_w, N, c.hidden, norm_eps, xn, static_cast<hipStream_t>(stream_));
+    if (rc) return rc;
+  }
   const bool fuse_dn = fuse && bf16_chunks(c.shared_inter) <= 8;
-  // one or two tokens: slot-major routing written by the top-k, no permute launch (each slot
+  // a few tokens: slot-major routing written by the top-k, no permute launch (each slot
   // its own m-tile; an expert two tokens share is read twice, cheaper than the launch)
   // (AWQ prescaling finds each row's expert from the permute's segment offsets)
-  const bool slot_major = !hybrid && N <= kSlotMajorMaxTokens && !c.awq;
+  const bool slot_major = !hybrid && N <= slot_major_max_tokens(c) && !c.awq;
   // m-tiles of the small-kernel launches: one per slot when slot-major
   const int64_t tiles_small = slot_major ? std::max<int64_t>(bound_small, mc) : bound_small;
   std::unique_lock<std::mutex> aux_lock;
@@ -700,6 +742,10 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.act = x; a.act_rows = N; a.slot_div = 1; a.dense_rows = N; a.n_experts = 1;
     a.K = c.hidden; a.n_rows = decode ? std::min(live_rows, c.router_rows) : c.router_rows;
     a.codes = wts->router_w; a.out = logits; a.ld_out = ld;
+    if (fuse_norm) {   // both products read the raw rows and normalise them; the router writes xn
+      a.act = x_in; a.norm_w = norm_w; a.norm_eps = norm_eps; a.norm_out = xn;
+      sgu.act = x_in; sgu.norm_w = norm_w; sgu.norm_eps = norm_eps;
+    }
     if (fuse_gu)
       rc = launch_qmm_pair_bf16(a, sgu, stream);
     else
@@ -857,14 +903,14 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
 
 extern "C" int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* wts, const uint16_t* x,
                             int64_t N, uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
-  return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream, nullptr);
+  return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream);
 }
 
 extern "C" int qmoe_forward_mixed(const qmoe_config_t* cfg, const qmoe_weights_t* wts,
                                   const qmoe_mixed_t* mixed, const uint16_t* x, int64_t N,
                                   uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
   if (!mixed) return fail("qmoe_forward_mixed: null pointer");
-  return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream, nullptr, mixed);
+  return forward_impl(cfg, wts, x, N, y, ws, ws_bytes, stream, mixed);
 }
 
 // The block with the decoder layer's steps either side of it: the normalised rows go to the
@@ -885,10 +931,9 @@ extern "C" int qmoe_forward_residual(const qmoe_config_t* cfg, const qmoe_weight
   const size_t main = ws_layout(*cfg, N).total;
   if (ws_bytes < qmoe_forward_residual_workspace(cfg, N))
     return fail("qmoe_forward_residual: workspace too small");
+  if (!(eps >= 0.f) || !isfinite(eps)) return fail("qmoe_forward_residual: eps must be finite and >= 0");
   uint16_t* xn = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + main);
-  rc = launch_rmsnorm(x, norm_w, N, cfg->hidden, eps, xn, static_cast<hipStream_t>(stream));
-  if (rc) return rc;
-  return forward_impl(cfg, wts, xn, N, y, ws, main, stream, x);
+  return forward_impl(cfg, wts, x, N, y, ws, main, stream, nullptr, false, norm_w, eps, xn);
 }
 
 // ------------------------------------------------------------------ allocation-free entry point
@@ -944,5 +989,5 @@ extern "C" int qmoe_forward_noalloc(const qmoe_config_t* cfg, const qmoe_weights
   hipStream_t st = static_cast<hipStream_t>(stream);
   rc = scratch_on(st, &ws);
   if (rc) return rc;
-  return forward_impl(cfg, wts, x, N, y, ws, kScratchBytes, stream, nullptr, nullptr, true);
+  return forward_impl(cfg, wts, x, N, y, ws, kScratchBytes, stream, nullptr, true);
 }

@@ -328,7 +328,7 @@ __global__ void __launch_bounds__(256) tile_bf16_kernel(const uint16_t* __restri
 }
 
 // ---------------------------------------------------------------------------- row exponents
-// One thread per weight row: M = the row's largest dequantized magnitude, max over its groups of
+// One wavefront per weight row: M = the row's largest dequantized magnitude, max over its groups of
 // max(|b|, |qmax * s + b|) (the affine map is monotone in the code, so its extremes sit at codes
 // 0 and qmax), and row_exp = 14 - ex with 2^(ex-1) <= M < 2^ex, so every weight of the row times
 // 2^row_exp lies below 2^14 and fp16 holds it at full precision down to 2^-14 of that (2^28 of
@@ -337,15 +337,19 @@ __global__ void __launch_bounds__(256) row_exp_kernel(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ bias,
                                                       int64_t n_rows, int groups, float qmax,
                                                       int8_t* __restrict__ row_exp) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= n_rows) return;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n_rows) return;   // the whole wavefront
   const uint16_t* sr = scale + r * groups;
   const uint16_t* br = bias + r * groups;
   float m = 0.f;
-  for (int g = 0; g < groups; ++g) {
+  for (int g = lane; g < groups; g += 64) {
     const float sv = bf16_to_f32(sr[g]), bv = bf16_to_f32(br[g]);
     m = fmaxf(m, fmaxf(fabsf(bv), fabsf(fmaf(qmax, sv, bv))));
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane) return;
   int ex = 0;
   if (m > 0.f && m <= 3.4e38f) {
     frexpf(m, &ex);
@@ -410,7 +414,7 @@ extern "C" int qmoe_row_exponents(const uint16_t* scale, const uint16_t* bias, i
   if (bits < 2 || bits > 8) return fail("qmoe_row_exponents: 2 <= bits <= 8");
   if (group_size <= 0 || in_features % group_size) return fail("qmoe_row_exponents: in % group_size != 0");
   const int64_t n = n_mats * rows;
-  row_exp_kernel<<<grid_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+  row_exp_kernel<<<grid_for(n, 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
       scale, bias, n, static_cast<int>(in_features / group_size), static_cast<float>((1 << bits) - 1),
       row_exp);
   return check_launch("row_exponents");

@@ -127,7 +127,7 @@ struct SmallCfg {
 // Body of one workgroup: job block `bx` of m-tile `by` (MT > 1, dense bf16 products only:
 // m-tiles by*MT .. by*MT+MT-1, every weight fragment feeding MT MFMAs), chunk sums in `red`
 // (LDS).
-template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1>
+template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1, bool NORM = false>
 __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx, int by,
                                            f32x4_t* red) {
   using C = SmallCfg<FMT, EPI, W, CPW, JPW, MT>;
@@ -345,8 +345,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       // Batches of steps: all loads of a batch issue before its MFMAs (indices clamped into
       // the range, so no load is conditional); the MFMAs run in step order.
       constexpr int BS = (MT > 1) ? 4 : 8;
-      for (int cb = k0; cb < k1; cb += BS) {
-        u32x4 wv[BS][NT], xv[BS][MT];
+      auto load_batch = [&](int cb, u32x4 (&wv)[BS][NT], u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           const int c = min(cb + i, k1 - 1);
@@ -355,6 +354,17 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
 #pragma unroll
           for (int u = 0; u < MT; ++u) xv[i][u] = xp[u][c * 4];
         }
+      };
+      // RMSNorm on the fly (NORM, the bf16 pair launch; the launcher guarantees W >= 4, so the
+      // workgroup is one job and every wavefront reaches the barrier): the rows' sums of squares
+      // over the job's W chunks in the canonical order of rmsnorm_row (lane group sums over the
+      // chunk's steps in order, then (g0 + g1) + (g2 + g3), then the chunks in order), taken while
+      // the first batch's weights are already in flight; each activation fragment is then
+      // normalised, bf16(w * (x * r)), and job 0 writes the normalised rows for later launches.
+      float rn[MT];
+      u32x4* outp[MT];
+      const u32x4* wnp = NORM ? reinterpret_cast<const u32x4*>(a.norm_w) + lg : nullptr;
+      auto mma_batch = [&](int cb, const u32x4 (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           if (cb + i < k1) {
@@ -365,6 +375,113 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
                 accm[u][t] = mfma16(as_bf16x8(xv[i][u]), as_bf16x8(wv[i][t]), accm[u][t]);
           }
         }
+      };
+      // NORM: each step's fragments normalised right before its MFMAs (short register lives)
+      auto norm_mma_batch = [&](int cb, const u32x4 (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < BS; ++i) {
+          const int c = min(cb + i, k1 - 1);
+          const u32x4 g = wnp[c * 4];
+#pragma unroll
+          for (int u = 0; u < MT; ++u) {
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              o[j] = pack_bf16x2_rne(bf16lo_to_f32(g[j]) * (bf16lo_to_f32(xv[i][u][j]) * rn[u]),
+                                     bf16hi_to_f32(g[j]) * (bf16hi_to_f32(xv[i][u][j]) * rn[u]));
+            if (outp[u]) outp[u][c * 4] = o;
+            if (cb + i < k1) {
+#pragma unroll
+              for (int t = 0; t < NT; ++t) accm[u][t] = mfma16(as_bf16x8(o), as_bf16x8(wv[i][t]), accm[u][t]);
+            }
+          }
+        }
+      };
+      int cb = k0;
+      if constexpr (NORM) {
+        auto sq = [&](float acc, u32x4 v) __attribute__((always_inline)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float lo = bf16lo_to_f32(v[j]), hi = bf16hi_to_f32(v[j]);
+            acc = fmaf(lo, lo, acc);
+            acc = fmaf(hi, hi, acc);
+          }
+          return acc;
+        };
+        float ssl[MT];
+#pragma unroll
+        for (int u = 0; u < MT; ++u) ssl[u] = 0.f;
+        u32x4 wv[BS][NT], xv[BS][MT];
+        const bool one_batch = k1 - k0 <= BS;
+        if (one_batch) {
+          // the batch's activations, then its weights: loads complete in issue order, so the
+          // sums wait only for the activations and the weights stay in flight over the barrier
+#pragma unroll
+          for (int i = 0; i < BS; ++i) {
+            const int c = min(cb + i, k1 - 1);
+#pragma unroll
+            for (int u = 0; u < MT; ++u) xv[i][u] = xp[u][c * 4];
+          }
+#pragma unroll
+          for (int i = 0; i < BS; ++i) {
+            const int c = min(cb + i, k1 - 1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) wv[i][t] = wp[t][c * 64];
+          }
+#pragma unroll
+          for (int i = 0; i < BS; ++i)
+            if (cb + i < k1) {
+#pragma unroll
+              for (int u = 0; u < MT; ++u) ssl[u] = sq(ssl[u], xv[i][u]);
+            }
+        } else {
+          // a longer chunk (pair_norm_fusable: at most NS steps): all its activations at once,
+          // summed in step order; the products re-read them (L1/L2 hits)
+          constexpr int NS = (MT > 1) ? 8 : 16;
+          u32x4 xs[NS][MT];
+#pragma unroll
+          for (int i = 0; i < NS; ++i) {
+            const int c = min(k0 + i, k1 - 1);
+#pragma unroll
+            for (int u = 0; u < MT; ++u) xs[i][u] = xp[u][c * 4];
+          }
+#pragma unroll
+          for (int i = 0; i < NS; ++i)
+            if (k0 + i < k1) {
+#pragma unroll
+              for (int u = 0; u < MT; ++u) ssl[u] = sq(ssl[u], xs[i][u]);
+            }
+        }
+        float* nred = reinterpret_cast<float*>(red + SmallCfg<FMT, EPI, W, CPW, JPW, MT>::RED);
+#pragma unroll
+        for (int u = 0; u < MT; ++u) {
+          ssl[u] += __shfl_xor(ssl[u], 16);
+          ssl[u] += __shfl_xor(ssl[u], 32);
+          if (lg == 0) nred[(wave * MT + u) * 16 + mrow] = ssl[u];
+        }
+        __syncthreads();
+        const bool wr_norm = a.norm_out && job == 0;
+#pragma unroll
+        for (int u = 0; u < MT; ++u) {
+          float ss = nred[u * 16 + mrow];
+          for (int c = 1; c < W; ++c) ss += nred[(c * MT + u) * 16 + mrow];
+          rn[u] = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.norm_eps);
+          outp[u] = (wr_norm && mrow < mtc[u])
+                        ? reinterpret_cast<u32x4*>(a.norm_out + static_cast<int64_t>(mt0[u] + mrow) * a.K) + lg
+                        : nullptr;
+        }
+        if (one_batch) {
+          norm_mma_batch(cb, wv, xv);
+          cb += BS;
+        }
+      }
+      for (; cb < k1; cb += BS) {
+        u32x4 wv[BS][NT], xv[BS][MT];
+        load_batch(cb, wv, xv);
+        if constexpr (NORM)
+          norm_mma_batch(cb, wv, xv);
+        else
+          mma_batch(cb, wv, xv);
       }
     }
   }
@@ -435,16 +552,21 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
 // Two dense bf16 products over the same activation rows in one launch (the router logits and
 // the shared expert's gate_up): job blocks [0, gx1) run the first, the rest the second. Both
 // use the same K, so the same chunking W, and each keeps the arithmetic of its own launch.
-template <int EPI1, int EPI2, int W, int MT>
+// NORM: both products RMSNorm their activation rows on the fly (QmmArgs::norm_w), and the first
+// product's job 0 writes the normalised rows (norm_out).
+template <int EPI1, int EPI2, int W, int MT, bool NORM = false>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
 qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2) {
   constexpr int R1 = SmallCfg<FMT_BF16, EPI1, W, 1, 1, MT>::RED;
   constexpr int R2 = SmallCfg<FMT_BF16, EPI2, W, 1, 1, MT>::RED;
-  __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
+  constexpr int RR = R1 > R2 ? R1 : R2;
+  // (NORM: behind the chunk sums, the norm's chunk sums [WAVES][MT][16] floats)
+  constexpr int WAVES = W > 4 ? W : 4;
+  __shared__ f32x4_t red[RR + (NORM ? (WAVES * MT * 16 + 3) / 4 : 0)];
   if (static_cast<int>(blockIdx.x) < gx1)
-    small_body<FMT_BF16, EPI1, W, 1, 1, MT>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
+    small_body<FMT_BF16, EPI1, W, 1, 1, MT, NORM>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
   else
-    small_body<FMT_BF16, EPI2, W, 1, 1, MT>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
+    small_body<FMT_BF16, EPI2, W, 1, 1, MT, NORM>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
 }
 
 // ============================================================================ large-M kernel
@@ -1185,19 +1307,40 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
   constexpr int JPWG = WAVES / W;
   const int n1 = a1.n_rows / 16, n2 = a2.n_rows / 32;   // fp32 epilogue jobs, SwiGLU jobs
   const int gx1 = (n1 + JPWG - 1) / JPWG, gx2 = (n2 + JPWG - 1) / JPWG;
-  if (mtiles >= kSmallMt2MinTiles)   // two m-tiles per wavefront, as in launch_small_k
-    qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2>
-        <<<dim3(gx1 + gx2, static_cast<unsigned>((mtiles + 1) / 2)), 64 * WAVES, 0, stream>>>(
-            a1, n1, gx1, a2, n2);
-  else
-    qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1>
-        <<<dim3(gx1 + gx2, static_cast<unsigned>(mtiles)), 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+  const dim3 g2(gx1 + gx2, static_cast<unsigned>((mtiles + 1) / 2)), g1(gx1 + gx2, static_cast<unsigned>(mtiles));
+  if (a1.norm_w) {
+    if (mtiles >= kSmallMt2MinTiles)   // two m-tiles per wavefront, as in launch_small_k
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2, true><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+    else
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1, true><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+  } else {
+    if (mtiles >= kSmallMt2MinTiles)
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+    else
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+  }
+}
+
+bool pair_norm_fusable(int K, int64_t rows) {
+  const int W = bf16_chunks(K);
+  const int64_t mtiles = (rows + kSmallMTile - 1) / kSmallMTile;
+  const bool mt2 = mtiles >= kSmallMt2MinTiles;
+  const int nks = K / 32, steps = (nks + W - 1) / W;
+  if (K % 32 || W < 4) return false;
+  // one load batch per chunk: the norm's sums overlap the first weight loads (measured within
+  // 3 us of the plain launch); longer chunks only for one or two tokens, where the separate norm
+  // launch costs a kernel boundary more than the fused pass does
+  return steps <= (mt2 ? 4 : 8) || (rows <= 2 && steps <= 16);
 }
 
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream) {
   if (a1.offsets || a2.offsets || a1.dense_rows != a2.dense_rows || a1.K != a2.K || a1.K % 32 ||
       a1.n_rows % 16 || a2.n_rows % 32 || a1.dense_rows <= 0)
     return fail("qmm pair: two dense bf16 products over the same rows and K required");
+  if ((a1.norm_w != nullptr) != (a2.norm_w != nullptr) || a2.norm_out)
+    return fail("qmm pair: the fused norm applies to both products; the first writes the rows");
+  if (a1.norm_w && !pair_norm_fusable(a1.K, a1.dense_rows))
+    return fail("qmm pair: the fused norm needs one job per workgroup and one load batch per chunk");
   const int64_t mtiles = (a1.dense_rows + kSmallMTile - 1) / kSmallMTile;
   if (mtiles > 65535) return fail("qmm pair: too many m-tiles for one launch");
   switch (bf16_chunks(a1.K)) {

@@ -55,6 +55,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
+// The same round-to-nearest-even pack in one instruction (gfx950's v_cvt_pk_bf16_f32): equal to
+// pack_bf16x2 for every non-NaN input (a NaN stays a NaN, its payload may differ). Used where the
+// conversion is the hot loop (the RMSNorm paths, which both use it, so they agree bit for bit).
+typedef __bf16 bf16x2_hw_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_hw_t));
+}
 
 // Native word (nibble i = code i) <-> stored tiled word (nibbles [c0 c2 c4 c6 c1 c3 c5 c7]).
 __host__ __device__ __forceinline__ uint32_t interleave_nibbles(uint32_t w) {
@@ -250,6 +258,11 @@ struct QmmArgs {
   const int8_t* row_exp;      // large int4 regime, nullable: per weight row [n_experts][n_rows]
                               // the power of two 2^row_exp that brings the row's dequantized
                               // weights into fp16's normal range (undone in the epilogue)
+  const uint16_t* norm_w;     // dense bf16 pair launch, nullable: the rows of `act` are RMSNorm'd
+                              // on the fly, bf16(norm_w * (x * r)), r = 1/sqrt(mean(x^2) + eps)
+                              // summed in the canonical order of rmsnorm_row (norm.hip)
+  float norm_eps;
+  uint16_t* norm_out;         // nullable: the normalised rows, written by job 0's wavefronts
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3 };
@@ -268,6 +281,10 @@ inline int bf16_chunks(int K) {
 // One launch of two dense bf16 small-regime products over the same rows and K: a1 with the
 // fp32 epilogue (router logits), a2 with SwiGLU (shared expert gate_up).
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream);
+// Whether the pair launch over `rows` rows of K normalises them itself (QmmArgs::norm_w): one
+// job per workgroup (K >= 1024), and each wavefront's K chunk one load batch (8 32-wide steps
+// with one m-tile per wavefront, 4 with two), or up to 16 steps for one or two rows.
+bool pair_norm_fusable(int K, int64_t rows);
 // Decode combine with the shared expert's down projection fused in (wd: tiled bf16 [H, Is]).
 // resid (nullable): the decoder layer's residual row, y = bf16(resid + bf16(block output)).
 int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
@@ -297,6 +314,10 @@ int launch_awq_prescale(const uint16_t* x, const int32_t* sorted, const int32_t*
 int launch_awq_glu(const uint16_t* gu, const int32_t* offsets, int E, int64_t mc, int I,
                    const uint16_t* s_dn, int act, float alpha, float limit, uint16_t* h,
                    hipStream_t stream);
+// For H % 32 == 0 the sum of squares follows the canonical order that the fused-norm pair launch
+// also follows: H cut into bf16_chunks(H) chunks of 32-wide steps; within a chunk, lane group g
+// (0..3) sums the elements 32 s + 8 g + j (steps s in order, j = 0..7 in order) with fmaf from
+// zero; the four group sums combine as (g0 + g1) + (g2 + g3); the chunk sums add in chunk order.
 int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float eps, uint16_t* out,
                    hipStream_t stream);
 

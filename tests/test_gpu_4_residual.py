@@ -35,7 +35,8 @@ def _ulp_bf16(v: np.ndarray) -> np.ndarray:
     return 2.0 ** (e - 7)
 
 
-@pytest.mark.parametrize("N,H,eps", [(1, 512, EPS), (37, 4096, EPS), (9, 7168, 1e-5), (4, 2048, 0.25)])
+@pytest.mark.parametrize("N,H,eps", [(1, 512, EPS), (37, 4096, EPS), (9, 7168, 1e-5), (4, 2048, 0.25),
+                                     (6, 200, EPS)])
 def test_rmsnorm_vs_oracle(gpu, N, H, eps):
     rng = np.random.default_rng(N * 7 + H)
     x = rng.standard_normal((N, H)) * 3.0
@@ -64,11 +65,14 @@ def _parts(x, p, cfg, nw, eps):
     return (x.float() + ym.float()).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("name,N", [("c1", 1), ("c1", 64), ("c2", 2), ("c2", 32), ("c2", 300), ("c3", 16)])
+@pytest.mark.parametrize("name,N", [("c1", 1), ("c1", 17), ("c1", 64), ("c2", 2), ("c2", 8), ("c2", 32),
+                                    ("c2", 49), ("c2", 65), ("c2", 300), ("c3", 1), ("c3", 16),
+                                    ("c0", 8)])
 def test_residual_equals_its_parts(gpu, name, N):
-    """The fused call (norm into the workspace, residual add in the combine) against qmoe_rmsnorm
-    + qmoe_forward + a bf16 add: bit for bit, in every regime the token count selects (slot-major
-    top-k, fused shared expert, auxiliary-stream shared expert, hybrid prefill); and in place."""
+    """The fused call against qmoe_rmsnorm + qmoe_forward + a bf16 add: bit for bit, in every
+    regime the token count selects (up to 64 tokens the norm runs inside the router launch, one
+    or two m-tiles per wavefront; above, and with c0's fp32 router, as a launch of its own;
+    slot-major top-k, auxiliary-stream shared expert, hybrid prefill); and in place."""
     cfg = synth.spec(name).cfg
     p = _layer(name, gpu)
     x = (synth.make_inputs(name, N, device=gpu, seed=N).float() * 4.0).to(torch.bfloat16)
