@@ -71,7 +71,8 @@ def parse():
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
     ap.add_argument("--write-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="summarise two rocprofv3 counter runs into profiles/hbm_traffic.json")
+                    help="summarise two rocprofv3 counter runs into profiles/hbm_traffic.json "
+                         "(the workload of --batch / --zipf: its dominant gate_up kernel)")
     return ap.parse_args()
 
 
@@ -81,7 +82,7 @@ COPY_BYTES = 2 << 30          # the 2 GiB device copy of the `--only kernel` run
 
 def kernel_key(workload, regime_small):
     """Counter-CSV kernel name prefix of the routed gate_up+SwiGLU launch."""
-    return "qmm_small_kernel<0, 0," if regime_small else "qmm_large_kernel<0, 0>"
+    return "qmm_small_kernel<0, 0," if regime_small else "qmm_wide_kernel<0>"
 
 
 def write_traffic(fetch_dir, write_dir, workload="c2-decode-N32", regime_small=True):
@@ -138,7 +139,9 @@ def log(msg):
 def main():
     args = parse()
     if args.write_traffic:
-        write_traffic(*args.write_traffic)
+        wl = ("c4-prefill-zipf" if args.zipf else
+              f"{args.config}-decode" if args.batch <= 256 else f"{args.config}-prefill") + f"-N{args.batch}"
+        write_traffic(*args.write_traffic, workload=wl, regime_small=args.batch <= 256)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
@@ -461,7 +464,7 @@ def main():
             achieved = kern["flops"] / (kern["us"] * 1e-6) / 1e12
             roofline = dict(bound="mfma", achieved=round(achieved, 1), peak=BF16_PEAK_TFLOPS,
                             unit="TFLOP/s", frac=round(achieved / BF16_PEAK_TFLOPS, 4),
-                            traffic=None, kernel=kern["name"], kernel_us=round(kern["us"], 2),
+                            traffic=traffic, kernel=kern["name"], kernel_us=round(kern["us"], 2),
                             flops_per_launch=int(kern["flops"]), distinct_experts=round(kern["U"], 1))
         else:
             achieved = kern["bytes"] / (kern["us"] * 1e-6) / 1e9

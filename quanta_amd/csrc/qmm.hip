@@ -631,6 +631,15 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds_off) {
 }
 // Wait until at most n of this wavefront's vector-memory operations are outstanding (they
 // complete in issue order).
+// A byte loaded and waited for in one asm block, before any DMA of the kernel is issued: the
+// compiler then sees a ready value and never guards its later uses with a vmcnt wait, which it
+// cannot tell from the DMA prefetch's own (those waits would drain the prefetch every superblock).
+__device__ __forceinline__ int load_i8_now(const int8_t* p) {
+  int v;
+  asm volatile("global_load_sbyte %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -705,7 +714,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
-      rex[t] = a.row_exp ? a.row_exp[(ebase + tl) * 16 + (lane & 15)] : 0;
+      rex[t] = a.row_exp ? load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) : 0;
     } else {
       wcode[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
@@ -965,7 +974,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     const int64_t tb = (ebase + tl) * nsb;
     wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
     wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
-    rex[t] = a.row_exp ? a.row_exp[(ebase + tl) * 16 + (lane & 15)] : 0;
+    rex[t] = a.row_exp ? load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) : 0;
   }
   // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
   const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
