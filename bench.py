@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--extra", default="residual,int6,int3,mixed,awq",
                     help="widened rows timed at the headline batch ('' = none): residual, int6, "
                          "int3, mixed, awq")
+    ap.add_argument("--shared", choices=("int8", "bf16"), default="int8",
+                    help="shared-expert weights: int8 g64 as the bake stores them (dequantized in "
+                         "registers to the bf16 weights the reference loads; same outputs) or bf16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
@@ -164,12 +167,13 @@ def main():
     cfg = spec.cfg
     H, E, k, I = cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size
     Is = cfg.shared_expert_intermediate_size
+    SB = 8 if args.shared == "int8" else 16   # shared-expert bits (algorithmic bytes too)
 
     def resident_layers(name, copies):
         """`copies` resident (tiled) copies of config `name`'s synthetic layer at distinct
         addresses, and the native layer on the host (for the CPU baseline) or None."""
         t0 = time.time()
-        base = synth.make_layer(name, device=dev)
+        base = synth.make_layer(name, device=dev, shared_bits=SB)
         gu0 = TiledExperts(**tile_experts_packed(base["experts_gate_up"]))
         dn0 = TiledExperts(**tile_experts_packed(base["experts_down"]))
         native = {kk: ({q: (v.cpu() if isinstance(v, torch.Tensor) else v) for q, v in vv.items()}
@@ -179,7 +183,8 @@ def main():
         for li in range(copies):
             def cp(te):
                 return TiledExperts({q: (v.clone() if isinstance(v, torch.Tensor) else v) for q, v in te.items()})
-            p = {kk: v.clone() for kk, v in base.items()}
+            p = {kk: ({q: (t.clone() if isinstance(t, torch.Tensor) else t) for q, t in v.items()}
+                      if isinstance(v, dict) else v.clone()) for kk, v in base.items()}
             p["experts_gate_up"] = gu0 if li == 0 else cp(gu0)
             p["experts_down"] = dn0 if li == 0 else cp(dn0)
             out.append(p)
@@ -255,7 +260,7 @@ def main():
         steps_layer = args.steps
     ms, us, xs, preps = run_batch(N, steps_layer, args.warmup, args.pool, zipf=args.zipf)
     U = sum(us) / len(us)
-    layer_bytes = synth.algorithmic_bytes(cfg, U, N)
+    layer_bytes = synth.algorithmic_bytes(cfg, U, N, shared_bits=SB)
     log(f"N={N}: {ms * 1e3:.1f} us/step, U={U:.1f}, layer {layer_bytes / ms / 1e6:.0f} GB/s")
 
     # ------------------------------------------------------------------ dominant kernel
@@ -311,7 +316,7 @@ def main():
             st = max(100, args.steps // 4) if n2 <= 256 else max(20, args.steps // 20)
             m2, u2, _, _ = run_batch(n2, st, 3, min(args.pool, 8), zipf=zipf)
             U2 = sum(u2) / len(u2)
-            b2 = synth.algorithmic_bytes(cfg, U2, n2)
+            b2 = synth.algorithmic_bytes(cfg, U2, n2, shared_bits=SB)
             f2 = synth.algorithmic_flops(cfg, n2)
             rec = dict(workload=f"c4-prefill-N{n2}-zipf" if zipf else f"{args.config}-N{n2}",
                        N=n2, ms_per_step=round(m2, 5), tokens_per_s=round(n2 / (m2 / 1e3), 1),
@@ -329,14 +334,14 @@ def main():
         for part in args.configs_sweep.split(";"):
             name, ns = part.split(":")
             c_ = synth.spec(name).cfg
-            layer_mb = synth.algorithmic_bytes(c_, c_.num_experts, 0) / 2**20
+            layer_mb = synth.algorithmic_bytes(c_, c_.num_experts, 0, shared_bits=SB) / 2**20
             copies = max(2, min(8, int(2048 // layer_mb) + 1))
             lays_c, _ = resident_layers(name, copies)
             for n2 in (int(v) for v in ns.split(",") if v):
                 m2, u2, _, _ = run_batch(n2, max(100, args.steps // 4), 3, min(args.pool, 8),
                                          lays=lays_c, cfg_=name)
                 U2 = sum(u2) / len(u2)
-                b2 = synth.algorithmic_bytes(c_, U2, n2)
+                b2 = synth.algorithmic_bytes(c_, U2, n2, shared_bits=SB)
                 rec = dict(workload=f"{name}-N{n2}", N=n2, ms_per_step=round(m2, 5),
                            tokens_per_s=round(n2 / (m2 / 1e3), 1), distinct_experts=round(U2, 1),
                            hbm_gbps=round(b2 / m2 / 1e6, 1),
@@ -352,7 +357,8 @@ def main():
     if args.only == "" and N <= 256:
         def record(name, m2, u2, extra_bytes=0, per_expert_bytes=0, **fmt):
             U2 = sum(u2) / len(u2)
-            b2 = synth.algorithmic_bytes(cfg, U2, N, **fmt) + extra_bytes + U2 * per_expert_bytes
+            b2 = (synth.algorithmic_bytes(cfg, U2, N, shared_bits=SB, **fmt) + extra_bytes
+                  + U2 * per_expert_bytes)
             rec = dict(workload=name, N=N, ms_per_step=round(m2, 5),
                        tokens_per_s=round(N / (m2 / 1e3), 1), distinct_experts=round(U2, 1),
                        hbm_gbps=round(b2 / m2 / 1e6, 1), hbm_frac=round(b2 / m2 / 1e6 / HBM_PEAK_GBPS, 4))
@@ -369,7 +375,7 @@ def main():
                 continue
             lays_f = []
             for li in range(2):
-                pf = synth.make_layer(args.config, device=dev, layer=li, **fmt)
+                pf = synth.make_layer(args.config, device=dev, layer=li, shared_bits=SB, **fmt)
                 pf["experts_gate_up"] = TiledExperts(**tile_experts_packed(pf["experts_gate_up"]))
                 pf["experts_down"] = TiledExperts(**tile_experts_packed(pf["experts_down"]))
                 lays_f.append(pf)
@@ -441,6 +447,8 @@ def main():
     if native_cpu is not None and args.only == "":
         from oracle import torch_cpu
 
+        # the reference's loader dequantizes an int8 shared expert to bf16 once, at load
+        native_cpu = torch_cpu.load_shared(native_cpu)
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)
         xs_cpu = [x.cpu() for x in xs[:args.cpu_reps]]
@@ -491,6 +499,8 @@ def main():
         "config": {"workload": workload,
                    "hidden": H, "experts": E, "top_k": k, "inter": I, "shared_inter": Is,
                    "batch_tokens": N, "weights": "int4-g64 affine, bf16 scale/bias",
+                   "shared_weights": ("int8-g64 as baked, dequantized in registers to the bf16 "
+                                      "weights the reference loads" if SB == 8 else "bf16"),
                    "layer_copies": args.layers, "input_pool": args.pool},
         "layer_hbm_gbps": round(layer_bytes / ms / 1e6, 1),
         "measured_copy_gbps": copy_gbps,

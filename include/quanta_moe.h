@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 6
+#define QMOE_ABI_VERSION 7
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -61,6 +61,10 @@ extern "C" {
                                src/quanta/minimax/model_m3.py:414-450); small regime only */
 #define QMOE_FMT_INT3_G64 3 /* affine int3 codes, bf16 scale/bias per 64 (Kimi's int3 gate/up
                                stacks, src/quanta/modeling/quantized.py:1-84); small regime only */
+#define QMOE_FMT_INT8_G64 4 /* affine int8 codes, bf16 scale/bias per 64: the shared expert as the
+                               bake stores it (src/quanta/qwen35/bake.py:147-151); shared expert
+                               only (qmoe_config_t.shared_format) and qmoe_grouped_qmm's small
+                               regime */
 
 /* router weight storage */
 #define QMOE_ROUTER_BF16_TILED 0 /* bf16 [router_rows, H] tiled; row E = shared-expert gate */
@@ -119,6 +123,12 @@ typedef struct {
                             each projection; small regime only */
   int32_t mixed;         /* 1: routed experts of mixed widths per (expert, projection), passed to
                             qmoe_forward_mixed (weights' gu/dn fields unused); small regime only */
+  int32_t shared_format; /* QMOE_FMT_BF16 or QMOE_FMT_INT8_G64: the shared expert's weights.
+                            int8 weights are dequantized in registers to bf16(s*q + b), the bf16
+                            weights the reference's loader makes of them
+                            (src/quanta/qwen35/artifact.py:105-115), so both formats give the same
+                            outputs; int8 reads half the bytes. Above 256 tokens the block first
+                            expands them into its workspace. */
 } qmoe_config_t;
 
 /* Prepared (resident) weights of one block; every array is device memory. */
@@ -130,8 +140,11 @@ typedef struct {
   const uint16_t* gu_sb;          /* tiled scale/bias (int4 only) */
   const uint32_t* dn_codes;       /* routed down [E, H, I] */
   const uint16_t* dn_sb;
-  const uint16_t* sh_gu;          /* shared gate|up [2*Is, H] tiled bf16 */
-  const uint16_t* sh_dn;          /* shared down [H, Is] tiled bf16 */
+  const uint16_t* sh_gu;          /* shared gate|up [2*Is, H]: tiled bf16, or tiled int8 codes
+                                     (qmoe_tile_int8) with shared_format QMOE_FMT_INT8_G64 */
+  const uint16_t* sh_dn;          /* shared down [H, Is], as sh_gu */
+  const uint16_t* sh_gu_sb;       /* int8 shared expert: tiled scale/bias of sh_gu, else unused */
+  const uint16_t* sh_dn_sb;       /* int8 shared expert: tiled scale/bias of sh_dn, else unused */
   const uint16_t* awq_gu;         /* config awq: bf16 [E, 2, H] input-channel scales of the gate
                                      (row 0) and up (row 1) projections, else NULL */
   const uint16_t* awq_dn;         /* config awq: bf16 [E, I] scales of the down projection */
@@ -256,8 +269,9 @@ int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_
 /* Grouped matmul over expert segments: out[p, :] = act[row(p)] . W_e^T for sorted positions
  * p of expert e (offsets/tile_off from qmoe_permute; m_tile 16 for QMOE_REGIME_SMALL, 128 for
  * QMOE_REGIME_LARGE), with row(p) = slot_of[p] / slot_div (slot_of NULL: row(p) = p). With
- * offsets == NULL the call is one dense segment of dense_rows rows. W is tiled int4-g64
- * (codes + sb) or tiled bf16 (codes), [n_experts][n_rows][K]; row_exp (int4, nullable) holds the
+ * offsets == NULL the call is one dense segment of dense_rows rows. W is tiled int3/int4/int6
+ * (codes + sb), tiled int8 (codes + sb; small regime, K % 64 == 0) or tiled bf16 (codes),
+ * [n_experts][n_rows][K]; row_exp (int4, nullable) holds the
  * per-row exponents of qmoe_row_exponents for the large regime's fp16 dequant. Epilogue QMOE_EPI_SWIGLU treats
  * rows [0, n_rows/2) as gate and [n_rows/2, n_rows) as up, with the gated activation `glu`
  * (QMOE_ACT_*; glu_alpha and glu_limit as act_alpha and act_limit of qmoe_config_t; other
@@ -337,6 +351,18 @@ int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, const uint16_t
 int qmoe_row_exponents(const uint16_t* scale, const uint16_t* bias, int64_t n_mats, int64_t rows,
                        int64_t in_features, int bits, int group_size, int8_t* row_exp,
                        void* stream);
+
+/* One-time layout transform of a native int8 matrix stack [n_mats][rows][in] (packed u32
+ * [.., in/4], code k in byte k%4 of word k/4; scale/bias bf16 [.., in/group_size], group 64 or
+ * 128) into the tiled int8 layout: codes [n_mats][rows/16][in/32][64 lanes][8 codes] (lane l:
+ * row l%16, codes 32c + 8(l/16) .. +8, the bf16 tiling at one byte per weight) and sb
+ * [n_mats][rows/16][in/64][16 rows][scale, bias] bf16 (a 128-column group's pair written for
+ * both of its halves). rows % 16 == 0, in % 64 == 0. Stands in for the load-time dequant of the
+ * bake's int8 shared expert (src/quanta/qwen35/artifact.py:171-184): the kernels read the codes
+ * and dequantize in registers. */
+int qmoe_tile_int8(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                   int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                   uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream);
 
 /* Inverse check of qmoe_tile_int4: tiled stack -> bf16 [n_mats][rows][in], bit-identical to
  * qmoe_dequant of the native stack. Test/inspection entry point. */

@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle.quant import dequant_exact, round_bf16
+from oracle.quant import bf16_bits_to_f32, dequant_bf16_bits, dequant_exact, round_bf16
 
 
 def _silu(v: np.ndarray) -> np.ndarray:
@@ -280,6 +280,23 @@ def combine(d: np.ndarray, w: np.ndarray) -> np.ndarray:
     return (d.reshape(n, k, -1) * w[:, :, None]).sum(axis=1)
 
 
+def shared_weight(v) -> np.ndarray:
+    """A shared-expert projection as the reference's loader hands it to the block: bf16 values as
+    given, or the bake's int8 triplet (`src/quanta/qwen35/bake.py:106-110, 150-151`: a dict
+    {packed uint32 [out, in/4], scale, bias: bf16 bits [out, in/g], group_size, bits: 8})
+    dequantized to bf16 (`src/quanta/qwen35/artifact.py:105-115`, read by `moe()` at
+    :171-184), under the dequant convention of oracle.quant.dequant_bf16_bits."""
+    if not isinstance(v, dict):
+        return v
+    if int(v.get("bits", 8)) != 8:
+        raise ValueError("shared expert triplets are int8")
+    packed = np.asarray(v["packed"])
+    in_features = packed.shape[-1] * 4
+    bits = dequant_bf16_bits(packed, np.asarray(v["scale"]), np.asarray(v["bias"]), in_features,
+                             bits=8, group_size=int(v.get("group_size", 64)))
+    return bf16_bits_to_f32(bits).astype(np.float64)
+
+
 def shared_expert(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
                   gate: np.ndarray | None, act: str = "silu", alpha: float = 1.702,
                   limit: float = 0.0):
@@ -311,8 +328,8 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
     `p` keys (numpy, bf16 data as float64 values, int4 stacks as uint32/uint16 bit arrays):
       gate [E,H]; gu_packed [E,2I,H/8], gu_scale/gu_bias [E,2I,H/64] (bf16 bits);
       dn_packed [E,H,I/8], dn_scale/dn_bias [E,H,I/64]; optional e_score_correction_bias [E];
-      optional shared_gate_proj [Is,H], shared_up_proj [Is,H], shared_down_proj [H,Is],
-      shared_expert_gate [1,H]; optional gu_awq [E,2,H] and dn_awq [E,I] (bf16 values): the
+      optional shared_gate_proj [Is,H], shared_up_proj [Is,H], shared_down_proj [H,Is] (bf16
+      values, or int8 triplets, see shared_weight), shared_expert_gate [1,H]; optional gu_awq [E,2,H] and dn_awq [E,I] (bf16 values): the
       activation-aware scales of DeepSeek-V4's packed experts (see awq_expert_rows); or, in
       place of the gu_/dn_ stacks, "mixed" (per-(expert, projection) widths, see mixed_proj).
     Returns (y bf16-valued float64 [N,H], dict of intermediates).
@@ -348,9 +365,10 @@ def moe_forward(x: np.ndarray, p: dict, *, k: int, inter: int, scoring: str = "s
     y = routed.copy()
     sh = None
     if p.get("shared_gate_proj") is not None:
-        sh, sh_out, sg = shared_expert(x, p["shared_gate_proj"], p["shared_up_proj"],
-                                       p["shared_down_proj"], p.get("shared_expert_gate"),
-                                       act, alpha, limit)
+        sh, sh_out, sg = shared_expert(x, shared_weight(p["shared_gate_proj"]),
+                                       shared_weight(p["shared_up_proj"]),
+                                       shared_weight(p["shared_down_proj"]),
+                                       p.get("shared_expert_gate"), act, alpha, limit)
         y = y + sh
     inter_d = dict(idx=idx, w=w, logits=logits, scores=scores, choice=choice, gu=gu, h=h, d=d,
                    routed=routed, shared=sh, y_exact=y)

@@ -9,6 +9,7 @@ qwen35_moe (src/quanta/qwen35/moe.py:154-202) in torch on the host cores:
   per expert: dequant s*q+b of its int4 g64 stack, matmul, SwiGLU   (moe.py:85-124)
   per expert down projection, fp32 weighted combine                 (moe.py:191)
   bf16 shared expert with the sigmoid gate, bf16 output             (moe.py:145-151,201-202)
+  (an int8 shared expert dequantized to bf16 first, as the loader does: artifact.py:105-115)
 Only the experts a batch routes to are dequantized, as gather_qmm only reads those.
 """
 
@@ -25,6 +26,30 @@ def _dequant(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor) -> t
     s = scale.to(torch.float32).repeat_interleave(64, dim=1)
     b = bias.to(torch.float32).repeat_interleave(64, dim=1)
     return torch.addcmul(b, s, q)
+
+
+def _dequant8(t: dict) -> torch.Tensor:
+    """int8 triplet {packed [rows, K/4] int32, scale/bias [rows, K/g] bf16} -> bf16 [rows, K],
+    bf16(fp32(s*q + b)) (s*q is exact in fp32)."""
+    packed = t["packed"]
+    rows, nw = packed.shape
+    shifts = torch.arange(0, 32, 8, dtype=torch.int32)
+    q = ((packed[:, :, None] >> shifts) & 0xFF).reshape(rows, nw * 4).to(torch.float32)
+    g = int(t.get("group_size", 64))
+    s = t["scale"].to(torch.float32).repeat_interleave(g, dim=1)
+    b = t["bias"].to(torch.float32).repeat_interleave(g, dim=1)
+    return torch.addcmul(b, s, q).to(torch.bfloat16)
+
+
+def load_shared(p: dict) -> dict:
+    """The layer as the reference's loader hands it to the block: an int8 shared expert (the
+    bake's format, src/quanta/qwen35/bake.py:150-151) dequantized to bf16 once
+    (src/quanta/qwen35/artifact.py:105-115, 171-184); other entries unchanged."""
+    q = dict(p)
+    for key in ("shared_gate_proj", "shared_up_proj", "shared_down_proj"):
+        if isinstance(q.get(key), dict):
+            q[key] = _dequant8(q[key])
+    return q
 
 
 def route(x: torch.Tensor, gate: torch.Tensor, cfg, k: int, bias=None):
@@ -79,6 +104,7 @@ def moe_forward(x: torch.Tensor, p: dict, cfg, k: int | None = None) -> torch.Te
     d[order] = d_sorted
     y = (d.view(n, k, H) * w[:, :, None]).sum(1)
     if p.get("shared_gate_proj") is not None:
+        p = load_shared(p)
         xb = x.to(torch.bfloat16)
         hs = torch.nn.functional.silu(xb @ p["shared_gate_proj"].T) * (xb @ p["shared_up_proj"].T)
         out = (hs @ p["shared_down_proj"].T).to(torch.float32)

@@ -17,13 +17,13 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "quanta_moe.h"
 QMOE_OK, QMOE_EINVAL, QMOE_EHIP = 0, -1, -2
 SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
 NORM_NONE, NORM_ALWAYS, NORM_MULTI = 0, 1, 2
-FMT_INT4_G64, FMT_BF16, FMT_INT6_G64, FMT_INT3_G64 = 0, 1, 2, 3
+FMT_INT4_G64, FMT_BF16, FMT_INT6_G64, FMT_INT3_G64, FMT_INT8_G64 = 0, 1, 2, 3, 4
 ROUTER_BF16_TILED, ROUTER_F32 = 0, 1
 REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 6
+ABI_VERSION = 7
 NOALLOC_SCRATCH_BYTES = 64 << 20   # QMOE_NOALLOC_SCRATCH_BYTES
 
 
@@ -55,7 +55,12 @@ class QmoeConfig(ctypes.Structure):
         ("down_format", ctypes.c_int32),
         ("awq", ctypes.c_int32),
         ("mixed", ctypes.c_int32),
+        ("shared_format", ctypes.c_int32),
     ]
+
+    def __init__(self, **kw):
+        kw.setdefault("shared_format", FMT_BF16)
+        super().__init__(**kw)
 
 
 class QmoeWeights(ctypes.Structure):
@@ -69,6 +74,8 @@ class QmoeWeights(ctypes.Structure):
         ("dn_sb", ctypes.c_void_p),
         ("sh_gu", ctypes.c_void_p),
         ("sh_dn", ctypes.c_void_p),
+        ("sh_gu_sb", ctypes.c_void_p),
+        ("sh_dn_sb", ctypes.c_void_p),
         ("awq_gu", ctypes.c_void_p),
         ("awq_dn", ctypes.c_void_p),
         ("gu_rexp", ctypes.c_void_p),
@@ -129,6 +136,7 @@ SIGNATURES = {
     "qmoe_row_exponents": (_I, [_P, _P, _I64, _I64, _I64, _I, _I, _P, _P]),
     "qmoe_dequant_tiled": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "qmoe_tile_int6": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "qmoe_tile_int8": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_int3": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_bf16": (_I, [_P, _I64, _I64, _I64, _P, _P]),
 }

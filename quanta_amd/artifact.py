@@ -211,10 +211,16 @@ class QuantaArtifact:
                 "bits": int(meta["bits"])}
 
     # --- the MoE block --------------------------------------------------------------------
-    def moe_packed(self, i: int, device: torch.device | str, *, prefix: str = LM_PREFIX) -> dict:
+    def moe_packed(self, i: int, device: torch.device | str, *, prefix: str = LM_PREFIX,
+                   shared: str = "bf16") -> dict:
         """The parameter dict of layer i's MoE block for `qwen35_moe`: the routed experts as packed
         triplets, the router gate, the shared expert and its gate in bf16
-        (src/quanta/qwen35/artifact.py:205-229). A block without a shared expert omits its keys."""
+        (src/quanta/qwen35/artifact.py:205-229). A block without a shared expert omits its keys.
+        shared="int8": a shared expert the bake stored as int8 (bake.py:150-151) is handed over
+        as its packed triplets, which the block reads at half the bytes with the same outputs
+        (a dense one is still read as bf16)."""
+        if shared not in ("bf16", "int8"):
+            raise ValueError("moe_packed: shared must be 'bf16' or 'int8'")
         p = f"{prefix}layers.{i}.mlp."
         out: dict[str, object] = {
             "gate": self.read(p + "gate.weight", device),
@@ -228,7 +234,13 @@ class QuantaArtifact:
                 device).to(torch.float32)
         if self.has(p + "shared_expert.gate_proj.weight"):
             for proj in SHARED_EXPERT_PROJS:
-                out[f"shared_{proj}"] = self.read(p + f"shared_expert.{proj}.weight", device)
+                base = p + f"shared_expert.{proj}"
+                meta = self.manifest.get(base)
+                if (shared == "int8" and meta is not None and meta.get("format") == "affine_packed"
+                        and int(meta.get("bits", 0)) == 8):
+                    out[f"shared_{proj}"] = self.packed_triplet(base, device)
+                else:
+                    out[f"shared_{proj}"] = self.read(base + ".weight", device)
             if self.has(p + "shared_expert_gate.weight"):
                 out["shared_expert_gate"] = self.read(p + "shared_expert_gate.weight", device)
         return out

@@ -122,14 +122,15 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 // into the same chunks as the standalone small-regime bf16 product (bf16_chunks, one wavefront
 // each, summed from zero and added in chunk order; the other wavefronts add exact zeros), so
 // the result is bit-identical to the unfused shared down and independent of the other tokens.
-// Wd is the tiled bf16 [H/16][Is/32][64][8].
+// Wd is the tiled bf16 [H/16][Is/32][64][8], or (FMT_INT8) the tiled int8 codes with their
+// scale/bias, dequantized in registers to the same bf16 weights.
 constexpr int kCsWaves = 8;
-template <int MT>
+template <int MT, int FMT>
 __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     const uint16_t* __restrict__ d, const int32_t* __restrict__ inv, const float* __restrict__ w,
     int N, int k, int H, int64_t n_pos, const uint16_t* __restrict__ sh_h, int Is, int nch,
-    const u32x4* __restrict__ wd, const float* __restrict__ shared_gate, const uint16_t* resid,
-    uint16_t* y) {
+    const void* __restrict__ wd, const uint16_t* __restrict__ wd_sb,
+    const float* __restrict__ shared_gate, const uint16_t* resid, uint16_t* y) {
   constexpr int TOK = 16 * MT;   // tokens per workgroup
   __shared__ f32x4_t part[kCsWaves][MT][64];
   __shared__ float sh[TOK][17];
@@ -139,7 +140,8 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
   const int tm = blockIdx.y * TOK;
   const int nks = Is / 32;
   const int c0 = (wave < nch) ? wave * nks / nch : 0, c1 = (wave < nch) ? (wave + 1) * nks / nch : 0;
-  const u32x4* wp = wd + static_cast<int64_t>(fb) * nks * 64 + lane;
+  DenseTile<FMT> wt;
+  wt.init(wd, wd_sb, fb, Is, lane);
   // the routed gather-sum of (token tl, feature f) runs on wavefronts 4-7 while wavefronts 0-3
   // compute the shared down (when it has at most 4 chunks), else after it; 256 threads, MT
   // tokens each
@@ -179,19 +181,21 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
     // batches of steps, all loads first (clamped indices), MFMAs in step order
     constexpr int BS = 8;
     for (int cb = c0; cb < c1; cb += BS) {
-      u32x4 wv[BS], xv[BS][MT];
+      DenseFrag<FMT> wv[BS];
+      u32x4 xv[BS][MT];
 #pragma unroll
       for (int i = 0; i < BS; ++i) {
         const int c = min(cb + i, c1 - 1);
-        wv[i] = wp[c * 64];
+        wv[i] = wt.load(c);
 #pragma unroll
         for (int u = 0; u < MT; ++u) xv[i][u] = *reinterpret_cast<const u32x4*>(xr[u] + 32 * c);
       }
 #pragma unroll
       for (int i = 0; i < BS; ++i)
         if (cb + i < c1) {
+          const bf16x8_t B = as_bf16x8(dense_bf16<FMT>(wv[i]));
 #pragma unroll
-          for (int u = 0; u < MT; ++u) acc[u] = mfma16(as_bf16x8(xv[i][u]), as_bf16x8(wv[i]), acc[u]);
+          for (int u = 0; u < MT; ++u) acc[u] = mfma16(as_bf16x8(xv[i][u]), B, acc[u]);
         }
     }
 #pragma unroll
@@ -228,25 +232,38 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
   }
 }
 
-int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
-                          int H, const uint16_t* sh_h, int Is, const uint16_t* wd,
-                          const float* shared_gate, uint16_t* y, hipStream_t stream,
-                          const uint16_t* resid) {
-  const int nch = bf16_chunks(Is);
-  if (H % 16 || Is % 32 || Is <= 0 || nch > kCsWaves)
-    return fail("combine: fused shared down needs H % 16 == 0, Is % 32 == 0, Is < 4096");
+template <int FMT>
+static void launch_cs(const uint16_t* d, const int32_t* inv, const float* w, int N, int k, int H,
+                      const uint16_t* sh_h, int Is, int nch, const void* wd, const uint16_t* wd_sb,
+                      const float* shared_gate, uint16_t* y, hipStream_t stream,
+                      const uint16_t* resid) {
   // above 48 tokens, 32 per workgroup: the shared down weights are read once per 32 tokens
   // (below that the halved grid leaves CUs idle)
   if (N > 48) {
     dim3 grid(H / 16, (N + 31) / 32);
-    combine_shared_kernel<2><<<grid, 64 * kCsWaves, 0, stream>>>(
-        d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
-        reinterpret_cast<const u32x4*>(wd), shared_gate, resid, y);
+    combine_shared_kernel<2, FMT><<<grid, 64 * kCsWaves, 0, stream>>>(
+        d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch, wd, wd_sb, shared_gate,
+        resid, y);
   } else {
     dim3 grid(H / 16, (N + 15) / 16);
-    combine_shared_kernel<1><<<grid, 64 * kCsWaves, 0, stream>>>(
-        d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch,
-        reinterpret_cast<const u32x4*>(wd), shared_gate, resid, y);
+    combine_shared_kernel<1, FMT><<<grid, 64 * kCsWaves, 0, stream>>>(
+        d, inv, w, N, k, H, static_cast<int64_t>(N) * k, sh_h, Is, nch, wd, wd_sb, shared_gate,
+        resid, y);
+  }
+}
+
+int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
+                          int H, const uint16_t* sh_h, int Is, const void* wd,
+                          const uint16_t* wd_sb, int fmt, const float* shared_gate, uint16_t* y,
+                          hipStream_t stream, const uint16_t* resid) {
+  const int nch = bf16_chunks(Is);
+  if (H % 16 || Is % 32 || Is <= 0 || nch > kCsWaves)
+    return fail("combine: fused shared down needs H % 16 == 0, Is % 32 == 0, Is < 4096");
+  if (fmt == FMT_INT8) {
+    if (Is % 64 || !wd_sb) return fail("combine: int8 shared down needs Is % 64 == 0 and scale/bias");
+    launch_cs<FMT_INT8>(d, inv, w, N, k, H, sh_h, Is, nch, wd, wd_sb, shared_gate, y, stream, resid);
+  } else {
+    launch_cs<FMT_BF16>(d, inv, w, N, k, H, sh_h, Is, nch, wd, wd_sb, shared_gate, y, stream, resid);
   }
   return check_launch("combine_shared");
 }
@@ -330,10 +347,24 @@ static int aux_stream(hipStream_t caller, AuxStream** out) {
   return 0;
 }
 
+// Large-M tiles pay off once a batch gives experts tens of rows; they also need the output
+// widths (hidden for the down projection) to be multiples of the 256-row tile.
+static int dense_regime(const qmoe_config_t& c, int64_t N) {
+  return (N > 256 && c.hidden % 256 == 0) ? QMOE_REGIME_LARGE : QMOE_REGIME_SMALL;
+}
+
+// Whether an int8 shared expert is expanded to bf16 for this call: the large-M kernel stages
+// bf16 (or int4) weights only, and above the decode sizes the expansion (half the bf16 bytes
+// read, all of them written once) is small beside the block.
+static bool shared_expands(const qmoe_config_t& c, int64_t N) {
+  return c.shared_inter > 0 && c.shared_format == QMOE_FMT_INT8_G64 &&
+         dense_regime(c, N) == QMOE_REGIME_LARGE;
+}
+
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
   size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, tile_map_big, sorted, inv, h,
-      d, sh_h, sh_out, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, total;
+      d, sh_h, sh_out, sh_w16, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, total;
   int64_t max_tiles, max_tiles_big;
 };
 
@@ -369,6 +400,9 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.d = take(static_cast<size_t>(mc) * c.hidden * 2);
   L.sh_h = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.shared_inter : 0) * 2);
   L.sh_out = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.hidden : 0) * 2);
+  // int8 shared expert above the decode sizes: its weights expanded to tiled bf16 for the
+  // large-M kernel (gate|up [2 Is, H] then down [H, Is])
+  L.sh_w16 = take(shared_expands(c, N) ? static_cast<size_t>(3) * c.shared_inter * c.hidden * 2 : 0);
   // fp16 per-row-scaled activation copies for the large-M int4 regime
   L.x16 = take(static_cast<size_t>(N) * c.hidden * 2);
   L.x_sinv = take(static_cast<size_t>(N) * 4);
@@ -394,7 +428,7 @@ static int validate_glu(int act, float alpha, float limit) {
 // Kernel format of a QMOE_FMT_* value.
 static int kernel_fmt(int f) {
   return f == QMOE_FMT_INT4_G64 ? FMT_INT4 : f == QMOE_FMT_INT6_G64 ? FMT_INT6
-         : f == QMOE_FMT_INT3_G64 ? FMT_INT3 : FMT_BF16;
+         : f == QMOE_FMT_INT3_G64 ? FMT_INT3 : f == QMOE_FMT_INT8_G64 ? FMT_INT8 : FMT_BF16;
 }
 // int3 or int6 codes on either projection: the large-M kernels stage int4 superblocks only.
 static bool narrow_codes(const qmoe_config_t& c) {
@@ -438,6 +472,8 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: the large-M regime needs hidden % 256 == 0");
   if (c.inter <= 0 || c.inter % 128) return fail("config: inter % 128 == 0 required");
   if (c.shared_inter < 0 || c.shared_inter % 128) return fail("config: shared_inter % 128 == 0 required");
+  if (c.shared_format != QMOE_FMT_BF16 && c.shared_format != QMOE_FMT_INT8_G64)
+    return fail("config: shared_format must be QMOE_FMT_BF16 (1) or QMOE_FMT_INT8_G64 (4)");
   if (c.expert_format < QMOE_FMT_INT4_G64 || c.expert_format > QMOE_FMT_INT3_G64 ||
       c.down_format < QMOE_FMT_INT4_G64 || c.down_format > QMOE_FMT_INT3_G64)
     return fail("config: expert_format / down_format must be int4-g64 (0), bf16 (1), int6-g64 (2) or int3-g64 (3)");
@@ -501,7 +537,7 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
     const int rc = validate_glu(glu, glu_alpha, glu_limit);
     if (rc) return rc;
   }
-  if (weight_format < QMOE_FMT_INT4_G64 || weight_format > QMOE_FMT_INT3_G64)
+  if (weight_format < QMOE_FMT_INT4_G64 || weight_format > QMOE_FMT_INT8_G64)
     return fail("qmoe_grouped_qmm: bad weight_format");
   if (weight_format != QMOE_FMT_BF16 && !sb) return fail("qmoe_grouped_qmm: quantized weights need sb");
   if (epilogue < QMOE_EPI_SWIGLU || epilogue > QMOE_EPI_F32) return fail("qmoe_grouped_qmm: bad epilogue");
@@ -560,12 +596,6 @@ extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
   return ws_layout(*cfg, N).total;
 }
 
-// Large-M tiles pay off once a batch gives experts tens of rows; they also need the output
-// widths (hidden for the down projection) to be multiples of the 256-row tile.
-static int dense_regime(const qmoe_config_t& c, int64_t N) {
-  return (N > 256 && c.hidden % 256 == 0) ? QMOE_REGIME_LARGE : QMOE_REGIME_SMALL;
-}
-
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
   // no large-regime kernel for int3/int6, AWQ scales or mixed widths
@@ -603,6 +633,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   if (!mixed && c.expert_format != QMOE_FMT_BF16 && (!wts->gu_sb || !wts->dn_sb))
     return fail("qmoe_forward: quantized experts need scale/bias");
   if (c.shared_inter > 0 && (!wts->sh_gu || !wts->sh_dn)) return fail("qmoe_forward: missing shared expert");
+  if (c.shared_inter > 0 && c.shared_format == QMOE_FMT_INT8_G64 && (!wts->sh_gu_sb || !wts->sh_dn_sb))
+    return fail("qmoe_forward: an int8 shared expert needs sh_gu_sb and sh_dn_sb");
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
   if (c.awq && (!wts->awq_gu || !wts->awq_dn)) return fail("qmoe_forward: awq needs awq_gu and awq_dn");
@@ -706,22 +738,43 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // 1. shared expert gate_up + SwiGLU -> sh_h (fused with the router below when decoding)
   const int st = decode ? kSmallMTile : kLargeMTile;
   QmmArgs sgu{};
+  // the shared expert's weights as the kernels read them: int8 codes dequantized in registers,
+  // or (large regime) expanded to bf16 in the workspace first
+  int sfmt = (c.shared_format == QMOE_FMT_INT8_G64) ? FMT_INT8 : FMT_BF16;
+  const void* sh_gu_w = wts->sh_gu;
+  const void* sh_dn_w = wts->sh_dn;
+  if (shared && shared_expands(c, N)) {
+    uint16_t* w16 = reinterpret_cast<uint16_t*>(base + L.sh_w16);
+    const int64_t gu_elems = static_cast<int64_t>(2) * c.shared_inter * c.hidden;
+    rc = launch_expand_int8(reinterpret_cast<const uint32_t*>(wts->sh_gu), wts->sh_gu_sb,
+                            2 * c.shared_inter, c.hidden, w16, sstream);
+    if (!rc)
+      rc = launch_expand_int8(reinterpret_cast<const uint32_t*>(wts->sh_dn), wts->sh_dn_sb,
+                              c.hidden, c.shared_inter, w16 + gu_elems, sstream);
+    if (rc) return rc;
+    sh_gu_w = w16;
+    sh_dn_w = w16 + gu_elems;
+    sfmt = FMT_BF16;
+  }
+  const bool sh8 = (sfmt == FMT_INT8);
   if (shared) {
     sgu.act = x; sgu.act_rows = N; sgu.slot_div = 1; sgu.dense_rows = N; sgu.n_experts = 1;
-    sgu.K = c.hidden; sgu.n_rows = 2 * c.shared_inter; sgu.codes = wts->sh_gu; sgu.out = sh_h;
+    sgu.K = c.hidden; sgu.n_rows = 2 * c.shared_inter; sgu.codes = sh_gu_w; sgu.out = sh_h;
+    sgu.sb = sh8 ? wts->sh_gu_sb : nullptr;
     sgu.ld_out = c.shared_inter;
     sgu.glu = c.act; sgu.glu_alpha = c.act_alpha; sgu.glu_limit = c.act_limit;
     if (!fuse_gu) {
-      rc = launch_qmm(sgu, FMT_BF16, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
+      rc = launch_qmm(sgu, sfmt, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
       if (rc) return rc;
     }
     // shared down -> sh_out (fused into the combine when decoding)
     if (!fuse_dn) {
       QmmArgs b{};
       b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
-      b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = wts->sh_dn; b.out = sh_out;
+      b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = sh_dn_w; b.out = sh_out;
+      b.sb = sh8 ? wts->sh_dn_sb : nullptr;
       b.ld_out = c.hidden;
-      rc = launch_qmm(b, FMT_BF16, EPI_BF16, sreg, (N + st - 1) / st, sstream);
+      rc = launch_qmm(b, sfmt, EPI_BF16, sreg, (N + st - 1) / st, sstream);
       if (rc) return rc;
     }
   }
@@ -747,7 +800,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       sgu.act = x_in; sgu.norm_w = norm_w; sgu.norm_eps = norm_eps;
     }
     if (fuse_gu)
-      rc = launch_qmm_pair_bf16(a, sgu, stream);
+      rc = launch_qmm_pair_bf16(a, sgu, stream, sfmt);
     else
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + st - 1) / st, stream);
   }
@@ -895,8 +948,9 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   }
   // 7. unpermute + weighted combine + gated shared (its down projection fused when decoding) + bf16
   if (fuse_dn)
-    return launch_combine_shared(d, inv, wv, n, c.top_k, c.hidden, sh_h, c.shared_inter, wts->sh_dn,
-                                 has_sg ? sg : nullptr, y, stream, resid);
+    return launch_combine_shared(d, inv, wv, n, c.top_k, c.hidden, sh_h, c.shared_inter, sh_dn_w,
+                                 sh8 ? wts->sh_dn_sb : nullptr, sfmt, has_sg ? sg : nullptr, y,
+                                 stream, resid);
   return launch_combine(d, inv, wv, n, c.top_k, c.hidden, shared ? sh_out : nullptr,
                         has_sg ? sg : nullptr, y, stream, resid);
 }

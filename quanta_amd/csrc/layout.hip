@@ -327,6 +327,61 @@ __global__ void __launch_bounds__(256) tile_bf16_kernel(const uint16_t* __restri
   out[i] = *src;
 }
 
+// Native int8 [mats][rows][K] (code k in byte k%4 of word k/4, so a row's bytes are its codes in
+// order) -> tiled codes [mats][rows/16][K/32][64 lanes][8 codes], lane l holding row l%16's codes
+// 32c + 8(l/16) .. +8, and sb [mats][rows/16][K/64][16 rows][scale, bias]. One thread per 8-byte
+// lane slot; the lanes of the even steps' first lane group also write the scale/bias pairs.
+__global__ void __launch_bounds__(256) tile_int8_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ bias, int64_t n_lanes_total, int K, int rows,
+    int halves_per_group, uint2* __restrict__ codes, uint32_t* __restrict__ sb) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_lanes_total) return;
+  const int nk = K / 32, gpr = K / (64 * halves_per_group);
+  const int lane = static_cast<int>(i & 63);
+  const int64_t blk = i >> 6;                 // (mat, R, c)
+  const int c = static_cast<int>(blk % nk);
+  const int64_t mr = blk / nk;                // mat * rows/16 + R
+  const int rt = rows / 16;
+  const int64_t mat = mr / rt;
+  const int R = static_cast<int>(mr - mat * rt);
+  const int r = lane & 15;
+  const int64_t row = mat * rows + R * 16 + r;
+  codes[i] = *reinterpret_cast<const uint2*>(packed + row * (K / 4) + c * 8 + (lane >> 4) * 2);
+  if ((c & 1) == 0 && lane < 16) {
+    const int64_t g = row * gpr + (c / 2) / halves_per_group;
+    sb[(mr * (K / 64) + c / 2) * 16 + r] =
+        static_cast<uint32_t>(scale[g]) | (static_cast<uint32_t>(bias[g]) << 16);
+  }
+}
+
+// Tiled int8 -> tiled bf16 [mats][rows/16][K/32][64][8]: every lane slot's 8 codes become the 8
+// bf16 weights the dense kernels make of them in registers (dense_bf16).
+__global__ void __launch_bounds__(256) expand_int8_kernel(const u32x2* __restrict__ codes,
+                                                          const uint16_t* __restrict__ sb,
+                                                          int64_t n_lanes_total, int K,
+                                                          u32x4* __restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_lanes_total) return;
+  const int nk = K / 32;
+  const int lane = static_cast<int>(i & 63);
+  const int64_t blk = i >> 6;
+  const int c = static_cast<int>(blk % nk);
+  const int64_t tile = blk / nk;
+  DenseTile<FMT_INT8> t;
+  t.init(codes, sb, tile, K, lane);
+  out[i] = dense_bf16<FMT_INT8>(t.load(c));
+}
+
+int launch_expand_int8(const uint32_t* codes, const uint16_t* sb, int64_t rows, int K,
+                       uint16_t* out, hipStream_t stream) {
+  if (rows <= 0 || rows % 16 || K <= 0 || K % 64) return fail("expand int8: rows % 16, K % 64 == 0");
+  const int64_t lanes = rows * (K / 32) * 4;
+  expand_int8_kernel<<<static_cast<unsigned>((lanes + 255) / 256), 256, 0, stream>>>(
+      reinterpret_cast<const u32x2*>(codes), sb, lanes, K, reinterpret_cast<u32x4*>(out));
+  return check_launch("expand int8");
+}
+
 // ---------------------------------------------------------------------------- row exponents
 // One wavefront per weight row: M = the row's largest dequantized magnitude, max over its groups of
 // max(|b|, |qmax * s + b|) (the affine map is monotone in the code, so its extremes sit at codes
@@ -466,6 +521,23 @@ extern "C" int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, con
       packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
       group_size / 64, tiled_codes, tiled_sb);
   return check_launch("qmoe_tile_int6");
+}
+
+extern "C" int qmoe_tile_int8(const uint32_t* packed, const uint16_t* scale, const uint16_t* bias,
+                              int64_t n_mats, int64_t rows, int64_t in_features, int group_size,
+                              uint32_t* tiled_codes, uint16_t* tiled_sb, void* stream) {
+  if (group_size != 64 && group_size != 128) return fail("qmoe_tile_int8: group_size must be 64 or 128");
+  if (n_mats <= 0 || rows <= 0 || rows % 16 || in_features <= 0 || in_features % 64 ||
+      in_features % group_size)
+    return fail("qmoe_tile_int8: need rows % 16 == 0 and in_features % 64 == 0 (and % group_size)");
+  if (!packed || !scale || !bias || !tiled_codes || !tiled_sb)
+    return fail("qmoe_tile_int8: null pointer");
+  if (rows > (1 << 30) || in_features > (1 << 30)) return fail("qmoe_tile_int8: dims too large");
+  const int64_t lanes = n_mats * rows * (in_features / 32) * 4;   // 64 lanes per 16 rows x 32
+  tile_int8_kernel<<<grid_for(lanes, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      packed, scale, bias, lanes, static_cast<int>(in_features), static_cast<int>(rows),
+      group_size / 64, reinterpret_cast<uint2*>(tiled_codes), reinterpret_cast<uint32_t*>(tiled_sb));
+  return check_launch("qmoe_tile_int8");
 }
 
 extern "C" int qmoe_dequant_tiled(const uint32_t* tiled_codes, const uint16_t* tiled_sb,

@@ -131,7 +131,7 @@ template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1, bool NORM = fal
 __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx, int by,
                                            f32x4_t* red) {
   using C = SmallCfg<FMT, EPI, W, CPW, JPW, MT>;
-  static_assert(MT == 1 || FMT == FMT_BF16, "several m-tiles per wavefront: bf16 weights only");
+  static_assert(MT == 1 || fmt_dense(FMT), "several m-tiles per wavefront: dense weights only");
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
   constexpr int NT = C::NT;
   constexpr int CH = C::CH;
@@ -330,32 +330,31 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
           chunk_end(p + 1);
         }
       }
-    } else {  // FMT_BF16
+    } else {  // dense: bf16 weights, or int8 codes dequantized to bf16 in registers
       const int nks = a.K / 32;
       const int k0 = kpart * nks / W, k1 = (kpart + 1) * nks / W;
-      const u32x4* wp[NT];
+      using Frag = DenseFrag<FMT>;
+      DenseTile<FMT> wt[NT];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int64_t tb = (static_cast<int64_t>(e) * tiles_per_expert + tile[t]) * nks;
-        wp[t] = static_cast<const u32x4*>(a.codes) + tb * 64 + lane;
-      }
+      for (int t = 0; t < NT; ++t)
+        wt[t].init(a.codes, a.sb, static_cast<int64_t>(e) * tiles_per_expert + tile[t], a.K, lane);
       const u32x4* xp[MT];
 #pragma unroll
       for (int u = 0; u < MT; ++u) xp[u] = reinterpret_cast<const u32x4*>(xrows[u]) + lg;   // 8 lg bf16
       // Batches of steps: all loads of a batch issue before its MFMAs (indices clamped into
       // the range, so no load is conditional); the MFMAs run in step order.
       constexpr int BS = (MT > 1) ? 4 : 8;
-      auto load_batch = [&](int cb, u32x4 (&wv)[BS][NT], u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
+      auto load_batch = [&](int cb, Frag (&wv)[BS][NT], u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           const int c = min(cb + i, k1 - 1);
 #pragma unroll
-          for (int t = 0; t < NT; ++t) wv[i][t] = wp[t][c * 64];
+          for (int t = 0; t < NT; ++t) wv[i][t] = wt[t].load(c);
 #pragma unroll
           for (int u = 0; u < MT; ++u) xv[i][u] = xp[u][c * 4];
         }
       };
-      // RMSNorm on the fly (NORM, the bf16 pair launch; the launcher guarantees W >= 4, so the
+      // RMSNorm on the fly (NORM, the pair launch; the launcher guarantees W >= 4, so the
       // workgroup is one job and every wavefront reaches the barrier): the rows' sums of squares
       // over the job's W chunks in the canonical order of rmsnorm_row (lane group sums over the
       // chunk's steps in order, then (g0 + g1) + (g2 + g3), then the chunks in order), taken while
@@ -364,24 +363,28 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       float rn[MT];
       u32x4* outp[MT];
       const u32x4* wnp = NORM ? reinterpret_cast<const u32x4*>(a.norm_w) + lg : nullptr;
-      auto mma_batch = [&](int cb, const u32x4 (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
+      auto mma_batch = [&](int cb, const Frag (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           if (cb + i < k1) {
 #pragma unroll
-            for (int u = 0; u < MT; ++u)
+            for (int t = 0; t < NT; ++t) {
+              const bf16x8_t B = as_bf16x8(dense_bf16<FMT>(wv[i][t]));
 #pragma unroll
-              for (int t = 0; t < NT; ++t)
-                accm[u][t] = mfma16(as_bf16x8(xv[i][u]), as_bf16x8(wv[i][t]), accm[u][t]);
+              for (int u = 0; u < MT; ++u) accm[u][t] = mfma16(as_bf16x8(xv[i][u]), B, accm[u][t]);
+            }
           }
         }
       };
       // NORM: each step's fragments normalised right before its MFMAs (short register lives)
-      auto norm_mma_batch = [&](int cb, const u32x4 (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
+      auto norm_mma_batch = [&](int cb, const Frag (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           const int c = min(cb + i, k1 - 1);
           const u32x4 g = wnp[c * 4];
+          bf16x8_t B[NT];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) B[t] = as_bf16x8(dense_bf16<FMT>(wv[i][t]));
 #pragma unroll
           for (int u = 0; u < MT; ++u) {
             u32x4 o;
@@ -392,7 +395,8 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
             if (outp[u]) outp[u][c * 4] = o;
             if (cb + i < k1) {
 #pragma unroll
-              for (int t = 0; t < NT; ++t) accm[u][t] = mfma16(as_bf16x8(o), as_bf16x8(wv[i][t]), accm[u][t]);
+              for (int t = 0; t < NT; ++t)
+                accm[u][t] = mfma16(as_bf16x8(o), B[t], accm[u][t]);
             }
           }
         }
@@ -411,7 +415,8 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         float ssl[MT];
 #pragma unroll
         for (int u = 0; u < MT; ++u) ssl[u] = 0.f;
-        u32x4 wv[BS][NT], xv[BS][MT];
+        Frag wv[BS][NT];
+        u32x4 xv[BS][MT];
         const bool one_batch = k1 - k0 <= BS;
         if (one_batch) {
           // the batch's activations, then its weights: loads complete in issue order, so the
@@ -426,7 +431,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
           for (int i = 0; i < BS; ++i) {
             const int c = min(cb + i, k1 - 1);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) wv[i][t] = wp[t][c * 64];
+            for (int t = 0; t < NT; ++t) wv[i][t] = wt[t].load(c);
           }
 #pragma unroll
           for (int i = 0; i < BS; ++i)
@@ -476,7 +481,8 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         }
       }
       for (; cb < k1; cb += BS) {
-        u32x4 wv[BS][NT], xv[BS][MT];
+        Frag wv[BS][NT];
+        u32x4 xv[BS][MT];
         load_batch(cb, wv, xv);
         if constexpr (NORM)
           norm_mma_batch(cb, wv, xv);
@@ -549,16 +555,17 @@ qmm_small_kernel(QmmArgs a, int n_jobs) {
   small_body<FMT, EPI, W, CPW, JPW, MT>(a, n_jobs, blockIdx.x, blockIdx.y, red);
 }
 
-// Two dense bf16 products over the same activation rows in one launch (the router logits and
-// the shared expert's gate_up): job blocks [0, gx1) run the first, the rest the second. Both
-// use the same K, so the same chunking W, and each keeps the arithmetic of its own launch.
+// Two dense products over the same activation rows in one launch (the router logits, tiled
+// bf16, and the shared expert's gate_up, tiled bf16 or int8 as FMT2): job blocks [0, gx1) run
+// the first, the rest the second. Both use the same K, so the same chunking W, and each keeps the
+// arithmetic of its own launch.
 // NORM: both products RMSNorm their activation rows on the fly (QmmArgs::norm_w), and the first
 // product's job 0 writes the normalised rows (norm_out).
-template <int EPI1, int EPI2, int W, int MT, bool NORM = false>
+template <int EPI1, int EPI2, int W, int MT, bool NORM = false, int FMT2 = FMT_BF16>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
 qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2) {
   constexpr int R1 = SmallCfg<FMT_BF16, EPI1, W, 1, 1, MT>::RED;
-  constexpr int R2 = SmallCfg<FMT_BF16, EPI2, W, 1, 1, MT>::RED;
+  constexpr int R2 = SmallCfg<FMT2, EPI2, W, 1, 1, MT>::RED;
   constexpr int RR = R1 > R2 ? R1 : R2;
   // (NORM: behind the chunk sums, the norm's chunk sums [WAVES][MT][16] floats)
   constexpr int WAVES = W > 4 ? W : 4;
@@ -566,7 +573,7 @@ qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2)
   if (static_cast<int>(blockIdx.x) < gx1)
     small_body<FMT_BF16, EPI1, W, 1, 1, MT, NORM>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
   else
-    small_body<FMT_BF16, EPI2, W, 1, 1, MT, NORM>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
+    small_body<FMT2, EPI2, W, 1, 1, MT, NORM>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
 }
 
 // ============================================================================ large-M kernel
@@ -1188,9 +1195,9 @@ static void launch_small_k(const QmmArgs& a, int64_t mtiles, hipStream_t stream)
   constexpr int WAVES = W > 4 ? W : 4;
   const int n_jobs = ((EPI == EPI_SWIGLU) ? a.n_rows / 32 : a.n_rows / 16) / JPW;
   const int jobs_per_wg = WAVES / W;
-  // dense bf16 products over kSmallMt2MinTiles or more m-tiles: two per wavefront (weights
-  // read once per 32 rows; below that, halving the grid leaves CUs idle)
-  if constexpr (FMT == FMT_BF16) {
+  // dense products over kSmallMt2MinTiles or more m-tiles: two per wavefront (weights read, and
+  // int8 weights dequantized, once per 32 rows; below that, halving the grid leaves CUs idle)
+  if constexpr (fmt_dense(FMT)) {
     if (mtiles >= kSmallMt2MinTiles && !a.offsets && !a.tile_map) {
       dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>((mtiles + 1) / 2));
       qmm_small_kernel<FMT, EPI, W, CPW, JPW, 2><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs);
@@ -1310,7 +1317,7 @@ static int launch_wide(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   return 0;
 }
 
-template <int W>
+template <int W, int FMT2>
 static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream) {
   constexpr int WAVES = W > 4 ? W : 4;
   constexpr int JPWG = WAVES / W;
@@ -1319,14 +1326,25 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
   const dim3 g2(gx1 + gx2, static_cast<unsigned>((mtiles + 1) / 2)), g1(gx1 + gx2, static_cast<unsigned>(mtiles));
   if (a1.norm_w) {
     if (mtiles >= kSmallMt2MinTiles)   // two m-tiles per wavefront, as in launch_small_k
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2, true><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2, true, FMT2><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
     else
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1, true><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1, true, FMT2><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
   } else {
     if (mtiles >= kSmallMt2MinTiles)
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2, false, FMT2><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
     else
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1, false, FMT2><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+  }
+}
+
+template <int FMT2>
+static void launch_pair_f(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream) {
+  switch (bf16_chunks(a1.K)) {
+    case 16: launch_pair_w<16, FMT2>(a1, a2, mtiles, stream); break;
+    case 8: launch_pair_w<8, FMT2>(a1, a2, mtiles, stream); break;
+    case 4: launch_pair_w<4, FMT2>(a1, a2, mtiles, stream); break;
+    case 2: launch_pair_w<2, FMT2>(a1, a2, mtiles, stream); break;
+    default: launch_pair_w<1, FMT2>(a1, a2, mtiles, stream); break;
   }
 }
 
@@ -1342,23 +1360,22 @@ bool pair_norm_fusable(int K, int64_t rows) {
   return steps <= (mt2 ? 4 : 8) || (rows <= 2 && steps <= 16);
 }
 
-int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream) {
+int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2) {
   if (a1.offsets || a2.offsets || a1.dense_rows != a2.dense_rows || a1.K != a2.K || a1.K % 32 ||
       a1.n_rows % 16 || a2.n_rows % 32 || a1.dense_rows <= 0)
-    return fail("qmm pair: two dense bf16 products over the same rows and K required");
+    return fail("qmm pair: two dense products over the same rows and K required");
+  if (fmt2 != FMT_BF16 && fmt2 != FMT_INT8) return fail("qmm pair: the second product is bf16 or int8");
+  if (fmt2 == FMT_INT8 && (a1.K % 64 || !a2.sb)) return fail("qmm pair: int8 weights need K % 64 == 0 and sb");
   if ((a1.norm_w != nullptr) != (a2.norm_w != nullptr) || a2.norm_out)
     return fail("qmm pair: the fused norm applies to both products; the first writes the rows");
   if (a1.norm_w && !pair_norm_fusable(a1.K, a1.dense_rows))
     return fail("qmm pair: the fused norm needs one job per workgroup and one load batch per chunk");
   const int64_t mtiles = (a1.dense_rows + kSmallMTile - 1) / kSmallMTile;
   if (mtiles > 65535) return fail("qmm pair: too many m-tiles for one launch");
-  switch (bf16_chunks(a1.K)) {
-    case 16: launch_pair_w<16>(a1, a2, mtiles, stream); break;
-    case 8: launch_pair_w<8>(a1, a2, mtiles, stream); break;
-    case 4: launch_pair_w<4>(a1, a2, mtiles, stream); break;
-    case 2: launch_pair_w<2>(a1, a2, mtiles, stream); break;
-    default: launch_pair_w<1>(a1, a2, mtiles, stream); break;
-  }
+  if (fmt2 == FMT_INT8)
+    launch_pair_f<FMT_INT8>(a1, a2, mtiles, stream);
+  else
+    launch_pair_f<FMT_BF16>(a1, a2, mtiles, stream);
   return check_launch("qmm pair");
 }
 
@@ -1379,6 +1396,7 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (regime == QMOE_REGIME_SMALL) {
     if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int3/int4/int6 need K % 128 == 0");
     if (fmt == FMT_BF16 && a.K % 32) return fail("qmm: bf16 needs K % 32 == 0");
+    if (fmt == FMT_INT8 && (a.K % 64 || !a.sb)) return fail("qmm: int8 needs K % 64 == 0 and sb");
     if (a.n_rows % (epi == EPI_SWIGLU ? 32 : 16)) return fail("qmm: weight rows not a tile multiple");
     // The chunk count depends on the shape only (never on the token count), so a row's
     // summation order, and therefore its result, is the same at every batch size (batch
@@ -1408,6 +1426,10 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT3, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT3, EPI_BF16);
       else QMOE_SMALL(FMT_INT3, EPI_F32);
+    } else if (fmt == FMT_INT8) {
+      if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_INT8, EPI_SWIGLU);
+      else if (epi == EPI_BF16) QMOE_SMALL(FMT_INT8, EPI_BF16);
+      else QMOE_SMALL(FMT_INT8, EPI_F32);
     } else {
       if (epi == EPI_SWIGLU) QMOE_SMALL(FMT_BF16, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_SMALL(FMT_BF16, EPI_BF16);
@@ -1418,6 +1440,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     if (fmt == FMT_INT6 || fmt == FMT_INT3)
       return fail("qmm(large): int3/int6 weights run in the small regime only (the large kernels "
                   "stage int4 tile superblocks)");
+    if (fmt == FMT_INT8)
+      return fail("qmm(large): int8 weights run in the small regime only (expand them to bf16 "
+                  "for the large kernels)");
     if (a.K % 128) return fail("qmm(large): K % 128 == 0 required");
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
     if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))

@@ -265,9 +265,65 @@ struct QmmArgs {
   uint16_t* norm_out;         // nullable: the normalised rows, written by job 0's wavefronts
 };
 
-enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3 };
-// affine-quantized weight formats (int3, int4 or int6 codes with per-64 scale/bias)
+enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3, FMT_INT8 = 4 };
+// affine-quantized weight formats summed as codes (int3, int4 or int6 codes with per-64
+// scale/bias, the affine part applied to the products). int8 weights are not among them: they
+// are dequantized to bf16 in registers and run the bf16 products (dense formats).
 constexpr bool fmt_quant(int fmt) { return fmt == FMT_INT4 || fmt == FMT_INT6 || fmt == FMT_INT3; }
+constexpr bool fmt_dense(int fmt) { return fmt == FMT_BF16 || fmt == FMT_INT8; }
+
+// One lane's weight fragment of a 32-deep step of a dense product: 8 bf16 weights (tiled bf16),
+// or 8 int8 codes with their row's (scale, bias) pair of the 64-column group (tiled int8).
+template <int FMT> struct DenseFrag { u32x4 w; };
+template <> struct DenseFrag<FMT_INT8> { u32x2 q; uint32_t sb; };
+
+// Streams of a tiled dense matrix for one lane: bf16 [rows/16][K/32][64][8] or int8 codes
+// [rows/16][K/32][64][8 B] + sb [rows/16][K/64][16][scale, bias]; `tile` = 16-row tile index of
+// the whole stack (expert * rows/16 + tile of the expert).
+template <int FMT>
+struct DenseTile {
+  const void* p;
+  const uint32_t* sb;
+  __device__ __forceinline__ void init(const void* codes, const uint16_t* sbase, int64_t tile, int K,
+                                       int lane) {
+    const int nks = K / 32;
+    if constexpr (FMT == FMT_INT8) {
+      p = static_cast<const u32x2*>(codes) + tile * nks * 64 + lane;
+      sb = reinterpret_cast<const uint32_t*>(sbase) + tile * (K / 64) * 16 + (lane & 15);
+    } else {
+      p = static_cast<const u32x4*>(codes) + tile * nks * 64 + lane;
+      sb = nullptr;
+    }
+  }
+  // fragment of step c
+  __device__ __forceinline__ DenseFrag<FMT> load(int c) const {
+    if constexpr (FMT == FMT_INT8)
+      return DenseFrag<FMT>{static_cast<const u32x2*>(p)[c * 64], sb[(c >> 1) * 16]};
+    else
+      return DenseFrag<FMT>{static_cast<const u32x4*>(p)[c * 64]};
+  }
+};
+
+// bf16 fragment of a dense weight fragment. int8: code byte j (LSB-first) becomes
+// bf16(fmaf(s, c_j, b)), the product exact in fp32 (8-bit x 8-bit mantissas), rounded to nearest
+// even: the same bits as the dequant of the native int8 matrix (qmoe_dequant), so the int8 and
+// bf16 forms of a matrix give identical products.
+template <int FMT>
+__device__ __forceinline__ u32x4 dense_bf16(const DenseFrag<FMT>& f) {
+  if constexpr (FMT == FMT_INT8) {
+    const float s = __uint_as_float(f.sb << 16), b = __uint_as_float(f.sb & 0xFFFF0000u);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = f.q[j >> 1] >> (16 * (j & 1));
+      const float lo = static_cast<float>(w & 0xFFu), hi = static_cast<float>((w >> 8) & 0xFFu);
+      o[j] = pack_bf16x2_rne(fmaf(s, lo, b), fmaf(s, hi, b));
+    }
+    return o;
+  } else {
+    return f.w;
+  }
+}
 enum { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,
@@ -278,19 +334,26 @@ inline int bf16_chunks(int K) {
   const int nks = K / 32;
   return (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
 }
-// One launch of two dense bf16 small-regime products over the same rows and K: a1 with the
-// fp32 epilogue (router logits), a2 with SwiGLU (shared expert gate_up).
-int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream);
+// One launch of two dense small-regime products over the same rows and K: a1 (tiled bf16) with
+// the fp32 epilogue (router logits), a2 (tiled bf16 or int8, fmt2) with SwiGLU (shared expert
+// gate_up).
+int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream,
+                         int fmt2 = FMT_BF16);
 // Whether the pair launch over `rows` rows of K normalises them itself (QmmArgs::norm_w): one
 // job per workgroup (K >= 1024), and each wavefront's K chunk one load batch (8 32-wide steps
 // with one m-tile per wavefront, 4 with two), or up to 16 steps for one or two rows.
 bool pair_norm_fusable(int K, int64_t rows);
-// Decode combine with the shared expert's down projection fused in (wd: tiled bf16 [H, Is]).
+// Decode combine with the shared expert's down projection fused in (wd: tiled bf16 [H, Is], or
+// tiled int8 codes with their scale/bias wd_sb when fmt is FMT_INT8).
 // resid (nullable): the decoder layer's residual row, y = bf16(resid + bf16(block output)).
 int launch_combine_shared(const uint16_t* d, const int32_t* inv, const float* w, int N, int k,
-                          int H, const uint16_t* sh_h, int Is, const uint16_t* wd,
-                          const float* shared_gate, uint16_t* y, hipStream_t stream,
-                          const uint16_t* resid = nullptr);
+                          int H, const uint16_t* sh_h, int Is, const void* wd,
+                          const uint16_t* wd_sb, int fmt, const float* shared_gate, uint16_t* y,
+                          hipStream_t stream, const uint16_t* resid = nullptr);
+// Tiled int8 [rows/16][K/32][64][8 B] + sb -> tiled bf16 [rows/16][K/32][64][8], each weight
+// bf16(s*q + b) as dense_bf16 makes it.
+int launch_expand_int8(const uint32_t* codes, const uint16_t* sb, int64_t rows, int K,
+                       uint16_t* out, hipStream_t stream);
 // act [rows][K] bf16 -> act16 fp16 with a per-row power-of-two scale (exact for bf16 values
 // within 2^28 of the row's largest magnitude); row_sinv[r] = the inverse scale.
 int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16, float* row_sinv,

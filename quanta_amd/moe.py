@@ -335,6 +335,8 @@ class Prepared:
     sh_dn: torch.Tensor | None
     bias: torch.Tensor | None
     mixed: L.QmoeMixed | None = None
+    sh_gu_sb: torch.Tensor | None = None   # int8 shared expert: tiled scale/bias
+    sh_dn_sb: torch.Tensor | None = None
 
 
 def _prepare_router(gate: torch.Tensor, sgate: torch.Tensor | None, E: int, H: int):
@@ -362,14 +364,44 @@ def _prepare_router(gate: torch.Tensor, sgate: torch.Tensor | None, E: int, H: i
 
 
 def _prepare_shared(p: dict, H: int, Is: int):
-    wg, wu, wd = p["shared_gate_proj"], p["shared_up_proj"], p["shared_down_proj"]
-    for t, nm in ((wg, "shared_gate_proj"), (wu, "shared_up_proj"), (wd, "shared_down_proj")):
+    """Shared expert -> (format, gate|up tiles, their sb, down tiles, their sb). bf16 [Is, H] /
+    [H, Is] matrices tile as bf16. int8 triplets {packed, scale, bias, group_size, bits: 8}, the
+    bake's shared-expert format (src/quanta/qwen35/bake.py:106-110, 150-151), stay int8: the
+    kernels dequantize them in registers to the bf16 weights the reference's loader makes of them
+    (src/quanta/qwen35/artifact.py:105-115), so the outputs are those of the dequantized bf16
+    matrices, at half the bytes read."""
+    names = ("shared_gate_proj", "shared_up_proj", "shared_down_proj")
+    wg, wu, wd = (p[nm] for nm in names)
+    quant = [isinstance(t, dict) for t in (wg, wu, wd)]
+    if any(quant) and not all(quant):
+        raise ValueError("shared expert: gate, up and down must all be int8 triplets or all bf16")
+    if all(quant):
+        for t, nm in zip((wg, wu, wd), names):
+            if int(t.get("bits", 8)) != 8:
+                raise ValueError(f"{nm}: a quantized shared expert must be int8 (bits 8), as baked")
+        gs = int(wg.get("group_size", 64))
+        if any(int(t.get("group_size", 64)) != gs for t in (wu, wd)) or gs not in (64, 128):
+            raise ValueError("shared expert: one group size (64 or 128) for gate, up and down")
+        if (tuple(wg["packed"].shape) != (Is, H // 4) or tuple(wu["packed"].shape) != (Is, H // 4)
+                or tuple(wd["packed"].shape) != (H, Is // 4)):
+            raise ValueError("shared expert int8 shapes must be gate/up [Is, H/4] and down [H, Is/4] words")
+        cat = [torch.cat([wg[k], wu[k]], dim=0).contiguous() for k in ("packed", "scale", "bias")]
+        gu_c, gu_sb = ops.tile_int8(*cat, group_size=gs)
+        dn_c, dn_sb = ops.tile_int8(wd["packed"].contiguous(), wd["scale"].contiguous(),
+                                    wd["bias"].contiguous(), group_size=gs)
+        return "int8", gu_c, gu_sb, dn_c, dn_sb
+    for t, nm in zip((wg, wu, wd), names):
         if t.dtype != torch.bfloat16:
-            raise TypeError(f"{nm} must be bf16 (the shared expert runs in bf16)")
+            raise TypeError(f"{nm} must be bf16 or an int8 triplet (the shared expert runs in bf16)")
     if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is):
         raise ValueError("shared expert shapes must be gate/up [Is, H] and down [H, Is]")
     gu = torch.cat([wg, wu], dim=0).contiguous()
-    return ops.tile_bf16(gu), ops.tile_bf16(wd.contiguous())
+    return "bf16", ops.tile_bf16(gu), None, ops.tile_bf16(wd.contiguous()), None
+
+
+def _anchor(v) -> torch.Tensor:
+    """The tensor a memo entry of parameter value `v` hangs off (a triplet's packed codes)."""
+    return v["packed"] if isinstance(v, dict) else v
 
 
 def gated_activation(cfg) -> tuple[int, float, float]:
@@ -433,10 +465,11 @@ def _build_prepared(p: dict, cfg, *, topk: int | None, regime: int) -> Prepared:
     gate = p["gate"]
     rkind, rw, rrows, sg32 = _memo(gate, ("router", sgate is not None), (gate, sgate),
                                    lambda: _prepare_router(gate, sgate, E, H))
-    sh_gu = sh_dn = None
+    sh_fmt, sh_gu, sh_gu_sb, sh_dn, sh_dn_sb = "bf16", None, None, None, None
     if has_shared:
         shw = (p["shared_gate_proj"], p["shared_up_proj"], p["shared_down_proj"])
-        sh_gu, sh_dn = _memo(shw[0], "shared", shw, lambda: _prepare_shared(p, H, Is))
+        sh_fmt, sh_gu, sh_gu_sb, sh_dn, sh_dn_sb = _memo(_anchor(shw[0]), "shared", shw,
+                                                         lambda: _prepare_shared(p, H, Is))
     bias = p.get("e_score_correction_bias")
     if bias is not None:
         bias = bias.to(torch.float32).reshape(E).contiguous()
@@ -457,6 +490,7 @@ def _build_prepared(p: dict, cfg, *, topk: int | None, regime: int) -> Prepared:
     c.router_format = L.ROUTER_BF16_TILED if rkind == "bf16" else L.ROUTER_F32
     c.router_rows = rrows
     c.shared_gated = int(sgate is not None)
+    c.shared_format = L.FMT_INT8_G64 if sh_fmt == "int8" else L.FMT_BF16
     c.regime = regime
     c.act, c.act_alpha, c.act_limit = gated_activation(cfg)
     # DeepSeek-V4's activation-aware scales (src/quanta/dsv4/moe.py:112-137): gate and up
@@ -481,14 +515,16 @@ def _build_prepared(p: dict, cfg, *, topk: int | None, regime: int) -> Prepared:
     w.dn_sb = dn["sb"].data_ptr() if dn["sb"] is not None else None
     w.sh_gu = sh_gu.data_ptr() if sh_gu is not None else None
     w.sh_dn = sh_dn.data_ptr() if sh_dn is not None else None
+    w.sh_gu_sb = sh_gu_sb.data_ptr() if sh_gu_sb is not None else None
+    w.sh_dn_sb = sh_dn_sb.data_ptr() if sh_dn_sb is not None else None
     w.awq_gu = awq_gu.data_ptr() if awq_gu is not None else None
     w.awq_dn = awq_dn.data_ptr() if awq_dn is not None else None
     gu_rexp, dn_rexp = gu.get("rexp"), dn.get("rexp")
     w.gu_rexp = gu_rexp.data_ptr() if gu_rexp is not None else None
     w.dn_rexp = dn_rexp.data_ptr() if dn_rexp is not None else None
-    keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn, awq_gu, awq_dn)
+    keep = (rw, bias, sg32, gu, dn, sh_gu, sh_dn, sh_gu_sb, sh_dn_sb, awq_gu, awq_dn)
     return Prepared(c, w, keep, rw if rkind == "bf16" else None, rw if rkind == "f32" else None,
-                    sg32, gu, dn, sh_gu, sh_dn, bias)
+                    sg32, gu, dn, sh_gu, sh_dn, bias, sh_gu_sb=sh_gu_sb, sh_dn_sb=sh_dn_sb)
 
 
 def _prepare_mixed(p: dict, cfg, *, topk, regime) -> Prepared:
@@ -620,13 +656,15 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
                         n_experts=E)
     sh_out = None
     if c.shared_inter > 0:
-        sreg = _dense_regime(n, c.hidden)
-        sh_h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.shared_inter, weight_format=L.FMT_BF16,
-                               codes=pr.sh_gu, sb=None, epilogue=L.EPI_SWIGLU, out_rows=n,
+        # (int8 shared weights: the small regime, which dequantizes them in registers)
+        sfmt = c.shared_format
+        sreg = L.REGIME_SMALL if sfmt == L.FMT_INT8_G64 else _dense_regime(n, c.hidden)
+        sh_h = ops.grouped_qmm(xf, K=c.hidden, n_rows=2 * c.shared_inter, weight_format=sfmt,
+                               codes=pr.sh_gu, sb=pr.sh_gu_sb, epilogue=L.EPI_SWIGLU, out_rows=n,
                                regime=sreg, dense_rows=n, glu=c.act, glu_alpha=c.act_alpha,
                                glu_limit=c.act_limit)
-        sh_out = ops.grouped_qmm(sh_h, K=c.shared_inter, n_rows=c.hidden, weight_format=L.FMT_BF16,
-                                 codes=pr.sh_dn, sb=None, epilogue=L.EPI_BF16, out_rows=n,
+        sh_out = ops.grouped_qmm(sh_h, K=c.shared_inter, n_rows=c.hidden, weight_format=sfmt,
+                                 codes=pr.sh_dn, sb=pr.sh_dn_sb, epilogue=L.EPI_BF16, out_rows=n,
                                  regime=sreg, dense_rows=n)
     return ops.combine(d, inv, w_all, sh_out, sg)
 
@@ -638,8 +676,9 @@ def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chun
     Mirrors `qwen35_moe` (src/quanta/qwen35/moe.py:154-202). `p` keys: gate [E,H];
     experts_gate_up / experts_down as packed triplet dicts {packed, scale, bias, group_size, bits}
     (int4 g64; or TiledExperts) or bf16 stacks [E,2I,H] / [E,H,I]; shared_gate_proj,
-    shared_up_proj [Is,H]; shared_down_proj [H,Is]; shared_expert_gate [1,H] (omit it for an
-    ungated DeepSeek/GLM shared expert); optional e_score_correction_bias [E].
+    shared_up_proj [Is,H]; shared_down_proj [H,Is] in bf16, or all three as the bake's int8
+    triplets (same outputs as their bf16 dequant, half the bytes read); shared_expert_gate [1,H]
+    (omit it for an ungated DeepSeek/GLM shared expert); optional e_score_correction_bias [E].
     `sparse=False` is the run-every-expert oracle and, as in the reference, refuses packed experts.
     Tokens beyond `token_chunk` are processed chunk by chunk (output-equivalent).
     """

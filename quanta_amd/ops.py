@@ -111,9 +111,10 @@ def row_exponents(scale: torch.Tensor, bias: torch.Tensor, *, bits: int = 4,
 
 def _tile_narrow(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, bits: int,
                  group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Native int3/int6 stack [E, rows, K*bits/32] (+ scale/bias [E, rows, K/group_size]) -> the
-    tiled layout of the decode kernel (codes: the planes of the code bits per tile superblock, the
-    same byte count; sb as tile_int4)."""
+    """Native int3/int6/int8 stack [E, rows, K*bits/32] (+ scale/bias [E, rows, K/group_size]) ->
+    the tiled layout of the decode kernel (codes: the same byte count; int3/int6 the planes of the
+    code bits per tile superblock, int8 one byte per weight in the bf16 tiling's order; sb as
+    tile_int4)."""
     packed = _words(packed, "packed")
     _need(scale, torch.bfloat16, "scale")
     _need(bias, torch.bfloat16, "bias")
@@ -129,9 +130,11 @@ def _tile_narrow(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, 
         raise ValueError(f"tile_int{bits}: group_size must be 64 or 128")
     if scale.shape != (E, rows, K // group_size) or bias.shape != scale.shape:
         raise ValueError(f"tile_int{bits}: scale/bias must be [E, rows, K/{group_size}]")
+    if packed.data_ptr() % 16:   # (the int8 tiling reads 8-byte pieces of the rows)
+        packed = packed.clone()
     codes = torch.empty(E * rows * W, dtype=torch.int32, device=packed.device)
     sb = torch.empty(E * rows * (K // 64) * 2, dtype=torch.bfloat16, device=packed.device)
-    fn = L.load().qmoe_tile_int6 if bits == 6 else L.load().qmoe_tile_int3
+    fn = {6: L.load().qmoe_tile_int6, 3: L.load().qmoe_tile_int3, 8: L.load().qmoe_tile_int8}[bits]
     L.check(fn(_p(packed), _p(scale), _p(bias), E, rows, K, group_size, _p(codes), _p(sb),
                _stream(packed.device)), f"qmoe_tile_int{bits}")
     return codes, sb
@@ -141,6 +144,13 @@ def tile_int6(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
               group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
     """Native int6 stack -> the decode kernel's tiled int6 layout (qmoe_tile_int6)."""
     return _tile_narrow(packed, scale, bias, 6, group_size)
+
+
+def tile_int8(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
+              group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Native int8 matrix [rows, K/4] or stack [E, rows, K/4] -> the tiled int8 layout the dense
+    kernels dequantize in registers (qmoe_tile_int8): the bake's int8 shared expert."""
+    return _tile_narrow(packed, scale, bias, 8, group_size)
 
 
 def tile_int3(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor, *,
@@ -253,7 +263,7 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     _need(act, torch.bfloat16, "act")
     if act.dim() != 2 or act.shape[1] != K:
         raise ValueError("grouped_qmm: act must be [rows, K]")
-    if weight_format in (L.FMT_INT4_G64, L.FMT_INT6_G64, L.FMT_INT3_G64):
+    if weight_format in (L.FMT_INT4_G64, L.FMT_INT6_G64, L.FMT_INT3_G64, L.FMT_INT8_G64):
         codes = _words(codes, "codes")
         _need(sb, torch.bfloat16, "sb")
     else:

@@ -148,10 +148,11 @@ def zipf_router(gate: torch.Tensor, seed: int = 4) -> torch.Tensor:
 
 def make_layer(name: str | SynthSpec, *, device="cuda", seed: int | None = None,
                layer: int = 0, bits: int = 4, down_bits: int | None = None,
-               group_size: int = 64) -> dict:
+               group_size: int = 64, shared_bits: int = 16) -> dict:
     """Parameter dict with the reference keys (src/quanta/qwen35/moe.py:159-161); routed experts as
     packed triplets in the reference's native layout (gate_up int`bits`, down int`down_bits`,
-    default the same width)."""
+    default the same width). shared_bits 8: the shared expert as the bake stores it, int8 g64
+    triplets of the same bf16 draws (src/quanta/qwen35/bake.py:106-110, 150-151)."""
     s = SPECS[name] if isinstance(name, str) else name
     c = s.cfg
     cid = int(name[1]) if isinstance(name, str) else 9
@@ -169,6 +170,12 @@ def make_layer(name: str | SynthSpec, *, device="cuda", seed: int | None = None,
         p["shared_gate_proj"] = _normal((Is, H), 0.02, g, device, torch.bfloat16)
         p["shared_up_proj"] = _normal((Is, H), 0.02, g, device, torch.bfloat16)
         p["shared_down_proj"] = _normal((H, Is), 0.02, g, device, torch.bfloat16)
+        if shared_bits == 8:
+            for key in ("shared_gate_proj", "shared_up_proj", "shared_down_proj"):
+                pk, sc, bi = quantize_affine(p[key], 8, group_size=64)
+                p[key] = {"packed": pk, "scale": sc, "bias": bi, "group_size": 64, "bits": 8}
+        elif shared_bits != 16:
+            raise ValueError("shared_bits: 16 (bf16) or 8 (int8 g64, as baked)")
         if s.shared_gated:
             p["shared_expert_gate"] = _normal((1, H), 0.02, g, device, torch.bfloat16)
     if s.bias_std > 0:
@@ -187,16 +194,19 @@ def make_inputs(name: str | SynthSpec, N: int, *, device="cuda", seed: int = 0) 
 
 
 def algorithmic_bytes(cfg, distinct_experts: int, N: int, router_bytes_per_elem: int = 2,
-                      bits: int = 4, down_bits: int | None = None, group_size: int = 64) -> int:
+                      bits: int = 4, down_bits: int | None = None, group_size: int = 64,
+                      shared_bits: int = 16) -> int:
     """Bytes a layer call must move at minimum: U*B_e + S + R + A with
     B_e = 2*I*H*(bits/8 + 4/g) + I*H*(down_bits/8 + 4/g) (codes + a bf16 scale and bias per group
     of g: 0.5625 B per weight for int4 g64, 0.8125 for int6 g64, 0.40625 for int3 g128),
-    S = 3*Is*H*2, R = E*H*elem, A = 4*N*H (bf16 in and out)."""
+    S = 3*Is*H*2 (bf16) or 3*Is*H*(1 + 4/64) (int8 g64), R = E*H*elem, A = 4*N*H (bf16 in and
+    out)."""
     H, E, I = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size
     Is = cfg.shared_expert_intermediate_size
     db = bits if down_bits is None else down_bits
     be = (2 * I * H * (bits * group_size + 32) + I * H * (db * group_size + 32)) // (8 * group_size)
-    return distinct_experts * be + 3 * Is * H * 2 + E * H * router_bytes_per_elem + 4 * N * H
+    sh = 3 * Is * H * 2 if shared_bits == 16 else 3 * Is * H * (8 * 64 + 32) // (8 * 64)
+    return distinct_experts * be + sh + E * H * router_bytes_per_elem + 4 * N * H
 
 
 def algorithmic_flops(cfg, N: int, k: int | None = None) -> int:

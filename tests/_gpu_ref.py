@@ -36,6 +36,22 @@ def dequant_exact(packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor,
     return s * q.to(torch.float64) + b
 
 
+def shared_weight(v) -> torch.Tensor:
+    """A shared-expert projection in float64: bf16 as given, or an int8 triplet dequantized to
+    bf16 (oracle.moe.shared_weight: fp32(s*q + b) rounded to bf16; s*q is exact in float64 and in
+    float32, so rounding the exact float64 sum to float32 then bf16 gives the same bits)."""
+    if not isinstance(v, dict):
+        return v.to(torch.float64)
+    pk, sc, bi = v["packed"], v["scale"], v["bias"]
+    rows, nw = pk.shape
+    shifts = torch.arange(0, 32, 8, dtype=torch.int32, device=pk.device)
+    q = ((pk.to(torch.int32)[:, :, None] >> shifts) & 0xFF).reshape(rows, nw * 4)
+    gs = int(v.get("group_size", 64))
+    s = sc.to(torch.float64).repeat_interleave(gs, dim=1)
+    b = bi.to(torch.float64).repeat_interleave(gs, dim=1)
+    return round_bf16(s * q.to(torch.float64) + b)
+
+
 def _silu(v: torch.Tensor) -> torch.Tensor:
     return v / (1.0 + torch.exp(-v))
 
@@ -70,10 +86,12 @@ def block_reference(p: dict, cfg, x: torch.Tensor, idx: np.ndarray, w: np.ndarra
         del wd
     y = (d.reshape(N, k, H) * w_t[:, :, None]).sum(dim=1)
     if p.get("shared_gate_proj") is not None:
-        g = round_bf16(x64 @ p["shared_gate_proj"].to(torch.float64).T)
-        u = round_bf16(x64 @ p["shared_up_proj"].to(torch.float64).T)
+        wg, wu, wd = (shared_weight(p[k]) for k in ("shared_gate_proj", "shared_up_proj",
+                                                    "shared_down_proj"))
+        g = round_bf16(x64 @ wg.T)
+        u = round_bf16(x64 @ wu.T)
         hs = round_bf16(_silu(g) * u)
-        out = round_bf16(hs @ p["shared_down_proj"].to(torch.float64).T)
+        out = round_bf16(hs @ wd.T)
         if p.get("shared_expert_gate") is not None:
             sg = torch.sigmoid(x64 @ p["shared_expert_gate"].to(torch.float64).reshape(-1))
             out = out * sg[:, None]

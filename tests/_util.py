@@ -75,8 +75,13 @@ def oracle_params_from_torch(p: dict) -> dict:
         out[f"{pre}_scale"] = bits_np(p[key]["scale"])
         out[f"{pre}_bias"] = bits_np(p[key]["bias"])
     for k in ("shared_gate_proj", "shared_up_proj", "shared_down_proj", "shared_expert_gate"):
-        if p.get(k) is not None:
-            out[k] = f64(p[k])
+        v = p.get(k)
+        if isinstance(v, dict):   # the bake's int8 shared-expert triplet
+            out[k] = {"packed": words_np(v["packed"]), "scale": bits_np(v["scale"]),
+                      "bias": bits_np(v["bias"]), "group_size": int(v.get("group_size", 64)),
+                      "bits": int(v.get("bits", 8))}
+        elif v is not None:
+            out[k] = f64(v)
     if p.get("e_score_correction_bias") is not None:
         out["e_score_correction_bias"] = f64(p["e_score_correction_bias"])
     for pre, key in (("gu", "experts_gate_up"), ("dn", "experts_down")):

@@ -13,7 +13,7 @@ from quanta_amd import _lib as L
 
 def test_library_loads_and_abi_version():
     lib = L.load()
-    assert lib.qmoe_abi_version() == L.ABI_VERSION == 6
+    assert lib.qmoe_abi_version() == L.ABI_VERSION == 7
 
 
 def test_every_header_symbol_is_exported_and_bound():
@@ -75,6 +75,16 @@ _DUMMY = ctypes.c_void_p(16)   # never dereferenced: each call fails validation 
      "group_size"),
     (lambda lib: lib.qmoe_dequant(None, None, None, 4, 128, 4, 32, None, None), "group_size 64 or 128"),
     (lambda lib: lib.qmoe_tile_int4(None, None, None, 1, 16, 128, 32, None, None, None), "64 or 128"),
+    (lambda lib: lib.qmoe_tile_int8(None, None, None, 1, 16, 96, 64, None, None, None), "in_features % 64"),
+    (lambda lib: lib.qmoe_tile_int8(None, None, None, 1, 8, 128, 64, None, None, None), "rows % 16"),
+    (lambda lib: lib.qmoe_tile_int8(_DUMMY, _DUMMY, _DUMMY, 1, 16, 128, 64, None, _DUMMY, None),
+     "null pointer"),
+    (lambda lib: lib.qmoe_grouped_qmm(_DUMMY, 1, None, 1, 1, None, None, None, 1, 1, 128, 32, 4,
+                                      _DUMMY, None, None, 1, 0, 1.0, 0.0, _DUMMY, 32, 1, None, 0,
+                                      None), "quantized weights need sb"),
+    (lambda lib: lib.qmoe_grouped_qmm(_DUMMY, 1, None, 1, 1, None, None, None, 1, 1, 128, 32, 5,
+                                      _DUMMY, _DUMMY, None, 1, 0, 1.0, 0.0, _DUMMY, 32, 1, None, 0,
+                                      None), "bad weight_format"),
 ])
 def test_invalid_arguments_rejected(call, fragment):
     rc = call(L.load())
@@ -138,6 +148,30 @@ def test_forward_rejects_mixed_bf16_and_unknown_down_format():
             continue
         rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
         assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()
+
+
+def test_forward_rejects_bad_shared_format():
+    """shared_format must be named (bf16 or int8 g64); an int8 shared expert needs its scale/bias
+    arrays; the large-M regime's expanded bf16 copy is part of the workspace."""
+    lib = L.load()
+    base = dict(hidden=512, n_experts=16, top_k=2, inter=128, shared_inter=256, scoring=0,
+                norm_topk=1, n_group=1, topk_group=1, routed_scale=1.0, router_format=1,
+                router_rows=0, shared_gated=0, regime=0, expert_format=0, down_format=0)
+    dummy = ctypes.c_void_p(16)
+    w = L.QmoeWeights(router_w=16, gu_codes=16, gu_sb=16, dn_codes=16, dn_sb=16, sh_gu=16, sh_dn=16)
+    for fmt, frag in ((L.FMT_INT4_G64, "shared_format must be"), (L.FMT_INT6_G64, "shared_format must be"),
+                      (L.FMT_INT8_G64, "needs sh_gu_sb and sh_dn_sb")):
+        cfg = L.QmoeConfig(shared_format=fmt, **base)
+        rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 30, None)
+        assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()
+    assert L.QmoeConfig().shared_format == L.FMT_BF16
+    c16 = L.QmoeConfig(shared_format=L.FMT_BF16, **base)
+    c8 = L.QmoeConfig(shared_format=L.FMT_INT8_G64, **base)
+    for n in (1, 64, 256):
+        assert lib.qmoe_forward_workspace(ctypes.byref(c8), n) == lib.qmoe_forward_workspace(ctypes.byref(c16), n)
+    extra = 3 * 256 * 512 * 2
+    assert (lib.qmoe_forward_workspace(ctypes.byref(c8), 300)
+            == lib.qmoe_forward_workspace(ctypes.byref(c16), 300) + extra)
 
 
 def test_forward_rejects_bad_awq_config():

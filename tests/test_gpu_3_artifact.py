@@ -99,6 +99,13 @@ def test_block_from_artifact(gpu, tmp_path, shared_int8):
         assert_close(f64(y), a["y_exact"], "c1mini from artifact")
     m = art.moe_module(0, gpu)
     assert torch.equal(m(x[None])[0], y)
+    # the int8 shared expert handed over as its triplets (read at half the bytes): same outputs
+    p8 = art.moe_packed(0, gpu, shared="int8")
+    for proj in deq:
+        assert isinstance(p8[f"shared_{proj}"], dict) == shared_int8, proj
+    for n in (1, 9, 16):
+        assert torch.equal(qwen35_moe(x[None, :n], p8, art.moe_config()),
+                           qwen35_moe(x[None, :n], p, art.moe_config())), n
 
 
 def test_sigmoid_router_from_artifact(gpu, tmp_path):

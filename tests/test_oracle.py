@@ -641,3 +641,60 @@ def test_route_sqrtsoftplus_matches_torch_softplus():
         assert list(idx[r]) == order
         sel = scores[r, order]
         assert np.allclose(w[r], sel / (sel.sum() + 1e-20) * 1.5, rtol=1e-14)
+
+
+def test_shared_weight_int8_triplet():
+    """oracle.moe.shared_weight: an int8 shared-expert triplet becomes the bf16 matrix of its
+    dequant (codes 0 and 255 at the closed forms b and 255 s + b; random codes at the rounding
+    pinned by test_dequant_exact_rational), bf16 values pass through, and the block with the
+    triplets equals the block with their dequantized matrices."""
+    s_bits = oq.f32_to_bf16_bits(np.array([[0.0078125, 0.25]], np.float32))
+    b_bits = oq.f32_to_bf16_bits(np.array([[-1.0, 3.0]], np.float32))
+    codes = np.array([[0] * 32 + [255] * 32 + [0] * 32 + [255] * 32], np.uint32)
+    t = {"packed": oq.pack_affine(codes, 8), "scale": s_bits, "bias": b_bits, "group_size": 64,
+         "bits": 8}
+    w = om.shared_weight(t)
+    assert w.shape == (1, 128)
+    assert np.all(w[0, :32] == -1.0) and np.all(w[0, 32:64] == 255 * 0.0078125 - 1.0)
+    assert np.all(w[0, 64:96] == 3.0) and np.all(w[0, 96:] == oq.round_bf16(np.array(255 * 0.25 + 3.0)))
+    plain = np.ones((2, 3))
+    assert om.shared_weight(plain) is plain
+    with pytest.raises(ValueError):
+        om.shared_weight(dict(t, bits=4))
+
+    rng = np.random.default_rng(29)
+    E, H, I, Is, k, N = 8, 128, 64, 64, 3, 5
+    p = _tiny_layer(rng, E=E, H=H, I=I, Is=Is)
+    q = dict(p)
+    for key in ("shared_gate_proj", "shared_up_proj", "shared_down_proj"):
+        words, sb, bb, _ = oq.quantize_rtn(p[key].astype(np.float32), bits=8, group_size=64)
+        q[key] = {"packed": words, "scale": sb, "bias": bb, "group_size": 64, "bits": 8}
+        p[key] = oq.bf16_bits_to_f32(oq.dequant_bf16_bits(words, sb, bb, p[key].shape[1], bits=8)
+                                     ).astype(np.float64)
+    x = oq.round_bf16(rng.standard_normal((N, H)))
+    y_t, _ = om.moe_forward(x, q, k=k, inter=I)
+    y_d, _ = om.moe_forward(x, p, k=k, inter=I)
+    assert np.array_equal(y_t, y_d)
+
+
+def test_synth_int8_shared_layer_cpu():
+    """synth.make_layer(shared_bits=8): the bake's int8 g64 triplets of the same bf16 draws (the
+    rest of the layer unchanged), each weight within half a quantization step of its draw."""
+    from quanta_amd import synth
+    from quanta_amd.quant import unpack_affine
+
+    s = synth.scaled_spec("c1", hidden_size=256, num_experts=4, moe_intermediate_size=128,
+                          shared_expert_intermediate_size=128)
+    p16 = synth.make_layer(s, device="cpu", seed=5)
+    p8 = synth.make_layer(s, device="cpu", seed=5, shared_bits=8)
+    assert torch.equal(p16["gate"], p8["gate"])
+    assert torch.equal(p16["experts_down"]["packed"], p8["experts_down"]["packed"])
+    for key in ("shared_gate_proj", "shared_up_proj", "shared_down_proj"):
+        t, w = p8[key], p16[key].float()
+        assert t["bits"] == 8 and t["group_size"] == 64
+        q = unpack_affine(t["packed"], w.shape[1], 8).float()
+        sc = t["scale"].float().repeat_interleave(64, dim=1)
+        bi = t["bias"].float().repeat_interleave(64, dim=1)
+        assert float((sc * q + bi - w).abs().max()) <= float((0.5 * sc + w.abs() * 2 ** -7).max())
+    with pytest.raises(ValueError):
+        synth.make_layer(s, device="cpu", seed=5, shared_bits=4)

@@ -64,3 +64,26 @@ def test_torch_cpu_port_matches_oracle(name, k1):
     ok = om.route_margin(it["choice"], kk) > 1e-5
     assert all(set(r) == set(o) for r, o, m in zip(idx.tolist(), it["idx"].tolist(), ok) if m)
     assert_close(y.float().numpy().astype(np.float64), it["y_exact"], f"torch_cpu {name} k={kk}")
+
+
+def test_torch_cpu_port_int8_shared_matches_oracle():
+    """The CPU port with the bake's int8 shared expert (c1mini fixture's shared weights
+    quantized): load_shared gives the bf16 dequant the oracle's shared_weight makes, and the
+    block stays within the gates of the oracle run on the same triplets."""
+    a = dict(np.load(GOLDEN / "c1mini.npz"))
+    H, E, k, I, Is, ng, tg, norm, sig = a["dims"].tolist()
+    cfg = MoEConfig(H, E, k, I, Is, norm_topk_prob=bool(norm))
+    op = oracle_params(a)
+    p = _torch_params(a)
+    for key in ("shared_gate_proj", "shared_up_proj", "shared_down_proj"):
+        w = oq.bf16_bits_to_f32(a[key]).astype(np.float32)
+        words, sb, bb, _ = oq.quantize_rtn(w, bits=8, group_size=64)
+        op[key] = {"packed": words, "scale": sb, "bias": bb, "group_size": 64, "bits": 8}
+        p[key] = {"packed": torch.from_numpy(words.view(np.int32)), "scale": _bf16(sb),
+                  "bias": _bf16(bb), "group_size": 64, "bits": 8}
+        got = torch_cpu.load_shared(p)[key].float().numpy().astype(np.float64)
+        assert np.array_equal(got, om.shared_weight(op[key]))
+    xf = oq.bf16_bits_to_f32(a["x"]).astype(np.float64)
+    _, it = om.moe_forward(xf, op, k=k, inter=I)
+    y = torch_cpu.moe_forward(_bf16(a["x"]), p, cfg)
+    assert_close(y.float().numpy().astype(np.float64), it["y_exact"], "torch_cpu c1mini int8 shared")
