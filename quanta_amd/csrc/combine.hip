@@ -805,7 +805,14 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + st - 1) / st, stream);
   }
   if (rc) return rc;
-  if (slot_major) {
+  // slot-major int4 SwiGLU experts: the top-k runs inside the routed gate_up launch
+  // (every wavefront ranks its token's logits: at most two tokens, where the launch is a few
+  // thousand wavefronts)
+  const bool route_in_gate_up = slot_major && N <= 2 && !mixed && gfmt == FMT_INT4 &&
+                                route_gate_up_fits(c.n_experts, c.top_k);
+  if (route_in_gate_up) {
+    // (the routed gate_up below ranks the logits itself)
+  } else if (slot_major) {
     // 3-4. top-k with the slot-major tile map
     rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,
                      c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx, wv, sg, stream,
@@ -906,12 +913,27 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       const hipError_t err = hipStreamWaitEvent(stream, aux->xready, 0);
       if (err != hipSuccess) return fail(std::string("forward: x16 wait: ") + hipGetErrorString(err));
     }
-    rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
+    if (route_in_gate_up) {
+      a.slot_of = nullptr; a.slot_div = 1; a.n_slots = 0; a.offsets = nullptr; a.tile_off = nullptr;
+      rc = launch_route_gate_up(a, n, logits, ld, wts->router_bias, c.n_experts, c.top_k, c.scoring,
+                                c.n_group, c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx,
+                                wv, sg, tile_map, tiles_small, sorted, inv, stream);
+    } else {
+      rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
+    }
     if (rc) return rc;
     if (hybrid && aux) {   // h complete (cold rows from the auxiliary stream) before its fp16 copy
       rc = link(aux->cold, aux->s, stream, "cold gate_up");
       if (rc) return rc;
     }
+  }
+  // 6-7. slot-major decode with a shared expert and one int4 down stack: routed down, shared
+  // down and combine in one launch per 16 output features (the down output stays on chip)
+  if (slot_major && fuse_dn && !mixed && dfmt == FMT_INT4 &&
+      down_combine_fits(n, c.top_k, c.hidden, c.inter, c.shared_inter)) {
+    return launch_down_combine(h, idx, wv, has_sg ? sg : nullptr, n, c.top_k, c.hidden, c.inter,
+                               wts->dn_codes, wts->dn_sb, sh_h, c.shared_inter, sh_dn_w,
+                               sh8 ? wts->sh_dn_sb : nullptr, sfmt, resid, y, stream);
   }
   // 6. routed down -> d (sorted order)
   {

@@ -29,9 +29,25 @@
 #include <type_traits>
 
 #include "qmoe_internal.h"
+#include "route_common.h"
 #include "../../include/quanta_moe.h"
 
 namespace qmoe {
+
+// Routing done inside the routed gate_up launch (slot-major batches): the logits, the top-k
+// parameters and where the routing results go for the launches after it.
+struct SlotRoute {
+  const float* logits;
+  int ld;
+  TopkParams P;
+  int32_t* idx;
+  float* w;
+  float* sg;
+  int4* tile_map;
+  int max_tiles;
+  int32_t* sorted;
+  int32_t* inv;
+};
 
 __device__ __forceinline__ int find_segment(const int32_t* __restrict__ tile_off, int E, int mt) {
   int lo = 0, hi = E - 1;
@@ -127,9 +143,18 @@ struct SmallCfg {
 // Body of one workgroup: job block `bx` of m-tile `by` (MT > 1, dense bf16 products only:
 // m-tiles by*MT .. by*MT+MT-1, every weight fragment feeding MT MFMAs), chunk sums in `red`
 // (LDS).
-template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1, bool NORM = false>
+// RVPL > 0 (slot-major routing in the launch, int4 SwiGLU): m-tile `by` is slot m = t*k + s,
+// one row; every wavefront ranks token t's logits (topk_token with RVPL experts per lane, the
+// top-k kernel's arithmetic) and takes lane s's expert; workgroups with bx == 0 store the slot's
+// expert, weight and tile (and slot 0 the token's shared-expert gate) for the later launches.
+// DEEP > 0 (with RVPL, one chunk per wavefront of exactly DEEP superblocks): the wavefront
+// stages its K range of the token row in its own LDS range (xlds, DEEP * 256 bytes) and issues
+// every weight load of its chunk at once, then multiplies superblock by superblock.
+template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1, bool NORM = false, int RVPL = 0,
+          int DEEP = 0>
 __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx, int by,
-                                           f32x4_t* red) {
+                                           f32x4_t* red, const SlotRoute* route = nullptr,
+                                           u32x4* xlds = nullptr) {
   using C = SmallCfg<FMT, EPI, W, CPW, JPW, MT>;
   static_assert(MT == 1 || fmt_dense(FMT), "several m-tiles per wavefront: dense weights only");
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
@@ -141,7 +166,34 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
   // wave index as a scalar, so per-wavefront quantities (job, k-range) stay in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   int e, mt0[MT], mtc[MT];
-  if (MT == 1) {
+  int route_tok = -1;
+  if constexpr (RVPL > 0) {
+    static_assert(MT == 1, "slot-major routing: one m-tile per wavefront");
+    const SlotRoute& R = *route;
+    const int m = by, t = m / R.P.k, s = m - t * R.P.k;
+    const float* lrow = R.logits + static_cast<int64_t>(t) * R.ld;
+    int id;
+    float wsel;
+    topk_token<RVPL>(lrow, R.P, lane, id, wsel);
+    e = __builtin_amdgcn_readlane(id, s);
+    mt0[0] = m;
+    mtc[0] = 1;
+    route_tok = t;
+    if (bx == 0 && wave == 0) {
+      if (lane == s) {
+        R.idx[m] = id;
+        R.w[m] = wsel;
+        R.tile_map[m] = make_int4(id, m, 1, 0);
+        R.sorted[m] = m;
+        R.inv[m] = m;
+      }
+      if (s == 0 && lane == 0 && R.P.has_sg) R.sg[t] = 1.0f / (1.0f + expf(-lrow[R.P.E]));
+      if (m == 0) {
+        const int mc = gridDim.y;
+        for (int i = mc + lane; i < R.max_tiles; i += 64) R.tile_map[i] = make_int4(-1, 0, 0, 0);
+      }
+    }
+  } else if (MT == 1) {
     if (!resolve_mtile(a, by, kSmallMTile, e, mt0[0], mtc[0])) return;
     // (one stack of a projection whose experts have different widths: the others' m-tiles exit;
     // every wavefront of the workgroup resolves the same m-tile)
@@ -174,7 +226,8 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
 #pragma unroll
   for (int u = 0; u < MT; ++u) {
     int64_t arow = -1;
-    if (mrow < mtc[u]) arow = act_row(a, mt0[u] + mrow);
+    if (RVPL > 0) arow = (mrow == 0) ? route_tok : -1;
+    else if (mrow < mtc[u]) arow = act_row(a, mt0[u] + mrow);
     const bool row_ok = arow >= 0;
     xrows[u] = act + (row_ok ? arow : 0) * static_cast<int64_t>(a.K);
     rows_okm[u] = static_cast<uint32_t>(__ballot(row_ok)) & 0xFFFFu;   // lanes 0-15
@@ -297,6 +350,50 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
           }
         }
       };
+      if constexpr (DEEP > 0) {
+        static_assert(RVPL > 0 && CPW == 1, "deep prefetch: slot-major routed launches");
+        // the chunk's activations (one token row, the same for every lane), first, so the
+        // weight loads behind them stay in flight when the compiler waits for them
+        constexpr int XV = DEEP * 16 / 64;
+        const u32x4* xg = reinterpret_cast<const u32x4*>(a.act + static_cast<int64_t>(route_tok) * a.K) +
+                          p0 * 16;
+        u32x4 xv[XV];
+#pragma unroll
+        for (int i = 0; i < XV; ++i) xv[i] = xg[lane + 64 * i];
+        u32x4 qd[DEEP][NT];
+        uint2 sd[DEEP][NT];
+#pragma unroll
+        for (int pp = 0; pp < DEEP; ++pp)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            qd[pp][t] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(cb[t] + static_cast<int64_t>(p0 + pp) * SBB + lane_c));
+            const u32x2 v = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x2*>(sbb[t] + static_cast<int64_t>(p0 + pp) * 128 + lane_s));
+            sd[pp][t] = uint2{v.x, v.y};
+          }
+        // (keeps the loads issued together: the scheduler would otherwise sink each one down to
+        // its superblock)
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4* xl = xlds + wave * (DEEP * 16);
+#pragma unroll
+        for (int i = 0; i < XV; ++i) xl[lane + 64 * i] = xv[i];
+        const u32x4* xr = xl + 2 * lg;
+#pragma unroll
+        for (int pp = 0; pp < DEEP; ++pp) {
+          SmallStage<NT, FMT> sg;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            sg.q[t] = qd[pp][t];
+            sg.sb[t] = sd[pp][t];
+          }
+          sg.x[0] = xr[pp * 16 + 0];
+          sg.x[1] = xr[pp * 16 + 1];
+          sg.x[2] = xr[pp * 16 + 8];
+          sg.x[3] = xr[pp * 16 + 9];
+          compute(sg);
+        }
+      } else {
       // Steady state: two superblocks per iteration with every load unconditional, so the
       // compiler waits only for the stage about to be computed; then a one- or two-superblock
       // tail (p1 - p0 >= 1).
@@ -329,6 +426,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
           compute(st[0]);
           chunk_end(p + 1);
         }
+      }
       }
     } else {  // dense: bf16 weights, or int8 codes dequantized to bf16 in registers
       const int nks = a.K / 32;
@@ -553,6 +651,17 @@ __attribute__((amdgpu_waves_per_eu(SmallCfg<FMT, EPI, W, CPW, JPW>::WPE)))
 qmm_small_kernel(QmmArgs a, int n_jobs) {
   __shared__ f32x4_t red[SmallCfg<FMT, EPI, W, CPW, JPW, MT>::RED];
   small_body<FMT, EPI, W, CPW, JPW, MT>(a, n_jobs, blockIdx.x, blockIdx.y, red);
+}
+
+// The routed gate_up of a slot-major batch with its routing (grid.y = N*k slots).
+template <int W, int JPW, int VPL, int DEEP>
+__global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
+__attribute__((amdgpu_waves_per_eu(SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW>::WPE)))
+qmm_route_gate_up_kernel(QmmArgs a, int n_jobs, SlotRoute route) {
+  __shared__ f32x4_t red[SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1>::RED];
+  __shared__ u32x4 xlds[DEEP > 0 ? (W > 4 ? W : 4) * DEEP * 16 : 1];
+  small_body<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1, false, VPL, DEEP>(a, n_jobs, blockIdx.x, blockIdx.y,
+                                                                    red, &route, xlds);
 }
 
 // Two dense products over the same activation rows in one launch (the router logits, tiled
@@ -1315,6 +1424,53 @@ static int launch_wide(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   b.mtiles = static_cast<int>(mtiles);
   qmm_wide_kernel<EPI><<<dim3(static_cast<unsigned>(mpad * nbk)), kWdThreads, kWdLdsBytes, stream>>>(b);
   return 0;
+}
+
+// Slot-major routed gate_up with its routing (qmm_route_gate_up_kernel): int4 weights, SwiGLU,
+// the decode kernel's chunking (W = CH wavefronts per job, one chunk each, one tile pair each).
+template <int W, int VPL>
+static void launch_route_k(const QmmArgs& a, int64_t mc, const SlotRoute& R, hipStream_t stream) {
+  constexpr int WAVES = W > 4 ? W : 4;
+  const int n_jobs = a.n_rows / 32;
+  const int jobs_per_wg = WAVES / W;
+  dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mc));
+  // every weight load of a wavefront's chunk in flight at once when the chunk is 8 superblocks
+  if (a.K / 128 == 8 * W)
+    qmm_route_gate_up_kernel<W, 1, VPL, 8><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
+  else
+    qmm_route_gate_up_kernel<W, 1, VPL, 0><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
+}
+template <int W>
+static void launch_route_w(const QmmArgs& a, int64_t mc, const SlotRoute& R, int vpl, hipStream_t stream) {
+  switch (vpl) {
+    case 1: launch_route_k<W, 1>(a, mc, R, stream); break;
+    case 2: launch_route_k<W, 2>(a, mc, R, stream); break;
+    case 4: launch_route_k<W, 4>(a, mc, R, stream); break;
+    default: launch_route_k<W, 8>(a, mc, R, stream); break;
+  }
+}
+
+bool route_gate_up_fits(int E, int k) { return E <= 512 && k <= 64; }
+
+int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, const float* bias,
+                         int E, int k, int scoring, int n_group, int topk_group, int norm_topk,
+                         float scale, int has_sg, int32_t* idx, float* w, float* sg,
+                         int32_t* tile_map, int64_t max_tiles, int32_t* sorted, int32_t* inv,
+                         hipStream_t stream) {
+  const int64_t mc = static_cast<int64_t>(N) * k;
+  if (!route_gate_up_fits(E, k) || a.K % 128 || a.n_rows % 32 || mc <= 0 || mc > 65535 ||
+      max_tiles < mc || max_tiles > (int64_t(1) << 30) || a.slot_of || a.offsets)
+    return fail("qmm(route): outside the slot-major routed gate_up");
+  SlotRoute R{logits, ld, topk_params(bias, E, k, scoring, n_group, topk_group, norm_topk, scale, has_sg),
+              idx, w, sg, reinterpret_cast<int4*>(tile_map), static_cast<int>(max_tiles), sorted, inv,
+};
+  const int nsb = a.K / 128;
+  const int ch = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;   // the int4 chunk rule of launch_qmm
+  const int vpl = topk_vpl(E);
+  if (ch == 4) launch_route_w<4>(a, mc, R, vpl, stream);
+  else if (ch == 2) launch_route_w<2>(a, mc, R, vpl, stream);
+  else launch_route_w<1>(a, mc, R, vpl, stream);
+  return check_launch("qmm(route)");
 }
 
 template <int W, int FMT2>

@@ -384,6 +384,25 @@ int launch_awq_glu(const uint16_t* gu, const int32_t* offsets, int E, int64_t mc
 int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float eps, uint16_t* out,
                    hipStream_t stream);
 
+// Slot-major routed gate_up with the top-k done in the launch (qmm.hip): int4 weights, SwiGLU
+// epilogue, a.act the N token rows (no slot_of/offsets); writes idx/w/sg and the slot-major
+// tile map, sorted and inv exactly as launch_topk does with a tile map.
+bool route_gate_up_fits(int E, int k);
+int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, const float* bias,
+                         int E, int k, int scoring, int n_group, int topk_group, int norm_topk,
+                         float scale, int has_sg, int32_t* idx, float* w, float* sg,
+                         int32_t* tile_map, int64_t max_tiles, int32_t* sorted, int32_t* inv,
+                         hipStream_t stream);
+// Slot-major decode tail (fused.hip): routed int4 down, shared down (tiled bf16 or int8 as sfmt)
+// and the combine in one launch; h/idx/w in slot order. down_combine_fits: the shapes it takes
+// (I = 512 or 1024, a shared expert of <= 8 bf16 chunks, at most 24 units of work per
+// workgroup: one or two tokens).
+bool down_combine_fits(int N, int k, int H, int I, int Is);
+int launch_down_combine(const uint16_t* h, const int32_t* idx, const float* w, const float* sg,
+                        int N, int k, int H, int I, const void* codes, const uint16_t* sb,
+                        const uint16_t* sh_h, int Is, const void* wd, const uint16_t* wd_sb,
+                        int sfmt, const uint16_t* resid, uint16_t* y, hipStream_t stream);
+
 constexpr int kSmallMTile = 16;
 constexpr int kLargeMTile = 128;
 // Large-M (prefill) regime: experts routed more rows than this use 128-row tiles on the large

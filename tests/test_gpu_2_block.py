@@ -285,10 +285,11 @@ def test_batch_invariance_full_size(gpu, name, N):
 @pytest.mark.parametrize("name", ["c1", "c2", "c3"])
 def test_fused_shared_expert_matches_unfused(gpu, name):
     """Up to 64 tokens the shared expert runs inside the router and combine launches; above, as
-    its own launches. Up to a few tokens (3 at c3, 6 at c2, 11 at c1) the top-k also writes a
-    slot-major tile map in place of the permute. The summation order is the same on every path,
-    so the first N tokens of a 65-token call equal an N-token call bit for bit, on every
-    repeat."""
+    its own launches. Up to a few tokens (3 at c3, 5 at c2, 11 at c1) the batch is routed
+    slot-major in place of the permute; for one or two tokens the top-k runs inside the routed
+    gate_up launch, and the routed down, the shared down and the combine run as one launch per
+    16 output features (c2 N=1, c1 N<=2). The summation order is the same on every path, so the first N
+    tokens of a 65-token call equal an N-token call bit for bit, on every repeat."""
     cfg = synth.spec(name).cfg
     p = _layer(name, gpu)
     x = synth.make_inputs(name, 65, device=gpu, seed=65)
