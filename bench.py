@@ -23,9 +23,9 @@ cores, bounded sample).
 `roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
 profiles/hbm_traffic.json, written from two rocprofv3 counter passes over `--only kernel` runs:
 
-    rocprofv3 --pmc FETCH_SIZE --output-format csv -d F -o pmc -- python bench.py --only kernel
-    rocprofv3 --pmc WRITE_SIZE --output-format csv -d W -o pmc -- python bench.py --only kernel
-    python bench.py --write-traffic F W
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d F -o pmc -- python bench.py --only kernel --kernel-reps 8
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d W -o pmc -- python bench.py --only kernel --kernel-reps 8
+    python bench.py --write-traffic F W --kernel-reps 8
 
 Each counter is scaled by what it reads for the 2 GiB device copy of the same run (the copy's
 known read and write bytes divided by its counter values).
@@ -88,8 +88,11 @@ def kernel_key(workload, regime_small):
     return "qmm_small_kernel<0, 0," if regime_small else "qmm_wide_kernel<0>"
 
 
-def write_traffic(fetch_dir, write_dir, workload="c2-decode-N32", regime_small=True):
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant kernel, scaled by the copy."""
+def write_traffic(fetch_dir, write_dir, workload="c2-decode-N32", regime_small=True, reps=8):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant kernel, scaled by the copy.
+    Only the last `reps` dispatches of the kernel count: the timed kernel loop of an
+    `--only kernel --kernel-reps reps` run (the layer steps before it may launch the same kernel
+    over a different tile set: the hot experts alone in the hybrid prefill)."""
     import csv
     import glob
 
@@ -105,10 +108,11 @@ def write_traffic(fetch_dir, write_dir, workload="c2-decode-N32", regime_small=T
             if "copyBuffer" in r["Kernel_Name"]:
                 copy.append(v)
             elif kernel_key(workload, regime_small) in r["Kernel_Name"]:
-                kern.append(v)
+                kern.append((int(r["Dispatch_Id"]), v))
                 name = r["Kernel_Name"]
         if not kern or not copy:
             sys.exit(f"bench.py: {counter}: kernel or copy dispatches missing in {d}")
+        kern = [v for _, v in sorted(kern)[-reps:]]
         return sum(kern) / len(kern), max(copy), name, len(kern)
 
     fk, fcopy, name, n1 = read(fetch_dir, "FETCH_SIZE")
@@ -144,7 +148,8 @@ def main():
     if args.write_traffic:
         wl = ("c4-prefill-zipf" if args.zipf else
               f"{args.config}-decode" if args.batch <= 256 else f"{args.config}-prefill") + f"-N{args.batch}"
-        write_traffic(*args.write_traffic, workload=wl, regime_small=args.batch <= 256)
+        write_traffic(*args.write_traffic, workload=wl, regime_small=args.batch <= 256,
+                      reps=args.kernel_reps)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
