@@ -65,14 +65,16 @@ def _parts(x, p, cfg, nw, eps):
     return (x.float() + ym.float()).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("name,N", [("c1", 1), ("c1", 17), ("c1", 64), ("c2", 2), ("c2", 8), ("c2", 32),
+@pytest.mark.parametrize("name,N", [("c1", 1), ("c1", 2), ("c1", 17), ("c1", 64), ("c2", 1), ("c2", 2),
+                                    ("c2", 8), ("c2", 32),
                                     ("c2", 49), ("c2", 65), ("c2", 300), ("c3", 1), ("c3", 16),
                                     ("c0", 8)])
 def test_residual_equals_its_parts(gpu, name, N):
     """The fused call against qmoe_rmsnorm + qmoe_forward + a bf16 add: bit for bit, in every
     regime the token count selects (up to 64 tokens the norm runs inside the router launch, one
     or two m-tiles per wavefront; above, and with c0's fp32 router, as a launch of its own;
-    slot-major top-k, auxiliary-stream shared expert, hybrid prefill); and in place."""
+    slot-major top-k, the top-k inside the routed gate_up and the fused down/combine tail (c1
+    N=1-2, c2 N=1), auxiliary-stream shared expert, hybrid prefill); and in place."""
     cfg = synth.spec(name).cfg
     p = _layer(name, gpu)
     x = (synth.make_inputs(name, N, device=gpu, seed=N).float() * 4.0).to(torch.bfloat16)

@@ -35,11 +35,13 @@ def _pair(dev, spec, p, n_first, n_second, seed):
 
 
 def test_noalloc_decode_c2(gpu):
-    """c2 at 32 then 8 tokens (fused shared expert), then 2 tokens (slot-major routing)."""
+    """c2 at 32 then 8 tokens (fused shared expert), then 2 tokens (slot-major routing, the
+    top-k inside the routed gate_up), then 4 and 1 (the fused down/combine tail)."""
     spec = synth.spec("c2")
     p = synth.make_layer("c2", device=gpu, seed=21)
     _pair(gpu, spec, p, 32, 8, 1)
     _pair(gpu, spec, p, 128, 2, 2)   # shared expert on its own launches, then slot-major
+    _pair(gpu, spec, p, 4, 1, 3)
 
 
 def test_noalloc_hybrid_prefill(gpu):
