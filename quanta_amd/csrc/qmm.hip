@@ -1239,10 +1239,58 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
 }
 
 // ---------------------------------------------------------------- fp16 activation copy
-// One workgroup per row: absmax, then act16 = fp16(act * 2^(14 - e)) with 2^(e-1) <= absmax < 2^e,
-// so every value sits below 2^14 and all bf16 values within 2^28 of the row maximum convert
-// exactly. row_sinv = 2^(e - 14) undoes it on the product (a power of two: exact).
+// One wavefront per row, the row held in registers (RPL 16-byte pieces per lane): absmax by a
+// wavefront reduction, then act16 = fp16(act * 2^(14 - e)) with 2^(e-1) <= absmax < 2^e, so every
+// value sits below 2^14 and all bf16 values within 2^28 of the row maximum convert exactly.
+// row_sinv = 2^(e - 14) undoes it on the product (a power of two: exact). The maximum is exact in
+// any order, so the result does not depend on the launch shape.
+template <int RPL>
 __global__ void __launch_bounds__(256) act_to_f16_kernel(const uint16_t* __restrict__ act, int K,
+                                                         int64_t rows,
+                                                         uint16_t* __restrict__ act16,
+                                                         float* __restrict__ row_sinv) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;   // whole wavefront
+  const u32x4* src = reinterpret_cast<const u32x4*>(act + row * K);
+  const int n8 = K / 8;
+  u32x4 v[RPL];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = (c < n8) ? src[c] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m = fmaxf(m, fabsf(bf16lo_to_f32(v[i][j])));
+      m = fmaxf(m, fabsf(bf16hi_to_f32(v[i][j])));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  int ex = 0;
+  if (m > 0.f && m <= 3.4e38f) frexpf(m, &ex);   // m = f * 2^ex, f in [0.5, 1)
+  const int sh = (m > 0.f && m <= 3.4e38f) ? 14 - ex : 0;
+  if (lane == 0) row_sinv[row] = ldexpf(1.0f, -sh);
+  u32x4* dst = reinterpret_cast<u32x4*>(act16 + row * K);
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < n8) {
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f16x2_t h = {static_cast<_Float16>(ldexpf(bf16lo_to_f32(v[i][j]), sh)),
+                           static_cast<_Float16>(ldexpf(bf16hi_to_f32(v[i][j]), sh))};
+        o[j] = __builtin_bit_cast(uint32_t, h);
+      }
+      dst[c] = o;
+    }
+  }
+}
+
+// Rows longer than 8192: one workgroup per row, the row read twice (absmax, then convert).
+__global__ void __launch_bounds__(256) act_to_f16_wide_kernel(const uint16_t* __restrict__ act, int K,
                                                          uint16_t* __restrict__ act16,
                                                          float* __restrict__ row_sinv) {
   __shared__ float red[4];
@@ -1285,8 +1333,21 @@ int launch_act_to_f16(const uint16_t* act, int64_t rows, int K, uint16_t* act16,
                       hipStream_t stream) {
   if (rows <= 0) return 0;
   if (K % 8) return fail("act_to_f16: K % 8 == 0 required");
-  if (rows > 0x7fffffff) return fail("act_to_f16: too many rows");
-  act_to_f16_kernel<<<static_cast<unsigned>(rows), 256, 0, stream>>>(act, K, act16, row_sinv);
+  if (K > 8 * 64 * 16) {
+    if (rows > 0x7fffffff) return fail("act_to_f16: too many rows");
+    act_to_f16_wide_kernel<<<static_cast<unsigned>(rows), 256, 0, stream>>>(act, K, act16, row_sinv);
+    return check_launch("act_to_f16");
+  }
+  if (rows > (int64_t(1) << 32)) return fail("act_to_f16: too many rows");
+  const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
+  const int rpl = (K / 8 + 63) / 64;   // 16-byte pieces per lane
+#define QMOE_A16(R) act_to_f16_kernel<R><<<grid, 256, 0, stream>>>(act, K, rows, act16, row_sinv)
+  if (rpl <= 2) QMOE_A16(2);
+  else if (rpl <= 4) QMOE_A16(4);
+  else if (rpl <= 8) QMOE_A16(8);
+  else if (rpl <= 14) QMOE_A16(14);
+  else QMOE_A16(16);
+#undef QMOE_A16
   return check_launch("act_to_f16");
 }
 
