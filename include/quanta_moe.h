@@ -149,9 +149,9 @@ typedef struct {
                                      (row 0) and up (row 1) projections, else NULL */
   const uint16_t* awq_dn;         /* config awq: bf16 [E, I] scales of the down projection */
   const int8_t* gu_rexp;          /* int4 gate|up: per weight row [E, 2I] power-of-two exponent
-                                     (qmoe_row_exponents) for the prefill kernels' fp16 dequant,
-                                     or NULL (exponent 0: scales and biases must then lie in
-                                     fp16's normal range for full prefill precision) */
+                                     (qmoe_row_exponents) for the prefill kernels' fp16 dequant;
+                                     required when a call reaches the large regime (N > 256), may
+                                     be NULL for decode-only use */
   const int8_t* dn_rexp;          /* int4 down: per weight row [E, H], as gu_rexp */
 } qmoe_weights_t;
 
@@ -271,8 +271,8 @@ int qmoe_permute(const int32_t* idx, int64_t N, int k, int E, int m_tile, int32_
  * QMOE_REGIME_LARGE), with row(p) = slot_of[p] / slot_div (slot_of NULL: row(p) = p). With
  * offsets == NULL the call is one dense segment of dense_rows rows. W is tiled int3/int4/int6
  * (codes + sb), tiled int8 (codes + sb; small regime, K % 64 == 0) or tiled bf16 (codes),
- * [n_experts][n_rows][K]; row_exp (int4, nullable) holds the
- * per-row exponents of qmoe_row_exponents for the large regime's fp16 dequant. Epilogue QMOE_EPI_SWIGLU treats
+ * [n_experts][n_rows][K]; row_exp (int4; required in the large regime, else ignored) holds
+ * the per-row exponents of qmoe_row_exponents for the large regime's fp16 dequant. Epilogue QMOE_EPI_SWIGLU treats
  * rows [0, n_rows/2) as gate and [n_rows/2, n_rows) as up, with the gated activation `glu`
  * (QMOE_ACT_*; glu_alpha and glu_limit as act_alpha and act_limit of qmoe_config_t; other
  * epilogues ignore them).
@@ -344,9 +344,10 @@ int qmoe_tile_int6(const uint32_t* packed, const uint16_t* scale, const uint16_t
  * [.., in/group_size]): row_exp[r] = 14 - ex, 2^(ex-1) <= M_r < 2^ex, M_r the row's largest
  * dequantized magnitude max_g max(|b_g|, |(2^bits - 1) s_g + b_g|); 0 for an all-zero row; within
  * [-100, 100]. The prefill (large-regime) kernels dequantize int4 weights to fp16 as
- * fp16(2^row_exp (s q + b)) and undo the power of two on the fp32 result, so rows of any
- * magnitude keep fp16's full precision (scales far below fp16's normal range, 2^-14, would
- * otherwise lose bits or vanish). No counterpart in the reference (MLX dequantizes in bf16);
+ * fp16(2^(row_exp - 20) (s q + b)) (the code nibble enters the fp16 FMA as a subnormal, so the
+ * scale is taken times 2^24 or 2^20, which row_exp keeps below fp16's maximum) and undo the
+ * power of two on the fp32 result, so rows of any magnitude keep fp16's precision (scales far
+ * below fp16's normal range, 2^-14, would otherwise lose bits or vanish). No counterpart in the reference (MLX dequantizes in bf16);
  * computed once per stack with the tiling. */
 int qmoe_row_exponents(const uint16_t* scale, const uint16_t* bias, int64_t n_mats, int64_t rows,
                        int64_t in_features, int bits, int group_size, int8_t* row_exp,

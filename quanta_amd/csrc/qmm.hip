@@ -775,6 +775,33 @@ struct LgStageBf {
   u32x4 q[2][4];
 };
 
+// int4 -> fp16 dequant of the prefill kernels, one packed register (two weights) per VALU FMA.
+// A code nibble masked in place is an fp16 subnormal: at bits 0-3 of a half it reads q * 2^-24,
+// at bits 4-7 q * 2^-20, so fma(code, s * 2^(e+24) or s * 2^(e+20), b * 2^e) yields
+// fp16(2^e (s q + b)) with a single rounding (the product is exact inside the FMA). e = row_exp
+// - kDeqShift: row_exp puts the row's largest magnitude in [2^13, 2^14), which bounds
+// s * 2^row_exp below 2^15 / 15 (15 s = (15 s + b) - b), so the larger scale factor, s *
+// 2^(row_exp + 4), stays below 2^15.1 < 65504; the weights themselves lie below 2^-6 and keep
+// fp16's full precision down to 2^-8 of the row maximum, below that an absolute 2^-20 of it
+// (fp16 subnormals; the MFMAs take them exactly). Pairs 2 and 3 share one 8-bit shift.
+constexpr int kDeqShift = 20;
+struct DeqSb {
+  f16x2_t s_lo, s_hi, b;   // scale for nibbles at bits 0-3 / 4-7 of each half, bias
+};
+__device__ __forceinline__ DeqSb deq_sb(uint32_t sbw, int e) {
+  const float sv = bf16lo_to_f32(sbw), bv = bf16hi_to_f32(sbw);
+  const _Float16 lo = static_cast<_Float16>(ldexpf(sv, e + 24));
+  const _Float16 hi = static_cast<_Float16>(ldexpf(sv, e + 20));
+  const _Float16 b = static_cast<_Float16>(ldexpf(bv, e));
+  return DeqSb{f16x2_t{lo, lo}, f16x2_t{hi, hi}, f16x2_t{b, b}};
+}
+// nibble pair j (0..3) of code word w: weights k = j and j+4 of the word's two 16-bit halves
+__device__ __forceinline__ uint32_t deq_pair(uint32_t w, int j, const DeqSb& d) {
+  const uint32_t src = (j >= 2) ? (w >> 8) : w;
+  const f16x2_t q = __builtin_bit_cast(f16x2_t, src & ((j & 1) ? 0x00F000F0u : 0x000F000Fu));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, (j & 1) ? d.s_hi : d.s_lo, d.b));
+}
+
 template <int FMT, int EPI>
 __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   extern __shared__ u32x4 lds[];
@@ -820,7 +847,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const char* wcode[2];
   const char* wsb[2];
   const u32x4* wp[2];
-  int rex[2] = {0, 0};   // int4: the lane's weight row of each tile, its power-of-two exponent
+  int rex[2] = {0, 0};   // int4: the lane's weight row of each tile, its dequant exponent e
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int tl = (EPI == EPI_SWIGLU) ? (t == 0 ? 8 * cb + wave : a.n_rows / 32 + 8 * cb + wave)
@@ -830,7 +857,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
-      rex[t] = a.row_exp ? load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) : 0;
+      rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - kDeqShift;
     } else {
       wcode[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
@@ -868,12 +895,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // i issues the two MFMAs of m-block i, the read of m-block i's A fragment for step s+1 and
   // 1/MB of step s+1's weight dequant, and a scheduling barrier keeps that order, so LDS reads
   // have a full step to land and the dequant VALU work is spread between the MFMAs.
-  // fp16 bit insertion: nibble pair 0 (2) of a word OR'd into 1024.0 (0x6400, mantissa LSB 1)
-  // gives 1024 + q; pair 1 (3), masked in place at bits 4-7, into 64.0 (0x5400, mantissa LSB
-  // 1/16) gives 64 + q. Pairs 2 and 3 share one 8-bit shift. Subtracting 1024 or 64 is exact.
-  const uint32_t exp_lo = 0x64006400u, exp_hi = 0x54005400u;
-  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-  const f16x2_t k64 = {static_cast<_Float16>(64.0f), static_cast<_Float16>(64.0f)};
+  // (int4 dequant: deq_sb / deq_pair)
   auto compute = [&](int p, const LgStageBf& gb, auto mbc) __attribute__((always_inline)) {
     constexpr int MB = decltype(mbc)::value;
     constexpr int UPS = 8 / MB;                 // dequant units (nibble pairs) per slot
@@ -888,28 +910,17 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
         sbv[t] = reinterpret_cast<const uint2*>(lb + 2048 + t * 128)[lane & 15];
       }
     }
-    f16x2_t s2[2], b2[2];
-    // scale and bias of the row times 2^rex (exact), so the fp16 weights stay normal
+    DeqSb dsb[2];
+    // the group's scale and bias, scaled by 2^e (exact)
     auto sb_conv = [&](int grp) __attribute__((always_inline)) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint32_t sbw = grp ? sbv[t].y : sbv[t].x;
-        const _Float16 sv = static_cast<_Float16>(ldexpf(bf16lo_to_f32(sbw), rex[t]));
-        const _Float16 bv = static_cast<_Float16>(ldexpf(bf16hi_to_f32(sbw), rex[t]));
-        s2[t] = f16x2_t{sv, sv};
-        b2[t] = f16x2_t{bv, bv};
-      }
+      for (int t = 0; t < 2; ++t) dsb[t] = deq_sb(grp ? sbv[t].y : sbv[t].x, rex[t]);
     };
     // dequant unit u (0..7) of step s: tile u/4, nibble pair u%4 -> one packed fp16 register
     auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
       const int t = u >> 2, j = u & 3;
       if (FMT == FMT_INT4) {
-        uint32_t r;
-        const uint32_t src = (j >= 2) ? (q[t][s] >> 8) : q[t][s];
-        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(src),
-            "s"((j & 1) ? 0x00F000F0u : 0x000F000Fu), "v"((j & 1) ? exp_hi : exp_lo));
-        const f16x2_t qq = __builtin_bit_cast(f16x2_t, r) - ((j & 1) ? k64 : k1024);
-        bfo[t][j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qq, s2[t], b2[t]));
+        bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
       } else if (j == 0) {
         bfo[t] = gb.q[t][s];
       }
@@ -1081,7 +1092,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
   // this wavefront's four weight tiles (SwiGLU: gate tiles first, then their up tiles)
   const char* wcode[4];
   const char* wsb[4];
-  int rex[4];   // the lane's weight row of each tile: its power-of-two exponent (row_exp)
+  int rex[4];   // the lane's weight row of each tile: its dequant exponent e (deq_sb)
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int tl = (EPI == EPI_SWIGLU)
@@ -1090,7 +1101,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     const int64_t tb = (ebase + tl) * nsb;
     wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
     wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
-    rex[t] = a.row_exp ? load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) : 0;
+    rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - kDeqShift;
   }
   // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
   const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
@@ -1117,9 +1128,6 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t exp_lo = 0x64006400u, exp_hi = 0x54005400u;
-  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-  const f16x2_t k64 = {static_cast<_Float16>(64.0f), static_cast<_Float16>(64.0f)};
   // One superblock: four 32-k steps. Step s is MB slots; slot i issues the four MFMAs of
   // m-block i, the LDS read of the A fragment two slots ahead, and 16/MB of step s+1's weight
   // dequant units (tile u/4, nibble pair u%4), in that order (scheduling barriers).
@@ -1136,26 +1144,15 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
       sbv[t] = reinterpret_cast<const uint2*>(lb + 4096 + t * 128)[lane & 15];
     }
-    f16x2_t s2[4], b2[4];
-    // scale and bias of the row times 2^rex (exact), so the fp16 weights stay normal
+    DeqSb dsb[4];
+    // the group's scale and bias, scaled by 2^e (exact)
     auto sb_conv = [&](int grp) __attribute__((always_inline)) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint32_t sbw = grp ? sbv[t].y : sbv[t].x;
-        const _Float16 sv = static_cast<_Float16>(ldexpf(bf16lo_to_f32(sbw), rex[t]));
-        const _Float16 bv = static_cast<_Float16>(ldexpf(bf16hi_to_f32(sbw), rex[t]));
-        s2[t] = f16x2_t{sv, sv};
-        b2[t] = f16x2_t{bv, bv};
-      }
+      for (int t = 0; t < 4; ++t) dsb[t] = deq_sb(grp ? sbv[t].y : sbv[t].x, rex[t]);
     };
     auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
       const int t = u >> 2, j = u & 3;
-      uint32_t r;
-      const uint32_t src = (j >= 2) ? (q[t][s] >> 8) : q[t][s];
-      asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(src),
-          "s"((j & 1) ? 0x00F000F0u : 0x000F000Fu), "v"((j & 1) ? exp_hi : exp_lo));
-      const f16x2_t qq = __builtin_bit_cast(f16x2_t, r) - ((j & 1) ? k64 : k1024);
-      bfo[t][j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qq, s2[t], b2[t]));
+      bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
     };
     u32x4 bf[2][4];
     u32x4 A[NI];
@@ -1664,6 +1661,8 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
     if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))
       return fail("qmm(large): int4 weights need the fp16 activation copy");
+    if (fmt == FMT_INT4 && !a.row_exp)
+      return fail("qmm(large): int4 weights need their row exponents (qmoe_row_exponents)");
     int rc;
 #define QMOE_LARGE(F, P) rc = launch_large<F, P>(a, mtile_bound, stream)
     // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves) take the wide kernel

@@ -158,40 +158,6 @@ __device__ __forceinline__ f32x16_t mfma32_bf16(u32x4 a, u32x4 b, f32x16_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Dequantize one stored word to 8 fp16 weights (natural k order): (1024 + c) built by bit
-// insertion is exact in fp16, minus 1024 gives c exactly, and one packed fp16 FMA gives
-// fp16(s*c + b) with a single round-to-nearest-even. s2/b2 hold the group's scale and bias
-// converted to fp16 (exact for bf16 values in fp16's normal range).
-__device__ __forceinline__ u32x4 dequant_word_f16(uint32_t w, f16x2_t s2, f16x2_t b2) {
-  const uint32_t m = 0x000F000Fu, o = 0x64006400u;
-  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-  u32x4 out;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t r = ((w >> (4 * j)) & m) | o;
-    const f16x2_t q = __builtin_bit_cast(f16x2_t, r) - k1024;
-    out[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
-  }
-  return out;
-}
-
-// Same result as dequant_word_f16; the nibble pair extraction is one v_and_or_b32 per pair (mask
-// and exponent bits as register operands, which gfx9-family VOP3 encodings require) instead of
-// the separate and + or the compiler otherwise emits for two literal constants.
-__device__ __forceinline__ u32x4 dequant_word_f16_ao(uint32_t w, f16x2_t s2, f16x2_t b2,
-                                                     uint32_t exp_bits) {
-  const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-  u32x4 out;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w >> (4 * j)), "s"(0x000F000Fu), "v"(exp_bits));
-    const f16x2_t q = __builtin_bit_cast(f16x2_t, r) - k1024;
-    out[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
-  }
-  return out;
-}
-
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 // The gated activation on (bf16-valued) gate/up values, fp32 (QMOE_ACT_*: silu(g)*u; its clamped
 // form, src/quanta/dsv4/moe.py:74-77; SwiGLU-OAI, src/quanta/minimax/model_m3.py:112-128).

@@ -259,7 +259,7 @@ def grouped_qmm(act: torch.Tensor, *, K: int, n_rows: int, weight_format: int,
     """Grouped matmul over expert segments (see qmoe_grouped_qmm). Returns out [out_rows, cols]
     (bf16, or fp32 for EPI_F32); cols = n_rows/2 for SwiGLU else n_rows. `glu`, `glu_alpha`,
     `glu_limit`: the SwiGLU epilogue's gated activation (L.ACT_*). `row_exp`: int4 stacks' per-row
-    exponents (row_exponents) for the large regime's fp16 dequant."""
+    exponents (row_exponents) for the large regime's fp16 dequant (required there)."""
     _need(act, torch.bfloat16, "act")
     if act.dim() != 2 or act.shape[1] != K:
         raise ValueError("grouped_qmm: act must be [rows, K]")
