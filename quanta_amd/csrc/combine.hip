@@ -544,6 +544,8 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
   if (regime != QMOE_REGIME_SMALL && regime != QMOE_REGIME_LARGE)
     return fail("qmoe_grouped_qmm: regime must be small (1) or large (2)");
   if (slot_of && slot_div <= 0) return fail("qmoe_grouped_qmm: slot_div must be positive");
+  if (regime == QMOE_REGIME_LARGE && weight_format == QMOE_FMT_INT4_G64 && !row_exp)
+    return fail("qmoe_grouped_qmm: int4 weights in the large regime need row_exp (qmoe_row_exponents)");
   const int out_cols = (epilogue == QMOE_EPI_SWIGLU) ? n_rows / 2 : n_rows;
   if (ld_out < out_cols) return fail("qmoe_grouped_qmm: ld_out too small");
   QmmArgs a{};
@@ -638,6 +640,11 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
   if (c.awq && (!wts->awq_gu || !wts->awq_dn)) return fail("qmoe_forward: awq needs awq_gu and awq_dn");
+  if (pick_regime(c, N) == QMOE_REGIME_LARGE &&
+      ((kernel_fmt(c.expert_format) == FMT_INT4 && !wts->gu_rexp) ||
+       (kernel_fmt(c.down_format) == FMT_INT4 && !wts->dn_rexp)))
+    return fail("qmoe_forward: int4 experts in the large regime (N > 256) need gu_rexp and dn_rexp "
+                "(qmoe_row_exponents)");
 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* base = static_cast<char*>(ws);

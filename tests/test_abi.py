@@ -69,6 +69,9 @@ _DUMMY = ctypes.c_void_p(16)   # never dereferenced: each call fails validation 
     (lambda lib: lib.qmoe_grouped_qmm(_DUMMY, 1, None, 1, 1, None, None, None, 1, 1, 128, 32, 1,
                                       _DUMMY, None, None, 0, 5, 1.0, 7.0, _DUMMY, 16, 1, None, 0,
                                       None), "unknown act"),
+    (lambda lib: lib.qmoe_grouped_qmm(_DUMMY, 1, None, 1, 1, None, None, None, 1, 1, 128, 256, 0,
+                                      _DUMMY, _DUMMY, None, 1, 0, 1.0, 0.0, _DUMMY, 256, 2, None,
+                                      0, None), "need row_exp"),
     (lambda lib: lib.qmoe_row_exponents(None, None, 1, 16, 128, 4, 64, None, None), "null pointer"),
     (lambda lib: lib.qmoe_forward_noalloc(None, None, None, 1, None, None), "null pointer"),
     (lambda lib: lib.qmoe_row_exponents(_DUMMY, _DUMMY, 1, 16, 100, 4, 64, _DUMMY, None),
@@ -148,6 +151,21 @@ def test_forward_rejects_mixed_bf16_and_unknown_down_format():
             continue
         rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
         assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()
+
+
+def test_forward_large_int4_needs_row_exponents():
+    """The prefill kernels' fp16 dequant scales each weight row by its exponent (row_exponents):
+    an int4 call that reaches the large regime without them is rejected before any launch."""
+    lib = L.load()
+    cfg = L.QmoeConfig(hidden=512, n_experts=16, top_k=2, inter=256, shared_inter=0, scoring=0,
+                       norm_topk=1, n_group=1, topk_group=1, routed_scale=1.0, expert_format=0,
+                       router_format=1, router_rows=0, shared_gated=0, regime=L.REGIME_LARGE)
+    w = L.QmoeWeights()
+    dummy = ctypes.c_void_p(16)
+    for f in ("router_w", "gu_codes", "gu_sb", "dn_codes", "dn_sb"):
+        setattr(w, f, dummy.value)
+    rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
+    assert rc == L.QMOE_EINVAL and "gu_rexp and dn_rexp" in _last_error(), _last_error()
 
 
 def test_forward_rejects_bad_shared_format():
