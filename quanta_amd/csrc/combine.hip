@@ -806,10 +806,14 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       a.act = x_in; a.norm_w = norm_w; a.norm_eps = norm_eps; a.norm_out = xn;
       sgu.act = x_in; sgu.norm_w = norm_w; sgu.norm_eps = norm_eps;
     }
+    // (large regime: 64-token m-tiles, so the few row blocks of the router still give twice
+    // as many workgroups)
+    const int rt = decode ? st : 64;
+    if (!decode) a.dense_mtile = rt;
     if (fuse_gu)
       rc = launch_qmm_pair_bf16(a, sgu, stream, sfmt);
     else
-      rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + st - 1) / st, stream);
+      rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + rt - 1) / rt, stream);
   }
   if (rc) return rc;
   // slot-major int4 SwiGLU experts: the top-k runs inside the routed gate_up launch

@@ -821,7 +821,8 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const int gk = kx / (G * nbk), rk = kx - gk * (G * nbk);
   const int mt = (gk * 8 + xcd) * G + rk / nbk;
   const int cb = rk % nbk;
-  if (mt >= a.mtiles || !resolve_mtile(a, mt, kLargeMTile, e, m0, m_cnt)) return;
+  const int mrows = (a.dense_mtile > 0 && !a.offsets && !a.tile_map) ? a.dense_mtile : kLargeMTile;
+  if (mt >= a.mtiles || !resolve_mtile(a, mt, mrows, e, m0, m_cnt)) return;
   const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
   const int nsb = a.K / 128;
   const int mb_act = __builtin_amdgcn_readfirstlane((m_cnt + 15) >> 4);   // 1..8
@@ -1658,6 +1659,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       return fail("qmm(large): int8 weights run in the small regime only (expand them to bf16 "
                   "for the large kernels)");
     if (a.K % 128) return fail("qmm(large): K % 128 == 0 required");
+    if (a.dense_mtile && (a.offsets || a.tile_map || a.dense_mtile % 16 || a.dense_mtile < 16 ||
+                          a.dense_mtile > kLargeMTile || fmt != FMT_BF16))
+      return fail("qmm(large): dense_mtile is a multiple of 16 up to 128, for one dense bf16 segment");
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
     if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))
       return fail("qmm(large): int4 weights need the fp16 activation copy");

@@ -229,6 +229,9 @@ struct QmmArgs {
                               // summed in the canonical order of rmsnorm_row (norm.hip)
   float norm_eps;
   uint16_t* norm_out;         // nullable: the normalised rows, written by job 0's wavefronts
+  int dense_mtile;            // large regime, one dense segment: rows per m-tile (16..128, a
+                              // multiple of 16; 0 = 128), so a short product still spreads
+                              // over enough workgroups
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3, FMT_INT8 = 4 };
