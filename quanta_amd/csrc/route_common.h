@@ -337,6 +337,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* 
   return warp_sums[16 + wid] + incl - v;
 }
 
+constexpr int kPermBatch = 8;   // expert ids loaded per thread before they are used
+
 // Optional split tile maps (hybrid regime): experts with more than `split_rows` rows get
 // m-tiles of `m_tile_big` rows in tile_map_big; the others keep m_tile-row tiles in tile_map.
 // Must be called by all 1024 threads of the workgroup.
@@ -361,13 +363,24 @@ __device__ __forceinline__ void permute_body(
   for (int i = tid; i < nbits; i += nthr) bits[i] = 0u;
   __syncthreads();
 
-  for (int m = tid; m < mc; m += nthr) {
-    const int e = idx[m];
-    if (e < 0 || e >= E) continue;
-    atomicAdd(&hist[e], 1);
-    if (e >= e0 && e < e1) {
-      const int t = m / k;
-      atomicOr(&bits[(e - e0) * words_per_expert + (t >> 5)], 1u << (t & 31));
+  // (the expert ids are read kPermBatch per thread before any is used, so a long list costs
+  // one global-load latency per batch rather than one per entry)
+  for (int mb = tid; mb < mc; mb += kPermBatch * nthr) {
+    int ev[kPermBatch];
+#pragma unroll
+    for (int j = 0; j < kPermBatch; ++j) {
+      const int m = mb + j * nthr;
+      ev[j] = (m < mc) ? idx[m] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kPermBatch; ++j) {
+      const int e = ev[j];
+      if (e < 0 || e >= E) continue;
+      atomicAdd(&hist[e], 1);
+      if (e >= e0 && e < e1) {
+        const int t = (mb + j * nthr) / k;
+        atomicOr(&bits[(e - e0) * words_per_expert + (t >> 5)], 1u << (t & 31));
+      }
     }
   }
   __syncthreads();
@@ -470,19 +483,30 @@ __device__ __forceinline__ void permute_body(
     for (int p = offs[e0] + tid; p < offs[e1]; p += nthr) sorted_slot[p] = -1;
   __syncthreads();
 
-  for (int m = tid; m < mc; m += nthr) {
-    const int e = idx[m];
-    if (e < 0 || e >= E) {
-      if (is_first) inv[m] = -1;
-      continue;
+  for (int mb = tid; mb < mc; mb += kPermBatch * nthr) {
+    int ev[kPermBatch];
+#pragma unroll
+    for (int j = 0; j < kPermBatch; ++j) {
+      const int m = mb + j * nthr;
+      ev[j] = (m < mc) ? idx[m] : E;
     }
-    if (e < e0 || e >= e1) continue;
-    const int t = m / k;
-    const int wi = (e - e0) * words_per_expert + (t >> 5);
-    const uint32_t below = bits[wi] & ((1u << (t & 31)) - 1u);
-    const int pos = offs[e] + static_cast<int>(pref[wi]) + __popc(below);
-    sorted_slot[pos] = m;
-    inv[m] = pos;
+#pragma unroll
+    for (int j = 0; j < kPermBatch; ++j) {
+      const int m = mb + j * nthr;
+      if (m >= mc) break;
+      const int e = ev[j];
+      if (e < 0 || e >= E) {
+        if (is_first) inv[m] = -1;
+        continue;
+      }
+      if (e < e0 || e >= e1) continue;
+      const int t = m / k;
+      const int wi = (e - e0) * words_per_expert + (t >> 5);
+      const uint32_t below = bits[wi] & ((1u << (t & 31)) - 1u);
+      const int pos = offs[e] + static_cast<int>(pref[wi]) + __popc(below);
+      sorted_slot[pos] = m;
+      inv[m] = pos;
+    }
   }
 }
 
