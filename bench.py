@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time decode steps replayed from a captured HIP graph (one step per "
+                         "layer copy per replay), beside the stream launches")
     ap.add_argument("--write-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 counter runs into profiles/hbm_traffic.json "
                          "(the workload of --batch / --zipf: its dominant gate_up kernel)")
@@ -200,6 +203,7 @@ def main():
     layers, native = resident_layers(args.config, args.layers)
     native_cpu = None if args.no_cpu_baseline else native
     warm_runs = []
+    graph_runs = []
 
     def warm(step, warmup):
         """At least `warmup` steps and at least --warmup-ms of steps, then a synchronize. From
@@ -248,6 +252,33 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
+        if args.graph and N <= 256:
+            # the same steps captured once (one per layer copy, kernel launches only: the block
+            # records no memset or copy) and replayed: the step time without host launch cost
+            n_cap = len(preps)
+            s_cap = torch.cuda.Stream()
+            s_cap.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s_cap):
+                for i in range(n_cap):
+                    step(i)
+            torch.cuda.current_stream().wait_stream(s_cap)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(n_cap):
+                    step(i)
+            warm(lambda i: g.replay(), max(1, warmup // n_cap))
+            reps = max(1, steps // n_cap)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            gms = e0.elapsed_time(e1) / (reps * n_cap)
+            graph_runs.append(dict(workload=f"{src}-N{N}" + ("-residual" if residual else ""),
+                                   ms_per_step_stream=round(ms, 5), ms_per_step_graph=round(gms, 5)))
+            log(f"graph {graph_runs[-1]}")
+            del g
         # distinct experts per batch (U) for the algorithmic byte count
         us = []
         for x in xs:
@@ -514,6 +545,8 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
     }
+    if graph_runs:
+        line["graph"] = graph_runs
     print(json.dumps(line), flush=True)
 
 
