@@ -174,7 +174,11 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
     const float* lrow = R.logits + static_cast<int64_t>(t) * R.ld;
     int id;
     float wsel;
-    topk_token<RVPL>(lrow, R.P, lane, id, wsel);
+    // (only the storing wavefront needs the weights; the others rank up to their own slot)
+    if (bx == 0 && wave == 0)
+      topk_token<RVPL>(lrow, R.P, lane, id, wsel);
+    else
+      topk_token<RVPL, true>(lrow, R.P, lane, id, wsel, s + 1);
     e = __builtin_amdgcn_readlane(id, s);
     mt0[0] = m;
     mtc[0] = 1;

@@ -100,9 +100,12 @@ struct TopkParams {
 // lowest id of that value (a lane's candidates are taken in id order, and only a strictly
 // larger value replaces the current best). Lane r < k returns the r-th expert and its final
 // weight.
-template <int VPL>
+// IDS_ONLY: lane r < rounds returns the r-th expert and out_w is undefined; the selection is the
+// same, and softmax routing without a bias (which selects by logit) then skips the
+// probabilities altogether.
+template <int VPL, bool IDS_ONLY = false>
 __device__ __forceinline__ void topk_token(const float* __restrict__ row, const TopkParams& P,
-                                           int lane, int& out_id, float& out_w) {
+                                           int lane, int& out_id, float& out_w, int rounds = 0) {
   const float NEG_INF = -INFINITY;
   const int E = P.E;
   const int e_base = lane * VPL;
@@ -114,7 +117,11 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
     const float v = row[min(e_base + i, E - 1)];
     lg[i] = (e_base + i < E) ? v : NEG_INF;
   }
-  if (P.scoring == QMOE_SCORE_SOFTMAX) {
+  const bool by_logit = (P.scoring == QMOE_SCORE_SOFTMAX);
+  if (IDS_ONLY && by_logit && !P.bias) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) sc[i] = 0.f;
+  } else if (P.scoring == QMOE_SCORE_SOFTMAX) {
     float m = NEG_INF;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) m = fmaxf(m, lg[i]);
@@ -141,7 +148,6 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
   // Without a bias, softmax selection by probability equals selection by logit (monotone); the
   // logit avoids ties manufactured by rounding exp(). Sigmoid and sqrt-softplus select on the
   // score, as the reference does.
-  const bool by_logit = (P.scoring == QMOE_SCORE_SOFTMAX);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int e = e_base + i;
@@ -234,7 +240,8 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
 
   int my_id = 0;
   float my_w = 0.f;
-  for (int r = 0; r < P.k; ++r) {
+  const int n_rounds = (IDS_ONLY && rounds > 0) ? min(rounds, P.k) : P.k;
+  for (int r = 0; r < n_rounds; ++r) {
     const uint32_t m = wave_max_u32(hk);
     unsigned long long win = __ballot((hi >= 0) & (hk == m));
     win = win ? win : __ballot(hi >= 0);   // the fallback is unreachable while k <= E
@@ -246,6 +253,11 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
     head();
     my_id = (lane == r) ? id : my_id;
     my_w = (lane == r) ? s_win : my_w;
+  }
+  if (IDS_ONLY) {
+    out_id = my_id;
+    out_w = 0.f;
+    return;
   }
   const float tot = wave_sum_f32(lane < P.k ? my_w : 0.f);
   // QMOE_NORM_ALWAYS, or QMOE_NORM_MULTI with more than one expert (a MoEGate keeps a single
