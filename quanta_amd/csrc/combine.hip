@@ -295,6 +295,9 @@ constexpr int64_t kFuseSharedMaxTokens = 64;
 // permute once per call; the permute launch costs about as much as streaming this many bytes.
 constexpr double kPermuteLaunchBytes = 24e6;
 constexpr int64_t kSlotMajorCapTokens = 16;
+// The routed gate_up ranks the logits in every workgroup: past ~2048 workgroups that costs more
+// than the top-k launch it replaces (c2: N <= 3, 64 workgroups per slot; c1: N <= 8, 16).
+constexpr int64_t kRouteMaxWorkgroups = 2048;
 
 // Routed expert bytes (gate_up + down) of one expert in the config's formats.
 static double expert_bytes(const qmoe_config_t& c) {
@@ -816,11 +819,11 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + rt - 1) / rt, stream);
   }
   if (rc) return rc;
-  // slot-major int4 SwiGLU experts: the top-k runs inside the routed gate_up launch
-  // (every wavefront ranks its token's logits: at most two tokens, where the launch is a few
-  // thousand wavefronts)
-  const bool route_in_gate_up = slot_major && N <= 2 && !mixed && gfmt == FMT_INT4 &&
-                                route_gate_up_fits(c.n_experts, c.top_k);
+  // slot-major int4 SwiGLU experts: the top-k runs inside the routed gate_up launch (one
+  // wavefront per workgroup ranks its slot's token), while the launch has few enough workgroups
+  const bool route_in_gate_up =
+      slot_major && !mixed && gfmt == FMT_INT4 && route_gate_up_fits(c.n_experts, c.top_k) &&
+      route_gate_up_workgroups(c.hidden, 2 * c.inter, mc) <= kRouteMaxWorkgroups;
   if (route_in_gate_up) {
     // (the routed gate_up below ranks the logits itself)
   } else if (slot_major) {

@@ -154,7 +154,7 @@ template <int FMT, int EPI, int W, int CPW, int JPW, int MT = 1, bool NORM = fal
           int DEEP = 0>
 __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx, int by,
                                            f32x4_t* red, const SlotRoute* route = nullptr,
-                                           u32x4* xlds = nullptr) {
+                                           u32x4* xlds = nullptr, int* route_e = nullptr) {
   using C = SmallCfg<FMT, EPI, W, CPW, JPW, MT>;
   static_assert(MT == 1 || fmt_dense(FMT), "several m-tiles per wavefront: dense weights only");
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
@@ -172,14 +172,20 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
     const SlotRoute& R = *route;
     const int m = by, t = m / R.P.k, s = m - t * R.P.k;
     const float* lrow = R.logits + static_cast<int64_t>(t) * R.ld;
-    int id;
-    float wsel;
-    // (only the storing wavefront needs the weights; the others rank up to their own slot)
-    if (bx == 0 && wave == 0)
-      topk_token<RVPL>(lrow, R.P, lane, id, wsel);
-    else
-      topk_token<RVPL, true>(lrow, R.P, lane, id, wsel, s + 1);
-    e = __builtin_amdgcn_readlane(id, s);
+    int id = 0;
+    float wsel = 0.f;
+    // Every wavefront of the workgroup serves slot m: wavefront 0 ranks the logits and shares
+    // the expert through LDS. Only the storing workgroup needs the routing weights; the others
+    // rank by logit up to the slot's own rank.
+    if (wave == 0) {
+      if (bx == 0)
+        topk_token<RVPL>(lrow, R.P, lane, id, wsel);
+      else
+        topk_token<RVPL, true>(lrow, R.P, lane, id, wsel, s + 1);
+      if (lane == 0) *route_e = __builtin_amdgcn_readlane(id, s);
+    }
+    __syncthreads();
+    e = __builtin_amdgcn_readfirstlane(*route_e);
     mt0[0] = m;
     mtc[0] = 1;
     route_tok = t;
@@ -664,8 +670,9 @@ __attribute__((amdgpu_waves_per_eu(SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW>::WP
 qmm_route_gate_up_kernel(QmmArgs a, int n_jobs, SlotRoute route) {
   __shared__ f32x4_t red[SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1>::RED];
   __shared__ u32x4 xlds[DEEP > 0 ? (W > 4 ? W : 4) * DEEP * 16 : 1];
+  __shared__ int route_e;
   small_body<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1, false, VPL, DEEP>(a, n_jobs, blockIdx.x, blockIdx.y,
-                                                                    red, &route, xlds);
+                                                                    red, &route, xlds, &route_e);
 }
 
 // Two dense products over the same activation rows in one launch (the router logits, tiled
@@ -1514,6 +1521,13 @@ static void launch_route_w(const QmmArgs& a, int64_t mc, const SlotRoute& R, int
 }
 
 bool route_gate_up_fits(int E, int k) { return E <= 512 && k <= 64; }
+
+int64_t route_gate_up_workgroups(int K, int n_rows, int64_t mc) {
+  const int nsb = K / 128;
+  const int W = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;   // launch_route_gate_up's chunking
+  const int jobs_per_wg = 4 / W, n_jobs = n_rows / 32;
+  return static_cast<int64_t>((n_jobs + jobs_per_wg - 1) / jobs_per_wg) * mc;
+}
 
 int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, const float* bias,
                          int E, int k, int scoring, int n_group, int topk_group, int norm_topk,

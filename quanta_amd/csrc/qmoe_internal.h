@@ -357,6 +357,8 @@ int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float
 // epilogue, a.act the N token rows (no slot_of/offsets); writes idx/w/sg and the slot-major
 // tile map, sorted and inv exactly as launch_topk does with a tile map.
 bool route_gate_up_fits(int E, int k);
+// Workgroups of that launch for mc slots (each ranks its token's logits once).
+int64_t route_gate_up_workgroups(int K, int n_rows, int64_t mc);
 int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, const float* bias,
                          int E, int k, int scoring, int n_group, int topk_group, int norm_topk,
                          float scale, int has_sg, int32_t* idx, float* w, float* sg,
