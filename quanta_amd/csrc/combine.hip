@@ -157,10 +157,22 @@ __global__ void __launch_bounds__(64 * kCsWaves) combine_shared_kernel(
       float acc1 = 0.f;
       if (t < N) {
         const int64_t m0 = static_cast<int64_t>(t) * k;
-        for (int s0 = 0; s0 < k; ++s0) {
-          const int pos = inv[m0 + s0];
-          if (pos >= 0 && pos < n_pos)
-            acc1 = fmaf(bf16_to_f32(d[static_cast<int64_t>(pos) * H + col]), w[m0 + s0], acc1);
+        // eight slots' positions, then their values, then the sums in slot order (one
+        // dependent-load round trip per eight slots instead of one per slot)
+        for (int s0 = 0; s0 < k; s0 += 8) {
+          int pos[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pos[j] = (s0 + j < k) ? inv[m0 + s0 + j] : -1;
+          float dv[8], wv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const bool ok = pos[j] >= 0 && pos[j] < n_pos;
+            dv[j] = ok ? bf16_to_f32(d[static_cast<int64_t>(pos[j]) * H + col]) : 0.f;
+            wv[j] = ok ? w[m0 + s0 + j] : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (pos[j] >= 0 && pos[j] < n_pos) acc1 = fmaf(dv[j], wv[j], acc1);
         }
       }
       routed[tl][f] = acc1;
