@@ -1141,11 +1141,10 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     for (int t = 0; t < 4; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // One superblock: four 32-k steps. Step s is MB slots; slot i issues the four MFMAs of
-  // m-block i, the LDS read of the A fragment two slots ahead, and 16/MB of step s+1's weight
-  // dequant units (tile u/4, nibble pair u%4), in that order (scheduling barriers).
+  // m-block i, the LDS read of the A fragment two slots ahead, and step s+1's weight dequant
+  // units [16i/MB, 16(i+1)/MB) (tile u/4, nibble pair u%4), in that order (scheduling barriers).
   auto compute = [&](int p, auto mbc) __attribute__((always_inline)) {
     constexpr int MB = decltype(mbc)::value;
-    constexpr int UPS = 16 / MB;
     constexpr int NI = 4 * MB;                 // A fragments (slots) per superblock
     const u32x4* la = reinterpret_cast<const u32x4*>(lds_c + a_slot(p)) + lane;
     const char* lb = lds_c + b_slot(p);
@@ -1188,7 +1187,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
         }
         if (s < 3) {
 #pragma unroll
-          for (int v = 0; v < UPS; ++v) deq_unit(s + 1, i * UPS + v, bf[c ^ 1]);
+          for (int u = i * 16 / MB; u < (i + 1) * 16 / MB; ++u) deq_unit(s + 1, u, bf[c ^ 1]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1215,6 +1214,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
   };
   if (mb_act <= 2) run(std::integral_constant<int, 2>{});
   else if (mb_act <= 4) run(std::integral_constant<int, 4>{});
+  else if (mb_act <= 6) run(std::integral_constant<int, 6>{});
   else run(std::integral_constant<int, 8>{});
 
   // epilogue: lane holds C[row 4(lane/16) + j][col lane%16] of each 16x16 block
