@@ -1212,10 +1212,16 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       }
     }
   };
-  if (mb_act <= 2) run(std::integral_constant<int, 2>{});
-  else if (mb_act <= 4) run(std::integral_constant<int, 4>{});
-  else if (mb_act <= 6) run(std::integral_constant<int, 6>{});
-  else run(std::integral_constant<int, 8>{});
+  switch (mb_act) {
+    case 1:
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    case 4: run(std::integral_constant<int, 4>{}); break;
+    case 5: run(std::integral_constant<int, 5>{}); break;
+    case 6: run(std::integral_constant<int, 6>{}); break;
+    case 7: run(std::integral_constant<int, 7>{}); break;
+    default: run(std::integral_constant<int, 8>{}); break;
+  }
 
   // epilogue: lane holds C[row 4(lane/16) + j][col lane%16] of each 16x16 block
 #pragma unroll
