@@ -789,16 +789,22 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = launch_qmm(sgu, sfmt, EPI_SWIGLU, sreg, (N + st - 1) / st, sstream);
       if (rc) return rc;
     }
-    // shared down -> sh_out (fused into the combine when decoding)
-    if (!fuse_dn) {
-      QmmArgs b{};
-      b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
-      b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = sh_dn_w; b.out = sh_out;
-      b.sb = sh8 ? wts->sh_dn_sb : nullptr;
-      b.ld_out = c.hidden;
-      rc = launch_qmm(b, sfmt, EPI_BF16, sreg, (N + st - 1) / st, sstream);
-      if (rc) return rc;
-    }
+  }
+  // shared down -> sh_out (fused into the combine when decoding). In the hybrid regime it is
+  // enqueued on the auxiliary stream after the cold experts' launches, so it runs beside the hot
+  // experts' down projection (where the auxiliary stream has slack) rather than their gate_up.
+  auto shared_down = [&]() -> int {
+    QmmArgs b{};
+    b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
+    b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = sh_dn_w; b.out = sh_out;
+    b.sb = sh8 ? wts->sh_dn_sb : nullptr;
+    b.ld_out = c.hidden;
+    return launch_qmm(b, sfmt, EPI_BF16, sreg, (N + st - 1) / st, sstream);
+  };
+  const bool shared_down_late = shared && !fuse_dn && hybrid && aux && sstream == aux->s;
+  if (shared && !fuse_dn && !shared_down_late) {
+    rc = shared_down();
+    if (rc) return rc;
   }
 
   // 2. router logits (+ the shared-expert gate logit in column E)
@@ -989,6 +995,10 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = routed(a, dfmt, EPI_BF16, h16, h_sinv);
       if (rc) return rc;
     }
+  }
+  if (shared_down_late) {
+    rc = shared_down();
+    if (rc) return rc;
   }
   if (aux) {
     rc = link(aux->join, aux->s, stream, "join");
