@@ -793,14 +793,21 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // shared down -> sh_out (fused into the combine when decoding). In the hybrid regime it is
   // enqueued on the auxiliary stream after the cold experts' launches, so it runs beside the hot
   // experts' down projection (where the auxiliary stream has slack) rather than their gate_up.
-  auto shared_down = [&]() -> int {
+  auto shared_down_args = [&]() {
     QmmArgs b{};
     b.act = sh_h; b.act_rows = N; b.slot_div = 1; b.dense_rows = N; b.n_experts = 1;
     b.K = c.shared_inter; b.n_rows = c.hidden; b.codes = sh_dn_w; b.out = sh_out;
     b.sb = sh8 ? wts->sh_dn_sb : nullptr;
     b.ld_out = c.hidden;
-    return launch_qmm(b, sfmt, EPI_BF16, sreg, (N + st - 1) / st, sstream);
+    return b;
   };
+  auto shared_down = [&]() -> int {
+    return launch_qmm(shared_down_args(), sfmt, EPI_BF16, sreg, (N + st - 1) / st, sstream);
+  };
+  // decode batches whose shared down would ride in the combine: with int8 shared weights and
+  // int4 routed experts it rides in the routed gate_up's launch instead (the combine then only
+  // gathers), when that launch pair has a compiled shape
+  bool sdn_in_gate_up = false;
   const bool shared_down_late = shared && !fuse_dn && hybrid && aux && sstream == aux->s;
   if (shared && !fuse_dn && !shared_down_late) {
     rc = shared_down();
@@ -950,6 +957,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       rc = launch_route_gate_up(a, n, logits, ld, wts->router_bias, c.n_experts, c.top_k, c.scoring,
                                 c.n_group, c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx,
                                 wv, sg, tile_map, tiles_small, sorted, inv, stream);
+    } else if (fuse_dn && sh8 && !hybrid && gfmt == FMT_INT4 &&
+               !(slot_major && dfmt == FMT_INT4 &&
+                 down_combine_fits(n, c.top_k, c.hidden, c.inter, c.shared_inter))) {
+      a.tile_map = reinterpret_cast<const int4*>(tile_map);
+      rc = launch_gate_up_shared_down(a, tiles_small, shared_down_args(), stream);
+      if (rc == 1) rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
+      else sdn_in_gate_up = (rc == 0);
     } else {
       rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);
     }
@@ -1005,7 +1019,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (rc) return rc;
   }
   // 7. unpermute + weighted combine + gated shared (its down projection fused when decoding) + bf16
-  if (fuse_dn)
+  if (fuse_dn && !sdn_in_gate_up)
     return launch_combine_shared(d, inv, wv, n, c.top_k, c.hidden, sh_h, c.shared_inter, sh_dn_w,
                                  sh8 ? wts->sh_dn_sb : nullptr, sfmt, has_sg ? sg : nullptr, y,
                                  stream, resid);

@@ -696,6 +696,30 @@ qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2)
     small_body<FMT2, EPI2, W, 1, 1, MT, NORM>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
 }
 
+// The routed gate_up (int4 SwiGLU over the permuted m-tiles, small-regime shape W/CPW/JPW) and
+// the shared expert's down projection (int8 codes, K = its intermediate size, one dense segment
+// of N rows; W2 chunks, MT2 m-tiles per wavefront) in one launch of 4-wavefront workgroups on a
+// flat grid: the gate_up's job blocks x m-tiles first, the shared down's after them. Each keeps
+// the arithmetic of its own launch, so the outputs are those of the two launches bit for bit.
+template <int W, int CPW, int JPW, int W2, int MT2>
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(SmallCfg<FMT_INT4, EPI_SWIGLU, W, CPW, JPW>::WPE)))
+qmm_gate_up_shdown_kernel(QmmArgs a1, int n_jobs1, int gx1, int64_t n1, QmmArgs a2, int n_jobs2,
+                          int gx2) {
+  constexpr int R1 = SmallCfg<FMT_INT4, EPI_SWIGLU, W, CPW, JPW, 1>::RED;
+  constexpr int R2 = SmallCfg<FMT_INT8, EPI_BF16, W2, 1, 1, MT2>::RED;
+  __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
+  const int64_t b = blockIdx.x;
+  if (b < n1) {
+    small_body<FMT_INT4, EPI_SWIGLU, W, CPW, JPW, 1>(a1, n_jobs1, static_cast<int>(b % gx1),
+                                                     static_cast<int>(b / gx1), red);
+  } else {
+    const int64_t b2 = b - n1;
+    small_body<FMT_INT8, EPI_BF16, W2, 1, 1, MT2>(a2, n_jobs2, static_cast<int>(b2 % gx2),
+                                                  static_cast<int>(b2 / gx2), red);
+  }
+}
+
 // ============================================================================ large-M kernel
 // Workgroup tile: 128 sorted positions x 256 weight rows (SwiGLU: 128 gate + 128 up rows ->
 // 128 h columns), one 128-deep k superblock per iteration. 8 wavefronts side by side along the
@@ -1616,6 +1640,47 @@ int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t strea
   else
     launch_pair_f<FMT_BF16>(a1, a2, mtiles, stream);
   return check_launch("qmm pair");
+}
+
+template <int W, int CPW, int JPW, int W2, int MT2>
+static int launch_gsd(const QmmArgs& a1, int64_t mtiles1, const QmmArgs& a2, int64_t mtiles2,
+                      hipStream_t stream) {
+  static_assert(W <= 4 && W2 <= 4, "one 4-wavefront workgroup shape for both products");
+  const int n_jobs1 = a1.n_rows / 32 / JPW, gx1 = (n_jobs1 + 4 / W - 1) / (4 / W);
+  const int n_jobs2 = a2.n_rows / 16, gx2 = (n_jobs2 + 4 / W2 - 1) / (4 / W2);
+  const int64_t n1 = static_cast<int64_t>(gx1) * mtiles1;
+  const int64_t n2 = static_cast<int64_t>(gx2) * ((MT2 == 2) ? (mtiles2 + 1) / 2 : mtiles2);
+  if (n1 + n2 > 0x7fffffff) return fail("qmm(gate_up + shared down): grid too large");
+  qmm_gate_up_shdown_kernel<W, CPW, JPW, W2, MT2>
+      <<<dim3(static_cast<unsigned>(n1 + n2)), 256, 0, stream>>>(a1, n_jobs1, gx1, n1, a2, n_jobs2, gx2);
+  return check_launch("qmm(gate_up + shared down)");
+}
+
+int launch_gate_up_shared_down(const QmmArgs& a1, int64_t mtiles1, const QmmArgs& a2,
+                               hipStream_t stream) {
+  if (a1.K % 128 || a1.n_rows % 32 || !a1.tile_map || mtiles1 <= 0 || mtiles1 > 65535 ||
+      a2.K % 64 || a2.n_rows % 16 || !a2.sb || a2.offsets || a2.tile_map || a2.dense_rows <= 0)
+    return fail("qmm(gate_up + shared down): routed int4 gate_up and a dense int8 product required");
+  const int nsb = a1.K / 128;
+  const int ch = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;   // launch_qmm's int4 chunk rule
+  const SmallShape sh = pick_small_shape(FMT_INT4, EPI_SWIGLU, ch, mtiles1, a1.n_rows / 32);
+  const int w2 = bf16_chunks(a2.K);
+  const int64_t mtiles2 = (a2.dense_rows + kSmallMTile - 1) / kSmallMTile;
+  const bool mt2 = mtiles2 >= kSmallMt2MinTiles;   // as launch_small_k for dense products
+#define QMOE_GSD(W, CPW, JPW, W2)                                                    \
+  if (sh.w == W && sh.cpw == CPW && sh.jpw == JPW && w2 == W2)                        \
+    return mt2 ? launch_gsd<W, CPW, JPW, W2, 2>(a1, mtiles1, a2, mtiles2, stream)     \
+               : launch_gsd<W, CPW, JPW, W2, 1>(a1, mtiles1, a2, mtiles2, stream);
+  // c2-like shapes (H 4096, shared intermediate 1024). With two m-tiles per wavefront the
+  // shared down does not fit beside this gate_up shape's registers (c2 N=64 461 vs 445 us)
+  if (sh.w == 2 && sh.cpw == 2 && sh.jpw == 2 && w2 == 4 && !mt2)
+    return launch_gsd<2, 2, 2, 4, 1>(a1, mtiles1, a2, mtiles2, stream);
+  QMOE_GSD(4, 1, 2, 4)
+  QMOE_GSD(4, 1, 1, 4)
+  QMOE_GSD(2, 1, 1, 2)   // c1-like shapes (H 2048, shared intermediate 512)
+  QMOE_GSD(2, 1, 2, 2)
+#undef QMOE_GSD
+  return 1;   // no compiled combination: the caller launches the two products apart
 }
 
 int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bound,

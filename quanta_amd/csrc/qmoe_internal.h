@@ -356,6 +356,12 @@ int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int64_t N, int H, float
 // Slot-major routed gate_up with the top-k done in the launch (qmm.hip): int4 weights, SwiGLU
 // epilogue, a.act the N token rows (no slot_of/offsets); writes idx/w/sg and the slot-major
 // tile map, sorted and inv exactly as launch_topk does with a tile map.
+// The routed int4 SwiGLU gate_up (small regime, a1 with its tile map over mtiles1 m-tiles) and a
+// dense int8 product (a2: the shared expert's down projection) in one launch, each with the
+// arithmetic of its own launch. Returns 1 without launching when the two shapes have no
+// compiled combination.
+int launch_gate_up_shared_down(const QmmArgs& a1, int64_t mtiles1, const QmmArgs& a2,
+                               hipStream_t stream);
 bool route_gate_up_fits(int E, int k);
 // Workgroups of that launch for mc slots (each ranks its token's logits once).
 int64_t route_gate_up_workgroups(int K, int n_rows, int64_t mc);
