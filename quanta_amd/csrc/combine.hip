@@ -952,14 +952,24 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       const hipError_t err = hipStreamWaitEvent(stream, aux->xready, 0);
       if (err != hipSuccess) return fail(std::string("forward: x16 wait: ") + hipGetErrorString(err));
     }
+    // (the fused tail below computes the shared down itself)
+    const bool tail = slot_major && dfmt == FMT_INT4 &&
+                      down_combine_fits(n, c.top_k, c.hidden, c.inter, c.shared_inter);
     if (route_in_gate_up) {
       a.slot_of = nullptr; a.slot_div = 1; a.n_slots = 0; a.offsets = nullptr; a.tile_off = nullptr;
+      const QmmArgs sdn = shared_down_args();
+      const bool with_sdn = fuse_dn && sh8 && !tail;
       rc = launch_route_gate_up(a, n, logits, ld, wts->router_bias, c.n_experts, c.top_k, c.scoring,
                                 c.n_group, c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx,
-                                wv, sg, tile_map, tiles_small, sorted, inv, stream);
-    } else if (fuse_dn && sh8 && !hybrid && gfmt == FMT_INT4 &&
-               !(slot_major && dfmt == FMT_INT4 &&
-                 down_combine_fits(n, c.top_k, c.hidden, c.inter, c.shared_inter))) {
+                                wv, sg, tile_map, tiles_small, sorted, inv, stream,
+                                with_sdn ? &sdn : nullptr);
+      if (rc == 1)
+        rc = launch_route_gate_up(a, n, logits, ld, wts->router_bias, c.n_experts, c.top_k,
+                                  c.scoring, c.n_group, c.topk_group, c.norm_topk, c.routed_scale,
+                                  has_sg, idx, wv, sg, tile_map, tiles_small, sorted, inv, stream);
+      else
+        sdn_in_gate_up = with_sdn && rc == 0;
+    } else if (fuse_dn && sh8 && !hybrid && gfmt == FMT_INT4 && !tail) {
       a.tile_map = reinterpret_cast<const int4*>(tile_map);
       rc = launch_gate_up_shared_down(a, tiles_small, shared_down_args(), stream);
       if (rc == 1) rc = routed(a, gfmt, EPI_SWIGLU, x16, x_sinv);

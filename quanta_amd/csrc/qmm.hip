@@ -47,6 +47,7 @@ struct SlotRoute {
   int max_tiles;
   int32_t* sorted;
   int32_t* inv;
+  int mc;   // slots (N * k): the m-tiles of the launch
 };
 
 __device__ __forceinline__ int find_segment(const int32_t* __restrict__ tile_off, int E, int mt) {
@@ -199,7 +200,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       }
       if (s == 0 && lane == 0 && R.P.has_sg) R.sg[t] = 1.0f / (1.0f + expf(-lrow[R.P.E]));
       if (m == 0) {
-        const int mc = gridDim.y;
+        const int mc = R.mc;
         for (int i = mc + lane; i < R.max_tiles; i += 64) R.tile_map[i] = make_int4(-1, 0, 0, 0);
       }
     }
@@ -673,6 +674,31 @@ qmm_route_gate_up_kernel(QmmArgs a, int n_jobs, SlotRoute route) {
   __shared__ int route_e;
   small_body<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1, false, VPL, DEEP>(a, n_jobs, blockIdx.x, blockIdx.y,
                                                                     red, &route, xlds, &route_e);
+}
+
+// The same with the shared expert's int8 down projection (a2: W2 chunks, one m-tile per
+// wavefront) in the launch, on a flat grid of 4-wavefront workgroups: the routed gate_up's job
+// blocks x slots first, then the shared down's job blocks x m-tiles.
+template <int W, int JPW, int VPL, int DEEP, int W2>
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW>::WPE)))
+qmm_route_gate_up_shdown_kernel(QmmArgs a, int n_jobs, SlotRoute route, int gx1, int64_t n1,
+                                QmmArgs a2, int n_jobs2, int gx2) {
+  static_assert(W <= 4 && W2 <= 4, "one 4-wavefront workgroup shape for both products");
+  constexpr int R1 = SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1>::RED;
+  constexpr int R2 = SmallCfg<FMT_INT8, EPI_BF16, W2, 1, 1, 1>::RED;
+  __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
+  __shared__ u32x4 xlds[DEEP > 0 ? 4 * DEEP * 16 : 1];
+  __shared__ int route_e;
+  const int64_t b = blockIdx.x;
+  if (b < n1) {
+    small_body<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1, false, VPL, DEEP>(
+        a, n_jobs, static_cast<int>(b % gx1), static_cast<int>(b / gx1), red, &route, xlds, &route_e);
+  } else {
+    const int64_t b2 = b - n1;
+    small_body<FMT_INT8, EPI_BF16, W2, 1, 1, 1>(a2, n_jobs2, static_cast<int>(b2 % gx2),
+                                                static_cast<int>(b2 / gx2), red);
+  }
 }
 
 // Two dense products over the same activation rows in one launch (the router logits, tiled
@@ -1529,10 +1555,26 @@ static int launch_wide(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
 // Slot-major routed gate_up with its routing (qmm_route_gate_up_kernel): int4 weights, SwiGLU,
 // the decode kernel's chunking (W = CH wavefronts per job, one chunk each, one tile pair each).
 template <int W, int VPL>
-static void launch_route_k(const QmmArgs& a, int64_t mc, const SlotRoute& R, hipStream_t stream) {
+static void launch_route_k(const QmmArgs& a, int64_t mc, const SlotRoute& R, hipStream_t stream,
+                           const QmmArgs* sdn = nullptr, int w2 = 0) {
   constexpr int WAVES = W > 4 ? W : 4;
   const int n_jobs = a.n_rows / 32;
   const int jobs_per_wg = WAVES / W;
+  if (sdn) {   // (the caller checked w2 and the m-tile count)
+    const int gx1 = (n_jobs + jobs_per_wg - 1) / jobs_per_wg;
+    const int64_t n1 = static_cast<int64_t>(gx1) * mc;
+    const int n_jobs2 = sdn->n_rows / 16, gx2 = (n_jobs2 + 4 / w2 - 1) / (4 / w2);
+    const int64_t n2 = static_cast<int64_t>(gx2) * ((sdn->dense_rows + kSmallMTile - 1) / kSmallMTile);
+    const dim3 g(static_cast<unsigned>(n1 + n2));
+#define QMOE_RSD(D, W2_)                                                                      \
+  qmm_route_gate_up_shdown_kernel<W, 1, VPL, D, W2_><<<g, 256, 0, stream>>>(a, n_jobs, R, gx1, n1, \
+                                                                          *sdn, n_jobs2, gx2)
+    const bool deep = (a.K / 128 == 8 * W);
+    if (w2 == 4) { if (deep) QMOE_RSD(8, 4); else QMOE_RSD(0, 4); }
+    else { if (deep) QMOE_RSD(8, 2); else QMOE_RSD(0, 2); }
+#undef QMOE_RSD
+    return;
+  }
   dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mc));
   // every weight load of a wavefront's chunk in flight at once when the chunk is 8 superblocks
   if (a.K / 128 == 8 * W)
@@ -1541,12 +1583,13 @@ static void launch_route_k(const QmmArgs& a, int64_t mc, const SlotRoute& R, hip
     qmm_route_gate_up_kernel<W, 1, VPL, 0><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
 }
 template <int W>
-static void launch_route_w(const QmmArgs& a, int64_t mc, const SlotRoute& R, int vpl, hipStream_t stream) {
+static void launch_route_w(const QmmArgs& a, int64_t mc, const SlotRoute& R, int vpl, hipStream_t stream,
+                           const QmmArgs* sdn, int w2) {
   switch (vpl) {
-    case 1: launch_route_k<W, 1>(a, mc, R, stream); break;
-    case 2: launch_route_k<W, 2>(a, mc, R, stream); break;
-    case 4: launch_route_k<W, 4>(a, mc, R, stream); break;
-    default: launch_route_k<W, 8>(a, mc, R, stream); break;
+    case 1: launch_route_k<W, 1>(a, mc, R, stream, sdn, w2); break;
+    case 2: launch_route_k<W, 2>(a, mc, R, stream, sdn, w2); break;
+    case 4: launch_route_k<W, 4>(a, mc, R, stream, sdn, w2); break;
+    default: launch_route_k<W, 8>(a, mc, R, stream, sdn, w2); break;
   }
 }
 
@@ -1563,20 +1606,30 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
                          int E, int k, int scoring, int n_group, int topk_group, int norm_topk,
                          float scale, int has_sg, int32_t* idx, float* w, float* sg,
                          int32_t* tile_map, int64_t max_tiles, int32_t* sorted, int32_t* inv,
-                         hipStream_t stream) {
+                         hipStream_t stream, const QmmArgs* sdn) {
   const int64_t mc = static_cast<int64_t>(N) * k;
   if (!route_gate_up_fits(E, k) || a.K % 128 || a.n_rows % 32 || mc <= 0 || mc > 65535 ||
       max_tiles < mc || max_tiles > (int64_t(1) << 30) || a.slot_of || a.offsets)
     return fail("qmm(route): outside the slot-major routed gate_up");
   SlotRoute R{logits, ld, topk_params(bias, E, k, scoring, n_group, topk_group, norm_topk, scale, has_sg),
               idx, w, sg, reinterpret_cast<int4*>(tile_map), static_cast<int>(max_tiles), sorted, inv,
-};
+              static_cast<int>(mc)};
   const int nsb = a.K / 128;
   const int ch = (nsb >= 32) ? 4 : (nsb >= 8) ? 2 : 1;   // the int4 chunk rule of launch_qmm
   const int vpl = topk_vpl(E);
-  if (ch == 4) launch_route_w<4>(a, mc, R, vpl, stream);
-  else if (ch == 2) launch_route_w<2>(a, mc, R, vpl, stream);
-  else launch_route_w<1>(a, mc, R, vpl, stream);
+  int w2 = 0;
+  if (sdn) {
+    if (sdn->K % 64 || sdn->n_rows % 16 || !sdn->sb || sdn->offsets || sdn->tile_map ||
+        sdn->dense_rows <= 0)
+      return fail("qmm(route): the shared down is one dense int8 segment");
+    w2 = bf16_chunks(sdn->K);
+    // one m-tile per wavefront below kSmallMt2MinTiles m-tiles, as its own launch would run it
+    if ((w2 != 2 && w2 != 4) || (sdn->dense_rows + kSmallMTile - 1) / kSmallMTile >= kSmallMt2MinTiles)
+      return 1;   // no compiled combination: the caller launches the shared down apart
+  }
+  if (ch == 4) launch_route_w<4>(a, mc, R, vpl, stream, sdn, w2);
+  else if (ch == 2) launch_route_w<2>(a, mc, R, vpl, stream, sdn, w2);
+  else launch_route_w<1>(a, mc, R, vpl, stream, sdn, w2);
   return check_launch("qmm(route)");
 }
 

@@ -369,7 +369,9 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
                          int E, int k, int scoring, int n_group, int topk_group, int norm_topk,
                          float scale, int has_sg, int32_t* idx, float* w, float* sg,
                          int32_t* tile_map, int64_t max_tiles, int32_t* sorted, int32_t* inv,
-                         hipStream_t stream);
+                         hipStream_t stream, const QmmArgs* sdn = nullptr);
+// (sdn: the shared expert's int8 down projection, one dense segment, in the same launch; returns 1
+// without launching when that pair has no compiled shape)
 // Slot-major decode tail (fused.hip): routed int4 down, shared down (tiled bf16 or int8 as sfmt)
 // and the combine in one launch; h/idx/w in slot order. down_combine_fits: the shapes it takes
 // (I = 512 or 1024, a shared expert of <= 8 bf16 chunks, at most 24 units of work per
