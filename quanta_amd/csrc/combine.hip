@@ -958,7 +958,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (route_in_gate_up) {
       a.slot_of = nullptr; a.slot_div = 1; a.n_slots = 0; a.offsets = nullptr; a.tile_off = nullptr;
       const QmmArgs sdn = shared_down_args();
-      const bool with_sdn = fuse_dn && sh8 && !tail;
+      // (the fused tail then adds the computed shared output instead of its shared units)
+      const bool with_sdn = fuse_dn && sh8;
       rc = launch_route_gate_up(a, n, logits, ld, wts->router_bias, c.n_experts, c.top_k, c.scoring,
                                 c.n_group, c.topk_group, c.norm_topk, c.routed_scale, has_sg, idx,
                                 wv, sg, tile_map, tiles_small, sorted, inv, stream,
@@ -987,6 +988,10 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // down and combine in one launch per 16 output features (the down output stays on chip)
   if (slot_major && fuse_dn && !mixed && dfmt == FMT_INT4 &&
       down_combine_fits(n, c.top_k, c.hidden, c.inter, c.shared_inter)) {
+    if (sdn_in_gate_up)
+      return launch_down_combine(h, idx, wv, has_sg ? sg : nullptr, n, c.top_k, c.hidden, c.inter,
+                                 wts->dn_codes, wts->dn_sb, nullptr, 0, nullptr, nullptr, sfmt,
+                                 resid, y, stream, sh_out);
     return launch_down_combine(h, idx, wv, has_sg ? sg : nullptr, n, c.top_k, c.hidden, c.inter,
                                wts->dn_codes, wts->dn_sb, sh_h, c.shared_inter, sh_dn_w,
                                sh8 ? wts->sh_dn_sb : nullptr, sfmt, resid, y, stream);

@@ -14,7 +14,8 @@
 //     MFMA on the raw codes as bf16 128 + q, affine fix-up per 64-wide group).
 // Partial sums meet in LDS, are added in chunk order, rounded to bf16 (the down output d and
 // the shared output, bf16 tensors in the reference), then summed over each token's slots in
-// slot order in fp32: y = bf16(fmaf(sh, g, sum_s w * d)) (+ the residual row). Every value
+// slot order in fp32: y = bf16(fmaf(sh, g, sum_s w * d)) (+ the residual row). With sh_out the
+// shared output comes computed (by the routed gate_up's launch) and no shared units run. Every value
 // equals the unfused path's (decode kernel, combine_shared_kernel) bit for bit, and the down
 // output never round-trips HBM.
 //
@@ -45,6 +46,7 @@ struct DcArgs {
   const void* wd;           // shared down, tiled bf16 or int8
   const uint16_t* wd_sb;    // shared down scale/bias (int8)
   const uint16_t* resid;    // nullable residual rows [N][H]
+  const uint16_t* sh_out;   // [N][H] bf16 shared output computed earlier (with sh_h null), or null
   uint16_t* y;              // [N][H]
   int N, k, H, I, Is, nch, chd;
 };
@@ -201,6 +203,9 @@ __global__ void __launch_bounds__(64 * WAVES) down_combine_kernel(DcArgs a) {
     if (a.sh_h) {
       const float g = a.sg ? a.sg[tl] : 1.0f;
       v = f32_to_bf16(fmaf(sh[tl][f], g, routed));
+    } else if (a.sh_out) {
+      const float g = a.sg ? a.sg[tl] : 1.0f;
+      v = f32_to_bf16(fmaf(bf16_to_f32(a.sh_out[o]), g, routed));
     } else {
       v = f32_to_bf16(routed);
     }
@@ -221,11 +226,13 @@ bool down_combine_fits(int N, int k, int H, int I, int Is) {
 int launch_down_combine(const uint16_t* h, const int32_t* idx, const float* w, const float* sg,
                         int N, int k, int H, int I, const void* codes, const uint16_t* sb,
                         const uint16_t* sh_h, int Is, const void* wd, const uint16_t* wd_sb,
-                        int sfmt, const uint16_t* resid, uint16_t* y, hipStream_t stream) {
+                        int sfmt, const uint16_t* resid, uint16_t* y, hipStream_t stream,
+                        const uint16_t* sh_out) {
+  if (sh_h && sh_out) return fail("down_combine: the shared output is computed here or given");
   if (!down_combine_fits(N, k, H, I, sh_h ? Is : 0))
     return fail("down_combine: shape outside the slot-major fused tail");
   const int nsb = I / 128;
-  DcArgs a{h, idx, w, sg, codes, sb, sh_h, wd, wd_sb, resid, y,
+  DcArgs a{h, idx, w, sg, codes, sb, sh_h, wd, wd_sb, resid, sh_out, y,
            N, k, H, I, sh_h ? Is : 0, sh_h ? bf16_chunks(Is) : 0, (nsb >= 8) ? 2 : 1};
   const dim3 grid(H / 16);
   if (sfmt == FMT_INT8) down_combine_kernel<FMT_INT8, 8><<<grid, 512, 0, stream>>>(a);

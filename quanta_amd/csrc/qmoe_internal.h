@@ -375,12 +375,14 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
 // Slot-major decode tail (fused.hip): routed int4 down, shared down (tiled bf16 or int8 as sfmt)
 // and the combine in one launch; h/idx/w in slot order. down_combine_fits: the shapes it takes
 // (I = 512 or 1024, a shared expert of <= 8 bf16 chunks, at most 24 units of work per
-// workgroup: one or two tokens).
+// workgroup: one or two tokens). sh_out (with sh_h null): the bf16 shared output, computed
+// earlier, added in the combine.
 bool down_combine_fits(int N, int k, int H, int I, int Is);
 int launch_down_combine(const uint16_t* h, const int32_t* idx, const float* w, const float* sg,
                         int N, int k, int H, int I, const void* codes, const uint16_t* sb,
                         const uint16_t* sh_h, int Is, const void* wd, const uint16_t* wd_sb,
-                        int sfmt, const uint16_t* resid, uint16_t* y, hipStream_t stream);
+                        int sfmt, const uint16_t* resid, uint16_t* y, hipStream_t stream,
+                        const uint16_t* sh_out = nullptr);
 
 constexpr int kSmallMTile = 16;
 constexpr int kLargeMTile = 128;
