@@ -1569,18 +1569,26 @@ static void launch_route_k(const QmmArgs& a, int64_t mc, const SlotRoute& R, hip
 #define QMOE_RSD(D, W2_)                                                                      \
   qmm_route_gate_up_shdown_kernel<W, 1, VPL, D, W2_><<<g, 256, 0, stream>>>(a, n_jobs, R, gx1, n1, \
                                                                           *sdn, n_jobs2, gx2)
-    const bool deep = (a.K / 128 == 8 * W);
-    if (w2 == 4) { if (deep) QMOE_RSD(8, 4); else QMOE_RSD(0, 4); }
-    else { if (deep) QMOE_RSD(8, 2); else QMOE_RSD(0, 2); }
+    // (one chunk per job, W = 1, means fewer than 8 superblocks: never the deep form)
+    if constexpr (W > 1) {
+      if (a.K / 128 == 8 * W) {
+        if (w2 == 4) QMOE_RSD(8, 4); else QMOE_RSD(8, 2);
+        return;
+      }
+    }
+    if (w2 == 4) QMOE_RSD(0, 4); else QMOE_RSD(0, 2);
 #undef QMOE_RSD
     return;
   }
   dim3 grid((n_jobs + jobs_per_wg - 1) / jobs_per_wg, static_cast<unsigned>(mc));
   // every weight load of a wavefront's chunk in flight at once when the chunk is 8 superblocks
-  if (a.K / 128 == 8 * W)
-    qmm_route_gate_up_kernel<W, 1, VPL, 8><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
-  else
-    qmm_route_gate_up_kernel<W, 1, VPL, 0><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
+  if constexpr (W > 1) {
+    if (a.K / 128 == 8 * W) {
+      qmm_route_gate_up_kernel<W, 1, VPL, 8><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
+      return;
+    }
+  }
+  qmm_route_gate_up_kernel<W, 1, VPL, 0><<<grid, 64 * WAVES, 0, stream>>>(a, n_jobs, R);
 }
 template <int W>
 static void launch_route_w(const QmmArgs& a, int64_t mc, const SlotRoute& R, int vpl, hipStream_t stream,
