@@ -1733,8 +1733,9 @@ int launch_gate_up_shared_down(const QmmArgs& a1, int64_t mtiles1, const QmmArgs
     return mt2 ? launch_gsd<W, CPW, JPW, W2, 2>(a1, mtiles1, a2, mtiles2, stream)     \
                : launch_gsd<W, CPW, JPW, W2, 1>(a1, mtiles1, a2, mtiles2, stream);
   // c2-like shapes (H 4096, shared intermediate 1024). With two m-tiles per wavefront the
-  // shared down does not fit beside this gate_up shape's registers (c2 N=64 461 vs 445 us)
-  if (sh.w == 2 && sh.cpw == 2 && sh.jpw == 2 && w2 == 4 && !mt2)
+  // shared down does not fit beside this gate_up shape's registers (c2 N=64 461 vs 445 us), so
+  // it runs one m-tile per wavefront there (the same sums: m-tiles are independent)
+  if (sh.w == 2 && sh.cpw == 2 && sh.jpw == 2 && w2 == 4)
     return launch_gsd<2, 2, 2, 4, 1>(a1, mtiles1, a2, mtiles2, stream);
   QMOE_GSD(4, 1, 2, 4)
   QMOE_GSD(4, 1, 1, 4)
