@@ -418,9 +418,11 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   // int8 shared expert above the decode sizes: its weights expanded to tiled bf16 for the
   // large-M kernel (gate|up [2 Is, H] then down [H, Is])
   L.sh_w16 = take(shared_expands(c, N) ? static_cast<size_t>(3) * c.shared_inter * c.hidden * 2 : 0);
-  // fp16 per-row-scaled activation copies for the large-M int4 regime
-  L.x16 = take(static_cast<size_t>(N) * c.hidden * 2);
-  L.x_sinv = take(static_cast<size_t>(N) * 4);
+  // fp16 per-row-scaled activation copies for the large-M int4 regime (AWQ: of the gate's and
+  // the up projection's prescaled rows, [2][mc])
+  const int64_t x16_rows = c.awq ? 2 * mc : N;
+  L.x16 = take(static_cast<size_t>(x16_rows) * c.hidden * 2);
+  L.x_sinv = take(static_cast<size_t>(x16_rows) * 4);
   L.h16 = take(static_cast<size_t>(mc) * c.inter * 2);
   L.h_sinv = take(static_cast<size_t>(mc) * 4);
   // AWQ: the gate and up projections' prescaled rows [2][mc][H] and their outputs [mc][2I]
@@ -446,6 +448,13 @@ static int kernel_fmt(int f) {
          : f == QMOE_FMT_INT3_G64 ? FMT_INT3 : f == QMOE_FMT_INT8_G64 ? FMT_INT8 : FMT_BF16;
 }
 // int3 or int6 codes on either projection: the large-M kernels stage int4 superblocks only.
+// AWQ-scaled experts in the large regime: int4 weights, and gate and up halves that split at a
+// whole 256-row block (the large kernels pick the activation copy per weight-row block)
+static bool awq_large_ok(const qmoe_config_t& c) {
+  return c.expert_format == QMOE_FMT_INT4_G64 && c.down_format == QMOE_FMT_INT4_G64 &&
+         c.inter % 256 == 0;
+}
+
 static bool narrow_codes(const qmoe_config_t& c) {
   return c.expert_format == QMOE_FMT_INT6_G64 || c.expert_format == QMOE_FMT_INT3_G64 ||
          c.down_format == QMOE_FMT_INT6_G64 || c.down_format == QMOE_FMT_INT3_G64;
@@ -499,8 +508,8 @@ static int validate_config(const qmoe_config_t& c) {
   if (c.awq != 0 && c.awq != 1) return fail("config: awq must be 0 or 1");
   if (c.awq && c.expert_format == QMOE_FMT_BF16)
     return fail("config: awq scales need quantized experts");
-  if (c.awq && c.regime == QMOE_REGIME_LARGE)
-    return fail("config: experts with awq scales run in the small regime only");
+  if (c.awq && c.regime == QMOE_REGIME_LARGE && !awq_large_ok(c))
+    return fail("config: awq scales in the large regime need int4 experts and inter % 256 == 0");
   if (c.mixed != 0 && c.mixed != 1) return fail("config: mixed must be 0 or 1");
   if (c.mixed && (c.awq || c.regime == QMOE_REGIME_LARGE))
     return fail("config: mixed-width experts run in the small regime, without awq scales");
@@ -615,8 +624,8 @@ extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  // no large-regime kernel for int3/int6, AWQ scales or mixed widths
-  if (narrow_codes(c) || c.awq || c.mixed) return QMOE_REGIME_SMALL;
+  // no large-regime kernel for int3/int6 or mixed widths
+  if (narrow_codes(c) || c.mixed || (c.awq && !awq_large_ok(c))) return QMOE_REGIME_SMALL;
   return dense_regime(c, N);
 }
 
@@ -746,8 +755,11 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (shared_aux) sstream = aux->s;
   }
   // hybrid prefill with int4 experts: the hot experts' gate_up reads an fp16 copy of x, made
-  // first on the auxiliary stream, beside the routing chain (hybrid implies int4 or bf16 experts)
-  const bool f16_acts = (hybrid && gfmt == FMT_INT4);
+  // first on the auxiliary stream, beside the routing chain (hybrid implies int4 or bf16 experts;
+  // AWQ: copies of the prescaled rows instead, made after the permute), and their down an fp16
+  // copy of h
+  const bool f16_acts = (hybrid && gfmt == FMT_INT4 && !c.awq);
+  const bool f16_h = (hybrid && dfmt == FMT_INT4);
   if (f16_acts) {
     rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, aux ? aux->s : stream);
     if (rc) return rc;
@@ -868,6 +880,20 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                         hybrid ? tile_map_big : nullptr, L.max_tiles_big);
     if (rc) return rc;
   }
+  // AWQ: each sorted row divided by its expert's gate and up scales (and, for the hybrid
+  // regime's hot experts, the fp16 copies of both row sets)
+  uint16_t* awq_xg = reinterpret_cast<uint16_t*>(base + L.awq_x);
+  if (c.awq && hybrid && c.hidden <= kAwqSplitMaxH) {
+    // (hot experts' rows only as their fp16 copies, cold experts' only as bf16)
+    rc = launch_awq_prescale_split(x, sorted, offsets, c.n_experts, c.top_k, mc, c.hidden,
+                                   wts->awq_gu, kHybridSplitRows, awq_xg, x16, x_sinv, stream);
+    if (rc) return rc;
+  } else if (c.awq) {
+    rc = launch_awq_prescale(x, sorted, offsets, c.n_experts, c.top_k, mc, c.hidden, wts->awq_gu,
+                             awq_xg, awq_xg + mc * c.hidden, stream);
+    if (!rc && hybrid) rc = launch_act_to_f16(awq_xg, 2 * mc, c.hidden, x16, x_sinv, stream);
+    if (rc) return rc;
+  }
   // the cold experts' tiles wait for the permute on the auxiliary stream
   hipStream_t cstream = stream;
   if (hybrid && aux) {
@@ -923,20 +949,21 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   } else if (c.awq) {
     // AWQ: gate and up on their own prescaled rows (one launch over all 2I rows of each expert,
     // the up half's tiles reading the up rows) into awq_gu, then h = bf16(glu / s_dn)
-    uint16_t* xg = reinterpret_cast<uint16_t*>(base + L.awq_x);
-    uint16_t* xu = xg + mc * c.hidden;
     uint16_t* gu = reinterpret_cast<uint16_t*>(base + L.awq_gu);
-    rc = launch_awq_prescale(x, sorted, offsets, c.n_experts, c.top_k, mc, c.hidden, wts->awq_gu,
-                             xg, xu, stream);
-    if (rc) return rc;
     QmmArgs a{};
-    a.act = xg; a.act_hi = xu; a.split_tile = c.inter / 16;
+    a.act = awq_xg; a.act_hi = awq_xg + mc * c.hidden; a.split_tile = c.inter / 16;
     a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
+    a.row_exp = (gfmt == FMT_INT4) ? wts->gu_rexp : nullptr;
     a.out = gu; a.ld_out = 2 * c.inter;
-    rc = routed(a, gfmt, EPI_BF16, nullptr, nullptr);
+    if (hybrid) { a.act16_hi = x16 + mc * c.hidden; a.row_sinv_hi = x_sinv + mc; }
+    rc = routed(a, gfmt, EPI_BF16, x16, x_sinv);
     if (rc) return rc;
+    if (hybrid && aux) {   // all of gu (cold rows from the auxiliary stream) before the glu pass
+      rc = link(aux->cold, aux->s, stream, "cold gate_up");
+      if (rc) return rc;
+    }
     rc = launch_awq_glu(gu, offsets, c.n_experts, mc, c.inter, wts->awq_dn, c.act, c.act_alpha,
                         c.act_limit, h, stream);
     if (rc) return rc;
@@ -1004,7 +1031,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
     a.row_exp = (dfmt == FMT_INT4) ? wts->dn_rexp : nullptr;
     a.out = d; a.ld_out = c.hidden;
-    if (f16_acts) {
+    if (f16_h) {
       rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);
       if (rc) return rc;
     }

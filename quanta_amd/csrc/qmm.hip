@@ -884,6 +884,10 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const int cb = rk % nbk;
   const int mrows = (a.dense_mtile > 0 && !a.offsets && !a.tile_map) ? a.dense_mtile : kLargeMTile;
   if (mt >= a.mtiles || !resolve_mtile(a, mt, mrows, e, m0, m_cnt)) return;
+  // (AWQ: the 256-row blocks from split_tile on read the second activation copy)
+  const bool hi = (FMT == FMT_INT4) && a.act16_hi && 16 * cb >= a.split_tile;
+  const uint16_t* act16 = hi ? a.act16_hi : a.act16;
+  const float* row_sinv = hi ? a.row_sinv_hi : a.row_sinv;
   const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
   const int nsb = a.K / 128;
   const int mb_act = __builtin_amdgcn_readfirstlane((m_cnt + 15) >> 4);   // 1..8
@@ -897,7 +901,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   {
     const int r = 16 * wave + (lane & 15);
     const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
-    const uint16_t* abase = (FMT == FMT_INT4) ? a.act16 : a.act;
+    const uint16_t* abase = (FMT == FMT_INT4) ? act16 : a.act;
     arow_ptr = reinterpret_cast<const char*>(abase + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
                16 * lg_chunk<FMT>(0, lane >> 4);
   }
@@ -1077,7 +1081,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       // rows whose activation row is invalid read as zeros (their A data was row 0's)
       const int64_t ar2 = act_row(a, m0 + mr);
       const bool ok = ar2 >= 0;
-      const float rs = (FMT == FMT_INT4 && ok) ? a.row_sinv[ar2] : 1.0f;
+      const float rs = (FMT == FMT_INT4 && ok) ? row_sinv[ar2] : 1.0f;
       // undo both power-of-two scalings (activation row, int4 weight row): exact
       auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {
@@ -1137,6 +1141,10 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
   const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
   const int nsb = a.K / 128;
   const int mb_act = __builtin_amdgcn_readfirstlane((m_cnt + 15) >> 4);   // 1..8
+  // (AWQ: the 512-row blocks from split_tile on read the second activation copy)
+  const bool hi = a.act16_hi && 32 * cb >= a.split_tile;
+  const uint16_t* act16 = hi ? a.act16_hi : a.act16;
+  const float* row_sinv = hi ? a.row_sinv_hi : a.row_sinv;
 
   // activation source: wavefront w loads m-block w (see qmm_large_kernel)
   const bool a_on = wave < mb_act;
@@ -1144,7 +1152,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
   {
     const int r = 16 * wave + (lane & 15);
     const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
-    arow_ptr = reinterpret_cast<const char*>(a.act16 + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
+    arow_ptr = reinterpret_cast<const char*>(act16 + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
                16 * lg_chunk<FMT_INT4>(0, lane >> 4);
   }
   const uint32_t lds_base = lds_offset(lds);
@@ -1283,7 +1291,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       if (mr >= m_cnt) continue;
       const int64_t ar2 = act_row(a, m0 + mr);
       const bool ok = ar2 >= 0;
-      const float rs = ok ? a.row_sinv[ar2] : 1.0f;
+      const float rs = ok ? row_sinv[ar2] : 1.0f;
       // undo both power-of-two scalings (activation row, weight row): exact
       auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {
@@ -1752,12 +1760,16 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (mtile_bound > 65535) return fail("qmm: too many m-tiles for one launch");
   if (a.expert_map && regime != QMOE_REGIME_SMALL)
     return fail("qmm: an expert map needs the small regime");
-  if (a.act_hi) {
-    if (regime != QMOE_REGIME_SMALL || !fmt_quant(fmt) || epi == EPI_SWIGLU || a.slot_of)
-      return fail("qmm: a second activation needs quantized weights, the small regime, a "
-                  "non-SwiGLU epilogue and rows by sorted position");
+  const bool two_acts = (regime == QMOE_REGIME_SMALL) ? a.act_hi != nullptr : a.act16_hi != nullptr;
+  if (two_acts) {
+    if (!fmt_quant(fmt) || epi == EPI_SWIGLU || a.slot_of)
+      return fail("qmm: a second activation needs quantized weights, a non-SwiGLU epilogue and "
+                  "rows by sorted position");
     if (a.split_tile <= 0 || a.split_tile % 4 || a.split_tile >= a.n_rows / 16)
       return fail("qmm: split_tile must be a positive multiple of 4 inside the weight tiles");
+    if (regime != QMOE_REGIME_SMALL && (fmt != FMT_INT4 || !a.row_sinv_hi || a.split_tile % 16))
+      return fail("qmm(large): a second activation needs int4 weights, its row scales and "
+                  "split_tile % 16 == 0");
   }
   if (regime == QMOE_REGIME_SMALL) {
     if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int3/int4/int6 need K % 128 == 0");
@@ -1820,8 +1832,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       return fail("qmm(large): int4 weights need their row exponents (qmoe_row_exponents)");
     int rc;
 #define QMOE_LARGE(F, P) rc = launch_large<F, P>(a, mtile_bound, stream)
-    // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves) take the wide kernel
-    if (fmt == FMT_INT4 && a.n_rows % 512 == 0) {
+    // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves; a second activation:
+    // blocks on one side of its split) take the wide kernel
+    if (fmt == FMT_INT4 && a.n_rows % 512 == 0 && (!two_acts || a.split_tile % 32 == 0)) {
       if (epi == EPI_SWIGLU) rc = launch_wide<EPI_SWIGLU>(a, mtile_bound, stream);
       else if (epi == EPI_BF16) rc = launch_wide<EPI_BF16>(a, mtile_bound, stream);
       else rc = launch_wide<EPI_F32>(a, mtile_bound, stream);

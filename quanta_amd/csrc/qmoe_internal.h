@@ -218,7 +218,10 @@ struct QmmArgs {
   const uint16_t* act_hi;     // small quantized regime, nullable: the activation rows of the
                               // weight tiles from split_tile on (AWQ: the up half of gate_up
                               // reads rows prescaled for the up projection)
-  int split_tile;             // first 16-row tile that reads act_hi (a multiple of 4)
+  int split_tile;             // first 16-row tile that reads act_hi (a multiple of 4; large
+                              // regime: of 16, of 32 for the 512-row kernel)
+  const uint16_t* act16_hi;   // large int4 regime, nullable: act16 and row_sinv of act_hi, read
+  const float* row_sinv_hi;   // by the weight-row blocks from split_tile on
   const int32_t* expert_map;  // small regime, nullable: expert -> its slot in this launch's
                               // weight stack, -1 when it is not in the stack (its m-tiles exit)
   const int8_t* row_exp;      // large int4 regime, nullable: per weight row [n_experts][n_rows]
@@ -341,6 +344,14 @@ int launch_combine(const uint16_t* d, const int32_t* inv, const float* w, int N,
 int launch_awq_prescale(const uint16_t* x, const int32_t* sorted, const int32_t* offsets, int E,
                         int k, int64_t mc, int H, const uint16_t* s_gu, uint16_t* xg, uint16_t* xu,
                         hipStream_t stream);
+// The same quotients for the hybrid regime, in one pass: rows of experts with at most split_rows
+// rows as bf16 into xgu [2][mc][H] (gate rows, then up rows), the others only as fp16 copies
+// x16 [2][mc][H] with row scales x_sinv [2][mc] (launch_act_to_f16's conversion). H <= 8192.
+constexpr int kAwqSplitMaxH = 8192;
+int launch_awq_prescale_split(const uint16_t* x, const int32_t* sorted, const int32_t* offsets,
+                              int E, int k, int64_t mc, int H, const uint16_t* s_gu,
+                              int split_rows, uint16_t* xgu, uint16_t* x16, float* x_sinv,
+                              hipStream_t stream);
 // h[m] = bf16(glu(g, u) / s_dn[e]) over gu [mc][2I] (gate | up, bf16) with s_dn bf16 [E][I];
 // s_dn NULL: h[m] = bf16(glu(g, u)) (offsets unused).
 int launch_awq_glu(const uint16_t* gu, const int32_t* offsets, int E, int64_t mc, int I,

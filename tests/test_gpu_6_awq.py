@@ -4,9 +4,13 @@ The block divides each routed row's activation by its expert's per-input-channel
 the gate, the up and the down projection (qmoe_config_t.awq; kernels in awq.hip; gate_up as one
 launch whose up-half wavefronts read the rows prescaled for the up projection).
 
-Bars: unit scales give the plain path's output bit for bit (same per-output arithmetic); random
-scales within the BASELINE gates of the oracle (max-abs 2e-2 scaled, relative L2 5e-3) at every
-batch regime the AWQ path uses; batch invariance bit for bit.
+Above 256 tokens int4 layers whose intermediate size is a multiple of 256 take the large
+regime: the hot experts' gate_up on the prefill (MFMA) kernels, each 256- or 512-row weight
+block reading the fp16 copy of the gate's or the up projection's prescaled rows.
+
+Bars: unit scales give the plain path's output bit for bit in both regimes (same per-output
+arithmetic); random scales within the BASELINE gates of the oracle (max-abs 2e-2 scaled,
+relative L2 5e-3) at every batch regime the AWQ path uses; batch invariance bit for bit.
 """
 
 from __future__ import annotations
@@ -26,8 +30,8 @@ pytestmark = pytest.mark.gpu
 LIMIT = 2.0   # DeepSeek-V4's clamped SwiGLU, small enough to bind on part of the values
 
 
-def _cfg(**kw):
-    return MoEConfig(512, 8, 2, 256, 256, scoring_func="sigmoid", norm_topk_prob=True,
+def _cfg(E=8, I=256, H=512, **kw):
+    return MoEConfig(H, E, 2, I, 256, scoring_func="sigmoid", norm_topk_prob=True,
                      routed_scaling_factor=1.5, hidden_act="silu", swiglu_limit=LIMIT, **kw)
 
 
@@ -44,17 +48,48 @@ def _with_awq(p, dev, seed, E=8, H=512, I=256, unit=False):
     return q
 
 
-@pytest.mark.parametrize("N", [1, 8, 40, 300])
-def test_awq_unit_scales_equal_plain_path(gpu, N):
+@pytest.mark.parametrize("N,regime,E,I", [(1, L.REGIME_SMALL, 8, 256), (8, L.REGIME_SMALL, 8, 256),
+                                          (40, L.REGIME_SMALL, 8, 256),
+                                          (300, L.REGIME_SMALL, 8, 256),
+                                          (300, L.REGIME_LARGE, 32, 256),
+                                          (700, L.REGIME_LARGE, 32, 512)])
+def test_awq_unit_scales_equal_plain_path(gpu, N, regime, E, I):
     """All-ones scales: prescaling is exact and the gated activation divides by one, so the
     bf16-epilogue gate_up launch plus the AWQ activation pass reproduce the fused SwiGLU launch
-    bit for bit (the K chunks and their order depend on the shape only)."""
-    cfg = _cfg()
-    p = _layer(gpu, 64, seed=3 * N, gated=False)
+    bit for bit (the K chunks and their order depend on the shape only; in the large regime the
+    prefill kernels sum each output in the same order under either epilogue, and the fp16 copy
+    of a prescaled row equals that of its token's row)."""
+    cfg = _cfg(E, I)
+    p = _layer(gpu, 64, seed=3 * N, E=E, I=I, gated=False)
     x = _inputs(gpu, N, 512, N)
-    y_plain = qwen35_moe(x[None], p, cfg, regime=L.REGIME_SMALL)[0]
-    y_awq = qwen35_moe(x[None], _with_awq(p, gpu, N, unit=True), cfg)[0]
+    y_plain = qwen35_moe(x[None], p, cfg, regime=regime)[0]
+    y_awq = qwen35_moe(x[None], _with_awq(p, gpu, N, E=E, I=I, unit=True), cfg, regime=regime)[0]
     assert torch.equal(y_awq, y_plain)
+
+
+@pytest.mark.parametrize("E,I,N,H", [(32, 256, 300, 512), (32, 512, 300, 512),
+                                     (8, 512, 1100, 512), (32, 256, 300, 8704)])
+def test_awq_large_regime_vs_oracle(gpu, E, I, N, H):
+    """AWQ int4 layers above 256 tokens: hot experts (more than 16 rows) on the prefill kernels,
+    the rest on the decode kernel beside them. I = 256 splits gate and up between 256-row blocks
+    (the 256-row kernel), I = 512 between 512-row blocks (the 512-row kernel); E = 32 at 300
+    tokens leaves both hot and cold experts. The prescaled rows come from one pass that writes
+    hot rows as fp16 copies and cold rows as bf16 (H <= 8192), or above that from the bf16 pass
+    and a separate fp16 conversion (H = 8704)."""
+    cfg = _cfg(E, I, H)
+    base = _layer(gpu, 64, seed=41 * N + I, H=H, E=E, I=I, gated=False)
+    base.pop("shared_expert_gate", None)
+    p = _with_awq(base, gpu, seed=43 * N + I, E=E, H=H, I=I)
+    # (inputs scaled so the router logits keep H = 512's spread: at H = 8704 and scale 4 the
+    # sigmoid scores of several experts round to 1.0 in fp32 and tie, unlike the fp64 oracle's)
+    x = _inputs(gpu, N, H, N, scale=4.0 * (512 / H) ** 0.5)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=2, inter=I, scoring="sigmoid",
+                           norm_topk=True, scale=1.5, act="silu", limit=LIMIT, group_size=64)
+    counts = np.bincount(it["idx"].reshape(-1), minlength=E)
+    if E == 32:
+        assert counts.max() > 16 and counts.min() <= 16, "the layer must hold hot and cold experts"
+    assert_close(f64(y), it["y_exact"], f"awq large regime E={E} I={I} N={N} H={H}")
 
 
 @pytest.mark.parametrize("gs,gu_bits,dn_bits", [(64, 4, 4), (128, 4, 4), (128, 3, 4)])
@@ -114,5 +149,8 @@ def test_awq_argument_errors(gpu):
     bad = dict(q, experts_down=dict(q["experts_down"], awq_scale=q["experts_down"]["awq_scale"][:, :128]))
     with pytest.raises(ValueError, match="awq_scale must be"):
         qwen35_moe(x[None], bad, cfg)
-    with pytest.raises(ValueError, match="small regime only"):
-        qwen35_moe(x[None], q, cfg, regime=L.REGIME_LARGE)
+    # the large regime needs gate and up halves of whole 256-row blocks
+    p128 = _layer(gpu, 64, seed=1, I=128, gated=False)
+    with pytest.raises(ValueError, match="inter % 256 == 0"):
+        qwen35_moe(x[None], _with_awq(p128, gpu, seed=2, I=128), _cfg(I=128),
+                   regime=L.REGIME_LARGE)
