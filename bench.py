@@ -16,8 +16,8 @@ on the launch stream), a sweep over the other decode batches and the 4096-token 
 widened rows at the headline batch (`--extra`: the block with the decoder layer's RMSNorm and
 residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, and with
 Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies; and with
-DeepSeek-V4's activation-aware expert scales on the int4 experts; with Kimi's widths drawn per
-(expert, projection)), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
+DeepSeek-V4's activation-aware expert scales on the int4 experts, also at the c4 prefill; with
+Kimi's widths drawn per (expert, projection)), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
 cores, bounded sample).
 
 `roofline.traffic` (measured HBM bytes per launch of the dominant kernel) comes from
@@ -455,6 +455,19 @@ def main():
             m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), lays=lays_a)
             record(f"{args.config}-N{N}-awq", m2, u2,
                    per_expert_bytes=(2 * H + cfg.moe_intermediate_size) * 2)
+            if args.prefill > 0:
+                # the same scaled layers at the c4 prefill (Zipf routing): the large regime, the
+                # hot experts' gate_up on the prefill kernel reading fp16 copies of the prescaled
+                # rows; FLOPs as the plain prefill line (the AWQ passes are elementwise)
+                n3 = args.prefill
+                m3, _, _, _ = run_batch(n3, max(20, args.steps // 20), 3, min(args.pool, 8),
+                                        zipf=True, lays=lays_a)
+                f3 = synth.algorithmic_flops(cfg, n3)
+                rec = dict(workload=f"c4-prefill-N{n3}-zipf-awq", N=n3, ms_per_step=round(m3, 5),
+                           tokens_per_s=round(n3 / (m3 / 1e3), 1), tflops=round(f3 / m3 / 1e9, 2),
+                           mfma_frac=round(f3 / m3 / 1e9 / BF16_PEAK_TFLOPS, 4))
+                sweep.append(rec)
+                log(f"sweep {rec}")
             del lays_a
 
     # ------------------------------------------------------------------ measured copy peak
