@@ -58,7 +58,8 @@ extern "C" {
 #define QMOE_FMT_INT4_G64 0
 #define QMOE_FMT_BF16 1
 #define QMOE_FMT_INT6_G64 2 /* affine int6 codes, bf16 scale/bias per 64 (MiniMax M3 experts,
-                               src/quanta/minimax/model_m3.py:414-450); small regime only */
+                               src/quanta/minimax/model_m3.py:414-450); the large regime needs
+                               row exponents, as int4 */
 #define QMOE_FMT_INT3_G64 3 /* affine int3 codes, bf16 scale/bias per 64 (Kimi's int3 gate/up
                                stacks, src/quanta/modeling/quantized.py:1-84); small regime only */
 #define QMOE_FMT_INT8_G64 4 /* affine int8 codes, bf16 scale/bias per 64: the shared expert as the

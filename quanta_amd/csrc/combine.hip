@@ -455,9 +455,15 @@ static bool awq_large_ok(const qmoe_config_t& c) {
          c.inter % 256 == 0;
 }
 
+// int3 codes: no large-regime kernel (the prefill kernels stage int4 or int6 superblocks)
 static bool narrow_codes(const qmoe_config_t& c) {
-  return c.expert_format == QMOE_FMT_INT6_G64 || c.expert_format == QMOE_FMT_INT3_G64 ||
-         c.down_format == QMOE_FMT_INT6_G64 || c.down_format == QMOE_FMT_INT3_G64;
+  return c.expert_format == QMOE_FMT_INT3_G64 || c.down_format == QMOE_FMT_INT3_G64;
+}
+
+// formats the large-regime kernels dequantize to fp16 (an fp16 activation copy, row exponents)
+static bool fp16_large_fmt(int kfmt) { return kfmt == FMT_INT4 || kfmt == FMT_INT6; }
+static bool fp16_large_fmt_q(int qfmt) {
+  return qfmt == QMOE_FMT_INT4_G64 || qfmt == QMOE_FMT_INT6_G64;
 }
 
 static bool has_split(const qmoe_mixed_t& m) {
@@ -504,7 +510,7 @@ static int validate_config(const qmoe_config_t& c) {
   if ((c.expert_format == QMOE_FMT_BF16) != (c.down_format == QMOE_FMT_BF16))
     return fail("config: gate_up and down must both be quantized or both bf16");
   if (narrow_codes(c) && c.regime == QMOE_REGIME_LARGE)
-    return fail("config: int3/int6 experts run in the small regime only");
+    return fail("config: int3 experts run in the small regime only");
   if (c.awq != 0 && c.awq != 1) return fail("config: awq must be 0 or 1");
   if (c.awq && c.expert_format == QMOE_FMT_BF16)
     return fail("config: awq scales need quantized experts");
@@ -543,7 +549,7 @@ extern "C" int qmoe_combine(const uint16_t* d, const int32_t* inv, const float* 
 extern "C" size_t qmoe_grouped_qmm_workspace(int64_t act_rows, int K, int weight_format,
                                              int regime) {
   if (act_rows <= 0 || K <= 0) return 0;
-  if (regime == QMOE_REGIME_LARGE && weight_format == QMOE_FMT_INT4_G64)
+  if (regime == QMOE_REGIME_LARGE && fp16_large_fmt_q(weight_format))
     return act16_ws_bytes(act_rows, K);
   return 0;
 }
@@ -568,7 +574,7 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
   if (regime != QMOE_REGIME_SMALL && regime != QMOE_REGIME_LARGE)
     return fail("qmoe_grouped_qmm: regime must be small (1) or large (2)");
   if (slot_of && slot_div <= 0) return fail("qmoe_grouped_qmm: slot_div must be positive");
-  if (regime == QMOE_REGIME_LARGE && weight_format == QMOE_FMT_INT4_G64 && !row_exp)
+  if (regime == QMOE_REGIME_LARGE && fp16_large_fmt_q(weight_format) && !row_exp)
     return fail("qmoe_grouped_qmm: int4 weights in the large regime need row_exp (qmoe_row_exponents)");
   const int out_cols = (epilogue == QMOE_EPI_SWIGLU) ? n_rows / 2 : n_rows;
   if (ld_out < out_cols) return fail("qmoe_grouped_qmm: ld_out too small");
@@ -587,7 +593,7 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
   a.n_rows = n_rows;
   a.codes = codes;
   a.sb = sb;
-  a.row_exp = (weight_format == QMOE_FMT_INT4_G64) ? row_exp : nullptr;
+  a.row_exp = fp16_large_fmt_q(weight_format) ? row_exp : nullptr;
   a.out = out;
   a.ld_out = ld_out;
   a.glu = glu;
@@ -603,7 +609,7 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
     bound = (dense_rows + m_tile - 1) / m_tile;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (regime == QMOE_REGIME_LARGE && weight_format == QMOE_FMT_INT4_G64) {
+  if (regime == QMOE_REGIME_LARGE && fp16_large_fmt_q(weight_format)) {
     const size_t need = act16_ws_bytes(act_rows, K);
     if (!ws || ws_bytes < need) return fail("qmoe_grouped_qmm: workspace too small for the fp16 copy");
     uint16_t* act16 = static_cast<uint16_t*>(ws);
@@ -665,10 +671,10 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
   if (c.awq && (!wts->awq_gu || !wts->awq_dn)) return fail("qmoe_forward: awq needs awq_gu and awq_dn");
   if (pick_regime(c, N) == QMOE_REGIME_LARGE &&
-      ((kernel_fmt(c.expert_format) == FMT_INT4 && !wts->gu_rexp) ||
-       (kernel_fmt(c.down_format) == FMT_INT4 && !wts->dn_rexp)))
-    return fail("qmoe_forward: int4 experts in the large regime (N > 256) need gu_rexp and dn_rexp "
-                "(qmoe_row_exponents)");
+      ((fp16_large_fmt(kernel_fmt(c.expert_format)) && !wts->gu_rexp) ||
+       (fp16_large_fmt(kernel_fmt(c.down_format)) && !wts->dn_rexp)))
+    return fail("qmoe_forward: int4/int6 experts in the large regime (N > 256) need gu_rexp and "
+                "dn_rexp (qmoe_row_exponents)");
 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* base = static_cast<char*>(ws);
@@ -758,8 +764,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // first on the auxiliary stream, beside the routing chain (hybrid implies int4 or bf16 experts;
   // AWQ: copies of the prescaled rows instead, made after the permute), and their down an fp16
   // copy of h
-  const bool f16_acts = (hybrid && gfmt == FMT_INT4 && !c.awq);
-  const bool f16_h = (hybrid && dfmt == FMT_INT4);
+  const bool f16_acts = (hybrid && fp16_large_fmt(gfmt) && !c.awq);
+  const bool f16_h = (hybrid && fp16_large_fmt(dfmt));
   if (f16_acts) {
     rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, aux ? aux->s : stream);
     if (rc) return rc;
@@ -955,7 +961,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
-    a.row_exp = (gfmt == FMT_INT4) ? wts->gu_rexp : nullptr;
+    a.row_exp = fp16_large_fmt(gfmt) ? wts->gu_rexp : nullptr;
     a.out = gu; a.ld_out = 2 * c.inter;
     if (hybrid) { a.act16_hi = x16 + mc * c.hidden; a.row_sinv_hi = x_sinv + mc; }
     rc = routed(a, gfmt, EPI_BF16, x16, x_sinv);
@@ -972,7 +978,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = wts->gu_codes; a.sb = wts->gu_sb;
-    a.row_exp = (gfmt == FMT_INT4) ? wts->gu_rexp : nullptr;
+    a.row_exp = fp16_large_fmt(gfmt) ? wts->gu_rexp : nullptr;
     a.out = h; a.ld_out = c.inter;
     a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
     if (f16_acts && aux) {   // the fp16 copy of x, made on the auxiliary stream at the fork
@@ -1029,7 +1035,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.act = h; a.act_rows = mc; a.slot_div = 1; a.n_slots = mc;
     a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
     a.K = c.inter; a.n_rows = c.hidden; a.codes = wts->dn_codes; a.sb = wts->dn_sb;
-    a.row_exp = (dfmt == FMT_INT4) ? wts->dn_rexp : nullptr;
+    a.row_exp = fp16_large_fmt(dfmt) ? wts->dn_rexp : nullptr;
     a.out = d; a.ld_out = c.hidden;
     if (f16_h) {
       rc = launch_act_to_f16(h, mc, c.inter, h16, h_sinv, stream);

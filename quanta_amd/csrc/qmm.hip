@@ -832,9 +832,18 @@ __device__ __forceinline__ void lg_barrier() {
 }
 
 // bf16-weight superblock registers of a wavefront: 2 tiles x 4 steps of B fragments.
-struct LgStageBf {
+// Weight data a wavefront holds in registers one superblock ahead: bf16, the B fragments of its
+// two tiles; int6, the tiles' high-bit words (one per 64-column group); int4, none.
+template <int FMT>
+struct LgStage {
   u32x4 q[2][4];
 };
+template <>
+struct LgStage<FMT_INT6> {
+  u32x2 h[2];
+};
+template <>
+struct LgStage<FMT_INT4> {};
 
 // int4 -> fp16 dequant of the prefill kernels, one packed register (two weights) per VALU FMA.
 // A code nibble masked in place is an fp16 subnormal: at bits 0-3 of a half it reads q * 2^-24,
@@ -863,8 +872,24 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int j, const DeqSb& d) 
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, (j & 1) ? d.s_hi : d.s_lo, d.b));
 }
 
+// int6 pair j (0..3) of step half h: the nibble pair of word w as deq_pair's, with its two high
+// bits from the group's high-bit word hw (bits 2j + 8h and 16 + 2j + 8h, as unpack_q128_6) moved
+// to bits 4-5, so each half holds the 6-bit code q at bits 0-5: the fp16 subnormal q * 2^-24.
+// row_exp bounds s * 2^row_exp below 2^15 / 63, so s * 2^(e+24) stays below 2^19 / 63.
+__device__ __forceinline__ uint32_t deq_pair6(uint32_t w, uint32_t hw, int h, int j, const DeqSb& d) {
+  const int hs = 2 * j + 8 * h - 4;   // high bits to bits 4-5: a right shift by hs (left if < 0)
+  const uint32_t hb = (hs >= 0) ? (hw >> hs) : (hw << -hs);
+  const uint32_t v = ((w >> (4 * j)) & 0x000F000Fu) | (hb & 0x00300030u);
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, v), d.s_lo, d.b));
+}
+
 template <int FMT, int EPI>
 __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
+  // QF: int4 or int6 codes, dequantized to fp16 (int6: the nibble plane staged as int4's, the
+  // high-bit words in registers one superblock ahead)
+  constexpr bool QF = (FMT == FMT_INT4 || FMT == FMT_INT6);
+  constexpr int SBB = (FMT == FMT_INT6) ? 1536 : 1024;   // bytes of a tile superblock
   extern __shared__ u32x4 lds[];
   char* lds_c = reinterpret_cast<char*>(lds);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -885,7 +910,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const int mrows = (a.dense_mtile > 0 && !a.offsets && !a.tile_map) ? a.dense_mtile : kLargeMTile;
   if (mt >= a.mtiles || !resolve_mtile(a, mt, mrows, e, m0, m_cnt)) return;
   // (AWQ: the 256-row blocks from split_tile on read the second activation copy)
-  const bool hi = (FMT == FMT_INT4) && a.act16_hi && 16 * cb >= a.split_tile;
+  const bool hi = (QF) && a.act16_hi && 16 * cb >= a.split_tile;
   const uint16_t* act16 = hi ? a.act16_hi : a.act16;
   const float* row_sinv = hi ? a.row_sinv_hi : a.row_sinv;
   const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
@@ -901,9 +926,9 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   {
     const int r = 16 * wave + (lane & 15);
     const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
-    const uint16_t* abase = (FMT == FMT_INT4) ? act16 : a.act;
+    const uint16_t* abase = (QF) ? act16 : a.act;
     arow_ptr = reinterpret_cast<const char*>(abase + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
-               16 * lg_chunk<FMT>(0, lane >> 4);
+               16 * lg_chunk<QF ? FMT_INT4 : FMT>(0, lane >> 4);
   }
   const uint32_t lds_base = lds_offset(lds);
   auto a_slot = [&](int p) { return (p % kLgNBuf) * kLgABytes; };
@@ -911,26 +936,28 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
 
   // ---- this wavefront's two weight tiles
   const char* wcode[2];
+  const char* whi[2];    // int6: the lane's 8 bytes of the tile's high-bit plane
   const char* wsb[2];
   const u32x4* wp[2];
-  int rex[2] = {0, 0};   // int4: the lane's weight row of each tile, its dequant exponent e
+  int rex[2] = {0, 0};   // int4/int6: the lane's weight row of each tile, its dequant exponent e
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int tl = (EPI == EPI_SWIGLU) ? (t == 0 ? 8 * cb + wave : a.n_rows / 32 + 8 * cb + wave)
                                        : 16 * cb + 2 * wave + t;
-    if (FMT == FMT_INT4) {
+    if (QF) {
       const int64_t tb = (ebase + tl) * nsb;
-      wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
+      wcode[t] = static_cast<const char*>(a.codes) + tb * SBB + lane * 16;
+      whi[t] = static_cast<const char*>(a.codes) + tb * SBB + 1024 + lane * 8;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
       rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - kDeqShift;
     } else {
-      wcode[t] = wsb[t] = nullptr;
+      wcode[t] = whi[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
     }
   }
   // scale/bias copy: lanes 0-31 take tile 0's 128 B, lanes 32-63 tile 1's, 4 B each
-  const char* sb_src = (FMT == FMT_INT4) ? wsb[lane >> 5] + 4 * (lane & 31) : nullptr;
+  const char* sb_src = (QF) ? wsb[lane >> 5] + 4 * (lane & 31) : nullptr;
 
   // issue all loads of superblock p (A: 4 instructions when a_on; int4 weights: 3)
   auto issue = [&](int p) __attribute__((always_inline)) {
@@ -939,14 +966,14 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       const uint32_t dst = lds_base + a_slot(p) + wave * 4 * 1024;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int off = 16 * ((FMT == FMT_INT4) ? 8 * (s >> 1) + (s & 1) : 4 * s);
+        const int off = 16 * ((QF) ? 8 * (s >> 1) + (s & 1) : 4 * s);
         dma16(src + off, dst + s * 1024);
       }
     }
-    if (FMT == FMT_INT4) {
+    if (QF) {
       const uint32_t dst = lds_base + b_slot(p);
-      dma16(wcode[0] + static_cast<int64_t>(p) * 1024, dst);
-      dma16(wcode[1] + static_cast<int64_t>(p) * 1024, dst + 1024);
+      dma16(wcode[0] + static_cast<int64_t>(p) * SBB, dst);
+      dma16(wcode[1] + static_cast<int64_t>(p) * SBB, dst + 1024);
       dma4(sb_src + static_cast<int64_t>(p) * 128, dst + 2048);
     }
   };
@@ -962,13 +989,13 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // 1/MB of step s+1's weight dequant, and a scheduling barrier keeps that order, so LDS reads
   // have a full step to land and the dequant VALU work is spread between the MFMAs.
   // (int4 dequant: deq_sb / deq_pair)
-  auto compute = [&](int p, const LgStageBf& gb, auto mbc) __attribute__((always_inline)) {
+  auto compute = [&](int p, const LgStage<FMT>& gb, auto mbc) __attribute__((always_inline)) {
     constexpr int MB = decltype(mbc)::value;
     constexpr int UPS = 8 / MB;                 // dequant units (nibble pairs) per slot
     const u32x4* la = reinterpret_cast<const u32x4*>(lds_c + a_slot(p)) + lane;
     u32x4 q[2];
     uint2 sbv[2];
-    if (FMT == FMT_INT4) {
+    if (QF) {
       const char* lb = lds_c + b_slot(p);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -985,14 +1012,16 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
     // dequant unit u (0..7) of step s: tile u/4, nibble pair u%4 -> one packed fp16 register
     auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
       const int t = u >> 2, j = u & 3;
-      if (FMT == FMT_INT4) {
+      if constexpr (FMT == FMT_INT6) {
+        bfo[t][j] = deq_pair6(q[t][s], (s >> 1) ? gb.h[t].y : gb.h[t].x, s & 1, j, dsb[t]);
+      } else if constexpr (FMT == FMT_INT4) {
         bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
       } else if (j == 0) {
         bfo[t] = gb.q[t][s];
       }
     };
     u32x4 bf[2][2], A[2][MB];
-    if (FMT == FMT_INT4) sb_conv(0);
+    if (QF) sb_conv(0);
 #pragma unroll
     for (int u = 0; u < 8; ++u) deq_unit(0, u, bf[0]);
 #pragma unroll
@@ -1000,12 +1029,12 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int c = s & 1;
-      if (FMT == FMT_INT4 && s == 1) sb_conv(1);      // group 1 feeds steps 2 and 3
+      if (QF && s == 1) sb_conv(1);      // group 1 feeds steps 2 and 3
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          acc[i][t] = (FMT == FMT_INT4) ? mfma16_f16(A[c][i], bf[c][t], acc[i][t])
+          acc[i][t] = (QF) ? mfma16_f16(A[c][i], bf[c][t], acc[i][t])
                                         : mfma16(as_bf16x8(A[c][i]), as_bf16x8(bf[c][t]), acc[i][t]);
         if (s < 3) {
           A[c ^ 1][i] = la[256 * i + 64 * (s + 1)];
@@ -1018,9 +1047,13 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   };
 
   // bf16 weights: registers, one superblock ahead
-  LgStageBf gbf[2];
-  auto load_bf = [&](int p, LgStageBf& g) __attribute__((always_inline)) {
-    if (FMT == FMT_BF16) {
+  LgStage<FMT> gbf[2];
+  auto load_bf = [&](int p, LgStage<FMT>& g) __attribute__((always_inline)) {
+    if constexpr (FMT == FMT_INT6) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        g.h[t] = *reinterpret_cast<const u32x2*>(whi[t] + static_cast<int64_t>(p) * SBB);
+    } else if constexpr (FMT == FMT_BF16) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1031,7 +1064,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // Loads in flight per wavefront and superblock: NA (A, when a_on) + NB (int4 weights).
   // Before the barrier that publishes superblock p+1, a wavefront waits until only the loads
   // of p+2 remain outstanding.
-  constexpr int NB = (FMT == FMT_INT4) ? 3 : 0;
+  constexpr int NB = (QF) ? 3 : 0;
   auto run = [&](auto mbc) __attribute__((always_inline)) {
     auto wait_next = [&](bool far) __attribute__((always_inline)) {
       // loads of the superblock after the next one, if issued, may stay in flight
@@ -1041,15 +1074,19 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
         if (far) wait_vmcnt<NB>(); else wait_vmcnt<0>();
       }
     };
+    if (FMT == FMT_INT6) load_bf(0, gbf[0]);
     issue(0);
     if (nsb > 1) issue(1);
-    load_bf(0, gbf[0]);
+    if (FMT != FMT_INT6) load_bf(0, gbf[0]);
     wait_next(nsb > 1);
     lg_barrier();
-    auto iter = [&](int p, const LgStageBf& cur, LgStageBf& nxt) __attribute__((always_inline)) {
+    auto iter = [&](int p, const LgStage<FMT>& cur, LgStage<FMT>& nxt) __attribute__((always_inline)) {
       const bool far = p + 2 < nsb;
+      // (int6: the high-bit words of p+1 ahead of the loads of p+2, so the wait below, which
+      // leaves only the latter in flight, covers them)
+      if (FMT == FMT_INT6) load_bf(p + 1, nxt);
       if (far) issue(p + 2);
-      load_bf(p + 1, nxt);
+      if (FMT != FMT_INT6) load_bf(p + 1, nxt);
       compute(p, cur, mbc);
       wait_next(far);
       lg_barrier();
@@ -1081,7 +1118,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       // rows whose activation row is invalid read as zeros (their A data was row 0's)
       const int64_t ar2 = act_row(a, m0 + mr);
       const bool ok = ar2 >= 0;
-      const float rs = (FMT == FMT_INT4 && ok) ? row_sinv[ar2] : 1.0f;
+      const float rs = (QF && ok) ? row_sinv[ar2] : 1.0f;
       // undo both power-of-two scalings (activation row, int4 weight row): exact
       auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {
@@ -1767,8 +1804,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
                   "rows by sorted position");
     if (a.split_tile <= 0 || a.split_tile % 4 || a.split_tile >= a.n_rows / 16)
       return fail("qmm: split_tile must be a positive multiple of 4 inside the weight tiles");
-    if (regime != QMOE_REGIME_SMALL && (fmt != FMT_INT4 || !a.row_sinv_hi || a.split_tile % 16))
-      return fail("qmm(large): a second activation needs int4 weights, its row scales and "
+    if (regime != QMOE_REGIME_SMALL &&
+        ((fmt != FMT_INT4 && fmt != FMT_INT6) || !a.row_sinv_hi || a.split_tile % 16))
+      return fail("qmm(large): a second activation needs int4/int6 weights, its row scales and "
                   "split_tile % 16 == 0");
   }
   if (regime == QMOE_REGIME_SMALL) {
@@ -1815,9 +1853,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     }
 #undef QMOE_SMALL
   } else {
-    if (fmt == FMT_INT6 || fmt == FMT_INT3)
-      return fail("qmm(large): int3/int6 weights run in the small regime only (the large kernels "
-                  "stage int4 tile superblocks)");
+    if (fmt == FMT_INT3)
+      return fail("qmm(large): int3 weights run in the small regime only (the large kernels "
+                  "stage int4 or int6 tile superblocks)");
     if (fmt == FMT_INT8)
       return fail("qmm(large): int8 weights run in the small regime only (expand them to bf16 "
                   "for the large kernels)");
@@ -1826,10 +1864,11 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
                           a.dense_mtile > kLargeMTile || fmt != FMT_BF16))
       return fail("qmm(large): dense_mtile is a multiple of 16 up to 128, for one dense bf16 segment");
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
-    if (fmt == FMT_INT4 && (!a.act16 || !a.row_sinv))
-      return fail("qmm(large): int4 weights need the fp16 activation copy");
-    if (fmt == FMT_INT4 && !a.row_exp)
-      return fail("qmm(large): int4 weights need their row exponents (qmoe_row_exponents)");
+    const bool qf = (fmt == FMT_INT4 || fmt == FMT_INT6);
+    if (qf && (!a.act16 || !a.row_sinv))
+      return fail("qmm(large): int4/int6 weights need the fp16 activation copy");
+    if (qf && !a.row_exp)
+      return fail("qmm(large): int4/int6 weights need their row exponents (qmoe_row_exponents)");
     int rc;
 #define QMOE_LARGE(F, P) rc = launch_large<F, P>(a, mtile_bound, stream)
     // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves; a second activation:
@@ -1842,6 +1881,10 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT4, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT4, EPI_BF16);
       else QMOE_LARGE(FMT_INT4, EPI_F32);
+    } else if (fmt == FMT_INT6) {   // (1.5 KiB superblocks: the 256-row kernel only)
+      if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT6, EPI_SWIGLU);
+      else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT6, EPI_BF16);
+      else QMOE_LARGE(FMT_INT6, EPI_F32);
     } else {
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_BF16, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_BF16, EPI_BF16);

@@ -145,32 +145,46 @@ def test_dequant_int6_bit_exact(gpu, gs):
     assert np.array_equal(bits_np(got), oq.dequant_bf16_bits(words, s, b, K, bits=6, group_size=gs))
 
 
+@pytest.mark.parametrize("regime", [L.REGIME_SMALL, L.REGIME_LARGE])
 @pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
 @pytest.mark.parametrize("N,k,E,H,rows", [(1, 4, 8, 4096, 256), (7, 3, 6, 256, 256),
-                                          (200, 4, 4, 1024, 128), (1024, 4, 32, 256, 512)])
-def test_grouped_qmm_int6_vs_oracle(gpu, epi, N, k, E, H, rows):
-    """The decode kernel's int6 path (tiled nibble + high-bit planes) against the oracle's exact
-    affine weights, through several launch shapes (chunks per wavefront, tiles per wavefront)."""
+                                          (200, 4, 4, 1024, 128), (1024, 4, 32, 256, 512),
+                                          (300, 3, 5, 768, 768)])
+def test_grouped_qmm_int6_vs_oracle(gpu, regime, epi, N, k, E, H, rows):
+    """int6 (tiled nibble + high-bit planes) against the oracle's exact affine weights: the
+    decode kernel through several launch shapes (chunks per wavefront, tiles per wavefront), and
+    the 256-row prefill kernel (nibble plane staged in LDS as int4's, high-bit words in registers,
+    fp16 dequant under per-row exponents computed for 6-bit codes)."""
+    if regime == L.REGIME_LARGE and rows % 256:
+        pytest.skip("the large regime tiles 256 weight rows")
     rng = np.random.default_rng(N + E + H + rows)
     idx = np.stack([rng.permutation(E)[:k] for _ in range(N)]).astype(np.int32)
     x = oq.round_bf16(rng.standard_normal((N, H)))
     w = torch.from_numpy(rng.standard_normal((E, rows, H)).astype(np.float32) * 0.05).to(gpu)
     packed, s, b = quantize_affine(w, 6, group_size=64)
     dense = oq.dequant_exact(words_np(packed), bits_np(s), bits_np(b), H, bits=6)
+    m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
     counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(torch.from_numpy(idx).to(gpu), E,
-                                                                        L.SMALL_M_TILE)
+                                                                        m_tile)
     codes, sb = ops.tile_int6(packed, s, b)
+    rexp = None
+    if regime == L.REGIME_LARGE:
+        rexp = ops.row_exponents(s, b, bits=6)
+        # each row's largest dequantized magnitude (codes 0..63) times 2^rexp lies in [2^13, 2^14)
+        peak = np.abs(dense).max(axis=-1) * np.exp2(rexp.cpu().numpy().astype(np.float64))
+        assert np.all((peak >= 2.0 ** 13) & (peak < 2.0 ** 14))
     out = ops.grouped_qmm(bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu), K=H, n_rows=rows,
                           weight_format=L.FMT_INT6_G64, codes=codes, sb=sb, epilogue=epi,
-                          out_rows=N * k, regime=L.REGIME_SMALL, slot_of=sorted_slot, slot_div=k,
+                          out_rows=N * k, regime=regime, slot_of=sorted_slot, slot_div=k,
                           n_slots=N * k, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
-                          n_experts=E)
+                          n_experts=E, row_exp=rexp)
     order = sorted_slot.cpu().numpy()
     full = np.einsum("mh,moh->mo", x[order // k], dense[idx.reshape(-1)[order]])
     want = oq.round_bf16(full)
     if epi == L.EPI_SWIGLU:
         want = om.swiglu(want, rows // 2)
-    assert_close(f64(out), want, f"int6 qmm epi={epi} N={N} E={E} H={H} rows={rows}", rel_l2=4e-3)
+    assert_close(f64(out), want, f"int6 qmm regime={regime} epi={epi} N={N} E={E} H={H} rows={rows}",
+                 rel_l2=4e-3)
 
 
 def _layer6(dev, gs, seed, H=512, E=8, I=256, Is=256):
@@ -186,8 +200,8 @@ def _layer6(dev, gs, seed, H=512, E=8, I=256, Is=256):
 @pytest.mark.parametrize("N", [1, 8, 40, 300])
 def test_block_int6_vs_oracle(gpu, gs, act, N):
     """int6 experts through the block (MiniMax M3's combination is int6 + SwiGLU-OAI): slot-major,
-    fused shared expert, auxiliary-stream shared expert, and above 256 tokens the decode kernel
-    (int6 has no large-regime kernel)."""
+    fused shared expert, auxiliary-stream shared expert, and above 256 tokens the large regime
+    (the 256-row prefill kernel)."""
     limit = 1.5 if act == "swigluoai" else 0.0
     cfg = MoEConfig(512, 8, 2, 256, 256, hidden_act=act, swiglu_alpha=1.702, swiglu_limit=limit)
     p = _layer6(gpu, gs, seed=11 * N + gs)
@@ -195,12 +209,22 @@ def test_block_int6_vs_oracle(gpu, gs, act, N):
            gs=gs, bits=6)
 
 
-def test_int6_large_regime_refused(gpu):
-    cfg = MoEConfig(512, 8, 2, 256, 256)
-    p = _layer6(gpu, 64, seed=1)
-    x = _inputs(gpu, 300, 512, 1)
-    with pytest.raises(ValueError, match="int6"):
-        qwen35_moe(x[None], p, cfg, regime=L.REGIME_LARGE)
+@pytest.mark.parametrize("E,I,N", [(32, 256, 300), (8, 512, 1100)])
+def test_block_int6_large_regime_vs_oracle(gpu, E, I, N):
+    """int6 layers above 256 tokens: hot experts (more than 16 rows) on the 256-row prefill
+    kernel, the rest on the decode kernel (E = 32 at 300 tokens holds both); the large regime's
+    output against the oracle and against the decode kernel's."""
+    cfg = MoEConfig(512, E, 2, I, 256, hidden_act="swigluoai", swiglu_alpha=1.702,
+                    swiglu_limit=1.5)
+    p = _layer6(gpu, 64, seed=5 * N + I, E=E, I=I)
+    x = _inputs(gpu, N, 512, N)
+    y, it = _check(p, cfg, x, f"int6 large regime E={E} I={I} N={N}", act="swigluoai",
+                   limit=1.5, bits=6)
+    counts = np.bincount(it["idx"].reshape(-1), minlength=E)
+    if E == 32:
+        assert counts.max() > 16 and counts.min() <= 16, "the layer must hold hot and cold experts"
+    y_small = qwen35_moe(x[None], p, cfg, regime=L.REGIME_SMALL)[0]
+    assert_close(f64(y), f64(y_small), f"int6 large vs decode kernel E={E} N={N}")
 
 
 
@@ -259,8 +283,8 @@ def _layer_widths(dev, gs, seed, gu_bits, dn_bits, H=512, E=8, I=256, Is=256):
 def test_block_mixed_widths_vs_oracle(gpu, gs, gu_bits, dn_bits, N):
     """Per-projection widths through the block: Kimi's gate/up int3 + down int4 at group 128, int3
     throughout, and the other mixes of the decode kernel's formats. Slot-major, fused shared
-    expert, auxiliary-stream shared expert, and above 256 tokens the decode kernel (no narrow
-    format has a large-regime kernel, so the block keeps such layers on the decode kernel)."""
+    expert, auxiliary-stream shared expert, and above 256 tokens the large regime for int4/int6
+    mixes (the 256-row prefill kernel for int6) and the decode kernel for any int3 stack."""
     cfg = MoEConfig(512, 8, 2, 256, 256)
     p = _layer_widths(gpu, gs, 13 * N + gs + gu_bits, gu_bits, dn_bits)
     _check(p, cfg, _inputs(gpu, N, 512, N), f"gate_up int{gu_bits} down int{dn_bits} g{gs} N={N}",
@@ -271,7 +295,7 @@ def test_int3_large_regime_refused(gpu):
     cfg = MoEConfig(512, 8, 2, 256, 256)
     p = _layer_widths(gpu, 128, 1, 3, 4)
     x = _inputs(gpu, 300, 512, 1)
-    with pytest.raises(ValueError, match="int3|int6|narrow|large"):
+    with pytest.raises(ValueError, match="int3"):
         qwen35_moe(x[None], p, cfg, regime=L.REGIME_LARGE)
 
 
