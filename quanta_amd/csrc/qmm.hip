@@ -776,6 +776,9 @@ constexpr int kLgABytes = 8 * 4 * 64 * 16;                // one A slot: 32 KiB
 constexpr int kLgBWaveBytes = 2 * 1024 + 2 * 128;         // one wavefront's int4 weight slot
 constexpr int kLgBBytes = 8 * kLgBWaveBytes;              // 18 KiB
 constexpr size_t kLgLdsBytes = kLgNBuf * (kLgABytes + kLgBBytes);   // 150 KiB
+// int6: a wavefront's slot adds the tiles' high-bit planes (2 x 512 B); two slots, 116 KiB
+constexpr int kLg6BWaveBytes = 2 * 1024 + 2 * 128 + 2 * 512;
+constexpr size_t kLg6LdsBytes = 2 * (kLgABytes + 8 * kLg6BWaveBytes);
 
 // 16-byte k-chunk (of 16 in a superblock) that MFMA step s consumes in lane group g: int4 weight
 // fragments follow the tiled code words, bf16 ones the natural 32-k chunks.
@@ -833,15 +836,13 @@ __device__ __forceinline__ void lg_barrier() {
 
 // bf16-weight superblock registers of a wavefront: 2 tiles x 4 steps of B fragments.
 // Weight data a wavefront holds in registers one superblock ahead: bf16, the B fragments of its
-// two tiles; int6, the tiles' high-bit words (one per 64-column group); int4, none.
+// two tiles; int4 and int6 (staged in LDS), none.
 template <int FMT>
 struct LgStage {
   u32x4 q[2][4];
 };
 template <>
-struct LgStage<FMT_INT6> {
-  u32x2 h[2];
-};
+struct LgStage<FMT_INT6> {};
 template <>
 struct LgStage<FMT_INT4> {};
 
@@ -886,10 +887,12 @@ __device__ __forceinline__ uint32_t deq_pair6(uint32_t w, uint32_t hw, int h, in
 
 template <int FMT, int EPI>
 __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
-  // QF: int4 or int6 codes, dequantized to fp16 (int6: the nibble plane staged as int4's, the
-  // high-bit words in registers one superblock ahead)
+  // QF: int4 or int6 codes, dequantized to fp16 (int6: the nibble plane staged as int4's and
+  // the high-bit plane after the scale/bias copy, in two slots instead of three)
   constexpr bool QF = (FMT == FMT_INT4 || FMT == FMT_INT6);
   constexpr int SBB = (FMT == FMT_INT6) ? 1536 : 1024;   // bytes of a tile superblock
+  constexpr int NBUF = (FMT == FMT_INT6) ? 2 : kLgNBuf;
+  constexpr int BWAVE = (FMT == FMT_INT6) ? kLg6BWaveBytes : kLgBWaveBytes;
   extern __shared__ u32x4 lds[];
   char* lds_c = reinterpret_cast<char*>(lds);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -931,12 +934,12 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
                16 * lg_chunk<QF ? FMT_INT4 : FMT>(0, lane >> 4);
   }
   const uint32_t lds_base = lds_offset(lds);
-  auto a_slot = [&](int p) { return (p % kLgNBuf) * kLgABytes; };
-  auto b_slot = [&](int p) { return kLgNBuf * kLgABytes + (p % kLgNBuf) * kLgBBytes + wave * kLgBWaveBytes; };
+  auto a_slot = [&](int p) { return (p % NBUF) * kLgABytes; };
+  auto b_slot = [&](int p) { return NBUF * kLgABytes + (p % NBUF) * 8 * BWAVE + wave * BWAVE; };
 
   // ---- this wavefront's two weight tiles
   const char* wcode[2];
-  const char* whi[2];    // int6: the lane's 8 bytes of the tile's high-bit plane
+  const char* wtile[2];   // int4/int6: the tile's first superblock
   const char* wsb[2];
   const u32x4* wp[2];
   int rex[2] = {0, 0};   // int4/int6: the lane's weight row of each tile, its dequant exponent e
@@ -946,18 +949,20 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
                                        : 16 * cb + 2 * wave + t;
     if (QF) {
       const int64_t tb = (ebase + tl) * nsb;
-      wcode[t] = static_cast<const char*>(a.codes) + tb * SBB + lane * 16;
-      whi[t] = static_cast<const char*>(a.codes) + tb * SBB + 1024 + lane * 8;
+      wtile[t] = static_cast<const char*>(a.codes) + tb * SBB;
+      wcode[t] = wtile[t] + lane * 16;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
       rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - kDeqShift;
     } else {
-      wcode[t] = whi[t] = wsb[t] = nullptr;
+      wcode[t] = wtile[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
     }
   }
   // scale/bias copy: lanes 0-31 take tile 0's 128 B, lanes 32-63 tile 1's, 4 B each
   const char* sb_src = (QF) ? wsb[lane >> 5] + 4 * (lane & 31) : nullptr;
+  // int6 high-bit planes: lanes 0-31 take tile 0's 512 B, lanes 32-63 tile 1's, 16 B each
+  const char* hb_src = (FMT == FMT_INT6) ? wtile[lane >> 5] + 1024 + 16 * (lane & 31) : nullptr;
 
   // issue all loads of superblock p (A: 4 instructions when a_on; int4 weights: 3)
   auto issue = [&](int p) __attribute__((always_inline)) {
@@ -975,6 +980,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       dma16(wcode[0] + static_cast<int64_t>(p) * SBB, dst);
       dma16(wcode[1] + static_cast<int64_t>(p) * SBB, dst + 1024);
       dma4(sb_src + static_cast<int64_t>(p) * 128, dst + 2048);
+      if (FMT == FMT_INT6) dma16(hb_src + static_cast<int64_t>(p) * SBB, dst + 2048 + 256);
     }
   };
 
@@ -995,12 +1001,14 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
     const u32x4* la = reinterpret_cast<const u32x4*>(lds_c + a_slot(p)) + lane;
     u32x4 q[2];
     uint2 sbv[2];
+    u32x2 hq[2];   // int6: the lane's high-bit words of each tile (group 0, group 1)
     if (QF) {
       const char* lb = lds_c + b_slot(p);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
         sbv[t] = reinterpret_cast<const uint2*>(lb + 2048 + t * 128)[lane & 15];
+        if (FMT == FMT_INT6) hq[t] = reinterpret_cast<const u32x2*>(lb + 2304 + t * 512)[lane];
       }
     }
     DeqSb dsb[2];
@@ -1013,7 +1021,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
     auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
       const int t = u >> 2, j = u & 3;
       if constexpr (FMT == FMT_INT6) {
-        bfo[t][j] = deq_pair6(q[t][s], (s >> 1) ? gb.h[t].y : gb.h[t].x, s & 1, j, dsb[t]);
+        bfo[t][j] = deq_pair6(q[t][s], (s >> 1) ? hq[t].y : hq[t].x, s & 1, j, dsb[t]);
       } else if constexpr (FMT == FMT_INT4) {
         bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
       } else if (j == 0) {
@@ -1049,11 +1057,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // bf16 weights: registers, one superblock ahead
   LgStage<FMT> gbf[2];
   auto load_bf = [&](int p, LgStage<FMT>& g) __attribute__((always_inline)) {
-    if constexpr (FMT == FMT_INT6) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        g.h[t] = *reinterpret_cast<const u32x2*>(whi[t] + static_cast<int64_t>(p) * SBB);
-    } else if constexpr (FMT == FMT_BF16) {
+    if constexpr (FMT == FMT_BF16) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1064,8 +1068,30 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // Loads in flight per wavefront and superblock: NA (A, when a_on) + NB (int4 weights).
   // Before the barrier that publishes superblock p+1, a wavefront waits until only the loads
   // of p+2 remain outstanding.
-  constexpr int NB = (QF) ? 3 : 0;
+  constexpr int NB = (FMT == FMT_INT6) ? 4 : (QF) ? 3 : 0;
   auto run = [&](auto mbc) __attribute__((always_inline)) {
+    if constexpr (FMT == FMT_INT6) {
+      // two slots (the 512-row kernel's ring): at the end of superblock p each wavefront waits
+      // for its own loads of p+1, the barrier publishes slot p+1 and retires slot p, and the
+      // loads of p+2 go into slot p
+      issue(0);
+      if (nsb > 1) {
+        issue(1);
+        if (a_on) wait_vmcnt<4 + NB>(); else wait_vmcnt<NB>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      lg_barrier();
+      for (int p = 0; p < nsb; ++p) {
+        compute(p, gbf[0], mbc);
+        if (p + 1 < nsb) {
+          wait_vmcnt<0>();
+          lg_barrier();
+          if (p + 2 < nsb) issue(p + 2);
+        }
+      }
+      return;
+    }
     auto wait_next = [&](bool far) __attribute__((always_inline)) {
       // loads of the superblock after the next one, if issued, may stay in flight
       if (a_on) {
@@ -1074,19 +1100,15 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
         if (far) wait_vmcnt<NB>(); else wait_vmcnt<0>();
       }
     };
-    if (FMT == FMT_INT6) load_bf(0, gbf[0]);
     issue(0);
     if (nsb > 1) issue(1);
-    if (FMT != FMT_INT6) load_bf(0, gbf[0]);
+    load_bf(0, gbf[0]);
     wait_next(nsb > 1);
     lg_barrier();
     auto iter = [&](int p, const LgStage<FMT>& cur, LgStage<FMT>& nxt) __attribute__((always_inline)) {
       const bool far = p + 2 < nsb;
-      // (int6: the high-bit words of p+1 ahead of the loads of p+2, so the wait below, which
-      // leaves only the latter in flight, covers them)
-      if (FMT == FMT_INT6) load_bf(p + 1, nxt);
       if (far) issue(p + 2);
-      if (FMT != FMT_INT6) load_bf(p + 1, nxt);
+      load_bf(p + 1, nxt);
       compute(p, cur, mbc);
       wait_next(far);
       lg_barrier();
@@ -1564,10 +1586,12 @@ static void launch_small(const QmmArgs& a, const SmallShape& sh, int64_t mtiles,
 
 template <int FMT, int EPI>
 static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
-  // 150 KiB of dynamic LDS is above the default per-kernel limit; set it for the current device
+  // 150 KiB (int6: 116 KiB) of dynamic LDS is above the default per-kernel limit; set it for
+  // the current device
+  const size_t lds_bytes = (FMT == FMT_INT6) ? kLg6LdsBytes : kLgLdsBytes;
   const hipError_t err =
       hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_large_kernel<FMT, EPI>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLgLdsBytes));
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
   if (err != hipSuccess) return fail(std::string("qmm(large): LDS attribute: ") + hipGetErrorString(err));
   // 1-D grid in the XCD-grouped order the kernel decodes: m-tiles padded to whole groups of
   // 8 XCDs x G m-tiles; workgroups past `mtiles` exit at once
@@ -1576,7 +1600,7 @@ static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   const int64_t mpad = (mtiles + 8 * G - 1) / (8 * G) * (8 * G);
   QmmArgs b = a;
   b.mtiles = static_cast<int>(mtiles);
-  qmm_large_kernel<FMT, EPI><<<dim3(static_cast<unsigned>(mpad * nbk)), kLgThreads, kLgLdsBytes, stream>>>(b);
+  qmm_large_kernel<FMT, EPI><<<dim3(static_cast<unsigned>(mpad * nbk)), kLgThreads, lds_bytes, stream>>>(b);
   return 0;
 }
 
