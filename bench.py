@@ -14,9 +14,9 @@ Printed (one JSON line): whole-layer tokens/s (`value`), per-step time, the domi
 roofline (routed gate_up+SwiGLU: algorithmic bytes per launch / its average duration, HIP events
 on the launch stream), a sweep over the other decode batches and the 4096-token prefill, the
 widened rows at the headline batch (`--extra`: the block with the decoder layer's RMSNorm and
-residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format (also at
-the c4 prefill), and with
-Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies; and with
+residual add, qmoe_forward_residual; the layer with int6 experts, MiniMax M3's format, and with
+Kimi's widths, gate_up int3 + down int4 at group 128, each rotating two copies and each also at
+the c4 prefill; and with
 DeepSeek-V4's activation-aware expert scales on the int4 experts, also at the c4 prefill; with
 Kimi's widths drawn per (expert, projection)), and the CPU baseline (the torch-CPU port in oracle/torch_cpu.py on the host
 cores, bounded sample).
@@ -419,14 +419,14 @@ def main():
             torch.cuda.synchronize()
             m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), lays=lays_f)
             record(f"{args.config}-N{N}-{tag}", m2, u2, **fmt)
-            if tag == "int6" and args.prefill > 0:
-                # int6 at the c4 prefill (Zipf routing): the large regime, hot experts on the
-                # 256-row prefill kernel; FLOPs as the int4 prefill line
+            if args.prefill > 0:
+                # the same layers at the c4 prefill (Zipf routing): the large regime, hot experts
+                # on the 256-row prefill kernel; FLOPs as the int4 prefill line
                 n3 = args.prefill
                 m3, _, _, _ = run_batch(n3, max(20, args.steps // 20), 3, min(args.pool, 8),
                                         zipf=True, lays=lays_f)
                 f3 = synth.algorithmic_flops(cfg, n3)
-                rec = dict(workload=f"c4-prefill-N{n3}-zipf-int6", N=n3, ms_per_step=round(m3, 5),
+                rec = dict(workload=f"c4-prefill-N{n3}-zipf-{tag}", N=n3, ms_per_step=round(m3, 5),
                            tokens_per_s=round(n3 / (m3 / 1e3), 1), tflops=round(f3 / m3 / 1e9, 2),
                            mfma_frac=round(f3 / m3 / 1e9 / BF16_PEAK_TFLOPS, 4))
                 sweep.append(rec)

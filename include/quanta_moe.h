@@ -61,7 +61,8 @@ extern "C" {
                                src/quanta/minimax/model_m3.py:414-450); the large regime needs
                                row exponents, as int4 */
 #define QMOE_FMT_INT3_G64 3 /* affine int3 codes, bf16 scale/bias per 64 (Kimi's int3 gate/up
-                               stacks, src/quanta/modeling/quantized.py:1-84); small regime only */
+                               stacks, src/quanta/modeling/quantized.py:1-84); the large regime
+                               needs row exponents, as int4 */
 #define QMOE_FMT_INT8_G64 4 /* affine int8 codes, bf16 scale/bias per 64: the shared expert as the
                                bake stores it (src/quanta/qwen35/bake.py:147-151); shared expert
                                only (qmoe_config_t.shared_format) and qmoe_grouped_qmm's small

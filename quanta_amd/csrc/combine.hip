@@ -447,7 +447,6 @@ static int kernel_fmt(int f) {
   return f == QMOE_FMT_INT4_G64 ? FMT_INT4 : f == QMOE_FMT_INT6_G64 ? FMT_INT6
          : f == QMOE_FMT_INT3_G64 ? FMT_INT3 : f == QMOE_FMT_INT8_G64 ? FMT_INT8 : FMT_BF16;
 }
-// int3 or int6 codes on either projection: the large-M kernels stage int4 superblocks only.
 // AWQ-scaled experts in the large regime: int4 weights, and gate and up halves that split at a
 // whole 256-row block (the large kernels pick the activation copy per weight-row block)
 static bool awq_large_ok(const qmoe_config_t& c) {
@@ -455,15 +454,10 @@ static bool awq_large_ok(const qmoe_config_t& c) {
          c.inter % 256 == 0;
 }
 
-// int3 codes: no large-regime kernel (the prefill kernels stage int4 or int6 superblocks)
-static bool narrow_codes(const qmoe_config_t& c) {
-  return c.expert_format == QMOE_FMT_INT3_G64 || c.down_format == QMOE_FMT_INT3_G64;
-}
-
 // formats the large-regime kernels dequantize to fp16 (an fp16 activation copy, row exponents)
-static bool fp16_large_fmt(int kfmt) { return kfmt == FMT_INT4 || kfmt == FMT_INT6; }
+static bool fp16_large_fmt(int kfmt) { return fmt_quant(kfmt); }
 static bool fp16_large_fmt_q(int qfmt) {
-  return qfmt == QMOE_FMT_INT4_G64 || qfmt == QMOE_FMT_INT6_G64;
+  return qfmt == QMOE_FMT_INT4_G64 || qfmt == QMOE_FMT_INT6_G64 || qfmt == QMOE_FMT_INT3_G64;
 }
 
 static bool has_split(const qmoe_mixed_t& m) {
@@ -509,8 +503,6 @@ static int validate_config(const qmoe_config_t& c) {
     return fail("config: expert_format / down_format must be int4-g64 (0), bf16 (1), int6-g64 (2) or int3-g64 (3)");
   if ((c.expert_format == QMOE_FMT_BF16) != (c.down_format == QMOE_FMT_BF16))
     return fail("config: gate_up and down must both be quantized or both bf16");
-  if (narrow_codes(c) && c.regime == QMOE_REGIME_LARGE)
-    return fail("config: int3 experts run in the small regime only");
   if (c.awq != 0 && c.awq != 1) return fail("config: awq must be 0 or 1");
   if (c.awq && c.expert_format == QMOE_FMT_BF16)
     return fail("config: awq scales need quantized experts");
@@ -630,8 +622,8 @@ extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  // no large-regime kernel for int3/int6 or mixed widths
-  if (narrow_codes(c) || c.mixed || (c.awq && !awq_large_ok(c))) return QMOE_REGIME_SMALL;
+  // no large-regime path for mixed widths per expert
+  if (c.mixed || (c.awq && !awq_large_ok(c))) return QMOE_REGIME_SMALL;
   return dense_regime(c, N);
 }
 
@@ -673,7 +665,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   if (pick_regime(c, N) == QMOE_REGIME_LARGE &&
       ((fp16_large_fmt(kernel_fmt(c.expert_format)) && !wts->gu_rexp) ||
        (fp16_large_fmt(kernel_fmt(c.down_format)) && !wts->dn_rexp)))
-    return fail("qmoe_forward: int4/int6 experts in the large regime (N > 256) need gu_rexp and "
+    return fail("qmoe_forward: quantized experts in the large regime (N > 256) need gu_rexp and "
                 "dn_rexp (qmoe_row_exponents)");
 
   hipStream_t stream = static_cast<hipStream_t>(stream_);

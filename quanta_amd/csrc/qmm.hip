@@ -779,6 +779,9 @@ constexpr size_t kLgLdsBytes = kLgNBuf * (kLgABytes + kLgBBytes);   // 150 KiB
 // int6: a wavefront's slot adds the tiles' high-bit planes (2 x 512 B); two slots, 116 KiB
 constexpr int kLg6BWaveBytes = 2 * 1024 + 2 * 128 + 2 * 512;
 constexpr size_t kLg6LdsBytes = 2 * (kLgABytes + 8 * kLg6BWaveBytes);
+// int3: 768 B of codes per tile superblock; three slots, 138 KiB
+constexpr int kLg3BWaveBytes = 2 * 768 + 2 * 128;
+constexpr size_t kLg3LdsBytes = kLgNBuf * (kLgABytes + 8 * kLg3BWaveBytes);
 
 // 16-byte k-chunk (of 16 in a superblock) that MFMA step s consumes in lane group g: int4 weight
 // fragments follow the tiled code words, bf16 ones the natural 32-k chunks.
@@ -845,6 +848,8 @@ template <>
 struct LgStage<FMT_INT6> {};
 template <>
 struct LgStage<FMT_INT4> {};
+template <>
+struct LgStage<FMT_INT3> {};
 
 // int4 -> fp16 dequant of the prefill kernels, one packed register (two weights) per VALU FMA.
 // A code nibble masked in place is an fp16 subnormal: at bits 0-3 of a half it reads q * 2^-24,
@@ -885,14 +890,32 @@ __device__ __forceinline__ uint32_t deq_pair6(uint32_t w, uint32_t hw, int h, in
                             __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, v), d.s_lo, d.b));
 }
 
+// int3 pair q (0..15) of the lane's three code words, as unpack_q128_3: the 3-bit codes at bits
+// 0-2 of each half, the fp16 subnormal q * 2^-24. (int3 dequantizes with a shift one larger than
+// kDeqShift: row_exp bounds s * 2^row_exp below 2^15 / 7, so s * 2^(e+24) stays below 2^18 / 7.)
+__device__ __forceinline__ uint32_t deq_pair3(uint32_t w0, uint32_t w1, uint32_t w2, int q,
+                                             const DeqSb& d) {
+  const uint32_t w = (q < 5) ? w0 : (q < 10) ? w1 : w2;
+  const uint32_t v = (q < 15) ? (w >> (3 * (q % 5))) & 0x00070007u
+                              : ((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) |
+                                    ((w2 >> 13) & 0x00040004u);
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, v), d.s_lo, d.b));
+}
+
 template <int FMT, int EPI>
 __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // QF: int4 or int6 codes, dequantized to fp16 (int6: the nibble plane staged as int4's and
   // the high-bit plane after the scale/bias copy, in two slots instead of three)
-  constexpr bool QF = (FMT == FMT_INT4 || FMT == FMT_INT6);
-  constexpr int SBB = (FMT == FMT_INT6) ? 1536 : 1024;   // bytes of a tile superblock
+  constexpr bool QF = (FMT == FMT_INT4 || FMT == FMT_INT6 || FMT == FMT_INT3);
+  // bytes of a tile superblock, and of its codes in a wavefront's LDS slot (int6: the nibble
+  // plane; its high-bit plane follows the scale/bias copy)
+  constexpr int SBB = (FMT == FMT_INT6) ? 1536 : (FMT == FMT_INT3) ? 768 : 1024;
+  constexpr int CB = (FMT == FMT_INT3) ? 768 : 1024;
   constexpr int NBUF = (FMT == FMT_INT6) ? 2 : kLgNBuf;
-  constexpr int BWAVE = (FMT == FMT_INT6) ? kLg6BWaveBytes : kLgBWaveBytes;
+  constexpr int BWAVE = (FMT == FMT_INT6) ? kLg6BWaveBytes
+                        : (FMT == FMT_INT3) ? kLg3BWaveBytes : kLgBWaveBytes;
+  constexpr int DS = (FMT == FMT_INT3) ? kDeqShift + 1 : kDeqShift;   // row_exp - e
   extern __shared__ u32x4 lds[];
   char* lds_c = reinterpret_cast<char*>(lds);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -953,7 +976,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       wcode[t] = wtile[t] + lane * 16;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
-      rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - kDeqShift;
+      rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - DS;
     } else {
       wcode[t] = wtile[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
@@ -977,9 +1000,18 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
     }
     if (QF) {
       const uint32_t dst = lds_base + b_slot(p);
-      dma16(wcode[0] + static_cast<int64_t>(p) * SBB, dst);
-      dma16(wcode[1] + static_cast<int64_t>(p) * SBB, dst + 1024);
-      dma4(sb_src + static_cast<int64_t>(p) * 128, dst + 2048);
+      if (FMT == FMT_INT3) {
+        // 768 B per tile: three dword copies, lane l's 4 bytes at 256 i + 4 l of each
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 3; ++i)
+            dma4(wtile[t] + static_cast<int64_t>(p) * SBB + 256 * i + 4 * lane, dst + t * CB + 256 * i);
+      } else {
+        dma16(wcode[0] + static_cast<int64_t>(p) * SBB, dst);
+        dma16(wcode[1] + static_cast<int64_t>(p) * SBB, dst + 1024);
+      }
+      dma4(sb_src + static_cast<int64_t>(p) * 128, dst + 2 * CB);
       if (FMT == FMT_INT6) dma16(hb_src + static_cast<int64_t>(p) * SBB, dst + 2048 + 256);
     }
   };
@@ -1006,8 +1038,13 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       const char* lb = lds_c + b_slot(p);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
-        sbv[t] = reinterpret_cast<const uint2*>(lb + 2048 + t * 128)[lane & 15];
+        if (FMT == FMT_INT3) {   // the lane's three words
+          const uint32_t* w3 = reinterpret_cast<const uint32_t*>(lb + t * CB) + 3 * lane;
+          q[t] = u32x4{w3[0], w3[1], w3[2], 0u};
+        } else {
+          q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
+        }
+        sbv[t] = reinterpret_cast<const uint2*>(lb + 2 * CB + t * 128)[lane & 15];
         if (FMT == FMT_INT6) hq[t] = reinterpret_cast<const u32x2*>(lb + 2304 + t * 512)[lane];
       }
     }
@@ -1022,6 +1059,8 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       const int t = u >> 2, j = u & 3;
       if constexpr (FMT == FMT_INT6) {
         bfo[t][j] = deq_pair6(q[t][s], (s >> 1) ? hq[t].y : hq[t].x, s & 1, j, dsb[t]);
+      } else if constexpr (FMT == FMT_INT3) {
+        bfo[t][j] = deq_pair3(q[t].x, q[t].y, q[t].z, 4 * s + j, dsb[t]);
       } else if constexpr (FMT == FMT_INT4) {
         bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
       } else if (j == 0) {
@@ -1068,7 +1107,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // Loads in flight per wavefront and superblock: NA (A, when a_on) + NB (int4 weights).
   // Before the barrier that publishes superblock p+1, a wavefront waits until only the loads
   // of p+2 remain outstanding.
-  constexpr int NB = (FMT == FMT_INT6) ? 4 : (QF) ? 3 : 0;
+  constexpr int NB = (FMT == FMT_INT6) ? 4 : (FMT == FMT_INT3) ? 7 : (QF) ? 3 : 0;
   auto run = [&](auto mbc) __attribute__((always_inline)) {
     if constexpr (FMT == FMT_INT6) {
       // two slots (the 512-row kernel's ring): at the end of superblock p each wavefront waits
@@ -1588,7 +1627,8 @@ template <int FMT, int EPI>
 static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
   // 150 KiB (int6: 116 KiB) of dynamic LDS is above the default per-kernel limit; set it for
   // the current device
-  const size_t lds_bytes = (FMT == FMT_INT6) ? kLg6LdsBytes : kLgLdsBytes;
+  const size_t lds_bytes = (FMT == FMT_INT6) ? kLg6LdsBytes
+                           : (FMT == FMT_INT3) ? kLg3LdsBytes : kLgLdsBytes;
   const hipError_t err =
       hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_large_kernel<FMT, EPI>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
@@ -1829,9 +1869,9 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     if (a.split_tile <= 0 || a.split_tile % 4 || a.split_tile >= a.n_rows / 16)
       return fail("qmm: split_tile must be a positive multiple of 4 inside the weight tiles");
     if (regime != QMOE_REGIME_SMALL &&
-        ((fmt != FMT_INT4 && fmt != FMT_INT6) || !a.row_sinv_hi || a.split_tile % 16))
-      return fail("qmm(large): a second activation needs int4/int6 weights, its row scales and "
-                  "split_tile % 16 == 0");
+        (!fmt_quant(fmt) || !a.row_sinv_hi || a.split_tile % 16))
+      return fail("qmm(large): a second activation needs int3/int4/int6 weights, its row scales "
+                  "and split_tile % 16 == 0");
   }
   if (regime == QMOE_REGIME_SMALL) {
     if (fmt_quant(fmt) && a.K % 128) return fail("qmm: int3/int4/int6 need K % 128 == 0");
@@ -1877,9 +1917,6 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     }
 #undef QMOE_SMALL
   } else {
-    if (fmt == FMT_INT3)
-      return fail("qmm(large): int3 weights run in the small regime only (the large kernels "
-                  "stage int4 or int6 tile superblocks)");
     if (fmt == FMT_INT8)
       return fail("qmm(large): int8 weights run in the small regime only (expand them to bf16 "
                   "for the large kernels)");
@@ -1888,11 +1925,11 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
                           a.dense_mtile > kLargeMTile || fmt != FMT_BF16))
       return fail("qmm(large): dense_mtile is a multiple of 16 up to 128, for one dense bf16 segment");
     if (a.n_rows % 256) return fail("qmm(large): weight rows % 256 == 0 required");
-    const bool qf = (fmt == FMT_INT4 || fmt == FMT_INT6);
+    const bool qf = fmt_quant(fmt);
     if (qf && (!a.act16 || !a.row_sinv))
-      return fail("qmm(large): int4/int6 weights need the fp16 activation copy");
+      return fail("qmm(large): int3/int4/int6 weights need the fp16 activation copy");
     if (qf && !a.row_exp)
-      return fail("qmm(large): int4/int6 weights need their row exponents (qmoe_row_exponents)");
+      return fail("qmm(large): int3/int4/int6 weights need their row exponents (qmoe_row_exponents)");
     int rc;
 #define QMOE_LARGE(F, P) rc = launch_large<F, P>(a, mtile_bound, stream)
     // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves; a second activation:
@@ -1909,6 +1946,10 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT6, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT6, EPI_BF16);
       else QMOE_LARGE(FMT_INT6, EPI_F32);
+    } else if (fmt == FMT_INT3) {
+      if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT3, EPI_SWIGLU);
+      else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT3, EPI_BF16);
+      else QMOE_LARGE(FMT_INT3, EPI_F32);
     } else {
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_BF16, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_BF16, EPI_BF16);

@@ -128,10 +128,9 @@ def tile_experts_packed(d: dict) -> TiledExperts:
     E, rows, W = packed.shape
     tile = {4: ops.tile_int4, 6: ops.tile_int6, 3: ops.tile_int3}[bits]
     codes, sb = tile(packed.contiguous(), scale.contiguous(), bias.contiguous(), group_size=gs)
-    # int4 and int6 run on the prefill kernels' fp16 dequant: per-row power-of-two exponents keep
-    # any row's weights in fp16's normal range
-    rexp = (ops.row_exponents(scale.contiguous(), bias.contiguous(), bits=bits, group_size=gs)
-            if bits in (4, 6) else None)
+    # the prefill kernels' fp16 dequant: per-row power-of-two exponents keep any row's weights
+    # in fp16's normal range
+    rexp = ops.row_exponents(scale.contiguous(), bias.contiguous(), bits=bits, group_size=gs)
     awq = d.get("awq_scale")
     if awq is not None:
         awq = awq.to(device=packed.device, dtype=torch.bfloat16).contiguous()

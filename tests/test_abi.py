@@ -143,11 +143,10 @@ def test_forward_rejects_mixed_bf16_and_unknown_down_format():
                          (L.FMT_INT4_G64, 7, "down_format must be"),
                          (L.FMT_INT3_G64, L.FMT_INT4_G64, None)):
         cfg = L.QmoeConfig(expert_format=ef, down_format=df, **base)
-        if frag is None:   # a valid mix: the workspace query accepts it
+        if frag is None:   # a valid mix, in either regime: the workspace query accepts it
             assert lib.qmoe_forward_workspace(ctypes.byref(cfg), 4) > 0
             cfg.regime = L.REGIME_LARGE
-            rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
-            assert rc == L.QMOE_EINVAL and "small regime only" in _last_error()
+            assert lib.qmoe_forward_workspace(ctypes.byref(cfg), 4) > 0
             continue
         rc = lib.qmoe_forward(ctypes.byref(cfg), ctypes.byref(w), dummy, 4, dummy, dummy, 1 << 20, None)
         assert rc == L.QMOE_EINVAL and frag in _last_error(), _last_error()

@@ -241,32 +241,46 @@ def test_dequant_int3_bit_exact(gpu, gs):
     assert np.array_equal(bits_np(got), oq.dequant_bf16_bits(words, s, b, K, bits=3, group_size=gs))
 
 
+@pytest.mark.parametrize("regime", [L.REGIME_SMALL, L.REGIME_LARGE])
 @pytest.mark.parametrize("epi", [L.EPI_SWIGLU, L.EPI_BF16])
 @pytest.mark.parametrize("N,k,E,H,rows", [(1, 4, 8, 4096, 256), (7, 3, 6, 256, 256),
-                                          (200, 4, 4, 1024, 128), (1024, 4, 32, 256, 512)])
-def test_grouped_qmm_int3_vs_oracle(gpu, epi, N, k, E, H, rows):
-    """The decode kernel's int3 path (tiled 2-bit + top-bit planes) against the oracle's exact
-    affine weights, through several launch shapes."""
+                                          (200, 4, 4, 1024, 128), (1024, 4, 32, 256, 512),
+                                          (300, 3, 5, 768, 768)])
+def test_grouped_qmm_int3_vs_oracle(gpu, regime, epi, N, k, E, H, rows):
+    """int3 (three code words per lane per tile superblock) against the oracle's exact affine
+    weights: the decode kernel through several launch shapes, and the 256-row prefill kernel
+    (768-byte superblocks staged in LDS by dword copies, fp16 dequant under row exponents for
+    3-bit codes, one more power of two of headroom than int4)."""
+    if regime == L.REGIME_LARGE and rows % 256:
+        pytest.skip("the large regime tiles 256 weight rows")
     rng = np.random.default_rng(3 * N + E + H + rows)
     idx = np.stack([rng.permutation(E)[:k] for _ in range(N)]).astype(np.int32)
     x = oq.round_bf16(rng.standard_normal((N, H)))
     w = torch.from_numpy(rng.standard_normal((E, rows, H)).astype(np.float32) * 0.05).to(gpu)
     packed, s, b = quantize_affine(w, 3, group_size=64)
     dense = oq.dequant_exact(words_np(packed), bits_np(s), bits_np(b), H, bits=3)
+    m_tile = L.SMALL_M_TILE if regime == L.REGIME_SMALL else L.LARGE_M_TILE
     counts, offsets, tile_off, sorted_slot, inv, tile_map = ops.permute(torch.from_numpy(idx).to(gpu), E,
-                                                                        L.SMALL_M_TILE)
+                                                                        m_tile)
     codes, sb = ops.tile_int3(packed, s, b)
+    rexp = None
+    if regime == L.REGIME_LARGE:
+        rexp = ops.row_exponents(s, b, bits=3)
+        # each row's largest dequantized magnitude (codes 0..7) times 2^rexp lies in [2^13, 2^14)
+        peak = np.abs(dense).max(axis=-1) * np.exp2(rexp.cpu().numpy().astype(np.float64))
+        assert np.all((peak >= 2.0 ** 13) & (peak < 2.0 ** 14))
     out = ops.grouped_qmm(bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu), K=H, n_rows=rows,
                           weight_format=L.FMT_INT3_G64, codes=codes, sb=sb, epilogue=epi,
-                          out_rows=N * k, regime=L.REGIME_SMALL, slot_of=sorted_slot, slot_div=k,
+                          out_rows=N * k, regime=regime, slot_of=sorted_slot, slot_div=k,
                           n_slots=N * k, offsets=offsets, tile_off=tile_off, tile_map=tile_map,
-                          n_experts=E)
+                          n_experts=E, row_exp=rexp)
     order = sorted_slot.cpu().numpy()
     full = np.einsum("mh,moh->mo", x[order // k], dense[idx.reshape(-1)[order]])
     want = oq.round_bf16(full)
     if epi == L.EPI_SWIGLU:
         want = om.swiglu(want, rows // 2)
-    assert_close(f64(out), want, f"int3 qmm epi={epi} N={N} E={E} H={H} rows={rows}", rel_l2=4e-3)
+    assert_close(f64(out), want, f"int3 qmm regime={regime} epi={epi} N={N} E={E} H={H} rows={rows}",
+                 rel_l2=4e-3)
 
 
 def _layer_widths(dev, gs, seed, gu_bits, dn_bits, H=512, E=8, I=256, Is=256):
@@ -283,20 +297,29 @@ def _layer_widths(dev, gs, seed, gu_bits, dn_bits, H=512, E=8, I=256, Is=256):
 def test_block_mixed_widths_vs_oracle(gpu, gs, gu_bits, dn_bits, N):
     """Per-projection widths through the block: Kimi's gate/up int3 + down int4 at group 128, int3
     throughout, and the other mixes of the decode kernel's formats. Slot-major, fused shared
-    expert, auxiliary-stream shared expert, and above 256 tokens the large regime for int4/int6
-    mixes (the 256-row prefill kernel for int6) and the decode kernel for any int3 stack."""
+    expert, auxiliary-stream shared expert, and above 256 tokens the large regime (the 256-row
+    prefill kernel for int3 and int6 stacks)."""
     cfg = MoEConfig(512, 8, 2, 256, 256)
     p = _layer_widths(gpu, gs, 13 * N + gs + gu_bits, gu_bits, dn_bits)
     _check(p, cfg, _inputs(gpu, N, 512, N), f"gate_up int{gu_bits} down int{dn_bits} g{gs} N={N}",
            gs=gs, bits=gu_bits, down_bits=dn_bits)
 
 
-def test_int3_large_regime_refused(gpu):
-    cfg = MoEConfig(512, 8, 2, 256, 256)
-    p = _layer_widths(gpu, 128, 1, 3, 4)
-    x = _inputs(gpu, 300, 512, 1)
-    with pytest.raises(ValueError, match="int3"):
-        qwen35_moe(x[None], p, cfg, regime=L.REGIME_LARGE)
+@pytest.mark.parametrize("gs,gu_bits,dn_bits,E,N", [(128, 3, 4, 32, 300), (64, 3, 3, 8, 1100)])
+def test_block_int3_large_regime_vs_oracle(gpu, gs, gu_bits, dn_bits, E, N):
+    """int3 layers above 256 tokens (Kimi's gate/up int3 + down int4 at group 128, and int3
+    throughout): hot experts on the 256-row prefill kernel, the rest on the decode kernel (E = 32
+    at 300 tokens holds both); against the oracle and against the decode kernel's output."""
+    cfg = MoEConfig(512, E, 2, 256, 256)
+    p = _layer_widths(gpu, gs, 13 * N + gs, gu_bits, dn_bits, E=E)
+    x = _inputs(gpu, N, 512, N)
+    y, it = _check(p, cfg, x, f"int{gu_bits}/int{dn_bits} g{gs} large regime E={E} N={N}", gs=gs,
+                   bits=gu_bits, down_bits=dn_bits)
+    counts = np.bincount(it["idx"].reshape(-1), minlength=E)
+    if E == 32:
+        assert counts.max() > 16 and counts.min() <= 16, "the layer must hold hot and cold experts"
+    y_small = qwen35_moe(x[None], p, cfg, regime=L.REGIME_SMALL)[0]
+    assert_close(f64(y), f64(y_small), f"int3 large vs decode kernel E={E} N={N}")
 
 
 @pytest.mark.parametrize("fmt", [dict(bits=3, down_bits=4, group_size=128), dict(bits=6)],
