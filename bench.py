@@ -449,6 +449,19 @@ def main():
             # bytes: the int4-g64 figure with the mixed layer's mean bytes per expert in its place
             be4 = 3 * cfg.moe_intermediate_size * H * 36 / 64
             record(f"{args.config}-N{N}-mixed34", m2, u2, per_expert_bytes=be - be4)
+            if args.prefill > 0:
+                # the same layers at the c4 prefill (Zipf routing): each (projection, width)
+                # stack's launch on the prefill kernels over the hot experts' m-tiles
+                n3 = args.prefill
+                m3, _, _, _ = run_batch(n3, max(20, args.steps // 20), 3, min(args.pool, 8),
+                                        zipf=True, lays=lays_m)
+                f3 = synth.algorithmic_flops(cfg, n3)
+                rec = dict(workload=f"c4-prefill-N{n3}-zipf-mixed34", N=n3,
+                           ms_per_step=round(m3, 5), tokens_per_s=round(n3 / (m3 / 1e3), 1),
+                           tflops=round(f3 / m3 / 1e9, 2),
+                           mfma_frac=round(f3 / m3 / 1e9 / BF16_PEAK_TFLOPS, 4))
+                sweep.append(rec)
+                log(f"sweep {rec}")
             del lays_m
         if "awq" in args.extra:
             # DeepSeek-V4's activation-aware scales on the int4 experts: each routed row's

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 7
+#define QMOE_ABI_VERSION 8
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -201,6 +201,8 @@ typedef struct {
   const uint32_t* codes;       /* tiled codes */
   const uint16_t* sb;          /* tiled scale/bias */
   const int32_t* expert_slot;  /* [E] device: the expert's slot in this stack, or -1 */
+  const int8_t* row_exp;       /* [E_w][rows] device (qmoe_row_exponents of the stack): needed
+                                  in the large regime (N > 256), else may be NULL */
 } qmoe_stack_t;
 typedef struct {
   int32_t n_stacks;            /* 2 .. QMOE_MAX_STACKS, every projection at least once */

@@ -23,7 +23,7 @@ REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 7
+ABI_VERSION = 8
 NOALLOC_SCRATCH_BYTES = 64 << 20   # QMOE_NOALLOC_SCRATCH_BYTES
 
 
@@ -94,6 +94,7 @@ class QmoeStack(ctypes.Structure):
         ("codes", ctypes.c_void_p),
         ("sb", ctypes.c_void_p),
         ("expert_slot", ctypes.c_void_p),
+        ("row_exp", ctypes.c_void_p),
     ]
 
 

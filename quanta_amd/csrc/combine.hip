@@ -509,8 +509,7 @@ static int validate_config(const qmoe_config_t& c) {
   if (c.awq && c.regime == QMOE_REGIME_LARGE && !awq_large_ok(c))
     return fail("config: awq scales in the large regime need int4 experts and inter % 256 == 0");
   if (c.mixed != 0 && c.mixed != 1) return fail("config: mixed must be 0 or 1");
-  if (c.mixed && (c.awq || c.regime == QMOE_REGIME_LARGE))
-    return fail("config: mixed-width experts run in the small regime, without awq scales");
+  if (c.mixed && c.awq) return fail("config: mixed-width experts run without awq scales");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {
     if (c.router_rows < c.n_experts + (c.shared_gated ? 1 : 0) || c.router_rows % 256)
       return fail("config: router_rows must cover E (+1 shared gate row) and be a multiple of 256");
@@ -622,8 +621,7 @@ extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
   if (c.regime != QMOE_REGIME_AUTO) return c.regime;
-  // no large-regime path for mixed widths per expert
-  if (c.mixed || (c.awq && !awq_large_ok(c))) return QMOE_REGIME_SMALL;
+  if (c.awq && !awq_large_ok(c)) return QMOE_REGIME_SMALL;
   return dense_regime(c, N);
 }
 
@@ -662,7 +660,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   if (c.router_format == QMOE_ROUTER_F32 && c.shared_gated && !wts->shared_gate_w)
     return fail("qmoe_forward: fp32 router with a gated shared expert needs shared_gate_w");
   if (c.awq && (!wts->awq_gu || !wts->awq_dn)) return fail("qmoe_forward: awq needs awq_gu and awq_dn");
-  if (pick_regime(c, N) == QMOE_REGIME_LARGE &&
+  if (mixed && pick_regime(c, N) == QMOE_REGIME_LARGE) {
+    for (int i = 0; i < mixed->n_stacks; ++i)
+      if (!mixed->stacks[i].row_exp)
+        return fail("qmoe_forward_mixed: stacks in the large regime (N > 256) need row_exp "
+                    "(qmoe_row_exponents)");
+  }
+  if (!mixed && pick_regime(c, N) == QMOE_REGIME_LARGE &&
       ((fp16_large_fmt(kernel_fmt(c.expert_format)) && !wts->gu_rexp) ||
        (fp16_large_fmt(kernel_fmt(c.down_format)) && !wts->dn_rexp)))
     return fail("qmoe_forward: quantized experts in the large regime (N > 256) need gu_rexp and "
@@ -911,6 +915,10 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.row_sinv = sinv;
     return launch_qmm(a, fmt, epi, QMOE_REGIME_LARGE, hot_bound, stream);
   };
+  if (f16_acts && aux) {   // the fp16 copy of x, made on the auxiliary stream at the fork
+    const hipError_t err = hipStreamWaitEvent(stream, aux->xready, 0);
+    if (err != hipSuccess) return fail(std::string("forward: x16 wait: ") + hipGetErrorString(err));
+  }
   // 5. routed gate_up + SwiGLU -> h (sorted order)
   if (mixed && !has_split(*mixed)) {
     // fused gate_up stacks by width: SwiGLU in the epilogue, straight into h
@@ -922,8 +930,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
       a.K = c.hidden; a.n_rows = 2 * c.inter; a.codes = st.codes; a.sb = st.sb;
       a.expert_map = st.expert_slot; a.out = h; a.ld_out = c.inter;
+      a.row_exp = st.row_exp;
       a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
-      rc = routed(a, kernel_fmt(st.format), EPI_SWIGLU, nullptr, nullptr);
+      rc = routed(a, kernel_fmt(st.format), EPI_SWIGLU, x16, x_sinv);
+      if (rc) return rc;
+    }
+    if (hybrid && aux) {   // h complete (cold rows from the auxiliary stream)
+      rc = link(aux->cold, aux->s, stream, "cold gate_up");
       if (rc) return rc;
     }
   } else if (mixed) {
@@ -936,9 +949,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       a.act = x; a.act_rows = N; a.slot_of = sorted; a.slot_div = c.top_k; a.n_slots = mc;
       a.offsets = offsets; a.tile_off = tile_off; a.n_experts = c.n_experts;
       a.K = c.hidden; a.n_rows = c.inter; a.codes = st.codes; a.sb = st.sb;
-      a.expert_map = st.expert_slot;
+      a.expert_map = st.expert_slot; a.row_exp = st.row_exp;
       a.out = gu + (st.proj == QMOE_PROJ_UP ? c.inter : 0); a.ld_out = 2 * c.inter;
-      rc = routed(a, kernel_fmt(st.format), EPI_BF16, nullptr, nullptr);
+      rc = routed(a, kernel_fmt(st.format), EPI_BF16, x16, x_sinv);
+      if (rc) return rc;
+    }
+    if (hybrid && aux) {   // all of gu (cold rows from the auxiliary stream) before the glu pass
+      rc = link(aux->cold, aux->s, stream, "cold gate_up");
       if (rc) return rc;
     }
     rc = launch_awq_glu(gu, offsets, c.n_experts, mc, c.inter, nullptr, c.act, c.act_alpha,
@@ -973,10 +990,6 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     a.row_exp = fp16_large_fmt(gfmt) ? wts->gu_rexp : nullptr;
     a.out = h; a.ld_out = c.inter;
     a.glu = c.act; a.glu_alpha = c.act_alpha; a.glu_limit = c.act_limit;
-    if (f16_acts && aux) {   // the fp16 copy of x, made on the auxiliary stream at the fork
-      const hipError_t err = hipStreamWaitEvent(stream, aux->xready, 0);
-      if (err != hipSuccess) return fail(std::string("forward: x16 wait: ") + hipGetErrorString(err));
-    }
     // (the fused tail below computes the shared down itself)
     const bool tail = slot_major && dfmt == FMT_INT4 &&
                       down_combine_fits(n, c.top_k, c.hidden, c.inter, c.shared_inter);
@@ -1041,8 +1054,8 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       for (int i = 0; i < mixed->n_stacks; ++i) {
         const qmoe_stack_t& st = mixed->stacks[i];
         if (st.proj != QMOE_PROJ_DOWN) continue;
-        a.codes = st.codes; a.sb = st.sb; a.expert_map = st.expert_slot;
-        rc = routed(a, kernel_fmt(st.format), EPI_BF16, nullptr, nullptr);
+        a.codes = st.codes; a.sb = st.sb; a.expert_map = st.expert_slot; a.row_exp = st.row_exp;
+        rc = routed(a, kernel_fmt(st.format), EPI_BF16, h16, h_sinv);
         if (rc) return rc;
       }
     } else {

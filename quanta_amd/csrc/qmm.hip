@@ -935,6 +935,11 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const int cb = rk % nbk;
   const int mrows = (a.dense_mtile > 0 && !a.offsets && !a.tile_map) ? a.dense_mtile : kLargeMTile;
   if (mt >= a.mtiles || !resolve_mtile(a, mt, mrows, e, m0, m_cnt)) return;
+  // (one stack of a projection whose experts have different widths: the others' m-tiles exit)
+  if (a.expert_map) {
+    e = a.expert_map[e];
+    if (e < 0) return;
+  }
   // (AWQ: the 256-row blocks from split_tile on read the second activation copy)
   const bool hi = (QF) && a.act16_hi && 16 * cb >= a.split_tile;
   const uint16_t* act16 = hi ? a.act16_hi : a.act16;
@@ -1236,6 +1241,10 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
   const int mt = (gk * 8 + xcd) * G + rk / nbk;
   const int cb = rk % nbk;
   if (mt >= a.mtiles || !resolve_mtile(a, mt, kLargeMTile, e, m0, m_cnt)) return;
+  if (a.expert_map) {   // (as qmm_large_kernel)
+    e = a.expert_map[e];
+    if (e < 0) return;
+  }
   const int64_t ebase = static_cast<int64_t>(e) * (a.n_rows / 16);
   const int nsb = a.K / 128;
   const int mb_act = __builtin_amdgcn_readfirstlane((m_cnt + 15) >> 4);   // 1..8
@@ -1859,8 +1868,8 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
   if (a.K <= 0 || a.n_rows <= 0) return fail("qmm: empty problem");
   if (mtile_bound <= 0) return 0;
   if (mtile_bound > 65535) return fail("qmm: too many m-tiles for one launch");
-  if (a.expert_map && regime != QMOE_REGIME_SMALL)
-    return fail("qmm: an expert map needs the small regime");
+  if (a.expert_map && !fmt_quant(fmt))
+    return fail("qmm: an expert map needs int3/int4/int6 weights");
   const bool two_acts = (regime == QMOE_REGIME_SMALL) ? a.act_hi != nullptr : a.act16_hi != nullptr;
   if (two_acts) {
     if (!fmt_quant(fmt) || epi == EPI_SWIGLU || a.slot_of)

@@ -96,8 +96,8 @@ class TiledExperts(dict):
     Keys: "format" ("int4_g64" | "int6_g64" | "int3_g64" | "bf16"), "codes" (tiled int4 / int6 /
     int3 words or tiled bf16), "sb" (tiled scale+bias of the quantized formats), "shape"
     (E, rows, K), "group_size", "bits", "awq_scale" (bf16 per-input-channel activation scales, or
-    None) and "rexp" (int4: int8 [E, rows] per-row power-of-two exponents of the prefill
-    kernels' fp16 dequant, or None). Produced from the reference's packed triplet
+    None) and "rexp" (int3/int4/int6: int8 [E, rows] per-row power-of-two exponents of the
+    prefill kernels' fp16 dequant, or None). Produced from the reference's packed triplet
     {packed, scale, bias, group_size, bits} (src/quanta/qwen35/artifact.py:199-203; DeepSeek-V4's
     packed experts add awq_scale, src/quanta/dsv4/artifact.py:252-290) or from a bf16
     [E, rows, K] stack.
@@ -551,7 +551,8 @@ def _prepare_mixed(p: dict, cfg, *, topk, regime) -> Prepared:
             raise ValueError(f"mixed experts: {proj} stacks must be [E_w, {want[0]}, {want[1]}] "
                              f"(got {tuple(te['shape'])})")
         m.stacks[i] = L.QmoeStack(proj_id[proj], fmts[te["format"]], te["codes"].data_ptr(),
-                                  te["sb"].data_ptr(), emap.data_ptr())
+                                  te["sb"].data_ptr(), emap.data_ptr(),
+                                  te["rexp"].data_ptr() if te.get("rexp") is not None else None)
     # the rest of the block: a placeholder uniform stack pair supplies nothing but the shapes
     q = {kk: v for kk, v in p.items() if kk != "experts_mixed"}
     q["experts_gate_up"] = TiledExperts(format="int4_g64", codes=None, sb=None, shape=(E, 2 * I, H),

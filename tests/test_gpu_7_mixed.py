@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import moe as om
+from quanta_amd import _lib as L
 from quanta_amd.moe import MoEConfig, qwen35_moe, qwen35_moe_residual
 from quanta_amd.quant import quantize_affine
 from tests._util import assert_close, bits_np, f64, oracle_params_from_torch, words_np
@@ -27,7 +28,7 @@ H, E, I = 512, 8, 256
 GS = 128
 
 
-def _mixed(dev, seed, widths, permute=True, tie_slots=False, group_sizes=None):
+def _mixed(dev, seed, widths, permute=True, tie_slots=False, group_sizes=None, n_exp=E):
     """widths[proj] [E] -> (p["experts_mixed"] source dict, the oracle's "mixed" dict).
     tie_slots: up takes gate's slots (with equal widths, the layout that fuses gate and up);
     group_sizes[proj]: that projection's stacks' group size (default GS)."""
@@ -38,7 +39,7 @@ def _mixed(dev, seed, widths, permute=True, tie_slots=False, group_sizes=None):
         rows, K = (I, H) if proj != "down" else (H, I)
         gs = (group_sizes or {}).get(proj, GS)
         pb = np.asarray(widths[proj])
-        ps = np.zeros(E, np.int64)
+        ps = np.zeros(n_exp, np.int64)
         stacks[proj], ostacks[proj] = {}, {}
         for b in sorted(set(pb.tolist())):
             ids = np.flatnonzero(pb == b)
@@ -55,10 +56,10 @@ def _mixed(dev, seed, widths, permute=True, tie_slots=False, group_sizes=None):
     return src, {"stacks": ostacks, "pbits": pbits, "pslot": pslot, "group_size": GS}
 
 
-def _layer_mixed(dev, seed, widths, permute=True, **kw):
-    p = _layer(dev, GS, seed)
+def _layer_mixed(dev, seed, widths, permute=True, n_exp=E, **kw):
+    p = _layer(dev, GS, seed, E=n_exp)
     del p["experts_gate_up"], p["experts_down"]
-    src, om_mixed = _mixed(dev, seed, widths, permute, **kw)
+    src, om_mixed = _mixed(dev, seed, widths, permute, n_exp=n_exp, **kw)
     p["experts_mixed"] = src
     return p, om_mixed
 
@@ -76,7 +77,8 @@ def _oracle(p, om_mixed):
 
 def test_mixed_one_width_equals_uniform_path(gpu):
     """All experts int4 with identity slots: the gate, up and down stacks concatenated into the
-    uniform gate_up / down triplets give the same output bit for bit, at every regime."""
+    uniform gate_up / down triplets give the same output bit for bit, at every regime (the
+    decode kernel up to 256 tokens, the prefill kernels above)."""
     widths = {k: np.full(E, 4) for k in ("gate", "up", "down")}
     p, _ = _layer_mixed(gpu, 3, widths, permute=False)
     st = p["experts_mixed"]["stacks"]
@@ -88,7 +90,7 @@ def test_mixed_one_width_equals_uniform_path(gpu):
     cfg = MoEConfig(H, E, 2, I, 256)
     for N in (1, 8, 40, 300):
         x = _inputs(gpu, N, H, N)
-        y_uni = qwen35_moe(x[None], q, cfg, regime=1)[0]
+        y_uni = qwen35_moe(x[None], q, cfg, regime=L.REGIME_SMALL if N <= 256 else L.REGIME_AUTO)[0]
         y_mix = qwen35_moe(x[None], p, cfg)[0]
         assert torch.equal(y_mix, y_uni), f"N={N}"
 
@@ -109,6 +111,28 @@ def test_mixed_vs_oracle(gpu, case, N):
     y = qwen35_moe(x[None], p, cfg)[0]
     _, it = om.moe_forward(f64(x), _oracle(p, om_mixed), k=2, inter=I)
     assert_close(f64(y), it["y_exact"], f"mixed {case} N={N}")
+
+
+@pytest.mark.parametrize("case", ["kimi", "with_int6"])
+def test_mixed_large_regime_hot_and_cold_vs_oracle(gpu, case):
+    """Mixed widths above 256 tokens with 32 experts: each (projection, width) stack's launch on
+    the prefill kernels over the hot experts' m-tiles and on the decode kernel over the cold
+    ones, the other widths' experts exiting in both."""
+    n_exp, N = 32, 300
+    rng = np.random.default_rng(5)
+    if case == "kimi":
+        widths = {"gate": np.full(n_exp, 3), "up": np.full(n_exp, 3),
+                  "down": rng.choice([3, 4], n_exp, p=[0.2, 0.8])}
+    else:
+        widths = {k: rng.choice([3, 4, 6], n_exp) for k in ("gate", "up", "down")}
+    cfg = MoEConfig(H, n_exp, 2, I, 256)
+    p, om_mixed = _layer_mixed(gpu, 91 + len(case), widths, n_exp=n_exp)
+    x = _inputs(gpu, N, H, N)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), _oracle(p, om_mixed), k=2, inter=I)
+    counts = np.bincount(it["idx"].reshape(-1), minlength=n_exp)
+    assert counts.max() > 16 and counts.min() <= 16, "the layer must hold hot and cold experts"
+    assert_close(f64(y), it["y_exact"], f"mixed {case} hot+cold N={N}")
 
 
 @pytest.mark.parametrize("case", ["fused34", "fused346", "g64_g128"])
