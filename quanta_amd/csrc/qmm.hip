@@ -878,16 +878,20 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int j, const DeqSb& d) 
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, (j & 1) ? d.s_hi : d.s_lo, d.b));
 }
 
-// int6 pair j (0..3) of step half h: the nibble pair of word w as deq_pair's, with its two high
-// bits from the group's high-bit word hw (bits 2j + 8h and 16 + 2j + 8h, as unpack_q128_6) moved
-// to bits 4-5, so each half holds the 6-bit code q at bits 0-5: the fp16 subnormal q * 2^-24.
-// row_exp bounds s * 2^row_exp below 2^15 / 63, so s * 2^(e+24) stays below 2^19 / 63.
+// int6 pair j (0..3) of step half h: the nibble pair of word w as deq_pair takes it (even j at
+// bits 0-3 of each half, odd j in place at bits 4-7, pairs 2 and 3 sharing one 8-bit shift), its
+// two high bits from the group's high-bit word hw (bits 2j + 8h and 16 + 2j + 8h, as
+// unpack_q128_6) moved just above the nibble: each half holds the 6-bit code q as the fp16
+// subnormal q * 2^-24 (even j) or 16 q * 2^-24 (odd j, scaled by s_hi). row_exp bounds
+// s * 2^row_exp below 2^15 / 63, so both scale factors stay below 2^19 / 63.
 __device__ __forceinline__ uint32_t deq_pair6(uint32_t w, uint32_t hw, int h, int j, const DeqSb& d) {
-  const int hs = 2 * j + 8 * h - 4;   // high bits to bits 4-5: a right shift by hs (left if < 0)
+  const uint32_t src = (j >= 2) ? (w >> 8) : w;
+  const bool odd = (j & 1) != 0;
+  const int hs = 2 * j + 8 * h - (odd ? 8 : 4);   // right shift of the high bits (left if < 0)
   const uint32_t hb = (hs >= 0) ? (hw >> hs) : (hw << -hs);
-  const uint32_t v = ((w >> (4 * j)) & 0x000F000Fu) | (hb & 0x00300030u);
-  return __builtin_bit_cast(uint32_t,
-                            __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, v), d.s_lo, d.b));
+  const uint32_t v = (src & (odd ? 0x00F000F0u : 0x000F000Fu)) | (hb & (odd ? 0x03000300u : 0x00300030u));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, v),
+                                                                odd ? d.s_hi : d.s_lo, d.b));
 }
 
 // int3 pair q (0..15) of the lane's three code words, as unpack_q128_3: the 3-bit codes at bits
