@@ -1228,9 +1228,20 @@ constexpr int kWdABytes = 8 * 4 * 64 * 16;                 // 32 KiB
 constexpr int kWdBWaveBytes = 4 * 1024 + 4 * 128;          // 4.5 KiB
 constexpr int kWdSlotBytes = kWdABytes + 8 * kWdBWaveBytes; // 68 KiB
 constexpr size_t kWdLdsBytes = 2 * kWdSlotBytes;            // 136 KiB
+// int3 (qmm_wide_int3_kernel): 768 B of codes per tile superblock, 3.5 KiB per wavefront, 120 KiB
+constexpr int kWd3BWaveBytes = 4 * 768 + 4 * 128;
+constexpr int kWd3SlotBytes = kWdABytes + 8 * kWd3BWaveBytes;
+constexpr size_t kWd3LdsBytes = 2 * kWd3SlotBytes;
 
-template <int EPI>
-__global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
+// FMT: int4 (qmm_wide_kernel) or int3 (qmm_wide_int3_kernel, the tile superblocks staged by dword
+// copies as in qmm_large_kernel)
+template <int FMT, int EPI>
+__device__ __forceinline__ void wide_body(const QmmArgs& a) {
+  constexpr int SBB = (FMT == FMT_INT3) ? 768 : 1024;   // code bytes of a tile superblock
+  constexpr int BWAVE = (FMT == FMT_INT3) ? kWd3BWaveBytes : kWdBWaveBytes;
+  constexpr int SLOT = (FMT == FMT_INT3) ? kWd3SlotBytes : kWdSlotBytes;
+  constexpr int DS = (FMT == FMT_INT3) ? kDeqShift + 1 : kDeqShift;   // row_exp - e
+  constexpr int NB = (FMT == FMT_INT3) ? 14 : 6;   // weight loads per superblock
   extern __shared__ u32x4 lds[];
   char* lds_c = reinterpret_cast<char*>(lds);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1267,11 +1278,12 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
                16 * lg_chunk<FMT_INT4>(0, lane >> 4);
   }
   const uint32_t lds_base = lds_offset(lds);
-  auto a_slot = [&](int p) { return (p & 1) * kWdSlotBytes; };
-  auto b_slot = [&](int p) { return (p & 1) * kWdSlotBytes + kWdABytes + wave * kWdBWaveBytes; };
+  auto a_slot = [&](int p) { return (p & 1) * SLOT; };
+  auto b_slot = [&](int p) { return (p & 1) * SLOT + kWdABytes + wave * BWAVE; };
 
   // this wavefront's four weight tiles (SwiGLU: gate tiles first, then their up tiles)
   const char* wcode[4];
+  const char* wtile[4];   // the tile's first superblock
   const char* wsb[4];
   int rex[4];   // the lane's weight row of each tile: its dequant exponent e (deq_sb)
 #pragma unroll
@@ -1280,9 +1292,10 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
                        ? ((t < 2) ? 16 * cb + 2 * wave + t : a.n_rows / 32 + 16 * cb + 2 * wave + (t - 2))
                        : 32 * cb + 4 * wave + t;
     const int64_t tb = (ebase + tl) * nsb;
-    wcode[t] = static_cast<const char*>(a.codes) + (tb * 64 + lane) * 16;
+    wtile[t] = static_cast<const char*>(a.codes) + tb * SBB;
+    wcode[t] = wtile[t] + lane * 16;
     wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
-    rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - kDeqShift;
+    rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - DS;
   }
   // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
   const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
@@ -1297,10 +1310,19 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       for (int s = 0; s < 4; ++s) dma16(src + 16 * (8 * (s >> 1) + (s & 1)), dst + s * 1024);
     }
     const uint32_t dst = lds_base + b_slot(p);
+    if (FMT == FMT_INT3) {
+      // 768 B per tile: three dword copies, lane l's 4 bytes at 256 i + 4 l of each
 #pragma unroll
-    for (int t = 0; t < 4; ++t) dma16(wcode[t] + static_cast<int64_t>(p) * 1024, dst + t * 1024);
-    dma4(sb_src0 + static_cast<int64_t>(p) * 128, dst + 4096);
-    dma4(sb_src1 + static_cast<int64_t>(p) * 128, dst + 4096 + 256);
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          dma4(wtile[t] + static_cast<int64_t>(p) * SBB + 256 * i + 4 * lane, dst + t * SBB + 256 * i);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dma16(wcode[t] + static_cast<int64_t>(p) * SBB, dst + t * SBB);
+    }
+    dma4(sb_src0 + static_cast<int64_t>(p) * 128, dst + 4 * SBB);
+    dma4(sb_src1 + static_cast<int64_t>(p) * 128, dst + 4 * SBB + 256);
   };
 
   f32x4_t acc[8][4];
@@ -1321,8 +1343,13 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     uint2 sbv[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
-      sbv[t] = reinterpret_cast<const uint2*>(lb + 4096 + t * 128)[lane & 15];
+      if (FMT == FMT_INT3) {   // the lane's three words
+        const uint32_t* w3 = reinterpret_cast<const uint32_t*>(lb + t * SBB) + 3 * lane;
+        q[t] = u32x4{w3[0], w3[1], w3[2], 0u};
+      } else {
+        q[t] = reinterpret_cast<const u32x4*>(lb + t * 1024)[lane];
+      }
+      sbv[t] = reinterpret_cast<const uint2*>(lb + 4 * SBB + t * 128)[lane & 15];
     }
     DeqSb dsb[4];
     // the group's scale and bias, scaled by 2^e (exact)
@@ -1332,7 +1359,10 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     };
     auto deq_unit = [&](int s, int u, u32x4* bfo) __attribute__((always_inline)) {
       const int t = u >> 2, j = u & 3;
-      bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
+      if constexpr (FMT == FMT_INT3)
+        bfo[t][j] = deq_pair3(q[t].x, q[t].y, q[t].z, 4 * s + j, dsb[t]);
+      else
+        bfo[t][j] = deq_pair(q[t][s], j, dsb[t]);
     };
     u32x4 bf[2][4];
     u32x4 A[NI];
@@ -1367,7 +1397,7 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
     issue(0);
     if (nsb > 1) {
       issue(1);
-      if (a_on) wait_vmcnt<10>(); else wait_vmcnt<6>();
+      if (a_on) wait_vmcnt<4 + NB>(); else wait_vmcnt<NB>();
     } else {
       wait_vmcnt<0>();
     }
@@ -1420,6 +1450,15 @@ __global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
       }
     }
   }
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_kernel(QmmArgs a) {
+  wide_body<FMT_INT4, EPI>(a);
+}
+template <int EPI>
+__global__ void __launch_bounds__(kWdThreads, 1) qmm_wide_int3_kernel(QmmArgs a) {
+  wide_body<FMT_INT3, EPI>(a);
 }
 
 // ---------------------------------------------------------------- fp16 activation copy
@@ -1659,18 +1698,22 @@ static int launch_large(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
 
 // 1-D grid in the XCD-grouped order the wide kernel decodes (as in launch_large, with 512-row
 // weight blocks)
-template <int EPI>
+template <int FMT, int EPI>
 static int launch_wide(const QmmArgs& a, int64_t mtiles, hipStream_t stream) {
+  const void* fn = (FMT == FMT_INT3) ? reinterpret_cast<const void*>(qmm_wide_int3_kernel<EPI>)
+                                     : reinterpret_cast<const void*>(qmm_wide_kernel<EPI>);
+  const size_t lds_bytes = (FMT == FMT_INT3) ? kWd3LdsBytes : kWdLdsBytes;
   const hipError_t err =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_wide_kernel<EPI>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kWdLdsBytes));
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
   if (err != hipSuccess) return fail(std::string("qmm(wide): LDS attribute: ") + hipGetErrorString(err));
   const int nbk = a.n_rows / 512;
   const int G = (nbk >= 32) ? 1 : 32 / nbk;
   const int64_t mpad = (mtiles + 8 * G - 1) / (8 * G) * (8 * G);
   QmmArgs b = a;
   b.mtiles = static_cast<int>(mtiles);
-  qmm_wide_kernel<EPI><<<dim3(static_cast<unsigned>(mpad * nbk)), kWdThreads, kWdLdsBytes, stream>>>(b);
+  const dim3 grid(static_cast<unsigned>(mpad * nbk));
+  if (FMT == FMT_INT3) qmm_wide_int3_kernel<EPI><<<grid, kWdThreads, lds_bytes, stream>>>(b);
+  else qmm_wide_kernel<EPI><<<grid, kWdThreads, lds_bytes, stream>>>(b);
   return 0;
 }
 
@@ -1948,9 +1991,13 @@ int launch_qmm(const QmmArgs& a, int fmt, int epi, int regime, int64_t mtile_bou
     // int4 weights in 512-row blocks (SwiGLU: 256-row gate and up halves; a second activation:
     // blocks on one side of its split) take the wide kernel
     if (fmt == FMT_INT4 && a.n_rows % 512 == 0 && (!two_acts || a.split_tile % 32 == 0)) {
-      if (epi == EPI_SWIGLU) rc = launch_wide<EPI_SWIGLU>(a, mtile_bound, stream);
-      else if (epi == EPI_BF16) rc = launch_wide<EPI_BF16>(a, mtile_bound, stream);
-      else rc = launch_wide<EPI_F32>(a, mtile_bound, stream);
+      if (epi == EPI_SWIGLU) rc = launch_wide<FMT_INT4, EPI_SWIGLU>(a, mtile_bound, stream);
+      else if (epi == EPI_BF16) rc = launch_wide<FMT_INT4, EPI_BF16>(a, mtile_bound, stream);
+      else rc = launch_wide<FMT_INT4, EPI_F32>(a, mtile_bound, stream);
+    } else if (fmt == FMT_INT3 && a.n_rows % 512 == 0 && (!two_acts || a.split_tile % 32 == 0)) {
+      if (epi == EPI_SWIGLU) rc = launch_wide<FMT_INT3, EPI_SWIGLU>(a, mtile_bound, stream);
+      else if (epi == EPI_BF16) rc = launch_wide<FMT_INT3, EPI_BF16>(a, mtile_bound, stream);
+      else rc = launch_wide<FMT_INT3, EPI_F32>(a, mtile_bound, stream);
     } else if (fmt == FMT_INT4) {
       if (epi == EPI_SWIGLU) QMOE_LARGE(FMT_INT4, EPI_SWIGLU);
       else if (epi == EPI_BF16) QMOE_LARGE(FMT_INT4, EPI_BF16);
