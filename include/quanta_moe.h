@@ -122,8 +122,8 @@ typedef struct {
   int32_t awq;           /* 1: the quantized experts carry activation-aware scales (weights'
                             awq_gu / awq_dn, DeepSeek-V4, src/quanta/dsv4/moe.py:112-137): the
                             activation is divided by the expert's per-input-channel scale before
-                            each projection; the large regime needs int4 experts and inter %
-                            256 == 0 (else the small regime runs every batch size) */
+                            each projection; the large regime needs inter % 256 == 0 (else
+                            the small regime runs every batch size) */
   int32_t mixed;         /* 1: routed experts of mixed widths per (expert, projection), passed to
                             qmoe_forward_mixed (weights' gu/dn fields unused); small regime only */
   int32_t shared_format; /* QMOE_FMT_BF16 or QMOE_FMT_INT8_G64: the shared expert's weights.

@@ -447,11 +447,11 @@ static int kernel_fmt(int f) {
   return f == QMOE_FMT_INT4_G64 ? FMT_INT4 : f == QMOE_FMT_INT6_G64 ? FMT_INT6
          : f == QMOE_FMT_INT3_G64 ? FMT_INT3 : f == QMOE_FMT_INT8_G64 ? FMT_INT8 : FMT_BF16;
 }
-// AWQ-scaled experts in the large regime: int4 weights, and gate and up halves that split at a
-// whole 256-row block (the large kernels pick the activation copy per weight-row block)
+// AWQ-scaled experts in the large regime: quantized weights (awq implies them), and gate and up
+// halves that split at a whole 256-row block (the large kernels pick the activation copy per
+// weight-row block)
 static bool awq_large_ok(const qmoe_config_t& c) {
-  return c.expert_format == QMOE_FMT_INT4_G64 && c.down_format == QMOE_FMT_INT4_G64 &&
-         c.inter % 256 == 0;
+  return c.expert_format != QMOE_FMT_BF16 && c.down_format != QMOE_FMT_BF16 && c.inter % 256 == 0;
 }
 
 // formats the large-regime kernels dequantize to fp16 (an fp16 activation copy, row exponents)
@@ -507,7 +507,7 @@ static int validate_config(const qmoe_config_t& c) {
   if (c.awq && c.expert_format == QMOE_FMT_BF16)
     return fail("config: awq scales need quantized experts");
   if (c.awq && c.regime == QMOE_REGIME_LARGE && !awq_large_ok(c))
-    return fail("config: awq scales in the large regime need int4 experts and inter % 256 == 0");
+    return fail("config: awq scales in the large regime need inter % 256 == 0");
   if (c.mixed != 0 && c.mixed != 1) return fail("config: mixed must be 0 or 1");
   if (c.mixed && c.awq) return fail("config: mixed-width experts run without awq scales");
   if (c.router_format == QMOE_ROUTER_BF16_TILED) {

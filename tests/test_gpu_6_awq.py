@@ -4,8 +4,8 @@ The block divides each routed row's activation by its expert's per-input-channel
 the gate, the up and the down projection (qmoe_config_t.awq; kernels in awq.hip; gate_up as one
 launch whose up-half wavefronts read the rows prescaled for the up projection).
 
-Above 256 tokens int4 layers whose intermediate size is a multiple of 256 take the large
-regime: the hot experts' gate_up on the prefill (MFMA) kernels, each 256- or 512-row weight
+Above 256 tokens layers whose intermediate size is a multiple of 256 take the large regime
+(int3 gate/up with int4 down included, test_awq_block_vs_oracle at N = 300): the hot experts' gate_up on the prefill (MFMA) kernels, each 256- or 512-row weight
 block reading the fp16 copy of the gate's or the up projection's prescaled rows.
 
 Bars: unit scales give the plain path's output bit for bit in both regimes (same per-output
