@@ -125,7 +125,11 @@ typedef struct {
                             each projection; the large regime needs inter % 256 == 0 (else
                             the small regime runs every batch size) */
   int32_t mixed;         /* 1: routed experts of mixed widths per (expert, projection), passed to
-                            qmoe_forward_mixed (weights' gu/dn fields unused); small regime only */
+                            qmoe_forward_mixed; both regimes (above 256 tokens every stack needs
+                            qmoe_stack_t.row_exp). The weights' gu/dn fields are then unused and
+                            expert_format / down_format are placeholders (any pair the config
+                            check accepts, bf16 included): the stacks' formats pick every
+                            kernel */
   int32_t shared_format; /* QMOE_FMT_BF16 or QMOE_FMT_INT8_G64: the shared expert's weights.
                             int8 weights are dequantized in registers to bf16(s*q + b), the bf16
                             weights the reference's loader makes of them
@@ -151,11 +155,11 @@ typedef struct {
   const uint16_t* awq_gu;         /* config awq: bf16 [E, 2, H] input-channel scales of the gate
                                      (row 0) and up (row 1) projections, else NULL */
   const uint16_t* awq_dn;         /* config awq: bf16 [E, I] scales of the down projection */
-  const int8_t* gu_rexp;          /* int4 gate|up: per weight row [E, 2I] power-of-two exponent
-                                     (qmoe_row_exponents) for the prefill kernels' fp16 dequant;
-                                     required when a call reaches the large regime (N > 256), may
-                                     be NULL for decode-only use */
-  const int8_t* dn_rexp;          /* int4 down: per weight row [E, H], as gu_rexp */
+  const int8_t* gu_rexp;          /* int3/int4/int6 gate|up: per weight row [E, 2I] power-of-two
+                                     exponent (qmoe_row_exponents) for the prefill kernels' fp16
+                                     dequant; required when a call reaches the large regime
+                                     (N > 256), may be NULL for decode-only use */
+  const int8_t* dn_rexp;          /* int3/int4/int6 down: per weight row [E, H], as gu_rexp */
 } qmoe_weights_t;
 
 int qmoe_abi_version(void);

@@ -759,9 +759,10 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // hybrid prefill with int4 experts: the hot experts' gate_up reads an fp16 copy of x, made
   // first on the auxiliary stream, beside the routing chain (hybrid implies int4 or bf16 experts;
   // AWQ: copies of the prescaled rows instead, made after the permute), and their down an fp16
-  // copy of h
-  const bool f16_acts = (hybrid && fp16_large_fmt(gfmt) && !c.awq);
-  const bool f16_h = (hybrid && fp16_large_fmt(dfmt));
+  // copy of h. A mixed-width layer's stacks are all int3, int4 or int6 (validate_mixed), whatever
+  // placeholder formats the config carries, so its prefill kernels always read the copies.
+  const bool f16_acts = hybrid && !c.awq && (mixed || fp16_large_fmt(gfmt));
+  const bool f16_h = hybrid && (mixed || fp16_large_fmt(dfmt));
   if (f16_acts) {
     rc = launch_act_to_f16(x, N, c.hidden, x16, x_sinv, aux ? aux->s : stream);
     if (rc) return rc;

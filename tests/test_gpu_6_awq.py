@@ -92,6 +92,27 @@ def test_awq_large_regime_vs_oracle(gpu, E, I, N, H):
     assert_close(f64(y), it["y_exact"], f"awq large regime E={E} I={I} N={N} H={H}")
 
 
+@pytest.mark.parametrize("gu_bits,dn_bits,I", [(3, 4, 512), (6, 4, 256), (4, 6, 256)])
+def test_awq_narrow_widths_large_regime_vs_oracle(gpu, gu_bits, dn_bits, I):
+    """AWQ scales on int3 and int6 stacks above 256 tokens, hot and cold experts (E = 32): int3
+    gate_up at I = 512 runs the 512-row int3 kernel with its gate and up blocks reading their own
+    prescaled rows (split_tile a multiple of 32); int6 gate_up, and int6 down, on the 256-row
+    kernel."""
+    E, N, H = 32, 300, 512
+    cfg = _cfg(E, I, H)
+    base = _layer_widths(gpu, 64, 47 * gu_bits + I + dn_bits, gu_bits, dn_bits, H=H, E=E, I=I)
+    base.pop("shared_expert_gate", None)
+    p = _with_awq(base, gpu, seed=53 * gu_bits + I, E=E, H=H, I=I)
+    x = _inputs(gpu, N, H, N)
+    y = qwen35_moe(x[None], p, cfg)[0]
+    _, it = om.moe_forward(f64(x), oracle_params_from_torch(p), k=2, inter=I, scoring="sigmoid",
+                           norm_topk=True, scale=1.5, act="silu", limit=LIMIT, group_size=64,
+                           bits=gu_bits, down_bits=dn_bits)
+    counts = np.bincount(it["idx"].reshape(-1), minlength=E)
+    assert counts.max() > 16 and counts.min() <= 16, "the layer must hold hot and cold experts"
+    assert_close(f64(y), it["y_exact"], f"awq int{gu_bits}/int{dn_bits} large regime I={I} N={N}")
+
+
 @pytest.mark.parametrize("gs,gu_bits,dn_bits", [(64, 4, 4), (128, 4, 4), (128, 3, 4)])
 @pytest.mark.parametrize("N", [1, 8, 40, 300])
 def test_awq_block_vs_oracle(gpu, gs, gu_bits, dn_bits, N):

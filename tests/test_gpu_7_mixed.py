@@ -159,6 +159,36 @@ def test_mixed_gate_up_drawn_together_vs_oracle(gpu, case, N):
     assert_close(f64(y), it["y_exact"], f"mixed gate/up together {case} N={N}")
 
 
+def test_mixed_bf16_placeholder_formats_large_regime(gpu):
+    """qmoe_forward_mixed ignores the config's expert_format / down_format (placeholders of a
+    mixed layer): a C caller passing bf16 there still gets the prefill kernels' fp16 activation
+    copies above 256 tokens, and the output of the int4 placeholders, bit for bit."""
+    import ctypes
+
+    from quanta_amd import ops
+    from quanta_amd.moe import prepare
+
+    n_exp, N = 32, 300
+    rng = np.random.default_rng(9)
+    widths = {"gate": np.full(n_exp, 3), "up": np.full(n_exp, 3),
+              "down": rng.choice([3, 4], n_exp, p=[0.2, 0.8])}
+    cfg = MoEConfig(H, n_exp, 2, I, 256)
+    p, om_mixed = _layer_mixed(gpu, 77, widths, n_exp=n_exp)
+    x = _inputs(gpu, N, H, N)
+    pr = prepare(p, cfg)
+    y_int4 = ops.forward(pr.cfg, pr.weights, x, mixed=pr.mixed)
+    c16 = type(pr.cfg).from_buffer_copy(pr.cfg)
+    c16.expert_format = c16.down_format = L.FMT_BF16
+    ws = torch.full((ops.forward_workspace(c16, N),), 0x7F, dtype=torch.uint8, device=gpu)
+    y_bf16 = ops.forward(c16, pr.weights, x, ws=ws, mixed=pr.mixed)
+    torch.cuda.synchronize()
+    _, it = om.moe_forward(f64(x), _oracle(p, om_mixed), k=2, inter=I)
+    counts = np.bincount(it["idx"].reshape(-1), minlength=n_exp)
+    assert counts.max() > 16 and counts.min() <= 16, "the layer must hold hot and cold experts"
+    assert torch.equal(y_bf16, y_int4)
+    assert_close(f64(y_bf16), it["y_exact"], f"mixed bf16 placeholders N={N}")
+
+
 def test_mixed_argument_errors(gpu):
     cfg = MoEConfig(H, E, 2, I, 256)
     widths = {k: np.full(E, 4) for k in ("gate", "up", "down")}

@@ -61,7 +61,8 @@ def test_prefill_tiny_weight_scales(gpu, std, N):
     x = (torch.randn(N, H, generator=torch.Generator().manual_seed(N)) * 4).to(torch.bfloat16).to(gpu)
     y = _check(p, cfg, x, f"prefill std={std:g} N={N}")
     y_small = qwen35_moe(x[None], p, cfg, regime=L.REGIME_SMALL)[0]
-    assert_close(f64(y), f64(y_small), f"prefill std={std:g} N={N}: large vs small regime")
+    assert_close(f64(y), f64(y_small), f"prefill std={std:g} N={N}: large vs small regime",
+                 want_rounded=True)
 
 
 @pytest.mark.parametrize("N", [300, 700])
