@@ -55,25 +55,30 @@ def raw_max_abs(got, want) -> float:
     return float(np.max(np.abs(d))) if d.size else 0.0
 
 
-# Below these output magnitudes the raw (unscaled) max-abs gate is asserted as well. Against the
-# oracle's unrounded result a correctly rounded bf16 output is off by at most half an ulp, 2^-7
-# below 4; two bf16-rounded results (want_rounded) can sit an ulp or two apart, 2^-7 each below 2.
-RAW_GATE_PEAK = 4.0
-RAW_GATE_PEAK_ROUNDED = 2.0
+# Below these output magnitudes the raw (unscaled) max-abs gate, |got - want| <= max_abs, is
+# asserted as well. The bf16 output carries half an ulp of rounding, and the reference's bf16
+# intermediates (gate/up, h, d) flip to the neighbouring bf16 value wherever float32 and float64
+# evaluation straddle a rounding boundary, each flip moving the output by up to an ulp of that
+# intermediate. Below 2 an ulp is 2^-7, so a correct result sits far inside 2e-2 even with
+# flips; below 4 (ulp 2^-6) it still does at the BASELINE shapes and inputs (x ~ N(0,1), weights
+# N(0,0.02); _full_parity passes raw_peak=4), while the stress layers of the format tests (x
+# scaled by 4) can sum two flips to 1.5 ulps there. Above, the gate scales with max|want|.
+RAW_GATE_PEAK = 2.0
+RAW_GATE_PEAK_BASELINE = 4.0
 
 
-def assert_close(got, want, what="", max_abs=MAX_ABS, rel_l2=REL_L2, want_rounded=False):
+def assert_close(got, want, what="", max_abs=MAX_ABS, rel_l2=REL_L2, want_rounded=False,
+                 raw_peak=RAW_GATE_PEAK):
     """`want` should be the oracle's unrounded (float64) result: the GPU's bf16 output then
     carries exactly one rounding, not two. want_rounded: `want` is itself a bf16 output (another
-    path of this build).
+    path of this build), which caps the raw gate at RAW_GATE_PEAK.
 
-    Asserts the scaled max-abs and relative-L2 gates always, and the raw max-abs gate
-    (|got - want| <= max_abs, the north-star bound as written) whenever max|want| lies below
-    RAW_GATE_PEAK (RAW_GATE_PEAK_ROUNDED for a rounded `want`)."""
+    Asserts the scaled max-abs and relative-L2 gates always, and the raw max-abs gate (the
+    north-star bound as written) whenever max|want| lies below raw_peak."""
     ma, rl = metrics(got, want)
     raw = raw_max_abs(got, want)
     peak = float(np.max(np.abs(want))) if np.size(want) else 0.0
-    raw_on = peak < (RAW_GATE_PEAK_ROUNDED if want_rounded else RAW_GATE_PEAK)
+    raw_on = peak < (min(raw_peak, RAW_GATE_PEAK) if want_rounded else raw_peak)
     print(f"[parity] {what}: max_abs(scaled)={ma:.3e} max_abs(raw)={raw:.3e} max|want|={peak:.3g} "
           f"rel_l2={rl:.3e} raw_gate={'on' if raw_on else 'off'}", flush=True)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"

@@ -21,8 +21,8 @@ from quanta_amd import _lib as L
 from quanta_amd import ops, synth
 from quanta_amd.moe import MoEConfig, Qwen35MoEModule, qwen35_moe, qwen35_route
 from tests import _gpu_ref as gpu_ref
-from tests._util import (assert_close, bf16_dev, bits_np, f64, oracle_params_from_torch,
-                         words_dev, words_np)
+from tests._util import (RAW_GATE_PEAK_BASELINE, assert_close, bf16_dev, bits_np, f64,
+                         oracle_params_from_torch, words_dev, words_np)
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -54,7 +54,7 @@ def _fixture(name, dev):
 def test_block_golden(gpu, name):
     a, cfg, p, x = _fixture(name, gpu)
     y = qwen35_moe(x[None], p, cfg)[0]
-    assert_close(f64(y), a["y_exact"], f"golden {name}")
+    assert_close(f64(y), a["y_exact"], f"golden {name}", raw_peak=RAW_GATE_PEAK_BASELINE)
     idx, w = qwen35_route(x, p["gate"], cfg,
                           e_score_correction_bias=p.get("e_score_correction_bias"))
     ok = a["margin"] > 1e-6
@@ -252,7 +252,7 @@ def _full_parity(gpu, name, p, cfg, x, y, *, sample=3, tie_tol=1e-5):
     toks = sorted({0, N // 2, N - 1})[:sample] if N > 2 else list(range(N))
     gpu_ref.pin_to_oracle(y_ref[toks], _oracle_tokens(p, cfg, x64, toks, idx_ref, w_ref),
                           f"{name} N={N} tokens {toks}")
-    assert_close(f64(y), y_ref, f"{name} N={N}, all {N} tokens")
+    assert_close(f64(y), y_ref, f"{name} N={N}, all {N} tokens", raw_peak=RAW_GATE_PEAK_BASELINE)
 
 
 @pytest.mark.parametrize("name,N", [("c1", 1), ("c1", 8), ("c1", 32), ("c1", 64),
