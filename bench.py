@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--shared", choices=("int8", "bf16"), default="int8",
                     help="shared-expert weights: int8 g64 as the bake stores them (dequantized in "
                          "registers to the bf16 weights the reference loads; same outputs) or bf16")
+    ap.add_argument("--no-flow", action="store_true",
+                    help="launch the decode stages one by one (qmoe_set_decode_flow(0)) instead of "
+                         "the one dataflow launch after the router")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")
@@ -171,6 +174,8 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     L.load()
+    if args.no_flow:
+        L.load().qmoe_set_decode_flow(0)
     dev = torch.device("cuda", 0)
     spec = synth.spec(args.config)
     cfg = spec.cfg

@@ -185,6 +185,20 @@ int qmoe_forward(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16
 int qmoe_forward_noalloc(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x,
                          int64_t N, uint16_t* y, void* stream);
 
+/* Decode dataflow launch (tuning and diagnostics; no counterpart in the reference, whose MLX
+ * graph schedules its primitives itself). Decode batches routed slot-major, with int4 experts, a
+ * bf16 router and a shared expert, can run everything after the router launch (top-k, routed
+ * gate_up and down, shared down, combine) as one launch whose units wait on each other through
+ * counters in the workspace; the outputs equal the multi-launch path's bit for bit.
+ * Mode 1 (the default) takes it for one- and two-token calls, where it is the faster path;
+ * qmoe_set_decode_flow(0) makes later calls launch the stages one by one, (2) takes the single
+ * launch for every batch it covers (up to the slot-major sizes; for tests and measurements). It
+ * returns the previous mode (process-wide, not thread-safe against calls in flight).
+ * qmoe_flow_timeouts() returns how many in-kernel waits have run out of their bound on the
+ * current device since the library loaded (0 in a healthy run; synchronous). */
+int qmoe_set_decode_flow(int mode);
+uint32_t qmoe_flow_timeouts(void);
+
 /* Routed experts whose widths vary per (expert, projection) (Kimi's QuantizedSparseMoE,
  * src/quanta/modeling/quantized.py:40-84: one packed stack per projection and width, each expert
  * carrying per projection its width and its slot in that width's stack). Each stack is tiled as

@@ -140,6 +140,8 @@ SIGNATURES = {
     "qmoe_tile_int8": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_int3": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_bf16": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+    "qmoe_set_decode_flow": (_I, [_I]),
+    "qmoe_flow_timeouts": (ctypes.c_uint32, []),
 }
 
 _lock = threading.Lock()

@@ -15,6 +15,7 @@
 #include <string>
 
 #include "qmoe_internal.h"
+#include "flow.h"
 #include "../../include/quanta_moe.h"
 
 namespace qmoe {
@@ -379,8 +380,8 @@ static bool shared_expands(const qmoe_config_t& c, int64_t N) {
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
   size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, tile_map_big, sorted, inv, h,
-      d, sh_h, sh_out, sh_w16, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, total;
-  int64_t max_tiles, max_tiles_big;
+      d, sh_h, sh_out, sh_w16, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, sync, total;
+  int64_t max_tiles, max_tiles_big, sync_words;
 };
 
 static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
@@ -429,6 +430,9 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.awq_x = take(c.awq ? static_cast<size_t>(2) * mc * c.hidden * 2 : 0);
   // (mixed widths also route gate and up through awq_gu)
   L.awq_gu = take((c.awq || c.mixed) ? static_cast<size_t>(mc) * 2 * c.inter * 2 : 0);
+  // the decode dataflow kernel's counters (cleared by the router launch of every call)
+  L.sync_words = decode_flow_sync_words(mc, c.hidden);
+  L.sync = take(static_cast<size_t>(L.sync_words) * 4);
   L.total = o;
   return L;
 }
@@ -829,6 +833,14 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (rc) return rc;
   }
 
+  // Decode batches with int4 experts whose shared expert rides in the router launch: everything
+  // after that launch (top-k, permute, routed gate_up and down, shared down, combine) runs as one
+  // dataflow launch (flow.hip), whose counters the router launch clears. Same outputs, bit for bit.
+  const bool use_flow = fuse_gu && slot_major && !mixed && gfmt == FMT_INT4 && dfmt == FMT_INT4 &&
+                        decode_flow_enabled(n) &&
+                        decode_flow_fits(n, c.top_k, c.n_experts, c.hidden, c.inter, c.shared_inter);
+  uint32_t* sync = reinterpret_cast<uint32_t*>(base + L.sync);
+
   // 2. router logits (+ the shared-expert gate logit in column E)
   int ld = 0;
   if (c.router_format == QMOE_ROUTER_F32) {
@@ -853,12 +865,30 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     // as many workgroups)
     const int rt = decode ? st : 64;
     if (!decode) a.dense_mtile = rt;
+    if (use_flow) {
+      a.zero_words = sync;
+      a.n_zero = static_cast<int>(L.sync_words / kSyncStride);
+    }
     if (fuse_gu)
       rc = launch_qmm_pair_bf16(a, sgu, stream, sfmt);
     else
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + rt - 1) / rt, stream);
   }
   if (rc) return rc;
+  if (use_flow) {
+    FlowLaunch F{};
+    F.x = x; F.N = n; F.k = c.top_k; F.H = c.hidden; F.I = c.inter; F.Is = c.shared_inter;
+    F.logits = logits; F.ld = ld;
+    F.P = topk_params(wts->router_bias, c.n_experts, c.top_k, c.scoring, c.n_group, c.topk_group,
+                      c.norm_topk, c.routed_scale, has_sg);
+    F.gu_codes = wts->gu_codes; F.gu_sb = wts->gu_sb; F.dn_codes = wts->dn_codes; F.dn_sb = wts->dn_sb;
+    F.glu = c.act; F.glu_alpha = c.act_alpha; F.glu_limit = c.act_limit;
+    F.sh_h = sh_h; F.sh_dn = sh_dn_w; F.sh_dn_sb = sh8 ? wts->sh_dn_sb : nullptr; F.sfmt = sfmt;
+    F.w = wv; F.sg = sg;
+    F.h = h; F.d = d; F.sh_out = sh_out; F.sync = sync;
+    F.resid = resid; F.y = y;
+    return launch_decode_flow(F, stream);
+  }
   // slot-major int4 SwiGLU experts: the top-k runs inside the routed gate_up launch (one
   // wavefront per workgroup ranks its slot's token), while the launch has few enough workgroups
   const bool route_in_gate_up =

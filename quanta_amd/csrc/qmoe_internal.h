@@ -235,6 +235,11 @@ struct QmmArgs {
   int dense_mtile;            // large regime, one dense segment: rows per m-tile (16..128, a
                               // multiple of 16; 0 = 128), so a short product still spreads
                               // over enough workgroups
+  const uint32_t* act_ready;  // decode dataflow kernel: per m-tile counters (kSyncStride words
+  uint32_t act_ready_target;  // apart) of the activation rows' producers; complete at the target
+  uint32_t* timeouts;         // where a bounded wait that ran out is counted
+  uint32_t* zero_words;       // dense pair launch, nullable: n_zero counters (kSyncStride words
+  int n_zero;                 // apart) its first workgroup clears for the dataflow kernel after it
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3, FMT_INT8 = 4 };
@@ -394,6 +399,10 @@ int launch_down_combine(const uint16_t* h, const int32_t* idx, const float* w, c
                         const uint16_t* sh_h, int Is, const void* wd, const uint16_t* wd_sb,
                         int sfmt, const uint16_t* resid, uint16_t* y, hipStream_t stream,
                         const uint16_t* sh_out = nullptr);
+
+// Counters of the decode dataflow kernel sit kSyncStride words apart (256 bytes): polls and
+// atomics of one counter then never queue behind another's on the same cache line.
+constexpr int kSyncStride = 64;
 
 constexpr int kSmallMTile = 16;
 constexpr int kLargeMTile = 128;

@@ -211,3 +211,12 @@ def test_forward_rejects_bad_awq_config():
     cfg1 = L.QmoeConfig(expert_format=0, down_format=0, awq=1, regime=0, **base)
     extra = lib.qmoe_forward_workspace(ctypes.byref(cfg1), 5) - lib.qmoe_forward_workspace(ctypes.byref(cfg0), 5)
     assert extra >= 2 * 10 * 512 * 2 + 10 * 256 * 2
+
+
+def test_decode_flow_mode_switch_returns_previous():
+    lib = L.load()
+    assert lib.qmoe_set_decode_flow(0) == 1
+    assert lib.qmoe_set_decode_flow(1) == 0
+    assert lib.qmoe_set_decode_flow(2) == 1
+    assert lib.qmoe_set_decode_flow(7) == 2   # unknown modes leave the mode as it was
+    assert lib.qmoe_set_decode_flow(1) == 2
