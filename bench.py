@@ -408,7 +408,9 @@ def main():
             log(f"sweep {rec}")
 
         if "residual" in args.extra:
-            m2, u2, _, _ = run_batch(N, max(100, args.steps // 4), 3, min(args.pool, 8), residual=True)
+            # (the same steps, warm-up and input pool as the headline loop, so the two lines
+            # differ only by the norm and the residual add)
+            m2, u2, _, _ = run_batch(N, args.steps, args.warmup, args.pool, residual=True)
             record(f"{args.config}-N{N}-residual", m2, u2, extra_bytes=2 * H)
         # int6: MiniMax M3's experts; int3: Kimi's widths (gate_up int3 + down int4, group 128).
         # Two copies suffice to stream from HBM: one step touches U experts x 6-10 MB.
