@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 8
+#define QMOE_ABI_VERSION 9
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -248,6 +248,64 @@ size_t qmoe_forward_residual_workspace(const qmoe_config_t* cfg, int64_t N);
 int qmoe_forward_residual(const qmoe_config_t* cfg, const qmoe_weights_t* w, const uint16_t* x,
                           const uint16_t* norm_w, float eps, int64_t N, uint16_t* y, void* ws,
                           size_t ws_bytes, void* stream);
+
+/* ---- the block at the reference's own dtypes and group sizes ----
+ * qmoe_forward requires bf16 activations, bf16 scale/bias, group 64/128 and dimensions that are
+ * multiples of 128. The reference's block takes any float dtype the caller baked: its
+ * packed-expert parity gate (parity/qwen35_forward_test.py:213-271) runs float32 activations
+ * with float32 scale/bias, int4 group 32, hidden 32 and moe_intermediate 64, and its
+ * sparse-vs-dense gate (parity/qwen35_forward_test.py:192-209) float32 dense stacks at
+ * moe_intermediate 16. qmoe_forward_general runs those, following the reference's dtype flow
+ * (src/quanta/qwen35/moe.py:36-56, 66-124, 145-151, 154-202):
+ *   logits = f32(x) @ f32(gate)^T (+ column E = the shared gate logit); top-k as qmoe_router_topk
+ *   routed experts in dtype T: a dense stack's dtype (x cast to it), or for packed codes the
+ *     promotion of x's and the scales' dtypes (f32 if either is); gate_up, SwiGLU, down each
+ *     rounded to T; codes any width 2..6 or 8, LSB-first bitstream rows, groups 32/64/128
+ *   routed = sum_s f32(d) * w;  shared = f32(down(glu(xs Wg^T, xs Wu^T))) * sigmoid(f32(x) .
+ *     f32(shared_expert_gate)), xs = x cast to the shared weights' dtype
+ *   y = cast to x's dtype (routed + shared)
+ * Every product accumulates in fp32 with one wavefront per output value; a matvec kernel for
+ * small and odd shapes, not the production path. dense_all = 1 is the run-every-expert form
+ * (qwen35_moe(sparse=False), src/quanta/qwen35/moe.py:127-142; dense stacks only). */
+#define QMOE_DT_BF16 0
+#define QMOE_DT_F32 1
+
+typedef struct {
+  int32_t hidden, n_experts, top_k, inter, shared_inter;  /* shared_inter 0: no shared expert */
+  int32_t scoring, norm_topk, n_group, topk_group;        /* as qmoe_config_t */
+  float routed_scale;
+  int32_t act;                /* QMOE_ACT_* with act_alpha, act_limit as in qmoe_config_t */
+  float act_alpha, act_limit;
+  int32_t x_dtype;            /* QMOE_DT_* of x and y */
+  int32_t gate_dtype;         /* router weight [E, H] */
+  int32_t experts_packed;     /* 1: affine codes + scale/bias; 0: dense stacks */
+  int32_t expert_dtype;       /* dense stacks' dtype, or the packed scale/bias dtype */
+  int32_t bits, group_size;   /* packed codes: 2..6 or 8 bits, groups of 32, 64 or 128 */
+  int32_t shared_dtype;       /* shared gate/up/down weights */
+  int32_t shared_gated;       /* 1: sh_expert_gate [1, H] scales the shared expert */
+  int32_t shared_gate_dtype;
+  int32_t dense_all;          /* 1: run every expert (sparse=False) */
+} qmoe_general_config_t;
+
+typedef struct {
+  const void* gate;           /* [E, H] */
+  const float* router_bias;   /* [E] correction bias for selection, or NULL */
+  const void* gu;             /* packed [E, 2I, H*bits/32] uint32, or dense [E, 2I, H] */
+  const void* gu_scale;       /* [E, 2I, H/gs] (packed only) */
+  const void* gu_bias;
+  const void* dn;             /* packed [E, H, I*bits/32], or dense [E, H, I] */
+  const void* dn_scale;       /* [E, H, I/gs] */
+  const void* dn_bias;
+  const void* sh_gate;        /* [Is, H] */
+  const void* sh_up;          /* [Is, H] */
+  const void* sh_down;        /* [H, Is] */
+  const void* sh_expert_gate; /* [1, H] */
+} qmoe_general_weights_t;
+
+size_t qmoe_forward_general_workspace(const qmoe_general_config_t* cfg, int64_t N);
+int qmoe_forward_general(const qmoe_general_config_t* cfg, const qmoe_general_weights_t* w,
+                         const void* x, int64_t N, void* y, void* ws, size_t ws_bytes,
+                         void* stream);
 
 /* RMSNorm rows alone (the same arithmetic as qmoe_forward_residual's norm):
  * out[t] = bf16(w * (x[t] * rsqrt(mean(x[t]^2) + eps))), fp32 math, H % 8 == 0. Replaces

@@ -19,7 +19,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle.quant import bf16_bits_to_f32, dequant_bf16_bits, dequant_exact, round_bf16
+from oracle.quant import (bf16_bits_to_f32, dequant_bf16_bits, dequant_exact, dequant_float,
+                          round_bf16)
 
 
 def _silu(v: np.ndarray) -> np.ndarray:
@@ -390,3 +391,100 @@ def moe_dense_reference(x: np.ndarray, idx: np.ndarray, w: np.ndarray, gu_dense:
     rows = np.repeat(np.arange(n), idx.shape[1])
     gates[rows, idx.reshape(-1)] = w.reshape(-1)
     return (d * gates[:, :, None]).sum(axis=1)
+
+
+# ----------------------------------------------------------------------------- reference dtypes
+
+
+def round_to(v: np.ndarray, dt: str) -> np.ndarray:
+    """v materialised in dtype dt: "f32" (float32 round to nearest even) or "bf16"."""
+    if dt == "bf16":
+        return round_bf16(v)
+    if dt == "f32":
+        return np.asarray(v, dtype=np.float64).astype(np.float32).astype(np.float64)
+    raise ValueError(f"unknown dtype {dt!r}")
+
+
+def moe_forward_general(x: np.ndarray, p: dict, *, k: int, inter: int, x_dtype: str = "f32",
+                        dense_all: bool = False, scoring: str = "softmax", norm_topk: bool = True,
+                        n_group: int = 1, topk_group: int = 1, scale: float = 1.0,
+                        act: str = "silu", alpha: float = 1.702, limit: float = 0.0,
+                        norm_single: bool = True):
+    """The block at the reference's own dtype flow, for float32 or bf16 data
+    (`src/quanta/qwen35/moe.py:36-56, 66-124, 145-151, 154-202`):
+      logits = f32(x) @ f32(gate)^T, routing as `route`
+      routed experts in dtype T: dense stacks' dtype (x cast to it, :77), or for packed codes the
+        promotion of x's and the scales' dtypes (the qmm output follows the scale dtype, :98-104;
+        float32 if either is float32)
+      gu = T(x_T . W^T); h = T(glu(g, u)); d = T(h . W_d^T)   (one rounding per op here)
+      routed = sum_s d * w (float32 in the reference, float64 here)
+      shared = T_s(T_s(glu(T_s(x_s Wg^T), T_s(x_s Wu^T))) Wd^T) * sigmoid(x . g), x_s = x cast to
+        the shared weights' dtype T_s (:145-151)
+      y = cast to x's dtype (routed + shared) (:201-202)
+    With `dense_all` every expert runs on every token and the combine weights are the routing
+    weights scattered onto the chosen experts, zero elsewhere (the sparse=False oracle, :127-142).
+
+    `p` keys: gate [E,H]; packed experts: gu_packed, dn_packed (uint32 words), gu_scale, gu_bias,
+    dn_scale, dn_bias (float arrays holding float32 or bf16 values), "bits", "group_size",
+    "sb_dtype"; or dense experts: gu_dense [E,2I,H], dn_dense [E,H,I] and "expert_dtype";
+    optional shared_gate_proj/shared_up_proj [Is,H], shared_down_proj [H,Is], "shared_dtype",
+    shared_expert_gate [1,H]; optional e_score_correction_bias [E]. Float arrays hold values
+    exactly representable in their stated dtypes. Returns (y float64 in x's dtype, dict).
+    """
+    n, hdim = x.shape
+    idx, w, logits, scores, choice = route(
+        x, p["gate"], k=k, scoring=scoring, norm_topk=norm_topk,
+        bias=p.get("e_score_correction_bias"), n_group=n_group, topk_group=topk_group,
+        scale=scale, norm_single=norm_single)
+    packed = "gu_packed" in p
+    if packed:
+        T = "f32" if "f32" in (x_dtype, p["sb_dtype"]) else "bf16"
+        bits, gs = int(p["bits"]), int(p["group_size"])
+    else:
+        T = p["expert_dtype"]
+    E = p["gate"].shape[0]
+    if dense_all:
+        if packed:
+            raise ValueError("the run-every-expert form takes dense stacks")
+        ks = E
+        exp = np.tile(np.arange(E), n)
+        wk = np.zeros((n, E))
+        wk[np.repeat(np.arange(n), k), idx.reshape(-1)] = w.reshape(-1)
+    else:
+        ks, exp, wk = k, idx.reshape(-1), w
+    tok = np.repeat(np.arange(n), ks)
+    xr = round_to(x[tok].astype(np.float64), T)
+
+    def weight(proj: str, e: int, in_features: int) -> np.ndarray:
+        if packed:
+            return dequant_float(p[f"{proj}_packed"][e], p[f"{proj}_scale"][e], p[f"{proj}_bias"][e],
+                                 in_features, bits=bits, group_size=gs)
+        return np.asarray(p[f"{proj}_dense"][e], dtype=np.float64)
+
+    gu = np.zeros((n * ks, 2 * inter))
+    for e in np.unique(exp):
+        sel = exp == e
+        gu[sel] = xr[sel] @ weight("gu", e, hdim).T
+    gu = round_to(gu, T)
+    h = round_to(glu(gu[:, :inter], gu[:, inter:], act, alpha, limit), T)
+    d = np.zeros((n * ks, hdim))
+    for e in np.unique(exp):
+        sel = exp == e
+        d[sel] = h[sel] @ weight("dn", e, inter).T
+    d = round_to(d, T)
+    routed = combine(d, wk)
+    y = routed.copy()
+    sh = None
+    if p.get("shared_gate_proj") is not None:
+        S = p["shared_dtype"]
+        xs = round_to(x.astype(np.float64), S)
+        g = round_to(xs @ np.asarray(p["shared_gate_proj"], dtype=np.float64).T, S)
+        u = round_to(xs @ np.asarray(p["shared_up_proj"], dtype=np.float64).T, S)
+        hh = round_to(glu(g, u, act, alpha, limit), S)
+        out = round_to(hh @ np.asarray(p["shared_down_proj"], dtype=np.float64).T, S)
+        sgw = p.get("shared_expert_gate")
+        sh = out if sgw is None else out * _sigmoid(x.astype(np.float64) @ np.asarray(sgw, dtype=np.float64).reshape(-1))[:, None]
+        y = y + sh
+    inter_d = dict(idx=idx, w=w, logits=logits, scores=scores, choice=choice, gu=gu, h=h, d=d,
+                   routed=routed, shared=sh, y_exact=y, routed_dtype=T)
+    return round_to(y, x_dtype), inter_d

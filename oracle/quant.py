@@ -135,6 +135,25 @@ def quantize_rtn(w: np.ndarray, bits: int = 4, group_size: int = 64):
 # ----------------------------------------------------------------------------- dequantize
 
 
+def quantize_rtn_f32(w: np.ndarray, bits: int = 4, group_size: int = 32):
+    """quantize_rtn with float32 scale and bias (the layout mx.quantize gives float32 weights,
+    `parity/qwen35_forward_test.py:236-237`): per group, scale = f32((max-min)/(2^bits-1)),
+    bias = f32(min), code = clip(rint((w - bias)/scale)). Test data, like quantize_rtn.
+    Returns (packed uint32, scale float32, bias float32, codes uint32)."""
+    w = np.asarray(w, dtype=np.float32)
+    *lead, n_in = w.shape
+    if n_in % group_size:
+        raise ValueError("in_features must be a multiple of group_size")
+    g = w.reshape(*lead, n_in // group_size, group_size)
+    wmin = g.min(axis=-1)
+    levels = np.float32((1 << bits) - 1)
+    scale = ((g.max(axis=-1) - wmin) / levels).astype(np.float32)
+    scale = np.where(scale == 0, np.float32(1e-8), scale)
+    q = np.rint(((g - wmin[..., None]) / scale[..., None]).astype(np.float32))
+    q = np.clip(q, 0, levels).astype(np.uint32).reshape(*lead, n_in)
+    return pack_affine(q, bits), scale, wmin.astype(np.float32), q
+
+
 def dequant_bf16_bits(words: np.ndarray, scale_bits: np.ndarray, bias_bits: np.ndarray,
                       in_features: int, bits: int = 4, group_size: int = 64) -> np.ndarray:
     """Dequantize to bf16 under this build's declared rounding convention (bit patterns out).
@@ -165,4 +184,16 @@ def dequant_exact(words: np.ndarray, scale_bits: np.ndarray, bias_bits: np.ndarr
     codes = _unpack(words, in_features, bits).astype(np.float64)
     s = np.repeat(bf16_bits_to_f32(scale_bits).astype(np.float64), group_size, axis=-1)
     b = np.repeat(bf16_bits_to_f32(bias_bits).astype(np.float64), group_size, axis=-1)
+    return s * codes + b
+
+
+def dequant_float(words: np.ndarray, scale: np.ndarray, bias: np.ndarray, in_features: int,
+                  bits: int = 4, group_size: int = 64) -> np.ndarray:
+    """dequant_exact for float-valued scale/bias (float32 or bf16 values as float arrays): the
+    float64 value s*c + b of every weight, groups of `group_size` along the in-features. The
+    reference's float32 parity gates bake float32 scales (mx.quantize of float32 weights,
+    `parity/qwen35_forward_test.py:236-237`) at group 32."""
+    codes = _unpack(words, in_features, bits).astype(np.float64)
+    s = np.repeat(np.asarray(scale, dtype=np.float64), group_size, axis=-1)
+    b = np.repeat(np.asarray(bias, dtype=np.float64), group_size, axis=-1)
     return s * codes + b

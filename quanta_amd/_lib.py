@@ -23,7 +23,7 @@ REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 8
+ABI_VERSION = 9
 NOALLOC_SCRATCH_BYTES = 64 << 20   # QMOE_NOALLOC_SCRATCH_BYTES
 
 
@@ -80,6 +80,54 @@ class QmoeWeights(ctypes.Structure):
         ("awq_dn", ctypes.c_void_p),
         ("gu_rexp", ctypes.c_void_p),
         ("dn_rexp", ctypes.c_void_p),
+    ]
+
+
+DT_BF16, DT_F32 = 0, 1
+
+
+class QmoeGeneralConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int32),
+        ("n_experts", ctypes.c_int32),
+        ("top_k", ctypes.c_int32),
+        ("inter", ctypes.c_int32),
+        ("shared_inter", ctypes.c_int32),
+        ("scoring", ctypes.c_int32),
+        ("norm_topk", ctypes.c_int32),
+        ("n_group", ctypes.c_int32),
+        ("topk_group", ctypes.c_int32),
+        ("routed_scale", ctypes.c_float),
+        ("act", ctypes.c_int32),
+        ("act_alpha", ctypes.c_float),
+        ("act_limit", ctypes.c_float),
+        ("x_dtype", ctypes.c_int32),
+        ("gate_dtype", ctypes.c_int32),
+        ("experts_packed", ctypes.c_int32),
+        ("expert_dtype", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("shared_dtype", ctypes.c_int32),
+        ("shared_gated", ctypes.c_int32),
+        ("shared_gate_dtype", ctypes.c_int32),
+        ("dense_all", ctypes.c_int32),
+    ]
+
+
+class QmoeGeneralWeights(ctypes.Structure):
+    _fields_ = [
+        ("gate", ctypes.c_void_p),
+        ("router_bias", ctypes.c_void_p),
+        ("gu", ctypes.c_void_p),
+        ("gu_scale", ctypes.c_void_p),
+        ("gu_bias", ctypes.c_void_p),
+        ("dn", ctypes.c_void_p),
+        ("dn_scale", ctypes.c_void_p),
+        ("dn_bias", ctypes.c_void_p),
+        ("sh_gate", ctypes.c_void_p),
+        ("sh_up", ctypes.c_void_p),
+        ("sh_down", ctypes.c_void_p),
+        ("sh_expert_gate", ctypes.c_void_p),
     ]
 
 
@@ -140,6 +188,9 @@ SIGNATURES = {
     "qmoe_tile_int8": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_int3": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "qmoe_tile_bf16": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+    "qmoe_forward_general_workspace": (ctypes.c_size_t, [ctypes.POINTER(QmoeGeneralConfig), _I64]),
+    "qmoe_forward_general": (_I, [ctypes.POINTER(QmoeGeneralConfig), ctypes.POINTER(QmoeGeneralWeights),
+                                  _P, _I64, _P, _P, ctypes.c_size_t, _P]),
     "qmoe_set_decode_flow": (_I, [_I]),
     "qmoe_flow_timeouts": (ctypes.c_uint32, []),
 }

@@ -669,9 +669,170 @@ def _routed_dense(xf: torch.Tensor, pr: Prepared, k: int) -> torch.Tensor:
     return ops.combine(d, inv, w_all, sh_out, sg)
 
 
+# --------------------------------------------------------- the reference's own dtypes and groups
+
+_SHARED_KEYS = ("shared_gate_proj", "shared_up_proj", "shared_down_proj")
+
+
+def _fast_packed(d) -> bool:
+    """Whether a packed triplet is one of the fast path's formats (bf16 scale/bias, int3/4/6,
+    groups of 64 or 128)."""
+    if isinstance(d, TiledExperts):
+        return True
+    return (int(d["bits"]) in (3, 4, 6) and int(d["group_size"]) in (64, 128)
+            and d["scale"].dtype == torch.bfloat16 and d["bias"].dtype == torch.bfloat16)
+
+
+def needs_general(x: torch.Tensor, p: dict, cfg) -> bool:
+    """Whether the block must run at the reference's own dtypes (qmoe_forward_general): float32
+    activations, float32 (or otherwise non-bf16) expert or shared weights, packed groups other
+    than 64/128, code widths other than 3/4/6, or dimensions the tiled kernels do not take
+    (hidden, moe_intermediate or shared_intermediate not a multiple of 128) -- all of which the
+    reference's block accepts (src/quanta/qwen35/moe.py:98-104: the qmm output follows the
+    scale dtype; parity/qwen35_forward_test.py:213-271 runs float32, group 32, hidden 32)."""
+    if p.get("experts_mixed") is not None:
+        return False
+    if x.dtype != torch.bfloat16:
+        return True
+    H, I = int(_cfg(cfg, "hidden_size")), int(_cfg(cfg, "moe_intermediate_size"))
+    Is = int(_cfg(cfg, "shared_expert_intermediate_size", 0))
+    if H % 128 or I % 128 or (Is > 0 and Is % 128):
+        return True
+    for v in (p["experts_gate_up"], p["experts_down"]):
+        if isinstance(v, dict):
+            if not _fast_packed(v):
+                return True
+        elif v.dtype != torch.bfloat16:
+            return True
+    if Is > 0 and p.get("shared_gate_proj") is not None:
+        if any(isinstance(p[k], torch.Tensor) and p[k].dtype != torch.bfloat16 for k in _SHARED_KEYS):
+            return True
+    return False
+
+
+def _gen_tensor(t: torch.Tensor, shape: tuple, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor")
+    if tuple(t.shape) != shape:
+        raise ValueError(f"{name} must be {list(shape)} (got {list(t.shape)})")
+    ops.dtype_code(t.dtype, name)
+    return t.contiguous()
+
+
+def _gen_experts(v, rows: int, K: int, E: int, name: str):
+    """(packed?, dtype code, bits, group_size, tensors) of one routed stack for the general path."""
+    if isinstance(v, TiledExperts):
+        raise TypeError(f"{name}: this block needs the native packed triplet (the tiled resident "
+                        "form serves bf16 activations with bf16 scales only)")
+    if isinstance(v, dict):
+        if v.get("awq_scale") is not None:
+            raise ValueError(f"{name}: activation-aware scales need bf16 activations and bf16 scales")
+        bits, gs = int(v["bits"]), int(v["group_size"])
+        if bits not in (2, 3, 4, 5, 6, 8) or gs not in (32, 64, 128) or K % gs or (K * bits) % 32:
+            raise ValueError(f"{name}: packed experts must be 2..6 or 8 bits with group_size 32, 64 "
+                             f"or 128 dividing the in-features (got bits={bits}, group_size={gs})")
+        words = v["packed"]
+        if words.dtype == torch.uint32:
+            words = words.view(torch.int32)
+        if words.dtype != torch.int32 or tuple(words.shape) != (E, rows, K * bits // 32):
+            raise ValueError(f"{name}: packed must be uint32 [{E}, {rows}, {K * bits // 32}]")
+        sc = _gen_tensor(v["scale"], (E, rows, K // gs), f"{name}.scale")
+        bi = _gen_tensor(v["bias"], (E, rows, K // gs), f"{name}.bias")
+        if sc.dtype != bi.dtype:
+            raise TypeError(f"{name}: scale and bias must share a dtype")
+        return True, ops.dtype_code(sc.dtype, name), bits, gs, (words.contiguous(), sc, bi)
+    st = _gen_tensor(v, (E, rows, K), name)
+    return False, ops.dtype_code(st.dtype, name), 0, 0, (st,)
+
+
+def _shared_dense(p: dict):
+    """The shared expert's three matrices as dense tensors: int8 triplets are dequantized (once,
+    memoised) to the bf16 weights the reference's loader makes of them
+    (src/quanta/qwen35/artifact.py:105-115)."""
+    wg, wu, wd = (p[k] for k in _SHARED_KEYS)
+    if not isinstance(wg, dict):
+        return wg, wu, wd
+
+    def build():
+        return tuple(ops.dequant(t["packed"].contiguous(), t["scale"].contiguous(),
+                                 t["bias"].contiguous(), bits=int(t.get("bits", 8)),
+                                 group_size=int(t.get("group_size", 64))) for t in (wg, wu, wd))
+    return _memo(_anchor(wg), "shared_dense", (wg, wu, wd), build)
+
+
+def _general_call(x: torch.Tensor, p: dict, cfg, topk: int, dense_all: bool, token_chunk: int):
+    """qwen35_moe at the reference's own dtypes through qmoe_forward_general."""
+    H, E = int(_cfg(cfg, "hidden_size")), int(_cfg(cfg, "num_experts"))
+    I = int(_cfg(cfg, "moe_intermediate_size"))
+    Is = int(_cfg(cfg, "shared_expert_intermediate_size", 0))
+    scoring = str(_cfg(cfg, "scoring_func", "softmax"))
+    if scoring not in _SCORING:
+        raise ValueError(f"scoring_func {scoring!r} not supported (softmax | sigmoid | sqrtsoftplus)")
+    if p.get("experts_mixed") is not None:
+        raise TypeError("mixed-width experts need bf16 activations")
+    c, w = L.QmoeGeneralConfig(), L.QmoeGeneralWeights()
+    c.hidden, c.n_experts, c.top_k, c.inter = H, E, topk, I
+    c.x_dtype = ops.dtype_code(x.dtype, "x")
+    gate = _gen_tensor(p["gate"], (E, H), "gate")
+    c.gate_dtype = ops.dtype_code(gate.dtype, "gate")
+    gpk, gdt, gbits, ggs, gts = _gen_experts(p["experts_gate_up"], 2 * I, H, E, "experts_gate_up")
+    dpk, ddt, dbits, dgs, dts = _gen_experts(p["experts_down"], H, I, E, "experts_down")
+    if (gpk, gdt, gbits, ggs) != (dpk, ddt, dbits, dgs):
+        raise ValueError("experts_gate_up and experts_down must share one format (packed or dense, "
+                         "dtype, bits and group_size) on this path")
+    c.experts_packed, c.expert_dtype, c.bits, c.group_size = int(gpk), gdt, gbits, ggs
+    c.dense_all = int(dense_all)
+    keep = [gate, *gts, *dts]
+    w.gate = gate.data_ptr()
+    if gpk:
+        w.gu, w.gu_scale, w.gu_bias = (t.data_ptr() for t in gts)
+        w.dn, w.dn_scale, w.dn_bias = (t.data_ptr() for t in dts)
+    else:
+        w.gu, w.dn = gts[0].data_ptr(), dts[0].data_ptr()
+    has_shared = Is > 0 and p.get("shared_gate_proj") is not None
+    if has_shared:
+        wg, wu, wd = _shared_dense(p)
+        wg = _gen_tensor(wg, (Is, H), "shared_gate_proj")
+        wu = _gen_tensor(wu, (Is, H), "shared_up_proj")
+        wd = _gen_tensor(wd, (H, Is), "shared_down_proj")
+        if not wg.dtype == wu.dtype == wd.dtype:
+            raise TypeError("shared expert: gate, up and down must share a dtype")
+        c.shared_inter, c.shared_dtype = Is, ops.dtype_code(wg.dtype, "shared_gate_proj")
+        w.sh_gate, w.sh_up, w.sh_down = wg.data_ptr(), wu.data_ptr(), wd.data_ptr()
+        keep += [wg, wu, wd]
+        sg = p.get("shared_expert_gate")
+        if sg is not None:
+            sg = _gen_tensor(sg.reshape(1, H), (1, H), "shared_expert_gate")
+            c.shared_gated, c.shared_gate_dtype = 1, ops.dtype_code(sg.dtype, "shared_expert_gate")
+            w.sh_expert_gate = sg.data_ptr()
+            keep.append(sg)
+    bias = p.get("e_score_correction_bias")
+    if bias is not None:
+        bias = bias.to(device=x.device, dtype=torch.float32).reshape(E).contiguous()
+        w.router_bias = bias.data_ptr()
+        keep.append(bias)
+    c.scoring = _SCORING[scoring]
+    c.norm_topk = norm_mode(cfg, scoring, bias is not None)
+    c.n_group = int(_cfg(cfg, "n_group", 1))
+    c.topk_group = int(_cfg(cfg, "topk_group", 1))
+    c.routed_scale = float(_cfg(cfg, "routed_scaling_factor", 1.0))
+    c.act, c.act_alpha, c.act_limit = gated_activation(cfg)
+    b, s, _ = x.shape
+    n = b * s
+    xf = x.reshape(n, H).contiguous()
+    y = torch.empty_like(xf)
+    chunk = min(token_chunk if token_chunk and token_chunk > 0 else n, 65535)
+    ws = None
+    for c0 in range(0, n, chunk):
+        c1 = min(c0 + chunk, n)
+        ops.forward_general(c, w, xf[c0:c1], out=y[c0:c1], ws=ws)
+    del keep
+    return y.reshape(b, s, H)
+
+
 def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chunk: int = 8192,
                topk_override: int | None = None, regime: int = L.REGIME_AUTO) -> torch.Tensor:
-    """Full MoE block: routed top-k experts + gated shared expert. `x` [B,S,H] bf16 -> [B,S,H].
+    """Full MoE block: routed top-k experts + gated shared expert. `x` [B,S,H] -> [B,S,H].
 
     Mirrors `qwen35_moe` (src/quanta/qwen35/moe.py:154-202). `p` keys: gate [E,H];
     experts_gate_up / experts_down as packed triplet dicts {packed, scale, bias, group_size, bits}
@@ -681,11 +842,16 @@ def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chun
     (omit it for an ungated DeepSeek/GLM shared expert); optional e_score_correction_bias [E].
     `sparse=False` is the run-every-expert oracle and, as in the reference, refuses packed experts.
     Tokens beyond `token_chunk` are processed chunk by chunk (output-equivalent).
+
+    bf16 activations over the formats above run the tiled MFMA kernels (qmoe_forward). Anything
+    else the reference's block takes -- float32 activations, float32 weights or scale/bias, packed
+    groups of 32 or code widths 2..8, dimensions that are not multiples of 128 -- runs
+    qmoe_forward_general at the reference's own dtype flow (see `needs_general`).
     """
     if x.dim() != 3:
         raise ValueError("x must be [B, S, hidden]")
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"x must be bf16 (got {x.dtype}); the block computes on bf16 activations")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be bf16 or float32 (got {x.dtype})")
     b, s, hidden = x.shape
     n = b * s
     k_max = int(_cfg(cfg, "num_experts_per_tok"))
@@ -696,6 +862,10 @@ def qwen35_moe(x: torch.Tensor, p: dict, cfg, *, sparse: bool = True, token_chun
     if not sparse and packed:
         raise ValueError("qwen35_moe(sparse=False) is the bf16 dense oracle; packed int4 experts "
                          "require sparse=True (gather_qmm). Refusing to dequant silently.")
+    if needs_general(x, p, cfg):
+        if n == 0:
+            return x.clone()
+        return _general_call(x, p, cfg, topk, not sparse, token_chunk)
     pr = prepare(p, cfg, topk=topk, regime=regime)
     xf = x.reshape(n, hidden).contiguous()
     if n == 0:
@@ -791,14 +961,22 @@ class Qwen35MoEModule(torch.nn.Module):
         self.token_chunk = 8192
 
     def set_experts(self, gate_up: torch.Tensor, down: torch.Tensor) -> None:
-        """bf16 expert stacks [E,2I,H] / [E,H,I] (src/quanta/qwen35/model.py:46-47)."""
-        self.experts_gate_up, self.experts_down = tile_experts_bf16(gate_up), tile_experts_bf16(down)
+        """Expert stacks [E,2I,H] / [E,H,I] (src/quanta/qwen35/model.py:46-47): bf16 stacks are
+        converted once to the tiled resident layout; float32 stacks are held as given (the
+        reference-dtype path reads them natively)."""
+        if gate_up.dtype == torch.bfloat16 and down.dtype == torch.bfloat16:
+            gate_up, down = tile_experts_bf16(gate_up), tile_experts_bf16(down)
+        self.experts_gate_up, self.experts_down = gate_up, down
         self.experts_mixed = None
 
     def set_experts_packed(self, gate_up: dict, down: dict) -> None:
-        """Packed int4 triplets {packed, scale, bias, group_size, bits}
-        (src/quanta/qwen35/model.py:49-55); converted once to the tiled resident layout."""
-        self.experts_gate_up, self.experts_down = tile_experts_packed(gate_up), tile_experts_packed(down)
+        """Packed triplets {packed, scale, bias, group_size, bits} (src/quanta/qwen35/
+        model.py:49-55). The tiled kernels' formats (bf16 scale/bias, int3/int4/int6, groups of
+        64/128) are converted once to the tiled resident layout; other triplets (float32 scales,
+        group 32, other widths) are held as given for the reference-dtype path."""
+        if _fast_packed(gate_up) and _fast_packed(down):
+            gate_up, down = tile_experts_packed(gate_up), tile_experts_packed(down)
+        self.experts_gate_up, self.experts_down = gate_up, down
         self.experts_mixed = None
 
     def set_experts_mixed(self, stacks: dict, pbits: dict, pslot: dict, *, group_size: int = 128) -> None:

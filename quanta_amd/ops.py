@@ -349,6 +349,37 @@ def forward(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
     return out
 
 
+_DT = {torch.bfloat16: L.DT_BF16, torch.float32: L.DT_F32}
+
+
+def dtype_code(dt: torch.dtype, name: str) -> int:
+    """QMOE_DT_* of a torch dtype (bf16 or float32; anything else raises)."""
+    if dt not in _DT:
+        raise TypeError(f"{name}: dtype {dt} not supported (bfloat16 or float32)")
+    return _DT[dt]
+
+
+def forward_general(cfg: L.QmoeGeneralConfig, weights: L.QmoeGeneralWeights, x: torch.Tensor,
+                    out: torch.Tensor | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """Whole block on x [N, H] of the config's x_dtype at the reference's own dtypes and group
+    sizes (qmoe_forward_general)."""
+    dt = torch.float32 if cfg.x_dtype == L.DT_F32 else torch.bfloat16
+    _need(x, dt, "x")
+    N, H = x.shape
+    if H != cfg.hidden:
+        raise ValueError("forward_general: x hidden size does not match the config")
+    need = int(L.load().qmoe_forward_general_workspace(ctypes.byref(cfg), N))
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty(N, H, dtype=dt, device=x.device)
+    _need(out, dt, "out")
+    L.check(L.load().qmoe_forward_general(ctypes.byref(cfg), ctypes.byref(weights), _p(x), N,
+                                          _p(out), _p(ws), ws.numel(), _stream(x.device)),
+            "qmoe_forward_general")
+    return out
+
+
 def forward_noalloc(cfg: L.QmoeConfig, weights: L.QmoeWeights, x: torch.Tensor,
                     out: torch.Tensor) -> torch.Tensor:
     """Whole block on x [N, H] bf16 into `out` (qmoe_forward_noalloc): the library's fixed

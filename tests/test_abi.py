@@ -13,7 +13,7 @@ from quanta_amd import _lib as L
 
 def test_library_loads_and_abi_version():
     lib = L.load()
-    assert lib.qmoe_abi_version() == L.ABI_VERSION == 8
+    assert lib.qmoe_abi_version() == L.ABI_VERSION == 9
 
 
 def test_every_header_symbol_is_exported_and_bound():
@@ -220,3 +220,86 @@ def test_decode_flow_mode_switch_returns_previous():
     assert lib.qmoe_set_decode_flow(2) == 1
     assert lib.qmoe_set_decode_flow(7) == 2   # unknown modes leave the mode as it was
     assert lib.qmoe_set_decode_flow(1) == 2
+
+
+def _general_cfg(**kw) -> L.QmoeGeneralConfig:
+    base = dict(hidden=32, n_experts=8, top_k=3, inter=64, shared_inter=64, scoring=0, norm_topk=1,
+                n_group=1, topk_group=1, routed_scale=1.0, act=0, act_alpha=1.702,
+                act_limit=float("inf"), x_dtype=L.DT_F32, gate_dtype=L.DT_F32, experts_packed=1,
+                expert_dtype=L.DT_F32, bits=4, group_size=32, shared_dtype=L.DT_F32, shared_gated=1,
+                shared_gate_dtype=L.DT_F32, dense_all=0)
+    base.update(kw)
+    return L.QmoeGeneralConfig(**base)
+
+
+@pytest.mark.parametrize("kw, fragment", [
+    (dict(bits=7), "bits must be"),
+    (dict(group_size=16), "group_size must be 32, 64 or 128"),
+    (dict(hidden=48), "multiples of group_size"),
+    (dict(x_dtype=5), "dtypes must be"),
+    (dict(experts_packed=1, dense_all=1), "dense stacks only"),
+    (dict(top_k=9), "k <= min"),
+    (dict(act=1, act_limit=0.0), "act_limit"),
+    (dict(inter=0), "inter > 0"),
+])
+def test_forward_general_rejects_bad_config(kw, fragment):
+    """qmoe_forward_general validates the whole configuration before it enqueues anything."""
+    lib = L.load()
+    cfg = _general_cfg(**kw)
+    w = L.QmoeGeneralWeights(gate=16, gu=16, dn=16, gu_scale=16, gu_bias=16, dn_scale=16,
+                             dn_bias=16, sh_gate=16, sh_up=16, sh_down=16, sh_expert_gate=16)
+    rc = lib.qmoe_forward_general(ctypes.byref(cfg), ctypes.byref(w), _DUMMY, 4, _DUMMY, _DUMMY,
+                                  1 << 24, None)
+    assert rc == L.QMOE_EINVAL and fragment in _last_error(), _last_error()
+
+
+def test_forward_general_null_and_workspace():
+    lib = L.load()
+    cfg = _general_cfg()
+    w = L.QmoeGeneralWeights()
+    rc = lib.qmoe_forward_general(ctypes.byref(cfg), ctypes.byref(w), _DUMMY, 4, _DUMMY, _DUMMY,
+                                  1 << 24, None)
+    assert rc == L.QMOE_EINVAL and "missing weights" in _last_error()
+    rc = lib.qmoe_forward_general(None, ctypes.byref(w), _DUMMY, 4, _DUMMY, _DUMMY, 1 << 24, None)
+    assert rc == L.QMOE_EINVAL and "null pointer" in _last_error()
+    small = lib.qmoe_forward_general_workspace(ctypes.byref(cfg), 9)
+    big = lib.qmoe_forward_general_workspace(ctypes.byref(cfg), 900)
+    assert 0 < small < big
+    dense = _general_cfg(experts_packed=0, dense_all=1)
+    # the run-every-expert form holds E slots per token instead of k
+    assert lib.qmoe_forward_general_workspace(ctypes.byref(dense), 9) > small
+    w = L.QmoeGeneralWeights(gate=16, gu=16, dn=16, gu_scale=16, gu_bias=16, dn_scale=16,
+                             dn_bias=16, sh_gate=16, sh_up=16, sh_down=16, sh_expert_gate=16)
+    rc = lib.qmoe_forward_general(ctypes.byref(cfg), ctypes.byref(w), _DUMMY, 9, _DUMMY, _DUMMY,
+                                  small - 1, None)
+    assert rc == L.QMOE_EINVAL and "workspace too small" in _last_error()
+
+
+def test_struct_offsets_match_the_c_compiler(tmp_path):
+    """Every ctypes struct has the C compiler's field offsets and size for the header's struct."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    structs = [(L.QmoeConfig, "qmoe_config_t"), (L.QmoeWeights, "qmoe_weights_t"),
+               (L.QmoeStack, "qmoe_stack_t"), (L.QmoeMixed, "qmoe_mixed_t"),
+               (L.QmoeGeneralConfig, "qmoe_general_config_t"),
+               (L.QmoeGeneralWeights, "qmoe_general_weights_t")]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{L.HEADER}"', "int main(void) {"]
+    for st, cname in structs:
+        lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')
+        for fname, _ in st._fields_:
+            lines.append(f'  printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "offsets.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "offsets"
+    subprocess.run([gcc, "-std=c11", str(src), "-o", str(exe)], check=True)
+    out = dict(line.rsplit(" ", 1) for line in subprocess.run(
+        [str(exe)], check=True, capture_output=True, text=True).stdout.splitlines())
+    for st, cname in structs:
+        assert int(out[cname]) == ctypes.sizeof(st), cname
+        for fname, _ in st._fields_:
+            assert int(out[f"{cname}.{fname}"]) == getattr(st, fname).offset, f"{cname}.{fname}"
