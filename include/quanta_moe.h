@@ -326,6 +326,21 @@ int qmoe_router_topk(const float* logits, int64_t ld_logits, const float* bias, 
                      float routed_scale, int has_shared_gate, int32_t* idx, float* w,
                      float* shared_gate_out, void* stream);
 
+/* The router in one call, from the gate weight as the artifact stores it: wr [E, H] row-major,
+ * bf16 (wr_is_f32 = 0, the bake's dtype, src/quanta/qwen35/bake.py:147-148) or fp32
+ * (wr_is_f32 = 1). logits = x . wr^T in fp32 (bf16 x bf16 products are exact in fp32), then the
+ * top-k of qmoe_router_topk: idx[N,k] int32 in canonical order, w[N,k] fp32. shared_gate
+ * (nullable; [H], wr's dtype) adds the shared-expert gate: shared_gate_out[N] =
+ * sigmoid(x . shared_gate). The logits live in `ws` (qmoe_router_workspace bytes). x, wr and
+ * shared_gate 16-byte aligned, H % 8 == 0, N <= 262140 per call.
+ * Replaces qwen35_route(xf, gate_w, cfg) (src/quanta/qwen35/moe.py:36-56) and MoEGate.__call__
+ * (src/quanta/modeling/moe.py:33-44) taking the raw gate, with no tiling step. */
+size_t qmoe_router_workspace(int64_t N, int E);
+int qmoe_router(const uint16_t* x, const void* wr, int wr_is_f32, const void* shared_gate,
+                const float* bias, int64_t N, int H, int E, int k, int scoring, int n_group,
+                int topk_group, int norm_topk, float routed_scale, int32_t* idx, float* w,
+                float* shared_gate_out, void* ws, size_t ws_bytes, void* stream);
+
 /* Router logits for an fp32 router weight [E,H] (row-major): logits[t, e] = x[t] . wr[e] in
  * fp32; column E = x[t] . shared_gate when shared_gate != NULL. Replaces the fp32 matmul
  * xf.astype(f32) @ gate_w.astype(f32).T (src/quanta/qwen35/moe.py:47). bf16 routers go through

@@ -175,6 +175,9 @@ SIGNATURES = {
     "qmoe_rmsnorm": (_I, [_P, _P, _I64, _I, _F, _P, _P]),
     "qmoe_router_topk": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P]),
     "qmoe_router_logits_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _I64, _P]),
+    "qmoe_router_workspace": (ctypes.c_size_t, [_I64, _I]),
+    "qmoe_router": (_I, [_P, _P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P,
+                         ctypes.c_size_t, _P]),
     "qmoe_permute": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "qmoe_grouped_qmm": (_I, [_P, _I64, _P, _I, _I64, _P, _P, _P, _I, _I64, _I, _I, _I, _P, _P, _P,
                               _I, _I, _F, _F, _P, _I, _I, _P, ctypes.c_size_t, _P]),

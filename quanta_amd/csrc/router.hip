@@ -48,6 +48,64 @@ __global__ void __launch_bounds__(256) router_f32_kernel(const uint16_t* __restr
   }
 }
 
+// ---------------------------------------------------------------- one-call router logits
+// Logits from the router weight as stored, bf16 or fp32 [E, H] row-major, for qmoe_router.
+// One wavefront per (expert row, 4-token group): lanes take 8 consecutive columns per step
+// (16-byte loads of bf16 x and bf16 weights, two 16-byte loads of fp32 weights), fp32 FMAs, and
+// the fixed-order DPP wavefront sum. Row E (shared_gate != null) is the shared-expert gate
+// logit. bf16 x bf16 products are exact in fp32, so the logits equal xf.f32 @ gate.f32^T up to
+// the fp32 summation order.
+template <bool F32W>
+__global__ void __launch_bounds__(256) router_rows_kernel(const uint16_t* __restrict__ x,
+                                                          const void* __restrict__ wr,
+                                                          const void* __restrict__ shared_gate,
+                                                          int N, int H, int E, int rows,
+                                                          float* __restrict__ logits, int ld) {
+  constexpr int TT = 4;
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= rows) return;  // whole wavefronts exit together; no block barriers below
+  const int t0 = blockIdx.y * TT;
+  const int nt = min(TT, N - t0);
+  const size_t row_elems = static_cast<size_t>(e < E ? e : 0) * H;
+  const void* wbase = (e < E) ? wr : shared_gate;
+  float acc[TT] = {0.f, 0.f, 0.f, 0.f};
+  for (int h = lane * 8; h < H; h += 512) {
+    float wv[8];
+    if (F32W) {
+      const float4* wp = reinterpret_cast<const float4*>(static_cast<const float*>(wbase) + row_elems + h);
+      const float4 a = wp[0], b = wp[1];
+      wv[0] = a.x; wv[1] = a.y; wv[2] = a.z; wv[3] = a.w;
+      wv[4] = b.x; wv[5] = b.y; wv[6] = b.z; wv[7] = b.w;
+    } else {
+      const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(wbase) + row_elems + h);
+      const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wv[2 * i] = __uint_as_float(u[i] << 16);
+        wv[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      if (tt < nt) {
+        const uint4 q = *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0 + tt) * H + h);
+        const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[tt] = fmaf(__uint_as_float(u[i] << 16), wv[2 * i], acc[tt]);
+          acc[tt] = fmaf(__uint_as_float(u[i] & 0xFFFF0000u), wv[2 * i + 1], acc[tt]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const float v = wave_sum_f32(acc[tt]);
+    if (tt < nt && lane == 0) logits[static_cast<int64_t>(t0 + tt) * ld + e] = v;
+  }
+}
+
 int launch_router_f32(const uint16_t* x, const float* wr, const float* shared_gate, int N, int H,
                       int E, float* logits, int ld, hipStream_t stream) {
   int rows = E + (shared_gate ? 1 : 0);
@@ -160,4 +218,44 @@ extern "C" int qmoe_router_logits_f32(const uint16_t* x, const float* wr,
   if (!x || !wr || !logits) return fail("qmoe_router_logits_f32: null pointer");
   return launch_router_f32(x, wr, shared_gate, static_cast<int>(N), H, E, logits,
                            static_cast<int>(ld_logits), static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t qmoe_router_workspace(int64_t N, int E) {
+  if (N <= 0 || E <= 0) return 0;
+  return align256(static_cast<size_t>(N) * (E + 1) * sizeof(float));
+}
+
+extern "C" int qmoe_router(const uint16_t* x, const void* wr, int wr_is_f32, const void* shared_gate,
+                           const float* bias, int64_t N, int H, int E, int k, int scoring,
+                           int n_group, int topk_group, int norm_topk, float routed_scale,
+                           int32_t* idx, float* w, float* shared_gate_out, void* ws,
+                           size_t ws_bytes, void* stream) {
+  if (N <= 0 || N > (int64_t(1) << 30)) return fail("qmoe_router: 0 < N <= 2^30 required");
+  int rc = validate_routing(static_cast<int>(N), H, E, k, scoring, n_group, topk_group);
+  if (rc) return rc;
+  if (H % 8) return fail("qmoe_router: H % 8 == 0 required");
+  if (wr_is_f32 != 0 && wr_is_f32 != 1) return fail("qmoe_router: wr_is_f32 must be 0 or 1");
+  if (norm_topk < QMOE_NORM_NONE || norm_topk > QMOE_NORM_MULTI)
+    return fail("qmoe_router: norm_topk must be QMOE_NORM_NONE, _ALWAYS or _MULTI");
+  if (!x || !wr || !idx || !w || !ws || (shared_gate && !shared_gate_out))
+    return fail("qmoe_router: null pointer");
+  if (ws_bytes < qmoe_router_workspace(N, E)) return fail("qmoe_router: workspace too small");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wr) |
+       reinterpret_cast<uintptr_t>(shared_gate)) % 16)
+    return fail("qmoe_router: x, wr and shared_gate must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* logits = static_cast<float*>(ws);
+  const int ld = E + 1;
+  const int rows = E + (shared_gate ? 1 : 0);
+  const dim3 grid((rows + 3) / 4, static_cast<unsigned>((N + 3) / 4));
+  if (grid.y > 65535u) return fail("qmoe_router: N <= 262140 tokens per call");
+  if (wr_is_f32)
+    router_rows_kernel<true><<<grid, 256, 0, st>>>(x, wr, shared_gate, static_cast<int>(N), H, E,
+                                                   rows, logits, ld);
+  else
+    router_rows_kernel<false><<<grid, 256, 0, st>>>(x, wr, shared_gate, static_cast<int>(N), H, E,
+                                                    rows, logits, ld);
+  if ((rc = check_launch("qmoe_router logits"))) return rc;
+  return launch_topk(logits, ld, bias, static_cast<int>(N), E, k, scoring, n_group, topk_group,
+                     norm_topk, routed_scale, shared_gate ? 1 : 0, idx, w, shared_gate_out, st);
 }

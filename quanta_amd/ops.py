@@ -228,6 +228,38 @@ def router_topk(logits: torch.Tensor, n_experts: int, k: int, *, scoring: int = 
     return idx, w, sg
 
 
+def router(x: torch.Tensor, wr: torch.Tensor, k: int, *, shared_gate: torch.Tensor | None = None,
+           scoring: int = L.SCORE_SOFTMAX, bias: torch.Tensor | None = None, n_group: int = 1,
+           topk_group: int = 1, norm_topk: int = L.NORM_ALWAYS, routed_scale: float = 1.0):
+    """The router in one call (qmoe_router) from the gate as stored: x [N, H] bf16, wr [E, H]
+    bf16 or fp32 (shared_gate [H] or [1, H] of wr's dtype, optional) -> (idx [N,k] int32,
+    w [N,k] fp32, sg [N] fp32 or None)."""
+    _need(x, torch.bfloat16, "x")
+    _need(wr, (torch.bfloat16, torch.float32), "wr")
+    N, H = x.shape
+    E = wr.shape[0]
+    if wr.dim() != 2 or wr.shape[1] != H:
+        raise ValueError("router: wr must be [E, H]")
+    if shared_gate is not None:
+        _need(shared_gate, wr.dtype, "shared_gate")
+        if shared_gate.numel() != H:
+            raise ValueError("router: shared_gate must have H elements")
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.numel() != E:
+            raise ValueError("router: bias must have E elements")
+    lib = L.load()
+    ws = torch.empty(max(int(lib.qmoe_router_workspace(N, E)), 1), dtype=torch.uint8, device=x.device)
+    idx = torch.empty(N, k, dtype=torch.int32, device=x.device)
+    w = torch.empty(N, k, dtype=torch.float32, device=x.device)
+    sg = torch.empty(N, dtype=torch.float32, device=x.device) if shared_gate is not None else None
+    L.check(lib.qmoe_router(_p(x), _p(wr), int(wr.dtype == torch.float32), _p(shared_gate), _p(bias),
+                            N, H, E, k, scoring, n_group, topk_group, int(norm_topk),
+                            float(routed_scale), _p(idx), _p(w), _p(sg), _p(ws), ws.numel(),
+                            _stream(x.device)), "qmoe_router")
+    return idx, w, sg
+
+
 def permute(idx: torch.Tensor, n_experts: int, m_tile: int = L.SMALL_M_TILE):
     """Stable permute of idx [N, k] by expert -> (counts, offsets, tile_off, sorted_slot, inv,
     tile_map)."""

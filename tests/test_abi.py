@@ -303,3 +303,25 @@ def test_struct_offsets_match_the_c_compiler(tmp_path):
         assert int(out[cname]) == ctypes.sizeof(st), cname
         for fname, _ in st._fields_:
             assert int(out[f"{cname}.{fname}"]) == getattr(st, fname).offset, f"{cname}.{fname}"
+
+
+@pytest.mark.parametrize("args, fragment", [
+    (dict(H=100), "H % 8"),
+    (dict(k=17), "k <= min"),
+    (dict(wr_is_f32=2), "wr_is_f32"),
+    (dict(N=0), "0 < N"),
+    (dict(ws_bytes=16), "workspace too small"),
+    (dict(norm_topk=3), "norm_topk"),
+    (dict(x=ctypes.c_void_p(24)), "16-byte aligned"),
+])
+def test_router_one_call_validation(args, fragment):
+    lib = L.load()
+    a = dict(x=ctypes.c_void_p(256), wr=ctypes.c_void_p(256), wr_is_f32=0, sg=None, bias=None, N=4,
+             H=256, E=16, k=2, scoring=0, n_group=1, topk_group=1, norm_topk=1, scale=1.0,
+             idx=_DUMMY, w=_DUMMY, sg_out=None, ws=_DUMMY, ws_bytes=1 << 20)
+    a.update(args)
+    rc = lib.qmoe_router(a["x"], a["wr"], a["wr_is_f32"], a["sg"], a["bias"], a["N"], a["H"], a["E"],
+                         a["k"], a["scoring"], a["n_group"], a["topk_group"], a["norm_topk"],
+                         a["scale"], a["idx"], a["w"], a["sg_out"], a["ws"], a["ws_bytes"], None)
+    assert rc == L.QMOE_EINVAL and fragment in _last_error(), _last_error()
+    assert lib.qmoe_router_workspace(4, 16) >= 4 * 17 * 4

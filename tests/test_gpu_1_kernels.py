@@ -72,16 +72,26 @@ def _route_case(rng, N, E, H, k, scoring, bias=False, n_group=1, topk_group=1, s
                              norm_single=norm_single)
 
 
-def _check_route(gpu, x, wr, kw, logits_dev, E):
+def _route_kw(gpu, kw) -> dict:
+    """ops.router / ops.router_topk keyword arguments of an oracle routing case."""
+    return dict(scoring={"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}[kw["scoring"]],
+                bias=None if kw["bias"] is None else
+                torch.tensor(kw["bias"], dtype=torch.float32, device=gpu),
+                n_group=kw["n_group"], topk_group=kw["topk_group"],
+                norm_topk=(L.NORM_NONE if not kw["norm_topk"] else
+                           L.NORM_ALWAYS if kw["norm_single"] else L.NORM_MULTI),
+                routed_scale=kw["scale"])
+
+
+def _check_route(gpu, x, wr, kw, logits_dev, E, got=None):
+    """GPU routing vs the oracle: the top-k over `logits_dev`, or `got` = (idx, w) from a
+    one-call router."""
     idx_o, w_o, logits_o, scores_o, choice_o = om.route(x, wr, **kw)
     k = kw["k"]
-    idx, w, _ = ops.router_topk(logits_dev, E, k, scoring={"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}[kw["scoring"]],
-                                bias=None if kw["bias"] is None else
-                                torch.tensor(kw["bias"], dtype=torch.float32, device=gpu),
-                                n_group=kw["n_group"], topk_group=kw["topk_group"],
-                                norm_topk=(L.NORM_NONE if not kw["norm_topk"] else
-                                           L.NORM_ALWAYS if kw["norm_single"] else L.NORM_MULTI),
-                                routed_scale=kw["scale"])
+    if got is None:
+        idx, w, _ = ops.router_topk(logits_dev, E, k, **_route_kw(gpu, kw))
+    else:
+        idx, w = got
     idx, w = idx.cpu().numpy(), w.cpu().numpy().astype(np.float64)
     # float32 logits carry ~|x||w| * 2^-24 * sqrt(H) error: rows whose selection gap is below a
     # generous bound of that are reported and compared as sets only.
@@ -127,6 +137,44 @@ def test_router_topk_vs_oracle(gpu, case):
     lg = f64(logits)[:, :case["E"]]
     assert np.allclose(lg, x @ wr.T, rtol=1e-4, atol=1e-4)
     _check_route(gpu, x, wr, kw, logits, case["E"])
+
+
+@pytest.mark.parametrize("case", [
+    dict(N=1, E=512, H=2048, k=10, scoring="softmax"),
+    dict(N=32, E=512, H=2048, k=10, scoring="softmax"),
+    dict(N=7, E=256, H=2048, k=8, scoring="softmax"),
+    dict(N=64, E=256, H=7168, k=8, scoring="sigmoid", bias=True, n_group=8, topk_group=4, scale=2.5),
+    dict(N=5, E=64, H=256, k=1, scoring="sigmoid", bias=True, norm=False),
+    dict(N=3, E=1024, H=264, k=16, scoring="softmax"),
+    dict(N=40, E=256, H=1024, k=6, scoring="sqrtsoftplus", bias=True, scale=1.5),
+])
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+def test_router_one_call_vs_oracle(gpu, case, wdt):
+    """qmoe_router from the gate as stored (bf16 or fp32 [E, H], no tiling) against the oracle:
+    ids exact outside float32 near-ties, weights within 1e-5 relative, the shared-expert gate
+    sigmoid(x . g) alongside, and the same routing without the shared gate."""
+    rng = np.random.default_rng(case["N"] * 37 + case["E"])
+    x, wr, bvec, kw = _route_case(rng, case["N"], case["E"], case["H"], case["k"], case["scoring"],
+                                  case.get("bias", False), case.get("n_group", 1),
+                                  case.get("topk_group", 1), case.get("scale", 1.0),
+                                  case.get("norm", True), case.get("norm_single", True))
+    sgate = oq.round_bf16(rng.standard_normal(case["H"]) * 0.02)
+    xd = bf16_dev(oq.f32_to_bf16_bits(x.astype(np.float32)), gpu)
+    wd = torch.tensor(wr, dtype=torch.float32, device=gpu).to(wdt)
+    sd = torch.tensor(sgate, dtype=torch.float32, device=gpu).to(wdt)
+    idx, w, sg = ops.router(xd, wd, case["k"], shared_gate=sd, **_route_kw(gpu, kw))
+    _check_route(gpu, x, wr, kw, None, case["E"], got=(idx, w))
+    want_sg = 1.0 / (1.0 + np.exp(-(x @ sgate)))
+    assert np.allclose(f64(sg), want_sg, rtol=1e-5, atol=1e-7)
+    idx2, w2, sg2 = ops.router(xd, wd, case["k"], **_route_kw(gpu, kw))
+    assert torch.equal(idx2, idx) and torch.equal(w2, w) and sg2 is None
+
+
+def test_router_one_call_rejects():
+    lib = L.load()
+    rc = lib.qmoe_router(None, None, 0, None, None, 4, 100, 16, 2, 0, 1, 1, 1, 1.0, None, None, None,
+                         None, 0, None)
+    assert rc == L.QMOE_EINVAL
 
 
 def test_router_bf16_mfma_logits(gpu):
