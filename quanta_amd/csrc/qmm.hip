@@ -160,13 +160,14 @@ constexpr int kLgNBuf = 3;
 constexpr int kLgABytes = 8 * 4 * 64 * 16;                // one A slot: 32 KiB
 constexpr int kLgBWaveBytes = 2 * 1024 + 2 * 128;         // one wavefront's int4 weight slot
 constexpr int kLgBBytes = 8 * kLgBWaveBytes;              // 18 KiB
-constexpr size_t kLgLdsBytes = kLgNBuf * (kLgABytes + kLgBBytes);   // 150 KiB
+constexpr int kLgRowTabBytes = 128 * 4;   // after the slots: per-row scales (as the wide kernel)
+constexpr size_t kLgLdsBytes = kLgNBuf * (kLgABytes + kLgBBytes) + kLgRowTabBytes;   // 150.5 KiB
 // int6: a wavefront's slot adds the tiles' high-bit planes (2 x 512 B); two slots, 116 KiB
 constexpr int kLg6BWaveBytes = 2 * 1024 + 2 * 128 + 2 * 512;
-constexpr size_t kLg6LdsBytes = 2 * (kLgABytes + 8 * kLg6BWaveBytes);
+constexpr size_t kLg6LdsBytes = 2 * (kLgABytes + 8 * kLg6BWaveBytes) + kLgRowTabBytes;
 // int3: 768 B of codes per tile superblock; three slots, 138 KiB
 constexpr int kLg3BWaveBytes = 2 * 768 + 2 * 128;
-constexpr size_t kLg3LdsBytes = kLgNBuf * (kLgABytes + 8 * kLg3BWaveBytes);
+constexpr size_t kLg3LdsBytes = kLgNBuf * (kLgABytes + 8 * kLg3BWaveBytes) + kLgRowTabBytes;
 
 // 16-byte k-chunk (of 16 in a superblock) that MFMA step s consumes in lane group g: int4 weight
 // fragments follow the tiled code words, bf16 ones the natural 32-k chunks.
@@ -206,6 +207,38 @@ __device__ __forceinline__ int load_i8_now(const int8_t* p) {
   int v;
   asm volatile("global_load_sbyte %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
   return v;
+}
+
+// A lane's row data for the prologue of the prefill kernels, loaded and waited for in one asm
+// block before any DMA is issued (as load_i8_now, one memory round trip for all of it): the
+// four weight-row exponent bytes of its tiles and the row scale of its activation row.
+struct RowLoads {
+  int ex[4];
+  float rs;
+};
+__device__ __forceinline__ RowLoads load_rows_now(const int8_t* e0, const int8_t* e1,
+                                                  const int8_t* e2, const int8_t* e3,
+                                                  const float* rs) {
+  int v0, v1, v2, v3;
+  float f;
+  asm volatile("global_load_sbyte %0, %5, off\n\tglobal_load_sbyte %1, %6, off\n\t"
+               "global_load_sbyte %2, %7, off\n\tglobal_load_sbyte %3, %8, off\n\t"
+               "global_load_dword %4, %9, off\n\ts_waitcnt vmcnt(0)"
+               : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(f)
+               : "v"(e0), "v"(e1), "v"(e2), "v"(e3), "v"(rs)
+               : "memory");
+  return RowLoads{{v0, v1, v2, v3}, f};
+}
+
+__device__ __forceinline__ RowLoads load_rows_now2(const int8_t* e0, const int8_t* e1, const float* rs) {
+  int v0, v1;
+  float f;
+  asm volatile("global_load_sbyte %0, %3, off\n\tglobal_load_sbyte %1, %4, off\n\t"
+               "global_load_dword %2, %5, off\n\ts_waitcnt vmcnt(0)"
+               : "=&v"(v0), "=&v"(v1), "=&v"(f)
+               : "v"(e0), "v"(e1), "v"(rs)
+               : "memory");
+  return RowLoads{{v0, v1, 0, 0}, f};
 }
 
 template <int N>
@@ -305,6 +338,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   constexpr int BWAVE = (FMT == FMT_INT6) ? kLg6BWaveBytes
                         : (FMT == FMT_INT3) ? kLg3BWaveBytes : kLgBWaveBytes;
   constexpr int DS = (FMT == FMT_INT3) ? kDeqShift + 1 : kDeqShift;   // row_exp - e
+  constexpr int LDS_ROWTAB = NBUF * (kLgABytes + 8 * BWAVE);            // after the slots
   extern __shared__ u32x4 lds[];
   char* lds_c = reinterpret_cast<char*>(lds);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -343,11 +377,11 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   // as zeros by the epilogue). A wavefront whose m-block lies past the tile loads no A.
   const bool a_on = wave < mb_act;
   const char* arow_ptr;
+  const int arow_r = 16 * wave + (lane & 15);
+  const int64_t arow = (arow_r < m_cnt) ? act_row(a, m0 + arow_r) : -1;
   {
-    const int r = 16 * wave + (lane & 15);
-    const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
     const uint16_t* abase = (QF) ? act16 : a.act;
-    arow_ptr = reinterpret_cast<const char*>(abase + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
+    arow_ptr = reinterpret_cast<const char*>(abase + (arow >= 0 ? arow : 0) * static_cast<int64_t>(a.K)) +
                16 * lg_chunk<QF ? FMT_INT4 : FMT>(0, lane >> 4);
   }
   const uint32_t lds_base = lds_offset(lds);
@@ -359,6 +393,7 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
   const char* wtile[2];   // int4/int6: the tile's first superblock
   const char* wsb[2];
   const u32x4* wp[2];
+  const int8_t* wexp[2] = {nullptr, nullptr};
   int rex[2] = {0, 0};   // int4/int6: the lane's weight row of each tile, its dequant exponent e
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -370,11 +405,24 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       wcode[t] = wtile[t] + lane * 16;
       wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
       wp[t] = nullptr;
-      rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - DS;
+      wexp[t] = a.row_exp + (ebase + tl) * 16 + (lane & 15);
     } else {
       wcode[t] = wtile[t] = wsb[t] = nullptr;
       wp[t] = static_cast<const u32x4*>(a.codes) + (ebase + tl) * (a.K / 32) * 64 + lane;
     }
+  }
+  // the exponents and the activation row's scale in one round trip (bf16 weights: no scaling);
+  // wavefront w's lanes 0-15 publish m-block w's row scales for the epilogue (-1: no data)
+  float* row_tab = reinterpret_cast<float*>(lds_c + LDS_ROWTAB);
+  {
+    float rs = 1.0f;
+    if (QF) {
+      const RowLoads rl = load_rows_now2(wexp[0], wexp[1], row_sinv + (arow >= 0 ? arow : 0));
+      rex[0] = rl.ex[0] - DS;
+      rex[1] = rl.ex[1] - DS;
+      rs = rl.rs;
+    }
+    if (a_on && lane < 16) row_tab[arow_r] = (arow >= 0) ? rs : -1.0f;
   }
   // scale/bias copy: lanes 0-31 take tile 0's 128 B, lanes 32-63 tile 1's, 4 B each
   const char* sb_src = (QF) ? wsb[lane >> 5] + 4 * (lane & 31) : nullptr;
@@ -571,9 +619,8 @@ __global__ void __launch_bounds__(kLgThreads) qmm_large_kernel(QmmArgs a) {
       const int mr = 16 * i + 4 * (lane >> 4) + j;
       if (mr >= m_cnt) continue;
       // rows whose activation row is invalid read as zeros (their A data was row 0's)
-      const int64_t ar2 = act_row(a, m0 + mr);
-      const bool ok = ar2 >= 0;
-      const float rs = (QF && ok) ? row_sinv[ar2] : 1.0f;
+      const float rs = row_tab[mr];
+      const bool ok = rs >= 0.f;
       // undo both power-of-two scalings (activation row, int4 weight row): exact
       auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {
@@ -612,11 +659,13 @@ constexpr int kWdThreads = 512;
 constexpr int kWdABytes = 8 * 4 * 64 * 16;                 // 32 KiB
 constexpr int kWdBWaveBytes = 4 * 1024 + 4 * 128;          // 4.5 KiB
 constexpr int kWdSlotBytes = kWdABytes + 8 * kWdBWaveBytes; // 68 KiB
-constexpr size_t kWdLdsBytes = 2 * kWdSlotBytes;            // 136 KiB
+// after the two slots: the m-tile's per-row activation scales (-1 marks a row without data)
+constexpr int kWdRowTabBytes = 128 * 4;
+constexpr size_t kWdLdsBytes = 2 * kWdSlotBytes + kWdRowTabBytes;   // 136.5 KiB
 // int3 (qmm_wide_int3_kernel): 768 B of codes per tile superblock, 3.5 KiB per wavefront, 120 KiB
 constexpr int kWd3BWaveBytes = 4 * 768 + 4 * 128;
 constexpr int kWd3SlotBytes = kWdABytes + 8 * kWd3BWaveBytes;
-constexpr size_t kWd3LdsBytes = 2 * kWd3SlotBytes;
+constexpr size_t kWd3LdsBytes = 2 * kWd3SlotBytes + kWdRowTabBytes;
 
 // FMT: int4 (qmm_wide_kernel) or int3 (qmm_wide_int3_kernel, the tile superblocks staged by dword
 // copies as in qmm_large_kernel)
@@ -656,12 +705,10 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
   // activation source: wavefront w loads m-block w (see qmm_large_kernel)
   const bool a_on = wave < mb_act;
   const char* arow_ptr;
-  {
-    const int r = 16 * wave + (lane & 15);
-    const int64_t ar = (r < m_cnt) ? act_row(a, m0 + r) : -1;
-    arow_ptr = reinterpret_cast<const char*>(act16 + (ar >= 0 ? ar : 0) * static_cast<int64_t>(a.K)) +
-               16 * lg_chunk<FMT_INT4>(0, lane >> 4);
-  }
+  const int arow_r = 16 * wave + (lane & 15);
+  const int64_t arow = (arow_r < m_cnt) ? act_row(a, m0 + arow_r) : -1;
+  arow_ptr = reinterpret_cast<const char*>(act16 + (arow >= 0 ? arow : 0) * static_cast<int64_t>(a.K)) +
+             16 * lg_chunk<FMT_INT4>(0, lane >> 4);
   const uint32_t lds_base = lds_offset(lds);
   auto a_slot = [&](int p) { return (p & 1) * SLOT; };
   auto b_slot = [&](int p) { return (p & 1) * SLOT + kWdABytes + wave * BWAVE; };
@@ -670,6 +717,7 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
   const char* wcode[4];
   const char* wtile[4];   // the tile's first superblock
   const char* wsb[4];
+  const int8_t* wexp[4];
   int rex[4];   // the lane's weight row of each tile: its dequant exponent e (deq_sb)
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -680,7 +728,16 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
     wtile[t] = static_cast<const char*>(a.codes) + tb * SBB;
     wcode[t] = wtile[t] + lane * 16;
     wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
-    rex[t] = load_i8_now(a.row_exp + (ebase + tl) * 16 + (lane & 15)) - DS;
+    wexp[t] = a.row_exp + (ebase + tl) * 16 + (lane & 15);
+  }
+  // the exponents and the activation row's scale in one round trip; wavefront w's lanes 0-15
+  // publish the scales of m-block w for the epilogue (-1: no data), before the first barrier
+  float* row_tab = reinterpret_cast<float*>(lds_c + 2 * SLOT);
+  {
+    const RowLoads rl = load_rows_now(wexp[0], wexp[1], wexp[2], wexp[3], row_sinv + (arow >= 0 ? arow : 0));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) rex[t] = rl.ex[t] - DS;
+    if (a_on && lane < 16) row_tab[arow_r] = (arow >= 0) ? rl.rs : -1.0f;
   }
   // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
   const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
@@ -815,9 +872,8 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
     for (int j = 0; j < 4; ++j) {
       const int mr = 16 * i + 4 * (lane >> 4) + j;
       if (mr >= m_cnt) continue;
-      const int64_t ar2 = act_row(a, m0 + mr);
-      const bool ok = ar2 >= 0;
-      const float rs = ok ? row_sinv[ar2] : 1.0f;
+      const float rs = row_tab[mr];
+      const bool ok = rs >= 0.f;
       // undo both power-of-two scalings (activation row, weight row): exact
       auto val = [&](int t) { return ok ? ldexpf(acc[i][t][j] * rs, -rex[t]) : 0.f; };
       if (EPI == EPI_SWIGLU) {

@@ -158,7 +158,11 @@ __device__ __forceinline__ f32x16_t mfma32_bf16(u32x4 a, u32x4 b, f32x16_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+// x * sigmoid(x) with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each);
+// every kernel's SwiGLU goes through it, so they all agree bit for bit.
+__device__ __forceinline__ float silu_f(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+}
 // The gated activation on (bf16-valued) gate/up values, fp32 (QMOE_ACT_*: silu(g)*u; its clamped
 // form, src/quanta/dsv4/moe.py:74-77; SwiGLU-OAI, src/quanta/minimax/model_m3.py:112-128).
 __device__ __forceinline__ float glu_f(float g, float u, int act, float alpha, float limit) {
@@ -166,7 +170,7 @@ __device__ __forceinline__ float glu_f(float g, float u, int act, float alpha, f
   const float gc = fminf(g, limit);
   const float uc = fminf(fmaxf(u, -limit), limit);
   return (act == QMOE_ACT_SILU_CLAMP) ? silu_f(gc) * uc
-                                      : (uc + 1.0f) * (gc / (1.0f + __expf(-alpha * gc)));
+                                      : (uc + 1.0f) * (gc * __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * gc)));
 }
 
 // Upper bound on the number of m-tiles a permuted (token, slot) list can produce.

@@ -132,8 +132,9 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
     // gate/up are bf16 tensors in the reference's flow; the gated activation runs on them in
     // fp32 and rounds once to bf16 (QMOE_ACT_*: the clamped forms of src/quanta/dsv4/moe.py:74-77
     // and src/quanta/minimax/model_m3.py:112-128)
-    const float g = bf16_to_f32(f32_to_bf16(v));
-    const float u = bf16_to_f32(f32_to_bf16(v_up));
+    // (one conversion for both; a NaN's payload may differ, the output is the canonical NaN)
+    const uint32_t gu = pack_bf16x2_rne(v, v_up);
+    const float g = bf16lo_to_f32(gu), u = bf16hi_to_f32(gu);
     const uint16_t o = f32_to_bf16(glu_f(g, u, a.glu, a.glu_alpha, a.glu_limit));
     if (COH) coh_st16(static_cast<uint16_t*>(a.out) + off, o);
     else static_cast<uint16_t*>(a.out)[off] = o;

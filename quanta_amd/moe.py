@@ -736,6 +736,10 @@ def _gen_experts(v, rows: int, K: int, E: int, name: str):
             words = words.view(torch.int32)
         if words.dtype != torch.int32 or tuple(words.shape) != (E, rows, K * bits // 32):
             raise ValueError(f"{name}: packed must be uint32 [{E}, {rows}, {K * bits // 32}]")
+        for part in ("scale", "bias"):
+            if tuple(v[part].shape) != (E, rows, K // gs):
+                raise ValueError(f"{name}.{part} {list(v[part].shape)} does not match group_size "
+                                 f"{gs} (expected {[E, rows, K // gs]})")
         sc = _gen_tensor(v["scale"], (E, rows, K // gs), f"{name}.scale")
         bi = _gen_tensor(v["bias"], (E, rows, K // gs), f"{name}.bias")
         if sc.dtype != bi.dtype:

@@ -97,9 +97,15 @@ def test_topk_override_and_errors(gpu):
     with pytest.raises(ValueError, match="sparse=False"):
         qwen35_moe(x[None], p, cfg, sparse=False)
     with pytest.raises(TypeError):
-        qwen35_moe(x[None].float(), p, cfg)
+        qwen35_moe(x[None].half(), p, cfg)
+    # float32 activations take the reference-dtype path: float32 out, the bf16 block's routing
+    # and (x being bf16-valued) the same values to the bf16 output's rounding
+    y32 = qwen35_moe(x[None].float(), p, cfg)[0]
+    assert y32.dtype == torch.float32
+    assert_close(f64(y32), f64(qwen35_moe(x[None], p, cfg)[0]), "float32 x", want_rounded=True)
+    # a group size that does not match the stored scales fails loud
     bad = dict(p["experts_gate_up"], group_size=32)
-    with pytest.raises(ValueError, match="group_size 64"):
+    with pytest.raises(ValueError, match="group_size"):
         qwen35_moe(x[None], dict(p, experts_gate_up=bad), cfg)
 
 
