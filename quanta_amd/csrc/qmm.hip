@@ -200,6 +200,20 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds_off) {
 }
 // Wait until at most n of this wavefront's vector-memory operations are outstanding (they
 // complete in issue order).
+// The same copies from a wave-uniform base address (a scalar register pair) plus a 32-bit
+// per-lane offset: the base costs no vector registers.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_off) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(lds_off) : "memory");
+}
+__device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_off) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(lds_off) : "memory");
+}
 // A byte loaded and waited for in one asm block, before any DMA of the kernel is issued: the
 // compiler then sees a ready value and never guards its later uses with a vmcnt wait, which it
 // cannot tell from the DMA prefetch's own (those waits would drain the prefetch every superblock).
@@ -714,7 +728,7 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
   auto b_slot = [&](int p) { return (p & 1) * SLOT + kWdABytes + wave * BWAVE; };
 
   // this wavefront's four weight tiles (SwiGLU: gate tiles first, then their up tiles)
-  const char* wcode[4];
+  // (tile bases are wave-uniform: the copies take them from scalar registers)
   const char* wtile[4];   // the tile's first superblock
   const char* wsb[4];
   const int8_t* wexp[4];
@@ -726,7 +740,6 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
                        : 32 * cb + 4 * wave + t;
     const int64_t tb = (ebase + tl) * nsb;
     wtile[t] = static_cast<const char*>(a.codes) + tb * SBB;
-    wcode[t] = wtile[t] + lane * 16;
     wsb[t] = reinterpret_cast<const char*>(a.sb) + tb * 128;
     wexp[t] = a.row_exp + (ebase + tl) * 16 + (lane & 15);
   }
@@ -739,9 +752,9 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
     for (int t = 0; t < 4; ++t) rex[t] = rl.ex[t] - DS;
     if (a_on && lane < 16) row_tab[arow_r] = (arow >= 0) ? rl.rs : -1.0f;
   }
-  // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's
-  const char* sb_src0 = wsb[lane >> 5] + 4 * (lane & 31);
-  const char* sb_src1 = wsb[2 + (lane >> 5)] + 4 * (lane & 31);
+  // scale/bias copies: lanes 0-31 take the first tile's 128 B, lanes 32-63 the second's (tiles
+  // 0, 1 and 2, 3 are consecutive, nsb * 128 bytes apart)
+  const uint32_t sb_voff = static_cast<uint32_t>((lane >> 5) * nsb * 128 + 4 * (lane & 31));
 
   // all loads of superblock p: A 4 (when a_on) + codes 4 + scale/bias 2
   auto issue = [&](int p) __attribute__((always_inline)) {
@@ -758,13 +771,13 @@ __device__ __forceinline__ void wide_body(const QmmArgs& a) {
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 3; ++i)
-          dma4(wtile[t] + static_cast<int64_t>(p) * SBB + 256 * i + 4 * lane, dst + t * SBB + 256 * i);
+          dma4s(wtile[t] + static_cast<int64_t>(p) * SBB + 256 * i, 4 * lane, dst + t * SBB + 256 * i);
     } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dma16(wcode[t] + static_cast<int64_t>(p) * SBB, dst + t * SBB);
+      for (int t = 0; t < 4; ++t) dma16s(wtile[t] + static_cast<int64_t>(p) * SBB, 16 * lane, dst + t * SBB);
     }
-    dma4(sb_src0 + static_cast<int64_t>(p) * 128, dst + 4 * SBB);
-    dma4(sb_src1 + static_cast<int64_t>(p) * 128, dst + 4 * SBB + 256);
+    dma4s(wsb[0] + static_cast<int64_t>(p) * 128, sb_voff, dst + 4 * SBB);
+    dma4s(wsb[2] + static_cast<int64_t>(p) * 128, sb_voff, dst + 4 * SBB + 256);
   };
 
   f32x4_t acc[8][4];

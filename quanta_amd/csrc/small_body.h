@@ -132,15 +132,17 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
     // gate/up are bf16 tensors in the reference's flow; the gated activation runs on them in
     // fp32 and rounds once to bf16 (QMOE_ACT_*: the clamped forms of src/quanta/dsv4/moe.py:74-77
     // and src/quanta/minimax/model_m3.py:112-128)
-    // (one conversion for both; a NaN's payload may differ, the output is the canonical NaN)
+    // (the hardware round-to-nearest-even conversions: a NaN stays a NaN, its payload may differ)
     const uint32_t gu = pack_bf16x2_rne(v, v_up);
     const float g = bf16lo_to_f32(gu), u = bf16hi_to_f32(gu);
-    const uint16_t o = f32_to_bf16(glu_f(g, u, a.glu, a.glu_alpha, a.glu_limit));
+    const float h = glu_f(g, u, a.glu, a.glu_alpha, a.glu_limit);
+    const uint16_t o = static_cast<uint16_t>(pack_bf16x2_rne(h, h));
     if (COH) coh_st16(static_cast<uint16_t*>(a.out) + off, o);
     else static_cast<uint16_t*>(a.out)[off] = o;
   } else if (EPI == EPI_BF16) {
-    if (COH) coh_st16(static_cast<uint16_t*>(a.out) + off, f32_to_bf16(v));
-    else static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(v);
+    const uint16_t o = static_cast<uint16_t>(pack_bf16x2_rne(v, v));
+    if (COH) coh_st16(static_cast<uint16_t*>(a.out) + off, o);
+    else static_cast<uint16_t*>(a.out)[off] = o;
   } else {
     static_cast<float*>(a.out)[off] = v;
   }
