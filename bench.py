@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--shared", choices=("int8", "bf16"), default="int8",
                     help="shared-expert weights: int8 g64 as the bake stores them (dequantized in "
                          "registers to the bf16 weights the reference loads; same outputs) or bf16")
+    ap.add_argument("--flow-mode", type=int, choices=(0, 1, 2), default=None,
+                    help="qmoe_set_decode_flow mode: 0 chain, 1 the library's default (the dataflow "
+                         "launch for one and two tokens), 2 the dataflow launch wherever it fits")
     ap.add_argument("--no-flow", action="store_true",
                     help="launch the decode stages one by one (qmoe_set_decode_flow(0)) instead of "
                          "the one dataflow launch after the router")
@@ -176,6 +179,8 @@ def main():
     L.load()
     if args.no_flow:
         L.load().qmoe_set_decode_flow(0)
+    elif args.flow_mode is not None:
+        L.load().qmoe_set_decode_flow(args.flow_mode)
     dev = torch.device("cuda", 0)
     spec = synth.spec(args.config)
     cfg = spec.cfg
