@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define QMOE_ABI_VERSION 9
+#define QMOE_ABI_VERSION 10
 
 #define QMOE_OK 0
 #define QMOE_EINVAL (-1)
@@ -198,6 +198,16 @@ int qmoe_forward_noalloc(const qmoe_config_t* cfg, const qmoe_weights_t* w, cons
  * current device since the library loaded (0 in a healthy run; synchronous). */
 int qmoe_set_decode_flow(int mode);
 uint32_t qmoe_flow_timeouts(void);
+
+/* Routing tail (tuning; no counterpart in the reference, whose MLX graph schedules its
+ * primitives itself). Decode batches sorted by expert, with a bf16 router and a shared expert in
+ * the router launch, can rank their tokens and sort the slots in that launch's last router
+ * workgroup instead of the top-k and permute launches; the outputs are the same bit for bit.
+ * Mode 1 (the default) takes it while the batch has fewer tokens than that workgroup has
+ * wavefronts (c2's shape: up to 15 tokens), where it is the faster path; 2 takes it up to 64
+ * tokens (tests, measurements); 0 never. Returns the previous mode (process-wide; an unknown
+ * mode changes nothing). */
+int qmoe_set_route_tail(int mode);
 
 /* Routed experts whose widths vary per (expert, projection) (Kimi's QuantizedSparseMoE,
  * src/quanta/modeling/quantized.py:40-84: one packed stack per projection and width, each expert

@@ -23,7 +23,7 @@ REGIME_AUTO, REGIME_SMALL, REGIME_LARGE = 0, 1, 2
 EPI_SWIGLU, EPI_BF16, EPI_F32 = 0, 1, 2
 ACT_SILU, ACT_SILU_CLAMP, ACT_SWIGLU_OAI = 0, 1, 2
 SMALL_M_TILE, LARGE_M_TILE = 16, 128
-ABI_VERSION = 9
+ABI_VERSION = 10
 NOALLOC_SCRATCH_BYTES = 64 << 20   # QMOE_NOALLOC_SCRATCH_BYTES
 
 
@@ -195,6 +195,7 @@ SIGNATURES = {
     "qmoe_forward_general": (_I, [ctypes.POINTER(QmoeGeneralConfig), ctypes.POINTER(QmoeGeneralWeights),
                                   _P, _I64, _P, _P, ctypes.c_size_t, _P]),
     "qmoe_set_decode_flow": (_I, [_I]),
+    "qmoe_set_route_tail": (_I, [_I]),
     "qmoe_flow_timeouts": (ctypes.c_uint32, []),
 }
 

@@ -9,6 +9,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <map>
 #include <mutex>
@@ -312,6 +313,10 @@ constexpr int64_t kSlotMajorCapTokens = 16;
 // than the top-k launch it replaces (c2: N <= 3, 64 workgroups per slot; c1: N <= 8, 16).
 constexpr int64_t kRouteMaxWorkgroups = 2048;
 
+// The routing tail of the router pair launch (qmoe_set_route_tail): 0 off, 1 (default) where it
+// is the faster path, 2 wherever it fits.
+static std::atomic<int> g_route_tail{1};
+
 // Routed expert bytes (gate_up + down) of one expert in the config's formats.
 static double expert_bytes(const qmoe_config_t& c) {
   auto per_weight = [](int fmt) {
@@ -380,7 +385,7 @@ static bool shared_expands(const qmoe_config_t& c, int64_t N) {
 // ------------------------------------------------------------------ forward workspace layout
 struct WsLayout {
   size_t logits, idx, w, sg, counts, offsets, tile_off, tile_map, tile_map_big, sorted, inv, h,
-      d, sh_h, sh_out, sh_w16, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, sync, total;
+      d, sh_h, sh_out, sh_w16, x16, x_sinv, h16, h_sinv, awq_x, awq_gu, sync, route_ctr, total;
   int64_t max_tiles, max_tiles_big, sync_words;
 };
 
@@ -433,6 +438,8 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   // the decode dataflow kernel's counters (cleared by the router launch of every call)
   L.sync_words = decode_flow_sync_words(mc, c.hidden);
   L.sync = take(static_cast<size_t>(L.sync_words) * 4);
+  // the routing tail's arrival counter (one 64-bit word; no clearing needed, RouteTail)
+  L.route_ctr = take(8);
   L.total = o;
   return L;
 }
@@ -621,6 +628,11 @@ extern "C" int qmoe_grouped_qmm(const uint16_t* act, int64_t act_rows, const int
 extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
   if (!cfg || N <= 0) return 0;
   return ws_layout(*cfg, N).total;
+}
+
+extern "C" int qmoe_set_route_tail(int mode) {
+  if (mode < 0 || mode > 2) return qmoe::g_route_tail.load();
+  return qmoe::g_route_tail.exchange(mode);
 }
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
@@ -840,6 +852,17 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                         decode_flow_enabled(n) &&
                         decode_flow_fits(n, c.top_k, c.n_experts, c.hidden, c.inter, c.shared_inter);
   uint32_t* sync = reinterpret_cast<uint32_t*>(base + L.sync);
+  // Decode batches routed through the permute, with the router in the pair launch: that launch's
+  // last router workgroup also ranks the tokens and sorts the slots by expert (RouteTail), in
+  // place of the top-k and permute launches. Same outputs, bit for bit. One workgroup ranks at
+  // one token per wavefront here; with more tokens than its wavefronts the separate top-k launch,
+  // which spreads them over the chip, is faster (c2: 3 us saved at 8 tokens, even at 16, 6 us
+  // lost at 32).
+  const int tail_mode = g_route_tail.load(std::memory_order_relaxed);
+  const bool route_tail = fuse_gu && !use_flow && !slot_major && !hybrid &&
+                          c.n_experts <= kRouteTailMaxExperts && c.top_k <= 64 &&
+                          ((tail_mode == 1 && N < pair_waves(c.hidden)) ||
+                           (tail_mode == 2 && N <= kRouteTailMaxTokens));
 
   // 2. router logits (+ the shared-expert gate logit in column E)
   int ld = 0;
@@ -869,10 +892,23 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       a.zero_words = sync;
       a.n_zero = static_cast<int>(L.sync_words / kSyncStride);
     }
-    if (fuse_gu)
+    if (route_tail) {
+      RouteTail T{};
+      T.ctr = reinterpret_cast<unsigned long long*>(base + L.route_ctr);
+      T.logits = logits; T.ld = ld; T.N = n;
+      T.P = topk_params(wts->router_bias, c.n_experts, c.top_k, c.scoring, c.n_group, c.topk_group,
+                        c.norm_topk, c.routed_scale, has_sg);
+      T.idx = idx; T.w = wv; T.sg = sg;
+      T.counts = counts; T.offsets = offsets; T.tile_off = tile_off; T.sorted = sorted; T.inv = inv;
+      T.tile_map = tile_map; T.max_tiles = static_cast<int>(bound_small);
+      T.words = (n + 31) / 32;
+      T.vpl = topk_vpl(c.n_experts);
+      rc = launch_qmm_pair_route(a, sgu, stream, sfmt, T);
+    } else if (fuse_gu) {
       rc = launch_qmm_pair_bf16(a, sgu, stream, sfmt);
-    else
+    } else {
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + rt - 1) / rt, stream);
+    }
   }
   if (rc) return rc;
   if (use_flow) {
@@ -894,8 +930,9 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   const bool route_in_gate_up =
       slot_major && !mixed && gfmt == FMT_INT4 && route_gate_up_fits(c.n_experts, c.top_k) &&
       route_gate_up_workgroups(c.hidden, 2 * c.inter, mc) <= kRouteMaxWorkgroups;
-  if (route_in_gate_up) {
-    // (the routed gate_up below ranks the logits itself)
+  if (route_in_gate_up || route_tail) {
+    // (the routed gate_up below ranks the logits itself; the routing tail has written the
+    // routing and the permute's outputs)
   } else if (slot_major) {
     // 3-4. top-k with the slot-major tile map
     rc = launch_topk(logits, ld, wts->router_bias, n, c.n_experts, c.top_k, c.scoring, c.n_group,

@@ -88,9 +88,166 @@ qmm_route_gate_up_shdown_kernel(QmmArgs a, int n_jobs, SlotRoute route, int gx1,
 // arithmetic of its own launch.
 // NORM: both products RMSNorm their activation rows on the fly (QmmArgs::norm_w), and the first
 // product's job 0 writes the normalised rows (norm_out).
-template <int EPI1, int EPI2, int W, int MT, bool NORM = false, int FMT2 = FMT_BF16>
+// The routing tail (RouteTail): this router workgroup's coherent logit stores are complete
+// (s_waitcnt 0, then the workgroup barrier) before it counts itself; the last workgroup to
+// arrive ranks every token, one wavefront per token, with coherent loads of the logits, keeps
+// the ids in LDS, sorts the slots by expert from them and resets the counter.
+__device__ __forceinline__ bool route_tail_arrive(const RouteTail& T) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int s_last;
+  if (threadIdx.x == 0) {
+    constexpr unsigned long long kMask = (1ull << 20) - 1;
+    const unsigned long long old =
+        __hip_atomic_fetch_add(T.ctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long cnt;
+    if ((old >> 20) == kRouteTailTag) {
+      cnt = (old & kMask) + 1;
+    } else {
+      // a word without the tag (a fresh workspace): replace it by a tagged count of 1, or count
+      // on the tagged word another workgroup has put there since; this workgroup's add above
+      // landed on the untagged word and is discarded with it
+      unsigned long long cur = __hip_atomic_load(T.ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long want;
+      do {
+        want = ((cur >> 20) == kRouteTailTag) ? cur + 1 : ((kRouteTailTag << 20) | 1ull);
+      } while (!__hip_atomic_compare_exchange_strong(T.ctr, &cur, want, __ATOMIC_RELAXED,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      cnt = want & kMask;
+    }
+    s_last = static_cast<int>(cnt) == T.total;
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
+template <int VPL>
+__device__ __forceinline__ void route_tail_topk(const RouteTail& T, int32_t* ids) {
+  const int lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  for (int t = threadIdx.x >> 6; t < T.N; t += nw) {
+    const int id = topk_store<VPL, true>(T.logits, T.ld, T.P, t, lane, T.idx, T.w, T.sg);
+    if (lane < T.P.k) ids[t * T.P.k + lane] = id;
+  }
+}
+
+// Exclusive scan of one value per thread across the workgroup (1 to 16 wavefronts); tmp holds
+// 33 ints and is free again on return.
+__device__ __forceinline__ int tail_scan(int v, int* tmp, int& total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) tmp[wid] = incl;
+  __syncthreads();
+  if (wid == 0) {
+    const int s = lane < nw ? tmp[lane] : 0;
+    int si = s;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const int o = __shfl_up(si, off);
+      if (lane >= off) si += o;
+    }
+    if (lane < nw) tmp[16 + lane] = si - s;
+    if (lane == nw - 1) tmp[32] = si;
+  }
+  __syncthreads();
+  const int r = tmp[16 + wid] + incl - v;
+  total = tmp[32];
+  __syncthreads();
+  return r;
+}
+
+// The stable permute of the N * k slots by expert (N <= 64), the permute launch's outputs for
+// 16-row m-tiles: counts, offsets and the m-tile prefix (E + 1 entries each with the totals),
+// the tile descriptors {expert, first sorted position, rows, 0} with -1 sentinels up to
+// max_tiles, and sorted / inv. A slot's stable rank within its expert is the number of earlier
+// tokens that chose the expert (top-k experts of a token are distinct): the popcount of the
+// expert's 64-bit token mask below the token. Thread i owns experts [i * ve, i * ve + ve).
+__device__ __forceinline__ void route_tail_permute(const RouteTail& T, const int32_t* ids,
+                                                   unsigned long long* mask, int* hist, int* offs,
+                                                   int* tmp) {
+  const int E = T.P.E, k = T.P.k, mc = T.N * k, tid = threadIdx.x, nthr = blockDim.x;
+  for (int e = tid; e < E; e += nthr) {
+    hist[e] = 0;
+    mask[e] = 0ull;
+  }
+  __syncthreads();
+  for (int m = tid; m < mc; m += nthr) {
+    const int e = ids[m];
+    atomicAdd(&hist[e], 1);
+    atomicOr(&mask[e], 1ull << (m / k));
+  }
+  __syncthreads();
+  const int ve = (E + nthr - 1) / nthr;   // at most 2 (E <= 512 and 256 threads or more)
+  int c[2], rows = 0, tiles = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid * ve + j;
+    c[j] = (j < ve && e < E) ? hist[e] : 0;
+    rows += c[j];
+    tiles += (c[j] + kSmallMTile - 1) / kSmallMTile;
+  }
+  int rows_total, tiles_total;
+  int ex = tail_scan(rows, tmp, rows_total);
+  int tex = tail_scan(tiles, tmp, tiles_total);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid * ve + j;
+    if (j >= ve || e >= E) break;
+    T.counts[e] = c[j];
+    T.offsets[e] = ex;
+    T.tile_off[e] = tex;
+    offs[e] = ex;
+    const int nt = (c[j] + kSmallMTile - 1) / kSmallMTile;
+    for (int i = 0; i < nt; ++i)
+      reinterpret_cast<int4*>(T.tile_map)[tex + i] =
+          make_int4(e, ex + i * kSmallMTile, min(kSmallMTile, c[j] - i * kSmallMTile), 0);
+    ex += c[j];
+    tex += nt;
+  }
+  if (tid == 0) {
+    T.offsets[E] = rows_total;
+    T.tile_off[E] = tiles_total;
+  }
+  for (int t = tiles_total + tid; t < T.max_tiles; t += nthr)
+    reinterpret_cast<int4*>(T.tile_map)[t] = make_int4(-1, 0, 0, 0);
+  __syncthreads();
+  for (int m = tid; m < mc; m += nthr) {
+    const int e = ids[m], t = m / k;
+    const int pos = offs[e] + __popcll(mask[e] & ((1ull << t) - 1ull));
+    T.sorted[pos] = m;
+    T.inv[m] = pos;
+  }
+}
+
+__device__ __forceinline__ void route_tail_run(const RouteTail& T) {
+  // dynamic LDS: token masks [E] (8 bytes each), histogram [E], offsets [E], scan scratch [34],
+  // slot ids [N * k]
+  extern __shared__ unsigned long long tail_lds[];
+  unsigned long long* mask = tail_lds;
+  int* hist = reinterpret_cast<int*>(mask + T.P.E);
+  int* offs = hist + T.P.E;
+  int* tmp = offs + T.P.E;
+  int32_t* ids = tmp + 34;
+  switch (T.vpl) {
+    case 1: route_tail_topk<1>(T, ids); break;
+    case 2: route_tail_topk<2>(T, ids); break;
+    case 4: route_tail_topk<4>(T, ids); break;
+    default: route_tail_topk<8>(T, ids); break;
+  }
+  __syncthreads();
+  route_tail_permute(T, ids, mask, hist, offs, tmp);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(T.ctr, kRouteTailTag << 20, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int EPI1, int EPI2, int W, int MT, bool NORM = false, int FMT2 = FMT_BF16, bool TAIL = false>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
-qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2) {
+qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2, RouteTail T) {
   constexpr int R1 = SmallCfg<FMT_BF16, EPI1, W, 1, 1, MT>::RED;
   constexpr int R2 = SmallCfg<FMT2, EPI2, W, 1, 1, MT>::RED;
   constexpr int RR = R1 > R2 ? R1 : R2;
@@ -101,10 +258,16 @@ qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2)
   // follows this one
   if (a1.zero_words && blockIdx.x == 0 && blockIdx.y == 0)
     for (int i = threadIdx.x; i < a1.n_zero; i += blockDim.x) a1.zero_words[i * kSyncStride] = 0u;
-  if (static_cast<int>(blockIdx.x) < gx1)
-    small_body<FMT_BF16, EPI1, W, 1, 1, MT, NORM>(a1, n_jobs1, blockIdx.x, blockIdx.y, red);
-  else
+  if (static_cast<int>(blockIdx.x) < gx1) {
+    // (TAIL: the logits go out with coherent stores, read by the last router workgroup)
+    small_body<FMT_BF16, EPI1, W, 1, 1, MT, NORM, 0, 0, TAIL ? kCohOut : 0>(a1, n_jobs1, blockIdx.x,
+                                                                          blockIdx.y, red);
+    if constexpr (TAIL) {
+      if (route_tail_arrive(T)) route_tail_run(T);
+    }
+  } else {
     small_body<FMT2, EPI2, W, 1, 1, MT, NORM>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
+  }
 }
 
 // The routed gate_up (int4 SwiGLU over the permuted m-tiles, small-regime shape W/CPW/JPW) and
@@ -1260,24 +1423,28 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
   return check_launch("qmm(route)");
 }
 
-template <int W, int FMT2>
-static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream) {
+template <int W, int FMT2, bool TAIL = false>
+static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream,
+                          RouteTail T = RouteTail{}) {
   constexpr int WAVES = W > 4 ? W : 4;
   constexpr int JPWG = WAVES / W;
   const int n1 = a1.n_rows / 16, n2 = a2.n_rows / 32;   // fp32 epilogue jobs, SwiGLU jobs
   const int gx1 = (n1 + JPWG - 1) / JPWG, gx2 = (n2 + JPWG - 1) / JPWG;
-  const dim3 g2(gx1 + gx2, static_cast<unsigned>((mtiles + 1) / 2)), g1(gx1 + gx2, static_cast<unsigned>(mtiles));
-  if (a1.norm_w) {
-    if (mtiles >= kSmallMt2MinTiles)   // two m-tiles per wavefront, as in launch_small_k
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2, true, FMT2><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
-    else
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1, true, FMT2><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
-  } else {
-    if (mtiles >= kSmallMt2MinTiles)
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 2, false, FMT2><<<g2, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
-    else
-      qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, 1, false, FMT2><<<g1, 64 * WAVES, 0, stream>>>(a1, n1, gx1, a2, n2);
+  const bool mt2 = mtiles >= kSmallMt2MinTiles;   // two m-tiles per wavefront, as in launch_small_k
+  const dim3 g(gx1 + gx2, static_cast<unsigned>(mt2 ? (mtiles + 1) / 2 : mtiles));
+  size_t lds = 0;
+  if (TAIL) {
+    T.total = gx1 * static_cast<int>(g.y);
+    lds = route_tail_lds_bytes(T.P.E, T.N, T.P.k);
   }
+#define QMOE_PAIR(MT, NORM) \
+  qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, MT, NORM, FMT2, TAIL><<<g, 64 * WAVES, lds, stream>>>(a1, n1, gx1, a2, n2, T)
+  if (a1.norm_w) {
+    if (mt2) QMOE_PAIR(2, true); else QMOE_PAIR(1, true);
+  } else {
+    if (mt2) QMOE_PAIR(2, false); else QMOE_PAIR(1, false);
+  }
+#undef QMOE_PAIR
 }
 
 template <int FMT2>
@@ -1301,6 +1468,40 @@ bool pair_norm_fusable(int K, int64_t rows) {
   // 16.2 us against the plain launch's 11.0); longer chunks only for one or two tokens, where
   // the separate norm launch costs a kernel boundary more than the fused pass does
   return steps <= (mt2 ? 4 : 8) || (rows <= 2 && steps <= 16);
+}
+
+int launch_qmm_pair_route(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2,
+                          const RouteTail& tail) {
+  if (a1.offsets || a2.offsets || a1.dense_rows != a2.dense_rows || a1.K != a2.K || a1.K % 32 ||
+      a1.n_rows % 16 || a2.n_rows % 32 || a1.dense_rows <= 0)
+    return fail("qmm pair: two dense products over the same rows and K required");
+  if (fmt2 != FMT_BF16 && fmt2 != FMT_INT8) return fail("qmm pair: the second product is bf16 or int8");
+  if (fmt2 == FMT_INT8 && (a1.K % 64 || !a2.sb)) return fail("qmm pair: int8 weights need K % 64 == 0 and sb");
+  if ((a1.norm_w != nullptr) != (a2.norm_w != nullptr) || a2.norm_out)
+    return fail("qmm pair: the fused norm applies to both products; the first writes the rows");
+  if (a1.norm_w && !pair_norm_fusable(a1.K, a1.dense_rows))
+    return fail("qmm pair: the fused norm needs one job per workgroup and one load batch per chunk");
+  const int mc = tail.N * tail.P.k;
+  if (tail.N != a1.dense_rows || tail.N > kRouteTailMaxTokens || tail.P.E <= 0 ||
+      tail.P.E > kRouteTailMaxExperts || tail.P.k <= 0 || tail.P.k > 64 || tail.P.k > tail.P.E ||
+      !tail.ctr || tail.logits != a1.out ||
+      tail.ld != a1.ld_out || !tail.counts || !tail.tile_map || tail.words != (tail.N + 31) / 32 ||
+      tail.vpl != topk_vpl(tail.P.E) ||
+      tail.max_tiles < mtile_upper_bound(mc, tail.P.E, kSmallMTile))
+    return fail("qmm pair (routing tail): bad routing arguments");
+  const int64_t mtiles = (a1.dense_rows + kSmallMTile - 1) / kSmallMTile;
+#define QMOE_PAIR_T(W)                                                                     \
+  if (fmt2 == FMT_INT8) launch_pair_w<W, FMT_INT8, true>(a1, a2, mtiles, stream, tail);     \
+  else launch_pair_w<W, FMT_BF16, true>(a1, a2, mtiles, stream, tail);
+  switch (bf16_chunks(a1.K)) {
+    case 16: QMOE_PAIR_T(16) break;
+    case 8: QMOE_PAIR_T(8) break;
+    case 4: QMOE_PAIR_T(4) break;
+    case 2: QMOE_PAIR_T(2) break;
+    default: QMOE_PAIR_T(1) break;
+  }
+#undef QMOE_PAIR_T
+  return check_launch("qmm pair (routing tail)");
 }
 
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2) {

@@ -103,7 +103,18 @@ struct TopkParams {
 // IDS_ONLY: lane r < rounds returns the r-th expert and out_w is undefined; the selection is the
 // same, and softmax routing without a bias (which selects by logit) then skips the
 // probabilities altogether.
-template <int VPL, bool IDS_ONLY = false>
+// A logit read; COH: an agent-scope (cross-XCD coherent) load, for logits that other
+// workgroups of the same launch wrote with coherent stores.
+template <bool COH>
+__device__ __forceinline__ float logit_ld(const float* p) {
+  if constexpr (COH)
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+  else
+    return *p;
+}
+
+template <int VPL, bool IDS_ONLY = false, bool COH = false>
 __device__ __forceinline__ void topk_token(const float* __restrict__ row, const TopkParams& P,
                                            int lane, int& out_id, float& out_w, int rounds = 0) {
   const float NEG_INF = -INFINITY;
@@ -114,7 +125,7 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
   float lg[VPL], sc[VPL], ch[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const float v = row[min(e_base + i, E - 1)];
+    const float v = logit_ld<COH>(row + min(e_base + i, E - 1));
     lg[i] = (e_base + i < E) ? v : NEG_INF;
   }
   const bool by_logit = (P.scoring == QMOE_SCORE_SOFTMAX);
@@ -267,6 +278,44 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
   out_w = my_w * P.scale;
 }
 
+// The routing tail of the router pair launch, for decode batches routed through the stable
+// permute: the router workgroups store their logits with coherent stores and count their
+// arrival; the last one ranks every token (coherent loads) and runs the permute, in place of the
+// top-k and permute launches. The arrival counter is one 64-bit word in the workspace holding
+// (kRouteTailTag << 20) | count, counted with atomic adds; a workgroup that finds a word without
+// the tag (a fresh workspace) replaces it by a tagged count, so the word needs no clearing, and
+// the last workgroup resets it to a tagged 0 for the next call (or the next replay of a capture).
+constexpr unsigned long long kRouteTailTag = 0xA5C3E1F7B9Dull;   // 44 bits
+struct RouteTail {
+  unsigned long long* ctr;
+  int total;                  // router workgroups of the launch
+  const float* logits;
+  int ld;
+  TopkParams P;
+  int N;
+  int32_t* idx;
+  float* w;
+  float* sg;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* tile_off;
+  int32_t* sorted;
+  int32_t* inv;
+  int32_t* tile_map;
+  int max_tiles;
+  int words;                  // token bitmap words per expert, (N + 31) / 32
+  int vpl;                    // experts per lane of the top-k wavefront (topk_vpl)
+};
+constexpr int kRouteTailMaxTokens = 64, kRouteTailMaxExperts = 512;
+// dynamic LDS of the tail: a 64-bit token mask, a count and an offset per expert, scan scratch
+// and the ids of the N * k slots
+inline size_t route_tail_lds_bytes(int E, int N, int k) {
+  return 16 * static_cast<size_t>(E) + sizeof(int) * (34 + static_cast<size_t>(N) * k);
+}
+// The router pair launch (launch_qmm_pair_bf16) with the routing tail.
+int launch_qmm_pair_route(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2,
+                          const RouteTail& tail);
+
 inline TopkParams topk_params(const float* bias, int E, int k, int scoring, int n_group,
                               int topk_group, int norm_topk, float scale, int has_sg) {
   TopkParams P;
@@ -289,7 +338,7 @@ inline int topk_vpl(int E) {
 
 // Top-k of token t by one wavefront, stored as idx/w rows of k and the shared-expert gate
 // sigmoid(logit E); returns lane r's expert (r < k).
-template <int VPL>
+template <int VPL, bool COH = false>
 __device__ __forceinline__ int topk_store(const float* __restrict__ logits, int ld,
                                            const TopkParams& P, int t, int lane,
                                            int32_t* __restrict__ idx_out,
@@ -297,12 +346,12 @@ __device__ __forceinline__ int topk_store(const float* __restrict__ logits, int 
   const float* row = logits + static_cast<int64_t>(t) * ld;
   int id;
   float w;
-  topk_token<VPL>(row, P, lane, id, w);
+  topk_token<VPL, false, COH>(row, P, lane, id, w);
   if (lane < P.k) {
     idx_out[static_cast<int64_t>(t) * P.k + lane] = id;
     w_out[static_cast<int64_t>(t) * P.k + lane] = w;
   }
-  if (P.has_sg && lane == 0) sg_out[t] = 1.0f / (1.0f + expf(-row[P.E]));
+  if (P.has_sg && lane == 0) sg_out[t] = 1.0f / (1.0f + expf(-logit_ld<COH>(row + P.E)));
   return id;
 }
 

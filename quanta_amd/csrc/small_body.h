@@ -144,7 +144,8 @@ __device__ __forceinline__ void store_out(const QmmArgs& a, int row, int col, fl
     if (COH) coh_st16(static_cast<uint16_t*>(a.out) + off, o);
     else static_cast<uint16_t*>(a.out)[off] = o;
   } else {
-    static_cast<float*>(a.out)[off] = v;
+    if (COH) coh_st32(static_cast<float*>(a.out) + off, __float_as_uint(v));
+    else static_cast<float*>(a.out)[off] = v;
   }
 }
 

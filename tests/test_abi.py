@@ -13,7 +13,7 @@ from quanta_amd import _lib as L
 
 def test_library_loads_and_abi_version():
     lib = L.load()
-    assert lib.qmoe_abi_version() == L.ABI_VERSION == 9
+    assert lib.qmoe_abi_version() == L.ABI_VERSION == 10
 
 
 def test_every_header_symbol_is_exported_and_bound():
