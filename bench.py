@@ -77,10 +77,10 @@ def parse():
     ap.add_argument("--no-flow", action="store_true",
                     help="launch the decode stages one by one (qmoe_set_decode_flow(0)) instead of "
                          "the one dataflow launch after the router")
-    ap.add_argument("--route-tail", type=int, choices=(0, 1, 2), default=None,
-                    help="qmoe_set_route_tail mode: 0 the top-k and permute launches, 1 the "
-                         "library's default (the router launch's last workgroup ranks and sorts "
-                         "small decode batches), 2 that tail up to 64 tokens")
+    ap.add_argument("--route-tail", type=int, choices=(0, 1), default=None,
+                    help="qmoe_set_route_tail: 1 (the library's default) ranks and sorts decode "
+                         "batches in the router launch's last workgroups, 0 uses the top-k and "
+                         "permute launches")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3, help="batches in the CPU-baseline sample")
     ap.add_argument("--only", default="", help="profiling aid: 'layer' or 'kernel' loop only")

@@ -194,20 +194,20 @@ int qmoe_forward_noalloc(const qmoe_config_t* cfg, const qmoe_weights_t* w, cons
  * qmoe_set_decode_flow(0) makes later calls launch the stages one by one, (2) takes the single
  * launch for every batch it covers (up to the slot-major sizes; for tests and measurements). It
  * returns the previous mode (process-wide, not thread-safe against calls in flight).
- * qmoe_flow_timeouts() returns how many in-kernel waits have run out of their bound on the
- * current device since the library loaded (0 in a healthy run; synchronous). */
+ * qmoe_flow_timeouts() returns how many in-kernel waits (this launch's and the routing tail's,
+ * below) have run out of their bound on the current device since the library loaded (0 in a
+ * healthy run; synchronous). */
 int qmoe_set_decode_flow(int mode);
 uint32_t qmoe_flow_timeouts(void);
 
 /* Routing tail (tuning; no counterpart in the reference, whose MLX graph schedules its
- * primitives itself). Decode batches sorted by expert, with a bf16 router and a shared expert in
- * the router launch, can rank their tokens and sort the slots in that launch's last router
- * workgroup instead of the top-k and permute launches; the outputs are the same bit for bit.
- * Mode 1 (the default) takes it while the batch has fewer tokens than that workgroup has
- * wavefronts (c2's shape: up to 15 tokens), where it is the faster path; 2 takes it up to 64
- * tokens (tests, measurements); 0 never. Returns the previous mode (process-wide; an unknown
- * mode changes nothing). */
-int qmoe_set_route_tail(int mode);
+ * primitives itself). Decode batches of up to 64 tokens sorted by expert, with a bf16 router and
+ * a shared expert in the router launch, rank their tokens in that launch's last router
+ * workgroups and sort the slots in the last of them, instead of the top-k and permute launches;
+ * the outputs are the same bit for bit. On (1) by default; qmoe_set_route_tail(0) makes later
+ * calls use the separate launches. Returns the previous setting (process-wide; other values
+ * change nothing). */
+int qmoe_set_route_tail(int on);
 
 /* Routed experts whose widths vary per (expert, projection) (Kimi's QuantizedSparseMoE,
  * src/quanta/modeling/quantized.py:40-84: one packed stack per projection and width, each expert

@@ -313,8 +313,7 @@ constexpr int64_t kSlotMajorCapTokens = 16;
 // than the top-k launch it replaces (c2: N <= 3, 64 workgroups per slot; c1: N <= 8, 16).
 constexpr int64_t kRouteMaxWorkgroups = 2048;
 
-// The routing tail of the router pair launch (qmoe_set_route_tail): 0 off, 1 (default) where it
-// is the faster path, 2 wherever it fits.
+// The routing tail of the router pair launch (qmoe_set_route_tail): 1 (default) on, 0 off.
 static std::atomic<int> g_route_tail{1};
 
 // Routed expert bytes (gate_up + down) of one expert in the config's formats.
@@ -438,8 +437,8 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   // the decode dataflow kernel's counters (cleared by the router launch of every call)
   L.sync_words = decode_flow_sync_words(mc, c.hidden);
   L.sync = take(static_cast<size_t>(L.sync_words) * 4);
-  // the routing tail's arrival counter (one 64-bit word; no clearing needed, RouteTail)
-  L.route_ctr = take(8);
+  // the routing tail's two counters (64-bit words; no clearing needed, RouteTail)
+  L.route_ctr = take(16);
   L.total = o;
   return L;
 }
@@ -630,9 +629,9 @@ extern "C" size_t qmoe_forward_workspace(const qmoe_config_t* cfg, int64_t N) {
   return ws_layout(*cfg, N).total;
 }
 
-extern "C" int qmoe_set_route_tail(int mode) {
-  if (mode < 0 || mode > 2) return qmoe::g_route_tail.load();
-  return qmoe::g_route_tail.exchange(mode);
+extern "C" int qmoe_set_route_tail(int on) {
+  if (on < 0 || on > 1) return qmoe::g_route_tail.load();
+  return qmoe::g_route_tail.exchange(on);
 }
 
 static int pick_regime(const qmoe_config_t& c, int64_t N) {
@@ -853,16 +852,13 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                         decode_flow_fits(n, c.top_k, c.n_experts, c.hidden, c.inter, c.shared_inter);
   uint32_t* sync = reinterpret_cast<uint32_t*>(base + L.sync);
   // Decode batches routed through the permute, with the router in the pair launch: that launch's
-  // last router workgroup also ranks the tokens and sorts the slots by expert (RouteTail), in
-  // place of the top-k and permute launches. Same outputs, bit for bit. One workgroup ranks at
-  // one token per wavefront here; with more tokens than its wavefronts the separate top-k launch,
-  // which spreads them over the chip, is faster (c2: 3 us saved at 8 tokens, even at 16, 6 us
-  // lost at 32).
-  const int tail_mode = g_route_tail.load(std::memory_order_relaxed);
+  // last router workgroups also rank the tokens (one per wavefront, up to 8 workgroups) and the
+  // last of them sorts the slots by expert (RouteTail), in place of the top-k and permute
+  // launches. Same outputs, bit for bit; 3 us saved per call at c1's shape from 12 to 64 tokens
+  // and at c2's with 8, 12 and 48, level elsewhere.
   const bool route_tail = fuse_gu && !use_flow && !slot_major && !hybrid &&
                           c.n_experts <= kRouteTailMaxExperts && c.top_k <= 64 &&
-                          ((tail_mode == 1 && N < pair_waves(c.hidden)) ||
-                           (tail_mode == 2 && N <= kRouteTailMaxTokens));
+                          N <= kRouteTailMaxTokens && g_route_tail.load(std::memory_order_relaxed) != 0;
 
   // 2. router logits (+ the shared-expert gate logit in column E)
   int ld = 0;
@@ -895,6 +891,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
     if (route_tail) {
       RouteTail T{};
       T.ctr = reinterpret_cast<unsigned long long*>(base + L.route_ctr);
+      T.timeouts = route_tail_timeouts_ptr();
       T.logits = logits; T.ld = ld; T.N = n;
       T.P = topk_params(wts->router_bias, c.n_experts, c.top_k, c.scoring, c.n_group, c.topk_group,
                         c.norm_topk, c.routed_scale, has_sg);

@@ -276,12 +276,14 @@ extern "C" int qmoe_set_decode_flow(int mode) {
   return prev;
 }
 
+// (the decode dataflow launch's waits and the routing tail's)
 extern "C" uint32_t qmoe_flow_timeouts(void) {
   uint32_t v = 0;
   if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(qmoe::g_flow_timeouts), sizeof(v), 0, hipMemcpyDeviceToHost) !=
       hipSuccess)
     return 0xFFFFFFFFu;
-  return v;
+  const uint32_t r = qmoe::route_tail_timeouts();
+  return r == 0xFFFFFFFFu ? r : v + r;
 }
 
 namespace qmoe {

@@ -88,46 +88,71 @@ qmm_route_gate_up_shdown_kernel(QmmArgs a, int n_jobs, SlotRoute route, int gx1,
 // arithmetic of its own launch.
 // NORM: both products RMSNorm their activation rows on the fly (QmmArgs::norm_w), and the first
 // product's job 0 writes the normalised rows (norm_out).
-// The routing tail (RouteTail): this router workgroup's coherent logit stores are complete
-// (s_waitcnt 0, then the workgroup barrier) before it counts itself; the last workgroup to
-// arrive ranks every token, one wavefront per token, with coherent loads of the logits, keeps
-// the ids in LDS, sorts the slots by expert from them and resets the counter.
-__device__ __forceinline__ bool route_tail_arrive(const RouteTail& T) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  __shared__ int s_last;
-  if (threadIdx.x == 0) {
-    constexpr unsigned long long kMask = (1ull << 20) - 1;
-    const unsigned long long old =
-        __hip_atomic_fetch_add(T.ctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long cnt;
-    if ((old >> 20) == kRouteTailTag) {
-      cnt = (old & kMask) + 1;
-    } else {
-      // a word without the tag (a fresh workspace): replace it by a tagged count of 1, or count
-      // on the tagged word another workgroup has put there since; this workgroup's add above
-      // landed on the untagged word and is discarded with it
-      unsigned long long cur = __hip_atomic_load(T.ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      unsigned long long want;
-      do {
-        want = ((cur >> 20) == kRouteTailTag) ? cur + 1 : ((kRouteTailTag << 20) | 1ull);
-      } while (!__hip_atomic_compare_exchange_strong(T.ctr, &cur, want, __ATOMIC_RELAXED,
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      cnt = want & kMask;
-    }
-    s_last = static_cast<int>(cnt) == T.total;
-  }
-  __syncthreads();
-  return s_last != 0;
+// The routing tail (RouteTail). Counts go on tagged workspace words, (kRouteTailTag << 20) |
+// count: an atomic add, and a word found without the tag (a fresh workspace) is replaced by a
+// tagged count of 1 (compare-and-swap), or counted on once another workgroup has tagged it; the
+// add that landed on the untagged word is discarded with it. Returns the count after this one.
+__device__ __forceinline__ int tail_count(unsigned long long* w) {
+  constexpr unsigned long long kMask = (1ull << 20) - 1;
+  const unsigned long long old = __hip_atomic_fetch_add(w, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((old >> 20) == kRouteTailTag) return static_cast<int>((old & kMask) + 1);
+  unsigned long long cur = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned long long want;
+  do {
+    want = ((cur >> 20) == kRouteTailTag) ? cur + 1 : ((kRouteTailTag << 20) | 1ull);
+  } while (!__hip_atomic_compare_exchange_strong(w, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT));
+  return static_cast<int>(want & kMask);
 }
 
+// This workgroup's stores are complete (s_waitcnt 0, then the barrier); thread 0 counts it on
+// *w and the workgroup learns the count.
+__device__ __forceinline__ int tail_arrive(unsigned long long* w) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int s_cnt;
+  if (threadIdx.x == 0) s_cnt = tail_count(w);
+  __syncthreads();
+  return s_cnt;
+}
+
+// Bounded wait of the workgroup until *w holds a tagged count of at least `target`; a wait that
+// runs out adds to *timeouts and returns (the kernel always ends).
+__device__ __forceinline__ void tail_wait(const unsigned long long* w, int target, uint32_t* timeouts) {
+  if (threadIdx.x == 0) {
+    uint32_t n = 0;
+    for (;;) {
+      const unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((v >> 20) == kRouteTailTag && static_cast<int>(v & ((1ull << 20) - 1)) >= target) break;
+      __builtin_amdgcn_s_sleep(2);
+      if (++n >= kWaitLimit) {
+        __hip_atomic_fetch_add(timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Ranker r of R: tokens r, r + R, ... one wavefront each, with coherent loads of the logits; the
+// top-k launch's outputs (idx coherently, read by the last ranker), and the ids into `ids` (LDS)
+// when one workgroup ranks every token.
 template <int VPL>
-__device__ __forceinline__ void route_tail_topk(const RouteTail& T, int32_t* ids) {
+__device__ __forceinline__ void route_tail_rank(const RouteTail& T, int r, int R, int32_t* ids) {
   const int lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
-  for (int t = threadIdx.x >> 6; t < T.N; t += nw) {
-    const int id = topk_store<VPL, true>(T.logits, T.ld, T.P, t, lane, T.idx, T.w, T.sg);
-    if (lane < T.P.k) ids[t * T.P.k + lane] = id;
+  const int k = T.P.k;
+  for (int t = r + R * (threadIdx.x >> 6); t < T.N; t += R * nw) {
+    const float* row = T.logits + static_cast<int64_t>(t) * T.ld;
+    int id;
+    float wsel;
+    topk_token<VPL, false, true>(row, T.P, lane, id, wsel);
+    if (lane < k) {
+      __hip_atomic_store(T.idx + t * k + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      T.w[t * k + lane] = wsel;
+      if (ids) ids[t * k + lane] = id;
+    }
+    if (T.P.has_sg && lane == 0) T.sg[t] = 1.0f / (1.0f + expf(-logit_ld<true>(row + T.P.E)));
   }
 }
 
@@ -224,7 +249,9 @@ __device__ __forceinline__ void route_tail_permute(const RouteTail& T, const int
   }
 }
 
-__device__ __forceinline__ void route_tail_run(const RouteTail& T) {
+// The rankers' part of the tail; the last ranker to finish then sorts the slots by expert and
+// resets the counters.
+__device__ __forceinline__ void route_tail_run(const RouteTail& T, int r, int R) {
   // dynamic LDS: token masks [E] (8 bytes each), histogram [E], offsets [E], scan scratch [34],
   // slot ids [N * k]
   extern __shared__ unsigned long long tail_lds[];
@@ -233,16 +260,25 @@ __device__ __forceinline__ void route_tail_run(const RouteTail& T) {
   int* offs = hist + T.P.E;
   int* tmp = offs + T.P.E;
   int32_t* ids = tmp + 34;
+  int32_t* own = (R == 1) ? ids : nullptr;
   switch (T.vpl) {
-    case 1: route_tail_topk<1>(T, ids); break;
-    case 2: route_tail_topk<2>(T, ids); break;
-    case 4: route_tail_topk<4>(T, ids); break;
-    default: route_tail_topk<8>(T, ids); break;
+    case 1: route_tail_rank<1>(T, r, R, own); break;
+    case 2: route_tail_rank<2>(T, r, R, own); break;
+    case 4: route_tail_rank<4>(T, r, R, own); break;
+    default: route_tail_rank<8>(T, r, R, own); break;
+  }
+  if (R > 1) {
+    if (tail_arrive(T.ctr + 1) != R) return;
+    // the last ranker: every slot's expert, from the rankers' coherent stores
+    for (int m = threadIdx.x; m < T.N * T.P.k; m += blockDim.x)
+      ids[m] = static_cast<int32_t>(__hip_atomic_load(T.idx + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   }
   __syncthreads();
   route_tail_permute(T, ids, mask, hist, offs, tmp);
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
     __hip_atomic_store(T.ctr, kRouteTailTag << 20, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(T.ctr + 1, kRouteTailTag << 20, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 template <int EPI1, int EPI2, int W, int MT, bool NORM = false, int FMT2 = FMT_BF16, bool TAIL = false>
@@ -263,7 +299,13 @@ qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2,
     small_body<FMT_BF16, EPI1, W, 1, 1, MT, NORM, 0, 0, TAIL ? kCohOut : 0>(a1, n_jobs1, blockIdx.x,
                                                                           blockIdx.y, red);
     if constexpr (TAIL) {
-      if (route_tail_arrive(T)) route_tail_run(T);
+      // the last R router workgroups to finish rank the tokens, the first of them once all
+      // router workgroups have stored their logits
+      const int arrival = tail_arrive(T.ctr);
+      if (arrival > T.total - T.rankers) {
+        if (T.rankers > 1) tail_wait(T.ctr, T.total, T.timeouts);
+        route_tail_run(T, T.total - arrival, T.rankers);
+      }
     }
   } else {
     small_body<FMT2, EPI2, W, 1, 1, MT, NORM>(a2, n_jobs2, blockIdx.x - gx1, blockIdx.y, red);
@@ -1436,6 +1478,8 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
   if (TAIL) {
     T.total = gx1 * static_cast<int>(g.y);
     lds = route_tail_lds_bytes(T.P.E, T.N, T.P.k);
+    // rankers: one token per wavefront where the router workgroups allow
+    T.rankers = std::min(std::min((T.N + WAVES - 1) / WAVES, kRouteTailMaxRankers), T.total);
   }
 #define QMOE_PAIR(MT, NORM) \
   qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, MT, NORM, FMT2, TAIL><<<g, 64 * WAVES, lds, stream>>>(a1, n1, gx1, a2, n2, T)
@@ -1484,7 +1528,7 @@ int launch_qmm_pair_route(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stre
   const int mc = tail.N * tail.P.k;
   if (tail.N != a1.dense_rows || tail.N > kRouteTailMaxTokens || tail.P.E <= 0 ||
       tail.P.E > kRouteTailMaxExperts || tail.P.k <= 0 || tail.P.k > 64 || tail.P.k > tail.P.E ||
-      !tail.ctr || tail.logits != a1.out ||
+      !tail.ctr || !tail.timeouts || tail.logits != a1.out ||
       tail.ld != a1.ld_out || !tail.counts || !tail.tile_map || tail.words != (tail.N + 31) / 32 ||
       tail.vpl != topk_vpl(tail.P.E) ||
       tail.max_tiles < mtile_upper_bound(mc, tail.P.E, kSmallMTile))
@@ -1502,6 +1546,20 @@ int launch_qmm_pair_route(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stre
   }
 #undef QMOE_PAIR_T
   return check_launch("qmm pair (routing tail)");
+}
+
+__device__ uint32_t g_route_timeouts;
+
+uint32_t* route_tail_timeouts_ptr() {
+  uint32_t* p = nullptr;
+  return hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(g_route_timeouts)) == hipSuccess ? p : nullptr;
+}
+
+uint32_t route_tail_timeouts() {
+  uint32_t v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_route_timeouts), sizeof(v), 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return 0xFFFFFFFFu;
+  return v;
 }
 
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2) {

@@ -315,8 +315,6 @@ inline int bf16_chunks(int K) {
   const int nks = K / 32;
   return (nks >= 128) ? 16 : (nks >= 64) ? 8 : (nks >= 32) ? 4 : (nks >= 16) ? 2 : 1;
 }
-// wavefronts per workgroup of the router pair launch over K
-inline int pair_waves(int K) { return bf16_chunks(K) > 4 ? bf16_chunks(K) : 4; }
 // One launch of two dense small-regime products over the same rows and K: a1 (tiled bf16) with
 // the fp32 epilogue (router logits), a2 (tiled bf16 or int8, fmt2) with SwiGLU (shared expert
 // gate_up).

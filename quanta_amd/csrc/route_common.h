@@ -280,15 +280,19 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
 
 // The routing tail of the router pair launch, for decode batches routed through the stable
 // permute: the router workgroups store their logits with coherent stores and count their
-// arrival; the last one ranks every token (coherent loads) and runs the permute, in place of the
-// top-k and permute launches. The arrival counter is one 64-bit word in the workspace holding
-// (kRouteTailTag << 20) | count, counted with atomic adds; a workgroup that finds a word without
-// the tag (a fresh workspace) replaces it by a tagged count, so the word needs no clearing, and
-// the last workgroup resets it to a tagged 0 for the next call (or the next replay of a capture).
+// arrival; the last R to arrive rank the tokens (coherent loads of the logits; all but the last
+// arrival first wait, bounded, for the count to complete), and the last ranker to finish runs
+// the permute, in place of the top-k and permute launches. Each counter is a 64-bit workspace
+// word holding (kRouteTailTag << 20) | count, counted with atomic adds; a workgroup that finds a
+// word without the tag (a fresh workspace) replaces it by a tagged count, so the words need no
+// clearing, and the last ranker resets both to a tagged 0 for the next call (or the next replay
+// of a capture).
 constexpr unsigned long long kRouteTailTag = 0xA5C3E1F7B9Dull;   // 44 bits
 struct RouteTail {
-  unsigned long long* ctr;
+  unsigned long long* ctr;    // two words: router workgroups arrived, rankers done
+  uint32_t* timeouts;         // waits that ran out of their bound
   int total;                  // router workgroups of the launch
+  int rankers;                // the last `rankers` arrivals rank the tokens (the launcher's choice)
   const float* logits;
   int ld;
   TopkParams P;
@@ -306,7 +310,9 @@ struct RouteTail {
   int words;                  // token bitmap words per expert, (N + 31) / 32
   int vpl;                    // experts per lane of the top-k wavefront (topk_vpl)
 };
-constexpr int kRouteTailMaxTokens = 64, kRouteTailMaxExperts = 512;
+constexpr int kRouteTailMaxTokens = 64, kRouteTailMaxExperts = 512, kRouteTailMaxRankers = 8;
+uint32_t* route_tail_timeouts_ptr();   // device address of the tail's timeout counter
+uint32_t route_tail_timeouts();        // its value (synchronous)
 // dynamic LDS of the tail: a 64-bit token mask, a count and an offset per expert, scan scratch
 // and the ids of the N * k slots
 inline size_t route_tail_lds_bytes(int E, int N, int k) {
