@@ -143,8 +143,9 @@ typedef struct {
   const void* router_w;           /* see router_format */
   const float* router_bias;       /* [E] e_score_correction_bias (selection only) or NULL */
   const float* shared_gate_w;     /* [H] fp32, only with QMOE_ROUTER_F32 */
-  const uint32_t* gu_codes;       /* routed gate|up [E, 2I, H]: tiled int4 codes or tiled bf16 */
-  const uint16_t* gu_sb;          /* tiled scale/bias (int4 only) */
+  const uint32_t* gu_codes;       /* routed gate|up [E, 2I, H]: tiled int3/int4/int6 codes
+                                     (qmoe_tile_int3/int4/int6) or tiled bf16 */
+  const uint16_t* gu_sb;          /* tiled scale/bias (quantized formats only) */
   const uint32_t* dn_codes;       /* routed down [E, H, I] */
   const uint16_t* dn_sb;
   const uint16_t* sh_gu;          /* shared gate|up [2*Is, H]: tiled bf16, or tiled int8 codes
