@@ -20,6 +20,7 @@ namespace qmoe {
 constexpr int kPermThreads = 1024;
 constexpr int kPermLdsWords = 12 * 1024;   // 48 KiB of bitmap + prefix words per workgroup
 
+template <int RES>
 __global__ void __launch_bounds__(kPermThreads) permute_kernel(
     const int32_t* __restrict__ idx, int N, int k, int E, int m_tile, int experts_per_wg,
     int words_per_expert, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -31,12 +32,13 @@ __global__ void __launch_bounds__(kPermThreads) permute_kernel(
   __shared__ int scan_tmp[40];
   __shared__ uint32_t bits[kPermLdsWords / 2];
   __shared__ uint32_t pref[kPermLdsWords / 2];
+  __shared__ int toffs[1025], btoffs[1025];
   const int e0 = blockIdx.x * experts_per_wg;
   const int e1 = min(E, e0 + experts_per_wg);
-  const PermuteLds S{hist, offs, scan_tmp, bits, pref};
-  permute_body(idx, N, k, E, m_tile, e0, e1, words_per_expert, blockIdx.x == 0, S, counts,
-               offsets, tile_off, sorted_slot, inv, tile_map, max_tiles, split_rows, m_tile_big,
-               tile_map_big, max_tiles_big);
+  const PermuteLds S{hist, offs, scan_tmp, bits, pref, toffs, btoffs};
+  permute_body<RES>(idx, N, k, E, m_tile, e0, e1, words_per_expert, blockIdx.x == 0, S, counts,
+                    offsets, tile_off, sorted_slot, inv, tile_map, max_tiles, split_rows,
+                    m_tile_big, tile_map_big, max_tiles_big);
 }
 
 int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t* counts,
@@ -53,10 +55,17 @@ int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t*
   if (tile_map_big && (!tile_map || m_tile_big <= 0 ||
                        max_tiles_big < mtile_upper_bound(static_cast<int64_t>(N) * k, E, m_tile_big)))
     return fail("permute: split tile maps need both maps sized to their m-tile bounds");
-  permute_kernel<<<n_wg, kPermThreads, 0, stream>>>(
-      idx, N, k, E, m_tile, per_wg, words, counts, offsets, tile_off, sorted_slot, inv,
-      reinterpret_cast<int4*>(tile_map), static_cast<int>(max_tiles), split_rows, m_tile_big,
-      reinterpret_cast<int4*>(tile_map_big), static_cast<int>(max_tiles_big));
+  // (the slot list resident in registers up to 48 ids per thread; longer lists in batches)
+  const int64_t mc = static_cast<int64_t>(N) * k;
+#define QMOE_PERM(RES)                                                                            \
+  permute_kernel<RES><<<n_wg, kPermThreads, 0, stream>>>(                                         \
+      idx, N, k, E, m_tile, per_wg, words, counts, offsets, tile_off, sorted_slot, inv,           \
+      reinterpret_cast<int4*>(tile_map), static_cast<int>(max_tiles), split_rows, m_tile_big,    \
+      reinterpret_cast<int4*>(tile_map_big), static_cast<int>(max_tiles_big))
+  if (mc <= 8 * kPermThreads) QMOE_PERM(8);
+  else if (mc <= 48 * kPermThreads) QMOE_PERM(48);
+  else QMOE_PERM(0);
+#undef QMOE_PERM
   return check_launch("permute");
 }
 

@@ -376,6 +376,8 @@ struct PermuteLds {
   int* scan_tmp;    // [40]
   uint32_t* bits;   // [(e1 - e0) * words_per_expert]
   uint32_t* pref;   // same size
+  int* toffs;       // [1025] m-tile prefix per expert (the first workgroup's tile map)
+  int* btoffs;      // [1025] the big-tile map's prefix (hybrid split)
 };
 
 // Exclusive scan across a 1024-thread workgroup (16 wavefronts of 64).
@@ -406,9 +408,27 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* 
 
 constexpr int kPermBatch = 8;   // expert ids loaded per thread before they are used
 
+// Tile t's entry of a tile map whose expert m-tile prefix is toffs[0..E] (toffs[E] = tiles):
+// the expert e with toffs[e] <= t < toffs[e + 1] (binary search; experts without tiles repeat
+// the prefix and are never found), its i-th tile {e, first sorted position, rows, 0}.
+__device__ __forceinline__ int4 tile_entry(const int* toffs, const int* offs, const int* hist, int E,
+                                           int t, int m_tile) {
+  int lo = 0, hi = E;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (toffs[mid] <= t) lo = mid; else hi = mid;
+  }
+  const int i = t - toffs[lo];
+  return make_int4(lo, offs[lo] + i * m_tile, min(m_tile, hist[lo] - i * m_tile), 0);
+}
+
 // Optional split tile maps (hybrid regime): experts with more than `split_rows` rows get
 // m-tiles of `m_tile_big` rows in tile_map_big; the others keep m_tile-row tiles in tile_map.
+// RES > 0: every expert id is loaded once (RES per thread, all in flight together) and kept in
+// registers for the scatter (lists of up to RES * 1024 slots); RES = 0: batches of kPermBatch,
+// loaded again for the scatter.
 // Must be called by all 1024 threads of the workgroup.
+template <int RES>
 __device__ __forceinline__ void permute_body(
     const int32_t* idx, int N, int k, int E, int m_tile, int e0, int e1, int words_per_expert,
     bool is_first, const PermuteLds& S, int32_t* __restrict__ counts,
@@ -430,23 +450,41 @@ __device__ __forceinline__ void permute_body(
   for (int i = tid; i < nbits; i += nthr) bits[i] = 0u;
   __syncthreads();
 
-  // (the expert ids are read kPermBatch per thread before any is used, so a long list costs
-  // one global-load latency per batch rather than one per entry)
-  for (int mb = tid; mb < mc; mb += kPermBatch * nthr) {
-    int ev[kPermBatch];
+  auto count_slot = [&](int m, int e) __attribute__((always_inline)) {
+    if (e < 0 || e >= E) return;
+    atomicAdd(&hist[e], 1);
+    if (e >= e0 && e < e1) {
+      const int t = m / k;
+      atomicOr(&bits[(e - e0) * words_per_expert + (t >> 5)], 1u << (t & 31));
+    }
+  };
+  int evr[RES > 0 ? RES : 1];   // RES: slot tid + j * nthr's expert (-1 past the list)
+  if constexpr (RES > 0) {
 #pragma unroll
-    for (int j = 0; j < kPermBatch; ++j) {
-      const int m = mb + j * nthr;
-      ev[j] = (m < mc) ? idx[m] : -1;
+    for (int j = 0; j < RES; ++j) {
+      const int m = tid + j * nthr;
+      const int v = idx[min(m, mc - 1)];
+      evr[j] = (m < mc) ? v : -1;
     }
 #pragma unroll
-    for (int j = 0; j < kPermBatch; ++j) {
-      const int e = ev[j];
-      if (e < 0 || e >= E) continue;
-      atomicAdd(&hist[e], 1);
-      if (e >= e0 && e < e1) {
-        const int t = (mb + j * nthr) / k;
-        atomicOr(&bits[(e - e0) * words_per_expert + (t >> 5)], 1u << (t & 31));
+    for (int j = 0; j < RES; ++j) {
+      const int m = tid + j * nthr;
+      if (m < mc) count_slot(m, evr[j]);
+    }
+  } else {
+    // (the expert ids are read kPermBatch per thread before any is used, so a long list costs
+    // one global-load latency per batch rather than one per entry)
+    for (int mb = tid; mb < mc; mb += kPermBatch * nthr) {
+      int ev[kPermBatch];
+#pragma unroll
+      for (int j = 0; j < kPermBatch; ++j) {
+        const int m = mb + j * nthr;
+        ev[j] = (m < mc) ? idx[m] : -1;
+      }
+#pragma unroll
+      for (int j = 0; j < kPermBatch; ++j) {
+        const int m = mb + j * nthr;
+        if (m < mc) count_slot(m, ev[j]);
       }
     }
   }
@@ -485,24 +523,31 @@ __device__ __forceinline__ void permute_body(
     }
     // Per-tile descriptors {expert, first sorted position, rows, 0} for the grouped-qmm grid,
     // and a -1 sentinel in every unused entry up to max_tiles, so a workgroup resolves its tile
-    // with one 16-byte load.
+    // with one 16-byte load. One thread per tile (a hot expert's hundreds of tiles would
+    // otherwise be one thread's serial stores), its expert found in the tile prefix in LDS.
     if (tile_map && !tile_map_big) {
-      if (tid < E)
-        for (int i = 0; i < tiles; ++i)
-          tile_map[tex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
-      for (int t = scan_tmp[38] + tid; t < max_tiles; t += nthr) tile_map[t] = make_int4(-1, 0, 0, 0);
+      const int nt = scan_tmp[38];
+      if (tid < E) S.toffs[tid] = tex;
+      if (tid == 0) S.toffs[E] = nt;
+      __syncthreads();
+      for (int t = tid; t < max_tiles; t += nthr)
+        tile_map[t] = (t < nt) ? tile_entry(S.toffs, offs, hist, E, t, m_tile) : make_int4(-1, 0, 0, 0);
     }
     if (tile_map_big) {
       if (tid < E) {
-        for (int i = 0; i < s_tiles; ++i)
-          tile_map[s_ex + i] = make_int4(tid, ex + i * m_tile, min(m_tile, c - i * m_tile), 0);
-        for (int i = 0; i < b_tiles; ++i)
-          tile_map_big[b_ex + i] =
-              make_int4(tid, ex + i * m_tile_big, min(m_tile_big, c - i * m_tile_big), 0);
+        S.toffs[tid] = s_ex;
+        S.btoffs[tid] = b_ex;
       }
-      for (int t = s_total + tid; t < max_tiles; t += nthr) tile_map[t] = make_int4(-1, 0, 0, 0);
-      for (int t = b_total + tid; t < max_tiles_big; t += nthr)
-        tile_map_big[t] = make_int4(-1, 0, 0, 0);
+      if (tid == 0) {
+        S.toffs[E] = s_total;
+        S.btoffs[E] = b_total;
+      }
+      __syncthreads();
+      for (int t = tid; t < max_tiles; t += nthr)
+        tile_map[t] = (t < s_total) ? tile_entry(S.toffs, offs, hist, E, t, m_tile) : make_int4(-1, 0, 0, 0);
+      for (int t = tid; t < max_tiles_big; t += nthr)
+        tile_map_big[t] =
+            (t < b_total) ? tile_entry(S.btoffs, offs, hist, E, t, m_tile_big) : make_int4(-1, 0, 0, 0);
     }
   }
 
@@ -550,29 +595,38 @@ __device__ __forceinline__ void permute_body(
     for (int p = offs[e0] + tid; p < offs[e1]; p += nthr) sorted_slot[p] = -1;
   __syncthreads();
 
-  for (int mb = tid; mb < mc; mb += kPermBatch * nthr) {
-    int ev[kPermBatch];
-#pragma unroll
-    for (int j = 0; j < kPermBatch; ++j) {
-      const int m = mb + j * nthr;
-      ev[j] = (m < mc) ? idx[m] : E;
+  auto place_slot = [&](int m, int e) __attribute__((always_inline)) {
+    if (e < 0 || e >= E) {
+      if (is_first) inv[m] = -1;
+      return;
     }
+    if (e < e0 || e >= e1) return;
+    const int t = m / k;
+    const int wi = (e - e0) * words_per_expert + (t >> 5);
+    const uint32_t below = bits[wi] & ((1u << (t & 31)) - 1u);
+    const int pos = offs[e] + static_cast<int>(pref[wi]) + __popc(below);
+    sorted_slot[pos] = m;
+    inv[m] = pos;
+  };
+  if constexpr (RES > 0) {
 #pragma unroll
-    for (int j = 0; j < kPermBatch; ++j) {
-      const int m = mb + j * nthr;
-      if (m >= mc) break;
-      const int e = ev[j];
-      if (e < 0 || e >= E) {
-        if (is_first) inv[m] = -1;
-        continue;
+    for (int j = 0; j < RES; ++j) {
+      const int m = tid + j * nthr;
+      if (m < mc) place_slot(m, evr[j]);
+    }
+  } else {
+    for (int mb = tid; mb < mc; mb += kPermBatch * nthr) {
+      int ev[kPermBatch];
+#pragma unroll
+      for (int j = 0; j < kPermBatch; ++j) {
+        const int m = mb + j * nthr;
+        ev[j] = (m < mc) ? idx[m] : E;
       }
-      if (e < e0 || e >= e1) continue;
-      const int t = m / k;
-      const int wi = (e - e0) * words_per_expert + (t >> 5);
-      const uint32_t below = bits[wi] & ((1u << (t & 31)) - 1u);
-      const int pos = offs[e] + static_cast<int>(pref[wi]) + __popc(below);
-      sorted_slot[pos] = m;
-      inv[m] = pos;
+#pragma unroll
+      for (int j = 0; j < kPermBatch; ++j) {
+        const int m = mb + j * nthr;
+        if (m < mc) place_slot(m, ev[j]);
+      }
     }
   }
 }
