@@ -82,12 +82,6 @@ qmm_route_gate_up_shdown_kernel(QmmArgs a, int n_jobs, SlotRoute route, int gx1,
   }
 }
 
-// Two dense products over the same activation rows in one launch (the router logits, tiled
-// bf16, and the shared expert's gate_up, tiled bf16 or int8 as FMT2): job blocks [0, gx1) run
-// the first, the rest the second. Both use the same K, so the same chunking W, and each keeps the
-// arithmetic of its own launch.
-// NORM: both products RMSNorm their activation rows on the fly (QmmArgs::norm_w), and the first
-// product's job 0 writes the normalised rows (norm_out).
 // The routing tail (RouteTail). Counts go on tagged workspace words, (kRouteTailTag << 20) |
 // count: an atomic add, and a word found without the tag (a fresh workspace) is replaced by a
 // tagged count of 1 (compare-and-swap), or counted on once another workgroup has tagged it; the
@@ -281,6 +275,13 @@ __device__ __forceinline__ void route_tail_run(const RouteTail& T, int r, int R)
   }
 }
 
+// Two dense products over the same activation rows in one launch (the router logits, tiled
+// bf16, and the shared expert's gate_up, tiled bf16 or int8 as FMT2): job blocks [0, gx1) run
+// the first, the rest the second. Both use the same K, so the same chunking W, and each keeps the
+// arithmetic of its own launch.
+// NORM: both products RMSNorm their activation rows on the fly (QmmArgs::norm_w), and the first
+// product's job 0 writes the normalised rows (norm_out).
+// TAIL: the routing tail (RouteTail) after the router workgroups' products.
 template <int EPI1, int EPI2, int W, int MT, bool NORM = false, int FMT2 = FMT_BF16, bool TAIL = false>
 __global__ void __launch_bounds__(W > 4 ? 64 * W : 256)
 qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2, RouteTail T) {
