@@ -418,7 +418,8 @@ static WsLayout ws_layout(const qmoe_config_t& c, int64_t N) {
   L.inv = take(static_cast<size_t>(mc) * 4);
   L.h = take(static_cast<size_t>(mc) * c.inter * 2);
   L.d = take(static_cast<size_t>(mc) * c.hidden * 2);
-  L.sh_h = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.shared_inter : 0) * 2);
+  // (the shared expert's SwiGLU output, or with the decode dataflow launch its [gate | up] rows)
+  L.sh_h = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? 2 * c.shared_inter : 0) * 2);
   L.sh_out = take(static_cast<size_t>(N) * (c.shared_inter > 0 ? c.hidden : 0) * 2);
   // int8 shared expert above the decode sizes: its weights expanded to tiled bf16 for the
   // large-M kernel (gate|up [2 Is, H] then down [H, Is])
@@ -839,7 +840,9 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
   // gathers), when that launch pair has a compiled shape
   bool sdn_in_gate_up = false;
   const bool shared_down_late = shared && !fuse_dn && hybrid && aux && sstream == aux->s;
-  if (shared && !fuse_dn && !shared_down_late) {
+  // (a shared gate_up in the router pair launch: its down product follows that launch)
+  const bool shared_down_after_router = shared && !fuse_dn && !shared_down_late && fuse_gu;
+  if (shared && !fuse_dn && !shared_down_late && !fuse_gu) {
     rc = shared_down();
     if (rc) return rc;
   }
@@ -902,12 +905,20 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
       T.vpl = topk_vpl(c.n_experts);
       rc = launch_qmm_pair_route(a, sgu, stream, sfmt, T);
     } else if (fuse_gu) {
-      rc = launch_qmm_pair_bf16(a, sgu, stream, sfmt);
+      // (where the dataflow launch forms the shared expert's gated activation itself, the pair
+      // launch writes its gate and up halves, each tile a job of its own)
+      const bool split = use_flow && decode_flow_split_shared(c.hidden, c.inter, c.shared_inter);
+      if (split) sgu.ld_out = 2 * c.shared_inter;
+      rc = launch_qmm_pair_bf16(a, sgu, stream, sfmt, split);
     } else {
       rc = launch_qmm(a, FMT_BF16, EPI_F32, sreg, (N + rt - 1) / rt, stream);
     }
   }
   if (rc) return rc;
+  if (shared_down_after_router) {
+    rc = shared_down();
+    if (rc) return rc;
+  }
   if (use_flow) {
     FlowLaunch F{};
     F.x = x; F.N = n; F.k = c.top_k; F.H = c.hidden; F.I = c.inter; F.Is = c.shared_inter;

@@ -20,7 +20,8 @@ struct FlowLaunch {
   const uint16_t* dn_sb;
   int glu;                    // gated activation (QMOE_ACT_*)
   float glu_alpha, glu_limit;
-  const uint16_t* sh_h;       // [N][Is] shared expert's SwiGLU output (the router launch's)
+  const uint16_t* sh_h;       // [N][Is] shared expert's SwiGLU output, or [N][2 Is] its gate | up
+                              // rows (decode_flow_split_shared), from the router launch
   const void* sh_dn;          // shared down [H][Is], tiled bf16 or int8 (sfmt)
   const uint16_t* sh_dn_sb;
   int sfmt;
@@ -37,6 +38,8 @@ struct FlowLaunch {
 // Whether the compiled kernel covers this shape (a slot-major batch of up to 16 tokens, c1- or
 // c2-like chunking).
 bool decode_flow_fits(int N, int k, int E, int H, int I, int Is);
+// Whether its shared-down units read the router launch's split [gate | up] rows (sh_h 2 Is wide).
+bool decode_flow_split_shared(int H, int I, int Is);
 int64_t decode_flow_sync_words(int64_t mc, int H);
 bool decode_flow_enabled(int N);   // the process-wide mode's choice for an N-token call
 int launch_decode_flow(const FlowLaunch& L, hipStream_t stream);

@@ -139,7 +139,9 @@ template <int A, int B> struct CMax { static constexpr int v = A > B ? A : B; };
 // VPL: experts per lane of the top-k. G: routed gate_up (GW wavefronts per job, one tile pair
 // each, 8 superblocks per chunk staged deep); D: routed down (DW wavefronts per job, DJPW tiles
 // each, 4 superblocks per chunk); S: shared down (SW chunks, weights SFMT).
-template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT>
+// SGLU: the shared down reads the router launch's [gate | up] rows and forms the gated activation
+// itself (decode_flow_split_shared).
+template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT, bool SGLU>
 __global__ void __launch_bounds__(256) decode_flow_kernel(FlowArgs a) {
   constexpr int RG = SmallCfg<FMT_INT4, EPI_SWIGLU, GW, 1, 1, 1>::RED;
   constexpr int RD = SmallCfg<FMT_INT4, EPI_BF16, DW, 1, DJPW, 1>::RED;
@@ -207,7 +209,7 @@ __global__ void __launch_bounds__(256) decode_flow_kernel(FlowArgs a) {
   // ---- S: shared expert down projection
   if (b < a.nS) {
     const int tm = b / a.gx_s, bx = b - tm * a.gx_s;
-    small_body<SFMT, EPI_BF16, SW, 1, 1, 1, false, 0, 0, kCohOut>(a.s, a.n_sjobs, bx, tm, red);
+    small_body<SFMT, EPI_BF16, SW, 1, 1, 1, false, 0, 0, kCohOut | (SGLU ? kGluAct : 0)>(a.s, a.n_sjobs, bx, tm, red);
     const int fb = (bx * (4 / SW)) / a.fb_tiles;
     if (flow_arrive(cnt + fb * kSyncStride, &bcast)) flow_combine(a, fb);
     return;
@@ -298,16 +300,28 @@ bool decode_flow_enabled(int N) {
   return g_flow_mode == 2 || (g_flow_mode == 1 && N <= kFlowAutoTokens);
 }
 
-template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT>
+template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT, bool SGLU>
 static void flow_go(const FlowArgs& a, hipStream_t stream) {
   const int64_t grid = static_cast<int64_t>(a.nT) + a.nG + a.nS + a.nD;
-  decode_flow_kernel<VPL, GW, DW, DJPW, SW, SFMT><<<dim3(static_cast<unsigned>(grid)), 256, 0, stream>>>(a);
+  decode_flow_kernel<VPL, GW, DW, DJPW, SW, SFMT, SGLU><<<dim3(static_cast<unsigned>(grid)), 256, 0, stream>>>(a);
 }
 
 template <int VPL, int SFMT>
 static void flow_dispatch_shape(const FlowArgs& a, const FlowShape& f, hipStream_t stream) {
-  if (f.gw == 4) flow_go<VPL, 4, 2, 4, 4, SFMT>(a, stream);   // c2-like
-  else flow_go<VPL, 2, 1, 4, 2, SFMT>(a, stream);             // c1-like
+  if (f.gw == 4) flow_go<VPL, 4, 2, 4, 4, SFMT, false>(a, stream);   // c2-like
+  else flow_go<VPL, 2, 1, 4, 2, SFMT, true>(a, stream);              // c1-like
+}
+
+// Whether the dataflow launch for this shape takes the shared expert's [gate | up] rows (the
+// router launch then runs the shared gate_up's tiles as separate jobs, launch_qmm_pair_bf16
+// split) and forms the gated activation in its shared-down units. Measured on MI355X: c1's shape
+// 21.9 -> 20.3 us at one token, 25.7 -> 23.9 at two (the router launch ends with its router
+// workgroups instead of the shared gate_up's); c2's 33.0 -> 38.2 and 49.3 -> 58.7, where the 256
+// shared-down workgroups per m-tile, each forming the activation of the whole row, hold the
+// units the down products need.
+bool decode_flow_split_shared(int H, int I, int Is) {
+  const FlowShape f = flow_shape(1, 1, 256, H, I, Is);
+  return f.ok && f.gw != 4;
 }
 
 int launch_decode_flow(const FlowLaunch& L, hipStream_t stream) {
@@ -344,10 +358,12 @@ int launch_decode_flow(const FlowLaunch& L, hipStream_t stream) {
   d.act_ready = L.sync + kSyncStride;
   d.timeouts = timeouts;
   a.dout = L.d;
-  // shared down -> sh_out
+  // shared down -> sh_out, from the router launch's [gate | up] rows of the shared expert (the
+  // gated activation formed as the fragments are loaded)
   QmmArgs& s = a.s;
   s.act = L.sh_h; s.act_rows = L.N; s.slot_div = 1; s.dense_rows = L.N; s.n_experts = 1;
   s.K = L.Is; s.n_rows = L.H; s.codes = L.sh_dn; s.sb = L.sh_dn_sb; s.out = L.sh_out; s.ld_out = L.H;
+  s.glu = L.glu; s.glu_alpha = L.glu_alpha; s.glu_limit = L.glu_limit;
   a.sh_out = L.sh_out;
   // units
   a.n_gjobs = L.I / 16;

@@ -1466,12 +1466,17 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
   return check_launch("qmm(route)");
 }
 
-template <int W, int FMT2, bool TAIL = false>
+// SPLIT: the second product's gate and up tiles as jobs of their own with the bf16 epilogue, the
+// [gate | up] rows for a consumer that forms the gated activation (kGluAct): twice the
+// workgroups, each with one tile's dequant, for the launches whose time this product sets.
+template <int W, int FMT2, bool TAIL = false, bool SPLIT = false>
 static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream,
                           RouteTail T = RouteTail{}) {
   constexpr int WAVES = W > 4 ? W : 4;
   constexpr int JPWG = WAVES / W;
-  const int n1 = a1.n_rows / 16, n2 = a2.n_rows / 32;   // fp32 epilogue jobs, SwiGLU jobs
+  constexpr int EPI2 = SPLIT ? EPI_BF16 : EPI_SWIGLU;
+  // fp32 epilogue jobs; SwiGLU jobs (a gate and an up tile) or, split, single tiles
+  const int n1 = a1.n_rows / 16, n2 = a2.n_rows / (SPLIT ? 16 : 32);
   const int gx1 = (n1 + JPWG - 1) / JPWG, gx2 = (n2 + JPWG - 1) / JPWG;
   const bool mt2 = mtiles >= kSmallMt2MinTiles;   // two m-tiles per wavefront, as in launch_small_k
   const dim3 g(gx1 + gx2, static_cast<unsigned>(mt2 ? (mtiles + 1) / 2 : mtiles));
@@ -1483,7 +1488,7 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
     T.rankers = std::min(std::min((T.N + WAVES - 1) / WAVES, kRouteTailMaxRankers), T.total);
   }
 #define QMOE_PAIR(MT, NORM) \
-  qmm_small_pair_kernel<EPI_F32, EPI_SWIGLU, W, MT, NORM, FMT2, TAIL><<<g, 64 * WAVES, lds, stream>>>(a1, n1, gx1, a2, n2, T)
+  qmm_small_pair_kernel<EPI_F32, EPI2, W, MT, NORM, FMT2, TAIL><<<g, 64 * WAVES, lds, stream>>>(a1, n1, gx1, a2, n2, T)
   if (a1.norm_w) {
     if (mt2) QMOE_PAIR(2, true); else QMOE_PAIR(1, true);
   } else {
@@ -1492,14 +1497,14 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
 #undef QMOE_PAIR
 }
 
-template <int FMT2>
+template <int FMT2, bool SPLIT>
 static void launch_pair_f(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream) {
   switch (bf16_chunks(a1.K)) {
-    case 16: launch_pair_w<16, FMT2>(a1, a2, mtiles, stream); break;
-    case 8: launch_pair_w<8, FMT2>(a1, a2, mtiles, stream); break;
-    case 4: launch_pair_w<4, FMT2>(a1, a2, mtiles, stream); break;
-    case 2: launch_pair_w<2, FMT2>(a1, a2, mtiles, stream); break;
-    default: launch_pair_w<1, FMT2>(a1, a2, mtiles, stream); break;
+    case 16: launch_pair_w<16, FMT2, false, SPLIT>(a1, a2, mtiles, stream); break;
+    case 8: launch_pair_w<8, FMT2, false, SPLIT>(a1, a2, mtiles, stream); break;
+    case 4: launch_pair_w<4, FMT2, false, SPLIT>(a1, a2, mtiles, stream); break;
+    case 2: launch_pair_w<2, FMT2, false, SPLIT>(a1, a2, mtiles, stream); break;
+    default: launch_pair_w<1, FMT2, false, SPLIT>(a1, a2, mtiles, stream); break;
   }
 }
 
@@ -1563,7 +1568,7 @@ uint32_t route_tail_timeouts() {
   return v;
 }
 
-int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2) {
+int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream, int fmt2, bool split) {
   if (a1.offsets || a2.offsets || a1.dense_rows != a2.dense_rows || a1.K != a2.K || a1.K % 32 ||
       a1.n_rows % 16 || a2.n_rows % 32 || a1.dense_rows <= 0)
     return fail("qmm pair: two dense products over the same rows and K required");
@@ -1575,10 +1580,14 @@ int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t strea
     return fail("qmm pair: the fused norm needs one job per workgroup and one load batch per chunk");
   const int64_t mtiles = (a1.dense_rows + kSmallMTile - 1) / kSmallMTile;
   if (mtiles > 65535) return fail("qmm pair: too many m-tiles for one launch");
-  if (fmt2 == FMT_INT8)
-    launch_pair_f<FMT_INT8>(a1, a2, mtiles, stream);
-  else
-    launch_pair_f<FMT_BF16>(a1, a2, mtiles, stream);
+  if (split && a2.ld_out < a2.n_rows) return fail("qmm pair: split gate_up rows hold both halves");
+  if (fmt2 == FMT_INT8) {
+    if (split) launch_pair_f<FMT_INT8, true>(a1, a2, mtiles, stream);
+    else launch_pair_f<FMT_INT8, false>(a1, a2, mtiles, stream);
+  } else {
+    if (split) launch_pair_f<FMT_BF16, true>(a1, a2, mtiles, stream);
+    else launch_pair_f<FMT_BF16, false>(a1, a2, mtiles, stream);
+  }
   return check_launch("qmm pair");
 }
 

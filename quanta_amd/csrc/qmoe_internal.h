@@ -317,9 +317,10 @@ inline int bf16_chunks(int K) {
 }
 // One launch of two dense small-regime products over the same rows and K: a1 (tiled bf16) with
 // the fp32 epilogue (router logits), a2 (tiled bf16 or int8, fmt2) with SwiGLU (shared expert
-// gate_up).
+// gate_up), or with `split` the gate and up halves as bf16 [gate | up] rows (a2.ld_out >= its
+// rows) for a consumer that forms the gated activation itself (small_body's kGluAct).
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream,
-                         int fmt2 = FMT_BF16);
+                         int fmt2 = FMT_BF16, bool split = false);
 // Whether the pair launch over `rows` rows of K normalises them itself (QmmArgs::norm_w): one
 // job per workgroup (K >= 1024), and each wavefront's K chunk one load batch (8 32-wide steps
 // with one m-tile per wavefront, 4 with two), or up to 16 steps for one or two rows.

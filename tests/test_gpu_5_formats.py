@@ -87,6 +87,16 @@ def _check(p, cfg, x, what, *, act="silu", alpha=1.702, limit=0.0, gs=64, bits=4
     return y, it
 
 
+@pytest.mark.parametrize("N", [1, 2, 8, 40])
+def test_block_wide_shared_expert_vs_oracle(gpu, N):
+    """A shared expert wider than the fused decode down takes (4096 features: 16 chunks of K,
+    as Qwen2-MoE's 20480-wide one): its gate_up still rides in the router launch, and its down
+    product must run after that launch, on the rows it wrote."""
+    cfg = MoEConfig(512, 8, 2, 256, 4096)
+    p = _layer(gpu, 64, seed=70 + N, Is=4096)
+    _check(p, cfg, _inputs(gpu, N, 512, N), f"shared expert 4096 wide N={N}")
+
+
 @pytest.mark.parametrize("N", [1, 5, 40, 300])
 def test_block_group128_vs_oracle(gpu, N):
     """128-column groups through every regime (slot-major, decode, hybrid prefill)."""
