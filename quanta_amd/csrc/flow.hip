@@ -61,7 +61,8 @@ struct FlowArgs {
   int H;
   uint32_t* sync;        // counters kSyncStride words apart, zero at launch: T units done,
                          // then per slot its G units done, then per feature block its arrivals
-  int nT, nG, nS, nD;    // units of each kind, in that order in the grid
+  int nH, nT, nG, nS, nD;  // units of each kind, in that order in the grid
+  int Is;                // the shared expert's width (H unit: [gate | up] rows of 2 Is)
   int gx_g, gx_d, gx_s;  // job blocks (workgroups) per slot (G, D) or token m-tile (S)
   int n_gjobs, n_djobs, n_sjobs;
   int fb_tiles;          // 16-feature output tiles per feature block (one D workgroup's)
@@ -139,9 +140,11 @@ template <int A, int B> struct CMax { static constexpr int v = A > B ? A : B; };
 // VPL: experts per lane of the top-k. G: routed gate_up (GW wavefronts per job, one tile pair
 // each, 8 superblocks per chunk staged deep); D: routed down (DW wavefronts per job, DJPW tiles
 // each, 4 superblocks per chunk); S: shared down (SW chunks, weights SFMT).
-// SGLU: the shared down reads the router launch's [gate | up] rows and forms the gated activation
-// itself (decode_flow_split_shared).
-template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT, bool SGLU>
+// The router launch writes the shared expert's gate_up as [gate | up] rows (split: each tile a
+// job of its own, so that launch ends with its router workgroups); one H unit forms the gated
+// activation once, in place of the gate half (coherent stores, the SwiGLU epilogue's arithmetic
+// on the same bf16 values), and the shared-down units wait for it.
+template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT>
 __global__ void __launch_bounds__(256) decode_flow_kernel(FlowArgs a) {
   constexpr int RG = SmallCfg<FMT_INT4, EPI_SWIGLU, GW, 1, 1, 1>::RED;
   constexpr int RD = SmallCfg<FMT_INT4, EPI_BF16, DW, 1, DJPW, 1>::RED;
@@ -159,6 +162,27 @@ __global__ void __launch_bounds__(256) decode_flow_kernel(FlowArgs a) {
   route.mc = a.mc;
   route.store = 0;
   int b = blockIdx.x;
+  uint32_t* const hdone = a.sync + (1 + a.mc + a.H / 16) * kSyncStride;
+
+  // ---- H: the shared expert's gated activation, once per row element
+  if (b < a.nH) {
+    const int per = a.Is / 8;   // 16-byte groups of a half row
+    for (int v = threadIdx.x; v < a.N * per; v += 256) {
+      const int t = v / per, j = v - t * per;
+      u32x4* row = reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.s.act) + static_cast<int64_t>(t) * 2 * a.Is);
+      const u32x4 g = row[j], up = row[j + per];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        coh_st32(reinterpret_cast<uint32_t*>(row + j) + q,
+                 pack_bf16x2_rne(glu_f(bf16lo_to_f32(g[q]), bf16lo_to_f32(up[q]), a.s.glu, a.s.glu_alpha, a.s.glu_limit),
+                                 glu_f(bf16hi_to_f32(g[q]), bf16hi_to_f32(up[q]), a.s.glu, a.s.glu_alpha, a.s.glu_limit)));
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(hdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  b -= a.nH;
 
   // ---- T: each slot's routing weight and each token's shared gate, for the combine
   if (b < a.nT) {
@@ -209,7 +233,7 @@ __global__ void __launch_bounds__(256) decode_flow_kernel(FlowArgs a) {
   // ---- S: shared expert down projection
   if (b < a.nS) {
     const int tm = b / a.gx_s, bx = b - tm * a.gx_s;
-    small_body<SFMT, EPI_BF16, SW, 1, 1, 1, false, 0, 0, kCohOut | (SGLU ? kGluAct : 0)>(a.s, a.n_sjobs, bx, tm, red);
+    small_body<SFMT, EPI_BF16, SW, 1, 1, 1, false, 0, 0, kCohOut | kCohAct | kCohWaitAct>(a.s, a.n_sjobs, bx, tm, red);
     const int fb = (bx * (4 / SW)) / a.fb_tiles;
     if (flow_arrive(cnt + fb * kSyncStride, &bcast)) flow_combine(a, fb);
     return;
@@ -266,8 +290,9 @@ bool decode_flow_fits(int N, int k, int E, int H, int I, int Is) {
   return flow_shape(N, k, E, H, I, Is).ok;
 }
 
-// sync words the kernel needs for mc slots (cleared by the launch before it)
-int64_t decode_flow_sync_words(int64_t mc, int H) { return (1 + mc + H / 16) * kSyncStride; }
+// sync words the kernel needs for mc slots (cleared by the launch before it): the T count, a
+// count per slot, per feature block, and the H unit's
+int64_t decode_flow_sync_words(int64_t mc, int H) { return (2 + mc + H / 16) * kSyncStride; }
 
 static int g_flow_mode = 1;
 }  // namespace qmoe
@@ -300,29 +325,25 @@ bool decode_flow_enabled(int N) {
   return g_flow_mode == 2 || (g_flow_mode == 1 && N <= kFlowAutoTokens);
 }
 
-template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT, bool SGLU>
+template <int VPL, int GW, int DW, int DJPW, int SW, int SFMT>
 static void flow_go(const FlowArgs& a, hipStream_t stream) {
-  const int64_t grid = static_cast<int64_t>(a.nT) + a.nG + a.nS + a.nD;
-  decode_flow_kernel<VPL, GW, DW, DJPW, SW, SFMT, SGLU><<<dim3(static_cast<unsigned>(grid)), 256, 0, stream>>>(a);
+  const int64_t grid = static_cast<int64_t>(a.nH) + a.nT + a.nG + a.nS + a.nD;
+  decode_flow_kernel<VPL, GW, DW, DJPW, SW, SFMT><<<dim3(static_cast<unsigned>(grid)), 256, 0, stream>>>(a);
 }
 
 template <int VPL, int SFMT>
 static void flow_dispatch_shape(const FlowArgs& a, const FlowShape& f, hipStream_t stream) {
-  if (f.gw == 4) flow_go<VPL, 4, 2, 4, 4, SFMT, false>(a, stream);   // c2-like
-  else flow_go<VPL, 2, 1, 4, 2, SFMT, true>(a, stream);              // c1-like
+  if (f.gw == 4) flow_go<VPL, 4, 2, 4, 4, SFMT>(a, stream);   // c2-like
+  else flow_go<VPL, 2, 1, 4, 2, SFMT>(a, stream);             // c1-like
 }
 
 // Whether the dataflow launch for this shape takes the shared expert's [gate | up] rows (the
 // router launch then runs the shared gate_up's tiles as separate jobs, launch_qmm_pair_bf16
-// split) and forms the gated activation in its shared-down units. Measured on MI355X: c1's shape
-// 21.9 -> 20.3 us at one token, 25.7 -> 23.9 at two (the router launch ends with its router
-// workgroups instead of the shared gate_up's); c2's 33.0 -> 38.2 and 49.3 -> 58.7, where the 256
-// shared-down workgroups per m-tile, each forming the activation of the whole row, hold the
-// units the down products need.
-bool decode_flow_split_shared(int H, int I, int Is) {
-  const FlowShape f = flow_shape(1, 1, 256, H, I, Is);
-  return f.ok && f.gw != 4;
-}
+// split): every compiled shape does. Measured on MI355X (300-step loops, µs, SwiGLU rows ->
+// split with the H unit): c2 one token 33.0 -> 32.4, two 49.3 -> 46.2; c1 21.9 -> 20.5 and
+// 25.7 -> 24.1. (Forming the activation in every shared-down unit instead, 256 per m-tile at
+// c2, each for the whole row: c2 38.2 and 58.7.)
+bool decode_flow_split_shared(int H, int I, int Is) { return flow_shape(1, 1, 256, H, I, Is).ok; }
 
 int launch_decode_flow(const FlowLaunch& L, hipStream_t stream) {
   const FlowShape f = flow_shape(L.N, L.k, L.P.E, L.H, L.I, L.Is);
@@ -364,6 +385,13 @@ int launch_decode_flow(const FlowLaunch& L, hipStream_t stream) {
   s.act = L.sh_h; s.act_rows = L.N; s.slot_div = 1; s.dense_rows = L.N; s.n_experts = 1;
   s.K = L.Is; s.n_rows = L.H; s.codes = L.sh_dn; s.sb = L.sh_dn_sb; s.out = L.sh_out; s.ld_out = L.H;
   s.glu = L.glu; s.glu_alpha = L.glu_alpha; s.glu_limit = L.glu_limit;
+  a.Is = L.Is;
+  a.nH = 1;
+  // the H unit's rows: [h | up], h in place of the gate half, complete once it counts
+  s.act_stride = 2 * L.Is;
+  s.act_ready = L.sync + (1 + L.N * L.k + L.H / 16) * kSyncStride;
+  s.act_ready_target = 1;
+  s.timeouts = timeouts;
   a.sh_out = L.sh_out;
   // units
   a.n_gjobs = L.I / 16;

@@ -1467,8 +1467,9 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
 }
 
 // SPLIT: the second product's gate and up tiles as jobs of their own with the bf16 epilogue, the
-// [gate | up] rows for a consumer that forms the gated activation (kGluAct): twice the
-// workgroups, each with one tile's dequant, for the launches whose time this product sets.
+// [gate | up] rows for a consumer that forms the gated activation (the decode dataflow launch's
+// H unit): twice the workgroups, each with one tile's dequant, for the launches whose time this
+// product sets.
 template <int W, int FMT2, bool TAIL = false, bool SPLIT = false>
 static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, hipStream_t stream,
                           RouteTail T = RouteTail{}) {

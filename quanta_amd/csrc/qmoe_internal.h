@@ -197,7 +197,7 @@ int launch_permute(const int32_t* idx, int N, int k, int E, int m_tile, int32_t*
                    int m_tile_big = 0, int32_t* tile_map_big = nullptr, int64_t max_tiles_big = 0);
 
 struct QmmArgs {
-  const uint16_t* act;        // activation rows (bf16), row stride K
+  const uint16_t* act;        // activation rows (bf16), row stride K (or act_stride)
   int64_t act_rows;           // number of activation rows (bounds check)
   const int32_t* slot_of;     // sorted position -> slot id (nullable: identity)
   int slot_div;               // activation row = slot / slot_div
@@ -244,6 +244,7 @@ struct QmmArgs {
   uint32_t* timeouts;         // where a bounded wait that ran out is counted
   uint32_t* zero_words;       // dense pair launch, nullable: n_zero counters (kSyncStride words
   int n_zero;                 // apart) its first workgroup clears for the dataflow kernel after it
+  int act_stride;             // elements from one activation row to the next (0: K)
 };
 
 enum { FMT_INT4 = 0, FMT_BF16 = 1, FMT_INT6 = 2, FMT_INT3 = 3, FMT_INT8 = 4 };
@@ -318,7 +319,7 @@ inline int bf16_chunks(int K) {
 // One launch of two dense small-regime products over the same rows and K: a1 (tiled bf16) with
 // the fp32 epilogue (router logits), a2 (tiled bf16 or int8, fmt2) with SwiGLU (shared expert
 // gate_up), or with `split` the gate and up halves as bf16 [gate | up] rows (a2.ld_out >= its
-// rows) for a consumer that forms the gated activation itself (small_body's kGluAct).
+// rows) for a consumer that forms the gated activation itself (the decode dataflow launch).
 int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t stream,
                          int fmt2 = FMT_BF16, bool split = false);
 // Whether the pair launch over `rows` rows of K normalises them itself (QmmArgs::norm_w): one

@@ -67,15 +67,11 @@ __device__ __forceinline__ void coh_st32(void* p, uint32_t v) {
 // small_body's handoff modes (template COH, a bit set): the activation rows are read coherently
 // (kCohAct); outputs are stored coherently (kCohOut). With RVPL routing: kCohRowSlot: the
 // activation row is the slot (m-tile `by`) itself, not its token (the down projection of a slot's
-// h row); kCohWaitAct (DEEP staging only): every weight load of the chunk is issued first, then
-// the workgroup waits until QmmArgs::act_ready[by * kSyncStride] reaches act_ready_target (the rows' producers
-// have finished) before it loads the activations; thread 0 polls for the whole workgroup, so
-// every wavefront of the workgroup must hold a job.
+// h row); kCohWaitAct: the workgroup waits until QmmArgs::act_ready[by * kSyncStride] reaches
+// act_ready_target (the rows' producers have finished) before it loads the activations; thread 0
+// polls for the whole workgroup. With DEEP staging every weight load of the chunk is issued first
+// and every wavefront of the workgroup must hold a job; with dense weights the wait comes first.
 constexpr int kCohAct = 2, kCohOut = 4, kCohRowSlot = 16, kCohWaitAct = 32;
-// kGluAct (dense weights, not a handoff mode): the activation rows are [gate | up] pairs of K
-// bf16 each (row stride 2K, the pair launch's split shared gate_up), and every fragment is the
-// gated activation bf16(glu(gate, up)), the SwiGLU epilogue's arithmetic on the same bf16 values.
-constexpr int kGluAct = 64;
 
 
 // One lane of the wavefront polls *p until it reaches target, sleeping longer the longer it
@@ -208,8 +204,6 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
     if constexpr ((COH & kCohAct) != 0) return coh_ld128(p); else return *p;
   };
   static_assert(MT == 1 || fmt_dense(FMT), "several m-tiles per wavefront: dense weights only");
-  static_assert((COH & kGluAct) == 0 || (fmt_dense(FMT) && !NORM && RVPL == 0),
-                "the gated activation rows: dense weights, no fused norm, no routing");
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
   constexpr int NT = C::NT;
   constexpr int CH = C::CH;
@@ -292,10 +286,16 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
     if (RVPL > 0) arow = (mrow == 0 && route_tok < a.act_rows) ? route_tok : -1;
     else if (mrow < mtc[u]) arow = act_row(a, mt0[u] + mrow);
     const bool row_ok = arow >= 0;
-    xrows[u] = act + (row_ok ? arow : 0) * static_cast<int64_t>((COH & kGluAct) ? 2 * a.K : a.K);
+    xrows[u] = act + (row_ok ? arow : 0) * static_cast<int64_t>(a.act_stride ? a.act_stride : a.K);
     rows_okm[u] = static_cast<uint32_t>(__ballot(row_ok)) & 0xFFFFu;   // lanes 0-15
   }
   const uint16_t* xrow = xrows[0];
+  if constexpr ((COH & kCohWaitAct) != 0 && !fmt_quant(FMT)) {
+    // dense weights: the whole workgroup waits for the activation rows' producers first
+    if (threadIdx.x == 0)
+      poll_geq(a.act_ready + static_cast<int64_t>(by) * kSyncStride, a.act_ready_target, a.timeouts);
+    __syncthreads();
+  }
 
   f32x4_t accm[MT][NT];
 #pragma unroll
@@ -516,33 +516,17 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       const u32x4* xp[MT];
 #pragma unroll
       for (int u = 0; u < MT; ++u) xp[u] = reinterpret_cast<const u32x4*>(xrows[u]) + lg;   // 8 lg bf16
-      // kGluAct: the up fragments beside the gate fragments (their gated activation is formed
-      // right before the MFMAs, so the batch's loads stay in flight together)
-      constexpr bool GLU = (COH & kGluAct) != 0;
-      constexpr int BU = GLU ? ((MT > 1) ? 4 : 8) : 1;
-      auto glu_frag = [&](const u32x4& g, const u32x4& up) __attribute__((always_inline)) -> u32x4 {
-        u32x4 h;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          h[q] = pack_bf16x2_rne(glu_f(bf16lo_to_f32(g[q]), bf16lo_to_f32(up[q]), a.glu, a.glu_alpha, a.glu_limit),
-                                 glu_f(bf16hi_to_f32(g[q]), bf16hi_to_f32(up[q]), a.glu, a.glu_alpha, a.glu_limit));
-        return h;
-      };
       // Batches of steps: all loads of a batch issue before its MFMAs (indices clamped into
       // the range, so no load is conditional); the MFMAs run in step order.
       constexpr int BS = (MT > 1) ? 4 : 8;
-      auto load_batch = [&](int cb, Frag (&wv)[BS][NT], u32x4 (&xv)[BS][MT], u32x4 (&xu)[BU][MT])
-          __attribute__((always_inline)) {
+      auto load_batch = [&](int cb, Frag (&wv)[BS][NT], u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           const int c = min(cb + i, k1 - 1);
 #pragma unroll
           for (int t = 0; t < NT; ++t) wv[i][t] = wt[t].load(c);
 #pragma unroll
-          for (int u = 0; u < MT; ++u) {
-            xv[i][u] = xp[u][c * 4];
-            if constexpr (GLU) xu[i][u] = xp[u][c * 4 + a.K / 8];
-          }
+          for (int u = 0; u < MT; ++u) xv[i][u] = ldx(xp[u] + c * 4);
         }
       };
       // RMSNorm on the fly (NORM, the pair launch; the launcher guarantees W >= 4, so the
@@ -554,22 +538,15 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       float rn[MT];
       u32x4* outp[MT];
       const u32x4* wnp = NORM ? reinterpret_cast<const u32x4*>(a.norm_w) + lg : nullptr;
-      auto mma_batch = [&](int cb, const Frag (&wv)[BS][NT], const u32x4 (&xv)[BS][MT],
-                           const u32x4 (&xu)[BU][MT]) __attribute__((always_inline)) {
+      auto mma_batch = [&](int cb, const Frag (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
           if (cb + i < k1) {
-            u32x4 xa[MT];
-#pragma unroll
-            for (int u = 0; u < MT; ++u) {
-              if constexpr (GLU) xa[u] = glu_frag(xv[i][u], xu[i][u]);
-              else xa[u] = xv[i][u];
-            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
               const bf16x8_t B = as_bf16x8(dense_bf16<FMT>(wv[i][t]));
 #pragma unroll
-              for (int u = 0; u < MT; ++u) accm[u][t] = mfma16(as_bf16x8(xa[u]), B, accm[u][t]);
+              for (int u = 0; u < MT; ++u) accm[u][t] = mfma16(as_bf16x8(xv[i][u]), B, accm[u][t]);
             }
           }
         }
@@ -681,12 +658,11 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       for (; cb < k1; cb += BS) {
         Frag wv[BS][NT];
         u32x4 xv[BS][MT];
-        u32x4 xu[BU][MT];
-        load_batch(cb, wv, xv, xu);
+        load_batch(cb, wv, xv);
         if constexpr (NORM)
           norm_mma_batch(cb, wv, xv);
         else
-          mma_batch(cb, wv, xv, xu);
+          mma_batch(cb, wv, xv);
       }
     }
   }
