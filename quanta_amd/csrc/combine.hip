@@ -855,7 +855,7 @@ static int forward_impl(const qmoe_config_t* cfg, const qmoe_weights_t* wts, con
                         decode_flow_fits(n, c.top_k, c.n_experts, c.hidden, c.inter, c.shared_inter);
   uint32_t* sync = reinterpret_cast<uint32_t*>(base + L.sync);
   // Decode batches routed through the permute, with the router in the pair launch: that launch's
-  // last router workgroups also rank the tokens (one per wavefront, up to 8 workgroups) and the
+  // last router workgroups also rank the tokens (one per workgroup, up to 32 workgroups) and the
   // last of them sorts the slots by expert (RouteTail), in place of the top-k and permute
   // launches. Same outputs, bit for bit; 3 us saved per call at c1's shape from 12 to 64 tokens
   // and at c2's with 8, 12 and 48, level elsewhere.

@@ -1485,9 +1485,14 @@ static void launch_pair_w(const QmmArgs& a1, const QmmArgs& a2, int64_t mtiles, 
   if (TAIL) {
     T.total = gx1 * static_cast<int>(g.y);
     lds = route_tail_lds_bytes(T.P.E, T.N, T.P.k);
-    // rankers: one token per wavefront where the router workgroups allow
-    T.rankers = std::min(std::min((T.N + WAVES - 1) / WAVES, kRouteTailMaxRankers), T.total);
+    // rankers: one token per workgroup (its first wavefront), up to kRouteTailMaxRankers and
+    // the router workgroups; c2 at 32 tokens: 294.1 us per layer against 299.5 with one token
+    // per wavefront of two rankers (16 wavefronts ranking on one compute unit take about four
+    // times as long as one)
+    T.rankers = std::min(std::min(T.N, kRouteTailMaxRankers), T.total);
   }
+  // (NORM: the norm weights in the same dynamic LDS, used before the tail's)
+  if (a1.norm_w) lds = std::max(lds, static_cast<size_t>(a1.K) * 2);
 #define QMOE_PAIR(MT, NORM) \
   qmm_small_pair_kernel<EPI_F32, EPI2, W, MT, NORM, FMT2, TAIL><<<g, 64 * WAVES, lds, stream>>>(a1, n1, gx1, a2, n2, T)
   if (a1.norm_w) {

@@ -310,7 +310,7 @@ struct RouteTail {
   int words;                  // token bitmap words per expert, (N + 31) / 32
   int vpl;                    // experts per lane of the top-k wavefront (topk_vpl)
 };
-constexpr int kRouteTailMaxTokens = 64, kRouteTailMaxExperts = 512, kRouteTailMaxRankers = 8;
+constexpr int kRouteTailMaxTokens = 64, kRouteTailMaxExperts = 512, kRouteTailMaxRankers = 32;
 uint32_t* route_tail_timeouts_ptr();   // device address of the tail's timeout counter
 uint32_t route_tail_timeouts();        // its value (synchronous)
 // dynamic LDS of the tail: a 64-bit token mask, a count and an offset per expert, scan scratch

@@ -535,9 +535,13 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       // chunk's steps in order, then (g0 + g1) + (g2 + g3), then the chunks in order), taken while
       // the first batch's weights are already in flight; each activation fragment is then
       // normalised, bf16(w * (x * r)), and job 0 writes the normalised rows for later launches.
+      // The norm weights come to LDS (the launch's dynamic LDS, a.K * 2 bytes; the workgroup's
+      // threads load one 16-byte piece each, issued before the activations, so the sums' wait
+      // covers them) and are read from there after the barrier.
       float rn[MT];
       u32x4* outp[MT];
-      const u32x4* wnp = NORM ? reinterpret_cast<const u32x4*>(a.norm_w) + lg : nullptr;
+      extern __shared__ u32x4 norm_g[];
+      const u32x4* wnp = norm_g + lg;
       auto mma_batch = [&](int cb, const Frag (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
@@ -590,6 +594,10 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
         float ssl[MT];
 #pragma unroll
         for (int u = 0; u < MT; ++u) ssl[u] = 0.f;
+        // (pair_norm_fusable bounds a.K / 8 by the workgroup's threads)
+        const bool g_mine = static_cast<int>(threadIdx.x) < a.K / 8;
+        u32x4 g_piece{};
+        if (g_mine) g_piece = reinterpret_cast<const u32x4*>(a.norm_w)[threadIdx.x];
         Frag wv[BS][NT];
         u32x4 xv[BS][MT];
         const bool one_batch = k1 - k0 <= BS;
@@ -632,6 +640,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
               for (int u = 0; u < MT; ++u) ssl[u] = sq(ssl[u], xs[i][u]);
             }
         }
+        if (g_mine) norm_g[threadIdx.x] = g_piece;
         float* nred = reinterpret_cast<float*>(red + SmallCfg<FMT, EPI, W, CPW, JPW, MT>::RED);
 #pragma unroll
         for (int u = 0; u < MT; ++u) {

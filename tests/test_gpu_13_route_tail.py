@@ -3,12 +3,13 @@
 Decode batches sorted by expert (above the slot-major sizes) with a bf16 router and a shared
 expert run the router logits and the shared gate_up in one launch; its last router workgroups to
 finish can also rank the tokens (the top-k launch's arithmetic, on coherent loads of the logits;
-one workgroup, or up to 8 sharing the tokens once the count is complete) and the last of them
+one token per workgroup, up to 32 workgroups, once the count is complete) and the last of them
 sorts the slots by expert (the permute launch's outputs). The block's output must equal the
 separate launches' (qmoe_set_route_tail(0)) bit for bit at both BASELINE decode shapes, from
-one ranking workgroup to eight, on repeated calls (the arrival counter resets itself), with the residual add (the RMSNorm fused into the same
-launch), through the allocation-free entry and over a workspace whose bytes start as garbage (the
-counter needs no clearing).
+7 ranking workgroups to 32 (two tokens each at 64), on repeated calls (the arrival counter resets
+itself), with the residual add (the RMSNorm fused into the same launch), through the
+allocation-free entry and over a workspace whose bytes start as garbage (the counter needs no
+clearing).
 """
 
 from __future__ import annotations
