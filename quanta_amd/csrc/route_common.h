@@ -228,42 +228,108 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ row, const 
   uint32_t key[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) key[i] = orderable(ch[i] + 0.0f);
-  // remaining candidates of this lane (bit i = expert e_base + i) and the lane's best of them
+  // remaining candidates of this lane (bit i = expert e_base + i)
   uint32_t avail = 0u;
 #pragma unroll
   for (int i = 0; i < VPL; ++i)
     if (e_base + i < E) avail |= 1u << i;
-  uint32_t hk = 0u;
-  float hs = 0.f;
-  int hi = -1;
-  auto head = [&]() __attribute__((always_inline)) {
-    hk = 0u;
-    hi = -1;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const bool take = ((avail >> i) & 1u) & (key[i] > hk);
-      hk = take ? key[i] : hk;
-      hs = take ? sc[i] : hs;
-      hi = take ? i : hi;
-    }
-  };
-  head();
-
   int my_id = 0;
   float my_w = 0.f;
   const int n_rounds = (IDS_ONLY && rounds > 0) ? min(rounds, P.k) : P.k;
-  for (int r = 0; r < n_rounds; ++r) {
-    const uint32_t m = wave_max_u32(hk);
-    unsigned long long win = __ballot((hi >= 0) & (hk == m));
-    win = win ? win : __ballot(hi >= 0);   // the fallback is unreachable while k <= E
-    const int owner = static_cast<int>(__builtin_ctzll(win));
-    const int id = __builtin_amdgcn_readlane(e_base + hi, owner);
-    const float s_win = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
-    // the owner drops its winner and recomputes its best remaining candidate
-    avail = (lane == owner) ? (avail & ~(1u << (hi & 31))) : avail;
+  // Two forms of the same selection. Rescan: a round's owner rescans its remaining candidates
+  // after the wavefront reduction. Two heads: each lane also holds its next best candidate,
+  // recomputed at the start of every round beside the reduction, and the owner promotes it.
+  // Same choices in the same order; measured per use (300-step loops, same box): the two-head
+  // form is faster with four or fewer experts per lane and in the routing tail's rankers (c2
+  // 8-32 tokens and c1 1-8 tokens by 0.4-0.7 us per call), the rescan form in the dataflow
+  // launch's units with eight (c2 one token, 0.6 us).
+  constexpr bool kTwoHead = COH || VPL <= 4;
+  if constexpr (kTwoHead) {
+    // Best candidate of a mask: a pairwise tree in index order where the right operand wins
+    // only with a strictly larger key, so equal keys keep the lowest index; key 0 = none.
+    auto best = [&](uint32_t mask, uint32_t& bk, int& bi, float& bs) __attribute__((always_inline)) {
+      uint32_t tk[VPL];
+      int ti[VPL];
+      float ts[VPL];
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        tk[i] = ((mask >> i) & 1u) ? key[i] : 0u;
+        ti[i] = i;
+        ts[i] = sc[i];
+      }
+      auto pick = [&](int i, int j) __attribute__((always_inline)) {
+        const bool tb = tk[j] > tk[i];
+        tk[i] = tb ? tk[j] : tk[i];
+        ti[i] = tb ? ti[j] : ti[i];
+        ts[i] = tb ? ts[j] : ts[i];
+      };
+      // (one loop per level, each with a constant stride, so every index is static)
+#pragma unroll
+      for (int i = 0; i + 1 < VPL; i += 2) pick(i, i + 1);
+#pragma unroll
+      for (int i = 0; i + 2 < VPL; i += 4) pick(i, i + 2);
+#pragma unroll
+      for (int i = 0; i + 4 < VPL; i += 8) pick(i, i + 4);
+#pragma unroll
+      for (int i = 0; i + 8 < VPL; i += 16) pick(i, i + 8);
+      static_assert(VPL <= 16, "experts per lane");
+      bk = tk[0];
+      bi = ti[0];
+      bs = ts[0];
+    };
+    uint32_t hk;
+    float hs;
+    int hi;
+    best(avail, hk, hi, hs);
+    for (int r = 0; r < n_rounds; ++r) {
+      uint32_t k2;
+      float s2;
+      int i2;
+      best(avail & ~(1u << (hi & 31)), k2, i2, s2);
+      const uint32_t m = wave_max_u32(hk);
+      unsigned long long win = __ballot((hk > 0u) & (hk == m));
+      win = win ? win : __ballot(hk > 0u);   // the fallback is unreachable while k <= E
+      const int owner = static_cast<int>(__builtin_ctzll(win));
+      const int id = __builtin_amdgcn_readlane(e_base + hi, owner);
+      const float s_win = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
+      // the owner drops its winner and takes its next candidate
+      const bool own = lane == owner;
+      avail = own ? (avail & ~(1u << (hi & 31))) : avail;
+      hk = own ? k2 : hk;
+      hi = own ? i2 : hi;
+      hs = own ? s2 : hs;
+      my_id = (lane == r) ? id : my_id;
+      my_w = (lane == r) ? s_win : my_w;
+    }
+  } else {
+    uint32_t hk = 0u;
+    float hs = 0.f;
+    int hi = -1;
+    auto head = [&]() __attribute__((always_inline)) {
+      hk = 0u;
+      hi = -1;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const bool take = ((avail >> i) & 1u) & (key[i] > hk);
+        hk = take ? key[i] : hk;
+        hs = take ? sc[i] : hs;
+        hi = take ? i : hi;
+      }
+    };
     head();
-    my_id = (lane == r) ? id : my_id;
-    my_w = (lane == r) ? s_win : my_w;
+    for (int r = 0; r < n_rounds; ++r) {
+      const uint32_t m = wave_max_u32(hk);
+      unsigned long long win = __ballot((hi >= 0) & (hk == m));
+      win = win ? win : __ballot(hi >= 0);   // the fallback is unreachable while k <= E
+      const int owner = static_cast<int>(__builtin_ctzll(win));
+      const int id = __builtin_amdgcn_readlane(e_base + hi, owner);
+      const float s_win = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
+      // the owner drops its winner and recomputes its best remaining candidate
+      avail = (lane == owner) ? (avail & ~(1u << (hi & 31))) : avail;
+      head();
+      my_id = (lane == r) ? id : my_id;
+      my_w = (lane == r) ? s_win : my_w;
+    }
   }
   if (IDS_ONLY) {
     out_id = my_id;
