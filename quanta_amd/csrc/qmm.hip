@@ -138,6 +138,8 @@ __device__ __forceinline__ void route_tail_rank(const RouteTail& T, int r, int R
   const int k = T.P.k;
   for (int t = r + R * (threadIdx.x >> 6); t < T.N; t += R * nw) {
     const float* row = T.logits + static_cast<int64_t>(t) * T.ld;
+    // (the shared gate's logit is loaded before the ranking, so its latency overlaps it)
+    const float sgl = (T.P.has_sg && lane == 0) ? logit_ld<true>(row + T.P.E) : 0.f;
     int id;
     float wsel;
     topk_token<VPL, false, true>(row, T.P, lane, id, wsel);
@@ -146,7 +148,7 @@ __device__ __forceinline__ void route_tail_rank(const RouteTail& T, int r, int R
       T.w[t * k + lane] = wsel;
       if (ids) ids[t * k + lane] = id;
     }
-    if (T.P.has_sg && lane == 0) T.sg[t] = 1.0f / (1.0f + expf(-logit_ld<true>(row + T.P.E)));
+    if (T.P.has_sg && lane == 0) T.sg[t] = 1.0f / (1.0f + expf(-sgl));
   }
 }
 
