@@ -57,17 +57,18 @@ qmm_route_gate_up_kernel(QmmArgs a, int n_jobs, SlotRoute route) {
                                                                     red, &route, xlds, &route_e);
 }
 
-// The same with the shared expert's int8 down projection (a2: W2 chunks, one m-tile per
-// wavefront) in the launch, on a flat grid of 4-wavefront workgroups: the routed gate_up's job
-// blocks x slots first, then the shared down's job blocks x m-tiles.
-template <int W, int JPW, int VPL, int DEEP, int W2>
+// The same with the shared expert's int8 down projection (a2: W2 * CPW2 chunks, W2 wavefronts
+// per job each summing CPW2 of them, one m-tile per wavefront) in the launch, on a flat grid of
+// 4-wavefront workgroups: the routed gate_up's job blocks x slots first, then the shared down's
+// job blocks x m-tiles.
+template <int W, int JPW, int VPL, int DEEP, int W2, int CPW2 = 1>
 __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW>::WPE)))
 qmm_route_gate_up_shdown_kernel(QmmArgs a, int n_jobs, SlotRoute route, int gx1, int64_t n1,
                                 QmmArgs a2, int n_jobs2, int gx2) {
   static_assert(W <= 4 && W2 <= 4, "one 4-wavefront workgroup shape for both products");
   constexpr int R1 = SmallCfg<FMT_INT4, EPI_SWIGLU, W, 1, JPW, 1>::RED;
-  constexpr int R2 = SmallCfg<FMT_INT8, EPI_BF16, W2, 1, 1, 1>::RED;
+  constexpr int R2 = SmallCfg<FMT_INT8, EPI_BF16, W2, CPW2, 1, 1>::RED;
   __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
   __shared__ u32x4 xlds[DEEP > 0 ? 4 * DEEP * 16 : 1];
   __shared__ int route_e;
@@ -77,8 +78,8 @@ qmm_route_gate_up_shdown_kernel(QmmArgs a, int n_jobs, SlotRoute route, int gx1,
         a, n_jobs, static_cast<int>(b % gx1), static_cast<int>(b / gx1), red, &route, xlds, &route_e);
   } else {
     const int64_t b2 = b - n1;
-    small_body<FMT_INT8, EPI_BF16, W2, 1, 1, 1>(a2, n_jobs2, static_cast<int>(b2 % gx2),
-                                                static_cast<int>(b2 / gx2), red);
+    small_body<FMT_INT8, EPI_BF16, W2, CPW2, 1, 1>(a2, n_jobs2, static_cast<int>(b2 % gx2),
+                                                   static_cast<int>(b2 / gx2), red);
   }
 }
 
@@ -317,16 +318,17 @@ qmm_small_pair_kernel(QmmArgs a1, int n_jobs1, int gx1, QmmArgs a2, int n_jobs2,
 
 // The routed gate_up (int4 SwiGLU over the permuted m-tiles, small-regime shape W/CPW/JPW) and
 // the shared expert's down projection (int8 codes, K = its intermediate size, one dense segment
-// of N rows; W2 chunks, MT2 m-tiles per wavefront) in one launch of 4-wavefront workgroups on a
-// flat grid: the gate_up's job blocks x m-tiles first, the shared down's after them. Each keeps
-// the arithmetic of its own launch, so the outputs are those of the two launches bit for bit.
-template <int W, int CPW, int JPW, int W2, int MT2>
+// of N rows; W2 * CPW2 chunks, W2 wavefronts per job each summing CPW2 of them, MT2 m-tiles per
+// wavefront) in one launch of 4-wavefront workgroups on a flat grid: the gate_up's job blocks x
+// m-tiles first, the shared down's after them. Each keeps the arithmetic of its own launch, so
+// the outputs are those of the two launches bit for bit.
+template <int W, int CPW, int JPW, int W2, int MT2, int CPW2 = 1>
 __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(SmallCfg<FMT_INT4, EPI_SWIGLU, W, CPW, JPW>::WPE)))
 qmm_gate_up_shdown_kernel(QmmArgs a1, int n_jobs1, int gx1, int64_t n1, QmmArgs a2, int n_jobs2,
                           int gx2) {
   constexpr int R1 = SmallCfg<FMT_INT4, EPI_SWIGLU, W, CPW, JPW, 1>::RED;
-  constexpr int R2 = SmallCfg<FMT_INT8, EPI_BF16, W2, 1, 1, MT2>::RED;
+  constexpr int R2 = SmallCfg<FMT_INT8, EPI_BF16, W2, CPW2, 1, MT2>::RED;
   __shared__ f32x4_t red[R1 > R2 ? R1 : R2];
   const int64_t b = blockIdx.x;
   if (b < n1) {
@@ -334,8 +336,8 @@ qmm_gate_up_shdown_kernel(QmmArgs a1, int n_jobs1, int gx1, int64_t n1, QmmArgs 
                                                      static_cast<int>(b / gx1), red);
   } else {
     const int64_t b2 = b - n1;
-    small_body<FMT_INT8, EPI_BF16, W2, 1, 1, MT2>(a2, n_jobs2, static_cast<int>(b2 % gx2),
-                                                  static_cast<int>(b2 / gx2), red);
+    small_body<FMT_INT8, EPI_BF16, W2, CPW2, 1, MT2>(a2, n_jobs2, static_cast<int>(b2 % gx2),
+                                                     static_cast<int>(b2 / gx2), red);
   }
 }
 
@@ -1390,20 +1392,22 @@ static void launch_route_k(const QmmArgs& a, int64_t mc, const SlotRoute& R, hip
   if (sdn) {   // (the caller checked w2 and the m-tile count)
     const int gx1 = (n_jobs + jobs_per_wg - 1) / jobs_per_wg;
     const int64_t n1 = static_cast<int64_t>(gx1) * mc;
-    const int n_jobs2 = sdn->n_rows / 16, gx2 = (n_jobs2 + 4 / w2 - 1) / (4 / w2);
+    // (eight chunks: four wavefronts of two per job)
+    const int wv2 = (w2 == 8) ? 4 : w2;
+    const int n_jobs2 = sdn->n_rows / 16, gx2 = (n_jobs2 + 4 / wv2 - 1) / (4 / wv2);
     const int64_t n2 = static_cast<int64_t>(gx2) * ((sdn->dense_rows + kSmallMTile - 1) / kSmallMTile);
     const dim3 g(static_cast<unsigned>(n1 + n2));
-#define QMOE_RSD(D, W2_)                                                                      \
-  qmm_route_gate_up_shdown_kernel<W, 1, VPL, D, W2_><<<g, 256, 0, stream>>>(a, n_jobs, R, gx1, n1, \
-                                                                          *sdn, n_jobs2, gx2)
+#define QMOE_RSD(D, W2_, CPW2_)                                                                  \
+  qmm_route_gate_up_shdown_kernel<W, 1, VPL, D, W2_, CPW2_><<<g, 256, 0, stream>>>(a, n_jobs, R, gx1, n1, \
+                                                                                 *sdn, n_jobs2, gx2)
     // (one chunk per job, W = 1, means fewer than 8 superblocks: never the deep form)
     if constexpr (W > 1) {
       if (a.K / 128 == 8 * W) {
-        if (w2 == 4) QMOE_RSD(8, 4); else QMOE_RSD(8, 2);
+        if (w2 == 8) QMOE_RSD(8, 4, 2); else if (w2 == 4) QMOE_RSD(8, 4, 1); else QMOE_RSD(8, 2, 1);
         return;
       }
     }
-    if (w2 == 4) QMOE_RSD(0, 4); else QMOE_RSD(0, 2);
+    if (w2 == 8) QMOE_RSD(0, 4, 2); else if (w2 == 4) QMOE_RSD(0, 4, 1); else QMOE_RSD(0, 2, 1);
 #undef QMOE_RSD
     return;
   }
@@ -1459,7 +1463,8 @@ int launch_route_gate_up(const QmmArgs& a, int N, const float* logits, int ld, c
       return fail("qmm(route): the shared down is one dense int8 segment");
     w2 = bf16_chunks(sdn->K);
     // one m-tile per wavefront below kSmallMt2MinTiles m-tiles, as its own launch would run it
-    if ((w2 != 2 && w2 != 4) || (sdn->dense_rows + kSmallMTile - 1) / kSmallMTile >= kSmallMt2MinTiles)
+    if ((w2 != 2 && w2 != 4 && w2 != 8) ||
+        (sdn->dense_rows + kSmallMTile - 1) / kSmallMTile >= kSmallMt2MinTiles)
       return 1;   // no compiled combination: the caller launches the shared down apart
   }
   if (ch == 4) launch_route_w<4>(a, mc, R, vpl, stream, sdn, w2);
@@ -1599,7 +1604,7 @@ int launch_qmm_pair_bf16(const QmmArgs& a1, const QmmArgs& a2, hipStream_t strea
   return check_launch("qmm pair");
 }
 
-template <int W, int CPW, int JPW, int W2, int MT2>
+template <int W, int CPW, int JPW, int W2, int MT2, int CPW2 = 1>
 static int launch_gsd(const QmmArgs& a1, int64_t mtiles1, const QmmArgs& a2, int64_t mtiles2,
                       hipStream_t stream) {
   static_assert(W <= 4 && W2 <= 4, "one 4-wavefront workgroup shape for both products");
@@ -1608,7 +1613,7 @@ static int launch_gsd(const QmmArgs& a1, int64_t mtiles1, const QmmArgs& a2, int
   const int64_t n1 = static_cast<int64_t>(gx1) * mtiles1;
   const int64_t n2 = static_cast<int64_t>(gx2) * ((MT2 == 2) ? (mtiles2 + 1) / 2 : mtiles2);
   if (n1 + n2 > 0x7fffffff) return fail("qmm(gate_up + shared down): grid too large");
-  qmm_gate_up_shdown_kernel<W, CPW, JPW, W2, MT2>
+  qmm_gate_up_shdown_kernel<W, CPW, JPW, W2, MT2, CPW2>
       <<<dim3(static_cast<unsigned>(n1 + n2)), 256, 0, stream>>>(a1, n_jobs1, gx1, n1, a2, n_jobs2, gx2);
   return check_launch("qmm(gate_up + shared down)");
 }
@@ -1638,6 +1643,13 @@ int launch_gate_up_shared_down(const QmmArgs& a1, int64_t mtiles1, const QmmArgs
   QMOE_GSD(2, 1, 1, 2)   // c1-like shapes (H 2048, shared intermediate 512)
   QMOE_GSD(2, 1, 2, 2)
 #undef QMOE_GSD
+  // c3-like shapes (H 7168, shared intermediate 2048: eight chunks, four wavefronts of two, one
+  // m-tile per wavefront)
+  if (w2 == 8) {
+    if (sh.w == 2 && sh.cpw == 2 && sh.jpw == 2) return launch_gsd<2, 2, 2, 4, 1, 2>(a1, mtiles1, a2, mtiles2, stream);
+    if (sh.w == 4 && sh.cpw == 1 && sh.jpw == 2) return launch_gsd<4, 1, 2, 4, 1, 2>(a1, mtiles1, a2, mtiles2, stream);
+    if (sh.w == 4 && sh.cpw == 1 && sh.jpw == 1) return launch_gsd<4, 1, 1, 4, 1, 2>(a1, mtiles1, a2, mtiles2, stream);
+  }
   return 1;   // no compiled combination: the caller launches the two products apart
 }
 

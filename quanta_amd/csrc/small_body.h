@@ -207,7 +207,6 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
   constexpr int JOBS_PER_WG = C::JOBS_PER_WG;
   constexpr int NT = C::NT;
   constexpr int CH = C::CH;
-  static_assert(fmt_quant(FMT) || CPW == 1, "bf16 weights use one chunk per wavefront");
   constexpr bool kRed = CH > 1;
 
   // wave index as a scalar, so per-wavefront quantities (job, k-range) stay in SGPRs
@@ -506,8 +505,13 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       }
       }
     } else {  // dense: bf16 weights, or int8 codes dequantized to bf16 in registers
+      // (CPW == 2: the wavefront's two chunks [k0, kmid) and [kmid, k1), the first one's sums
+      // set aside in LDS at the boundary as the int4 path does, one m-tile, no fused norm)
+      static_assert(CPW == 1 || (CPW == 2 && MT == 1 && !NORM), "dense: two chunks per wavefront need one m-tile");
       const int nks = a.K / 32;
       const int k0 = kpart * nks / W, k1 = (kpart + 1) * nks / W;
+      const int kmid = (CPW == 2) ? (kpart * 2 + 1) * nks / (2 * W) : k1;
+      int kend = (CPW == 2) ? kmid : k1;   // the current chunk's end (loads are clamped to it)
       using Frag = DenseFrag<FMT>;
       DenseTile<FMT> wt[NT];
 #pragma unroll
@@ -522,7 +526,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       auto load_batch = [&](int cb, Frag (&wv)[BS][NT], u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
-          const int c = min(cb + i, k1 - 1);
+          const int c = min(cb + i, kend - 1);
 #pragma unroll
           for (int t = 0; t < NT; ++t) wv[i][t] = wt[t].load(c);
 #pragma unroll
@@ -545,7 +549,7 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
       auto mma_batch = [&](int cb, const Frag (&wv)[BS][NT], const u32x4 (&xv)[BS][MT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BS; ++i) {
-          if (cb + i < k1) {
+          if (cb + i < kend) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
               const bf16x8_t B = as_bf16x8(dense_bf16<FMT>(wv[i][t]));
@@ -663,6 +667,22 @@ __device__ __forceinline__ void small_body(const QmmArgs& a, int n_jobs, int bx,
           norm_mma_batch(cb, wv, xv);
           cb += BS;
         }
+      }
+      if constexpr (CPW == 2) {
+        for (; cb < kmid; cb += BS) {
+          Frag wv[BS][NT];
+          u32x4 xv[BS][MT];
+          load_batch(cb, wv, xv);
+          mma_batch(cb, wv, xv);
+        }
+        // the first chunk's sums to LDS, where the reduction below adds them in chunk order
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          red[((wave * CPW) * NT + t) * 64 + lane] = acc[t];
+          acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        cb = kmid;
+        kend = k1;
       }
       for (; cb < k1; cb += BS) {
         Frag wv[BS][NT];

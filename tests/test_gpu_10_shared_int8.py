@@ -102,9 +102,11 @@ def test_residual_and_noalloc_int8_shared(gpu, N):
     assert torch.equal(out, qwen35_moe(x, p16, s.cfg)[0]), f"noalloc N={N}"
 
 
-@pytest.mark.parametrize("name,N", [("c2", 1), ("c2", 8), ("c2", 32), ("c3", 16)])
+@pytest.mark.parametrize("name,N", [("c2", 1), ("c2", 8), ("c2", 32), ("c3", 1), ("c3", 16), ("c3", 64)])
 def test_full_size_int8_shared(gpu, name, N):
-    """Full-size c2 (Is 1024) and c3 (Is 2048, ungated) layers: int8 == bf16-dequant block."""
+    """Full-size c2 (Is 1024) and c3 (Is 2048, ungated) layers: int8 == bf16-dequant block. At c3
+    the int8 shared down (eight K chunks, four wavefronts of two) rides in the routed gate_up
+    launch (slot-major with the top-k at N=1, sorted at 16 and 64), the bf16 one in the combine."""
     s = _spec(name)
     p8, p16 = _pair(s, gpu, seed=23)
     x = synth.make_inputs(s, N, device=gpu, seed=N)[None]
